@@ -1,0 +1,385 @@
+"""StableHLO text parser and numpy interpreter (oracle; see oracle/__init__.py).
+
+Parses the pretty syntax that ryft-mlir's printer emits for the supported op set (printer goldens:
+crates/ryft-mlir/src/dialects/stable_hlo/operations/linear_algebra.rs:2240-2263, functional.rs:529-541,
+manipulation.rs:2022,2154, control_flow.rs:596, miscellaneous.rs:1181, casting.rs:456, comparison.rs:500) and
+evaluates it op by op. Floating-point values are carried as float64 holding exactly the value of their StableHLO
+element type: each op computes in float64 and rounds its result to the result element type (through f32, as an f32
+datapath would). Integers are carried as int64 and wrapped to their width. Per-op semantics cite the ryft-mlir
+documentation of each builder (file:line in the evaluator below).
+"""
+from __future__ import annotations
+
+import math
+import re
+from typing import Dict, List, Sequence, Tuple
+
+import numpy as np
+
+from . import numerics
+
+FLOAT = {"f16", "bf16", "f32", "f64", "f8E4M3FN", "f8E5M2"}
+INT_BITS = {"i1": 1, "i8": 8, "i16": 16, "i32": 32, "i64": 64, "ui8": 8, "ui16": 16, "ui32": 32, "ui64": 64}
+
+_TENSOR = re.compile(r"tensor<([^>]*)>")
+
+
+def parse_type(t: str) -> Tuple[Tuple[int, ...], str]:
+    m = _TENSOR.search(t)
+    if not m:
+        raise ValueError(f"not a tensor type: {t}")
+    parts = m.group(1).split("x")
+    # element types such as f8E4M3FN contain no 'x'; dims are the leading integer parts
+    dims = []
+    while parts and parts[0].isdigit():
+        dims.append(int(parts.pop(0)))
+    return tuple(dims), "x".join(parts)
+
+
+def _types(s: str) -> List[Tuple[Tuple[int, ...], str]]:
+    return [parse_type("tensor<" + g + ">") for g in _TENSOR.findall(s)]
+
+
+def _ints(s: str) -> List[int]:
+    return [int(v) for v in re.findall(r"-?\d+", s)] if s and s.strip() else []
+
+
+# ----------------------------------------------------------------------------------------------- values
+def wrap_int(x: np.ndarray, dtype: str) -> np.ndarray:
+    bits = INT_BITS[dtype]
+    x = np.asarray(x, dtype=np.int64)
+    if dtype == "i1":
+        return (x != 0).astype(np.int64)
+    if bits == 64:
+        return x
+    mask = (1 << bits) - 1
+    u = x & mask
+    if dtype.startswith("ui"):
+        return u
+    return np.where(u >= (1 << (bits - 1)), u - (1 << bits), u)
+
+
+def normalize(x, dtype: str) -> np.ndarray:
+    """Round / wrap an array to the values representable in `dtype`."""
+    if dtype in FLOAT:
+        return numerics.round_to(np.asarray(x, dtype=np.float64), dtype)
+    return wrap_int(np.asarray(x), dtype)
+
+
+def from_raw(raw: np.ndarray, dtype: str) -> np.ndarray:
+    """PJRT buffer contents (bf16/f8 as raw bits) → oracle values."""
+    raw = np.asarray(raw)
+    if dtype in ("bf16", "f16", "f8E4M3FN", "f8E5M2"):
+        return numerics.decode_bits(raw, dtype)
+    if dtype in ("f32", "f64"):
+        return raw.astype(np.float64)
+    return wrap_int(raw.astype(np.int64), dtype)
+
+
+def to_raw(x: np.ndarray, dtype: str) -> np.ndarray:
+    """Oracle values → PJRT buffer contents."""
+    if dtype in ("bf16", "f16", "f8E4M3FN", "f8E5M2"):
+        return numerics.encode_bits(x, dtype)
+    np_t = {"f32": np.float32, "f64": np.float64, "i1": np.bool_, "i8": np.int8, "i16": np.int16, "i32": np.int32,
+            "i64": np.int64, "ui8": np.uint8, "ui16": np.uint16, "ui32": np.uint32, "ui64": np.uint64}[dtype]
+    return np.asarray(x).astype(np_t)
+
+
+def _dense(payload: str, shape, dtype: str) -> np.ndarray:
+    p = payload.strip()
+    n = int(np.prod(shape)) if shape else 1
+    if p.startswith('"0x'):
+        raw = bytes.fromhex(p[3:-1])
+        np_bits = {"bf16": np.uint16, "f16": np.uint16, "f8E4M3FN": np.uint8, "f8E5M2": np.uint8, "f32": np.float32,
+                   "f64": np.float64, "i8": np.int8, "i16": np.int16, "i32": np.int32, "i64": np.int64,
+                   "i1": np.uint8}[dtype]
+        arr = np.frombuffer(raw, dtype=np_bits)
+        vals = from_raw(arr, dtype) if dtype not in ("i1",) else arr.astype(np.int64)
+        return np.broadcast_to(vals, (n,)).reshape(shape).copy() if vals.size in (1, n) else vals.reshape(shape)
+    toks = [t for t in re.split(r"[\[\],\s]+", p) if t]
+    out = []
+    for t in toks:
+        if t.startswith("0x") or t.startswith("0X"):
+            bits = int(t, 16)
+            if dtype == "f32":
+                out.append(float(np.array([bits], dtype=np.uint32).view(np.float32)[0]))
+            elif dtype == "f64":
+                out.append(float(np.array([bits], dtype=np.uint64).view(np.float64)[0]))
+            elif dtype in ("bf16", "f16", "f8E4M3FN", "f8E5M2"):
+                out.append(float(numerics.decode_bits(np.array([bits]), dtype)[0]))
+            else:
+                out.append(bits)
+        elif t in ("true", "false"):
+            out.append(1 if t == "true" else 0)
+        elif dtype in FLOAT:
+            out.append(float(t))
+        else:
+            out.append(int(float(t)) if any(c in t for c in ".eE") else int(t))
+    arr = np.array(out, dtype=np.float64 if dtype in FLOAT else np.int64)
+    if arr.size == 1:
+        arr = np.broadcast_to(arr.reshape(()), shape).copy()
+    return normalize(arr.reshape(shape), dtype)
+
+
+# ----------------------------------------------------------------------------------------------- parsing
+class Module:
+    def __init__(self, text: str, entry: str = "main"):
+        m = re.search(r"func\.func\s+(?:public\s+|private\s+)?@" + re.escape(entry) + r"\s*\((.*?)\)\s*->", text, re.S)
+        if not m:
+            raise ValueError(f"no func.func @{entry}")
+        self.params: List[Tuple[str, Tuple[int, ...], str]] = []
+        for a in re.finditer(r"(%[\w.$-]+)\s*:\s*(tensor<[^>]*>)", m.group(1)):
+            shape, dt = parse_type(a.group(2))
+            self.params.append((a.group(1), shape, dt))
+        body = text[m.end():]
+        body = body[body.index("{") + 1:]
+        self.stmts = self._statements(body)
+
+    @staticmethod
+    def _statements(body: str) -> List[str]:
+        out, lines = [], body.split("\n")
+        i = 0
+        while i < len(lines):
+            ln = lines[i].strip()
+            i += 1
+            if not ln or ln.startswith("//") or ln == "}":
+                continue
+            if "reducer(" in ln or (ln.startswith("%") and "stablehlo.reduce(" in ln and "applies" not in ln):
+                # region form: collect up to the closing brace of the reducer block
+                block = [ln]
+                while "}" not in lines[i - 1] or len(block) == 1:
+                    block.append(lines[i].strip())
+                    i += 1
+                    if block[-1].startswith("}"):
+                        break
+                out.append(" ".join(block))
+                continue
+            out.append(ln)
+        return out
+
+
+_BIN = {"add", "subtract", "multiply", "divide", "maximum", "minimum", "and", "or", "xor", "power", "remainder"}
+_UN = {"exponential", "log", "rsqrt", "sqrt", "tanh", "logistic", "negate", "abs", "not", "floor", "ceil", "sign",
+       "exponential_minus_one", "log_plus_one"}
+
+
+def evaluate(text: str, inputs: Sequence[np.ndarray], dot_precision: str = "f64") -> List[Tuple[np.ndarray, str]]:
+    """Runs `func.func @main` on `inputs` (oracle values, see from_raw); returns [(values, dtype)] per result.
+
+    dot_precision "f64" accumulates floating dots in float64 (parity checks); "f32" multiplies and accumulates in
+    float32 the way XLA's CPU backend upcasts bf16 dots to an f32 GEMM (used only for the timed CPU baseline)."""
+    mod = Module(text)
+    if len(inputs) != len(mod.params):
+        raise ValueError(f"expected {len(mod.params)} inputs, got {len(inputs)}")
+    env: Dict[str, Tuple[np.ndarray, str]] = {}
+    for (name, shape, dt), x in zip(mod.params, inputs):
+        x = np.asarray(x)
+        if tuple(x.shape) != tuple(shape):
+            raise ValueError(f"{name}: expected shape {shape}, got {x.shape}")
+        env[name] = (x, dt)
+    for st in mod.stmts:
+        r = _RET.match(st)
+        if r:
+            names = re.findall(r"%[\w.$#-]+", r.group(1))
+            return [env[n] for n in names]
+        m = re.match(r"(%[\w.$-]+)\s*=\s*(?:stablehlo|mhlo)\.(\w+)\s*(.*)$", st)
+        if not m:
+            raise ValueError(f"cannot parse statement: {st}")
+        res, op, rest = m.group(1), m.group(2), m.group(3)
+        env[res] = _eval_op(op, rest, env, dot_precision)
+    raise ValueError("function has no return")
+
+
+_RET = re.compile(r"(?:func\.)?return\s+(.*?)(?:\s*:\s*.*)?$")
+
+
+def _operands(rest: str, n: int, env) -> List[Tuple[np.ndarray, str]]:
+    names = re.findall(r"%[\w.$-]+", rest.split(":")[0])[:n]
+    return [env[x] for x in names]
+
+
+def _eval_op(op: str, rest: str, env, dot_precision: str) -> Tuple[np.ndarray, str]:
+    ty = rest[rest.rfind(":"):] if ":" in rest else ""
+    if op == "constant":
+        # miscellaneous.rs:16-60
+        m = re.match(r"dense<(.*)>\s*:\s*(tensor<.*>)$", rest)
+        shape, dt = parse_type(m.group(2))
+        return _dense(m.group(1), shape, dt), dt
+    if op == "iota":
+        # miscellaneous.rs:67-130: element = its index along `dim`
+        m = re.match(r"dim\s*=\s*(\d+)\s*:\s*(tensor<.*>)", rest)
+        shape, dt = parse_type(m.group(2))
+        d = int(m.group(1))
+        idx = np.arange(shape[d]).reshape([-1 if i == d else 1 for i in range(len(shape))])
+        return normalize(np.broadcast_to(idx, shape), dt), dt
+    out_shape, out_dt = _types(ty)[-1]
+    if op == "convert":
+        # casting.rs:75-122: float→float rounds to nearest even; float→int truncates toward zero (saturating, NaN→0
+        # here: out-of-range results are implementation-defined); int→float rounds; anything→i1 is x != 0.
+        (x, dt), = _operands(rest, 1, env)
+        if out_dt == "i1":
+            return (np.asarray(x) != 0).astype(np.int64), out_dt
+        if out_dt in FLOAT:
+            return normalize(np.asarray(x, dtype=np.float64), out_dt), out_dt
+        if dt in FLOAT:
+            bits = INT_BITS[out_dt]
+            lo, hi = (0, (1 << bits) - 1) if out_dt.startswith("ui") else (-(1 << (bits - 1)), (1 << (bits - 1)) - 1)
+            xf = np.nan_to_num(np.trunc(np.asarray(x, dtype=np.float64)), nan=0.0)
+            return np.clip(xf, lo, hi).astype(np.int64), out_dt
+        return wrap_int(x, out_dt), out_dt
+    if op == "broadcast_in_dim":
+        # manipulation.rs:271-338: result[i] = operand[j] with j_k = i[dims[k]] (or 0 where the operand dim is 1)
+        m = re.match(r"(%[\w.$-]+)\s*,\s*dims\s*=\s*\[(.*?)\]", rest)
+        x, dt = env[m.group(1)]
+        dims = _ints(m.group(2))
+        view = np.asarray(x).reshape([x.shape[k] for k in range(x.ndim)])
+        shape_in = [1] * len(out_shape)
+        for k, d in enumerate(dims):
+            shape_in[d] = x.shape[k]
+        order = np.argsort(dims) if dims else []
+        moved = np.transpose(view, order) if len(dims) > 1 else view
+        return np.broadcast_to(moved.reshape(shape_in), out_shape).copy(), dt
+    if op == "transpose":
+        # manipulation.rs:76-133: result dim i = operand dim perm[i]
+        m = re.match(r"(%[\w.$-]+)\s*,\s*dims\s*=\s*\[(.*?)\]", rest)
+        x, dt = env[m.group(1)]
+        return np.transpose(x, _ints(m.group(2))).copy(), dt
+    if op == "reshape":
+        (x, dt), = _operands(rest, 1, env)
+        return np.asarray(x).reshape(out_shape), dt
+    if op == "compare":
+        # comparison.rs:44-135
+        m = re.match(r"(\w+)\s*,\s*(%[\w.$-]+)\s*,\s*(%[\w.$-]+)", rest)
+        a, _ = env[m.group(2)]
+        b, _ = env[m.group(3)]
+        fn = {"EQ": np.equal, "NE": np.not_equal, "GE": np.greater_equal, "GT": np.greater, "LE": np.less_equal,
+              "LT": np.less}[m.group(1)]
+        return fn(a, b).astype(np.int64), "i1"
+    if op == "select":
+        # control_flow.rs:216-300: pred ? on_true : on_false (a scalar predicate selects whole tensors)
+        (p, _), (a, dt), (b, _) = _operands(rest, 3, env)
+        return np.where(np.asarray(p) != 0, a, b), dt
+    if op == "clamp":
+        (lo, _), (x, dt), (hi, _) = _operands(rest, 3, env)
+        return normalize(np.minimum(np.maximum(x, lo), hi), dt), dt
+    if op in _BIN:
+        # arithmetic.rs:190-420, comparison.rs:230-297 (maximum / minimum propagate NaN)
+        (a, dt), (b, _) = _operands(rest, 2, env)
+        if dt in FLOAT:
+            a, b = np.asarray(a, dtype=np.float64), np.asarray(b, dtype=np.float64)
+            with np.errstate(all="ignore"):
+                r = {"add": lambda: a + b, "subtract": lambda: a - b, "multiply": lambda: a * b,
+                     "divide": lambda: a / b, "maximum": lambda: np.maximum(a, b),
+                     "minimum": lambda: np.minimum(a, b), "power": lambda: np.power(a, b),
+                     "remainder": lambda: np.fmod(a, b)}[op]()
+            return normalize(r, dt), dt
+        a, b = np.asarray(a, dtype=np.int64), np.asarray(b, dtype=np.int64)
+        if op == "divide":
+            with np.errstate(all="ignore"):
+                r = np.where(b == 0, -1, np.trunc(a / np.where(b == 0, 1, b))).astype(np.int64)
+        elif op == "remainder":
+            r = np.where(b == 0, a, np.fmod(a, np.where(b == 0, 1, b)))
+        else:
+            r = {"add": lambda: a + b, "subtract": lambda: a - b, "multiply": lambda: a * b,
+                 "maximum": lambda: np.maximum(a, b), "minimum": lambda: np.minimum(a, b),
+                 "and": lambda: a & b, "or": lambda: a | b, "xor": lambda: a ^ b}[op]()
+        return wrap_int(r, dt), dt
+    if op in _UN:
+        # exponential.rs (exponential :245, rsqrt :151, logistic :434), arithmetic.rs:134 (negate)
+        (x, dt), = _operands(rest, 1, env)
+        if dt not in FLOAT:
+            x = np.asarray(x, dtype=np.int64)
+            r = {"negate": lambda: -x, "abs": lambda: np.abs(x), "sign": lambda: np.sign(x),
+                 "not": lambda: (x == 0).astype(np.int64) if dt == "i1" else ~x}[op]()
+            return wrap_int(r, dt), dt
+        x = np.asarray(x, dtype=np.float64)
+        with np.errstate(all="ignore"):
+            r = {"exponential": lambda: np.exp(x), "log": lambda: np.log(x), "rsqrt": lambda: 1.0 / np.sqrt(x),
+                 "sqrt": lambda: np.sqrt(x), "tanh": lambda: np.tanh(x),
+                 "logistic": lambda: 1.0 / (1.0 + np.exp(-x)), "negate": lambda: -x, "abs": lambda: np.abs(x),
+                 "floor": lambda: np.floor(x), "ceil": lambda: np.ceil(x), "sign": lambda: np.sign(x),
+                 "exponential_minus_one": lambda: np.expm1(x), "log_plus_one": lambda: np.log1p(x)}[op]()
+        return normalize(r, dt), dt
+    if op == "dot_general":
+        return _dot_general(rest, env, out_shape, out_dt, dot_precision)
+    if op == "reduce":
+        return _reduce(rest, env, out_shape, out_dt)
+    raise NotImplementedError(f"stablehlo.{op}")
+
+
+def _dot_general(rest, env, out_shape, out_dt, dot_precision):
+    """linear_algebra.rs:561-705: transpose each operand to batch + free + contracting dims, flatten, multiply, and
+    sum over the contracting dims; result dims are batch, lhs free, rhs free."""
+    m = re.match(r"(%[\w.$-]+)\s*,\s*(%[\w.$-]+)\s*,(.*)", rest)
+    (a, adt), (b, bdt) = env[m.group(1)], env[m.group(2)]
+    attrs = m.group(3)
+    bm = re.search(r"batching_dims\s*=\s*\[(.*?)\]\s*x\s*\[(.*?)\]", attrs)
+    cm = re.search(r"contracting_dims\s*=\s*\[(.*?)\]\s*x\s*\[(.*?)\]", attrs)
+    lb, rb = (_ints(bm.group(1)), _ints(bm.group(2))) if bm else ([], [])
+    lc, rc = _ints(cm.group(1)), _ints(cm.group(2))
+    a, b = np.asarray(a), np.asarray(b)
+    lf = [d for d in range(a.ndim) if d not in lb and d not in lc]
+    rf = [d for d in range(b.ndim) if d not in rb and d not in rc]
+    at = np.transpose(a, lb + lf + lc)
+    bt = np.transpose(b, rb + rc + rf)
+    nb = int(np.prod([a.shape[d] for d in lb])) if lb else 1
+    M = int(np.prod([a.shape[d] for d in lf])) if lf else 1
+    K = int(np.prod([a.shape[d] for d in lc])) if lc else 1
+    N = int(np.prod([b.shape[d] for d in rf])) if rf else 1
+    A3, B3 = at.reshape(nb, M, K), bt.reshape(nb, K, N)
+    if out_dt in FLOAT:
+        if dot_precision == "f32":
+            r = np.matmul(A3.astype(np.float32), B3.astype(np.float32)).astype(np.float64)
+        else:
+            r = np.matmul(A3.astype(np.float64), B3.astype(np.float64))
+        return normalize(r.reshape(out_shape), out_dt), out_dt
+    # integers: exact in float64 while |sum| < 2^53 (|acc| ≤ K·127² for i8), else int64 loop
+    if K * float(np.max(np.abs(A3), initial=0)) * float(np.max(np.abs(B3), initial=0)) < 2.0 ** 52:
+        r = np.rint(np.matmul(A3.astype(np.float64), B3.astype(np.float64))).astype(np.int64)
+    else:
+        r = np.einsum("bmk,bkn->bmn", A3.astype(np.int64), B3.astype(np.int64))
+    return wrap_int(r.reshape(out_shape), out_dt), out_dt
+
+
+def _reduce(rest, env, out_shape, out_dt):
+    """functional.rs:109-135: reduce `dimensions` of the input with the body, starting from the init value; the
+    combination order is implementation-defined (sums here are exact-as-float64 then rounded once)."""
+    m = re.match(r"\((%[\w.$-]+)\s+init:\s*(%[\w.$-]+)\)\s*(?:applies\s+stablehlo\.(\w+))?\s*across\s+dimensions\s*=\s*\[(.*?)\]", rest)
+    x, dt = env[m.group(1)]
+    init, _ = env[m.group(2)]
+    body = m.group(3)
+    if body is None:
+        bm = re.search(r"stablehlo\.(add|maximum|minimum|multiply|and|or)\s", rest[m.end():])
+        body = bm.group(1)
+    dims = tuple(_ints(m.group(4)))
+    init = np.asarray(init).reshape(())
+    x = np.asarray(x)
+    if dt in FLOAT:
+        x = x.astype(np.float64)
+        with np.errstate(all="ignore"):
+            if body == "add":
+                r = np.sum(x, axis=dims) + init
+            elif body == "multiply":
+                r = np.prod(x, axis=dims) * init
+            elif body == "maximum":
+                r = np.maximum(np.max(x, axis=dims, initial=-np.inf), init)
+            elif body == "minimum":
+                r = np.minimum(np.min(x, axis=dims, initial=np.inf), init)
+            else:
+                raise NotImplementedError(body)
+        return normalize(r, out_dt), out_dt
+    x = x.astype(np.int64)
+    r = {"add": lambda: np.sum(x, axis=dims) + init, "multiply": lambda: np.prod(x, axis=dims) * init,
+         "maximum": lambda: np.maximum(np.max(x, axis=dims, initial=np.iinfo(np.int64).min), init),
+         "minimum": lambda: np.minimum(np.min(x, axis=dims, initial=np.iinfo(np.int64).max), init),
+         "and": lambda: np.bitwise_and.reduce(x, axis=dims) & init,
+         "or": lambda: np.bitwise_or.reduce(x, axis=dims) | init}[body]()
+    return wrap_int(r, out_dt), out_dt
+
+
+def rel_error(got: np.ndarray, want: np.ndarray) -> float:
+    """Normwise relative error max|got - want| / max|want| (the tolerance metric of the parity tests)."""
+    got, want = np.asarray(got, dtype=np.float64), np.asarray(want, dtype=np.float64)
+    denom = float(np.max(np.abs(want))) if want.size else 0.0
+    diff = float(np.max(np.abs(got - want))) if want.size else 0.0
+    return diff / denom if denom > 0 else diff

@@ -1,0 +1,97 @@
+// Typed SSA graph of one StableHLO `func.func @main`, produced by the MLIR front-end and consumed by the planner.
+//
+// Op semantics follow the StableHLO builders documented in the reference:
+//   dot_general  crates/ryft-mlir/src/dialects/stable_hlo/operations/linear_algebra.rs:561-705
+//   reduce       .../operations/functional.rs:109-135
+//   transpose / broadcast_in_dim  .../operations/manipulation.rs:76-133, 271-338
+//   compare / maximum            .../operations/comparison.rs:44-135, 230-297
+//   convert      .../operations/casting.rs:75-122
+//   constant / iota               .../operations/miscellaneous.rs:16-130
+//   select       .../operations/control_flow.rs:216-300
+//   exp / rsqrt / logistic        .../operations/exponential.rs
+//   add / subtract / multiply / divide / negate  .../operations/arithmetic.rs:134-420
+#pragma once
+
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "common.h"
+
+namespace ryft {
+
+struct TensorType {
+  DType dtype = DType::INVALID;
+  std::vector<int64_t> shape;
+  int64_t elements() const { return num_elements(shape); }
+  size_t bytes() const { return (size_t)elements() * dtype_size(dtype); }
+  int rank() const { return (int)shape.size(); }
+  bool operator==(const TensorType& o) const { return dtype == o.dtype && shape == o.shape; }
+  std::string str() const;
+};
+
+enum class Op : uint8_t {
+  Parameter,
+  Constant,
+  // elementwise, unary
+  Negate, Abs, Exp, Log, Rsqrt, Sqrt, Tanh, Logistic, Not, Convert, Floor, Ceil, Sign, Expm1, Log1p,
+  // elementwise, binary
+  Add, Subtract, Multiply, Divide, Maximum, Minimum, Power, Remainder, And, Or, Xor, Compare,
+  // elementwise, ternary
+  Select, Clamp,
+  // data movement
+  BroadcastInDim, Transpose, Reshape, Iota,
+  // contractions and reductions
+  DotGeneral, Reduce,
+};
+const char* op_name(Op op);
+bool op_is_elementwise(Op op);  // one output element depends on the same-index elements of its operands
+
+enum class CmpDir : uint8_t { EQ, NE, GE, GT, LE, LT };
+enum class CmpType : uint8_t { NOTYPE, FLOAT, TOTALORDER, SIGNED, UNSIGNED };
+enum class ReduceBody : uint8_t { Add, Max, Min, Mul, And, Or };
+
+struct DotDims {
+  std::vector<int64_t> lhs_batch, rhs_batch, lhs_contract, rhs_contract;
+};
+
+struct Node {
+  Op op;
+  TensorType type;
+  std::vector<int> operands;
+  // attributes (meaning depends on op)
+  std::vector<int64_t> dims;  // broadcast_dimensions / permutation / reduce dimensions
+  int64_t iota_dim = 0;
+  CmpDir cmp = CmpDir::EQ;
+  CmpType cmp_type = CmpType::NOTYPE;
+  DotDims dot;
+  DType dot_lhs_precision = DType::INVALID;  // algorithm lhs/rhs_precision_type, if given
+  DType dot_rhs_precision = DType::INVALID;
+  ReduceBody reduce_body = ReduceBody::Add;
+  int param_index = -1;
+  // constant payload: raw little-endian bytes in `type.dtype`; splat constants hold one element
+  std::vector<uint8_t> literal;
+  bool splat = false;
+  std::string debug;  // SSA name in the source text
+};
+
+struct Graph {
+  std::vector<Node> nodes;
+  std::vector<int> params;   // node ids, in argument order
+  std::vector<int> results;  // node ids, in return order
+  std::string name = "main";
+  std::vector<std::vector<int>> users() const;
+  std::string dump() const;
+};
+
+// Front-end: StableHLO MLIR text (pretty or generic syntax) → Graph. Throws Status on malformed or unsupported input.
+Graph parse_mlir_text(const std::string& text, const std::string& entry = "main");
+// MLIR bytecode (the `MLïR` magic) is recognised and rejected with UNIMPLEMENTED.
+bool is_mlir_bytecode(const char* data, size_t size);
+
+// Literal helpers: constant element as double / int64 (splat or index 0).
+double literal_as_double(const Node& n, int64_t index = 0);
+int64_t literal_as_int(const Node& n, int64_t index = 0);
+
+}  // namespace ryft

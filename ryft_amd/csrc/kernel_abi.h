@@ -1,0 +1,154 @@
+// Argument blocks shared by the planner (host C++) and the gfx950 kernels (HIP). Plain POD structs passed by value
+// as kernel arguments; device pointers are patched in by the executor right before each launch.
+#pragma once
+
+#include <stdint.h>
+
+namespace ryft {
+
+// ------------------------------------------------------------------------------------------------ elementwise VM
+// A fused elementwise expression over an iteration space of up to EW_MAX_RANK dimensions. Each leaf is a strided
+// view of a device buffer (broadcast_in_dim → stride 0, transpose → permuted strides); instructions form an SSA
+// program over 32-bit registers (float math or int32 math), each result rounded to its StableHLO element type.
+#define EW_MAX_RANK 6
+#define EW_MAX_LEAVES 8
+#define EW_MAX_INSTR 48
+#define EW_MAX_REGS 12
+#define EW_MAX_OUT 2
+
+enum EwLeafKind : int32_t { EW_LEAF_GENERAL = 0, EW_LEAF_IDENTITY = 1, EW_LEAF_SCALAR = 2 };
+
+struct EwLeaf {
+  const void* ptr;
+  int32_t dtype;  // DType
+  int32_t kind;   // EwLeafKind
+  int64_t offset; // element offset
+  int64_t strides[EW_MAX_RANK];
+};
+
+enum EwOp : uint8_t {
+  EW_LOAD,      // r = leaves[a][index]
+  EW_CONST,     // r = imm (bits)
+  EW_IOTA,      // r = index[a]
+  EW_ACC,       // r = GEMM accumulator a (0: first dot, 1: second dot); epilogues only
+  // unary, float class
+  EW_NEG, EW_ABS, EW_EXP, EW_LOG, EW_RSQRT, EW_SQRT, EW_TANH, EW_LOGISTIC, EW_FLOOR, EW_CEIL, EW_SIGN,
+  EW_EXPM1, EW_LOG1P,
+  // unary, int class
+  EW_INEG, EW_IABS, EW_NOT, EW_ISIGN,
+  // conversions
+  EW_CVT_F2F, EW_CVT_F2I, EW_CVT_I2F, EW_CVT_I2I, EW_CVT_F2P, EW_CVT_I2P,
+  // binary, float class
+  EW_ADD, EW_SUB, EW_MUL, EW_DIV, EW_MAX, EW_MIN, EW_POW, EW_REM,
+  // binary, int class
+  EW_IADD, EW_ISUB, EW_IMUL, EW_IDIV, EW_IMAX, EW_IMIN, EW_IREM, EW_AND, EW_OR, EW_XOR,
+  EW_UDIV, EW_UREM, EW_UMAX, EW_UMIN,
+  // comparisons: imm.i = direction (0 EQ,1 NE,2 GE,3 GT,4 LE,5 LT)
+  EW_FCMP, EW_ICMP, EW_UCMP,
+  // ternary
+  EW_SELECT, EW_FCLAMP, EW_ICLAMP,
+};
+
+struct EwInstr {
+  uint8_t op;
+  uint8_t dst;     // register
+  uint8_t a, b, c; // source registers (or leaf / dim / acc index for LOAD, IOTA, ACC)
+  uint8_t round;   // DType the result is rounded/wrapped to (0: none)
+  uint16_t pad;
+  union { float f; int32_t i; uint32_t u; } imm;
+};
+
+struct EwProgram {
+  int32_t n_instr;
+  int32_t n_leaves;
+  int32_t rank;
+  int32_t n_out;
+  int64_t total;                    // elements in the iteration space
+  int64_t shape[EW_MAX_RANK];
+  int32_t out_reg[EW_MAX_OUT];
+  int32_t out_dtype[EW_MAX_OUT];
+  void* out_ptr[EW_MAX_OUT];        // contiguous row-major over `shape` (elementwise kernels)
+  int32_t needs_coords;             // any GENERAL leaf or IOTA
+  int32_t out_float_mask;           // bit o set: output o's register holds float bits
+  EwLeaf leaves[EW_MAX_LEAVES];
+  EwInstr instr[EW_MAX_INSTR];
+};
+
+// ------------------------------------------------------------------------------------------------ reduction
+// out[o] = init ⊕ prologue(o, r) over r, where the prologue program's iteration space is [outer..., reduced...]
+// (reduced dims moved last). Output is contiguous over `outer` elements.
+enum ReduceKind : int32_t { RED_ADD = 0, RED_MAX = 1, RED_MIN = 2, RED_MUL = 3, RED_AND = 4, RED_OR = 5 };
+struct ReduceArgs {
+  EwProgram prologue;  // n_out == 1, out_reg = value to reduce; out_ptr[0] = output (outer elements)
+  int64_t outer;       // number of output elements
+  int64_t inner;       // reduced elements per output
+  int32_t kind;        // ReduceKind
+  int32_t is_float;    // 1: float class, 0: int class
+  union { float f; int32_t i; } init;
+  int32_t init_dtype;  // with init_ptr: element type of the scalar init operand
+  const void* init_ptr;  // non-null: the init value is a device scalar (a program argument)
+};
+
+// ------------------------------------------------------------------------------------------------ GEMM
+// C[b, m, n] = Σ_k A[b, m, k] · B[b, n, k]   (B is addressed as [n, k]; its strides say which one is contiguous)
+struct GemmOperand {
+  const void* ptr;
+  int64_t sb;  // batch stride (elements)
+  int64_t sr;  // row stride: m for A, n for B
+  int64_t sk;  // contraction stride
+  int32_t dtype;
+  int32_t pad;
+};
+
+enum GemmEpilogue : int32_t {
+  EPI_STORE = 0,        // out[0] = convert(acc)
+  EPI_SCALE = 1,        // out[0] = convert(alpha · acc · row[m] · col[n]); optional raw acc in out[1]
+  EPI_SWIGLU = 2,       // out[0] = convert(silu(acc·col[n]) · (acc2·col2[n]))
+  EPI_PROGRAM = 3,      // out[k] = program(acc, acc2, leaves)   (generic)
+};
+
+struct GemmArgs {
+  int32_t M, N, K, batch;
+  GemmOperand A, B;
+  GemmOperand B2;       // second B for dual GEMMs sharing A (ptr == nullptr when absent)
+  int32_t acc_is_int;   // i32 accumulation (int8 GEMM)
+  int32_t epilogue;     // GemmEpilogue
+  int32_t out_dtype[EW_MAX_OUT];
+  void* out_ptr[EW_MAX_OUT];
+  int32_t n_out;
+  int32_t dual;         // B2 present
+  // output element at (b, m, n) is out_ptr[k][b*M*N + m*N + n] (row-major over the dot result)
+  // EPI_SCALE / EPI_SWIGLU operands (f32 vectors; a null pointer means "absent")
+  const float* row;
+  int64_t row_sb, row_sm;
+  const float* col;
+  int64_t col_sb, col_sn;
+  const float* col2;
+  int64_t col2_sb, col2_sn;
+  float alpha;
+  int32_t raw_out;      // EPI_SCALE: also store the raw accumulator into out[1]
+  int32_t mid_round;    // EPI_SCALE / EPI_SWIGLU: round the value to this dtype before the output conversion
+  // EPI_PROGRAM: iteration space = the dot result's dims; epi_groups = #dims in (batch, lhs-free, rhs-free)
+  int32_t epi_groups[3];
+  EwProgram epi;
+};
+
+// ------------------------------------------------------------------------------------------------ attention
+// O[b,h,q,:] = softmax_k(scale · Q[b,h,q,:]·K[b,h,k,:] + mask) · V[b,h,k,:], f32 softmax statistics.
+struct AttnArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  int32_t B, H, Sq, Sk, D;
+  int32_t causal;       // keep k <= q + causal_offset
+  int32_t causal_offset;
+  int32_t dtype;        // input dtype (bf16)
+  int32_t out_dtype;    // output dtype (bf16 or f32)
+  int32_t p_dtype;      // dtype P is rounded to before P·V (bf16, or f32 = none)
+  float scale;
+  // element strides of Q, K, V, O in (b, h, s, d) order
+  int64_t qs[4], ks[4], vs[4], os[4];
+};
+
+}  // namespace ryft

@@ -1,0 +1,273 @@
+// Fused softmax attention forward for gfx950 (bf16 in, f32 softmax statistics, bf16 P·V, bf16/f32 out).
+//
+// A workgroup owns 128 queries of one (batch, head); each of its 4 wavefronts owns 32 queries. Key/value blocks of
+// 64 rows stream through LDS (double-buffered: block j+1 is fetched while block j is consumed). Scores are computed
+// transposed, Sᵀ = K·Qᵀ, so that the 32×32 MFMA accumulator puts one query in each lane (lanes l and l+32 share a
+// query and split its keys): the running max / sum of the online softmax then need no cross-lane reductions except
+// one swap between the two half-waves, and the rescaling of the output Oᵀ = Vᵀ·Pᵀ is a per-lane multiply. P never
+// leaves registers: the Sᵀ accumulator, rounded to bf16, is directly the B operand of the P·V MFMA, with the
+// matching key order obtained by reading Vᵀ from LDS in the same permuted order. exp uses v_exp_f32 (2^x) on
+// pre-scaled logits. The [S, S] score matrix is never materialised.
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+#include "../common.h"
+#include "ew_device.h"
+#include "kernels.h"
+
+namespace ryft {
+
+typedef __bf16 bf16x8_a __attribute__((__vector_size__(8 * sizeof(__bf16))));
+typedef float f32x16_a __attribute__((__vector_size__(16 * sizeof(float))));
+
+bool attention_supported(int head_dim) { return head_dim == 64 || head_dim == 128; }
+
+namespace {
+
+constexpr int BQ = 128;  // queries per workgroup
+constexpr int BKV = 64;  // keys per block
+
+__device__ __forceinline__ f32x16_a mma_bf16(const uint4& a, const uint4& b, f32x16_a c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_a, a), __builtin_bit_cast(bf16x8_a, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+}
+
+template <int D>
+struct AttnCfg {
+  static constexpr int KP = D * 2 + 16;    // K row pitch (bytes): [key][d]
+  static constexpr int VP = BKV * 2 + 16;  // Vᵀ row pitch (bytes): [d][key]
+  static constexpr int KBYTES = BKV * KP;
+  static constexpr int VBYTES = D * VP;
+  static constexpr int STAGE = KBYTES + VBYTES;
+  static constexpr int OP = D * 4 + 16;     // output staging pitch (f32)
+  static constexpr int LDS = 2 * STAGE > BQ * OP ? 2 * STAGE : BQ * OP;
+};
+
+template <int D>
+__global__ void __launch_bounds__(256) attention_fwd_kernel(const AttnArgs A) {
+  using C = AttnCfg<D>;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nq = A.Sq / BQ;
+  // heaviest (latest) query blocks first under a causal mask
+  const int qb = A.causal ? nq - 1 - (int)(blockIdx.x % nq) : (int)(blockIdx.x % nq);
+  const int bh = blockIdx.x / nq;
+  const int b = bh / A.H, h = bh % A.H;
+  const int q0 = qb * BQ;
+  const uint16_t* Qg = (const uint16_t*)A.q + (int64_t)b * A.qs[0] + (int64_t)h * A.qs[1];
+  const char* Kg = (const char*)A.k + ((int64_t)b * A.ks[0] + (int64_t)h * A.ks[1]) * 2;
+  const char* Vg = (const char*)A.v + ((int64_t)b * A.vs[0] + (int64_t)h * A.vs[1]) * 2;
+
+  // Q fragments (B operand of Sᵀ = K·Qᵀ): lane holds Q[q][s·16 + 8·(lane/32) .. +8] for its query q
+  const int myq = q0 + wave * 32 + (lane & 31);
+  uint4 qf[D / 16];
+#pragma unroll
+  for (int s = 0; s < D / 16; ++s)
+    qf[s] = *(const uint4*)(Qg + (int64_t)myq * A.qs[2] + s * 16 + 8 * (lane >> 5));
+
+  const float sl2 = A.scale * 1.4426950408889634f;  // logits in the log2 domain
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x16_a o[D / 32];
+#pragma unroll
+  for (int t = 0; t < D / 32; ++t) o[t] = f32x16_a{};
+
+  int nkv = A.Sk / BKV;
+  if (A.causal) {
+    int last_key = q0 + BQ - 1 + A.causal_offset;  // largest key any query of this block may see
+    int lim = last_key < 0 ? 0 : last_key / BKV + 1;
+    if (lim < nkv) nkv = lim;
+  }
+
+  // K block: 64 keys × D → 4·(D/128)... vectors of 16 B per thread; Vᵀ block: 8×8 transposes by threads < 8·D/8
+  constexpr int KVEC = BKV * D / 8 / 256;  // 16-byte vectors of K per thread
+  constexpr int VBLK = (BKV / 8) * (D / 8); // 8×8 blocks of V
+  uint4 kreg[KVEC];
+  uint4 vreg[8];
+  auto gload = [&](int j) {
+    const int k0 = j * BKV;
+#pragma unroll
+    for (int i = 0; i < KVEC; ++i) {
+      int v = tid + i * 256;
+      int row = v / (D / 8), c = v % (D / 8);
+      kreg[i] = *(const uint4*)(Kg + ((int64_t)(k0 + row) * A.ks[2] + c * 8) * 2);
+    }
+    if (tid < VBLK) {
+      int dv = tid % (D / 8), kb = tid / (D / 8);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) vreg[q] = *(const uint4*)(Vg + ((int64_t)(k0 + kb * 8 + q) * A.vs[2] + dv * 8) * 2);
+    }
+  };
+  auto lstore = [&](int buf) {
+    char* sK = smem + buf * C::STAGE;
+    char* sV = sK + C::KBYTES;
+#pragma unroll
+    for (int i = 0; i < KVEC; ++i) {
+      int v = tid + i * 256;
+      int row = v / (D / 8), c = v % (D / 8);
+      *(uint4*)(sK + row * C::KP + c * 16) = kreg[i];
+    }
+    if (tid < VBLK) {
+      int dv = tid % (D / 8), kb = tid / (D / 8);
+      uint32_t w[8][4];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) { w[q][0] = vreg[q].x; w[q][1] = vreg[q].y; w[q][2] = vreg[q].z; w[q][3] = vreg[q].w; }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        uint4 lo, hi;
+        lo.x = __builtin_amdgcn_perm(w[1][t], w[0][t], 0x05040100u); hi.x = __builtin_amdgcn_perm(w[1][t], w[0][t], 0x07060302u);
+        lo.y = __builtin_amdgcn_perm(w[3][t], w[2][t], 0x05040100u); hi.y = __builtin_amdgcn_perm(w[3][t], w[2][t], 0x07060302u);
+        lo.z = __builtin_amdgcn_perm(w[5][t], w[4][t], 0x05040100u); hi.z = __builtin_amdgcn_perm(w[5][t], w[4][t], 0x07060302u);
+        lo.w = __builtin_amdgcn_perm(w[7][t], w[6][t], 0x05040100u); hi.w = __builtin_amdgcn_perm(w[7][t], w[6][t], 0x07060302u);
+        *(uint4*)(sV + (dv * 8 + 2 * t) * C::VP + kb * 16) = lo;
+        *(uint4*)(sV + (dv * 8 + 2 * t + 1) * C::VP + kb * 16) = hi;
+      }
+    }
+  };
+
+  if (nkv > 0) {
+    gload(0);
+    lstore(0);
+  }
+  __syncthreads();
+  const int half = lane >> 5;
+  for (int j = 0; j < nkv; ++j) {
+    const int cur = j & 1;
+    if (j + 1 < nkv) gload(j + 1);
+    const char* sK = smem + cur * C::STAGE;
+    const char* sV = sK + C::KBYTES;
+    // Sᵀ tiles: keys [32t, 32t+32) × this wave's 32 queries
+    f32x16_a st[2] = {f32x16_a{}, f32x16_a{}};
+#pragma unroll
+    for (int s = 0; s < D / 16; ++s) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        uint4 kf = *(const uint4*)(sK + (t * 32 + (lane & 31)) * C::KP + (s * 16 + 8 * half) * 2);
+        st[t] = mma_bf16(kf, qf[s], st[t]);
+      }
+    }
+    // scale, mask, block max
+    const int kbase = j * BKV;
+    const bool need_mask = A.causal && (kbase + BKV - 1 > q0 + wave * 32 + A.causal_offset);
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float v = st[t][r] * sl2;
+        if (need_mask) {
+          int key = kbase + t * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+          if (key > myq + A.causal_offset) v = -INFINITY;
+        }
+        st[t][r] = v;
+        mloc = fmaxf(mloc, v);
+      }
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+    const float m_new = fmaxf(m_run, mloc);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;  // a fully masked row keeps p = 0
+    const float alpha = exp2f(m_run - m_use);
+    m_run = m_new;
+    l_run *= alpha;
+#pragma unroll
+    for (int t = 0; t < D / 32; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
+    // P = 2^(s - m), rounded to bf16 as the B operand of Oᵀ = Vᵀ·Pᵀ
+    uint4 pf[4];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      float p[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        p[r] = exp2f(st[t][r] - m_use);
+        l_run += p[r];
+      }
+      // P enters the bf16 MFMA rounded to bf16 whether the program rounds it (p_dtype bf16) or keeps it in f32
+      pf[2 * t] = uint4{pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3]), pack_bf16(p[4], p[5]), pack_bf16(p[6], p[7])};
+      pf[2 * t + 1] = uint4{pack_bf16(p[8], p[9]), pack_bf16(p[10], p[11]), pack_bf16(p[12], p[13]), pack_bf16(p[14], p[15])};
+    }
+    // Oᵀ[d, q] += Σ_key Vᵀ[d, key] · P[q, key]; k-step s covers keys [16s, 16s+16) in the accumulator's key order:
+    // element e of lane l ↔ key 16s + 8·(e/4) + 4·(l/32) + e%4
+#pragma unroll
+    for (int s = 0; s < BKV / 16; ++s) {
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt) {
+        const char* row = sV + (dt * 32 + (lane & 31)) * C::VP + (s * 16 + 4 * half) * 2;
+        uint2 lo = *(const uint2*)row;
+        uint2 hi = *(const uint2*)(row + 16);
+        uint4 vf = uint4{lo.x, lo.y, hi.x, hi.y};
+        o[dt] = mma_bf16(vf, pf[s], o[dt]);
+      }
+    }
+    if (j + 1 < nkv) lstore(cur ^ 1);
+    __syncthreads();
+  }
+
+  // normalise and write out through LDS (lane-per-query layout → row-major rows)
+  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+  float* so = (float*)smem;
+  const int ql = wave * 32 + (lane & 31);
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      int d = dt * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+      *(float*)((char*)so + ql * C::OP + d * 4) = o[dt][r] * inv;
+    }
+  __syncthreads();
+  char* Og = (char*)A.o;
+  const int osz = A.out_dtype == DT_F32 ? 4 : 2;
+  for (int idx = tid; idx < BQ * D / 4; idx += 256) {
+    int qr = idx / (D / 4), c4 = idx % (D / 4);
+    float4 v = *(const float4*)((char*)so + qr * C::OP + c4 * 16);
+    int64_t off = (int64_t)b * A.os[0] + (int64_t)h * A.os[1] + (int64_t)(q0 + qr) * A.os[2] + c4 * 4;
+    if (osz == 4) {
+      *(float4*)(Og + off * 4) = v;
+    } else {
+      uint2 pk = uint2{pack_bf16(v.x, v.y), pack_bf16(v.z, v.w)};
+      *(uint2*)(Og + off * 2) = pk;
+    }
+  }
+}
+
+}  // namespace
+
+void launch_attention(const AttnArgs& a, hipStream_t stream) {
+  if (!attention_supported(a.D)) fail(PJRT_Error_Code_UNIMPLEMENTED, "attention head dim " + std::to_string(a.D));
+  if (a.Sq % BQ || a.Sk % BKV) fail(PJRT_Error_Code_UNIMPLEMENTED, "attention sequence lengths must be multiples of 128 / 64");
+  if (a.qs[3] != 1 || a.ks[3] != 1 || a.vs[3] != 1 || a.os[3] != 1)
+    fail(PJRT_Error_Code_UNIMPLEMENTED, "attention operands must be contiguous along the head dim");
+  if (!(a.out_dtype == DT_BF16 || a.out_dtype == DT_F32)) fail(PJRT_Error_Code_UNIMPLEMENTED, "attention output type");
+  if (((uintptr_t)a.q | (uintptr_t)a.k | (uintptr_t)a.v | (uintptr_t)a.o) & 15)
+    fail(PJRT_Error_Code_UNIMPLEMENTED, "attention operands must be 16-byte aligned");
+  int64_t blocks = (int64_t)a.B * a.H * (a.Sq / BQ);
+  if (blocks == 0) return;
+  hipError_t e;
+  if (a.D == 128) {
+    int lds = AttnCfg<128>::LDS;
+    static bool attr128 = false;
+    if (!attr128) {
+      e = hipFuncSetAttribute((const void*)&attention_fwd_kernel<128>, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+      if (e != hipSuccess) fail(PJRT_Error_Code_INTERNAL, std::string("attention LDS attribute: ") + hipGetErrorString(e));
+      attr128 = true;
+    }
+    hipLaunchKernelGGL(attention_fwd_kernel<128>, dim3((unsigned)blocks), dim3(256), lds, stream, a);
+  } else {
+    int lds = AttnCfg<64>::LDS;
+    static bool attr64 = false;
+    if (!attr64) {
+      e = hipFuncSetAttribute((const void*)&attention_fwd_kernel<64>, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+      if (e != hipSuccess) fail(PJRT_Error_Code_INTERNAL, std::string("attention LDS attribute: ") + hipGetErrorString(e));
+      attr64 = true;
+    }
+    hipLaunchKernelGGL(attention_fwd_kernel<64>, dim3((unsigned)blocks), dim3(256), lds, stream, a);
+  }
+  e = hipGetLastError();
+  if (e != hipSuccess) fail(PJRT_Error_Code_INTERNAL, std::string("attention launch failed: ") + hipGetErrorString(e));
+}
+
+}  // namespace ryft

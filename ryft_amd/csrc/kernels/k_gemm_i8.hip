@@ -1,0 +1,25 @@
+// MFMA GEMM instantiations: i8.
+#include "gemm_mfma.h"
+
+namespace ryft {
+
+bool pick_i8(const GemmArgs& g, bool br, Choice* c) {
+  auto fits = [&](int bm, int bn, int bk) { return g.M % bm == 0 && g.N % bn == 0 && g.K % bk == 0; };
+  const bool dual = g.dual != 0;
+  const int64_t tiles256 = (int64_t)(g.M / 256) * (g.N / 256) * g.batch;
+  (void)dual; (void)tiles256;
+    if (dual) return false;
+    if (fits(256, 256, 128) && tiles256 >= 128) {
+      *c = br ? make_choice<MMA_I8, 256, 256, 128, 2, 2, false, true, false>("gemm_i8_mfma_256x256")
+              : make_choice<MMA_I8, 256, 256, 128, 2, 2, false, false, false>("gemm_i8_mfma_256x256");
+      return true;
+    }
+    if (fits(128, 128, 128)) {
+      *c = br ? make_choice<MMA_I8, 128, 128, 128, 2, 2, false, true, false>("gemm_i8_mfma_128x128")
+              : make_choice<MMA_I8, 128, 128, 128, 2, 2, false, false, false>("gemm_i8_mfma_128x128");
+      return true;
+    }
+    return false;
+}
+
+}  // namespace ryft

@@ -1,0 +1,21 @@
+// Host-side launchers for the gfx950 kernel library. Every launcher validates the shapes its kernels assume before
+// launching and throws ryft::Status on anything it cannot run.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include "../kernel_abi.h"
+
+namespace ryft {
+
+void launch_elementwise(const EwProgram& p, hipStream_t stream);
+void launch_reduce(const ReduceArgs& a, hipStream_t stream);
+void launch_gemm(const GemmArgs& a, hipStream_t stream);
+void launch_attention(const AttnArgs& a, hipStream_t stream);
+
+// Name of the GEMM kernel launch_gemm() picks for these arguments (used for profiling labels).
+const char* gemm_kernel_name(const GemmArgs& a);
+// Head dims the fused attention kernel supports.
+bool attention_supported(int head_dim);
+
+}  // namespace ryft

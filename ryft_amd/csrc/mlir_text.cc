@@ -1,0 +1,999 @@
+// StableHLO MLIR text front-end: parses `func.func @main` in either the pretty (custom) syntax that ryft-mlir's
+// printer emits, or MLIR's generic `"stablehlo.op"(...) <{...}>` syntax, into a typed Graph.
+//
+// Printed forms this parser accepts are the ones pinned by ryft-mlir's printer tests:
+//   dot_general       crates/ryft-mlir/src/dialects/stable_hlo/operations/linear_algebra.rs:2240-2263
+//   reduce            .../functional.rs:529-541       transpose .../manipulation.rs:2022
+//   broadcast_in_dim  .../manipulation.rs:2154        select    .../control_flow.rs:596
+//   iota              .../miscellaneous.rs:1181       convert   .../casting.rs:456
+//   compare           .../comparison.rs:500, control_flow.rs:534
+#include <cctype>
+#include <cmath>
+#include <cstdlib>
+#include <functional>
+#include <sstream>
+#include <unordered_map>
+
+#include "ir.h"
+
+namespace ryft {
+
+std::string TensorType::str() const {
+  std::ostringstream os;
+  os << "tensor<";
+  for (auto d : shape) os << d << "x";
+  os << dtype_name(dtype) << ">";
+  return os.str();
+}
+
+const char* op_name(Op op) {
+  switch (op) {
+    case Op::Parameter: return "parameter";
+    case Op::Constant: return "constant";
+    case Op::Negate: return "negate";
+    case Op::Abs: return "abs";
+    case Op::Exp: return "exponential";
+    case Op::Log: return "log";
+    case Op::Rsqrt: return "rsqrt";
+    case Op::Sqrt: return "sqrt";
+    case Op::Tanh: return "tanh";
+    case Op::Logistic: return "logistic";
+    case Op::Not: return "not";
+    case Op::Convert: return "convert";
+    case Op::Floor: return "floor";
+    case Op::Ceil: return "ceil";
+    case Op::Sign: return "sign";
+    case Op::Expm1: return "exponential_minus_one";
+    case Op::Log1p: return "log_plus_one";
+    case Op::Add: return "add";
+    case Op::Subtract: return "subtract";
+    case Op::Multiply: return "multiply";
+    case Op::Divide: return "divide";
+    case Op::Maximum: return "maximum";
+    case Op::Minimum: return "minimum";
+    case Op::Power: return "power";
+    case Op::Remainder: return "remainder";
+    case Op::And: return "and";
+    case Op::Or: return "or";
+    case Op::Xor: return "xor";
+    case Op::Compare: return "compare";
+    case Op::Select: return "select";
+    case Op::Clamp: return "clamp";
+    case Op::BroadcastInDim: return "broadcast_in_dim";
+    case Op::Transpose: return "transpose";
+    case Op::Reshape: return "reshape";
+    case Op::Iota: return "iota";
+    case Op::DotGeneral: return "dot_general";
+    case Op::Reduce: return "reduce";
+  }
+  return "?";
+}
+
+bool op_is_elementwise(Op op) {
+  switch (op) {
+    case Op::Negate: case Op::Abs: case Op::Exp: case Op::Log: case Op::Rsqrt: case Op::Sqrt: case Op::Tanh:
+    case Op::Logistic: case Op::Not: case Op::Convert: case Op::Floor: case Op::Ceil: case Op::Sign: case Op::Expm1:
+    case Op::Log1p: case Op::Add: case Op::Subtract: case Op::Multiply: case Op::Divide: case Op::Maximum:
+    case Op::Minimum: case Op::Power: case Op::Remainder: case Op::And: case Op::Or: case Op::Xor: case Op::Compare:
+    case Op::Select: case Op::Clamp:
+      return true;
+    default:
+      return false;
+  }
+}
+
+std::vector<std::vector<int>> Graph::users() const {
+  std::vector<std::vector<int>> u(nodes.size());
+  for (size_t i = 0; i < nodes.size(); ++i)
+    for (int o : nodes[i].operands) u[o].push_back((int)i);
+  return u;
+}
+
+std::string Graph::dump() const {
+  std::ostringstream os;
+  for (size_t i = 0; i < nodes.size(); ++i) {
+    const Node& n = nodes[i];
+    os << "%" << i << " = " << op_name(n.op) << "(";
+    for (size_t j = 0; j < n.operands.size(); ++j) os << (j ? ", " : "") << "%" << n.operands[j];
+    os << ") : " << n.type.str();
+    if (!n.dims.empty()) os << " dims=" << shape_str(n.dims);
+    os << "\n";
+  }
+  os << "return";
+  for (int r : results) os << " %" << r;
+  os << "\n";
+  return os.str();
+}
+
+bool is_mlir_bytecode(const char* data, size_t size) {
+  // MLIR bytecode files start with the magic "ML\xEFR".
+  return size >= 4 && data[0] == 'M' && data[1] == 'L' && (unsigned char)data[2] == 0xEF && data[3] == 'R';
+}
+
+double literal_as_double(const Node& n, int64_t index) {
+  if (n.splat) index = 0;
+  const uint8_t* p = n.literal.data() + index * dtype_size(n.type.dtype);
+  switch (n.type.dtype) {
+    case DType::F32: { float v; memcpy(&v, p, 4); return v; }
+    case DType::F64: { double v; memcpy(&v, p, 8); return v; }
+    case DType::BF16: { uint16_t v; memcpy(&v, p, 2); return bf16_to_f32(v); }
+    case DType::F16: { uint16_t v; memcpy(&v, p, 2); return f16_to_f32(v); }
+    case DType::F8E4M3FN: return f8e4m3fn_to_f32(*p);
+    case DType::F8E5M2: return f8e5m2_to_f32(*p);
+    default: return (double)literal_as_int(n, index);
+  }
+}
+
+int64_t literal_as_int(const Node& n, int64_t index) {
+  if (n.splat) index = 0;
+  const uint8_t* p = n.literal.data() + index * dtype_size(n.type.dtype);
+  switch (n.type.dtype) {
+    case DType::PRED: case DType::U8: return *p;
+    case DType::S8: return (int8_t)*p;
+    case DType::S16: { int16_t v; memcpy(&v, p, 2); return v; }
+    case DType::U16: { uint16_t v; memcpy(&v, p, 2); return v; }
+    case DType::S32: { int32_t v; memcpy(&v, p, 4); return v; }
+    case DType::U32: { uint32_t v; memcpy(&v, p, 4); return v; }
+    case DType::S64: case DType::U64: { int64_t v; memcpy(&v, p, 8); return v; }
+    default: return (int64_t)literal_as_double(n, index);
+  }
+}
+
+namespace {
+
+// ------------------------------------------------------------------------------------------------ lexer helpers
+class Cursor {
+ public:
+  explicit Cursor(const std::string& s) : s_(s) {}
+  size_t pos() const { return p_; }
+  void set_pos(size_t p) { p_ = p; }
+  bool eof() { skip_ws(); return p_ >= s_.size(); }
+  char peek() { skip_ws(); return p_ < s_.size() ? s_[p_] : '\0'; }
+  char peek_raw() const { return p_ < s_.size() ? s_[p_] : '\0'; }
+
+  void skip_ws() {
+    for (;;) {
+      while (p_ < s_.size() && isspace((unsigned char)s_[p_])) ++p_;
+      if (p_ + 1 < s_.size() && s_[p_] == '/' && s_[p_ + 1] == '/') {
+        while (p_ < s_.size() && s_[p_] != '\n') ++p_;
+        continue;
+      }
+      // `loc(...)` trailers carry source locations only.
+      if (s_.compare(p_, 4, "loc(") == 0 && (p_ == 0 || !is_ident_char(s_[p_ - 1]))) {
+        p_ += 3;
+        skip_balanced('(', ')');
+        continue;
+      }
+      break;
+    }
+  }
+  static bool is_ident_char(char c) { return isalnum((unsigned char)c) || c == '_' || c == '.' || c == '$' || c == '-'; }
+
+  bool try_consume(const char* tok) {
+    skip_ws();
+    size_t n = strlen(tok);
+    if (s_.compare(p_, n, tok) != 0) return false;
+    // keywords must not run into an identifier
+    if (isalpha((unsigned char)tok[n - 1]) && p_ + n < s_.size() && is_ident_char(s_[p_ + n])) return false;
+    p_ += n;
+    return true;
+  }
+  void expect(const char* tok) {
+    if (!try_consume(tok)) error(std::string("expected '") + tok + "'");
+  }
+  std::string ident() {
+    skip_ws();
+    size_t b = p_;
+    while (p_ < s_.size() && (is_ident_char(s_[p_]))) ++p_;
+    if (b == p_) error("expected identifier");
+    return s_.substr(b, p_ - b);
+  }
+  // %name, %name#k, or @name
+  std::string sigil_name(char sigil) {
+    skip_ws();
+    if (peek_raw() != sigil) error(std::string("expected '") + sigil + "'");
+    size_t b = p_++;
+    while (p_ < s_.size() && (is_ident_char(s_[p_]) || s_[p_] == '#')) ++p_;
+    return s_.substr(b, p_ - b);
+  }
+  std::string quoted() {
+    skip_ws();
+    if (peek_raw() != '"') error("expected string");
+    size_t b = ++p_;
+    while (p_ < s_.size() && s_[p_] != '"') p_ += (s_[p_] == '\\') ? 2 : 1;
+    std::string r = s_.substr(b, p_ - b);
+    ++p_;
+    return r;
+  }
+  int64_t integer() {
+    skip_ws();
+    size_t b = p_;
+    if (p_ < s_.size() && (s_[p_] == '-' || s_[p_] == '+')) ++p_;
+    while (p_ < s_.size() && isdigit((unsigned char)s_[p_])) ++p_;
+    if (b == p_) error("expected integer");
+    return std::strtoll(s_.c_str() + b, nullptr, 10);
+  }
+  // Raw text up to the bracket matching the one just consumed (nesting aware, strings skipped).
+  std::string skip_balanced(char open, char close) {
+    size_t b = p_;
+    int depth = 1;
+    while (p_ < s_.size() && depth > 0) {
+      char c = s_[p_];
+      if (c == '"') { ++p_; while (p_ < s_.size() && s_[p_] != '"') p_ += (s_[p_] == '\\') ? 2 : 1; }
+      else if (c == open) ++depth;
+      else if (c == close) --depth;
+      ++p_;
+    }
+    if (depth) error("unbalanced brackets");
+    return s_.substr(b, p_ - b - 1);
+  }
+  // Angle-bracket body for types/attributes: `<` already consumed. `->` inside is not a closing bracket.
+  std::string angle_body() {
+    size_t b = p_;
+    int depth = 1;
+    while (p_ < s_.size() && depth > 0) {
+      char c = s_[p_];
+      if (c == '"') { ++p_; while (p_ < s_.size() && s_[p_] != '"') p_ += (s_[p_] == '\\') ? 2 : 1; }
+      else if (c == '-' && p_ + 1 < s_.size() && s_[p_ + 1] == '>') { p_ += 2; continue; }
+      else if (c == '<') ++depth;
+      else if (c == '>') --depth;
+      ++p_;
+    }
+    if (depth) error("unbalanced '<'");
+    return s_.substr(b, p_ - b - 1);
+  }
+  [[noreturn]] void error(const std::string& what) const {
+    size_t line = 1, col = 1;
+    for (size_t i = 0; i < p_ && i < s_.size(); ++i) { if (s_[i] == '\n') { ++line; col = 1; } else ++col; }
+    size_t e = s_.find('\n', p_);
+    std::string ctx = s_.substr(p_, std::min<size_t>(60, (e == std::string::npos ? s_.size() : e) - p_));
+    invalid("MLIR parse error at " + std::to_string(line) + ":" + std::to_string(col) + ": " + what + " near '" + ctx + "'");
+  }
+  const std::string& text() const { return s_; }
+
+ private:
+  const std::string& s_;
+  size_t p_ = 0;
+};
+
+DType parse_element_type(const std::string& t) {
+  static const std::unordered_map<std::string, DType> m = {
+      {"i1", DType::PRED},   {"i8", DType::S8},     {"i16", DType::S16},  {"i32", DType::S32},
+      {"i64", DType::S64},   {"ui8", DType::U8},    {"ui16", DType::U16}, {"ui32", DType::U32},
+      {"ui64", DType::U64},  {"f16", DType::F16},   {"f32", DType::F32},  {"f64", DType::F64},
+      {"bf16", DType::BF16}, {"f8E4M3FN", DType::F8E4M3FN}, {"f8E5M2", DType::F8E5M2},
+      {"si8", DType::S8},    {"si16", DType::S16},  {"si32", DType::S32}, {"si64", DType::S64},
+  };
+  auto it = m.find(t);
+  if (it == m.end()) unimplemented("unsupported element type '" + t + "'");
+  return it->second;
+}
+
+// `tensor<2x3xf32>` body → TensorType
+TensorType parse_tensor_body(const std::string& body) {
+  TensorType tt;
+  std::string b = body;
+  size_t comma = b.find(',');
+  if (comma != std::string::npos) b = b.substr(0, comma);  // drop an encoding, e.g. `#stablehlo.bounds<...>`
+  while (!b.empty() && isspace((unsigned char)b.back())) b.pop_back();
+  size_t i = 0;
+  while (i < b.size() && isspace((unsigned char)b[i])) ++i;
+  for (;;) {
+    size_t j = i;
+    while (j < b.size() && isdigit((unsigned char)b[j])) ++j;
+    if (j > i && j < b.size() && b[j] == 'x') {
+      tt.shape.push_back(std::strtoll(b.c_str() + i, nullptr, 10));
+      i = j + 1;
+      continue;
+    }
+    if (i < b.size() && b[i] == '?') unimplemented("dynamic shapes are not supported: tensor<" + body + ">");
+    break;
+  }
+  tt.dtype = parse_element_type(b.substr(i));
+  return tt;
+}
+
+TensorType parse_type(Cursor& c) {
+  c.skip_ws();
+  if (c.try_consume("tensor<")) return parse_tensor_body(c.angle_body());
+  // bare scalar element type, e.g. in reducer block arguments of some printers
+  std::string id = c.ident();
+  TensorType tt;
+  tt.dtype = parse_element_type(id);
+  return tt;
+}
+
+// `(t1, t2) -> t3`, `(t1) -> (t2, t3)`, or a bare type list `t1, t2`.
+struct FnType {
+  std::vector<TensorType> inputs, results;
+  bool has_arrow = false;
+};
+FnType parse_fn_or_types(Cursor& c) {
+  FnType ft;
+  c.skip_ws();
+  if (c.peek() == '(') {
+    c.expect("(");
+    if (!c.try_consume(")")) {
+      do { ft.inputs.push_back(parse_type(c)); } while (c.try_consume(","));
+      c.expect(")");
+    }
+    c.expect("->");
+    ft.has_arrow = true;
+    if (c.try_consume("(")) {
+      if (!c.try_consume(")")) {
+        do { ft.results.push_back(parse_type(c)); } while (c.try_consume(","));
+        c.expect(")");
+      }
+    } else {
+      ft.results.push_back(parse_type(c));
+    }
+    return ft;
+  }
+  do { ft.inputs.push_back(parse_type(c)); } while (c.try_consume(","));
+  return ft;
+}
+
+std::vector<int64_t> parse_int_list_text(const std::string& raw) {
+  // accepts "[0, 1]", "array<i64: 0, 1>", "dense<[0, 1]> : tensor<2xi64>", "dense<1> : ..."
+  std::string s = raw;
+  size_t colon_arr = s.find("array<");
+  if (colon_arr != std::string::npos) {
+    size_t c = s.find(':', colon_arr);
+    size_t e = s.rfind('>');
+    s = (c == std::string::npos || c > e) ? std::string() : s.substr(c + 1, e - c - 1);
+  } else {
+    size_t d = s.find("dense<");
+    if (d != std::string::npos) {
+      size_t e = s.find('>', d);
+      s = s.substr(d + 6, e - d - 6);
+    }
+  }
+  std::vector<int64_t> out;
+  size_t i = 0;
+  while (i < s.size()) {
+    if (isdigit((unsigned char)s[i]) || (s[i] == '-' && i + 1 < s.size() && isdigit((unsigned char)s[i + 1]))) {
+      char* end;
+      out.push_back(std::strtoll(s.c_str() + i, &end, 10));
+      i = end - s.c_str();
+    } else {
+      ++i;
+    }
+  }
+  return out;
+}
+
+// ------------------------------------------------------------------------------------------------ literals
+void append_element(std::vector<uint8_t>& out, DType t, const std::string& tok) {
+  std::string v = tok;
+  bool is_hex = v.size() > 2 && v[0] == '0' && (v[1] == 'x' || v[1] == 'X');
+  size_t sz = dtype_size(t);
+  if (is_hex) {
+    uint64_t bits = std::strtoull(v.c_str() + 2, nullptr, 16);
+    for (size_t k = 0; k < sz; ++k) out.push_back((uint8_t)(bits >> (8 * k)));
+    return;
+  }
+  if (v == "true" || v == "false") {
+    uint64_t b = (v == "true");
+    for (size_t k = 0; k < sz; ++k) out.push_back(k == 0 ? (uint8_t)b : 0);
+    return;
+  }
+  if (dtype_is_float(t)) {
+    double d;
+    if (v == "inf" || v == "+inf") d = INFINITY;
+    else if (v == "-inf") d = -INFINITY;
+    else if (v == "nan" || v == "-nan") d = NAN;
+    else d = std::strtod(v.c_str(), nullptr);
+    uint8_t buf[8];
+    switch (t) {
+      case DType::F32: { float f = (float)d; memcpy(buf, &f, 4); break; }
+      case DType::F64: memcpy(buf, &d, 8); break;
+      case DType::BF16: { uint16_t h = f32_to_bf16_rne((float)d); memcpy(buf, &h, 2); break; }
+      case DType::F16: { uint16_t h = f32_to_f16_rne((float)d); memcpy(buf, &h, 2); break; }
+      case DType::F8E4M3FN: buf[0] = f32_to_f8e4m3fn_rne((float)d); break;
+      case DType::F8E5M2: buf[0] = f32_to_f8e5m2_rne((float)d); break;
+      default: break;
+    }
+    out.insert(out.end(), buf, buf + sz);
+    return;
+  }
+  int64_t iv = std::strtoll(v.c_str(), nullptr, 10);
+  if (v.find_first_of(".eE") != std::string::npos) iv = (int64_t)std::strtod(v.c_str(), nullptr);
+  for (size_t k = 0; k < sz; ++k) out.push_back((uint8_t)((uint64_t)iv >> (8 * k)));
+}
+
+// `dense<...>` payload (text between the angle brackets) for a tensor of type `tt`.
+void parse_dense(const std::string& payload, const TensorType& tt, Node& n) {
+  std::string p = payload;
+  size_t a = p.find_first_not_of(" \t\n");
+  p = (a == std::string::npos) ? std::string() : p.substr(a);
+  while (!p.empty() && isspace((unsigned char)p.back())) p.pop_back();
+  int64_t count = tt.elements();
+  size_t sz = dtype_size(tt.dtype);
+  n.literal.clear();
+  if (!p.empty() && p[0] == '"') {  // hex blob "0x...." of all elements
+    std::string hex = p.substr(1, p.size() - 2);
+    if (hex.size() < 2 || hex[0] != '0' || (hex[1] != 'x' && hex[1] != 'X')) invalid("bad dense hex blob");
+    hex = hex.substr(2);
+    for (size_t i = 0; i + 1 < hex.size(); i += 2) n.literal.push_back((uint8_t)std::strtoul(hex.substr(i, 2).c_str(), nullptr, 16));
+    if ((int64_t)n.literal.size() == (int64_t)sz) { n.splat = true; return; }
+    if ((int64_t)n.literal.size() != count * (int64_t)sz) invalid("dense hex blob has the wrong size");
+    n.splat = false;
+    return;
+  }
+  // split on brackets / commas
+  std::vector<std::string> toks;
+  std::string cur;
+  for (char ch : p) {
+    if (ch == '[' || ch == ']' || ch == ',' || isspace((unsigned char)ch)) {
+      if (!cur.empty()) { toks.push_back(cur); cur.clear(); }
+    } else {
+      cur.push_back(ch);
+    }
+  }
+  if (!cur.empty()) toks.push_back(cur);
+  for (auto& t : toks) append_element(n.literal, tt.dtype, t);
+  if ((int64_t)toks.size() == 1) { n.splat = true; return; }
+  if ((int64_t)toks.size() != count) invalid("dense literal has " + std::to_string(toks.size()) + " elements, expected " + std::to_string(count));
+  n.splat = false;
+}
+
+// ------------------------------------------------------------------------------------------------ parser
+struct OpSyntax {  // everything an op line carries, in generic form
+  std::string name;
+  std::vector<std::string> results;  // SSA names
+  std::vector<std::string> operands;
+  std::map<std::string, std::string> attrs;  // raw attribute text
+  FnType type;
+  // reduce body, when given as a region
+  std::string body_op;
+};
+
+class Parser {
+ public:
+  explicit Parser(const std::string& text) : c_(text) {}
+
+  Graph parse(const std::string& entry) {
+    // find `func.func [visibility] @entry`
+    const std::string& s = c_.text();
+    size_t pos = 0;
+    for (;;) {
+      pos = s.find("func.func", pos);
+      if (pos == std::string::npos) invalid("no `func.func @" + entry + "` in the program");
+      c_.set_pos(pos + 9);
+      c_.try_consume("public") || c_.try_consume("private");
+      c_.skip_ws();
+      if (c_.peek_raw() == '@') {
+        std::string nm = c_.sigil_name('@');
+        if (nm == "@" + entry) break;
+      }
+      pos += 9;
+    }
+    graph_.name = entry;
+    parse_signature();
+    c_.expect("{");
+    parse_block_body(/*top=*/true);
+    return std::move(graph_);
+  }
+
+ private:
+  void parse_signature() {
+    c_.expect("(");
+    if (!c_.try_consume(")")) {
+      do {
+        std::string nm = c_.sigil_name('%');
+        c_.expect(":");
+        TensorType tt = parse_type(c_);
+        if (c_.peek() == '{') { c_.expect("{"); c_.skip_balanced('{', '}'); }
+        Node n;
+        n.op = Op::Parameter;
+        n.type = tt;
+        n.param_index = (int)graph_.params.size();
+        n.debug = nm;
+        int id = add(std::move(n));
+        graph_.params.push_back(id);
+        names_[nm] = id;
+      } while (c_.try_consume(","));
+      c_.expect(")");
+    }
+    if (c_.try_consume("->")) {
+      if (c_.try_consume("(")) {
+        if (!c_.try_consume(")")) {
+          do {
+            result_types_.push_back(parse_type(c_));
+            if (c_.peek() == '{') { c_.expect("{"); c_.skip_balanced('{', '}'); }
+          } while (c_.try_consume(","));
+          c_.expect(")");
+        }
+      } else {
+        result_types_.push_back(parse_type(c_));  // a bare result type carries no attribute dictionary
+      }
+    }
+    if (c_.try_consume("attributes")) { c_.expect("{"); c_.skip_balanced('{', '}'); }
+  }
+
+  int add(Node n) {
+    graph_.nodes.push_back(std::move(n));
+    return (int)graph_.nodes.size() - 1;
+  }
+
+  int value(const std::string& nm) {
+    auto it = names_.find(nm);
+    if (it == names_.end()) {
+      // `%x#0` for single-result ops
+      size_t h = nm.find('#');
+      if (h != std::string::npos && nm.substr(h) == "#0") {
+        it = names_.find(nm.substr(0, h));
+        if (it != names_.end()) return it->second;
+      }
+      c_.error("use of undefined value " + nm);
+    }
+    return it->second;
+  }
+
+  void parse_block_body(bool top) {
+    for (;;) {
+      if (c_.try_consume("}")) return;
+      if (c_.eof()) c_.error("unexpected end of input in function body");
+      if (c_.try_consume("func.return") || c_.try_consume("return") || c_.try_consume("stablehlo.return") ||
+          c_.try_consume("\"func.return\"") || c_.try_consume("\"stablehlo.return\"")) {
+        std::vector<std::string> vals;
+        bool generic = c_.try_consume("(");
+        c_.skip_ws();
+        if (c_.peek_raw() == '%') {
+          do { vals.push_back(c_.sigil_name('%')); } while (c_.try_consume(","));
+        }
+        if (generic) c_.expect(")");
+        if (c_.try_consume(":")) parse_fn_or_types(c_);
+        if (top) {
+          for (auto& v : vals) graph_.results.push_back(value(v));
+          if (!result_types_.empty() && result_types_.size() != graph_.results.size())
+            invalid("return arity does not match the function signature");
+        }
+        continue;
+      }
+      parse_op_line();
+    }
+  }
+
+  void parse_attr_dict(std::map<std::string, std::string>& attrs) {
+    // after '{' or '<{' consumed; parse `name = value, ...` up to the closing '}'
+    for (;;) {
+      if (c_.try_consume("}")) return;
+      std::string key = c_.ident();
+      std::string val;
+      if (c_.try_consume("=")) val = raw_attr_value();
+      attrs[key] = val;
+      c_.try_consume(",");
+    }
+  }
+
+  // Raw text of one attribute value, stopping at a top-level ',' or '}' (and ':' for the keyword attributes of the
+  // pretty syntax, where the op's type follows).
+  std::string raw_attr_value(bool stop_at_colon = false) {
+    c_.skip_ws();
+    size_t b = c_.pos();
+    const std::string& s = c_.text();
+    size_t p = b;
+    int depth = 0;
+    while (p < s.size()) {
+      char ch = s[p];
+      if (ch == '"') { ++p; while (p < s.size() && s[p] != '"') p += (s[p] == '\\') ? 2 : 1; ++p; continue; }
+      if (ch == '-' && p + 1 < s.size() && s[p + 1] == '>') { p += 2; continue; }
+      if (ch == '<' || ch == '[' || ch == '(' || ch == '{') ++depth;
+      else if (ch == '>' || ch == ']' || ch == ')' || ch == '}') {
+        if (depth == 0) break;
+        --depth;
+      } else if (ch == ',' && depth == 0) break;
+      else if (ch == ':' && depth == 0 && stop_at_colon) break;
+      ++p;
+    }
+    c_.set_pos(p);
+    return s.substr(b, p - b);
+  }
+
+  // Reducer region: returns the binary op the body applies to its two block arguments.
+  std::string parse_reducer_region() {
+    // generic: ({ ^bb0(%a: tensor<f32>, %b: tensor<f32>): %r = op %a, %b ...; return %r })
+    // pretty:  reducer(%a: tensor<f32>, %b: tensor<f32>) { ... }
+    std::string body_op;
+    size_t depth0 = 0;
+    (void)depth0;
+    std::map<std::string, int> saved = names_;
+    // block args
+    if (c_.try_consume("^bb0") || c_.try_consume("^bb")) {
+      if (c_.peek() != '(') c_.ident();
+    }
+    c_.expect("(");
+    std::vector<std::string> args;
+    do {
+      args.push_back(c_.sigil_name('%'));
+      c_.expect(":");
+      parse_type(c_);
+    } while (c_.try_consume(","));
+    c_.expect(")");
+    c_.try_consume(":");
+    c_.try_consume("{");
+    // body: expect exactly one binary op then a return
+    std::string op_name_s;
+    std::string result_name;
+    for (;;) {
+      if (c_.try_consume("stablehlo.return") || c_.try_consume("\"stablehlo.return\"") || c_.try_consume("return")) {
+        bool g = c_.try_consume("(");
+        std::string rv = c_.sigil_name('%');
+        if (g) c_.expect(")");
+        if (c_.try_consume(":")) parse_fn_or_types(c_);
+        if (rv != result_name) unimplemented("reduce body must return its single binary op result");
+        break;
+      }
+      if (!op_name_s.empty()) unimplemented("reduce bodies with more than one op are not supported");
+      result_name = c_.sigil_name('%');
+      c_.expect("=");
+      c_.skip_ws();
+      bool quoted = c_.peek_raw() == '"';
+      op_name_s = quoted ? c_.quoted() : c_.ident();
+      if (quoted) c_.expect("(");
+      std::string a = c_.sigil_name('%');
+      c_.expect(",");
+      std::string b = c_.sigil_name('%');
+      if (quoted) c_.expect(")");
+      if (!((a == args[0] && b == args[1]) || (a == args[1] && b == args[0])))
+        unimplemented("reduce body must combine its two block arguments");
+      c_.expect(":");
+      parse_fn_or_types(c_);
+    }
+    c_.try_consume("}");
+    names_ = saved;
+    return op_name_s;
+  }
+
+  void parse_op_line() {
+    OpSyntax os;
+    // results
+    c_.skip_ws();
+    if (c_.peek_raw() == '%') {
+      do {
+        std::string nm = c_.sigil_name('%');
+        if (c_.try_consume(":")) {
+          int64_t k = c_.integer();
+          if (k != 1) unimplemented("multi-result ops are not supported (" + nm + ")");
+        }
+        os.results.push_back(nm);
+      } while (c_.try_consume(","));
+      c_.expect("=");
+    }
+    c_.skip_ws();
+    bool generic = c_.peek_raw() == '"';
+    os.name = generic ? c_.quoted() : c_.ident();
+    if (os.name.rfind("stablehlo.", 0) == 0) os.name = os.name.substr(10);
+    else if (os.name.rfind("mhlo.", 0) == 0) os.name = os.name.substr(5);
+    else if (os.name.rfind("chlo.", 0) == 0) unimplemented("chlo op '" + os.name + "' is not supported");
+    else unimplemented("op '" + os.name + "' is not supported by the MI355X plugin");
+
+    if (generic) parse_generic(os);
+    else parse_pretty(os);
+    build(os);
+  }
+
+  void parse_generic(OpSyntax& os) {
+    c_.expect("(");
+    if (!c_.try_consume(")")) {
+      do { os.operands.push_back(c_.sigil_name('%')); } while (c_.try_consume(","));
+      c_.expect(")");
+    }
+    if (c_.try_consume("<{")) parse_attr_dict(os.attrs), c_.expect(">");
+    if (c_.try_consume("(")) {  // regions
+      c_.expect("{");
+      os.body_op = parse_reducer_region();
+      c_.expect(")");
+    }
+    if (c_.try_consume("{")) parse_attr_dict(os.attrs);
+    c_.expect(":");
+    os.type = parse_fn_or_types(c_);
+  }
+
+  void parse_pretty(OpSyntax& os) {
+    const std::string& n = os.name;
+    auto operand_list = [&]() {
+      c_.skip_ws();
+      while (c_.peek_raw() == '%') {
+        os.operands.push_back(c_.sigil_name('%'));
+        if (!c_.try_consume(",")) break;
+        c_.skip_ws();
+      }
+    };
+    if (n == "constant") {
+      // `stablehlo.constant dense<...> : tensor<...>` (the literal carries its own type)
+      if (c_.try_consume("{")) parse_attr_dict(os.attrs);
+      c_.expect("dense<");
+      os.attrs["value"] = "dense<" + c_.angle_body() + ">";
+      c_.expect(":");
+      os.type.results.push_back(parse_type(c_));
+      return;
+    }
+    if (n == "iota") {
+      c_.expect("dim");
+      c_.expect("=");
+      os.attrs["iota_dimension"] = std::to_string(c_.integer());
+      c_.expect(":");
+      os.type.results.push_back(parse_type(c_));
+      return;
+    }
+    if (n == "reduce") {
+      // stablehlo.reduce(%x init: %i) [applies <op>] across dimensions = [..] : fn  [reducer(...) {...}]
+      c_.expect("(");
+      os.operands.push_back(c_.sigil_name('%'));
+      c_.expect("init:");
+      os.operands.push_back(c_.sigil_name('%'));
+      c_.expect(")");
+      if (c_.try_consume(",")) unimplemented("variadic reduce is not supported");
+      if (c_.try_consume("applies")) os.body_op = c_.ident();
+      c_.expect("across");
+      c_.expect("dimensions");
+      c_.expect("=");
+      c_.expect("[");
+      os.attrs["dimensions"] = "[" + c_.skip_balanced('[', ']') + "]";
+      if (c_.try_consume("{")) parse_attr_dict(os.attrs);
+      c_.expect(":");
+      os.type = parse_fn_or_types(c_);
+      if (os.body_op.empty()) {
+        c_.expect("reducer");
+        os.body_op = parse_reducer_region();
+      }
+      return;
+    }
+    if (n == "compare") {
+      os.attrs["comparison_direction"] = c_.ident();
+      c_.expect(",");
+      os.operands.push_back(c_.sigil_name('%'));
+      c_.expect(",");
+      os.operands.push_back(c_.sigil_name('%'));
+      if (c_.try_consume(",")) os.attrs["compare_type"] = c_.ident();
+      if (c_.try_consume("{")) parse_attr_dict(os.attrs);
+      c_.expect(":");
+      os.type = parse_fn_or_types(c_);
+      return;
+    }
+    operand_list();
+    // keyword attributes before the ':' (dims = [...], batching_dims = [..] x [..], precision = [...], algorithm = <...>)
+    for (;;) {
+      c_.skip_ws();
+      if (c_.peek_raw() == ':' || c_.peek_raw() == '{') break;
+      std::string key = c_.ident();
+      c_.expect("=");
+      if (key == "batching_dims" || key == "contracting_dims") {
+        c_.expect("[");
+        std::string l = c_.skip_balanced('[', ']');
+        c_.expect("x");
+        c_.expect("[");
+        std::string r = c_.skip_balanced('[', ']');
+        os.attrs[key + ".lhs"] = "[" + l + "]";
+        os.attrs[key + ".rhs"] = "[" + r + "]";
+      } else {
+        os.attrs[key] = raw_attr_value(/*stop_at_colon=*/true);
+      }
+      c_.try_consume(",");
+    }
+    if (c_.try_consume("{")) parse_attr_dict(os.attrs);
+    c_.expect(":");
+    os.type = parse_fn_or_types(c_);
+  }
+
+  static CmpDir parse_dir(const std::string& raw) {
+    static const char* names[] = {"EQ", "NE", "GE", "GT", "LE", "LT"};
+    for (int i = 0; i < 6; ++i)
+      if (raw.find(names[i]) != std::string::npos) return (CmpDir)i;
+    invalid("bad comparison direction '" + raw + "'");
+  }
+  static CmpType parse_cmp_type(const std::string& raw) {
+    if (raw.find("TOTALORDER") != std::string::npos) return CmpType::TOTALORDER;
+    if (raw.find("UNSIGNED") != std::string::npos) return CmpType::UNSIGNED;
+    if (raw.find("SIGNED") != std::string::npos) return CmpType::SIGNED;
+    if (raw.find("FLOAT") != std::string::npos) return CmpType::FLOAT;
+    return CmpType::NOTYPE;
+  }
+
+  // Result type of an op: explicit fn-type result, or (for `op %a, %b : tensor<..>`) the single listed type.
+  TensorType result_type(const OpSyntax& os) {
+    if (!os.type.results.empty()) return os.type.results[0];
+    if (!os.type.inputs.empty()) return os.type.inputs.back();
+    c_.error("op without a type");
+  }
+
+  void build(const OpSyntax& os) {
+    static const std::unordered_map<std::string, Op> simple = {
+        {"negate", Op::Negate},       {"abs", Op::Abs},         {"exponential", Op::Exp},
+        {"log", Op::Log},             {"rsqrt", Op::Rsqrt},     {"sqrt", Op::Sqrt},
+        {"tanh", Op::Tanh},           {"logistic", Op::Logistic}, {"not", Op::Not},
+        {"convert", Op::Convert},     {"floor", Op::Floor},     {"ceil", Op::Ceil},
+        {"sign", Op::Sign},           {"exponential_minus_one", Op::Expm1}, {"log_plus_one", Op::Log1p},
+        {"add", Op::Add},             {"subtract", Op::Subtract}, {"multiply", Op::Multiply},
+        {"divide", Op::Divide},       {"maximum", Op::Maximum}, {"minimum", Op::Minimum},
+        {"power", Op::Power},         {"remainder", Op::Remainder}, {"and", Op::And},
+        {"or", Op::Or},               {"xor", Op::Xor},         {"select", Op::Select},
+        {"clamp", Op::Clamp},         {"reshape", Op::Reshape}, {"bitcast_convert", Op::Convert},
+    };
+    Node n;
+    n.debug = os.results.empty() ? std::string() : os.results[0];
+    for (auto& o : os.operands) n.operands.push_back(value(o));
+    n.type = result_type(os);
+    const std::string& nm = os.name;
+    auto get = [&](const char* k) -> std::string {
+      auto it = os.attrs.find(k);
+      return it == os.attrs.end() ? std::string() : it->second;
+    };
+    if (nm == "bitcast_convert") unimplemented("bitcast_convert is not supported");
+    auto it = simple.find(nm);
+    if (it != simple.end()) {
+      n.op = it->second;
+    } else if (nm == "constant") {
+      n.op = Op::Constant;
+      std::string v = get("value");
+      size_t d = v.find("dense<");
+      if (d == std::string::npos) unimplemented("constant value '" + v + "' is not a dense literal");
+      Cursor vc(v);
+      vc.set_pos(d + 6);
+      std::string payload = vc.angle_body();
+      parse_dense(payload, n.type, n);
+    } else if (nm == "iota") {
+      n.op = Op::Iota;
+      n.iota_dim = parse_int_list_text(get("iota_dimension")).at(0);
+    } else if (nm == "broadcast_in_dim") {
+      n.op = Op::BroadcastInDim;
+      std::string d = get("dims");
+      if (d.empty()) d = get("broadcast_dimensions");
+      n.dims = parse_int_list_text(d);
+    } else if (nm == "transpose") {
+      n.op = Op::Transpose;
+      std::string d = get("dims");
+      if (d.empty()) d = get("permutation");
+      n.dims = parse_int_list_text(d);
+    } else if (nm == "compare") {
+      n.op = Op::Compare;
+      n.cmp = parse_dir(get("comparison_direction"));
+      n.cmp_type = parse_cmp_type(get("compare_type"));
+    } else if (nm == "reduce") {
+      n.op = Op::Reduce;
+      if (n.operands.size() != 2) unimplemented("variadic reduce is not supported");
+      n.dims = parse_int_list_text(get("dimensions"));
+      std::string b = os.body_op;
+      if (b.rfind("stablehlo.", 0) == 0) b = b.substr(10);
+      if (b == "add") n.reduce_body = ReduceBody::Add;
+      else if (b == "maximum") n.reduce_body = ReduceBody::Max;
+      else if (b == "minimum") n.reduce_body = ReduceBody::Min;
+      else if (b == "multiply") n.reduce_body = ReduceBody::Mul;
+      else if (b == "and") n.reduce_body = ReduceBody::And;
+      else if (b == "or") n.reduce_body = ReduceBody::Or;
+      else unimplemented("reduce body '" + b + "' is not supported");
+    } else if (nm == "dot_general") {
+      n.op = Op::DotGeneral;
+      std::string dd = get("dot_dimension_numbers");
+      if (!dd.empty()) {
+        auto field = [&](const char* f) {
+          size_t p = dd.find(f);
+          if (p == std::string::npos) return std::vector<int64_t>();
+          size_t lb = dd.find('[', p), rb = dd.find(']', p);
+          return parse_int_list_text(dd.substr(lb, rb - lb + 1));
+        };
+        n.dot.lhs_batch = field("lhs_batching_dimensions");
+        n.dot.rhs_batch = field("rhs_batching_dimensions");
+        n.dot.lhs_contract = field("lhs_contracting_dimensions");
+        n.dot.rhs_contract = field("rhs_contracting_dimensions");
+      } else {
+        n.dot.lhs_batch = parse_int_list_text(get("batching_dims.lhs"));
+        n.dot.rhs_batch = parse_int_list_text(get("batching_dims.rhs"));
+        n.dot.lhs_contract = parse_int_list_text(get("contracting_dims.lhs"));
+        n.dot.rhs_contract = parse_int_list_text(get("contracting_dims.rhs"));
+      }
+      std::string alg = get("algorithm");
+      if (alg.empty()) alg = get("dot_algorithm");
+      if (!alg.empty()) {
+        auto ptype = [&](const char* f) {
+          size_t p = alg.find(f);
+          if (p == std::string::npos) return DType::INVALID;
+          p = alg.find('=', p) + 1;
+          while (p < alg.size() && isspace((unsigned char)alg[p])) ++p;
+          size_t e = p;
+          while (e < alg.size() && Cursor::is_ident_char(alg[e])) ++e;
+          std::string t = alg.substr(p, e - p);
+          if (t == "tf32") return DType::F32;
+          return parse_element_type(t);
+        };
+        n.dot_lhs_precision = ptype("lhs_precision_type");
+        n.dot_rhs_precision = ptype("rhs_precision_type");
+      }
+    } else {
+      unimplemented("stablehlo." + nm + " is not supported by the MI355X plugin");
+    }
+    validate(n);
+    int id = add(std::move(n));
+    for (auto& r : os.results) names_[r] = id;
+  }
+
+  void validate(Node& n) {
+    auto& g = graph_;
+    auto opt = [&](int i) -> const TensorType& { return g.nodes[n.operands.at(i)].type; };
+    auto need = [&](size_t k) {
+      if (n.operands.size() != k) invalid(std::string(op_name(n.op)) + " expects " + std::to_string(k) + " operands");
+    };
+    switch (n.op) {
+      case Op::BroadcastInDim:
+        need(1);
+        if (n.dims.size() != opt(0).shape.size()) invalid("broadcast_in_dim: dims size must equal operand rank");
+        for (size_t i = 0; i < n.dims.size(); ++i) {
+          int64_t d = n.dims[i];
+          if (d < 0 || d >= n.type.rank()) invalid("broadcast_in_dim: dimension out of range");
+          if (opt(0).shape[i] != 1 && opt(0).shape[i] != n.type.shape[d]) invalid("broadcast_in_dim: incompatible shape");
+        }
+        break;
+      case Op::Transpose:
+        need(1);
+        if ((int)n.dims.size() != opt(0).rank()) invalid("transpose: permutation size must equal rank");
+        for (size_t i = 0; i < n.dims.size(); ++i)
+          if (n.type.shape[i] != opt(0).shape[n.dims[i]]) invalid("transpose: result shape mismatch");
+        break;
+      case Op::Reshape:
+        need(1);
+        if (opt(0).elements() != n.type.elements()) invalid("reshape: element count mismatch");
+        break;
+      case Op::DotGeneral: {
+        need(2);
+        auto& L = opt(0);
+        auto& R = opt(1);
+        if (n.dot.lhs_batch.size() != n.dot.rhs_batch.size() || n.dot.lhs_contract.size() != n.dot.rhs_contract.size())
+          invalid("dot_general: mismatched dimension lists");
+        for (size_t i = 0; i < n.dot.lhs_batch.size(); ++i)
+          if (L.shape.at(n.dot.lhs_batch[i]) != R.shape.at(n.dot.rhs_batch[i])) invalid("dot_general: batch size mismatch");
+        for (size_t i = 0; i < n.dot.lhs_contract.size(); ++i)
+          if (L.shape.at(n.dot.lhs_contract[i]) != R.shape.at(n.dot.rhs_contract[i]))
+            invalid("dot_general: contracting size mismatch");
+        break;
+      }
+      case Op::Reduce: {
+        auto& in = opt(0);
+        std::vector<int64_t> out;
+        for (int d = 0; d < in.rank(); ++d) {
+          bool red = false;
+          for (auto r : n.dims) red |= (r == d);
+          if (!red) out.push_back(in.shape[d]);
+        }
+        if (out != n.type.shape) invalid("reduce: result shape mismatch");
+        if (opt(1).rank() != 0) invalid("reduce: init value must be a scalar");
+        break;
+      }
+      case Op::Select:
+        need(3);
+        if (opt(0).dtype != DType::PRED) invalid("select: predicate must be i1");
+        break;
+      case Op::Iota:
+        if (n.iota_dim < 0 || n.iota_dim >= n.type.rank()) invalid("iota: dimension out of range");
+        break;
+      default:
+        if (op_is_elementwise(n.op)) {
+          for (size_t i = 0; i < n.operands.size(); ++i) {
+            auto& t = opt(i);
+            bool scalar_ok = (n.op == Op::Select && i == 0) || n.op == Op::Clamp;
+            if (t.shape != n.type.shape && !(scalar_ok && t.rank() == 0))
+              invalid(std::string(op_name(n.op)) + ": operand shape " + shape_str(t.shape) + " does not match result " +
+                      shape_str(n.type.shape));
+          }
+        }
+        break;
+    }
+  }
+
+  Cursor c_;
+  Graph graph_;
+  std::map<std::string, int> names_;
+  std::vector<TensorType> result_types_;
+};
+
+}  // namespace
+
+Graph parse_mlir_text(const std::string& text, const std::string& entry) {
+  Parser p(text);
+  Graph g = p.parse(entry);
+  if (g.results.empty()) invalid("function @" + entry + " returns nothing");
+  return g;
+}
+
+}  // namespace ryft

@@ -1,0 +1,1249 @@
+// Graph → Plan lowering. Responsibilities:
+//   * fuse chains of elementwise / broadcast_in_dim / transpose / iota / constant ops into one elementwise program
+//     (a kernel reads each leaf buffer through a strided view, so broadcasts and transposes cost no copies);
+//   * fuse the elementwise consumers of a dot_general into the GEMM epilogue, two dots sharing an lhs into one dual
+//     GEMM (gate/up projections), and exact-widening converts / transposes of dot operands into the GEMM loads;
+//   * recognise dot → scale → causal mask → softmax → dot as one fused attention launch;
+//   * fuse the producer expression of a reduce into the reduction kernel.
+// Dot semantics: crates/ryft-mlir/src/dialects/stable_hlo/operations/linear_algebra.rs:561-705.
+// Reduce semantics: crates/ryft-mlir/src/dialects/stable_hlo/operations/functional.rs:109-135.
+#include "planner.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstddef>
+#include <functional>
+#include <map>
+#include <set>
+#include <sstream>
+
+#include "kernels/kernels.h"
+
+namespace ryft {
+
+namespace {
+
+std::vector<int64_t> row_major_strides(const std::vector<int64_t>& shape) {
+  std::vector<int64_t> s(shape.size(), 1);
+  for (int i = (int)shape.size() - 2; i >= 0; --i) s[i] = s[i + 1] * shape[i + 1];
+  return s;
+}
+
+bool float_class(DType t) { return dtype_is_float(t); }
+
+// Rounding tag for a register holding a value of StableHLO type `t` (0 when the 32-bit register is exact).
+uint8_t round_tag(DType t) {
+  switch (t) {
+    case DType::BF16: case DType::F16: case DType::F8E4M3FN: case DType::F8E5M2:
+    case DType::S8: case DType::S16: case DType::U8: case DType::U16: case DType::PRED:
+      return (uint8_t)t;
+    default:
+      return 0;
+  }
+}
+
+// Is every value of `from` exactly representable in `to`?
+bool exact_widening(DType from, DType to) {
+  if (from == to) return true;
+  switch (to) {
+    case DType::F32: return from == DType::BF16 || from == DType::F16 || from == DType::F8E4M3FN ||
+                            from == DType::F8E5M2 || from == DType::S8 || from == DType::U8 || from == DType::S16 ||
+                            from == DType::U16;
+    case DType::BF16: return from == DType::F8E4M3FN || from == DType::F8E5M2 || from == DType::S8 || from == DType::U8;
+    case DType::F16: return from == DType::F8E4M3FN || from == DType::F8E5M2 || from == DType::S8 || from == DType::U8;
+    case DType::S32: return from == DType::S8 || from == DType::S16 || from == DType::U8 || from == DType::U16;
+    case DType::S16: return from == DType::S8 || from == DType::U8;
+    default: return false;
+  }
+}
+
+// A strided view of a materialized value: element at node coords c lives at slot base + offset + Σ c[d]·strides[d].
+struct View {
+  int slot = -1;
+  DType dtype = DType::INVALID;
+  int64_t offset = 0;
+  std::vector<int64_t> strides;
+};
+
+struct Leaf {
+  int slot;
+  DType dtype;
+  int64_t offset;
+  std::vector<int64_t> strides;  // per iteration dim
+  bool same(const Leaf& o) const {
+    return slot == o.slot && dtype == o.dtype && offset == o.offset && strides == o.strides;
+  }
+};
+
+class Planner;
+
+// Builds one elementwise program over an iteration space.
+class ExprBuilder {
+ public:
+  ExprBuilder(Planner& p, std::vector<int64_t> space) : P_(p), space_(std::move(space)) {
+    for (size_t d = 0; d < space_.size(); ++d) ident_.push_back((int)d);
+  }
+
+  struct Val { int instr; bool is_float; };
+
+  std::map<int, int> acc_nodes;  // nodes read as GEMM accumulators (epilogues)
+  bool dry = false;              // dry run: record leaves, materialize nothing
+  std::vector<std::pair<int, std::vector<int>>> dry_leaves;
+  std::set<int> inner_nodes;     // elementwise nodes computed inside the program
+
+  Val emit(int node, const std::vector<int>& src);
+  void add_output(Val v, DType dtype) { outputs_.push_back({v.instr, dtype}); }
+  EwProgram finish();
+  const std::vector<Leaf>& leaves() const { return leaves_; }
+  // expression structure, for epilogue classification
+  const std::vector<EwInstr>& raw_instrs() const { return instrs_; }
+  const std::vector<std::vector<int>>& raw_srcs() const { return srcs_; }
+
+ private:
+  int push(EwInstr ins, bool is_float, std::vector<int> srcs);
+  int leaf_index(const Leaf& l);
+  Val leaf_load(int node, const std::vector<int>& src, DType dtype);
+  Val convert(Val v, DType from, DType to);
+
+  Planner& P_;
+  std::vector<int64_t> space_;
+  std::vector<EwInstr> instrs_;
+  std::vector<bool> is_float_;
+  std::vector<std::vector<int>> srcs_;
+  std::vector<Leaf> leaves_;
+  std::map<std::pair<int, std::vector<int>>, Val> memo_;
+  std::vector<std::pair<int, DType>> outputs_;
+  std::vector<int> ident_;
+};
+
+class Planner {
+ public:
+  explicit Planner(const Graph& g) : g_(g), users_(g.users()) {
+    for (int r : g.results) results_.insert(r);
+  }
+
+  Plan run();
+
+  View view_of(int node);
+  bool materialized(int node) const { return mat_.count(node) > 0; }
+  const Graph& graph() const { return g_; }
+
+ private:
+  int new_slot(Slot::Kind kind, const TensorType& t) {
+    Slot s;
+    s.kind = kind;
+    s.type = t;
+    plan_.slots.push_back(std::move(s));
+    return (int)plan_.slots.size() - 1;
+  }
+  int temp_or(int target, const TensorType& t) { return target >= 0 ? target : new_slot(Slot::TEMP, t); }
+
+  int materialize(int node, int target = -1);
+  void emit_elementwise_root(int node, int target);
+  void emit_reduce(int node, int target);
+  void emit_dot(const std::vector<int>& dots, int target, int root);
+  bool try_attention(int d2, int target, DType out_dtype, int root);
+  void emit_copy(int src_slot, int64_t src_off, int dst_slot, size_t bytes);
+  bool dot_operand(int dot, int which, GemmOperand* op, int* slot, int force_copy);
+  int canonical_copy(int node, const std::vector<int64_t>& order);
+  void push_program_patches(Step& st, size_t base, const EwProgram& p, const std::vector<Leaf>& leaves,
+                            const std::vector<int>& out_slots);
+  bool splat_value(int node, double* v);
+  int iota_axis(int node, int rank);
+  void classify_epilogue(Step& st, const std::vector<int>& unused);
+
+  const Graph& g_;
+  std::vector<std::vector<int>> users_;
+  std::set<int> results_;
+  Plan plan_;
+  std::map<int, int> mat_;  // node → slot holding it contiguously (row-major)
+};
+
+// ------------------------------------------------------------------------------------------------ ExprBuilder
+int ExprBuilder::push(EwInstr ins, bool is_float, std::vector<int> srcs) {
+  instrs_.push_back(ins);
+  is_float_.push_back(is_float);
+  srcs_.push_back(std::move(srcs));
+  return (int)instrs_.size() - 1;
+}
+
+int ExprBuilder::leaf_index(const Leaf& l) {
+  for (size_t i = 0; i < leaves_.size(); ++i)
+    if (leaves_[i].same(l)) return (int)i;
+  leaves_.push_back(l);
+  return (int)leaves_.size() - 1;
+}
+
+ExprBuilder::Val ExprBuilder::leaf_load(int node, const std::vector<int>& src, DType dtype) {
+  EwInstr ins{};
+  if (dry) {
+    dry_leaves.push_back({node, src});
+    ins.op = EW_CONST;
+    return {push(ins, float_class(dtype), {}), float_class(dtype)};
+  }
+  View v = P_.view_of(node);
+  Leaf l;
+  l.slot = v.slot;
+  l.dtype = v.dtype;
+  l.offset = v.offset;
+  l.strides.assign(space_.size(), 0);
+  for (size_t d = 0; d < src.size(); ++d)
+    if (src[d] >= 0) l.strides[src[d]] += v.strides[d];
+  ins.op = EW_LOAD;
+  ins.a = (uint8_t)std::min(leaf_index(l), 255);
+  return {push(ins, float_class(dtype), {}), float_class(dtype)};
+}
+
+ExprBuilder::Val ExprBuilder::convert(Val v, DType from, DType to) {
+  EwInstr ins{};
+  bool ff = float_class(from), tf = float_class(to);
+  if (to == DType::PRED) ins.op = ff ? EW_CVT_F2P : EW_CVT_I2P;
+  else if (ff && tf) ins.op = EW_CVT_F2F;
+  else if (ff && !tf) ins.op = EW_CVT_F2I;
+  else if (!ff && tf) { ins.op = EW_CVT_I2F; ins.imm.i = (from == DType::U32 || from == DType::U64); }
+  else ins.op = EW_CVT_I2I;
+  ins.round = round_tag(to);
+  return {push(ins, tf, {v.instr}), tf};
+}
+
+ExprBuilder::Val ExprBuilder::emit(int node, const std::vector<int>& src) {
+  auto key = std::make_pair(node, src);
+  auto it = memo_.find(key);
+  if (it != memo_.end()) return it->second;
+  const Graph& g = P_.graph();
+  const Node& n = g.nodes[node];
+  DType dt = n.type.dtype;
+  bool fl = float_class(dt);
+  Val out;
+  auto acc_it = acc_nodes.find(node);
+  if (acc_it != acc_nodes.end() && src == ident_) {
+    EwInstr ins{};
+    ins.op = EW_ACC;
+    ins.a = (uint8_t)acc_it->second;
+    out = {push(ins, fl, {}), fl};
+  } else if (n.op == Op::Constant && n.splat) {
+    EwInstr ins{};
+    ins.op = EW_CONST;
+    if (fl) ins.imm.f = (float)literal_as_double(n);
+    else ins.imm.i = (int32_t)literal_as_int(n);
+    out = {push(ins, fl, {}), fl};
+  } else if (P_.materialized(node)) {
+    out = leaf_load(node, src, dt);
+  } else if (n.op == Op::Iota) {
+    int d = src[n.iota_dim];
+    EwInstr ins{};
+    if (d < 0) { ins.op = EW_CONST; ins.imm.i = 0; }
+    else { ins.op = EW_IOTA; ins.a = (uint8_t)d; }
+    Val v{push(ins, false, {}), false};
+    out = (fl || round_tag(dt)) ? convert(v, DType::S32, dt) : v;
+  } else if (n.op == Op::BroadcastInDim) {
+    const Node& o = g.nodes[n.operands[0]];
+    std::vector<int> s2(o.type.rank());
+    for (int i = 0; i < o.type.rank(); ++i)
+      s2[i] = (o.type.shape[i] == 1 && n.type.shape[n.dims[i]] != 1) ? -1 : src[n.dims[i]];
+    out = emit(n.operands[0], s2);
+  } else if (n.op == Op::Transpose) {
+    const Node& o = g.nodes[n.operands[0]];
+    std::vector<int> s2(o.type.rank());
+    for (size_t i = 0; i < n.dims.size(); ++i) s2[n.dims[i]] = src[i];
+    out = emit(n.operands[0], s2);
+  } else if (op_is_elementwise(n.op)) {
+    inner_nodes.insert(node);
+    std::vector<Val> ops;
+    for (size_t i = 0; i < n.operands.size(); ++i) {
+      const Node& o = g.nodes[n.operands[i]];
+      ops.push_back(emit(n.operands[i], (o.type.rank() == 0 && n.type.rank() != 0) ? std::vector<int>() : src));
+    }
+    EwInstr ins{};
+    ins.round = round_tag(dt);
+    DType ot = g.nodes[n.operands[0]].type.dtype;
+    auto bin = [&](EwOp fop, EwOp iop, EwOp uop) {
+      ins.op = ops[0].is_float ? fop : (dtype_is_unsigned(ot) ? uop : iop);
+      return Val{push(ins, fl, {ops[0].instr, ops[1].instr}), fl};
+    };
+    auto un = [&](EwOp fop, EwOp iop) {
+      ins.op = ops[0].is_float ? fop : iop;
+      return Val{push(ins, fl, {ops[0].instr}), fl};
+    };
+    switch (n.op) {
+      case Op::Convert: out = convert(ops[0], ot, dt); break;
+      case Op::Add: out = bin(EW_ADD, EW_IADD, EW_IADD); break;
+      case Op::Subtract: out = bin(EW_SUB, EW_ISUB, EW_ISUB); break;
+      case Op::Multiply: out = bin(EW_MUL, EW_IMUL, EW_IMUL); break;
+      case Op::Divide: out = bin(EW_DIV, EW_IDIV, EW_UDIV); break;
+      case Op::Remainder: out = bin(EW_REM, EW_IREM, EW_UREM); break;
+      case Op::Maximum: out = bin(EW_MAX, EW_IMAX, EW_UMAX); break;
+      case Op::Minimum: out = bin(EW_MIN, EW_IMIN, EW_UMIN); break;
+      case Op::Power:
+        if (!fl) unimplemented("integer power is not supported");
+        out = bin(EW_POW, EW_POW, EW_POW);
+        break;
+      case Op::And: out = bin(EW_AND, EW_AND, EW_AND); break;
+      case Op::Or: out = bin(EW_OR, EW_OR, EW_OR); break;
+      case Op::Xor: out = bin(EW_XOR, EW_XOR, EW_XOR); break;
+      case Op::Negate: out = un(EW_NEG, EW_INEG); break;
+      case Op::Abs: out = un(EW_ABS, EW_IABS); break;
+      case Op::Sign: out = un(EW_SIGN, EW_ISIGN); break;
+      case Op::Not: out = un(EW_NOT, EW_NOT); break;
+      case Op::Exp: case Op::Log: case Op::Rsqrt: case Op::Sqrt: case Op::Tanh: case Op::Logistic:
+      case Op::Floor: case Op::Ceil: case Op::Expm1: case Op::Log1p: {
+        if (!ops[0].is_float) invalid(std::string(op_name(n.op)) + " requires a floating-point operand");
+        static const std::map<Op, EwOp> m = {{Op::Exp, EW_EXP},     {Op::Log, EW_LOG},     {Op::Rsqrt, EW_RSQRT},
+                                             {Op::Sqrt, EW_SQRT},   {Op::Tanh, EW_TANH},   {Op::Logistic, EW_LOGISTIC},
+                                             {Op::Floor, EW_FLOOR}, {Op::Ceil, EW_CEIL},   {Op::Expm1, EW_EXPM1},
+                                             {Op::Log1p, EW_LOG1P}};
+        out = un(m.at(n.op), m.at(n.op));
+        break;
+      }
+      case Op::Compare:
+        ins.op = float_class(ot) ? EW_FCMP
+                                 : ((dtype_is_unsigned(ot) || n.cmp_type == CmpType::UNSIGNED) ? EW_UCMP : EW_ICMP);
+        ins.imm.i = (int32_t)n.cmp;
+        ins.round = 0;
+        out = {push(ins, false, {ops[0].instr, ops[1].instr}), false};
+        break;
+      case Op::Select:
+        ins.op = EW_SELECT;
+        ins.round = 0;
+        out = {push(ins, fl, {ops[0].instr, ops[1].instr, ops[2].instr}), fl};
+        break;
+      case Op::Clamp:
+        ins.op = fl ? EW_FCLAMP : EW_ICLAMP;
+        ins.round = 0;
+        out = {push(ins, fl, {ops[0].instr, ops[1].instr, ops[2].instr}), fl};
+        break;
+      default:
+        unimplemented(std::string("elementwise op ") + op_name(n.op));
+    }
+  } else {
+    // parameters, constants, dots, reduces, reshapes: read through a strided view of their materialized value
+    out = leaf_load(node, src, dt);
+  }
+  memo_[key] = out;
+  return out;
+}
+
+EwProgram ExprBuilder::finish() {
+  int n = (int)instrs_.size();
+  if (n > EW_MAX_INSTR) fail(PJRT_Error_Code_RESOURCE_EXHAUSTED, "elementwise program has too many instructions");
+  if ((int)leaves_.size() > EW_MAX_LEAVES) fail(PJRT_Error_Code_RESOURCE_EXHAUSTED, "elementwise program has too many leaves");
+  if ((int)outputs_.size() > EW_MAX_OUT) fail(PJRT_Error_Code_INTERNAL, "too many program outputs");
+  if ((int)space_.size() > EW_MAX_RANK) unimplemented("rank > 6 is not supported");
+  EwProgram p{};
+  p.rank = (int32_t)space_.size();
+  p.total = num_elements(space_);
+  for (size_t d = 0; d < space_.size(); ++d) p.shape[d] = space_[d];
+  // Linear-scan register allocation over the SSA instruction list. Sources are read before the destination is
+  // written, so a value whose last use is instruction i can hand its register to instruction i's result.
+  std::vector<int> last(n, -1);
+  for (int i = 0; i < n; ++i)
+    for (int s : srcs_[i]) last[s] = std::max(last[s], i);
+  for (auto& o : outputs_) last[o.first] = n + 1;
+  std::vector<int> reg(n, -1);
+  std::vector<std::vector<int>> free_at(n + 2);
+  std::vector<int> free_regs;
+  for (int r = EW_MAX_REGS - 1; r >= 0; --r) free_regs.push_back(r);
+  for (int i = 0; i < n; ++i) {
+    for (int v : free_at[i]) free_regs.push_back(reg[v]);
+    if (free_regs.empty()) fail(PJRT_Error_Code_RESOURCE_EXHAUSTED, "elementwise program needs too many registers");
+    reg[i] = free_regs.back();
+    free_regs.pop_back();
+    int l = last[i] < 0 ? i + 1 : last[i];
+    if (l <= n) free_at[l].push_back(i);
+  }
+  p.n_instr = n;
+  p.needs_coords = 0;
+  for (int i = 0; i < n; ++i) {
+    EwInstr ins = instrs_[i];
+    ins.dst = (uint8_t)reg[i];
+    if (ins.op == EW_IOTA) p.needs_coords = 1;
+    if (ins.op != EW_LOAD && ins.op != EW_IOTA && ins.op != EW_ACC) {
+      ins.a = srcs_[i].size() > 0 ? (uint8_t)reg[srcs_[i][0]] : 0;
+      ins.b = srcs_[i].size() > 1 ? (uint8_t)reg[srcs_[i][1]] : 0;
+      ins.c = srcs_[i].size() > 2 ? (uint8_t)reg[srcs_[i][2]] : 0;
+    }
+    p.instr[i] = ins;
+  }
+  p.n_leaves = (int32_t)leaves_.size();
+  auto rm = row_major_strides(space_);
+  for (size_t i = 0; i < leaves_.size(); ++i) {
+    EwLeaf& L = p.leaves[i];
+    L.ptr = nullptr;
+    L.dtype = (int32_t)leaves_[i].dtype;
+    L.offset = leaves_[i].offset;
+    bool ident = true, scalar = true;
+    for (size_t d = 0; d < space_.size(); ++d) {
+      L.strides[d] = leaves_[i].strides[d];
+      if (space_[d] == 1) continue;
+      if (L.strides[d] != rm[d]) ident = false;
+      if (L.strides[d] != 0) scalar = false;
+    }
+    L.kind = scalar ? EW_LEAF_SCALAR : (ident ? EW_LEAF_IDENTITY : EW_LEAF_GENERAL);
+    if (L.kind == EW_LEAF_GENERAL) p.needs_coords = 1;
+  }
+  p.n_out = (int32_t)outputs_.size();
+  p.out_float_mask = 0;
+  for (size_t o = 0; o < outputs_.size(); ++o) {
+    p.out_reg[o] = reg[outputs_[o].first];
+    p.out_dtype[o] = (int32_t)outputs_[o].second;
+    if (is_float_[outputs_[o].first]) p.out_float_mask |= 1 << o;
+  }
+  return p;
+}
+
+// ------------------------------------------------------------------------------------------------ Planner
+void Planner::push_program_patches(Step& st, size_t base, const EwProgram& p, const std::vector<Leaf>& leaves,
+                                   const std::vector<int>& out_slots) {
+  for (int i = 0; i < p.n_leaves; ++i)
+    st.patches.push_back({base + offsetof(EwProgram, leaves) + i * sizeof(EwLeaf) + offsetof(EwLeaf, ptr), leaves[i].slot});
+  for (size_t o = 0; o < out_slots.size(); ++o)
+    if (out_slots[o] >= 0)
+      st.patches.push_back({base + offsetof(EwProgram, out_ptr) + o * sizeof(void*), out_slots[o]});
+}
+
+static double leaf_bytes(const Plan& plan, const std::vector<Leaf>& leaves) {
+  double b = 0;
+  std::set<int> seen;
+  for (auto& l : leaves)
+    if (seen.insert(l.slot).second) b += (double)plan.slots[l.slot].type.bytes();
+  return b;
+}
+
+View Planner::view_of(int node) {
+  const Node& n = g_.nodes[node];
+  View v;
+  if (n.op == Op::Reshape && !materialized(node)) {
+    // a reshape of a contiguous value is the same bytes with new row-major strides
+    v.slot = materialize(n.operands[0]);
+    v.dtype = plan_.slots[v.slot].type.dtype;
+    v.strides = row_major_strides(n.type.shape);
+    return v;
+  }
+  v.slot = materialize(node);
+  v.dtype = plan_.slots[v.slot].type.dtype;
+  v.strides = row_major_strides(n.type.shape);
+  return v;
+}
+
+void Planner::emit_copy(int src_slot, int64_t src_off, int dst_slot, size_t bytes) {
+  Step st{};
+  st.kind = Step::COPY;
+  st.name = "copy";
+  st.copy.bytes = (int64_t)bytes;
+  st.patches = {{0, src_slot}, {1, dst_slot}};  // copy steps: index 0 = source, 1 = destination
+  (void)src_off;
+  st.bytes = 2.0 * (double)bytes;
+  plan_.steps.push_back(std::move(st));
+}
+
+int Planner::materialize(int node, int target) {
+  auto it = mat_.find(node);
+  if (it != mat_.end()) {
+    if (target >= 0 && target != it->second) emit_copy(it->second, 0, target, g_.nodes[node].type.bytes());
+    return target >= 0 ? target : it->second;
+  }
+  const Node& n = g_.nodes[node];
+  switch (n.op) {
+    case Op::Parameter: {
+      int s = plan_.param_slots.at(n.param_index);
+      mat_[node] = s;
+      if (target >= 0) emit_copy(s, 0, target, n.type.bytes());
+      return target >= 0 ? target : s;
+    }
+    case Op::Constant:
+      if (!n.splat) {
+        int s = new_slot(Slot::CONSTANT, n.type);
+        plan_.slots[s].literal = n.literal;
+        mat_[node] = s;
+        if (target >= 0) emit_copy(s, 0, target, n.type.bytes());
+        return target >= 0 ? target : s;
+      }
+      emit_elementwise_root(node, target);
+      break;
+    case Op::DotGeneral:
+      if (!try_attention(node, target, n.type.dtype, node)) emit_dot({node}, target, -1);
+      break;
+    case Op::Reduce:
+      emit_reduce(node, target);
+      break;
+    case Op::Reshape: {
+      int s = materialize(n.operands[0]);
+      if (target >= 0) {
+        emit_copy(s, 0, target, n.type.bytes());
+        mat_[node] = target;
+        return target;
+      }
+      mat_[node] = s;
+      return s;
+    }
+    default:
+      emit_elementwise_root(node, target);
+      break;
+  }
+  return mat_.at(node);
+}
+
+void Planner::emit_elementwise_root(int node, int target) {
+  const Node& n = g_.nodes[node];
+  std::vector<int> ident(n.type.rank());
+  for (int d = 0; d < n.type.rank(); ++d) ident[d] = d;
+
+  // convert(attention-dot) → attention kernel writing the converted type directly
+  if (n.op == Op::Convert) {
+    int d = n.operands[0];
+    const Node& dn = g_.nodes[d];
+    if (dn.op == Op::DotGeneral && !materialized(d) && users_[d].size() == 1 && !results_.count(d) &&
+        try_attention(d, target, n.type.dtype, node))
+      return;
+  }
+
+  // Epilogue fusion: identity-mapped dot_general leaves of this expression run as the GEMM that produces them.
+  {
+    ExprBuilder dry(*this, n.type.shape);
+    dry.dry = true;
+    dry.emit(node, ident);
+    std::vector<int> dots;
+    for (auto& l : dry.dry_leaves) {
+      const Node& ln = g_.nodes[l.first];
+      if (ln.op == Op::DotGeneral && l.second == ident && ln.type.shape == n.type.shape && !materialized(l.first) &&
+          std::find(dots.begin(), dots.end(), l.first) == dots.end())
+        dots.push_back(l.first);
+    }
+    if (!dots.empty()) {
+      std::vector<int> chosen = {dots[0]};
+      // a second dot with the same lhs operand and dimension numbers → dual GEMM (shared A tiles)
+      for (size_t i = 1; i < dots.size(); ++i) {
+        const Node& a = g_.nodes[dots[0]];
+        const Node& b = g_.nodes[dots[i]];
+        if (a.operands[0] == b.operands[0] && a.dot.lhs_batch == b.dot.lhs_batch &&
+            a.dot.lhs_contract == b.dot.lhs_contract && a.dot.rhs_batch == b.dot.rhs_batch &&
+            a.dot.rhs_contract == b.dot.rhs_contract && a.type == b.type &&
+            g_.nodes[a.operands[1]].type.shape == g_.nodes[b.operands[1]].type.shape) {
+          chosen.push_back(dots[i]);
+          break;
+        }
+      }
+      emit_dot(chosen, target, node);
+      return;
+    }
+  }
+
+  // Plain elementwise kernel; split the expression at its operands if it does not fit one program.
+  for (int attempt = 0; attempt < 2; ++attempt) {
+    try {
+      ExprBuilder b(*this, n.type.shape);
+      auto v = b.emit(node, ident);
+      b.add_output(v, n.type.dtype);
+      EwProgram p = b.finish();
+      int out = temp_or(target, n.type);
+      Step st{};
+      // a bare identity load of the same type is a copy
+      if (p.n_instr == 1 && p.instr[0].op == EW_LOAD && p.leaves[0].kind == EW_LEAF_IDENTITY &&
+          p.leaves[0].dtype == (int32_t)n.type.dtype) {
+        st.kind = Step::COPY;
+        st.name = "copy";
+        st.copy.bytes = (int64_t)n.type.bytes();
+        st.patches = {{0, b.leaves()[0].slot}, {1, out}};
+        st.bytes = 2.0 * (double)n.type.bytes();
+      } else {
+        st.kind = Step::ELEMENTWISE;
+        st.name = "elementwise";
+        st.ew = p;
+        push_program_patches(st, 0, p, b.leaves(), {out});
+        st.bytes = leaf_bytes(plan_, b.leaves()) + (double)n.type.bytes();
+      }
+      plan_.steps.push_back(std::move(st));
+      mat_[node] = out;
+      return;
+    } catch (const Status& s) {
+      if (s.code != PJRT_Error_Code_RESOURCE_EXHAUSTED || attempt == 1) throw;
+      for (int o : n.operands) materialize(o);
+    }
+  }
+}
+
+void Planner::emit_reduce(int node, int target) {
+  const Node& n = g_.nodes[node];
+  int x = n.operands[0];
+  const Node& xn = g_.nodes[x];
+  double initv = 0.0;
+  int init_slot = -1;
+  if (!splat_value(n.operands[1], &initv)) init_slot = materialize(n.operands[1]);  // a device scalar
+  std::vector<int64_t> red = n.dims;
+  std::sort(red.begin(), red.end());
+  std::vector<int64_t> outer_dims, space;
+  for (int d = 0; d < xn.type.rank(); ++d)
+    if (!std::binary_search(red.begin(), red.end(), (int64_t)d)) outer_dims.push_back(d);
+  std::vector<int> src(xn.type.rank());
+  int pos = 0;
+  for (auto d : outer_dims) { src[d] = pos++; space.push_back(xn.type.shape[d]); }
+  for (auto d : red) { src[d] = pos++; space.push_back(xn.type.shape[d]); }
+  int64_t outer = 1, inner = 1;
+  for (auto d : outer_dims) outer *= xn.type.shape[d];
+  for (auto d : red) inner *= xn.type.shape[d];
+
+  for (int attempt = 0; attempt < 2; ++attempt) {
+    try {
+      ExprBuilder b(*this, space);
+      auto v = b.emit(x, src);
+      b.add_output(v, n.type.dtype);
+      EwProgram p = b.finish();
+      int out = temp_or(target, n.type);
+      Step st{};
+      st.kind = Step::REDUCE;
+      st.name = "reduce";
+      st.red.prologue = p;
+      st.red.outer = outer;
+      st.red.inner = inner;
+      st.red.is_float = float_class(xn.type.dtype);
+      switch (n.reduce_body) {
+        case ReduceBody::Add: st.red.kind = RED_ADD; break;
+        case ReduceBody::Max: st.red.kind = RED_MAX; break;
+        case ReduceBody::Min: st.red.kind = RED_MIN; break;
+        case ReduceBody::Mul: st.red.kind = RED_MUL; break;
+        case ReduceBody::And: st.red.kind = RED_AND; break;
+        case ReduceBody::Or: st.red.kind = RED_OR; break;
+      }
+      if (st.red.is_float) st.red.init.f = (float)initv;
+      else st.red.init.i = (int32_t)(int64_t)initv;
+      push_program_patches(st, offsetof(ReduceArgs, prologue), p, b.leaves(), {out});
+      if (init_slot >= 0) {
+        st.red.init_dtype = (int32_t)g_.nodes[n.operands[1]].type.dtype;
+        st.patches.push_back({offsetof(ReduceArgs, init_ptr), init_slot});
+      }
+      st.bytes = leaf_bytes(plan_, b.leaves()) + (double)n.type.bytes();
+      plan_.steps.push_back(std::move(st));
+      mat_[node] = out;
+      return;
+    } catch (const Status& s) {
+      if (s.code != PJRT_Error_Code_RESOURCE_EXHAUSTED || attempt == 1) throw;
+      materialize(x);
+    }
+  }
+}
+
+int Planner::canonical_copy(int node, const std::vector<int64_t>& order) {
+  const Node& n = g_.nodes[node];
+  std::vector<int64_t> shape;
+  for (auto d : order) shape.push_back(n.type.shape[d]);
+  ExprBuilder b(*this, shape);
+  std::vector<int> src(n.type.rank());
+  for (size_t i = 0; i < order.size(); ++i) src[order[i]] = (int)i;
+  auto v = b.emit(node, src);
+  b.add_output(v, n.type.dtype);
+  EwProgram p = b.finish();
+  int slot = new_slot(Slot::TEMP, TensorType{n.type.dtype, shape});
+  Step st{};
+  st.kind = Step::ELEMENTWISE;
+  st.name = "transpose_copy";
+  st.ew = p;
+  push_program_patches(st, 0, p, b.leaves(), {slot});
+  st.bytes = leaf_bytes(plan_, b.leaves()) + (double)n.type.bytes();
+  plan_.steps.push_back(std::move(st));
+  return slot;
+}
+
+// Describe operand `which` (0 = lhs → A, 1 = rhs → B) of a dot as a strided [batch, row, k] view, peeling transposes
+// and exact widening converts into the GEMM's loads. Falls back to a canonical contiguous copy.
+bool Planner::dot_operand(int dot, int which, GemmOperand* op, int* slot, int force_copy) {
+  const Node& d = g_.nodes[dot];
+  int node = d.operands[which];
+  const Node& on = g_.nodes[node];
+  const auto& batch = which == 0 ? d.dot.lhs_batch : d.dot.rhs_batch;
+  const auto& contract = which == 0 ? d.dot.lhs_contract : d.dot.rhs_contract;
+  std::vector<int64_t> free_dims;
+  for (int i = 0; i < on.type.rank(); ++i)
+    if (std::find(batch.begin(), batch.end(), i) == batch.end() &&
+        std::find(contract.begin(), contract.end(), i) == contract.end())
+      free_dims.push_back(i);
+
+  std::vector<int64_t> strides;
+  int src_slot;
+  DType src_dtype;
+  int64_t offset = 0;
+  if (!force_copy) {
+    int cur = node;
+    std::vector<int> map(on.type.rank());
+    for (int i = 0; i < on.type.rank(); ++i) map[i] = i;
+    for (;;) {
+      const Node& cn = g_.nodes[cur];
+      if (materialized(cur)) break;
+      if (cn.op == Op::Transpose) {
+        for (auto& m : map) m = (int)cn.dims[m];
+        cur = cn.operands[0];
+        continue;
+      }
+      if (cn.op == Op::Convert && exact_widening(g_.nodes[cn.operands[0]].type.dtype, cn.type.dtype)) {
+        cur = cn.operands[0];
+        continue;
+      }
+      break;
+    }
+    View v = view_of(cur);
+    src_slot = v.slot;
+    src_dtype = v.dtype;
+    offset = v.offset;
+    strides.resize(on.type.rank());
+    for (int i = 0; i < on.type.rank(); ++i) strides[i] = v.strides[map[i]];
+  } else {
+    std::vector<int64_t> order = batch;
+    order.insert(order.end(), free_dims.begin(), free_dims.end());
+    order.insert(order.end(), contract.begin(), contract.end());
+    src_slot = canonical_copy(node, order);
+    src_dtype = on.type.dtype;
+    std::vector<int64_t> shape;
+    for (auto o : order) shape.push_back(on.type.shape[o]);
+    auto rm = row_major_strides(shape);
+    strides.assign(on.type.rank(), 0);
+    for (size_t i = 0; i < order.size(); ++i) strides[order[i]] = rm[i];
+  }
+  // collapse a dim group into (size, stride); size-1 dims are ignored
+  auto collapse = [&](const std::vector<int64_t>& dims, int64_t* stride) {
+    int64_t st = 0, expect = -1;
+    bool any = false;
+    for (int i = (int)dims.size() - 1; i >= 0; --i) {
+      int64_t sz = on.type.shape[dims[i]];
+      if (sz == 1) continue;
+      int64_t s = strides[dims[i]];
+      if (!any) { st = s; expect = s * sz; any = true; continue; }
+      if (s != expect) return false;
+      expect = s * sz;
+    }
+    *stride = any ? st : 0;
+    return true;
+  };
+  int64_t sb, sr, sk;
+  if (!collapse(batch, &sb) || !collapse(free_dims, &sr) || !collapse(contract, &sk)) {
+    if (force_copy) fail(PJRT_Error_Code_INTERNAL, "canonical dot operand is not collapsible");
+    return false;
+  }
+  op->ptr = (const void*)(uintptr_t)(offset * (int64_t)dtype_size(src_dtype));
+  op->sb = sb;
+  op->sr = sr;
+  op->sk = sk;
+  op->dtype = (int32_t)src_dtype;
+  *slot = src_slot;
+  return true;
+}
+
+void Planner::emit_dot(const std::vector<int>& dots_in, int target, int root) {
+  std::vector<int> dots = dots_in;
+  const Node& d = g_.nodes[dots[0]];
+  int64_t batch = 1, M = 1, N = 1, K = 1;
+  const Node& L = g_.nodes[d.operands[0]];
+  const Node& R = g_.nodes[d.operands[1]];
+  for (auto b : d.dot.lhs_batch) batch *= L.type.shape[b];
+  for (auto c : d.dot.lhs_contract) K *= L.type.shape[c];
+  int n_lfree = L.type.rank() - (int)d.dot.lhs_batch.size() - (int)d.dot.lhs_contract.size();
+  int n_rfree = R.type.rank() - (int)d.dot.rhs_batch.size() - (int)d.dot.rhs_contract.size();
+  M = 1;
+  for (int i = 0; i < n_lfree; ++i) M *= d.type.shape[d.dot.lhs_batch.size() + i];
+  N = 1;
+  for (int i = 0; i < n_rfree; ++i) N *= d.type.shape[d.dot.lhs_batch.size() + n_lfree + i];
+  if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX || batch > INT32_MAX) unimplemented("dot_general too large");
+
+  Step st{};
+  st.kind = Step::GEMM;
+  GemmArgs& G = st.gemm;
+  G.M = (int32_t)M;
+  G.N = (int32_t)N;
+  G.K = (int32_t)K;
+  G.batch = (int32_t)batch;
+  int sa, sbs, sb2 = -1;
+  if (!dot_operand(dots[0], 0, &G.A, &sa, 0)) dot_operand(dots[0], 0, &G.A, &sa, 1);
+  if (!dot_operand(dots[0], 1, &G.B, &sbs, 0)) dot_operand(dots[0], 1, &G.B, &sbs, 1);
+  if (dots.size() > 1) {
+    GemmOperand a2;
+    int sa2;
+    if (!dot_operand(dots[1], 0, &a2, &sa2, 0) || sa2 != sa || a2.sb != G.A.sb || a2.sr != G.A.sr ||
+        a2.sk != G.A.sk || a2.dtype != G.A.dtype || !dot_operand(dots[1], 1, &G.B2, &sb2, 0) ||
+        G.B2.dtype != G.B.dtype) {
+      dots.resize(1);
+      G.B2 = GemmOperand{};
+      sb2 = -1;
+    } else {
+      G.dual = 1;
+    }
+  }
+  G.acc_is_int = !dtype_is_float(d.type.dtype);
+  G.n_out = 1;
+  G.alpha = 1.0f;
+  G.out_dtype[0] = (int32_t)d.type.dtype;
+  st.patches.push_back({offsetof(GemmArgs, A) + offsetof(GemmOperand, ptr), sa});
+  st.patches.push_back({offsetof(GemmArgs, B) + offsetof(GemmOperand, ptr), sbs});
+  if (sb2 >= 0) st.patches.push_back({offsetof(GemmArgs, B2) + offsetof(GemmOperand, ptr), sb2});
+  st.flops = 2.0 * (double)batch * (double)M * (double)N * (double)K * (double)dots.size();
+  st.bytes = (double)plan_.slots[sa].type.bytes() + (double)plan_.slots[sbs].type.bytes() +
+             (sb2 >= 0 ? (double)plan_.slots[sb2].type.bytes() : 0.0);
+
+  if (root < 0) {
+    int out = temp_or(target, d.type);
+    G.epilogue = EPI_STORE;
+    st.patches.push_back({offsetof(GemmArgs, out_ptr), out});
+    st.bytes += (double)d.type.bytes();
+    st.name = gemm_kernel_name(G);
+    plan_.steps.push_back(std::move(st));
+    mat_[dots[0]] = out;
+    return;
+  }
+
+  const Node& rn = g_.nodes[root];
+  std::vector<int> ident(rn.type.rank());
+  for (int i = 0; i < rn.type.rank(); ++i) ident[i] = i;
+  ExprBuilder b(*this, rn.type.shape);
+  for (size_t i = 0; i < dots.size(); ++i) b.acc_nodes[dots[i]] = (int)i;
+  auto v = b.emit(root, ident);
+  b.add_output(v, rn.type.dtype);
+  // Raw accumulator also needed outside the epilogue (a graph result, or a consumer this program does not cover)?
+  bool need_raw = results_.count(dots[0]) > 0;
+  for (int u : users_[dots[0]])
+    if (!b.inner_nodes.count(u) && u != root) need_raw = true;
+  for (int in : b.inner_nodes)
+    if (in != root)
+      for (int u : users_[in])
+        if (!b.inner_nodes.count(u) && u != root) need_raw = true;
+  if (need_raw && dots.size() > 1) {  // dual GEMMs cannot also hand out a raw accumulator: run them separately
+    emit_dot({dots[0]}, -1, -1);
+    emit_elementwise_root(root, target);
+    return;
+  }
+  int acc_slot = -1;
+  if (need_raw) {
+    for (size_t i = 0; i < g_.results.size() && acc_slot < 0; ++i)
+      if (g_.results[i] == dots[0]) acc_slot = plan_.output_slots[i];
+    if (acc_slot < 0) acc_slot = new_slot(Slot::TEMP, d.type);
+  }
+  EwProgram p = b.finish();
+  int out = temp_or(target, rn.type);
+  G.epilogue = EPI_PROGRAM;
+  G.epi = p;
+  G.n_out = 1;
+  G.out_dtype[0] = (int32_t)rn.type.dtype;
+  st.patches.push_back({offsetof(GemmArgs, out_ptr), out});
+  if (acc_slot >= 0) {
+    G.n_out = 2;
+    G.out_dtype[1] = (int32_t)d.type.dtype;
+    st.patches.push_back({offsetof(GemmArgs, out_ptr) + sizeof(void*), acc_slot});
+    st.bytes += (double)d.type.bytes();
+  }
+  G.epi_groups[0] = (int32_t)d.dot.lhs_batch.size();
+  G.epi_groups[1] = n_lfree;
+  G.epi_groups[2] = n_rfree;
+  for (int i = 0; i < p.n_leaves; ++i)
+    st.patches.push_back({offsetof(GemmArgs, epi) + offsetof(EwProgram, leaves) + i * sizeof(EwLeaf) + offsetof(EwLeaf, ptr),
+                          b.leaves()[i].slot});
+  st.bytes += leaf_bytes(plan_, b.leaves()) + (double)rn.type.bytes();
+  classify_epilogue(st, {});
+  if (G.epilogue == EPI_PROGRAM) {
+    // A generic epilogue program would force the slow generic GEMM; when an MFMA kernel can compute the dot
+    // itself, run the dot(s) there and the expression as its own elementwise kernel instead.
+    GemmArgs probe = G;
+    probe.epilogue = EPI_STORE;
+    probe.dual = 0;
+    if (std::string(gemm_kernel_name(probe)) != "gemm_generic") {
+      for (int dn : dots)
+        if (!materialized(dn)) emit_dot({dn}, -1, -1);
+      emit_elementwise_root(root, target);
+      return;
+    }
+  }
+  st.name = gemm_kernel_name(G);
+  plan_.steps.push_back(std::move(st));
+  mat_[root] = out;
+  if (acc_slot >= 0) mat_[dots[0]] = acc_slot;
+}
+
+// Replace a generic epilogue program by a specialised epilogue when its expression has one of the shapes the GEMM
+// kernels implement natively: convert(acc); convert(alpha·acc·row[m]·col[n]); convert(silu(acc·c1[n])·(acc2·c2[n])).
+void Planner::classify_epilogue(Step& st, const std::vector<int>&) {
+  GemmArgs& G = st.gemm;
+  const EwProgram& p = G.epi;
+  if (p.n_out < 1) return;
+  // Rebuild an expression tree view over the (already register-allocated) program by replaying it symbolically.
+  struct E { int op; int a = -1, b = -1, c = -1; int round = 0; int leaf = -1; int acc = -1; float imm = 0; };
+  std::vector<E> ex;
+  int regmap[EW_MAX_REGS];
+  for (auto& r : regmap) r = -1;
+  for (int i = 0; i < p.n_instr; ++i) {
+    const EwInstr& I = p.instr[i];
+    E e;
+    e.op = I.op;
+    e.round = I.round;
+    switch (I.op) {
+      case EW_LOAD: e.leaf = I.a; break;
+      case EW_ACC: e.acc = I.a; break;
+      case EW_CONST: e.imm = I.imm.f; break;
+      case EW_IOTA: return;  // not handled natively
+      default:
+        e.a = regmap[I.a];
+        e.b = regmap[I.b];
+        e.c = regmap[I.c];
+        break;
+    }
+    ex.push_back(e);
+    regmap[I.dst] = (int)ex.size() - 1;
+  }
+  int root = regmap[p.out_reg[0]];
+  int out_dtype = p.out_dtype[0];
+  // Only f32 intermediate math may be folded (no per-op rounding to narrower types before the output).
+  std::function<bool(int, std::vector<int>&)> factors = [&](int e, std::vector<int>& fs) -> bool {
+    const E& x = ex[e];
+    if (x.op == EW_MUL && x.round == 0) return factors(x.a, fs) && factors(x.b, fs);
+    fs.push_back(e);
+    return true;
+  };
+  // vector classification of a leaf over the (batch, M, N) groups: returns 'r', 'c', 's' or 0
+  int gb = G.epi_groups[0], gm = G.epi_groups[1], gn = G.epi_groups[2];
+  auto leaf_kind = [&](int li, int64_t* sb, int64_t* s_mn) -> char {
+    const EwLeaf& L = p.leaves[li];
+    if (L.dtype != 11 /* f32 */) return 0;
+    auto group_stride = [&](int begin, int count, int64_t* stride) -> bool {
+      int64_t st = 0, expect = -1;
+      bool any = false;
+      for (int i = begin + count - 1; i >= begin; --i) {
+        if (p.shape[i] == 1) continue;
+        int64_t s = L.strides[i];
+        if (!any) { st = s; expect = s * p.shape[i]; any = true; continue; }
+        if (s != expect && !(s == 0 && st == 0)) return false;
+        expect = s * p.shape[i];
+      }
+      *stride = any ? st : 0;
+      return true;
+    };
+    int64_t bs, ms, ns;
+    if (!group_stride(0, gb, &bs) || !group_stride(gb, gm, &ms) || !group_stride(gb + gm, gn, &ns)) return 0;
+    *sb = bs;
+    if (ms == 0 && ns == 0) return bs == 0 ? 's' : 0;
+    if (ns == 0) { *s_mn = ms; return 'r'; }
+    if (ms == 0) { *s_mn = ns; return 'c'; }
+    return 0;
+  };
+  auto is_acc = [&](int e, int which) {
+    const E& x = ex[e];
+    if (x.op == EW_ACC && x.acc == which) return true;
+    if (x.op == EW_CVT_I2F && x.round == 0 && ex[x.a].op == EW_ACC && ex[x.a].acc == which) return true;
+    return false;
+  };
+  // (1) output = acc (the store converts)
+  int top = root;
+  if ((ex[top].op == EW_CVT_F2F || ex[top].op == EW_CVT_I2F) && ex[top].round == out_dtype) top = ex[top].a;
+  int mid_round = 0;
+  if (ex[top].op == EW_CVT_F2F && ex[top].round != 0) { mid_round = ex[top].round; top = ex[top].a; }
+  if (G.n_out == 1 && !G.dual && ex[top].op == EW_ACC && ex[top].acc == 0) {
+    G.epilogue = EPI_STORE;
+    for (size_t i = 0; i < st.patches.size();)
+      if (st.patches[i].first >= offsetof(GemmArgs, epi)) st.patches.erase(st.patches.begin() + i);
+      else ++i;
+    return;
+  }
+  // (2) scale: product of acc and f32 row/col/scalar vectors / constants
+  if (!G.dual && p.n_out == 1) {
+    std::vector<int> fs;
+    factors(top, fs);
+    int accs = 0;
+    bool ok = true;
+    int row_leaf = -1, col_leaf = -1;
+    float alpha = 1.0f;
+    int64_t rsb = 0, rsm = 0, csb = 0, csn = 0;
+    for (int f : fs) {
+      if (is_acc(f, 0)) { ++accs; continue; }
+      const E& x = ex[f];
+      if (x.op == EW_CONST) { alpha *= x.imm; continue; }
+      if (x.op == EW_LOAD) {
+        int64_t sb = 0, smn = 0;
+        char k = leaf_kind(x.leaf, &sb, &smn);
+        if (k == 'r' && row_leaf < 0) { row_leaf = x.leaf; rsb = sb; rsm = smn; continue; }
+        if (k == 'c' && col_leaf < 0) { col_leaf = x.leaf; csb = sb; csn = smn; continue; }
+      }
+      ok = false;
+    }
+    if (ok && accs == 1) {
+      G.epilogue = EPI_SCALE;
+      G.mid_round = mid_round;
+      G.alpha = alpha;
+      G.raw_out = (G.n_out == 2);
+      G.row_sb = rsb; G.row_sm = rsm; G.col_sb = csb; G.col_sn = csn;
+      std::vector<std::pair<size_t, int>> keep;
+      for (auto& pt : st.patches) {
+        if (pt.first < offsetof(GemmArgs, epi)) { keep.push_back(pt); continue; }
+        size_t leaf_i = (pt.first - offsetof(GemmArgs, epi) - offsetof(EwProgram, leaves)) / sizeof(EwLeaf);
+        if ((int)leaf_i == row_leaf) keep.push_back({offsetof(GemmArgs, row), pt.second});
+        if ((int)leaf_i == col_leaf) keep.push_back({offsetof(GemmArgs, col), pt.second});
+      }
+      st.patches = keep;
+      return;
+    }
+  }
+  // (3) SwiGLU: silu(acc0·c1)·(acc1·c2) with silu(a) = a·logistic(a)
+  if (G.dual && p.n_out == 1) {
+    std::vector<int> fs;
+    factors(top, fs);
+    int lg = -1;
+    for (int f : fs)
+      if (ex[f].op == EW_LOGISTIC && ex[f].round == 0) lg = f;
+    if (lg < 0) return;
+    std::vector<int> fa;
+    factors(ex[lg].a, fa);
+    // the remaining factors must be fa (the logistic's own argument, once more) plus the second branch
+    std::vector<int> rest;
+    for (int f : fs)
+      if (f != lg) rest.push_back(f);
+    std::vector<int> fb = rest;
+    for (int f : fa) {
+      auto it = std::find(fb.begin(), fb.end(), f);
+      if (it == fb.end()) return;
+      fb.erase(it);
+    }
+    auto branch = [&](const std::vector<int>& f2, int which, int* leaf, int64_t* sb, int64_t* sn) -> bool {
+      int accs = 0;
+      *leaf = -1;
+      for (int f : f2) {
+        if (is_acc(f, which)) { ++accs; continue; }
+        if (ex[f].op == EW_LOAD && *leaf < 0) {
+          int64_t smn = 0;
+          if (leaf_kind(ex[f].leaf, sb, &smn) == 'c') { *leaf = ex[f].leaf; *sn = smn; continue; }
+        }
+        return false;
+      }
+      return accs == 1;
+    };
+    int la = -1, lb = -1;
+    int64_t asb = 0, asn = 0, bsb = 0, bsn = 0;
+    if (!branch(fa, 0, &la, &asb, &asn) || !branch(fb, 1, &lb, &bsb, &bsn)) return;
+    G.epilogue = EPI_SWIGLU;
+    G.mid_round = mid_round;
+    G.col_sb = asb; G.col_sn = asn; G.col2_sb = bsb; G.col2_sn = bsn;
+    std::vector<std::pair<size_t, int>> keep;
+    for (auto& pt : st.patches) {
+      if (pt.first < offsetof(GemmArgs, epi)) { keep.push_back(pt); continue; }
+      size_t leaf_i = (pt.first - offsetof(GemmArgs, epi) - offsetof(EwProgram, leaves)) / sizeof(EwLeaf);
+      if ((int)leaf_i == la) keep.push_back({offsetof(GemmArgs, col), pt.second});
+      if ((int)leaf_i == lb) keep.push_back({offsetof(GemmArgs, col2), pt.second});
+    }
+    st.patches = keep;
+  }
+}
+
+bool Planner::splat_value(int node, double* v) {
+  const Node& n = g_.nodes[node];
+  if (n.op == Op::Constant && n.splat) { *v = literal_as_double(n); return true; }
+  if (n.op == Op::Constant && n.type.elements() == 1) { *v = literal_as_double(n); return true; }
+  if ((n.op == Op::BroadcastInDim || n.op == Op::Reshape || n.op == Op::Convert) && !materialized(node))
+    return splat_value(n.operands[0], v);
+  return false;
+}
+
+// If `node` (of rank `rank`) equals one of its own coordinates (an iota, possibly broadcast or converted), returns
+// that dim; else -1.
+int Planner::iota_axis(int node, int rank) {
+  const Node& n = g_.nodes[node];
+  if (n.op == Op::Iota) return (int)n.iota_dim;
+  if (n.op == Op::Convert && !dtype_is_float(n.type.dtype)) return iota_axis(n.operands[0], rank);
+  if (n.op == Op::BroadcastInDim) {
+    const Node& o = g_.nodes[n.operands[0]];
+    int a = iota_axis(n.operands[0], o.type.rank());
+    if (a < 0) return -1;
+    if (o.type.shape[a] == 1 && n.type.shape[n.dims[a]] != 1) return -1;
+    return (int)n.dims[a];
+  }
+  return -1;
+}
+
+// dot(P, V) where P = softmax(mask(scale · dot(Q, K))) → one fused attention launch.
+bool Planner::try_attention(int d2, int target, DType out_dtype, int root) {
+  const Node& D2 = g_.nodes[d2];
+  if (D2.op != Op::DotGeneral) return false;
+  auto one_use = [&](int x) { return users_[x].size() == 1 && !results_.count(x) && !materialized(x); };
+  auto& dd = D2.dot;
+  if (dd.lhs_batch != std::vector<int64_t>{0, 1} || dd.rhs_batch != std::vector<int64_t>{0, 1} ||
+      dd.lhs_contract != std::vector<int64_t>{3} || dd.rhs_contract != std::vector<int64_t>{2})
+    return false;
+  int pn = D2.operands[0], vnode = D2.operands[1];
+  DType p_dtype = DType::F32;
+  int p = pn;
+  if (g_.nodes[pn].op == Op::Convert) {
+    if (!one_use(pn)) return false;
+    p_dtype = g_.nodes[pn].type.dtype;
+    p = g_.nodes[pn].operands[0];
+  }
+  const Node& P = g_.nodes[p];
+  if (P.op != Op::Divide || !one_use(p) || P.type.dtype != DType::F32) return false;
+  int e = P.operands[0], bsum = P.operands[1];
+  const Node& Bs = g_.nodes[bsum];
+  if (Bs.op != Op::BroadcastInDim || Bs.dims != std::vector<int64_t>{0, 1, 2} || !one_use(bsum)) return false;
+  int ssum = Bs.operands[0];
+  const Node& Ss = g_.nodes[ssum];
+  double z;
+  if (Ss.op != Op::Reduce || Ss.reduce_body != ReduceBody::Add || Ss.dims != std::vector<int64_t>{3} ||
+      Ss.operands[0] != e || !splat_value(Ss.operands[1], &z) || z != 0.0 || !one_use(ssum))
+    return false;
+  const Node& E = g_.nodes[e];
+  if (E.op != Op::Exp || users_[e].size() != 2 || results_.count(e) || materialized(e)) return false;
+  int x = E.operands[0];
+  const Node& X = g_.nodes[x];
+  if (X.op != Op::Subtract || !one_use(x)) return false;
+  int m = X.operands[0], bmax = X.operands[1];
+  const Node& Bm = g_.nodes[bmax];
+  if (Bm.op != Op::BroadcastInDim || Bm.dims != std::vector<int64_t>{0, 1, 2} || !one_use(bmax)) return false;
+  int smax = Bm.operands[0];
+  const Node& Sm = g_.nodes[smax];
+  double ninf;
+  if (Sm.op != Op::Reduce || Sm.reduce_body != ReduceBody::Max || Sm.dims != std::vector<int64_t>{3} ||
+      Sm.operands[0] != m || !splat_value(Sm.operands[1], &ninf) || !(ninf < -1e30) || !one_use(smax))
+    return false;
+  if (users_[m].size() != 2 || results_.count(m) || materialized(m)) return false;
+  // mask
+  int sc = m;
+  int causal = 0, causal_offset = 0;
+  const Node& Mn = g_.nodes[m];
+  if (Mn.op == Op::Select) {
+    double fill;
+    if (!splat_value(Mn.operands[2], &fill) || !(fill < -1e30)) return false;
+    // the predicate is compare(iota, iota), possibly computed at lower rank and broadcast up to the scores
+    int pred = Mn.operands[0];
+    std::vector<int64_t> axis_map = {0, 1, 2, 3};  // axis of the current predicate space → score axis
+    while (g_.nodes[pred].op == Op::BroadcastInDim && !materialized(pred)) {
+      const Node& bn = g_.nodes[pred];
+      std::vector<int64_t> next(bn.dims.size());
+      for (size_t i = 0; i < bn.dims.size(); ++i) next[i] = axis_map[bn.dims[i]];
+      axis_map = next;
+      pred = bn.operands[0];
+    }
+    const Node& C = g_.nodes[pred];
+    if (C.op != Op::Compare || materialized(pred)) return false;
+    int r = C.type.rank();
+    int a0 = iota_axis(C.operands[0], r), a1 = iota_axis(C.operands[1], r);
+    if (a0 < 0 || a1 < 0) return false;
+    if (g_.nodes[C.operands[0]].type.shape[a0] == 1 || g_.nodes[C.operands[1]].type.shape[a1] == 1) return false;
+    a0 = (int)axis_map[a0];
+    a1 = (int)axis_map[a1];
+    // normalise to "k <op> q"
+    CmpDir dir = C.cmp;
+    if (a0 == 2 && a1 == 3) {  // q <dir> k  → k <dir'> q
+      static const CmpDir flip[] = {CmpDir::EQ, CmpDir::NE, CmpDir::LE, CmpDir::LT, CmpDir::GE, CmpDir::GT};
+      dir = flip[(int)dir];
+    } else if (!(a0 == 3 && a1 == 2)) {
+      return false;
+    }
+    if (dir == CmpDir::LE) causal_offset = 0;       // keep k <= q
+    else if (dir == CmpDir::LT) causal_offset = -1;  // keep k < q
+    else return false;
+    causal = 1;
+    sc = Mn.operands[1];
+    if (!one_use(sc)) return false;
+  }
+  // scale
+  int d1 = sc;
+  double scale = 1.0;
+  const Node& Sn = g_.nodes[sc];
+  if (Sn.op == Op::Multiply) {
+    if (splat_value(Sn.operands[1], &scale)) d1 = Sn.operands[0];
+    else if (splat_value(Sn.operands[0], &scale)) d1 = Sn.operands[1];
+    else return false;
+    if (!one_use(d1)) return false;
+  }
+  const Node& D1 = g_.nodes[d1];
+  if (D1.op != Op::DotGeneral || D1.type.dtype != DType::F32 || D1.dot.lhs_batch != std::vector<int64_t>{0, 1} ||
+      D1.dot.rhs_batch != std::vector<int64_t>{0, 1} || D1.dot.lhs_contract != std::vector<int64_t>{3} ||
+      D1.dot.rhs_contract != std::vector<int64_t>{3})
+    return false;
+  int q = D1.operands[0], k = D1.operands[1];
+  const TensorType& Qt = g_.nodes[q].type;
+  const TensorType& Kt = g_.nodes[k].type;
+  const TensorType& Vt = g_.nodes[vnode].type;
+  if (Qt.dtype != DType::BF16 || Kt.dtype != DType::BF16 || Vt.dtype != DType::BF16) return false;
+  if (Qt.rank() != 4 || Kt.rank() != 4 || Vt.rank() != 4) return false;
+  int64_t B = Qt.shape[0], H = Qt.shape[1], Sq = Qt.shape[2], Dh = Qt.shape[3], Sk = Kt.shape[2];
+  if (Vt.shape[3] != Dh || Vt.shape[2] != Sk || !attention_supported((int)Dh)) return false;
+  if (!(out_dtype == DType::BF16 || out_dtype == DType::F32)) return false;
+  if (!(p_dtype == DType::BF16 || p_dtype == DType::F32)) return false;
+
+  View vq = view_of(q), vk = view_of(k), vv = view_of(vnode);
+  const Node& rn = g_.nodes[root];
+  int out = temp_or(target, rn.type);
+  Step st{};
+  st.kind = Step::ATTENTION;
+  st.name = "attention_fwd";
+  AttnArgs& A = st.attn;
+  A.B = (int32_t)B; A.H = (int32_t)H; A.Sq = (int32_t)Sq; A.Sk = (int32_t)Sk; A.D = (int32_t)Dh;
+  A.causal = causal;
+  A.causal_offset = causal_offset;
+  A.dtype = (int32_t)DType::BF16;
+  A.out_dtype = (int32_t)out_dtype;
+  A.p_dtype = (int32_t)p_dtype;
+  A.scale = (float)scale;
+  for (int i = 0; i < 4; ++i) { A.qs[i] = vq.strides[i]; A.ks[i] = vk.strides[i]; A.vs[i] = vv.strides[i]; }
+  auto orm = row_major_strides(rn.type.shape);
+  for (int i = 0; i < 4; ++i) A.os[i] = orm[i];
+  A.q = (const void*)(uintptr_t)(vq.offset * 2);
+  A.k = (const void*)(uintptr_t)(vk.offset * 2);
+  A.v = (const void*)(uintptr_t)(vv.offset * 2);
+  st.patches = {{offsetof(AttnArgs, q), vq.slot}, {offsetof(AttnArgs, k), vk.slot}, {offsetof(AttnArgs, v), vv.slot},
+                {offsetof(AttnArgs, o), out}};
+  double pairs = causal ? (double)Sq * (double)(Sk + 1) / 2.0 : (double)Sq * (double)Sk;  // Sq == Sk for causal
+  st.flops = 4.0 * (double)B * (double)H * (double)Dh * pairs;
+  st.bytes = (double)(Qt.bytes() + Kt.bytes() + Vt.bytes() + rn.type.bytes());
+  plan_.steps.push_back(std::move(st));
+  mat_[root] = out;
+  return true;
+}
+
+Plan Planner::run() {
+  for (size_t i = 0; i < g_.params.size(); ++i) {
+    const Node& pn = g_.nodes[g_.params[i]];
+    int s = new_slot(Slot::PARAM, pn.type);
+    plan_.slots[s].index = (int)i;
+    plan_.param_slots.push_back(s);
+    plan_.param_types.push_back(pn.type);
+  }
+  for (size_t i = 0; i < g_.results.size(); ++i) {
+    const Node& rn = g_.nodes[g_.results[i]];
+    int s = new_slot(Slot::OUTPUT, rn.type);
+    plan_.slots[s].index = (int)i;
+    plan_.output_slots.push_back(s);
+    plan_.output_types.push_back(rn.type);
+  }
+  // Elementwise results first: they are the roots that can absorb a producing dot_general (whose raw accumulator,
+  // when it is itself a result, is then written straight into that result's buffer by the same GEMM).
+  std::vector<size_t> order;
+  for (size_t i = 0; i < g_.results.size(); ++i)
+    if (op_is_elementwise(g_.nodes[g_.results[i]].op)) order.push_back(i);
+  for (size_t i = 0; i < g_.results.size(); ++i)
+    if (!op_is_elementwise(g_.nodes[g_.results[i]].op)) order.push_back(i);
+  for (size_t i : order) materialize(g_.results[i], plan_.output_slots[i]);
+  for (auto& st : plan_.steps) {
+    plan_.total_flops += st.flops;
+    plan_.total_bytes += st.bytes;
+  }
+  return std::move(plan_);
+}
+
+}  // namespace
+
+std::string Plan::describe() const {
+  std::ostringstream os;
+  for (size_t i = 0; i < steps.size(); ++i) {
+    const Step& s = steps[i];
+    os << i << ": " << s.name;
+    if (s.kind == Step::GEMM) {
+      const GemmArgs& g = s.gemm;
+      os << " batch=" << g.batch << " M=" << g.M << " N=" << g.N << " K=" << g.K << " A=" << dtype_name((DType)g.A.dtype)
+         << " B=" << dtype_name((DType)g.B.dtype) << (g.dual ? " dual" : "") << " epilogue=" << g.epilogue;
+    } else if (s.kind == Step::ELEMENTWISE) {
+      os << " instrs=" << s.ew.n_instr << " leaves=" << s.ew.n_leaves << " elems=" << s.ew.total;
+    } else if (s.kind == Step::REDUCE) {
+      os << " outer=" << s.red.outer << " inner=" << s.red.inner;
+    } else if (s.kind == Step::ATTENTION) {
+      os << " B=" << s.attn.B << " H=" << s.attn.H << " S=" << s.attn.Sq << " D=" << s.attn.D << " causal=" << s.attn.causal;
+    }
+    os << " flops=" << s.flops << " bytes=" << s.bytes << "\n";
+  }
+  return os.str();
+}
+
+Plan build_plan(const Graph& g) {
+  Planner p(g);
+  return p.run();
+}
+
+}  // namespace ryft

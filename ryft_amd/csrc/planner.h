@@ -1,0 +1,55 @@
+// StableHLO graph → fused execution plan: a list of kernel launches over numbered buffer slots.
+#pragma once
+
+#include <string>
+#include <vector>
+
+#include "ir.h"
+#include "kernel_abi.h"
+
+namespace ryft {
+
+struct Slot {
+  enum Kind { PARAM, TEMP, OUTPUT, CONSTANT } kind;
+  int index = 0;  // parameter index / output index
+  TensorType type;
+  std::vector<uint8_t> literal;  // CONSTANT payload
+};
+
+struct Step {
+  enum Kind { ELEMENTWISE, REDUCE, GEMM, ATTENTION, COPY } kind;
+  std::string name;  // kernel family, for profiling ("gemm_bf16_mfma", "attention_fwd", ...)
+  EwProgram ew;
+  ReduceArgs red;
+  GemmArgs gemm;
+  AttnArgs attn;
+  struct { int64_t bytes; } copy;
+  // Pointer fields inside the args block that refer to slots: (byte offset of the pointer field, slot). The
+  // field's initial value is a byte offset into the slot's buffer.
+  std::vector<std::pair<size_t, int>> patches;
+  double flops = 0;  // algorithmic FLOPs / OPs of this launch
+  double bytes = 0;  // algorithmic bytes read + written
+  void* args_block() {
+    switch (kind) {
+      case ELEMENTWISE: return &ew;
+      case REDUCE: return &red;
+      case GEMM: return &gemm;
+      case ATTENTION: return &attn;
+      default: return nullptr;
+    }
+  }
+};
+
+struct Plan {
+  std::vector<Slot> slots;
+  std::vector<Step> steps;
+  std::vector<int> param_slots;   // per graph parameter
+  std::vector<int> output_slots;  // per graph result
+  std::vector<TensorType> param_types, output_types;
+  double total_flops = 0, total_bytes = 0;
+  std::string describe() const;
+};
+
+Plan build_plan(const Graph& g);
+
+}  // namespace ryft

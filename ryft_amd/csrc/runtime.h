@@ -1,0 +1,220 @@
+// Runtime objects behind the PJRT handles: one client per process-visible MI355X, one HIP stream per device,
+// a caching device allocator, pinned staging for host transfers, and events completed by a worker thread.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <atomic>
+#include <condition_variable>
+#include <deque>
+#include <functional>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "common.h"
+#include "planner.h"
+
+namespace ryft {
+
+#define HIP_CHECK(expr)                                                                                    \
+  do {                                                                                                     \
+    hipError_t _e = (expr);                                                                                \
+    if (_e != hipSuccess)                                                                                  \
+      ::ryft::fail(PJRT_Error_Code_INTERNAL, std::string(#expr) + " failed: " + hipGetErrorString(_e));    \
+  } while (0)
+
+struct Client;
+
+// ------------------------------------------------------------------------------------------------ events
+struct EventState {
+  std::mutex mu;
+  std::condition_variable cv;
+  bool ready = false;
+  PJRT_Error_Code code = PJRT_Error_Code_OK;
+  std::string message;
+  std::vector<std::pair<PJRT_Event_OnReadyCallback, void*>> callbacks;
+  hipEvent_t hip_event = nullptr;  // completion marker on the device stream (null for host events)
+  std::function<void()> on_complete;  // host work run before the event turns ready (e.g. staging → user copy)
+
+  ~EventState();
+  // Marks the event ready (idempotent) and runs the registered callbacks on this thread.
+  void set_ready(PJRT_Error_Code c, const std::string& msg);
+  // Blocks until the event is ready; synchronizes its HIP event on the calling thread when it has one.
+  void wait();
+  bool poll();
+};
+using EventPtr = std::shared_ptr<EventState>;
+
+struct Event {  // PJRT_Event
+  EventPtr state;
+};
+
+// ------------------------------------------------------------------------------------------------ memory
+class DeviceAllocator {
+ public:
+  explicit DeviceAllocator(int device) : device_(device) {}
+  ~DeviceAllocator();
+  void* allocate(size_t bytes);
+  void release(void* p);
+  int64_t bytes_in_use() const { return in_use_; }
+  int64_t peak_bytes() const { return peak_; }
+  int64_t num_allocs() const { return allocs_; }
+
+ private:
+  static size_t round_size(size_t bytes);
+  void trim();
+  int device_;
+  std::mutex mu_;
+  std::map<size_t, std::vector<void*>> free_;  // size class → cached blocks
+  std::map<void*, size_t> live_;
+  int64_t in_use_ = 0, peak_ = 0, allocs_ = 0;
+};
+
+struct DeviceMem {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+  DeviceAllocator* alloc = nullptr;
+  ~DeviceMem() {
+    if (ptr && alloc) alloc->release(ptr);
+  }
+};
+
+class PinnedPool {
+ public:
+  ~PinnedPool();
+  struct Chunk {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    hipEvent_t last_use = nullptr;
+    bool busy = false;
+  };
+  Chunk* acquire(size_t bytes);
+  void release(Chunk* c, hipStream_t stream);  // reusable once the stream passes this point
+  void release_now(Chunk* c);
+
+ private:
+  std::mutex mu_;
+  std::vector<std::unique_ptr<Chunk>> chunks_;
+};
+
+// ------------------------------------------------------------------------------------------------ devices
+struct Memory;
+struct Device {  // PJRT_Device and PJRT_DeviceDescription
+  Client* client = nullptr;
+  int id = 0;
+  int hip_ordinal = 0;
+  std::string kind, debug, to_string, arch;
+  std::vector<PJRT_NamedValue> attributes;
+  std::vector<std::string> attribute_strings;
+  std::vector<Memory*> memories;
+  Memory* default_memory = nullptr;
+  hipStream_t stream = nullptr;
+  std::unique_ptr<DeviceAllocator> allocator;
+  std::recursive_mutex launch_mu;  // serializes enqueue on the device stream
+};
+
+struct Memory {  // PJRT_Memory
+  Client* client = nullptr;
+  int id = 0;
+  std::string kind = "device";
+  std::string debug, to_string;
+  std::vector<Device*> devices;
+};
+
+// ------------------------------------------------------------------------------------------------ buffers
+struct Buffer {  // PJRT_Buffer
+  Client* client = nullptr;
+  Device* device = nullptr;
+  DType dtype = DType::INVALID;
+  std::vector<int64_t> dims;
+  std::shared_ptr<DeviceMem> mem;
+  EventPtr ready;
+  std::atomic<bool> deleted{false};
+  std::atomic<int> external_refs{0};
+  std::vector<int64_t> minor_to_major;
+  size_t bytes() const { return (size_t)num_elements(dims) * dtype_size(dtype); }
+};
+
+// ------------------------------------------------------------------------------------------------ executables
+struct Executable {  // PJRT_Executable (shared by the loaded executable and every view handed out)
+  std::string name;
+  std::string fingerprint;
+  std::string program_text;
+  std::string compile_options;
+  Plan plan;
+  std::vector<PJRT_Buffer_Type> output_types;
+  std::vector<int64_t> output_dims_flat;
+  std::vector<size_t> output_ranks;
+  std::vector<const char*> output_memory_kinds;
+  std::vector<size_t> output_memory_kind_sizes;
+  std::vector<PJRT_NamedValue> cost_properties;
+  std::vector<std::shared_ptr<DeviceMem>> constants;  // by slot (null for non-constant slots)
+};
+
+struct ExecutableView {  // what PJRT_Executable* points to
+  std::shared_ptr<Executable> exe;
+};
+
+struct LoadedExecutable {  // PJRT_LoadedExecutable
+  Client* client = nullptr;
+  std::shared_ptr<Executable> exe;
+  std::vector<Device*> devices;
+  std::vector<PJRT_LogicalDeviceIds> logical_ids;
+  std::atomic<bool> deleted{false};
+};
+
+// ------------------------------------------------------------------------------------------------ client
+struct StepTiming {
+  std::string name;
+  double flops = 0, bytes = 0;
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+
+struct Client {  // PJRT_Client
+  std::string platform_name = "rocm";
+  std::string platform_version;
+  std::vector<std::unique_ptr<Device>> devices;
+  std::vector<Device*> device_ptrs;
+  std::vector<std::unique_ptr<Memory>> memories;
+  std::vector<Memory*> memory_ptrs;
+  PinnedPool pinned;
+
+  // completion worker: fires OnReady callbacks / host-side copy completions in stream order
+  std::mutex q_mu;
+  std::condition_variable q_cv;
+  std::deque<EventPtr> queue;
+  bool stopping = false;
+  std::thread worker;
+
+  // kernel timing (profiling extension)
+  std::mutex prof_mu;
+  bool profiling = false;
+  std::vector<StepTiming> timings;
+
+  Client(const std::vector<int>& visible, bool compile_only);
+  ~Client();
+  void enqueue_completion(const EventPtr& e);
+  EventPtr record_event(Device* d, std::function<void()> on_complete = nullptr);
+  std::shared_ptr<DeviceMem> allocate(Device* d, size_t bytes);
+};
+
+// Creates a device buffer holding a copy of `data` (dense row-major unless byte_strides is given).
+Buffer* buffer_from_host(Client* c, Device* d, const void* data, DType t, const std::vector<int64_t>& dims,
+                         const int64_t* byte_strides, size_t num_byte_strides, EventPtr* done_with_host);
+// Starts a device → host copy into `dst`; returns the completion event.
+EventPtr buffer_to_host(Buffer* b, void* dst, size_t dst_size);
+// Compiles a StableHLO program.
+std::shared_ptr<Executable> compile_program(Client* c, const std::string& code, const std::string& format,
+                                            const std::string& options);
+// Enqueues one execution; fills outputs and returns the completion event.
+EventPtr execute(LoadedExecutable* le, Device* d, Buffer* const* args, size_t num_args, std::vector<Buffer*>* outputs);
+// Copies a buffer to another buffer on the same device.
+Buffer* copy_buffer(Buffer* src, Device* d);
+
+std::string kernel_timing_json(Client* c);
+
+}  // namespace ryft

@@ -1,0 +1,135 @@
+"""GPU coverage of the generic kernels (elementwise programs, reductions, transposes, iota / compare / select,
+conversions, the generic GEMM) against the oracle on small shapes."""
+import numpy as np
+import pytest
+
+from oracle import stablehlo as sh
+from ryft_amd import configs, hostdata as hd, pjrt
+from tests.helpers import check, oracle_outputs, run_pjrt
+
+pytestmark = pytest.mark.gpu
+
+
+def _mod(args, rets, body):
+    sig = ", ".join(f"%arg{i}: {t}" for i, t in enumerate(args))
+    ret = rets[0] if len(rets) == 1 else "(" + ", ".join(rets) + ")"
+    return f"module {{\n  func.func @main({sig}) -> {ret} {{\n{body}\n  }}\n}}\n"
+
+
+F = "tensor<8x33xf32>"
+
+
+def _f32_inputs(n, shape=(8, 33), seed=1):
+    return [configs.HostInput(hd.normal(seed + i, shape), pjrt.BufferType.F32, shape) for i in range(n)]
+
+
+@pytest.mark.parametrize("op", ["add", "subtract", "multiply", "divide", "maximum", "minimum"])
+def test_binary_f32(gpu_client, op):
+    prog = _mod([F, F], [F], f"    %0 = stablehlo.{op} %arg0, %arg1 : {F}\n    return %0 : {F}")
+    ins = _f32_inputs(2)
+    outs, _ = run_pjrt(gpu_client, prog, ins)
+    check(outs[0], oracle_outputs(prog, ins)[0], 1e-6, op)
+
+
+@pytest.mark.parametrize("op", ["exponential", "log", "rsqrt", "sqrt", "tanh", "logistic", "negate", "abs", "floor"])
+def test_unary_f32(gpu_client, op):
+    prog = _mod([F], [F], f"    %0 = stablehlo.abs %arg0 : {F}\n    %1 = stablehlo.{op} %0 : {F}\n    return %1 : {F}")
+    ins = _f32_inputs(1)
+    outs, _ = run_pjrt(gpu_client, prog, ins)
+    check(outs[0], oracle_outputs(prog, ins)[0], 2e-6, op)
+
+
+def test_int_ops_and_wraparound(gpu_client):
+    T = "tensor<64xi32>"
+    body = f"""    %0 = stablehlo.multiply %arg0, %arg1 : {T}
+    %1 = stablehlo.add %0, %arg0 : {T}
+    %2 = stablehlo.divide %1, %arg1 : {T}
+    %3 = stablehlo.remainder %1, %arg1 : {T}
+    %4 = stablehlo.maximum %2, %3 : {T}
+    %5 = stablehlo.convert %4 : ({T}) -> tensor<64xi8>
+    return %1, %5 : {T}, tensor<64xi8>"""
+    prog = _mod([T, T], [T, "tensor<64xi8>"], body)
+    a = hd.int_uniform(3, (64,), -2 ** 30, 2 ** 30).astype(np.int32)
+    b = hd.int_uniform(4, (64,), 1, 1000).astype(np.int32) * np.where(np.arange(64) % 2, 1, -1).astype(np.int32)
+    ins = [configs.HostInput(a, pjrt.BufferType.S32, (64,)), configs.HostInput(b, pjrt.BufferType.S32, (64,))]
+    outs, _ = run_pjrt(gpu_client, prog, ins)
+    for o, w in zip(outs, oracle_outputs(prog, ins)):
+        check(o, w, 0, "int")
+
+
+def test_convert_chain_bf16_f8(gpu_client):
+    body = f"""    %0 = stablehlo.convert %arg0 : ({F}) -> tensor<8x33xbf16>
+    %1 = stablehlo.convert %0 : (tensor<8x33xbf16>) -> tensor<8x33xf8E4M3FN>
+    %2 = stablehlo.convert %arg0 : ({F}) -> tensor<8x33xi32>
+    return %0, %1, %2 : tensor<8x33xbf16>, tensor<8x33xf8E4M3FN>, tensor<8x33xi32>"""
+    prog = _mod([F], ["tensor<8x33xbf16>", "tensor<8x33xf8E4M3FN>", "tensor<8x33xi32>"], body)
+    x = np.concatenate([hd.normal(5, (8 * 33 - 6,), 0, 100), np.array([464, 470, -500, 1e-3, 2.5, -2.5])])
+    ins = [configs.HostInput(x.astype(np.float32).reshape(8, 33), pjrt.BufferType.F32, (8, 33))]
+    outs, _ = run_pjrt(gpu_client, prog, ins)
+    for i, (o, w) in enumerate(zip(outs, oracle_outputs(prog, ins))):
+        # conversions are exact: compare bits
+        assert np.array_equal(np.asarray(o).view(np.uint8), sh.to_raw(w[0], w[1]).view(np.uint8)) or \
+            np.array_equal(np.isnan(sh.from_raw(o, w[1])), np.isnan(w[0])), f"convert output {i}"
+
+
+@pytest.mark.parametrize("dims,body", [([1], "add"), ([0], "add"), ([0, 1], "maximum"), ([1], "minimum")])
+def test_reduce(gpu_client, dims, body):
+    out_shape = [s for i, s in enumerate((8, 33)) if i not in dims]
+    ot = "tensor<" + "".join(f"{s}x" for s in out_shape) + "f32>"
+    init = "0.000000e+00" if body == "add" else ("0xFF800000" if body == "maximum" else "0x7F800000")
+    prog = _mod([F], [ot], f"""    %cst = stablehlo.constant dense<{init}> : tensor<f32>
+    %0 = stablehlo.reduce(%arg0 init: %cst) applies stablehlo.{body} across dimensions = {dims} : ({F}, tensor<f32>) -> {ot}
+    return %0 : {ot}""")
+    ins = _f32_inputs(1)
+    outs, _ = run_pjrt(gpu_client, prog, ins)
+    check(outs[0], oracle_outputs(prog, ins)[0], 1e-6, "reduce")
+
+
+def test_reduce_with_argument_init(gpu_client):
+    prog = _mod(["tensor<3x4xi32>", "tensor<i32>"], ["tensor<3xi32>"], """    %0 = stablehlo.reduce(%arg0 init: %arg1) applies stablehlo.add across dimensions = [1] : (tensor<3x4xi32>, tensor<i32>) -> tensor<3xi32>
+    return %0 : tensor<3xi32>""")
+    ins = [configs.HostInput(np.arange(12, dtype=np.int32).reshape(3, 4), pjrt.BufferType.S32, (3, 4)),
+           configs.HostInput(np.array(100, dtype=np.int32), pjrt.BufferType.S32, ())]
+    outs, _ = run_pjrt(gpu_client, prog, ins)
+    assert outs[0].tolist() == [106, 122, 138]
+
+
+def test_transpose_broadcast_iota_select(gpu_client):
+    body = """    %0 = stablehlo.transpose %arg0, dims = [1, 0] : (tensor<8x33xf32>) -> tensor<33x8xf32>
+    %1 = stablehlo.iota dim = 0 : tensor<33x8xi32>
+    %2 = stablehlo.iota dim = 1 : tensor<33x8xi32>
+    %3 = stablehlo.compare  LT, %2, %1,  SIGNED : (tensor<33x8xi32>, tensor<33x8xi32>) -> tensor<33x8xi1>
+    %4 = stablehlo.broadcast_in_dim %arg1, dims = [1] : (tensor<8xf32>) -> tensor<33x8xf32>
+    %5 = stablehlo.select %3, %0, %4 : tensor<33x8xi1>, tensor<33x8xf32>
+    %6 = stablehlo.reshape %5 : (tensor<33x8xf32>) -> tensor<264xf32>
+    return %6 : tensor<264xf32>"""
+    prog = _mod([F, "tensor<8xf32>"], ["tensor<264xf32>"], body)
+    ins = _f32_inputs(1) + [configs.HostInput(hd.normal(9, (8,)), pjrt.BufferType.F32, (8,))]
+    outs, _ = run_pjrt(gpu_client, prog, ins)
+    check(outs[0], oracle_outputs(prog, ins)[0], 0.0, "select")
+
+
+def test_generic_gemm_transposed_operands(gpu_client):
+    # lhs contracting dim first (m-contiguous A) and a rank-3 batch layout: generic GEMM path
+    body = """    %0 = stablehlo.dot_general %arg0, %arg1, batching_dims = [2] x [0], contracting_dims = [0] x [2] : (tensor<24x20x3xf32>, tensor<3x18x24xf32>) -> tensor<3x20x18xf32>
+    %1 = stablehlo.exponential %0 : tensor<3x20x18xf32>
+    return %1 : tensor<3x20x18xf32>"""
+    prog = _mod(["tensor<24x20x3xf32>", "tensor<3x18x24xf32>"], ["tensor<3x20x18xf32>"], body)
+    ins = [configs.HostInput(hd.normal(11, (24, 20, 3), 0, 0.2), pjrt.BufferType.F32, (24, 20, 3)),
+           configs.HostInput(hd.normal(12, (3, 18, 24), 0, 0.2), pjrt.BufferType.F32, (3, 18, 24))]
+    outs, exe = run_pjrt(gpu_client, prog, ins)
+    check(outs[0], oracle_outputs(prog, ins)[0], 1e-5, "generic gemm")
+
+
+def test_mfma_bf16_with_generic_epilogue(gpu_client):
+    # an epilogue the MFMA kernels do not implement natively (tanh): dot on MFMA, expression as its own kernel
+    T, O = "tensor<128x128xbf16>", "tensor<128x128xf32>"
+    body = f"""    %0 = stablehlo.dot_general %arg0, %arg1, contracting_dims = [1] x [0] : ({T}, {T}) -> {O}
+    %1 = stablehlo.tanh %0 : {O}
+    return %1 : {O}"""
+    prog = _mod([T, T], [O], body)
+    ins = [configs.HostInput(hd.f32_to_bf16_bits(hd.normal(13 + i, (128, 128), 0, 0.1)), pjrt.BufferType.BF16,
+                             (128, 128)) for i in range(2)]
+    outs, exe = run_pjrt(gpu_client, prog, ins)
+    assert "gemm_bf16_mfma" in exe.describe_plan()
+    check(outs[0], oracle_outputs(prog, ins)[0], 1e-4, "bf16+tanh")

@@ -1,0 +1,183 @@
+"""GPU parity: every config through the PJRT C API (client.compile → buffer → execute → await → copy_to_host),
+compared with the oracle on the same seeded inputs.
+
+Tolerances (normwise relative error): f32 1e-4; bf16 1e-2; int8→i32 bit-exact and the scaled f32
+output 1e-5; causal attention 2e-2; fp8 SwiGLU 3e-2. Full BASELINE sizes run for C1, C2, C3 and C5; C4 at full size
+is checked on sampled heads plus size-independent properties (finite output, row 0 equals V[0]).
+"""
+import numpy as np
+import pytest
+
+from oracle import numerics as nm
+from oracle import stablehlo as sh
+from ryft_amd import configs, pjrt
+from tests.helpers import MLIR_DT, check, oracle_outputs, run_pjrt
+
+pytestmark = pytest.mark.gpu
+
+
+def _run_and_check(client, w, oracle_w=None):
+    print(f"[parity] {w.name}", flush=True)
+    outs, exe = run_pjrt(client, w.program, w.inputs)
+    want = oracle_outputs((oracle_w or w).program, (oracle_w or w).inputs)
+    errs = [check(o, r, w.tolerance, f"{w.name}[{i}]") for i, (o, r) in enumerate(zip(outs, want))]
+    print(f"[parity] {w.name} errors {errs}", flush=True)
+    return outs, exe
+
+
+def test_client_basics(gpu_client):
+    c = gpu_client
+    assert c.platform_name() == "rocm"
+    devs = c.addressable_devices()
+    assert len(devs) >= 1
+    d = devs[0]
+    assert d.attributes()["gfx_arch"].startswith("gfx950")
+    assert d.default_memory().kind() == "device"
+    assert c.lookup_device(0) == d
+    with pytest.raises(pjrt.PjrtError) as e:
+        c.lookup_device(len(devs))
+    assert e.value.code == pjrt.ErrorCode.INVALID_ARGUMENT
+
+
+@pytest.mark.parametrize("bt,np_t", [(pjrt.BufferType.F32, np.float32), (pjrt.BufferType.BF16, np.uint16),
+                                     (pjrt.BufferType.S8, np.int8), (pjrt.BufferType.S32, np.int32),
+                                     (pjrt.BufferType.F8E4M3FN, np.uint8), (pjrt.BufferType.PRED, np.bool_),
+                                     (pjrt.BufferType.F64, np.float64), (pjrt.BufferType.U8, np.uint8)])
+def test_buffer_round_trip(gpu_client, bt, np_t):
+    # buffers.rs:3874-3923: bytes in == bytes out
+    rng = np.random.default_rng(int(bt))
+    raw = rng.integers(0, 256, size=3 * 5 * 7 * np.dtype(np_t).itemsize, dtype=np.uint8)
+    if np_t == np.bool_:
+        raw = raw & 1
+    b = gpu_client.buffer(raw.tobytes(), bt, (3, 5, 7))
+    assert b.element_type() == bt and b.dimensions() == [3, 5, 7]
+    assert not b.is_on_cpu()
+    assert b.on_device_size_in_bytes() == raw.size
+    assert b.copy_to_host().await_() == raw.tobytes()
+
+
+def test_buffer_strided_upload(gpu_client):
+    x = np.arange(12, dtype=np.float32).reshape(3, 4)
+    xt = np.asfortranarray(x)
+    b = gpu_client.buffer(xt.tobytes(order="A"), pjrt.BufferType.F32, (3, 4), byte_strides=(4, 12))
+    assert np.array_equal(b.to_numpy(), x)
+
+
+def test_readme_kat(gpu_client):
+    prog = """module {
+  func.func @main(%arg0: tensor<2x3xf32>, %arg1: tensor<3x2xf32>) -> tensor<2x2xf32> {
+    %0 = stablehlo.dot_general %arg0, %arg1, contracting_dims = [1] x [0] : (tensor<2x3xf32>, tensor<3x2xf32>) -> tensor<2x2xf32>
+    return %0 : tensor<2x2xf32>
+  }
+}"""
+    exe = gpu_client.compile(pjrt.Program.mlir(prog), pjrt.CompilationOptions())
+    device = exe.addressable_devices()[0]
+    lhs = gpu_client.buffer(np.array([1, 2, 3, 4, 5, 6], np.float32), pjrt.BufferType.F32, (2, 3), device=device)
+    rhs = gpu_client.buffer(np.array([7, 8, 9, 10, 11, 12], np.float32), pjrt.BufferType.F32, (3, 2), device=device)
+    out = exe.execute([[lhs, rhs]])[0]
+    out.done.await_()
+    got = np.frombuffer(out.outputs[0].copy_to_host().await_(), np.float32)
+    assert got.tolist() == [58.0, 64.0, 139.0, 154.0]
+
+
+def test_add_kat(gpu_client):
+    prog = """module {
+  func.func @main(%arg0: tensor<2xi32>, %arg1: tensor<2xi32>) -> tensor<2xi32> {
+    %0 = stablehlo.add %arg0, %arg1 : tensor<2xi32>
+    return %0 : tensor<2xi32>
+  }
+}"""
+    exe = gpu_client.compile(pjrt.Program.mlir(prog))
+    a = gpu_client.buffer(np.array([7, -1], np.int32), pjrt.BufferType.S32, (2,))
+    b = gpu_client.buffer(np.array([35, -41], np.int32), pjrt.BufferType.S32, (2,))
+    out = exe.execute([[a, b]])[0]
+    seen = []
+    out.done.on_ready(lambda err: seen.append(err))
+    out.done.await_()
+    assert out.outputs[0].to_numpy().tolist() == [42, -42]
+    assert out.done.is_ready()
+
+
+def test_execute_validates_arguments(gpu_client):
+    w = configs.c1_f32_dot(m=64, k=64, n=64)
+    exe = gpu_client.compile(pjrt.Program.mlir(w.program))
+    a = gpu_client.buffer(w.inputs[0].data, w.inputs[0].type, w.inputs[0].dims)
+    with pytest.raises(pjrt.PjrtError) as e:
+        exe.execute([[a]])
+    assert e.value.code == pjrt.ErrorCode.INVALID_ARGUMENT
+    with pytest.raises(pjrt.PjrtError) as e:
+        exe.execute([[a, a]])  # wrong shape for the rhs
+    assert e.value.code == pjrt.ErrorCode.INVALID_ARGUMENT
+
+
+def test_c1_f32_full(gpu_client):
+    _run_and_check(gpu_client, configs.c1_f32_dot())
+
+
+@pytest.mark.parametrize("kw", [dict(batch=2, m=128, k=128, n=128), dict(batch=1, m=64, k=96, n=80),
+                                dict(batch=3, m=256, k=512, n=256)])
+def test_c2_bf16_small(gpu_client, kw):
+    _run_and_check(gpu_client, configs.c2_bf16_batched_dot(**kw))
+
+
+def test_c2_bf16_full(gpu_client):
+    _run_and_check(gpu_client, configs.c2_bf16_batched_dot())
+
+
+@pytest.mark.parametrize("kw", [dict(m=128, k=256, n=128), dict(m=256, k=512, n=512), dict(m=96, k=64, n=48)])
+def test_c3_int8_small(gpu_client, kw):
+    _run_and_check(gpu_client, configs.c3_int8_gemm(**kw))
+
+
+def test_c3_int8_full(gpu_client):
+    _run_and_check(gpu_client, configs.c3_int8_gemm())
+
+
+@pytest.mark.parametrize("kw", [dict(b=1, h=2, s=256, d=128), dict(b=2, h=1, s=128, d=64), dict(b=1, h=1, s=512, d=128)])
+def test_c4_attention_small(gpu_client, kw):
+    w = configs.c4_causal_attention(**kw)
+    outs, exe = _run_and_check(gpu_client, w)
+    assert "attention_fwd" in exe.describe_plan()
+
+
+def test_c4_attention_full_sampled(gpu_client):
+    w = configs.c4_causal_attention()
+    outs, exe = run_pjrt(gpu_client, w.program, w.inputs)
+    assert "attention_fwd" in exe.describe_plan()
+    got = sh.from_raw(outs[0], "bf16")
+    assert np.all(np.isfinite(got))
+    v = sh.from_raw(w.inputs[2].data, "bf16")
+    assert np.array_equal(got[:, :, 0, :], nm.round_to(v[:, :, 0, :], "bf16"))  # row 0 attends to key 0 only
+    small = configs.c4_causal_attention(b=1, h=1, s=2048, d=128)
+    for (bi, hi) in [(0, 0), (3, 31), (2, 17)]:
+        sub = [configs.HostInput(x.data[bi:bi + 1, hi:hi + 1].copy(), x.type, (1, 1, 2048, 128)) for x in w.inputs]
+        (want, dt), = oracle_outputs(small.program, sub)
+        err = sh.rel_error(got[bi:bi + 1, hi:hi + 1], want)
+        print(f"[parity] c4 head ({bi},{hi}) error {err:.3e}", flush=True)
+        assert err <= w.tolerance
+
+
+@pytest.mark.parametrize("kw", [dict(m=128, d=256, f=512), dict(m=64, d=256, f=384)])
+def test_c5_swiglu_small(gpu_client, kw):
+    _run_and_check(gpu_client, configs.c5_swiglu_fp8(**kw))
+
+
+def test_c5_swiglu_weight_only_bf16(gpu_client):
+    _run_and_check(gpu_client, configs.c5_swiglu_fp8(m=64, d=256, f=512, activations="bf16"))
+
+
+def test_c5_swiglu_full(gpu_client):
+    _run_and_check(gpu_client, configs.c5_swiglu_fp8())
+
+
+def test_repeated_execution_is_deterministic(gpu_client):
+    w = configs.c2_bf16_batched_dot(batch=2, m=256, k=256, n=256)
+    exe = gpu_client.compile(pjrt.Program.mlir(w.program))
+    bufs = [gpu_client.buffer(x.data, x.type, x.dims) for x in w.inputs]
+    first = None
+    for _ in range(5):
+        out = exe.execute([bufs])[0]
+        out.done.await_()
+        r = out.outputs[0].copy_to_host().await_()
+        first = first or r
+        assert r == first

@@ -1,0 +1,167 @@
+"""Pins the CPU oracle before it is trusted as the parity checker.
+
+Each oracle function is checked against something a plausible mistake would fail:
+  * dot_general   README KAT [58,64,139,154] (README.md:122-137); brute-force loops over batch / permuted
+                  contracting dims; exact int64 for i8→i32.
+  * add (i32)     KAT [7,-1]+[35,-41] = [42,-42] (crates/ryft-pjrt/src/programs.rs:2781-2829).
+  * narrow floats exhaustive decode of all bf16 / f8E4M3FN codes and random encodes vs torch's CPU dtype casts
+                  (third-party, not the reference), plus the f8 overflow edge (448 / 464 / 480).
+  * softmax attention  torch scaled_dot_product_attention(is_causal=True) in float64; rows of P sum to one.
+  * RMSNorm + SwiGLU   closed form in float64 numpy (independent code path).
+  * reduce / broadcast / transpose / iota / compare / select   closed forms on small inputs.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import numerics as nm
+from oracle import stablehlo as sh
+from ryft_amd import configs
+from ryft_amd import hostdata as hd
+
+
+def _mod(args, ret, body):
+    sig = ", ".join(f"%arg{i}: {t}" for i, t in enumerate(args))
+    return f"module {{\n  func.func @main({sig}) -> {ret} {{\n{body}\n  }}\n}}\n"
+
+
+def test_readme_dot_kat():
+    prog = _mod(["tensor<2x3xf32>", "tensor<3x2xf32>"], "tensor<2x2xf32>",
+                "    %0 = stablehlo.dot_general %arg0, %arg1, contracting_dims = [1] x [0] : "
+                "(tensor<2x3xf32>, tensor<3x2xf32>) -> tensor<2x2xf32>\n    return %0 : tensor<2x2xf32>")
+    (out, dt), = sh.evaluate(prog, [np.array([[1., 2, 3], [4, 5, 6]]), np.array([[7., 8], [9, 10], [11, 12]])])
+    assert dt == "f32"
+    assert out.ravel().tolist() == [58.0, 64.0, 139.0, 154.0]
+
+
+def test_add_kat():
+    prog = _mod(["tensor<2xi32>", "tensor<2xi32>"], "tensor<2xi32>",
+                "    %0 = stablehlo.add %arg0, %arg1 : tensor<2xi32>\n    return %0 : tensor<2xi32>")
+    (out, _), = sh.evaluate(prog, [np.array([7, -1]), np.array([35, -41])])
+    assert out.tolist() == [42, -42]
+
+
+def test_dot_general_brute_force_batch_and_permuted_contraction():
+    rng = np.random.default_rng(0)
+    a = rng.integers(-5, 6, (3, 4, 2, 5)).astype(float)  # [b, k1, m, k2]
+    b = rng.integers(-5, 6, (5, 3, 6, 4)).astype(float)  # [k2, b, n, k1]
+    prog = _mod(["tensor<3x4x2x5xf32>", "tensor<5x3x6x4xf32>"], "tensor<3x2x6xf32>",
+                "    %0 = stablehlo.dot_general %arg0, %arg1, batching_dims = [0] x [1], contracting_dims = [1, 3] x [3, 0]"
+                " : (tensor<3x4x2x5xf32>, tensor<5x3x6x4xf32>) -> tensor<3x2x6xf32>\n    return %0 : tensor<3x2x6xf32>")
+    (out, _), = sh.evaluate(prog, [a, b])
+    want = np.zeros((3, 2, 6))
+    for bb in range(3):
+        for m in range(2):
+            for n in range(6):
+                for k1 in range(4):
+                    for k2 in range(5):
+                        want[bb, m, n] += a[bb, k1, m, k2] * b[k2, bb, n, k1]
+    assert np.array_equal(out, want)
+
+
+def test_int8_dot_exact():
+    w = configs.c3_int8_gemm(m=64, k=96, n=32)
+    a, b = w.inputs[0].data.astype(np.int64), w.inputs[1].data.astype(np.int64)
+    outs = sh.evaluate(w.program, [sh.from_raw(x.data, t) for x, t in zip(w.inputs, ["i8", "i8", "f32", "f32"])])
+    assert outs[0][1] == "i32"
+    assert np.array_equal(outs[0][0], a @ b)
+    scaled = (a @ b).astype(np.float64) * w.inputs[2].data.astype(np.float64) * w.inputs[3].data.astype(np.float64)
+    assert sh.rel_error(outs[1][0], scaled) < 1e-6
+
+
+def test_bf16_decode_exhaustive_vs_torch():
+    codes = np.arange(1 << 16, dtype=np.uint16)
+    want = torch.from_numpy(codes.view(np.int16)).view(torch.bfloat16).float().numpy().astype(np.float64)
+    got = nm.decode_bits(codes, "bf16")
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(got[~np.isnan(got)], want[~np.isnan(want)])
+
+
+def test_f8e4m3fn_decode_exhaustive_vs_torch():
+    codes = np.arange(256, dtype=np.uint8)
+    want = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy().astype(np.float64)
+    got = nm.decode_bits(codes, "f8E4M3FN")
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(got[~np.isnan(got)], want[~np.isnan(want)])
+    assert np.nanmax(got) == 448.0
+
+
+@pytest.mark.parametrize("dtype,torch_dtype,scale", [("bf16", torch.bfloat16, 1e3), ("f8E4M3FN", torch.float8_e4m3fn, 30.0),
+                                                     ("f16", torch.float16, 1e2)])
+def test_encode_random_vs_torch(dtype, torch_dtype, scale):
+    x = hd.normal(7, (300000,), 0.0, scale)
+    edges = np.array([448, 460, 464, 465, 479, 480, 500, 1e6, -464, -470, 2 ** -10, 1.5 * 2 ** -9, 3 * 2 ** -10, 0.0,
+                      -0.0, 65504, 65520, 65536], dtype=np.float32)
+    x = np.concatenate([x, edges]).astype(np.float32)
+    bits = torch.from_numpy(x).to(torch_dtype)
+    want = bits.view(torch.uint8 if torch_dtype == torch.float8_e4m3fn else torch.int16).numpy()
+    got = nm.encode_bits(x, dtype)
+    assert np.array_equal(got.view(want.dtype), want)
+
+
+def test_product_encoders_agree_with_oracle():
+    x = np.concatenate([hd.normal(9, (200000,), 0.0, 50.0), np.array([464, 470, -1e9, 1e-12], np.float32)])
+    assert np.array_equal(hd.f32_to_bf16_bits(x), nm.encode_bits(x, "bf16"))
+    assert np.array_equal(hd.f32_to_e4m3fn_bits(x), nm.encode_bits(x, "f8E4M3FN"))
+    codes = np.arange(256, dtype=np.uint8)
+    a, b = hd.e4m3fn_bits_to_f32(codes), nm.decode_bits(codes, "f8E4M3FN")
+    assert np.array_equal(np.isnan(a), np.isnan(b)) and np.array_equal(a[~np.isnan(a)], b[~np.isnan(b)])
+
+
+def test_causal_attention_vs_torch_sdpa():
+    w = configs.c4_causal_attention(b=1, h=2, s=128, d=64)
+    ins = [sh.from_raw(x.data, "bf16") for x in w.inputs]
+    (out, dt), = sh.evaluate(w.program, ins)
+    assert dt == "bf16"
+    q, k, v = (torch.from_numpy(x) for x in ins)
+    ref = torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True).numpy()
+    assert sh.rel_error(out, ref) < 1e-2
+    # row 0 attends only to key 0: output row 0 = bf16(V[0])
+    assert np.array_equal(out[:, :, 0, :], nm.round_to(ins[2][:, :, 0, :], "bf16"))
+
+
+def test_rmsnorm_swiglu_closed_form():
+    m, d, f = 16, 64, 96
+    w = configs.c5_swiglu_fp8(m=m, d=d, f=f, activations="bf16")
+    ins = [sh.from_raw(x.data, t) for x, t in zip(w.inputs, ["bf16", "bf16", "f8E4M3FN", "f32", "f8E4M3FN", "f32",
+                                                               "f8E4M3FN", "f32"])]
+    (out, _), = sh.evaluate(w.program, ins)
+    x, g, wg, sg, wu, su, wd, sd = ins
+    xn = x / np.sqrt(np.mean(x * x, axis=1, keepdims=True) + 1e-6) * g[None, :]
+    xn = nm.round_to(xn, "bf16")
+    gg = (xn @ wg) * sg
+    uu = (xn @ wu) * su
+    h = nm.round_to(gg / (1 + np.exp(-gg)) * uu, "bf16")
+    ref = (h @ wd) * sd
+    assert sh.rel_error(out, ref) < 1e-2
+
+
+def test_reduce_broadcast_transpose_iota_select():
+    prog = _mod(["tensor<3x4xf32>"], "(tensor<3xf32>, tensor<4x3xf32>, tensor<3x4xf32>)", """
+    %cst = stablehlo.constant dense<0.000000e+00> : tensor<f32>
+    %0 = stablehlo.reduce(%arg0 init: %cst) applies stablehlo.add across dimensions = [1] : (tensor<3x4xf32>, tensor<f32>) -> tensor<3xf32>
+    %1 = stablehlo.transpose %arg0, dims = [1, 0] : (tensor<3x4xf32>) -> tensor<4x3xf32>
+    %2 = stablehlo.iota dim = 0 : tensor<3x4xi32>
+    %3 = stablehlo.iota dim = 1 : tensor<3x4xi32>
+    %4 = stablehlo.compare  LE, %3, %2,  SIGNED : (tensor<3x4xi32>, tensor<3x4xi32>) -> tensor<3x4xi1>
+    %5 = stablehlo.broadcast_in_dim %0, dims = [0] : (tensor<3xf32>) -> tensor<3x4xf32>
+    %6 = stablehlo.select %4, %arg0, %5 : tensor<3x4xi1>, tensor<3x4xf32>
+    return %0, %1, %6 : tensor<3xf32>, tensor<4x3xf32>, tensor<3x4xf32>""")
+    x = np.arange(12, dtype=float).reshape(3, 4)
+    (r, _), (t, _), (s, _) = sh.evaluate(prog, [x])
+    assert r.tolist() == x.sum(1).tolist()
+    assert np.array_equal(t, x.T)
+    want = np.where(np.arange(4)[None, :] <= np.arange(3)[:, None], x, x.sum(1)[:, None])
+    assert np.array_equal(s, want)
+
+
+def test_broadcast_in_dim_permuting_dims():
+    # manipulation.rs:305 example: [1,3] → [2,3,2] with dims = [2, 1]
+    prog = _mod(["tensor<1x3xi32>"], "tensor<2x3x2xi32>", """
+    %0 = stablehlo.broadcast_in_dim %arg0, dims = [2, 1] : (tensor<1x3xi32>) -> tensor<2x3x2xi32>
+    return %0 : tensor<2x3x2xi32>""")
+    (out, _), = sh.evaluate(prog, [np.array([[1, 2, 3]])])
+    want = np.array([[[1, 1], [2, 2], [3, 3]], [[1, 1], [2, 2], [3, 3]]])
+    assert np.array_equal(out, want)

@@ -1,0 +1,226 @@
+"""CPU-side checks of the plugin: the C-ABI library, the PJRT table, the StableHLO front-end and the planner.
+
+Runs without a GPU through a compile-only client (programs are parsed and planned; nothing executes).
+"""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from ryft_amd import configs, pjrt
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_library_exports_only_get_pjrt_api():
+    out = subprocess.run(["nm", "-D", "--defined-only", pjrt.DEFAULT_PLUGIN_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    syms = sorted({ln.split()[-1].split("@")[0] for ln in out.splitlines() if ln.strip()})
+    assert syms == ["GetPjrtApi"]
+
+
+def test_header_declares_what_the_library_exports():
+    header = open(os.path.join(ROOT, "include", "ryft_mi355x.h")).read()
+    decls = re.findall(r"^\s*(?:const\s+)?\w+\*?\s+(\w+)\(void\);", header, re.M)
+    lib = ctypes.CDLL(pjrt.DEFAULT_PLUGIN_PATH)
+    assert decls == ["GetPjrtApi"]
+    for d in decls:
+        assert hasattr(lib, d)
+
+
+def test_api_table(plugin):
+    api = plugin.api()
+    assert api.version == pjrt.VERSION == (0, 104)
+    assert api.struct_size == 40 + 135 * 8
+    assert len(pjrt.SLOTS) == 135
+    # slots ryft-pjrt calls on the hot path are populated
+    for name in ["PJRT_Client_Create", "PJRT_Client_Compile", "PJRT_Client_BufferFromHostBuffer",
+                 "PJRT_LoadedExecutable_Execute", "PJRT_LoadedExecutable_GetExecutable", "PJRT_Executable_NumOutputs",
+                 "PJRT_Executable_Destroy", "PJRT_Buffer_ToHostBuffer", "PJRT_Event_Await", "PJRT_Event_OnReady",
+                 "PJRT_Device_DefaultMemory", "PJRT_Error_Destroy"]:
+        assert api.fn(name) is not None
+    with pytest.raises(pjrt.PjrtError) as e:
+        api.fn("PJRT_Compile")
+    assert e.value.code == pjrt.ErrorCode.UNIMPLEMENTED
+
+
+def test_plugin_attributes(plugin):
+    attrs = plugin.attributes()
+    assert attrs["stablehlo_current_version"] == [1, 16, 0]
+    assert attrs["stablehlo_minimum_version"] == [0, 9, 0]
+    assert attrs["xla_version"] == 2
+    with pytest.raises(pjrt.PjrtError) as e:
+        plugin.attribute("__missing__")
+    assert e.value.code == pjrt.ErrorCode.NOT_FOUND
+
+
+def test_extension_chain(plugin):
+    assert plugin.api().extension(pjrt.RYFT_MI355X_EXTENSION_TYPE) is not None
+    assert plugin.api().extension(4) is None  # no layouts extension: ryft-pjrt reports Unimplemented
+
+
+def test_compile_only_client(compile_client):
+    c = compile_client
+    assert c.platform_name() == "rocm"
+    assert c.process_index() == 0
+    assert c.devices() == []
+
+
+def _plan(client, program):
+    exe = client.compile(pjrt.Program.mlir(program))
+    return exe, [ln.split(":")[1].split()[0] for ln in exe.describe_plan().strip().splitlines()]
+
+
+@pytest.mark.parametrize("name,kw,expect", [
+    ("c1", {}, ["gemm_f32_mfma_64x64"]),
+    ("c2", {}, ["gemm_bf16_mfma_256x256"]),
+    ("c3", {}, ["gemm_i8_mfma_256x256"]),
+    ("c4", {}, ["attention_fwd"]),
+    ("c5", {}, ["reduce", "elementwise", "gemm_fp8_mfma_dual_128x128", "gemm_fp8_mfma_64x128"]),
+])
+def test_full_size_plans(compile_client, name, kw, expect):
+    w = configs.CONFIGS[name](**kw)
+    exe, kernels = _plan(compile_client, w.program)
+    assert kernels == expect
+    e = exe.executable()
+    assert e.name() == "main"
+    assert e.replica_count() == 1 and e.computation_count() == 1
+    cost = e.cost_analysis()
+    assert cost["flops"] == pytest.approx(w.flops, rel=1e-3)
+
+
+def test_int8_epilogue_writes_both_outputs(compile_client):
+    w = configs.c3_int8_gemm()
+    exe = compile_client.compile(pjrt.Program.mlir(w.program))
+    e = exe.executable()
+    assert e.output_element_types() == [pjrt.BufferType.S32, pjrt.BufferType.F32]
+    assert e.output_dimensions() == [[4096, 4096], [4096, 4096]]
+    plan = exe.describe_plan()
+    assert "epilogue=1" in plan and len(plan.strip().splitlines()) == 1
+
+
+# Printer goldens of ryft-mlir, which fix the text the front-end must accept.
+GOLDENS = {
+    # crates/ryft-mlir/src/dialects/stable_hlo/operations/linear_algebra.rs:2240-2263 (joined lines)
+    "dot_general_algorithm": """module {
+  func.func @main(%arg0: tensor<2x2x2xi64>, %arg1: tensor<2x2x2xi64>) -> tensor<2x2x2xi64> {
+    %0 = stablehlo.dot_general %arg0, %arg1, batching_dims = [0] x [0], contracting_dims = [2] x [1], algorithm = <lhs_precision_type = f8E5M2, rhs_precision_type = f8E5M2, accumulation_type = f32, lhs_component_count = 1, rhs_component_count = 1, num_primitive_operations = 1, allow_imprecise_accumulation = true> : (tensor<2x2x2xi64>, tensor<2x2x2xi64>) -> tensor<2x2x2xi64>
+    return %0 : tensor<2x2x2xi64>
+  }
+}""",
+    # functional.rs:529-541
+    "reduce": """module {
+  func.func @main(%arg0: tensor<3x4xi32>, %arg1: tensor<i32>) -> tensor<3xi32> {
+    %0 = stablehlo.reduce(%arg0 init: %arg1) applies stablehlo.add across dimensions = [1] : (tensor<3x4xi32>, tensor<i32>) -> tensor<3xi32>
+    return %0 : tensor<3xi32>
+  }
+}""",
+    # manipulation.rs:2022
+    "transpose": """module {
+  func.func @main(%arg0: tensor<3x4x5xi32>) -> tensor<5x3x4xi32> {
+    %0 = stablehlo.transpose %arg0, dims = [2, 0, 1] : (tensor<3x4x5xi32>) -> tensor<5x3x4xi32>
+    return %0 : tensor<5x3x4xi32>
+  }
+}""",
+    # manipulation.rs:2154
+    "broadcast_in_dim": """module {
+  func.func @main(%arg0: tensor<1x3xi32>) -> tensor<2x3x2xi32> {
+    %0 = stablehlo.broadcast_in_dim %arg0, dims = [2, 1] : (tensor<1x3xi32>) -> tensor<2x3x2xi32>
+    return %0 : tensor<2x3x2xi32>
+  }
+}""",
+    # control_flow.rs:596
+    "select": """module {
+  func.func @main(%arg0: tensor<3x4xi1>, %arg1: tensor<3x4xi32>, %arg2: tensor<3x4xi32>) -> tensor<3x4xi32> {
+    %0 = stablehlo.select %arg0, %arg1, %arg2 : tensor<3x4xi1>, tensor<3x4xi32>
+    return %0 : tensor<3x4xi32>
+  }
+}""",
+    # miscellaneous.rs:1181
+    "iota": """module {
+  func.func @main() -> tensor<4x5xi32> {
+    %0 = stablehlo.iota dim = 1 : tensor<4x5xi32>
+    return %0 : tensor<4x5xi32>
+  }
+}""",
+    # comparison.rs:500
+    "compare": """module {
+  func.func @main(%arg0: tensor<3xf32>, %arg1: tensor<3xf32>) -> tensor<3xi1> {
+    %0 = stablehlo.compare GE, %arg0, %arg1, TOTALORDER : (tensor<3xf32>, tensor<3xf32>) -> tensor<3xi1>
+    return %0 : tensor<3xi1>
+  }
+}""",
+    # README.md example (programs.rs test program shape) with the reduce region form and generic syntax
+    "generic_forms": """module @jit_f attributes {mhlo.num_partitions = 1 : i32} {
+  func.func public @main(%arg0: tensor<4x8xf32> {mhlo.sharding = "{replicated}"}) -> (tensor<4xf32> {jax.result_info = ""}) {
+    %cst = stablehlo.constant dense<0xFF800000> : tensor<f32>
+    %0 = stablehlo.reduce(%arg0 init: %cst) across dimensions = [1] : (tensor<4x8xf32>, tensor<f32>) -> tensor<4xf32>
+     reducer(%arg1: tensor<f32>, %arg2: tensor<f32>)  {
+      %2 = stablehlo.maximum %arg1, %arg2 : tensor<f32>
+      stablehlo.return %2 : tensor<f32>
+    }
+    %1 = "stablehlo.exponential"(%0) : (tensor<4xf32>) -> tensor<4xf32>
+    return %1 : tensor<4xf32>
+  }
+}""",
+}
+
+
+@pytest.mark.parametrize("name", sorted(GOLDENS))
+def test_printer_golden_forms_compile(compile_client, name):
+    exe = compile_client.compile(pjrt.Program.mlir(GOLDENS[name]))
+    assert exe.executable().output_count() == 1
+
+
+def test_bytecode_is_rejected_clearly(compile_client):
+    with pytest.raises(pjrt.PjrtError) as e:
+        compile_client.compile(pjrt.Program.mlir(b"ML\xefR\x00\x05rest-of-bytecode"))
+    assert e.value.code == pjrt.ErrorCode.UNIMPLEMENTED
+    assert "bytecode" in e.value.message
+
+
+def test_hlo_format_is_rejected(compile_client):
+    with pytest.raises(pjrt.PjrtError) as e:
+        compile_client.compile(pjrt.Program(b"HloModule m", "hlo"))
+    assert e.value.code == pjrt.ErrorCode.UNIMPLEMENTED
+
+
+def test_parse_errors_are_invalid_argument(compile_client):
+    bad = GOLDENS["transpose"].replace("dims = [2, 0, 1]", "dims = [2, 0")
+    with pytest.raises(pjrt.PjrtError) as e:
+        compile_client.compile(pjrt.Program.mlir(bad))
+    assert e.value.code == pjrt.ErrorCode.INVALID_ARGUMENT
+
+
+def test_unsupported_op_is_unimplemented(compile_client):
+    prog = GOLDENS["transpose"].replace("stablehlo.transpose %arg0, dims = [2, 0, 1]", "stablehlo.fft %arg0")
+    with pytest.raises(pjrt.PjrtError) as e:
+        compile_client.compile(pjrt.Program.mlir(prog))
+    assert e.value.code in (pjrt.ErrorCode.UNIMPLEMENTED, pjrt.ErrorCode.INVALID_ARGUMENT)
+
+
+def test_shape_mismatch_is_invalid_argument(compile_client):
+    prog = GOLDENS["transpose"].replace("-> tensor<5x3x4xi32>\n    return", "-> tensor<5x4x3xi32>\n    return")
+    with pytest.raises(pjrt.PjrtError) as e:
+        compile_client.compile(pjrt.Program.mlir(prog))
+    assert e.value.code == pjrt.ErrorCode.INVALID_ARGUMENT
+
+
+def test_compile_options_round_trip(compile_client):
+    opts = pjrt.CompilationOptions(matrix_unit_operand_precision=0)
+    exe = compile_client.compile(pjrt.Program.mlir(GOLDENS["iota"]), opts)
+    assert exe.executable().compile_options() == opts.encode()
+    assert len(exe.executable().fingerprint()) == 16
+
+
+def test_attention_not_fused_when_intermediate_escapes(compile_client):
+    # returning the probabilities as well forces the unfused path (the [S,S] matrix is a program result)
+    w = configs.c4_causal_attention(b=1, h=1, s=128, d=64)
+    prog = w.program.replace("return %18 : ", "return %18, %15 : ").replace(
+        "-> tensor<1x1x128x64xbf16> {", "-> (tensor<1x1x128x64xbf16>, tensor<1x1x128x128xf32>) {").replace(
+        "return %18, %15 : tensor<1x1x128x64xbf16>", "return %18, %15 : tensor<1x1x128x64xbf16>, tensor<1x1x128x128xf32>")
+    exe, kernels = _plan(compile_client, prog)
+    assert "attention_fwd" not in kernels
+    assert exe.executable().output_count() == 2
