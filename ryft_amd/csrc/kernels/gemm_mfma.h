@@ -268,6 +268,16 @@ __device__ __forceinline__ void store_row16(void* out, int64_t lin, int dtype, c
   }
 }
 
+// Bits of accumulator element r (f32 → its bit pattern, i32 → itself).
+__device__ __forceinline__ uint32_t acc_elem_bits(const f32x16_t& v, int r) {
+  float x = v[r];
+  return __float_as_uint(x);
+}
+__device__ __forceinline__ uint32_t acc_elem_bits(const i32x16_t& v, int r) {
+  int x = v[r];
+  return (uint32_t)x;
+}
+
 template <int I> using int_c = std::integral_constant<int, I>;
 template <int I, int N, typename F>
 __device__ __forceinline__ void static_for(F&& f) {
@@ -431,8 +441,10 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_mfma_kernel(const GemmArgs 
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = il * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        patch[row * PITCH + j * 32 + (lane & 31)] = __builtin_bit_cast(uint32_t, acc[i][j][r]);
-        if constexpr (DUAL) patch[REGION + row * PITCH + j * 32 + (lane & 31)] = __builtin_bit_cast(uint32_t, acc2[i][j][r]);
+        // (element reads through the vector subscript, then a value conversion: a bit-cast of the subscript
+        //  expression was lowered to element 0 for every r)
+        patch[row * PITCH + j * 32 + (lane & 31)] = acc_elem_bits(acc[i][j], r);
+        if constexpr (DUAL) patch[REGION + row * PITCH + j * 32 + (lane & 31)] = acc_elem_bits(acc2[i][j], r);
       }
     });
     __syncthreads();

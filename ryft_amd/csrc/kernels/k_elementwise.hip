@@ -72,8 +72,17 @@ __global__ void __launch_bounds__(256) reduce_kernel(const ReduceArgs A) {
   const int wave = threadIdx.x >> 6;
   const bool fl = A.is_float != 0;
   const uint32_t init = A.init_ptr ? load_bits(A.init_ptr, 0, A.init_dtype) : (uint32_t)A.init.i;
+  // lanes start from the body's identity; the init value enters once, after the cross-lane combine
+  uint32_t ident;
+  switch (A.kind) {
+    case RED_ADD: case RED_OR: ident = 0u; break;
+    case RED_MUL: ident = fl ? __float_as_uint(1.0f) : 1u; break;
+    case RED_MAX: ident = fl ? 0xff800000u : 0x80000000u; break;
+    case RED_MIN: ident = fl ? 0x7f800000u : 0x7fffffffu; break;
+    default: ident = 0xffffffffu; break;  // RED_AND
+  }
   for (int64_t o = (int64_t)blockIdx.x * 4 + wave; o < A.outer; o += (int64_t)gridDim.x * 4) {
-    uint32_t acc = init;
+    uint32_t acc = ident;
     for (int64_t r = lane; r < A.inner; r += 64) {
       int64_t lin = o * A.inner + r;
       int32_t coord[EW_MAX_RANK];
@@ -86,7 +95,7 @@ __global__ void __launch_bounds__(256) reduce_kernel(const ReduceArgs A) {
       uint32_t other = (uint32_t)__shfl_xor((int)acc, off, 64);
       acc = red_combine(acc, other, A.kind, fl);
     }
-    if (lane == 0) store_bits(P.out_ptr[0], o, P.out_dtype[0], acc, fl);
+    if (lane == 0) store_bits(P.out_ptr[0], o, P.out_dtype[0], red_combine(acc, init, A.kind, fl), fl);
   }
 }
 

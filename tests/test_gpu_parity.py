@@ -99,9 +99,9 @@ def test_add_kat(gpu_client):
 
 
 def test_execute_validates_arguments(gpu_client):
-    w = configs.c1_f32_dot(m=64, k=64, n=64)
+    w = configs.c1_f32_dot(m=64, k=32, n=64)
     exe = gpu_client.compile(pjrt.Program.mlir(w.program))
-    a = gpu_client.buffer(w.inputs[0].data, w.inputs[0].type, w.inputs[0].dims)
+    a = gpu_client.buffer(w.inputs[0].data, w.inputs[0].type, w.inputs[0].dims)  # [64, 32]; the rhs is [32, 64]
     with pytest.raises(pjrt.PjrtError) as e:
         exe.execute([[a]])
     assert e.value.code == pjrt.ErrorCode.INVALID_ARGUMENT
