@@ -124,7 +124,9 @@ struct TileLoader {
         int row = v / (BK / VE), kv = v % (BK / VE);
         regs[i] = *(const uint4*)(base + ((int64_t)row * sr + (int64_t)kv * VE) * ESIZE);
       } else {
-        int rv = v % (R / VE), kb = v / (R / VE);
+        // consecutive lanes take consecutive k-blocks of one row group: their transposed LDS stores then land in
+        // distinct banks (lanes 8 rows apart would share banks), and each global row is still read in 128-byte runs
+        int kb = v % (BK / KP), rv = v / (BK / KP);
 #pragma unroll
         for (int q = 0; q < KP; ++q)
           regs[i * KP + q] = *(const uint4*)(base + ((int64_t)(kb * KP + q) * sk + (int64_t)rv * VE) * ESIZE);
@@ -142,7 +144,9 @@ struct TileLoader {
         int row = v / (BK / VE), kv = v % (BK / VE);
         *(uint4*)(lds + row * LDK + kv * 16) = regs[i];
       } else {
-        int rv = v % (R / VE), kb = v / (R / VE);
+        // consecutive lanes take consecutive k-blocks of one row group: their transposed LDS stores then land in
+        // distinct banks (lanes 8 rows apart would share banks), and each global row is still read in 128-byte runs
+        int kb = v % (BK / KP), rv = v / (BK / KP);
 #define IN(q) regs[i * KP + (q)]
         if (ESIZE == 2) {
           // 8 k-rows × 8 elements → 8 rows (one per element) of 8 consecutive k

@@ -96,7 +96,7 @@ __global__ void __launch_bounds__(256) attention_fwd_kernel(const AttnArgs A) {
       kreg[i] = *(const uint4*)(Kg + ((int64_t)(k0 + row) * A.ks[2] + c * 8) * 2);
     }
     if (tid < VBLK) {
-      int dv = tid % (D / 8), kb = tid / (D / 8);
+      int kb = tid % (BKV / 8), dv = tid / (BKV / 8);  // lanes spread over k-blocks: conflict-free LDS stores
 #pragma unroll
       for (int q = 0; q < 8; ++q) vreg[q] = *(const uint4*)(Vg + ((int64_t)(k0 + kb * 8 + q) * A.vs[2] + dv * 8) * 2);
     }
@@ -111,7 +111,7 @@ __global__ void __launch_bounds__(256) attention_fwd_kernel(const AttnArgs A) {
       *(uint4*)(sK + row * C::KP + c * 16) = kreg[i];
     }
     if (tid < VBLK) {
-      int dv = tid % (D / 8), kb = tid / (D / 8);
+      int kb = tid % (BKV / 8), dv = tid / (BKV / 8);  // lanes spread over k-blocks: conflict-free LDS stores
       uint32_t w[8][4];
 #pragma unroll
       for (int q = 0; q < 8; ++q) { w[q][0] = vreg[q].x; w[q][1] = vreg[q].y; w[q][2] = vreg[q].z; w[q][3] = vreg[q].w; }
