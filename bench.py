@@ -39,6 +39,7 @@ def _cpu_baseline(name, seconds):
         "c3": (configs.c3_int8_gemm, {"m": 512}, "512 of the 4096 rows of C3"),
         "c4": (configs.c4_causal_attention, {"b": 1, "h": 2}, "2 of the 128 heads of C4"),
         "c5": (configs.c5_swiglu_fp8, {"m": 64}, "64 of the 512 tokens of C5"),
+        "copy": (configs.hbm_copy_f32, {}, "the full copy calibration vector"),
     }
     fn, kw, desc = samples[name]
     w = fn(**kw)
@@ -52,6 +53,9 @@ def _cpu_baseline(name, seconds):
         if el >= seconds or reps >= 1000:
             break
     cores = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    if not w.flops:
+        return {"value": w.bytes * reps / el / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
+                "sample": f"{desc}, {reps} evaluation(s) in {el:.1f} s (numpy oracle)"}
     return {"value": w.flops * reps / el / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
             "sample": f"{desc}, {reps} evaluation(s) in {el:.1f} s (numpy oracle, f32 dots)"}
 
@@ -61,7 +65,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "copy"],
+                    help="c1..c5: the BASELINE configs (c2 is the headline); copy: the HBM calibration kernel")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -130,11 +135,14 @@ def main():
                 "kernel_avg_us": round(dom["avg_us"], 2), "work_per_launch": dom["flops"] if mfma else dom["bytes"]}
 
     cpu = None if args.no_cpu_baseline else _cpu_baseline(args.config, args.cpu_seconds)
-    value = w.flops / (ms_per_step * 1e-3) / 1e12
+    if w.flops:
+        value, vunit = w.flops / (ms_per_step * 1e-3) / 1e12, "TFLOP/s"
+    else:  # the copy calibration workload is priced in bytes
+        value, vunit = w.bytes / (ms_per_step * 1e-3) / 1e9, "GB/s"
     dtype = {"f32": "f32", "bf16": "bf16", "int8": "int8", "fp8": "fp8"}[w.compute_dtype]
     shapes = {x_i: list(x.dims) for x_i, x in enumerate(w.inputs)}
     line = {
-        "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "metric": METRIC, "value": round(value, 2), "unit": vunit, "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": dtype,
         "data": "synthetic (seeded splitmix64 inputs with the BASELINE.json distributions)",

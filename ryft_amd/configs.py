@@ -267,10 +267,28 @@ def c5_swiglu_fp8(m=512, d=4096, f=14336, seed=0xC5, activations="fp8") -> Workl
                     compute_dtype="fp8" if activations == "fp8" else "bf16", tolerance=3e-2)
 
 
+def hbm_copy_f32(n=64 * 1024 * 1024, seed=0xCC) -> Workload:
+    """Calibration workload, not a BASELINE config: negate an f32 vector of n elements (n·4 bytes read, n·4 bytes
+    written, nothing re-read). Profiling its one elementwise kernel with the FETCH_SIZE / WRITE_SIZE counters gives
+    the factor that turns those counters into bytes."""
+    t = _t((n,), "f32")
+    prog = f"""module {{
+  func.func @main(%arg0: {t}) -> {t} {{
+    %0 = stablehlo.negate %arg0 : {t}
+    return %0 : {t}
+  }}
+}}
+"""
+    x = hd.uniform(seed * 16, (n,), -1.0, 1.0)
+    return Workload("hbm_copy_f32", prog, [HostInput(x, BufferType.F32, (n,))], flops=0.0, bytes=8.0 * n,
+                    compute_dtype="f32", tolerance=0.0)
+
+
 CONFIGS: Dict[str, Callable[..., Workload]] = {
     "c1": c1_f32_dot,
     "c2": c2_bf16_batched_dot,
     "c3": c3_int8_gemm,
     "c4": c4_causal_attention,
     "c5": c5_swiglu_fp8,
+    "copy": hbm_copy_f32,
 }

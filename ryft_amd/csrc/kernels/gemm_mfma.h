@@ -34,6 +34,9 @@ typedef float f32x16_t __attribute__((__vector_size__(16 * sizeof(float))));
 typedef int i32x16_t __attribute__((__vector_size__(16 * sizeof(int))));
 typedef int i32x4_t __attribute__((__vector_size__(4 * sizeof(int))));
 typedef int i32x8_t __attribute__((__vector_size__(8 * sizeof(int))));
+// 16-byte register vector. A native vector type rather than HIP's uint4 struct: copies of the struct lower to
+// memcpy, which keeps register arrays of it (prefetched tiles, fragments) in private memory.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // ------------------------------------------------------------------------------------------------ MFMA GEMM
 enum MmaKind { MMA_BF16 = 0, MMA_F16 = 1, MMA_I8 = 2, MMA_FP8 = 3, MMA_F32 = 4 };
@@ -43,7 +46,7 @@ template <> struct Mma<MMA_BF16> {
   static constexpr int ESIZE = 2, KPACK = 8;
   using Acc = f32x16_t;
   static constexpr bool INT = false;
-  __device__ static Acc mma(const uint4& a, const uint4& b, Acc c) {
+  __device__ static Acc mma(const u32x4& a, const u32x4& b, Acc c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
   }
 };
@@ -51,7 +54,7 @@ template <> struct Mma<MMA_F16> {
   static constexpr int ESIZE = 2, KPACK = 8;
   using Acc = f32x16_t;
   static constexpr bool INT = false;
-  __device__ static Acc mma(const uint4& a, const uint4& b, Acc c) {
+  __device__ static Acc mma(const u32x4& a, const u32x4& b, Acc c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
   }
 };
@@ -59,11 +62,11 @@ template <> struct Mma<MMA_I8> {
   static constexpr int ESIZE = 1, KPACK = 16;
   using Acc = i32x16_t;
   static constexpr bool INT = true;
-  __device__ static Acc mma(const uint4& a, const uint4& b, Acc c) {
+  __device__ static Acc mma(const u32x4& a, const u32x4& b, Acc c) {
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4_t, a), __builtin_bit_cast(i32x4_t, b), c, 0, 0, 0);
   }
 };
-struct U8x32 { uint4 lo, hi; };
+struct U8x32 { u32x4 lo, hi; };
 template <> struct Mma<MMA_FP8> {
   static constexpr int ESIZE = 1, KPACK = 32;
   using Acc = f32x16_t;
@@ -89,12 +92,12 @@ template <> struct Frag<4> {
   __device__ static T load(const char* p) { return *(const float*)p; }
 };
 template <> struct Frag<16> {
-  using T = uint4;
-  __device__ static T load(const char* p) { return *(const uint4*)p; }
+  using T = u32x4;
+  __device__ static T load(const char* p) { return *(const u32x4*)p; }
 };
 template <> struct Frag<32> {
   using T = U8x32;
-  __device__ static T load(const char* p) { return U8x32{*(const uint4*)p, *(const uint4*)(p + 16)}; }
+  __device__ static T load(const char* p) { return U8x32{*(const u32x4*)p, *(const u32x4*)(p + 16)}; }
 };
 
 // v_perm_b32 helper: result bytes picked from {lo: bytes 0-3, hi: bytes 4-7} by `sel`.
@@ -112,7 +115,7 @@ struct TileLoader {
   static constexpr bool PARTIAL = (NTOT % THREADS) != 0;  // some threads idle on the last round
   static constexpr int NREG = RCONTIG ? NVEC * KP : NVEC;
   static_assert(!PARTIAL || NVEC == 1, "uneven tile split");
-  uint4 regs[NREG];
+  u32x4 regs[NREG];
 
   // base: element pointer of (row 0, k 0) of this tile; sr / sk: element strides
   __device__ __forceinline__ void load(const char* base, int64_t sr, int64_t sk, int tid) {
@@ -122,14 +125,14 @@ struct TileLoader {
       if (PARTIAL && v >= NTOT) break;
       if (!RCONTIG) {
         int row = v / (BK / VE), kv = v % (BK / VE);
-        regs[i] = *(const uint4*)(base + ((int64_t)row * sr + (int64_t)kv * VE) * ESIZE);
+        regs[i] = *(const u32x4*)(base + ((int64_t)row * sr + (int64_t)kv * VE) * ESIZE);
       } else {
         // consecutive lanes take consecutive k-blocks of one row group: their transposed LDS stores then land in
         // distinct banks (lanes 8 rows apart would share banks), and each global row is still read in 128-byte runs
         int kb = v % (BK / KP), rv = v / (BK / KP);
 #pragma unroll
         for (int q = 0; q < KP; ++q)
-          regs[i * KP + q] = *(const uint4*)(base + ((int64_t)(kb * KP + q) * sk + (int64_t)rv * VE) * ESIZE);
+          regs[i * KP + q] = *(const u32x4*)(base + ((int64_t)(kb * KP + q) * sk + (int64_t)rv * VE) * ESIZE);
       }
     }
   }
@@ -142,7 +145,7 @@ struct TileLoader {
       if (PARTIAL && v >= NTOT) break;
       if (!RCONTIG) {
         int row = v / (BK / VE), kv = v % (BK / VE);
-        *(uint4*)(lds + row * LDK + kv * 16) = regs[i];
+        *(u32x4*)(lds + row * LDK + kv * 16) = regs[i];
       } else {
         // consecutive lanes take consecutive k-blocks of one row group: their transposed LDS stores then land in
         // distinct banks (lanes 8 rows apart would share banks), and each global row is still read in 128-byte runs
@@ -155,13 +158,13 @@ struct TileLoader {
           for (int q = 0; q < 8; ++q) { w[q][0] = IN(q).x; w[q][1] = IN(q).y; w[q][2] = IN(q).z; w[q][3] = IN(q).w; }
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
-            uint4 lo, hi;
+            u32x4 lo, hi;
             lo.x = perm(w[1][t], w[0][t], 0x05040100u); hi.x = perm(w[1][t], w[0][t], 0x07060302u);
             lo.y = perm(w[3][t], w[2][t], 0x05040100u); hi.y = perm(w[3][t], w[2][t], 0x07060302u);
             lo.z = perm(w[5][t], w[4][t], 0x05040100u); hi.z = perm(w[5][t], w[4][t], 0x07060302u);
             lo.w = perm(w[7][t], w[6][t], 0x05040100u); hi.w = perm(w[7][t], w[6][t], 0x07060302u);
-            *(uint4*)(lds + (rv * VE + 2 * t) * LDK + kb * 16) = lo;
-            *(uint4*)(lds + (rv * VE + 2 * t + 1) * LDK + kb * 16) = hi;
+            *(u32x4*)(lds + (rv * VE + 2 * t) * LDK + kb * 16) = lo;
+            *(u32x4*)(lds + (rv * VE + 2 * t + 1) * LDK + kb * 16) = hi;
           }
         } else if (ESIZE == 1) {
           // 4 k-rows × 16 bytes → 16 rows of 4 consecutive k
@@ -215,7 +218,7 @@ struct MfmaCfg {
 __device__ __forceinline__ void store_row16(void* out, int64_t lin, int dtype, const uint32_t* v, bool is_float) {
   switch (dtype) {
     case DT_F32: case DT_S32: case DT_U32: {
-      uint4* p = (uint4*)((char*)out + lin * 4);
+      u32x4* p = (u32x4*)((char*)out + lin * 4);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         uint32_t w[4];
@@ -224,7 +227,7 @@ __device__ __forceinline__ void store_row16(void* out, int64_t lin, int dtype, c
           uint32_t x = v[4 * q + e];
           w[e] = (dtype == DT_F32) ? (is_float ? x : __float_as_uint((float)(int32_t)x)) : x;
         }
-        p[q] = uint4{w[0], w[1], w[2], w[3]};
+        p[q] = u32x4{w[0], w[1], w[2], w[3]};
       }
       break;
     }
@@ -241,9 +244,9 @@ __device__ __forceinline__ void store_row16(void* out, int64_t lin, int dtype, c
           w[e] = (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hc) << 16);
         }
       }
-      uint4* p = (uint4*)((char*)out + lin * 2);
-      p[0] = uint4{w[0], w[1], w[2], w[3]};
-      p[1] = uint4{w[4], w[5], w[6], w[7]};
+      u32x4* p = (u32x4*)((char*)out + lin * 2);
+      p[0] = u32x4{w[0], w[1], w[2], w[3]};
+      p[1] = u32x4{w[4], w[5], w[6], w[7]};
       break;
     }
     case DT_F8E4M3FN: case DT_F8E5M2: case DT_S8: case DT_U8: {
@@ -262,7 +265,7 @@ __device__ __forceinline__ void store_row16(void* out, int64_t lin, int dtype, c
         }
         w[q] = x;
       }
-      *(uint4*)((char*)out + lin) = uint4{w[0], w[1], w[2], w[3]};
+      *(u32x4*)((char*)out + lin) = u32x4{w[0], w[1], w[2], w[3]};
       break;
     }
     default:

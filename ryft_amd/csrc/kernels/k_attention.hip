@@ -20,6 +20,8 @@ namespace ryft {
 
 typedef __bf16 bf16x8_a __attribute__((__vector_size__(8 * sizeof(__bf16))));
 typedef float f32x16_a __attribute__((__vector_size__(16 * sizeof(float))));
+// native 16-byte vector (HIP's uint4 struct copies become memcpys that pin register arrays in private memory)
+typedef uint32_t u32x4a __attribute__((ext_vector_type(4)));
 
 bool attention_supported(int head_dim) { return head_dim == 64 || head_dim == 128; }
 
@@ -28,7 +30,7 @@ namespace {
 constexpr int BQ = 128;  // queries per workgroup
 constexpr int BKV = 64;  // keys per block
 
-__device__ __forceinline__ f32x16_a mma_bf16(const uint4& a, const uint4& b, f32x16_a c) {
+__device__ __forceinline__ f32x16_a mma_bf16(const u32x4a& a, const u32x4a& b, f32x16_a c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_a, a), __builtin_bit_cast(bf16x8_a, b), c, 0, 0, 0);
 }
 
@@ -64,10 +66,10 @@ __global__ void __launch_bounds__(256) attention_fwd_kernel(const AttnArgs A) {
 
   // Q fragments (B operand of Sᵀ = K·Qᵀ): lane holds Q[q][s·16 + 8·(lane/32) .. +8] for its query q
   const int myq = q0 + wave * 32 + (lane & 31);
-  uint4 qf[D / 16];
+  u32x4a qf[D / 16];
 #pragma unroll
   for (int s = 0; s < D / 16; ++s)
-    qf[s] = *(const uint4*)(Qg + (int64_t)myq * A.qs[2] + s * 16 + 8 * (lane >> 5));
+    qf[s] = *(const u32x4a*)(Qg + (int64_t)myq * A.qs[2] + s * 16 + 8 * (lane >> 5));
 
   const float sl2 = A.scale * 1.4426950408889634f;  // logits in the log2 domain
   float m_run = -INFINITY, l_run = 0.f;
@@ -85,20 +87,20 @@ __global__ void __launch_bounds__(256) attention_fwd_kernel(const AttnArgs A) {
   // K block: 64 keys × D → 4·(D/128)... vectors of 16 B per thread; Vᵀ block: 8×8 transposes by threads < 8·D/8
   constexpr int KVEC = BKV * D / 8 / 256;  // 16-byte vectors of K per thread
   constexpr int VBLK = (BKV / 8) * (D / 8); // 8×8 blocks of V
-  uint4 kreg[KVEC];
-  uint4 vreg[8];
+  u32x4a kreg[KVEC];
+  u32x4a vreg[8];
   auto gload = [&](int j) {
     const int k0 = j * BKV;
 #pragma unroll
     for (int i = 0; i < KVEC; ++i) {
       int v = tid + i * 256;
       int row = v / (D / 8), c = v % (D / 8);
-      kreg[i] = *(const uint4*)(Kg + ((int64_t)(k0 + row) * A.ks[2] + c * 8) * 2);
+      kreg[i] = *(const u32x4a*)(Kg + ((int64_t)(k0 + row) * A.ks[2] + c * 8) * 2);
     }
     if (tid < VBLK) {
       int kb = tid % (BKV / 8), dv = tid / (BKV / 8);  // lanes spread over k-blocks: conflict-free LDS stores
 #pragma unroll
-      for (int q = 0; q < 8; ++q) vreg[q] = *(const uint4*)(Vg + ((int64_t)(k0 + kb * 8 + q) * A.vs[2] + dv * 8) * 2);
+      for (int q = 0; q < 8; ++q) vreg[q] = *(const u32x4a*)(Vg + ((int64_t)(k0 + kb * 8 + q) * A.vs[2] + dv * 8) * 2);
     }
   };
   auto lstore = [&](int buf) {
@@ -108,7 +110,7 @@ __global__ void __launch_bounds__(256) attention_fwd_kernel(const AttnArgs A) {
     for (int i = 0; i < KVEC; ++i) {
       int v = tid + i * 256;
       int row = v / (D / 8), c = v % (D / 8);
-      *(uint4*)(sK + row * C::KP + c * 16) = kreg[i];
+      *(u32x4a*)(sK + row * C::KP + c * 16) = kreg[i];
     }
     if (tid < VBLK) {
       int kb = tid % (BKV / 8), dv = tid / (BKV / 8);  // lanes spread over k-blocks: conflict-free LDS stores
@@ -117,13 +119,13 @@ __global__ void __launch_bounds__(256) attention_fwd_kernel(const AttnArgs A) {
       for (int q = 0; q < 8; ++q) { w[q][0] = vreg[q].x; w[q][1] = vreg[q].y; w[q][2] = vreg[q].z; w[q][3] = vreg[q].w; }
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        uint4 lo, hi;
+        u32x4a lo, hi;
         lo.x = __builtin_amdgcn_perm(w[1][t], w[0][t], 0x05040100u); hi.x = __builtin_amdgcn_perm(w[1][t], w[0][t], 0x07060302u);
         lo.y = __builtin_amdgcn_perm(w[3][t], w[2][t], 0x05040100u); hi.y = __builtin_amdgcn_perm(w[3][t], w[2][t], 0x07060302u);
         lo.z = __builtin_amdgcn_perm(w[5][t], w[4][t], 0x05040100u); hi.z = __builtin_amdgcn_perm(w[5][t], w[4][t], 0x07060302u);
         lo.w = __builtin_amdgcn_perm(w[7][t], w[6][t], 0x05040100u); hi.w = __builtin_amdgcn_perm(w[7][t], w[6][t], 0x07060302u);
-        *(uint4*)(sV + (dv * 8 + 2 * t) * C::VP + kb * 16) = lo;
-        *(uint4*)(sV + (dv * 8 + 2 * t + 1) * C::VP + kb * 16) = hi;
+        *(u32x4a*)(sV + (dv * 8 + 2 * t) * C::VP + kb * 16) = lo;
+        *(u32x4a*)(sV + (dv * 8 + 2 * t + 1) * C::VP + kb * 16) = hi;
       }
     }
   };
@@ -145,7 +147,7 @@ __global__ void __launch_bounds__(256) attention_fwd_kernel(const AttnArgs A) {
     for (int s = 0; s < D / 16; ++s) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        uint4 kf = *(const uint4*)(sK + (t * 32 + (lane & 31)) * C::KP + (s * 16 + 8 * half) * 2);
+        u32x4a kf = *(const u32x4a*)(sK + (t * 32 + (lane & 31)) * C::KP + (s * 16 + 8 * half) * 2);
         st[t] = mma_bf16(kf, qf[s], st[t]);
       }
     }
@@ -176,7 +178,7 @@ __global__ void __launch_bounds__(256) attention_fwd_kernel(const AttnArgs A) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
     // P = 2^(s - m), rounded to bf16 as the B operand of Oᵀ = Vᵀ·Pᵀ
-    uint4 pf[4];
+    u32x4a pf[4];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       float p[16];
@@ -186,8 +188,8 @@ __global__ void __launch_bounds__(256) attention_fwd_kernel(const AttnArgs A) {
         l_run += p[r];
       }
       // P enters the bf16 MFMA rounded to bf16 whether the program rounds it (p_dtype bf16) or keeps it in f32
-      pf[2 * t] = uint4{pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3]), pack_bf16(p[4], p[5]), pack_bf16(p[6], p[7])};
-      pf[2 * t + 1] = uint4{pack_bf16(p[8], p[9]), pack_bf16(p[10], p[11]), pack_bf16(p[12], p[13]), pack_bf16(p[14], p[15])};
+      pf[2 * t] = u32x4a{pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3]), pack_bf16(p[4], p[5]), pack_bf16(p[6], p[7])};
+      pf[2 * t + 1] = u32x4a{pack_bf16(p[8], p[9]), pack_bf16(p[10], p[11]), pack_bf16(p[12], p[13]), pack_bf16(p[14], p[15])};
     }
     // Oᵀ[d, q] += Σ_key Vᵀ[d, key] · P[q, key]; k-step s covers keys [16s, 16s+16) in the accumulator's key order:
     // element e of lane l ↔ key 16s + 8·(e/4) + 4·(l/32) + e%4
@@ -198,7 +200,7 @@ __global__ void __launch_bounds__(256) attention_fwd_kernel(const AttnArgs A) {
         const char* row = sV + (dt * 32 + (lane & 31)) * C::VP + (s * 16 + 4 * half) * 2;
         uint2 lo = *(const uint2*)row;
         uint2 hi = *(const uint2*)(row + 16);
-        uint4 vf = uint4{lo.x, lo.y, hi.x, hi.y};
+        u32x4a vf = u32x4a{lo.x, lo.y, hi.x, hi.y};
         o[dt] = mma_bf16(vf, pf[s], o[dt]);
       }
     }
