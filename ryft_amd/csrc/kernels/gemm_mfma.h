@@ -4,8 +4,10 @@
 //
 // MFMA path: one workgroup computes a BM×BN tile of C[b] = A[b]·B[b]ᵀ (B addressed as [n, k]); WM×WN wavefronts
 // each own a (BM/WM)×(BN/WN) sub-tile made of 32×32 MFMA tiles. Operand tiles are staged through LDS in a
-// K-packed layout (each row holds BK consecutive k of one m or n), double-buffered so that the global loads of
-// k-tile t+1 are in flight while the MFMAs of k-tile t run. Operands whose contiguous dimension is m / n (row-major
+// K-packed layout (each row holds BK consecutive k of one m or n) in two LDS stages, fed from two register stages
+// of buffer loads, so that k-tiles t+1 and t+2 are in flight while the MFMAs of k-tile t run; LDS fragments are
+// double-buffered in registers across k-steps and across the one barrier per k-tile. Operands whose contiguous
+// dimension is m / n (row-major
 // [K, N] weights, for example) are transposed in registers with v_perm_b32 on their way into LDS, so no separate
 // transpose pass over HBM is needed. Workgroups are mapped onto the 8 XCDs so that the tiles one XCD computes
 // share A row-panels and B column-panels in that XCD's L2.
@@ -66,16 +68,15 @@ template <> struct Mma<MMA_I8> {
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4_t, a), __builtin_bit_cast(i32x4_t, b), c, 0, 0, 0);
   }
 };
-struct U8x32 { u32x4 lo, hi; };
+typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
 template <> struct Mma<MMA_FP8> {
   static constexpr int ESIZE = 1, KPACK = 32;
   using Acc = f32x16_t;
   static constexpr bool INT = false;
-  __device__ static Acc mma(const U8x32& a, const U8x32& b, Acc c) {
-    i32x8_t av = {(int)a.lo.x, (int)a.lo.y, (int)a.lo.z, (int)a.lo.w, (int)a.hi.x, (int)a.hi.y, (int)a.hi.z, (int)a.hi.w};
-    i32x8_t bv = {(int)b.lo.x, (int)b.lo.y, (int)b.lo.z, (int)b.lo.w, (int)b.hi.x, (int)b.hi.y, (int)b.hi.z, (int)b.hi.w};
+  __device__ static Acc mma(const u32x8& a, const u32x8& b, Acc c) {
     // format 0 = fp8 e4m3 for both operands; zero scale operands select the unscaled instruction
-    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bv, c, 0, 0, 0, 0, 0, 0);
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(__builtin_bit_cast(i32x8_t, a), __builtin_bit_cast(i32x8_t, b),
+                                                           c, 0, 0, 0, 0, 0, 0);
   }
 };
 template <> struct Mma<MMA_F32> {
@@ -96,8 +97,11 @@ template <> struct Frag<16> {
   __device__ static T load(const char* p) { return *(const u32x4*)p; }
 };
 template <> struct Frag<32> {
-  using T = U8x32;
-  __device__ static T load(const char* p) { return U8x32{*(const u32x4*)p, *(const u32x4*)(p + 16)}; }
+  using T = u32x8;
+  __device__ static T load(const char* p) {
+    u32x4 lo = *(const u32x4*)p, hi = *(const u32x4*)(p + 16);
+    return u32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+  }
 };
 
 // v_perm_b32 helper: result bytes picked from {lo: bytes 0-3, hi: bytes 4-7} by `sel`.
@@ -117,22 +121,26 @@ struct TileLoader {
   static_assert(!PARTIAL || NVEC == 1, "uneven tile split");
   u32x4 regs[NREG];
 
-  // base: element pointer of (row 0, k 0) of this tile; sr / sk: element strides
+  // base: element pointer of (row 0, k 0) of this tile; sr / sk: element strides. Loads go through a buffer
+  // resource whose base is this k-tile's origin (scalar registers), so the per-lane byte offsets are loop-invariant
+  // 32-bit values (the host checks that one tile spans less than 2 GiB).
   __device__ __forceinline__ void load(const char* base, int64_t sr, int64_t sk, int tid) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, -1, 0x00020000);
 #pragma unroll
     for (int i = 0; i < NVEC; ++i) {
       int v = tid + i * THREADS;
       if (PARTIAL && v >= NTOT) break;
       if (!RCONTIG) {
         int row = v / (BK / VE), kv = v % (BK / VE);
-        regs[i] = *(const u32x4*)(base + ((int64_t)row * sr + (int64_t)kv * VE) * ESIZE);
+        regs[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(((int64_t)row * sr + (int64_t)kv * VE) * ESIZE), 0, 0);
       } else {
         // consecutive lanes take consecutive k-blocks of one row group: their transposed LDS stores then land in
         // distinct banks (lanes 8 rows apart would share banks), and each global row is still read in 128-byte runs
         int kb = v % (BK / KP), rv = v / (BK / KP);
 #pragma unroll
         for (int q = 0; q < KP; ++q)
-          regs[i * KP + q] = *(const u32x4*)(base + ((int64_t)(kb * KP + q) * sk + (int64_t)rv * VE) * ESIZE);
+          regs[i * KP + q] = __builtin_amdgcn_raw_buffer_load_b128(
+              rs, (int)(((int64_t)(kb * KP + q) * sk + (int64_t)rv * VE) * ESIZE), 0, 0);
       }
     }
   }
@@ -207,73 +215,12 @@ struct MfmaCfg {
   static_assert(BK % MK == 0, "BK must be a multiple of the MFMA K");
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32");
   // epilogue rounds: the largest number of 32-row tile-rows (dividing TM) whose f32 patches fit in the LDS
-  static constexpr int epi_bytes(int rows) { return WM * WN * NB * rows * 32 * (WTN + 1) * 4; }
+  static constexpr int epi_bytes(int rows) { return WM * WN * NB * rows * 32 * (WTN + 4) * 4; }
   static constexpr int EPI_ROWS = (TM % 4 == 0 && epi_bytes(4) <= LDS_BYTES)   ? 4
                                   : (TM % 2 == 0 && epi_bytes(2) <= LDS_BYTES) ? 2
                                                                                : 1;
   static_assert(epi_bytes(EPI_ROWS) <= LDS_BYTES, "LDS too small for the epilogue patches");
 };
-
-// Stores 16 consecutive values of one output row with 16-byte vector stores.
-__device__ __forceinline__ void store_row16(void* out, int64_t lin, int dtype, const uint32_t* v, bool is_float) {
-  switch (dtype) {
-    case DT_F32: case DT_S32: case DT_U32: {
-      u32x4* p = (u32x4*)((char*)out + lin * 4);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        uint32_t w[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          uint32_t x = v[4 * q + e];
-          w[e] = (dtype == DT_F32) ? (is_float ? x : __float_as_uint((float)(int32_t)x)) : x;
-        }
-        p[q] = u32x4{w[0], w[1], w[2], w[3]};
-      }
-      break;
-    }
-    case DT_BF16: case DT_F16: {
-      uint32_t w[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float a = is_float ? __uint_as_float(v[2 * e]) : (float)(int32_t)v[2 * e];
-        float c = is_float ? __uint_as_float(v[2 * e + 1]) : (float)(int32_t)v[2 * e + 1];
-        if (dtype == DT_BF16) {
-          w[e] = (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(c) << 16);
-        } else {
-          _Float16 ha = (_Float16)a, hc = (_Float16)c;
-          w[e] = (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hc) << 16);
-        }
-      }
-      u32x4* p = (u32x4*)((char*)out + lin * 2);
-      p[0] = u32x4{w[0], w[1], w[2], w[3]};
-      p[1] = u32x4{w[4], w[5], w[6], w[7]};
-      break;
-    }
-    case DT_F8E4M3FN: case DT_F8E5M2: case DT_S8: case DT_U8: {
-      uint32_t w[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        uint32_t x = 0;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          uint32_t bits = v[4 * q + e], byte;
-          float f = is_float ? __uint_as_float(bits) : (float)(int32_t)bits;
-          if (dtype == DT_F8E4M3FN) byte = f32_to_e4m3fn_bits(f);
-          else if (dtype == DT_F8E5M2) byte = f32_to_e5m2_bits(f);
-          else byte = is_float ? (uint32_t)f2i_sat(f, dtype) & 0xffu : bits & 0xffu;
-          x |= byte << (8 * e);
-        }
-        w[q] = x;
-      }
-      *(u32x4*)((char*)out + lin) = u32x4{w[0], w[1], w[2], w[3]};
-      break;
-    }
-    default:
-#pragma unroll
-      for (int e = 0; e < 16; ++e) store_bits(out, lin + e, dtype, v[e], is_float);
-      break;
-  }
-}
 
 // Bits of accumulator element r (f32 → its bit pattern, i32 → itself).
 __device__ __forceinline__ uint32_t acc_elem_bits(const f32x16_t& v, int r) {
@@ -294,52 +241,134 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
-// Epilogue of 16 consecutive accumulators of output row m, columns [n, n+16): `seg` points at them in LDS, `seg2`
-// at the second accumulator of a dual GEMM. Handles EPI_STORE / EPI_SCALE / EPI_SWIGLU; programs (EPI_PROGRAM) run
-// on the generic kernel.
-template <bool INT, bool DUAL>
-__device__ __forceinline__ void epilogue_row16(const GemmArgs& G, int b, int m, int n, const uint32_t* seg,
-                                               const uint32_t* seg2) {
-  const int64_t lin = ((int64_t)b * G.M + m) * (int64_t)G.N + n;
-  uint32_t raw[16], v[16];
+// ------------------------------------------------------------------------------------------------ epilogue
+// Output types the MFMA epilogue writes (others run on the generic kernel): f32 / bf16 / f16 / f8e4m3fn for
+// float results, s32 / f32 (and, scaled, bf16 / f16) for integer accumulators.
+template <int DT> constexpr int out_size() { return DT == DT_F32 || DT == DT_S32 ? 4 : (DT == DT_BF16 || DT == DT_F16 ? 2 : 1); }
+
+// Element bits of one value in output type DT; `x` is an f32 bit pattern, or an i32 when !is_float.
+template <int DT>
+__device__ __forceinline__ uint32_t out_bits(uint32_t x, bool is_float) {
+  if constexpr (DT == DT_S32) {
+    return x;
+  } else {
+    const float f = is_float ? __uint_as_float(x) : (float)(int32_t)x;
+    if constexpr (DT == DT_F32) return __float_as_uint(f);
+    else if constexpr (DT == DT_BF16) return f32_to_bf16_bits(f);
+    else if constexpr (DT == DT_F16) return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
+    else return f32_to_e4m3fn_bits(f);
+  }
+}
+
+// One epilogue pass over a wave's staged accumulators: ROWS rows of WTN words at `reg` (and `reg2`, the second
+// accumulator of a dual GEMM), row pitch PITCH words. Each lane takes 16-byte output chunks (16 / size(DT) values)
+// in row order, so consecutive lanes write consecutive bytes of a row. KIND is EPI_STORE / EPI_SCALE /
+// EPI_SWIGLU; the output type and the epilogue kind are compile-time, so each pass is a short loop.
+template <int KIND, int DT, bool INT, int WTN, int PITCH, int ROWS>
+__device__ __forceinline__ void epi_pass(const GemmArgs& G, void* out, int b, int m0, int n0, const uint32_t* reg,
+                                         const uint32_t* reg2, int lane) {
+  constexpr int OS = out_size<DT>();
+  constexpr int VPC = 16 / OS;  // values per chunk
+  constexpr int CPR = WTN / VPC;
+  static_assert(WTN % VPC == 0, "wave tile narrower than a 16-byte chunk");
+  for (int c = lane; c < ROWS * CPR; c += 64) {
+    const int row = c / CPR, col = (c % CPR) * VPC;
+    const int m = m0 + row, n = n0 + col;
+    uint32_t v[VPC];
 #pragma unroll
-  for (int c = 0; c < 16; ++c) raw[c] = seg[c];
+    for (int q = 0; q < VPC / 4; ++q) {
+      const u32x4 w = *(const u32x4*)(reg + row * PITCH + col + 4 * q);
+      v[4 * q] = w.x, v[4 * q + 1] = w.y, v[4 * q + 2] = w.z, v[4 * q + 3] = w.w;
+    }
+    bool is_float = !INT;
+    if constexpr (KIND == EPI_SCALE) {
+      float rs = G.alpha;
+      if (G.row) rs *= G.row[(int64_t)b * G.row_sb + (int64_t)m * G.row_sm];
+      const float* cp = G.col ? G.col + (int64_t)b * G.col_sb + (int64_t)n * G.col_sn : nullptr;
+#pragma unroll
+      for (int e = 0; e < VPC; ++e) {
+        float x = INT ? (float)(int32_t)v[e] : __uint_as_float(v[e]);
+        x *= rs;
+        if (cp) x *= cp[(int64_t)e * G.col_sn];
+        if (G.mid_round) x = round_float(x, G.mid_round);
+        v[e] = __float_as_uint(x);
+      }
+      is_float = true;
+    } else if constexpr (KIND == EPI_SWIGLU) {
+      const float* c1 = G.col ? G.col + (int64_t)b * G.col_sb + (int64_t)n * G.col_sn : nullptr;
+      const float* c2 = G.col2 ? G.col2 + (int64_t)b * G.col2_sb + (int64_t)n * G.col2_sn : nullptr;
+#pragma unroll
+      for (int q = 0; q < VPC / 4; ++q) {
+        const u32x4 w = *(const u32x4*)(reg2 + row * PITCH + col + 4 * q);
+        const uint32_t u4[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+          const int e = 4 * q + e4;
+          float a = __uint_as_float(v[e]);
+          float u = __uint_as_float(u4[e4]);
+          if (c1) a *= c1[(int64_t)e * G.col_sn];
+          if (c2) u *= c2[(int64_t)e * G.col2_sn];
+          float lg = 1.0f / (1.0f + expf(-a));
+          float x = (a * lg) * u;
+          if (G.mid_round) x = round_float(x, G.mid_round);
+          v[e] = __float_as_uint(x);
+        }
+      }
+      is_float = true;
+    }
+    uint32_t w[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if constexpr (OS == 4) {
+        w[q] = out_bits<DT>(v[q], is_float);
+      } else if constexpr (OS == 2) {
+        w[q] = out_bits<DT>(v[2 * q], is_float) | (out_bits<DT>(v[2 * q + 1], is_float) << 16);
+      } else {
+        w[q] = out_bits<DT>(v[4 * q], is_float) | (out_bits<DT>(v[4 * q + 1], is_float) << 8) |
+               (out_bits<DT>(v[4 * q + 2], is_float) << 16) | (out_bits<DT>(v[4 * q + 3], is_float) << 24);
+      }
+    }
+    *(u32x4*)((char*)out + (((int64_t)b * G.M + m) * (int64_t)G.N + n) * OS) = u32x4{w[0], w[1], w[2], w[3]};
+  }
+}
+
+// Output types each epilogue kind supports on the MFMA kernels (`raw`: the raw-accumulator second output).
+__host__ __device__ inline bool mfma_out_supported(int dt, bool int_acc, int epilogue, bool raw) {
+  if (raw) return int_acc ? dt == DT_S32 : (dt == DT_F32 || dt == DT_BF16);
+  if (int_acc && epilogue == EPI_STORE) return dt == DT_S32 || dt == DT_F32;
+  return dt == DT_F32 || dt == DT_BF16 || dt == DT_F16 || (!int_acc && dt == DT_F8E4M3FN);
+}
+
+// Epilogue of one staged round: dispatch (uniform) on the epilogue kind and output type to one compact pass.
+template <bool INT, bool DUAL, int WTN, int PITCH, int ROWS>
+__device__ __forceinline__ void epi_round(const GemmArgs& G, int b, int m0, int n0, const uint32_t* reg,
+                                          const uint32_t* reg2, int lane) {
+#define RYFT_EPI(K, DT, OUT) epi_pass<K, DT, INT, WTN, PITCH, ROWS>(G, OUT, b, m0, n0, reg, reg2, lane)
+  const int dt = G.out_dtype[0];
   if (G.epilogue == EPI_STORE) {
-    store_row16(G.out_ptr[0], lin, G.out_dtype[0], raw, !INT);
-    return;
-  }
-  if (G.epilogue == EPI_SCALE) {
-    float rs = G.alpha;
-    if (G.row) rs *= G.row[(int64_t)b * G.row_sb + (int64_t)m * G.row_sm];
-    const float* col = G.col ? G.col + (int64_t)b * G.col_sb + (int64_t)n * G.col_sn : nullptr;
-#pragma unroll
-    for (int c = 0; c < 16; ++c) {
-      float x = INT ? (float)(int32_t)raw[c] : __uint_as_float(raw[c]);
-      x *= rs;
-      if (col) x *= col[(int64_t)c * G.col_sn];
-      if (G.mid_round) x = round_float(x, G.mid_round);
-      v[c] = __float_as_uint(x);
+    if (INT && dt == DT_S32) RYFT_EPI(EPI_STORE, DT_S32, G.out_ptr[0]);
+    else if (dt == DT_F32) RYFT_EPI(EPI_STORE, DT_F32, G.out_ptr[0]);
+    else if (!INT && dt == DT_BF16) RYFT_EPI(EPI_STORE, DT_BF16, G.out_ptr[0]);
+    else if (!INT && dt == DT_F16) RYFT_EPI(EPI_STORE, DT_F16, G.out_ptr[0]);
+    else if (!INT && dt == DT_F8E4M3FN) RYFT_EPI(EPI_STORE, DT_F8E4M3FN, G.out_ptr[0]);
+  } else if (G.epilogue == EPI_SCALE) {
+    if (dt == DT_F32) RYFT_EPI(EPI_SCALE, DT_F32, G.out_ptr[0]);
+    else if (dt == DT_BF16) RYFT_EPI(EPI_SCALE, DT_BF16, G.out_ptr[0]);
+    else if (dt == DT_F16) RYFT_EPI(EPI_SCALE, DT_F16, G.out_ptr[0]);
+    else if (!INT && dt == DT_F8E4M3FN) RYFT_EPI(EPI_SCALE, DT_F8E4M3FN, G.out_ptr[0]);
+    if (G.raw_out) {
+      const int rt = G.out_dtype[1];
+      if (INT) RYFT_EPI(EPI_STORE, DT_S32, G.out_ptr[1]);
+      else if (rt == DT_F32) RYFT_EPI(EPI_STORE, DT_F32, G.out_ptr[1]);
+      else RYFT_EPI(EPI_STORE, DT_BF16, G.out_ptr[1]);
     }
-    store_row16(G.out_ptr[0], lin, G.out_dtype[0], v, true);
-    if (G.raw_out) store_row16(G.out_ptr[1], lin, G.out_dtype[1], raw, !INT);
-    return;
+  } else if constexpr (DUAL) {
+    if (dt == DT_F32) RYFT_EPI(EPI_SWIGLU, DT_F32, G.out_ptr[0]);
+    else if (dt == DT_BF16) RYFT_EPI(EPI_SWIGLU, DT_BF16, G.out_ptr[0]);
+    else if (dt == DT_F16) RYFT_EPI(EPI_SWIGLU, DT_F16, G.out_ptr[0]);
+    else RYFT_EPI(EPI_SWIGLU, DT_F8E4M3FN, G.out_ptr[0]);
   }
-  if constexpr (DUAL) {  // EPI_SWIGLU
-    const float* c1 = G.col ? G.col + (int64_t)b * G.col_sb + (int64_t)n * G.col_sn : nullptr;
-    const float* c2 = G.col2 ? G.col2 + (int64_t)b * G.col2_sb + (int64_t)n * G.col2_sn : nullptr;
-#pragma unroll
-    for (int c = 0; c < 16; ++c) {
-      float a = __uint_as_float(raw[c]);
-      float u = __uint_as_float(seg2[c]);
-      if (c1) a *= c1[(int64_t)c * G.col_sn];
-      if (c2) u *= c2[(int64_t)c * G.col2_sn];
-      float lg = 1.0f / (1.0f + expf(-a));
-      float x = (a * lg) * u;
-      if (G.mid_round) x = round_float(x, G.mid_round);
-      v[c] = __float_as_uint(x);
-    }
-    store_row16(G.out_ptr[0], lin, G.out_dtype[0], v, true);
-  }
+#undef RYFT_EPI
 }
 
 template <int KIND, int BM, int BN, int BK, int WM, int WN, bool A_R, bool B_R, bool DUAL>
@@ -370,6 +399,8 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_mfma_kernel(const GemmArgs 
   const char* Bb = (const char*)G.B.ptr + ((int64_t)b * G.B.sb + (int64_t)n0 * G.B.sr) * ES;
   const char* B2b = DUAL ? (const char*)G.B2.ptr + ((int64_t)b * G.B2.sb + (int64_t)n0 * G.B2.sr) * ES : nullptr;
 
+  // One register stage of global prefetch: tile kt + 2 is requested at the start of k-tile kt (right after tile
+  // kt + 1 went from registers to LDS), so each load has a whole k-tile of MFMA work to arrive in. Two LDS stages.
   TileLoader<ES, BM, BK, C::THREADS, A_R> la;
   TileLoader<ES, BN, BK, C::THREADS, B_R> lb;
   TileLoader<ES, BN, BK, C::THREADS, B_R> lb2;
@@ -398,45 +429,92 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_mfma_kernel(const GemmArgs 
     if constexpr (DUAL) lb2.template store<C::LDK>(s + (BM + BN) * C::LDK, tid);
   };
 
-  gload(0);
-  lstore(0);
-  __syncthreads();
+  // Fragments of MFMA k-step s live in register slot s & 1: step s + 1 is read from LDS while step s multiplies.
+  constexpr int S = BK / C::MK;
+  static_assert(S % 2 == 0, "k-steps per tile must be even (fragment slots alternate)");
+  typename F::T fa[2][C::TM], fb[2][C::TN], fb2[2][DUAL ? C::TN : 1];
   const int lrow = lane & 31;
   const int lk = (lane >> 5) * C::KPACK * ES;  // byte offset of this lane's k-pack within an MFMA k-step
+  const int a_off = (wm * C::WTM + lrow) * C::LDK + lk;
+  const int b_off = BM * C::LDK + (wn * C::WTN + lrow) * C::LDK + lk;
+  auto lfrag = [&](int buf, auto s, auto slot) {
+    constexpr int SL = decltype(slot)::value;
+    constexpr int ko = decltype(s)::value * C::MK * ES;
+    const char* st = smem + buf * C::STAGE;
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i) fa[SL][i] = F::load(st + a_off + i * 32 * C::LDK + ko);
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j) {
+      fb[SL][j] = F::load(st + b_off + j * 32 * C::LDK + ko);
+      if constexpr (DUAL) fb2[SL][j] = F::load(st + b_off + BN * C::LDK + j * 32 * C::LDK + ko);
+    }
+  };
+
+  // prologue: tile 0 in LDS stage 0, tile 1 in flight in registers
+  gload(0);
+  lstore(0);
+  gload(min(1, KT - 1));
+  __syncthreads();
+  lfrag(0, int_c<0>{}, int_c<0>{});
+
+  // k-tile kt reads LDS stage kt & 1. Per k-step s: the fragments of step s + 1 are requested first and a
+  // scheduling barrier keeps them ahead of the MFMAs of step s (the compiler would otherwise sink each read to just
+  // before its first use and expose the LDS latency). After the MFMAs of step 0, tile kt + 1 goes from registers to
+  // the other stage and tile kt + 2 is requested (past the last tile the last one is re-read: unconditional loads
+  // keep the wait counters exact). The single barrier sits before the MFMAs of the last k-step: by then every wave
+  // holds its last fragments of this stage and has stored tile kt + 1, so the first fragments of tile kt + 1 are read
+  // while the last k-step multiplies; the barrier also orders the reads of this stage before its next overwrite.
+  //
+  // MFMA operands are swapped (B fragment first): each accumulator holds the transposed 32×32 tile, so a lane's
+  // registers are 4 runs of 4 consecutive output columns of one row, which the epilogue writes as 16-byte words.
   for (int kt = 0; kt < KT; ++kt) {
     const int cur = kt & 1;
-    if (kt + 1 < KT) gload(kt + 1);
-    const char* sA = smem + cur * C::STAGE + (wm * C::WTM + lrow) * C::LDK + lk;
-    const char* sB = smem + cur * C::STAGE + BM * C::LDK + (wn * C::WTN + lrow) * C::LDK + lk;
-    const char* sB2 = sB + BN * C::LDK;
-#pragma unroll
-    for (int s = 0; s < BK / C::MK; ++s) {
-      const int ko = s * C::MK * ES;
-      typename F::T af[C::TM], bf[C::TN], bf2[DUAL ? C::TN : 1];
-#pragma unroll
-      for (int i = 0; i < C::TM; ++i) af[i] = F::load(sA + i * 32 * C::LDK + ko);
-#pragma unroll
-      for (int j = 0; j < C::TN; ++j) {
-        bf[j] = F::load(sB + j * 32 * C::LDK + ko);
-        if constexpr (DUAL) bf2[j] = F::load(sB2 + j * 32 * C::LDK + ko);
+    static_for<0, S>([&](auto s) {
+      constexpr int SS = decltype(s)::value;
+      if constexpr (SS + 1 < S) {
+        lfrag(cur, int_c<SS + 1>{}, int_c<(SS + 1) & 1>{});
+      } else {
+        __syncthreads();
+        lfrag(cur ^ 1, int_c<0>{}, int_c<0>{});
       }
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < C::TM; ++i)
 #pragma unroll
         for (int j = 0; j < C::TN; ++j) {
-          acc[i][j] = M::mma(af[i], bf[j], acc[i][j]);
-          if constexpr (DUAL) acc2[i][j] = M::mma(af[i], bf2[j], acc2[i][j]);
+          acc[i][j] = M::mma(fb[SS & 1][j], fa[SS & 1][i], acc[i][j]);
+          if constexpr (DUAL) acc2[i][j] = M::mma(fb2[SS & 1][j], fa[SS & 1][i], acc2[i][j]);
         }
-    }
-    if (kt + 1 < KT) lstore(cur ^ 1);
-    __syncthreads();
+      // The LDS store of tile kt + 1 (step 0) and the loads of tile kt + 2 (step 1) are spread between this step's
+      // MFMAs, one memory instruction per MFMA: issued as a burst they would queue in the memory pipeline and stall
+      // the in-order issue of the MFMAs behind them.
+      constexpr int NM = C::TM * C::TN * C::NB;
+      if constexpr (SS == 0) {
+        lstore(cur ^ 1);
+        static_for<0, NM>([&](auto) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU (transposes, addresses)
+          __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS write
+        });
+      }
+      if constexpr (SS == (S > 2 ? 1 : 0)) {
+        gload(min(kt + 2, KT - 1));
+        static_for<0, NM>([&](auto) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global load
+        });
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    });
   }
 
-  // Epilogue: acc register r of lane l holds C[8·(r/4) + 4·(l/32) + r%4][l%32] of its 32×32 tile. The wave's
-  // accumulators go to LDS in rounds of EPI_ROWS tile-rows (compile-time indices keep them in registers until then);
-  // a rolled loop then hands each lane 16-column row segments, so stores are contiguous and the epilogue body is
-  // compiled once.
-  constexpr int PITCH = C::WTN + 1;  // words per LDS row (+1 against bank conflicts)
+  // Epilogue. With the swapped operands, register r of lane l holds C[l%32][8·(r/4) + 4·(l/32) + r%4] of its
+  // 32×32 tile: registers 4g..4g+3 are 4 consecutive columns of one row. Each wave stages its accumulators in its own
+  // LDS region, in rounds of EPI_ROWS tile-rows (compile-time indices keep them in registers until then), with one
+  // 16-byte write per run; a short loop specialised for the epilogue kind and output type then hands each lane 16-byte output
+  // chunks in row order, so global stores are contiguous.
+  __syncthreads();  // the main loop's last fragment reads of the LDS stages are complete in every wave
+  constexpr int PITCH = C::WTN + 4;  // words per LDS row (16-byte pad against bank conflicts)
   constexpr int EPI_ROWS = C::EPI_ROWS;
   constexpr int REGION = EPI_ROWS * 32 * PITCH;
   uint32_t* patch = (uint32_t*)smem + wave * C::NB * REGION;
@@ -445,24 +523,32 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_mfma_kernel(const GemmArgs 
     static_for<0, EPI_ROWS * C::TN>([&](auto t) {
       constexpr int il = decltype(t)::value / C::TN, j = decltype(t)::value % C::TN;
       constexpr int i = round * EPI_ROWS + il;
+      const int row = il * 32 + (lane & 31);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = il * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      for (int g = 0; g < 4; ++g) {
+        const int col = j * 32 + 8 * g + 4 * (lane >> 5);
         // (element reads through the vector subscript, then a value conversion: a bit-cast of the subscript
         //  expression was lowered to element 0 for every r)
-        patch[row * PITCH + j * 32 + (lane & 31)] = acc_elem_bits(acc[i][j], r);
-        if constexpr (DUAL) patch[REGION + row * PITCH + j * 32 + (lane & 31)] = acc_elem_bits(acc2[i][j], r);
+        *(u32x4*)(patch + row * PITCH + col) =
+            u32x4{acc_elem_bits(acc[i][j], 4 * g), acc_elem_bits(acc[i][j], 4 * g + 1),
+                  acc_elem_bits(acc[i][j], 4 * g + 2), acc_elem_bits(acc[i][j], 4 * g + 3)};
+        if constexpr (DUAL)
+          *(u32x4*)(patch + REGION + row * PITCH + col) =
+              u32x4{acc_elem_bits(acc2[i][j], 4 * g), acc_elem_bits(acc2[i][j], 4 * g + 1),
+                    acc_elem_bits(acc2[i][j], 4 * g + 2), acc_elem_bits(acc2[i][j], 4 * g + 3)};
       }
     });
-    __syncthreads();
-    constexpr int SEGS = EPI_ROWS * 32 * (C::WTN / 16);
-    for (int s = lane; s < SEGS; s += 64) {
-      const int row = s / (C::WTN / 16), c0 = (s % (C::WTN / 16)) * 16;
-      const uint32_t* seg = patch + row * PITCH + c0;
-      epilogue_row16<M::INT, DUAL>(G, b, m0 + wm * C::WTM + round * EPI_ROWS * 32 + row, n0 + wn * C::WTN + c0, seg,
-                                   DUAL ? seg + REGION : nullptr);
+    // the region is private to this wave: ordering its own LDS writes before its reads needs no workgroup barrier
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    epi_round<M::INT, DUAL, C::WTN, PITCH, EPI_ROWS * 32>(G, b, m0 + wm * C::WTM + round * EPI_ROWS * 32,
+                                                         n0 + wn * C::WTN, patch, patch + REGION, lane);
+    if constexpr (round + 1 < C::TM / EPI_ROWS) {  // this round's reads before the next round's writes
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    __syncthreads();
   });
 }
 

@@ -115,11 +115,18 @@ static bool pick_mfma(const GemmArgs& g, Choice* c) {
   if (g.N % 16) return false;  // 16-element row segments in the epilogue
   int kind = mma_kind(g);
   if (kind < 0) return false;
+  // output types the MFMA epilogue writes (outputs are whole device allocations, so 16-byte aligned)
+  const bool int_acc = kind == MMA_I8;
+  if (!mfma_out_supported(g.out_dtype[0], int_acc, g.epilogue, false)) return false;
+  if (g.epilogue == EPI_SCALE && g.raw_out && !mfma_out_supported(g.out_dtype[1], int_acc, g.epilogue, true))
+    return false;
   const int es = kind == MMA_BF16 || kind == MMA_F16 ? 2 : (kind == MMA_F32 ? 4 : 1);
   const int ve = 16 / es;
   // operand layouts: K-contiguous (sk == 1) or row-contiguous (sr == 1)
   auto layout = [&](const GemmOperand& o, int rows, int* r) -> bool {
     if (((uintptr_t)o.ptr & 15) != 0) return false;
+    // tiles (≤ 256 rows / k-rows) are read through 32-bit buffer offsets from the tile origin
+    if ((o.sr > o.sk ? o.sr : o.sk) * (int64_t)es * 256 >= ((int64_t)1 << 31)) return false;
     if (o.sk == 1 && (o.sr % ve) == 0 && (o.sb % ve) == 0) { *r = 0; return true; }
     if (o.sr == 1 && (o.sk % ve) == 0 && (o.sb % ve) == 0) { *r = 1; return true; }
     (void)rows;
