@@ -261,19 +261,38 @@ __device__ __forceinline__ uint32_t out_bits(uint32_t x, bool is_float) {
 }
 
 // One epilogue pass over a wave's staged accumulators: ROWS rows of WTN words at `reg` (and `reg2`, the second
-// accumulator of a dual GEMM), row pitch PITCH words. Each lane takes 16-byte output chunks (16 / size(DT) values)
-// in row order, so consecutive lanes write consecutive bytes of a row. KIND is EPI_STORE / EPI_SCALE /
-// EPI_SWIGLU; the output type and the epilogue kind are compile-time, so each pass is a short loop.
-template <int KIND, int DT, bool INT, int WTN, int PITCH, int ROWS>
+// accumulator of a dual GEMM), row pitch PITCH words. Each lane owns one 16-byte output chunk column (16 / size(DT)
+// values) and walks the rows in steps of 64 / chunks-per-row, so consecutive lanes write consecutive bytes of a row.
+// KIND is EPI_STORE / EPI_SCALE / EPI_SWIGLU; the output type, the epilogue kind and the trip count are
+// compile-time, so each pass is a short unrolled loop whose LDS reads can be issued ahead of the conversions. MIDR:
+// the value is rounded to G.mid_round (bf16 or f16) before the output conversion.
+template <int KIND, int DT, bool INT, bool MIDR, int WTN, int PITCH, int ROWS>
 __device__ __forceinline__ void epi_pass(const GemmArgs& G, void* out, int b, int m0, int n0, const uint32_t* reg,
                                          const uint32_t* reg2, int lane) {
   constexpr int OS = out_size<DT>();
   constexpr int VPC = 16 / OS;  // values per chunk
   constexpr int CPR = WTN / VPC;
-  static_assert(WTN % VPC == 0, "wave tile narrower than a 16-byte chunk");
-  for (int c = lane; c < ROWS * CPR; c += 64) {
-    const int row = c / CPR, col = (c % CPR) * VPC;
-    const int m = m0 + row, n = n0 + col;
+  static_assert(WTN % VPC == 0 && 64 % CPR == 0 && (ROWS * CPR) % 64 == 0, "epilogue chunk layout");
+  constexpr int RSTEP = 64 / CPR, ITER = ROWS * CPR / 64;
+  const int row0 = lane / CPR, col = (lane % CPR) * VPC;
+  const int n = n0 + col;
+  char* optr = (char*)out + (((int64_t)b * G.M + m0 + row0) * (int64_t)G.N + n) * OS;
+  const int64_t ostep = (int64_t)RSTEP * G.N * OS;
+  // per-column operands are the same for every row this lane visits
+  float cs[VPC], cs2[VPC];
+  if constexpr (KIND == EPI_SCALE || KIND == EPI_SWIGLU) {
+    const float* cp = G.col ? G.col + (int64_t)b * G.col_sb + (int64_t)n * G.col_sn : nullptr;
+#pragma unroll
+    for (int e = 0; e < VPC; ++e) cs[e] = cp ? cp[(int64_t)e * G.col_sn] : 1.0f;
+  }
+  if constexpr (KIND == EPI_SWIGLU) {
+    const float* cp = G.col2 ? G.col2 + (int64_t)b * G.col2_sb + (int64_t)n * G.col2_sn : nullptr;
+#pragma unroll
+    for (int e = 0; e < VPC; ++e) cs2[e] = cp ? cp[(int64_t)e * G.col2_sn] : 1.0f;
+  }
+#pragma unroll 4
+  for (int it = 0; it < ITER; ++it) {
+    const int row = row0 + it * RSTEP;
     uint32_t v[VPC];
 #pragma unroll
     for (int q = 0; q < VPC / 4; ++q) {
@@ -283,20 +302,16 @@ __device__ __forceinline__ void epi_pass(const GemmArgs& G, void* out, int b, in
     bool is_float = !INT;
     if constexpr (KIND == EPI_SCALE) {
       float rs = G.alpha;
-      if (G.row) rs *= G.row[(int64_t)b * G.row_sb + (int64_t)m * G.row_sm];
-      const float* cp = G.col ? G.col + (int64_t)b * G.col_sb + (int64_t)n * G.col_sn : nullptr;
+      if (G.row) rs *= G.row[(int64_t)b * G.row_sb + (int64_t)(m0 + row) * G.row_sm];
 #pragma unroll
       for (int e = 0; e < VPC; ++e) {
         float x = INT ? (float)(int32_t)v[e] : __uint_as_float(v[e]);
-        x *= rs;
-        if (cp) x *= cp[(int64_t)e * G.col_sn];
-        if (G.mid_round) x = round_float(x, G.mid_round);
+        x = x * rs * cs[e];
+        if constexpr (MIDR) x = G.mid_round == DT_BF16 ? bf16_bits_to_f32(f32_to_bf16_bits(x)) : (float)(_Float16)x;
         v[e] = __float_as_uint(x);
       }
       is_float = true;
     } else if constexpr (KIND == EPI_SWIGLU) {
-      const float* c1 = G.col ? G.col + (int64_t)b * G.col_sb + (int64_t)n * G.col_sn : nullptr;
-      const float* c2 = G.col2 ? G.col2 + (int64_t)b * G.col2_sb + (int64_t)n * G.col2_sn : nullptr;
 #pragma unroll
       for (int q = 0; q < VPC / 4; ++q) {
         const u32x4 w = *(const u32x4*)(reg2 + row * PITCH + col + 4 * q);
@@ -304,13 +319,11 @@ __device__ __forceinline__ void epi_pass(const GemmArgs& G, void* out, int b, in
 #pragma unroll
         for (int e4 = 0; e4 < 4; ++e4) {
           const int e = 4 * q + e4;
-          float a = __uint_as_float(v[e]);
-          float u = __uint_as_float(u4[e4]);
-          if (c1) a *= c1[(int64_t)e * G.col_sn];
-          if (c2) u *= c2[(int64_t)e * G.col2_sn];
-          float lg = 1.0f / (1.0f + expf(-a));
+          const float a = __uint_as_float(v[e]) * cs[e];
+          const float u = __uint_as_float(u4[e4]) * cs2[e];
+          const float lg = 1.0f / (1.0f + expf(-a));
           float x = (a * lg) * u;
-          if (G.mid_round) x = round_float(x, G.mid_round);
+          if constexpr (MIDR) x = G.mid_round == DT_BF16 ? bf16_bits_to_f32(f32_to_bf16_bits(x)) : (float)(_Float16)x;
           v[e] = __float_as_uint(x);
         }
       }
@@ -328,24 +341,28 @@ __device__ __forceinline__ void epi_pass(const GemmArgs& G, void* out, int b, in
                (out_bits<DT>(v[4 * q + 2], is_float) << 16) | (out_bits<DT>(v[4 * q + 3], is_float) << 24);
       }
     }
-    *(u32x4*)((char*)out + (((int64_t)b * G.M + m) * (int64_t)G.N + n) * OS) = u32x4{w[0], w[1], w[2], w[3]};
+    *(u32x4*)(optr + it * ostep) = u32x4{w[0], w[1], w[2], w[3]};
   }
 }
 
 // Output types each epilogue kind supports on the MFMA kernels (`raw`: the raw-accumulator second output).
+__host__ __device__ inline bool mfma_mid_round_supported(int mid_round, bool raw_out) {
+  return mid_round == 0 || ((mid_round == DT_BF16 || mid_round == DT_F16) && !raw_out);
+}
 __host__ __device__ inline bool mfma_out_supported(int dt, bool int_acc, int epilogue, bool raw) {
   if (raw) return int_acc ? dt == DT_S32 : (dt == DT_F32 || dt == DT_BF16);
   if (int_acc && epilogue == EPI_STORE) return dt == DT_S32 || dt == DT_F32;
   return dt == DT_F32 || dt == DT_BF16 || dt == DT_F16 || (!int_acc && dt == DT_F8E4M3FN);
 }
 
-// Epilogue of one staged round: dispatch (uniform) on the epilogue kind and output type to one compact pass.
-template <bool INT, bool DUAL, int WTN, int PITCH, int ROWS>
-__device__ __forceinline__ void epi_round(const GemmArgs& G, int b, int m0, int n0, const uint32_t* reg,
-                                          const uint32_t* reg2, int lane) {
-#define RYFT_EPI(K, DT, OUT) epi_pass<K, DT, INT, WTN, PITCH, ROWS>(G, OUT, b, m0, n0, reg, reg2, lane)
+// Epilogue of one staged round: dispatch (uniform) on the epilogue kind, the intermediate rounding and the output
+// type to one compact pass.
+template <bool INT, bool DUAL, bool MIDR, int WTN, int PITCH, int ROWS>
+__device__ __forceinline__ void epi_round_mr(const GemmArgs& G, int b, int m0, int n0, const uint32_t* reg,
+                                             const uint32_t* reg2, int lane) {
+#define RYFT_EPI(K, DT, OUT) epi_pass<K, DT, INT, MIDR, WTN, PITCH, ROWS>(G, OUT, b, m0, n0, reg, reg2, lane)
   const int dt = G.out_dtype[0];
-  if (G.epilogue == EPI_STORE) {
+  if (!MIDR && G.epilogue == EPI_STORE) {
     if (INT && dt == DT_S32) RYFT_EPI(EPI_STORE, DT_S32, G.out_ptr[0]);
     else if (dt == DT_F32) RYFT_EPI(EPI_STORE, DT_F32, G.out_ptr[0]);
     else if (!INT && dt == DT_BF16) RYFT_EPI(EPI_STORE, DT_BF16, G.out_ptr[0]);
@@ -356,7 +373,7 @@ __device__ __forceinline__ void epi_round(const GemmArgs& G, int b, int m0, int 
     else if (dt == DT_BF16) RYFT_EPI(EPI_SCALE, DT_BF16, G.out_ptr[0]);
     else if (dt == DT_F16) RYFT_EPI(EPI_SCALE, DT_F16, G.out_ptr[0]);
     else if (!INT && dt == DT_F8E4M3FN) RYFT_EPI(EPI_SCALE, DT_F8E4M3FN, G.out_ptr[0]);
-    if (G.raw_out) {
+    if (!MIDR && G.raw_out) {
       const int rt = G.out_dtype[1];
       if (INT) RYFT_EPI(EPI_STORE, DT_S32, G.out_ptr[1]);
       else if (rt == DT_F32) RYFT_EPI(EPI_STORE, DT_F32, G.out_ptr[1]);
@@ -369,6 +386,13 @@ __device__ __forceinline__ void epi_round(const GemmArgs& G, int b, int m0, int 
     else RYFT_EPI(EPI_SWIGLU, DT_F8E4M3FN, G.out_ptr[0]);
   }
 #undef RYFT_EPI
+}
+
+template <bool INT, bool DUAL, int WTN, int PITCH, int ROWS>
+__device__ __forceinline__ void epi_round(const GemmArgs& G, int b, int m0, int n0, const uint32_t* reg,
+                                          const uint32_t* reg2, int lane) {
+  if (G.mid_round) epi_round_mr<INT, DUAL, true, WTN, PITCH, ROWS>(G, b, m0, n0, reg, reg2, lane);
+  else epi_round_mr<INT, DUAL, false, WTN, PITCH, ROWS>(G, b, m0, n0, reg, reg2, lane);
 }
 
 template <int KIND, int BM, int BN, int BK, int WM, int WN, bool A_R, bool B_R, bool DUAL>
@@ -538,17 +562,12 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_mfma_kernel(const GemmArgs 
                     acc_elem_bits(acc2[i][j], 4 * g + 2), acc_elem_bits(acc2[i][j], 4 * g + 3)};
       }
     });
-    // the region is private to this wave: ordering its own LDS writes before its reads needs no workgroup barrier
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // The region is private to this wave, and one wave's LDS operations execute in order: keeping the compiler from
+    // moving the reads above the writes is all the ordering needed (a memory fence would also wait for the stores).
+    __asm__ __volatile__("" ::: "memory");
     epi_round<M::INT, DUAL, C::WTN, PITCH, EPI_ROWS * 32>(G, b, m0 + wm * C::WTM + round * EPI_ROWS * 32,
                                                          n0 + wn * C::WTN, patch, patch + REGION, lane);
-    if constexpr (round + 1 < C::TM / EPI_ROWS) {  // this round's reads before the next round's writes
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    }
+    if constexpr (round + 1 < C::TM / EPI_ROWS) __asm__ __volatile__("" ::: "memory");  // reads before next writes
   });
 }
 

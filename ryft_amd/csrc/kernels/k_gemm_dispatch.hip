@@ -120,6 +120,8 @@ static bool pick_mfma(const GemmArgs& g, Choice* c) {
   if (!mfma_out_supported(g.out_dtype[0], int_acc, g.epilogue, false)) return false;
   if (g.epilogue == EPI_SCALE && g.raw_out && !mfma_out_supported(g.out_dtype[1], int_acc, g.epilogue, true))
     return false;
+  if (g.epilogue != EPI_STORE && !mfma_mid_round_supported(g.mid_round, g.raw_out != 0)) return false;
+  if (g.epilogue == EPI_STORE && g.mid_round) return false;
   const int es = kind == MMA_BF16 || kind == MMA_F16 ? 2 : (kind == MMA_F32 ? 4 : 1);
   const int ve = 16 / es;
   // operand layouts: K-contiguous (sk == 1) or row-contiguous (sr == 1)

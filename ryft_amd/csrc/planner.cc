@@ -1228,7 +1228,10 @@ std::string Plan::describe() const {
     if (s.kind == Step::GEMM) {
       const GemmArgs& g = s.gemm;
       os << " batch=" << g.batch << " M=" << g.M << " N=" << g.N << " K=" << g.K << " A=" << dtype_name((DType)g.A.dtype)
-         << " B=" << dtype_name((DType)g.B.dtype) << (g.dual ? " dual" : "") << " epilogue=" << g.epilogue;
+         << " B=" << dtype_name((DType)g.B.dtype) << (g.dual ? " dual" : "") << " epilogue=" << g.epilogue
+         << " out=" << dtype_name((DType)g.out_dtype[0]);
+      if (g.raw_out) os << "+" << dtype_name((DType)g.out_dtype[1]);
+      if (g.mid_round) os << " mid_round=" << dtype_name((DType)g.mid_round);
     } else if (s.kind == Step::ELEMENTWISE) {
       os << " instrs=" << s.ew.n_instr << " leaves=" << s.ew.n_leaves << " elems=" << s.ew.total;
     } else if (s.kind == Step::REDUCE) {
