@@ -409,14 +409,20 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_mfma_kernel(const GemmArgs 
   const int wm = wave / WN, wn = wave % WN;
 
   // XCD-aware tile order: consecutive workgroup ids land on different XCDs (round-robin), so regroup them such that
-  // each XCD owns a contiguous run of (batch, tile-row, tile-col) tiles.
+  // each XCD owns a contiguous run of tile ids; within a batch, ids run column-major through groups of up to 8
+  // tile-rows, so one XCD's run covers a compact block of tiles and each A row-panel / B column-panel is fetched
+  // into that XCD's L2 by few XCDs (with a row-major order every XCD would stream every B panel).
   const int tiles_n = G.N / BN, tiles_m = G.M / BM;
-  const int total = tiles_n * tiles_m * G.batch;
+  const int per_batch = tiles_n * tiles_m;
+  const int total = per_batch * G.batch;
   int bid = blockIdx.x;
   if ((total & 7) == 0) bid = (bid & 7) * (total >> 3) + (bid >> 3);
-  const int tn = bid % tiles_n;
-  const int tm = (bid / tiles_n) % tiles_m;
-  const int b = bid / (tiles_n * tiles_m);
+  const int b = bid / per_batch, t = bid % per_batch;
+  const int GM = tiles_m < 8 ? tiles_m : 8;
+  const int first_m = (t / (GM * tiles_n)) * GM;
+  const int gm = min(GM, tiles_m - first_m);  // the last group may hold fewer tile-rows
+  const int tg = t - first_m * tiles_n;
+  const int tm = first_m + tg % gm, tn = tg / gm;
   const int m0 = tm * BM, n0 = tn * BN;
 
   const char* Ab = (const char*)G.A.ptr + ((int64_t)b * G.A.sb + (int64_t)m0 * G.A.sr) * ES;
