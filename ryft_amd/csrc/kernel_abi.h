@@ -18,12 +18,18 @@ namespace ryft {
 
 enum EwLeafKind : int32_t { EW_LEAF_GENERAL = 0, EW_LEAF_IDENTITY = 1, EW_LEAF_SCALAR = 2 };
 
+// How a leaf is read when a thread evaluates V consecutive elements of the innermost dimension at once (set by the
+// launcher from the patched pointers; ignored at V = 1).
+enum EwVecMode : int32_t { EW_VEC_GATHER = 0, EW_VEC_CONTIG = 1, EW_VEC_BCAST = 2 };
+
 struct EwLeaf {
   const void* ptr;
   int32_t dtype;  // DType
   int32_t kind;   // EwLeafKind
   int64_t offset; // element offset
   int64_t strides[EW_MAX_RANK];
+  int32_t vmode;    // EwVecMode
+  int32_t vstride;  // EW_VEC_GATHER: element stride between consecutive innermost elements
 };
 
 enum EwOp : uint8_t {

@@ -8,6 +8,10 @@
 
 namespace ryft {
 
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+
+
 // DType values (PJRT_Buffer_Type numbering; kept literal so kernels do not include the C API header).
 enum : int {
   DT_PRED = 1, DT_S8 = 2, DT_S16 = 3, DT_S32 = 4, DT_S64 = 5, DT_U8 = 6, DT_U16 = 7, DT_U32 = 8, DT_U64 = 9,
@@ -194,92 +198,174 @@ __device__ __forceinline__ void decompose(int64_t lin, const EwProgram& P, int32
   }
 }
 
-// Runs the program; `acc` holds the GEMM accumulators (bits) for EW_ACC. Results land in regs[].
-__device__ __forceinline__ void ew_run(const EwProgram& P, int64_t lin, const int32_t* coord, const uint32_t* acc,
-                                       uint32_t* regs) {
+// Element bits of a leaf at V consecutive innermost positions starting at linear index `lin` (coordinates `coord`).
+template <int V>
+__device__ __forceinline__ void load_leaf(const EwLeaf& L, int64_t lin, const int32_t* coord, int rank, uint32_t* r) {
+  const int64_t off = leaf_offset(L, lin, coord, rank);
+  if constexpr (V == 1) {
+    r[0] = load_bits(L.ptr, off, L.dtype);
+  } else {
+    if (L.vmode == EW_VEC_BCAST) {
+      const uint32_t x = load_bits(L.ptr, off, L.dtype);
+#pragma unroll
+      for (int e = 0; e < V; ++e) r[e] = x;
+    } else if (L.vmode == EW_VEC_CONTIG) {
+      // V elements of ≤ 4 bytes, aligned to V·size (checked by the launcher)
+      static_assert(V == 8, "vector leaf loads are written for 8 elements");
+      const char* p = (const char*)L.ptr;
+      switch (L.dtype) {
+        case DT_F32: case DT_S32: case DT_U32: {
+          const u32x4v a = *(const u32x4v*)(p + off * 4), b = *(const u32x4v*)(p + off * 4 + 16);
+          r[0] = a.x, r[1] = a.y, r[2] = a.z, r[3] = a.w, r[4] = b.x, r[5] = b.y, r[6] = b.z, r[7] = b.w;
+          break;
+        }
+        case DT_BF16: case DT_F16: case DT_S16: case DT_U16: {
+          const u32x4v a = *(const u32x4v*)(p + off * 2);
+          const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t lo = w[q] & 0xffffu, hi = w[q] >> 16;
+            if (L.dtype == DT_BF16) r[2 * q] = lo << 16, r[2 * q + 1] = hi << 16;
+            else if (L.dtype == DT_F16) r[2 * q] = __float_as_uint((float)__builtin_bit_cast(_Float16, (uint16_t)lo)),
+                                        r[2 * q + 1] = __float_as_uint((float)__builtin_bit_cast(_Float16, (uint16_t)hi));
+            else if (L.dtype == DT_S16) r[2 * q] = (uint32_t)(int32_t)(int16_t)lo, r[2 * q + 1] = (uint32_t)(int32_t)(int16_t)hi;
+            else r[2 * q] = lo, r[2 * q + 1] = hi;
+          }
+          break;
+        }
+        default: {  // 1-byte types
+          const u32x2v a = *(const u32x2v*)(p + off);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const uint32_t byte = ((e < 4 ? a.x : a.y) >> (8 * (e & 3))) & 0xffu;
+            switch (L.dtype) {
+              case DT_F8E4M3FN: r[e] = __float_as_uint(e4m3fn_bits_to_f32(byte)); break;
+              case DT_F8E5M2: r[e] = __float_as_uint(e5m2_bits_to_f32(byte)); break;
+              case DT_S8: r[e] = (uint32_t)(int32_t)(int8_t)byte; break;
+              default: r[e] = byte; break;
+            }
+          }
+          break;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < V; ++e) r[e] = load_bits(L.ptr, off + (int64_t)e * L.vstride, L.dtype);
+    }
+  }
+}
+
+// The VM's registers for V elements per thread. At V = 1 the array is promoted to VGPRs (uniform indirect moves);
+// at V = 8 the compiler keeps it in private memory (L1-resident), which the 8-wide evaluation amortises.
+template <int V>
+struct RegFile {
+  uint32_t v[EW_MAX_REGS][V];
+  __device__ __forceinline__ uint32_t get(int r, int e) const { return v[r][e]; }
+  __device__ __forceinline__ void set(int r, int e, uint32_t x) { v[r][e] = x; }
+};
+
+// Runs the program on V consecutive elements of the innermost dimension (linear indices lin .. lin+V-1, all in one
+// innermost row; `coord` are the coordinates of `lin`). `acc` holds the GEMM accumulators (bits) for EW_ACC (V = 1
+// only). Results land in R (register, element). The instruction dispatch is uniform across the wave, so its cost
+// is paid once per V elements.
+template <int V>
+__device__ __forceinline__ void ew_run_v(const EwProgram& P, int64_t lin, const int32_t* coord, const uint32_t* acc,
+                                         RegFile<V>& R) {
+#define EW_FOR _Pragma("unroll") for (int e = 0; e < V; ++e)
+#define EW_FA __uint_as_float(R.get(I.a, e))
+#define EW_FB __uint_as_float(R.get(I.b, e))
+#define EW_IA ((int32_t)R.get(I.a, e))
+#define EW_IB ((int32_t)R.get(I.b, e))
+#define EW_UA (R.get(I.a, e))
+#define EW_UB (R.get(I.b, e))
+#define EW_F(OP, EXPR) case OP: EW_FOR r[e] = __float_as_uint(EXPR); break;
+#define EW_U(OP, EXPR) case OP: EW_FOR r[e] = (uint32_t)(EXPR); break;
   for (int pc = 0; pc < P.n_instr; ++pc) {
     const EwInstr I = P.instr[pc];
-    uint32_t r = 0;
-    float fa = __uint_as_float(regs[I.a]), fb = __uint_as_float(regs[I.b]);
-    int32_t ia = (int32_t)regs[I.a], ib = (int32_t)regs[I.b];
+    uint32_t r[V];
     switch (I.op) {
-      case EW_LOAD: {
-        const EwLeaf& L = P.leaves[I.a];
-        r = load_bits(L.ptr, leaf_offset(L, lin, coord, P.rank), L.dtype);
-        break;
-      }
-      case EW_CONST: r = I.imm.u; break;
-      case EW_IOTA: r = (uint32_t)coord[I.a]; break;
-      case EW_ACC: r = acc[I.a]; break;
-      case EW_NEG: r = __float_as_uint(-fa); break;
-      case EW_ABS: r = __float_as_uint(fabsf(fa)); break;
-      case EW_EXP: r = __float_as_uint(expf(fa)); break;
-      case EW_LOG: r = __float_as_uint(logf(fa)); break;
-      case EW_RSQRT: r = __float_as_uint(1.0f / sqrtf(fa)); break;
-      case EW_SQRT: r = __float_as_uint(sqrtf(fa)); break;
-      case EW_TANH: r = __float_as_uint(tanhf(fa)); break;
-      case EW_LOGISTIC: r = __float_as_uint(1.0f / (1.0f + expf(-fa))); break;
-      case EW_FLOOR: r = __float_as_uint(floorf(fa)); break;
-      case EW_CEIL: r = __float_as_uint(ceilf(fa)); break;
-      case EW_SIGN: r = __float_as_uint(fa != fa ? fa : (fa > 0.f ? 1.f : (fa < 0.f ? -1.f : fa))); break;
-      case EW_EXPM1: r = __float_as_uint(expm1f(fa)); break;
-      case EW_LOG1P: r = __float_as_uint(log1pf(fa)); break;
-      case EW_INEG: r = (uint32_t)(-ia); break;
-      case EW_IABS: r = (uint32_t)(ia < 0 ? -ia : ia); break;
-      case EW_NOT: r = (I.round == DT_PRED) ? (uint32_t)(ia == 0) : ~regs[I.a]; break;
-      case EW_ISIGN: r = (uint32_t)(ia > 0 ? 1 : (ia < 0 ? -1 : 0)); break;
-      case EW_CVT_F2F: r = __float_as_uint(fa); break;
-      case EW_CVT_F2I: r = (uint32_t)f2i_sat(fa, I.round); break;
-      case EW_CVT_I2F: r = __float_as_uint(I.imm.i ? (float)regs[I.a] : (float)ia); break;  // imm: source unsigned
-      case EW_CVT_I2I: r = regs[I.a]; break;
-      case EW_CVT_F2P: r = (uint32_t)(fa != 0.0f); break;
-      case EW_CVT_I2P: r = (uint32_t)(ia != 0); break;
-      case EW_ADD: r = __float_as_uint(fa + fb); break;
-      case EW_SUB: r = __float_as_uint(fa - fb); break;
-      case EW_MUL: r = __float_as_uint(fa * fb); break;
-      case EW_DIV: r = __float_as_uint(fa / fb); break;
-      case EW_MAX: r = __float_as_uint((fa != fa || fb != fb) ? __uint_as_float(0x7fc00000u) : fmaxf(fa, fb)); break;
-      case EW_MIN: r = __float_as_uint((fa != fa || fb != fb) ? __uint_as_float(0x7fc00000u) : fminf(fa, fb)); break;
-      case EW_POW: r = __float_as_uint(powf(fa, fb)); break;
-      case EW_REM: r = __float_as_uint(fmodf(fa, fb)); break;
-      case EW_IADD: r = (uint32_t)(ia + ib); break;
-      case EW_ISUB: r = (uint32_t)(ia - ib); break;
-      case EW_IMUL: r = (uint32_t)(ia * ib); break;
-      case EW_IDIV: r = (uint32_t)(ib == 0 ? -1 : (ia == (int32_t)0x80000000 && ib == -1) ? ia : ia / ib); break;
-      case EW_IREM: r = (uint32_t)(ib == 0 ? ia : (ib == -1 ? 0 : ia % ib)); break;
-      case EW_UDIV: r = regs[I.b] == 0 ? 0xffffffffu : regs[I.a] / regs[I.b]; break;
-      case EW_UREM: r = regs[I.b] == 0 ? regs[I.a] : regs[I.a] % regs[I.b]; break;
-      case EW_IMAX: r = (uint32_t)(ia > ib ? ia : ib); break;
-      case EW_IMIN: r = (uint32_t)(ia < ib ? ia : ib); break;
-      case EW_UMAX: r = regs[I.a] > regs[I.b] ? regs[I.a] : regs[I.b]; break;
-      case EW_UMIN: r = regs[I.a] < regs[I.b] ? regs[I.a] : regs[I.b]; break;
-      case EW_AND: r = regs[I.a] & regs[I.b]; break;
-      case EW_OR: r = regs[I.a] | regs[I.b]; break;
-      case EW_XOR: r = regs[I.a] ^ regs[I.b]; break;
-      case EW_FCMP: r = cmp_f(fa, fb, I.imm.i); break;
-      case EW_ICMP: r = cmp_i<int32_t>(ia, ib, I.imm.i); break;
-      case EW_UCMP: r = cmp_i<uint32_t>(regs[I.a], regs[I.b], I.imm.i); break;
-      case EW_SELECT: r = regs[I.a] ? regs[I.b] : regs[I.c]; break;
-      case EW_FCLAMP: {
-        float x = fb, lo = fa, hi = __uint_as_float(regs[I.c]);
-        r = __float_as_uint(fminf(fmaxf(x, lo), hi));
-        break;
-      }
-      case EW_ICLAMP: {
-        int32_t x = ib, lo = ia, hi = (int32_t)regs[I.c];
-        r = (uint32_t)(x < lo ? lo : (x > hi ? hi : x));
-        break;
-      }
-      default: break;
+      case EW_LOAD: load_leaf<V>(P.leaves[I.a], lin, coord, P.rank, r); break;
+      EW_U(EW_CONST, I.imm.u)
+      EW_U(EW_IOTA, coord[I.a] + (I.a == P.rank - 1 ? e : 0))
+      EW_U(EW_ACC, acc[I.a])
+      EW_F(EW_NEG, -EW_FA)
+      EW_F(EW_ABS, fabsf(EW_FA))
+      EW_F(EW_EXP, expf(EW_FA))
+      EW_F(EW_LOG, logf(EW_FA))
+      EW_F(EW_RSQRT, 1.0f / sqrtf(EW_FA))
+      EW_F(EW_SQRT, sqrtf(EW_FA))
+      EW_F(EW_TANH, tanhf(EW_FA))
+      EW_F(EW_LOGISTIC, 1.0f / (1.0f + expf(-EW_FA)))
+      EW_F(EW_FLOOR, floorf(EW_FA))
+      EW_F(EW_CEIL, ceilf(EW_FA))
+      EW_F(EW_SIGN, EW_FA != EW_FA ? EW_FA : (EW_FA > 0.f ? 1.f : (EW_FA < 0.f ? -1.f : EW_FA)))
+      EW_F(EW_EXPM1, expm1f(EW_FA))
+      EW_F(EW_LOG1P, log1pf(EW_FA))
+      EW_U(EW_INEG, -EW_IA)
+      EW_U(EW_IABS, EW_IA < 0 ? -EW_IA : EW_IA)
+      EW_U(EW_NOT, (I.round == DT_PRED) ? (uint32_t)(EW_IA == 0) : ~EW_UA)
+      EW_U(EW_ISIGN, EW_IA > 0 ? 1 : (EW_IA < 0 ? -1 : 0))
+      EW_F(EW_CVT_F2F, EW_FA)
+      EW_U(EW_CVT_F2I, f2i_sat(EW_FA, I.round))
+      EW_F(EW_CVT_I2F, I.imm.i ? (float)EW_UA : (float)EW_IA)  // imm: source unsigned
+      EW_U(EW_CVT_I2I, EW_UA)
+      EW_U(EW_CVT_F2P, EW_FA != 0.0f)
+      EW_U(EW_CVT_I2P, EW_IA != 0)
+      EW_F(EW_ADD, EW_FA + EW_FB)
+      EW_F(EW_SUB, EW_FA - EW_FB)
+      EW_F(EW_MUL, EW_FA * EW_FB)
+      EW_F(EW_DIV, EW_FA / EW_FB)
+      EW_F(EW_MAX, (EW_FA != EW_FA || EW_FB != EW_FB) ? __uint_as_float(0x7fc00000u) : fmaxf(EW_FA, EW_FB))
+      EW_F(EW_MIN, (EW_FA != EW_FA || EW_FB != EW_FB) ? __uint_as_float(0x7fc00000u) : fminf(EW_FA, EW_FB))
+      EW_F(EW_POW, powf(EW_FA, EW_FB))
+      EW_F(EW_REM, fmodf(EW_FA, EW_FB))
+      EW_U(EW_IADD, EW_IA + EW_IB)
+      EW_U(EW_ISUB, EW_IA - EW_IB)
+      EW_U(EW_IMUL, EW_IA * EW_IB)
+      EW_U(EW_IDIV, EW_IB == 0 ? -1 : (EW_IA == (int32_t)0x80000000 && EW_IB == -1) ? EW_IA : EW_IA / EW_IB)
+      EW_U(EW_IREM, EW_IB == 0 ? EW_IA : (EW_IB == -1 ? 0 : EW_IA % EW_IB))
+      EW_U(EW_UDIV, EW_UB == 0 ? 0xffffffffu : EW_UA / EW_UB)
+      EW_U(EW_UREM, EW_UB == 0 ? EW_UA : EW_UA % EW_UB)
+      EW_U(EW_IMAX, EW_IA > EW_IB ? EW_IA : EW_IB)
+      EW_U(EW_IMIN, EW_IA < EW_IB ? EW_IA : EW_IB)
+      EW_U(EW_UMAX, EW_UA > EW_UB ? EW_UA : EW_UB)
+      EW_U(EW_UMIN, EW_UA < EW_UB ? EW_UA : EW_UB)
+      EW_U(EW_AND, EW_UA & EW_UB)
+      EW_U(EW_OR, EW_UA | EW_UB)
+      EW_U(EW_XOR, EW_UA ^ EW_UB)
+      EW_U(EW_FCMP, cmp_f(EW_FA, EW_FB, I.imm.i))
+      EW_U(EW_ICMP, cmp_i<int32_t>(EW_IA, EW_IB, I.imm.i))
+      EW_U(EW_UCMP, cmp_i<uint32_t>(EW_UA, EW_UB, I.imm.i))
+      EW_U(EW_SELECT, EW_UA ? EW_UB : R.get(I.c, e))
+      EW_F(EW_FCLAMP, fminf(fmaxf(EW_FB, EW_FA), __uint_as_float(R.get(I.c, e))))
+      EW_U(EW_ICLAMP, EW_IB < EW_IA ? EW_IA : (EW_IB > (int32_t)R.get(I.c, e) ? (int32_t)R.get(I.c, e) : EW_IB))
+      default: EW_FOR r[e] = 0; break;
     }
     // per-op rounding to the StableHLO result element type
     if (I.round) {
-      if (dt_is_float(I.round)) r = __float_as_uint(round_float(__uint_as_float(r), I.round));
-      else if (I.op != EW_CVT_F2I) r = (uint32_t)wrap_int((int32_t)r, I.round);
-      else r = (uint32_t)wrap_int((int32_t)r, I.round);
+      if (dt_is_float(I.round)) {
+        EW_FOR r[e] = __float_as_uint(round_float(__uint_as_float(r[e]), I.round));
+      } else {
+        EW_FOR r[e] = (uint32_t)wrap_int((int32_t)r[e], I.round);
+      }
     }
-    regs[I.dst] = r;
+    EW_FOR R.set(I.dst, e, r[e]);
   }
+#undef EW_FOR
+#undef EW_FA
+#undef EW_FB
+#undef EW_IA
+#undef EW_IB
+#undef EW_UA
+#undef EW_UB
+#undef EW_F
+#undef EW_U
+}
+
+// Scalar form (one element): used by the generic GEMM epilogue and the unvectorised kernels.
+__device__ __forceinline__ void ew_run(const EwProgram& P, int64_t lin, const int32_t* coord, const uint32_t* acc,
+                                       RegFile<1>& R) {
+  ew_run_v<1>(P, lin, coord, acc, R);
 }
 
 }  // namespace ryft

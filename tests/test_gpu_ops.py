@@ -1,5 +1,9 @@
 """GPU coverage of the generic kernels (elementwise programs, reductions, transposes, iota / compare / select,
-conversions, the generic GEMM) against the oracle on small shapes."""
+conversions, the generic GEMM) against the oracle on small shapes.
+
+Shapes with an innermost extent of 33 run the one-element-per-thread kernels; extents that are multiples of 8 run
+the 8-wide kernels (vector loads / stores, broadcast and strided leaves), and rows of ≥1024 elements the
+workgroup-per-row reduction."""
 import numpy as np
 import pytest
 
@@ -17,24 +21,33 @@ def _mod(args, rets, body):
 
 
 F = "tensor<8x33xf32>"
+SHAPES = [(8, 33), (6, 64)]
+
+
+def _t(shape, dt="f32"):
+    return "tensor<" + "".join(f"{s}x" for s in shape) + dt + ">"
 
 
 def _f32_inputs(n, shape=(8, 33), seed=1):
     return [configs.HostInput(hd.normal(seed + i, shape), pjrt.BufferType.F32, shape) for i in range(n)]
 
 
+@pytest.mark.parametrize("shape", SHAPES)
 @pytest.mark.parametrize("op", ["add", "subtract", "multiply", "divide", "maximum", "minimum"])
-def test_binary_f32(gpu_client, op):
-    prog = _mod([F, F], [F], f"    %0 = stablehlo.{op} %arg0, %arg1 : {F}\n    return %0 : {F}")
-    ins = _f32_inputs(2)
+def test_binary_f32(gpu_client, op, shape):
+    T = _t(shape)
+    prog = _mod([T, T], [T], f"    %0 = stablehlo.{op} %arg0, %arg1 : {T}\n    return %0 : {T}")
+    ins = _f32_inputs(2, shape)
     outs, _ = run_pjrt(gpu_client, prog, ins)
     check(outs[0], oracle_outputs(prog, ins)[0], 1e-6, op)
 
 
+@pytest.mark.parametrize("shape", SHAPES)
 @pytest.mark.parametrize("op", ["exponential", "log", "rsqrt", "sqrt", "tanh", "logistic", "negate", "abs", "floor"])
-def test_unary_f32(gpu_client, op):
-    prog = _mod([F], [F], f"    %0 = stablehlo.abs %arg0 : {F}\n    %1 = stablehlo.{op} %0 : {F}\n    return %1 : {F}")
-    ins = _f32_inputs(1)
+def test_unary_f32(gpu_client, op, shape):
+    T = _t(shape)
+    prog = _mod([T], [T], f"    %0 = stablehlo.abs %arg0 : {T}\n    %1 = stablehlo.{op} %0 : {T}\n    return %1 : {T}")
+    ins = _f32_inputs(1, shape)
     outs, _ = run_pjrt(gpu_client, prog, ins)
     check(outs[0], oracle_outputs(prog, ins)[0], 2e-6, op)
 
@@ -57,14 +70,18 @@ def test_int_ops_and_wraparound(gpu_client):
         check(o, w, 0, "int")
 
 
-def test_convert_chain_bf16_f8(gpu_client):
-    body = f"""    %0 = stablehlo.convert %arg0 : ({F}) -> tensor<8x33xbf16>
-    %1 = stablehlo.convert %0 : (tensor<8x33xbf16>) -> tensor<8x33xf8E4M3FN>
-    %2 = stablehlo.convert %arg0 : ({F}) -> tensor<8x33xi32>
-    return %0, %1, %2 : tensor<8x33xbf16>, tensor<8x33xf8E4M3FN>, tensor<8x33xi32>"""
-    prog = _mod([F], ["tensor<8x33xbf16>", "tensor<8x33xf8E4M3FN>", "tensor<8x33xi32>"], body)
-    x = np.concatenate([hd.normal(5, (8 * 33 - 6,), 0, 100), np.array([464, 470, -500, 1e-3, 2.5, -2.5])])
-    ins = [configs.HostInput(x.astype(np.float32).reshape(8, 33), pjrt.BufferType.F32, (8, 33))]
+@pytest.mark.parametrize("shape", SHAPES)
+def test_convert_chain_bf16_f8(gpu_client, shape):
+    F, B, E, I = _t(shape), _t(shape, "bf16"), _t(shape, "f8E4M3FN"), _t(shape, "i32")
+    body = f"""    %0 = stablehlo.convert %arg0 : ({F}) -> {B}
+    %1 = stablehlo.convert %0 : ({B}) -> {E}
+    %2 = stablehlo.convert %arg0 : ({F}) -> {I}
+    %3 = stablehlo.convert %1 : ({E}) -> {F}
+    return %0, %1, %2, %3 : {B}, {E}, {I}, {F}"""
+    prog = _mod([F], [B, E, I, F], body)
+    n = shape[0] * shape[1]
+    x = np.concatenate([hd.normal(5, (n - 6,), 0, 100), np.array([464, 470, -500, 1e-3, 2.5, -2.5])])
+    ins = [configs.HostInput(x.astype(np.float32).reshape(shape), pjrt.BufferType.F32, shape)]
     outs, _ = run_pjrt(gpu_client, prog, ins)
     for i, (o, w) in enumerate(zip(outs, oracle_outputs(prog, ins))):
         # conversions are exact: compare bits
@@ -72,17 +89,41 @@ def test_convert_chain_bf16_f8(gpu_client):
             np.array_equal(np.isnan(sh.from_raw(o, w[1])), np.isnan(w[0])), f"convert output {i}"
 
 
+@pytest.mark.parametrize("shape", SHAPES + [(5, 2048)])
 @pytest.mark.parametrize("dims,body", [([1], "add"), ([0], "add"), ([0, 1], "maximum"), ([1], "minimum")])
-def test_reduce(gpu_client, dims, body):
-    out_shape = [s for i, s in enumerate((8, 33)) if i not in dims]
-    ot = "tensor<" + "".join(f"{s}x" for s in out_shape) + "f32>"
+def test_reduce(gpu_client, dims, body, shape):
+    F = _t(shape)
+    out_shape = [s for i, s in enumerate(shape) if i not in dims]
+    ot = _t(out_shape)
     init = "0.000000e+00" if body == "add" else ("0xFF800000" if body == "maximum" else "0x7F800000")
     prog = _mod([F], [ot], f"""    %cst = stablehlo.constant dense<{init}> : tensor<f32>
     %0 = stablehlo.reduce(%arg0 init: %cst) applies stablehlo.{body} across dimensions = {dims} : ({F}, tensor<f32>) -> {ot}
     return %0 : {ot}""")
-    ins = _f32_inputs(1)
+    ins = _f32_inputs(1, shape)
     outs, _ = run_pjrt(gpu_client, prog, ins)
     check(outs[0], oracle_outputs(prog, ins)[0], 1e-6, "reduce")
+
+
+@pytest.mark.parametrize("cols", [64, 4096])
+def test_rmsnorm_rows_bf16(gpu_client, cols):
+    # reduce with a fused prologue over bf16 rows (wavefront-per-row and workgroup-per-row reductions), then a
+    # broadcast row statistic applied by the elementwise kernel
+    X, R, XF = _t((6, cols), "bf16"), _t((6,)), _t((6, cols))
+    body = f"""    %0 = stablehlo.convert %arg0 : ({X}) -> {XF}
+    %1 = stablehlo.multiply %0, %0 : {XF}
+    %cst = stablehlo.constant dense<0.000000e+00> : tensor<f32>
+    %2 = stablehlo.reduce(%1 init: %cst) applies stablehlo.add across dimensions = [1] : ({XF}, tensor<f32>) -> {R}
+    %c = stablehlo.constant dense<{1.0 / cols:e}> : {R}
+    %3 = stablehlo.multiply %2, %c : {R}
+    %4 = stablehlo.rsqrt %3 : {R}
+    %5 = stablehlo.broadcast_in_dim %4, dims = [0] : ({R}) -> {XF}
+    %6 = stablehlo.multiply %0, %5 : {XF}
+    %7 = stablehlo.convert %6 : ({XF}) -> {X}
+    return %7 : {X}"""
+    prog = _mod([X], [X], body)
+    ins = [configs.HostInput(hd.f32_to_bf16_bits(hd.normal(21, (6, cols))), pjrt.BufferType.BF16, (6, cols))]
+    outs, _ = run_pjrt(gpu_client, prog, ins)
+    check(outs[0], oracle_outputs(prog, ins)[0], 1e-2, "rmsnorm")
 
 
 def test_reduce_with_argument_init(gpu_client):
