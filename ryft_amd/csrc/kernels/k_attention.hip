@@ -6,8 +6,9 @@
 // query and split its keys): the running max / sum of the online softmax then need no cross-lane reductions except
 // one swap between the two half-waves, and the rescaling of the output Oᵀ = Vᵀ·Pᵀ is a per-lane multiply. P never
 // leaves registers: the Sᵀ accumulator, rounded to bf16, is directly the B operand of the P·V MFMA, with the
-// matching key order obtained by reading Vᵀ from LDS in the same permuted order. exp uses v_exp_f32 (2^x) on
-// pre-scaled logits. The [S, S] score matrix is never materialised.
+// matching key order obtained by reading Vᵀ from LDS in the same permuted order. Row maxima are taken on the raw
+// scores and each probability costs one FMA and one v_exp_f32 (2^x). Two workgroups share a CU (≤ 256 registers
+// per lane), so one wave's softmax overlaps another's MFMAs. The [S, S] score matrix is never materialised.
 #include <hip/hip_runtime.h>
 
 #include <string>
@@ -34,8 +35,12 @@ __device__ __forceinline__ f32x16_a mma_bf16(const u32x4a& a, const u32x4a& b, f
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_a, a), __builtin_bit_cast(bf16x8_a, b), c, 0, 0, 0);
 }
 
+typedef __bf16 bf16x2_a __attribute__((ext_vector_type(2)));
+typedef float f32x2_a __attribute__((ext_vector_type(2)));
+
+// Two floats → packed bf16 pair with v_cvt_pk_bf16_f32 (round to nearest even; the values here are finite).
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-  return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_a{lo, hi}, bf16x2_a));
 }
 
 template <int D>
@@ -50,7 +55,7 @@ struct AttnCfg {
 };
 
 template <int D>
-__global__ void __launch_bounds__(256) attention_fwd_kernel(const AttnArgs A) {
+__global__ void __launch_bounds__(256, 2) attention_fwd_kernel(const AttnArgs A) {
   using C = AttnCfg<D>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -151,7 +156,7 @@ __global__ void __launch_bounds__(256) attention_fwd_kernel(const AttnArgs A) {
         st[t] = mma_bf16(kf, qf[s], st[t]);
       }
     }
-    // scale, mask, block max
+    // mask and block max on the unscaled scores (the scale is positive, so maxima commute with it)
     const int kbase = j * BKV;
     const bool need_mask = A.causal && (kbase + BKV - 1 > q0 + wave * 32 + A.causal_offset);
     float mloc = -INFINITY;
@@ -159,7 +164,7 @@ __global__ void __launch_bounds__(256) attention_fwd_kernel(const AttnArgs A) {
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        float v = st[t][r] * sl2;
+        float v = st[t][r];
         if (need_mask) {
           int key = kbase + t * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
           if (key > myq + A.causal_offset) v = -INFINITY;
@@ -170,24 +175,25 @@ __global__ void __launch_bounds__(256) attention_fwd_kernel(const AttnArgs A) {
     mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
     const float m_new = fmaxf(m_run, mloc);
     const float m_use = m_new == -INFINITY ? 0.f : m_new;  // a fully masked row keeps p = 0
-    const float alpha = exp2f(m_run - m_use);
+    const float alpha = __builtin_amdgcn_exp2f((m_run - m_use) * sl2);
     m_run = m_new;
     l_run *= alpha;
 #pragma unroll
     for (int t = 0; t < D / 32; ++t)
 #pragma unroll
       for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
-    // P = 2^(s - m), rounded to bf16 as the B operand of Oᵀ = Vᵀ·Pᵀ
+    // P = 2^((s - m)·scale·log2 e) with one FMA and v_exp_f32 per score, packed to bf16 (round to nearest even) as
+    // the B operand of Oᵀ = Vᵀ·Pᵀ
+    const float mb = -m_use * sl2;
     u32x4a pf[4];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       float p[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        p[r] = exp2f(st[t][r] - m_use);
+        p[r] = __builtin_amdgcn_exp2f(fmaf(st[t][r], sl2, mb));
         l_run += p[r];
       }
-      // P enters the bf16 MFMA rounded to bf16 whether the program rounds it (p_dtype bf16) or keeps it in f32
       pf[2 * t] = u32x4a{pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3]), pack_bf16(p[4], p[5]), pack_bf16(p[6], p[7])};
       pf[2 * t + 1] = u32x4a{pack_bf16(p[8], p[9]), pack_bf16(p[10], p[11]), pack_bf16(p[12], p[13]), pack_bf16(p[14], p[15])};
     }

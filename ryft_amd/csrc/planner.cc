@@ -1142,6 +1142,8 @@ bool Planner::try_attention(int d2, int target, DType out_dtype, int root) {
     else return false;
     if (!one_use(d1)) return false;
   }
+  // the kernel takes row maxima of the unscaled scores, which commutes with a positive scale only
+  if (!(scale > 0.0) || !std::isfinite(scale)) return false;
   const Node& D1 = g_.nodes[d1];
   if (D1.op != Op::DotGeneral || D1.type.dtype != DType::F32 || D1.dot.lhs_batch != std::vector<int64_t>{0, 1} ||
       D1.dot.rhs_batch != std::vector<int64_t>{0, 1} || D1.dot.lhs_contract != std::vector<int64_t>{3} ||
