@@ -75,6 +75,9 @@ __global__ void __launch_bounds__(256, 2) attention_fwd_kernel(const AttnArgs A)
 #pragma unroll
   for (int s = 0; s < D / 16; ++s)
     qf[s] = *(const u32x4a*)(Qg + (int64_t)myq * A.qs[2] + s * 16 + 8 * (lane >> 5));
+  // complete the Q loads here: waited for at their first use inside the loop, the wait would run every iteration
+  // and stall on the next KV block's prefetch (vmcnt(0), expcnt / lgkmcnt left open)
+  __builtin_amdgcn_s_waitcnt(0x0F70);
 
   const float sl2 = A.scale * 1.4426950408889634f;  // logits in the log2 domain
   float m_run = -INFINITY, l_run = 0.f;
@@ -94,18 +97,25 @@ __global__ void __launch_bounds__(256, 2) attention_fwd_kernel(const AttnArgs A)
   constexpr int VBLK = (BKV / 8) * (D / 8); // 8×8 blocks of V
   u32x4a kreg[KVEC];
   u32x4a vreg[8];
+  // Buffer loads with the KV block origin in the scalar resource: the per-lane byte offsets are loop-invariant
+  // 32-bit values (the launcher checks the extents), so no address registers are rewritten each block — with
+  // 64-bit address registers the allocator reuses them while the loads are in flight and the MFMAs then wait for
+  // the prefetch.
+  const int ks2 = (int)A.ks[2], vs2 = (int)A.vs[2];
   auto gload = [&](int j) {
     const int k0 = j * BKV;
+    const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc((void*)(Kg + (int64_t)k0 * ks2 * 2), (short)0, -1, 0x00020000);
+    const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc((void*)(Vg + (int64_t)k0 * vs2 * 2), (short)0, -1, 0x00020000);
 #pragma unroll
     for (int i = 0; i < KVEC; ++i) {
       int v = tid + i * 256;
       int row = v / (D / 8), c = v % (D / 8);
-      kreg[i] = *(const u32x4a*)(Kg + ((int64_t)(k0 + row) * A.ks[2] + c * 8) * 2);
+      kreg[i] = __builtin_amdgcn_raw_buffer_load_b128(kr, (row * ks2 + c * 8) * 2, 0, 0);
     }
     if (tid < VBLK) {
       int kb = tid % (BKV / 8), dv = tid / (BKV / 8);  // lanes spread over k-blocks: conflict-free LDS stores
 #pragma unroll
-      for (int q = 0; q < 8; ++q) vreg[q] = *(const u32x4a*)(Vg + ((int64_t)(k0 + kb * 8 + q) * A.vs[2] + dv * 8) * 2);
+      for (int q = 0; q < 8; ++q) vreg[q] = __builtin_amdgcn_raw_buffer_load_b128(vr, ((kb * 8 + q) * vs2 + dv * 8) * 2, 0, 0);
     }
   };
   auto lstore = [&](int buf) {
@@ -252,6 +262,9 @@ void launch_attention(const AttnArgs& a, hipStream_t stream) {
   if (!(a.out_dtype == DT_BF16 || a.out_dtype == DT_F32)) fail(PJRT_Error_Code_UNIMPLEMENTED, "attention output type");
   if (((uintptr_t)a.q | (uintptr_t)a.k | (uintptr_t)a.v | (uintptr_t)a.o) & 15)
     fail(PJRT_Error_Code_UNIMPLEMENTED, "attention operands must be 16-byte aligned");
+  // K / V blocks are read through 32-bit byte offsets from the block origin
+  if (a.ks[2] > (1 << 20) || a.vs[2] > (1 << 20))
+    fail(PJRT_Error_Code_UNIMPLEMENTED, "attention key/value row stride too large");
   int64_t blocks = (int64_t)a.B * a.H * (a.Sq / BQ);
   if (blocks == 0) return;
   hipError_t e;
