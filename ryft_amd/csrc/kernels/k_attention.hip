@@ -6,7 +6,7 @@
 // query and split its keys): the running max / sum of the online softmax then need no cross-lane reductions except
 // one swap between the two half-waves, and the rescaling of the output Oᵀ = Vᵀ·Pᵀ is a per-lane multiply. P never
 // leaves registers: the Sᵀ accumulator, rounded to bf16, is directly the B operand of the P·V MFMA, with the
-// matching key order obtained by reading Vᵀ from LDS in the same permuted order. Row maxima are taken on the raw
+// matching key order obtained by storing Vᵀ in LDS in that permuted order. Row maxima are taken on the raw
 // scores and each probability costs one FMA and one v_exp_f32 (2^x). Two workgroups share a CU (≤ 256 registers
 // per lane), so one wave's softmax overlaps another's MFMAs. The [S, S] score matrix is never materialised.
 #include <hip/hip_runtime.h>
@@ -139,8 +139,15 @@ __global__ void __launch_bounds__(256, 2) attention_fwd_kernel(const AttnArgs A)
         lo.y = __builtin_amdgcn_perm(w[3][t], w[2][t], 0x05040100u); hi.y = __builtin_amdgcn_perm(w[3][t], w[2][t], 0x07060302u);
         lo.z = __builtin_amdgcn_perm(w[5][t], w[4][t], 0x05040100u); hi.z = __builtin_amdgcn_perm(w[5][t], w[4][t], 0x07060302u);
         lo.w = __builtin_amdgcn_perm(w[7][t], w[6][t], 0x05040100u); hi.w = __builtin_amdgcn_perm(w[7][t], w[6][t], 0x07060302u);
-        *(u32x4a*)(sV + (dv * 8 + 2 * t) * C::VP + kb * 16) = lo;
-        *(u32x4a*)(sV + (dv * 8 + 2 * t + 1) * C::VP + kb * 16) = hi;
+        // Within each 16-key group, key 8a + 4h + i is stored at position 8h + 4a + i, so that the 8 keys one lane
+        // multiplies in a k-step (h = lane / 32: keys 4h..4h+3 and 8+4h..8+4h+3) are contiguous: the P·V loop then
+        // reads them with one conflict-free 16-byte read. This lane's 8 keys are group kb / 2, a = kb % 2.
+        char* r0 = sV + (dv * 8 + 2 * t) * C::VP + (kb >> 1) * 32 + (kb & 1) * 8;
+        char* r1 = r0 + C::VP;
+        *(uint2*)r0 = uint2{lo.x, lo.y};
+        *(uint2*)(r0 + 16) = uint2{lo.z, lo.w};
+        *(uint2*)r1 = uint2{hi.x, hi.y};
+        *(uint2*)(r1 + 16) = uint2{hi.z, hi.w};
       }
     }
   };
@@ -213,10 +220,7 @@ __global__ void __launch_bounds__(256, 2) attention_fwd_kernel(const AttnArgs A)
     for (int s = 0; s < BKV / 16; ++s) {
 #pragma unroll
       for (int dt = 0; dt < D / 32; ++dt) {
-        const char* row = sV + (dt * 32 + (lane & 31)) * C::VP + (s * 16 + 4 * half) * 2;
-        uint2 lo = *(const uint2*)row;
-        uint2 hi = *(const uint2*)(row + 16);
-        u32x4a vf = u32x4a{lo.x, lo.y, hi.x, hi.y};
+        const u32x4a vf = *(const u32x4a*)(sV + (dt * 32 + (lane & 31)) * C::VP + (s * 16 + 8 * half) * 2);
         o[dt] = mma_bf16(vf, pf[s], o[dt]);
       }
     }
