@@ -23,12 +23,15 @@ __device__ __forceinline__ bool dt_is_float(int t) {
 }
 
 // ---- bit-exact conversions (round to nearest even; f8E4M3FN overflow → NaN, f8E5M2 overflow → inf)
-__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+// f32 → bf16 with v_cvt_pk_bf16_f32: round to nearest even, and a NaN keeps its sign and high payload bits with the
+// quiet bit set ((bits >> 16) | 0x40) — the same bits as the integer formulation, checked over 2^20 random and
+// special patterns on gfx950.
+typedef __bf16 ew_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float ew_f32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2_bits(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(ew_f32x2{lo, hi}, ew_bf16x2));
 }
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) { return (uint16_t)f32x2_to_bf16x2_bits(f, 0.0f); }
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
 __device__ __forceinline__ uint8_t f32_to_e4m3fn_bits(float f) {

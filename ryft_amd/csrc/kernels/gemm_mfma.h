@@ -4,12 +4,11 @@
 //
 // MFMA path: one workgroup computes a BM×BN tile of C[b] = A[b]·B[b]ᵀ (B addressed as [n, k]); WM×WN wavefronts
 // each own a (BM/WM)×(BN/WN) sub-tile made of 32×32 MFMA tiles. Operand tiles are staged through LDS in a
-// K-packed layout (each row holds BK consecutive k of one m or n) in two LDS stages, fed from two register stages
-// of buffer loads, so that k-tiles t+1 and t+2 are in flight while the MFMAs of k-tile t run; LDS fragments are
-// double-buffered in registers across k-steps and across the one barrier per k-tile. Operands whose contiguous
-// dimension is m / n (row-major
-// [K, N] weights, for example) are transposed in registers with v_perm_b32 on their way into LDS, so no separate
-// transpose pass over HBM is needed. Workgroups are mapped onto the 8 XCDs so that the tiles one XCD computes
+// K-packed layout (each row holds BK consecutive k of one m or n) in two LDS stages, fed by buffer loads one k-tile
+// ahead (tile t+2 is requested while tile t multiplies); LDS fragments are double-buffered in registers across
+// k-steps and across the one barrier per k-tile. Operands whose contiguous dimension is m / n (row-major [K, N]
+// weights, for example) are transposed in registers with v_perm_b32 on their way into LDS, so no separate transpose
+// pass over HBM is needed. Workgroups are mapped onto the 8 XCDs so that the tiles one XCD computes
 // share A row-panels and B column-panels in that XCD's L2.
 //
 // Instruction per compute type (all dense, f32 or i32 accumulation):
@@ -334,6 +333,10 @@ __device__ __forceinline__ void epi_pass(const GemmArgs& G, void* out, int b, in
     for (int q = 0; q < 4; ++q) {
       if constexpr (OS == 4) {
         w[q] = out_bits<DT>(v[q], is_float);
+      } else if constexpr (OS == 2 && DT == DT_BF16) {
+        const float a = is_float ? __uint_as_float(v[2 * q]) : (float)(int32_t)v[2 * q];
+        const float c = is_float ? __uint_as_float(v[2 * q + 1]) : (float)(int32_t)v[2 * q + 1];
+        w[q] = f32x2_to_bf16x2_bits(a, c);
       } else if constexpr (OS == 2) {
         w[q] = out_bits<DT>(v[2 * q], is_float) | (out_bits<DT>(v[2 * q + 1], is_float) << 16);
       } else {

@@ -53,7 +53,7 @@ __device__ __forceinline__ void store_vec(void* out, int64_t lin, int dtype, con
       for (int q = 0; q < 4; ++q) {
         const float a = is_float ? __uint_as_float(v[2 * q]) : (float)(int32_t)v[2 * q];
         const float b = is_float ? __uint_as_float(v[2 * q + 1]) : (float)(int32_t)v[2 * q + 1];
-        if (dtype == DT_BF16) w[q] = (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
+        if (dtype == DT_BF16) w[q] = f32x2_to_bf16x2_bits(a, b);
         else w[q] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)a) | ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)b) << 16);
       }
       *(u32x4v*)(p + lin * 2) = u32x4v{w[0], w[1], w[2], w[3]};

@@ -1,20 +1,7 @@
-// GEMM kernels for gfx950.
-//
-// MFMA path: one workgroup computes a BM×BN tile of C[b] = A[b]·B[b]ᵀ (B addressed as [n, k]); WM×WN wavefronts
-// each own a (BM/WM)×(BN/WN) sub-tile made of 32×32 MFMA tiles. Operand tiles are staged through LDS in a
-// K-packed layout (each row holds BK consecutive k of one m or n), double-buffered so that the global loads of
-// k-tile t+1 are in flight while the MFMAs of k-tile t run. Operands whose contiguous dimension is m / n (row-major
-// [K, N] weights, for example) are transposed in registers with v_perm_b32 on their way into LDS, so no separate
-// transpose pass over HBM is needed. Workgroups are mapped onto the 8 XCDs so that the tiles one XCD computes
-// share A row-panels and B column-panels in that XCD's L2.
-//
-// Instruction per compute type (all dense, f32 or i32 accumulation):
-//   bf16  v_mfma_f32_32x32x16_bf16      f16  v_mfma_f32_32x32x16_f16
-//   i8    v_mfma_i32_32x32x32_i8        fp8  v_mfma_f32_32x32x64_f8f6f4 (e4m3 × e4m3, unit scales)
-//   f32   v_mfma_f32_32x32x2_f32
-//
-// Generic path: a 64×64 LDS-tiled FMA kernel that reads any element type through any strides (bounds-checked); it
-// serves shapes and type mixes the MFMA instantiations do not cover.
+// GEMM dispatch for gfx950: picks an MFMA instantiation (gemm_mfma.h, one translation unit per operand type) when
+// the operand types, layouts, alignments, epilogue and output types fit one, and otherwise runs the generic path —
+// a 64×64 LDS-tiled FMA kernel that reads any element type through any strides (bounds-checked), used for shapes
+// and type mixes the MFMA instantiations do not cover.
 #include <hip/hip_runtime.h>
 
 #include <string>
