@@ -34,20 +34,13 @@ __device__ __forceinline__ uint32_t f32x2_to_bf16x2_bits(float lo, float hi) {
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) { return (uint16_t)f32x2_to_bf16x2_bits(f, 0.0f); }
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
+// f32 → f8E4M3FN with v_cvt_pk_fp8_f32: round to nearest even, subnormals on the 2^-9 grid, |x| ≥ 464 → NaN — the
+// integer rule's bits on 2^20 random and special patterns on gfx950, except that the instruction writes every NaN
+// input as 0xff; a NaN input keeps its sign here (0x7f / 0xff).
 __device__ __forceinline__ uint8_t f32_to_e4m3fn_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  uint32_t sign = (u >> 24) & 0x80u;
-  uint32_t a = u & 0x7fffffffu;
-  if (a >= 0x7f800000u) return (uint8_t)(sign | 0x7fu);
-  uint32_t code;
-  if (a < 0x3c800000u) {  // |x| < 2^-6: subnormal grid of 2^-9
-    code = (uint32_t)rintf(__uint_as_float(a) * 512.0f);
-  } else {
-    uint32_t r = (a + 0x7ffffu + ((a >> 20) & 1u)) >> 20;
-    code = r - ((127u - 7u) << 3);
-    if (code > 0x7eu) code = 0x7fu;
-  }
-  return (uint8_t)(sign | code);
+  uint32_t code = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(f, 0.0f, 0, false) & 0xffu;
+  if (f != f) code = ((__float_as_uint(f) >> 24) & 0x80u) | 0x7fu;
+  return (uint8_t)code;
 }
 __device__ __forceinline__ float e4m3fn_bits_to_f32(uint32_t v) {
   uint32_t s = (v & 0x80u) << 24, e = (v >> 3) & 15u, m = v & 7u;
@@ -213,42 +206,53 @@ __device__ __forceinline__ void load_leaf(const EwLeaf& L, int64_t lin, const in
 #pragma unroll
       for (int e = 0; e < V; ++e) r[e] = x;
     } else if (L.vmode == EW_VEC_CONTIG) {
-      // V elements of ≤ 4 bytes, aligned to V·size (checked by the launcher)
-      static_assert(V == 8, "vector leaf loads are written for 8 elements");
+      // V elements of ≤ 4 bytes, aligned to V·size (checked by the launcher); read as 4-byte words
+      static_assert(V == 4 || V == 8, "vector leaf loads are written for 4 or 8 elements");
       const char* p = (const char*)L.ptr;
-      switch (L.dtype) {
-        case DT_F32: case DT_S32: case DT_U32: {
-          const u32x4v a = *(const u32x4v*)(p + off * 4), b = *(const u32x4v*)(p + off * 4 + 16);
-          r[0] = a.x, r[1] = a.y, r[2] = a.z, r[3] = a.w, r[4] = b.x, r[5] = b.y, r[6] = b.z, r[7] = b.w;
-          break;
+      const int es = L.dtype == DT_F32 || L.dtype == DT_S32 || L.dtype == DT_U32 ? 4
+                     : (L.dtype == DT_BF16 || L.dtype == DT_F16 || L.dtype == DT_S16 || L.dtype == DT_U16 ? 2 : 1);
+      uint32_t w[V];  // the first V·es/4 words hold the elements
+      if (es == 4) {
+        const u32x4v a = *(const u32x4v*)(p + off * 4);
+        w[0] = a.x, w[1] = a.y, w[2] = a.z, w[3] = a.w;
+        if constexpr (V == 8) {
+          const u32x4v b = *(const u32x4v*)(p + off * 4 + 16);
+          w[4] = b.x, w[5] = b.y, w[6] = b.z, w[7] = b.w;
         }
-        case DT_BF16: case DT_F16: case DT_S16: case DT_U16: {
+      } else if (es == 2) {
+        if constexpr (V == 8) {
           const u32x4v a = *(const u32x4v*)(p + off * 2);
-          const uint32_t w[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const uint32_t lo = w[q] & 0xffffu, hi = w[q] >> 16;
-            if (L.dtype == DT_BF16) r[2 * q] = lo << 16, r[2 * q + 1] = hi << 16;
-            else if (L.dtype == DT_F16) r[2 * q] = __float_as_uint((float)__builtin_bit_cast(_Float16, (uint16_t)lo)),
-                                        r[2 * q + 1] = __float_as_uint((float)__builtin_bit_cast(_Float16, (uint16_t)hi));
-            else if (L.dtype == DT_S16) r[2 * q] = (uint32_t)(int32_t)(int16_t)lo, r[2 * q + 1] = (uint32_t)(int32_t)(int16_t)hi;
-            else r[2 * q] = lo, r[2 * q + 1] = hi;
-          }
-          break;
+          w[0] = a.x, w[1] = a.y, w[2] = a.z, w[3] = a.w;
+        } else {
+          const u32x2v a = *(const u32x2v*)(p + off * 2);
+          w[0] = a.x, w[1] = a.y;
         }
-        default: {  // 1-byte types
+      } else {
+        if constexpr (V == 8) {
           const u32x2v a = *(const u32x2v*)(p + off);
+          w[0] = a.x, w[1] = a.y;
+        } else {
+          w[0] = *(const uint32_t*)(p + off);
+        }
+      }
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const uint32_t byte = ((e < 4 ? a.x : a.y) >> (8 * (e & 3))) & 0xffu;
-            switch (L.dtype) {
-              case DT_F8E4M3FN: r[e] = __float_as_uint(e4m3fn_bits_to_f32(byte)); break;
-              case DT_F8E5M2: r[e] = __float_as_uint(e5m2_bits_to_f32(byte)); break;
-              case DT_S8: r[e] = (uint32_t)(int32_t)(int8_t)byte; break;
-              default: r[e] = byte; break;
-            }
+      for (int e = 0; e < V; ++e) {
+        if (es == 4) {
+          r[e] = w[e];
+        } else if (es == 2) {
+          const uint32_t h = (w[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+          if (L.dtype == DT_BF16) r[e] = h << 16;
+          else if (L.dtype == DT_F16) r[e] = __float_as_uint((float)__builtin_bit_cast(_Float16, (uint16_t)h));
+          else if (L.dtype == DT_S16) r[e] = (uint32_t)(int32_t)(int16_t)h;
+          else r[e] = h;
+        } else {
+          const uint32_t byte = (w[e >> 2] >> (8 * (e & 3))) & 0xffu;
+          switch (L.dtype) {
+            case DT_F8E4M3FN: r[e] = __float_as_uint(e4m3fn_bits_to_f32(byte)); break;
+            case DT_F8E5M2: r[e] = __float_as_uint(e5m2_bits_to_f32(byte)); break;
+            case DT_S8: r[e] = (uint32_t)(int32_t)(int8_t)byte; break;
+            default: r[e] = byte; break;
           }
-          break;
         }
       }
     } else {
@@ -258,34 +262,85 @@ __device__ __forceinline__ void load_leaf(const EwLeaf& L, int64_t lin, const in
   }
 }
 
-// The VM's registers for V elements per thread. At V = 1 the array is promoted to VGPRs (uniform indirect moves);
-// at V = 8 the compiler keeps it in private memory (L1-resident), which the 8-wide evaluation amortises.
-template <int V>
-struct RegFile {
-  uint32_t v[EW_MAX_REGS][V];
-  __device__ __forceinline__ uint32_t get(int r, int e) const { return v[r][e]; }
-  __device__ __forceinline__ void set(int r, int e, uint32_t x) { v[r][e] = x; }
+// Register files of the VM. Operands are moved as whole rows of V elements.
+//  * RegFile1: one element per thread in a VGPR array (indexed with the uniform register number: indirect moves).
+//  * SwitchRegFile<V>: V elements per thread in twelve named VGPR rows picked by a uniform switch (a V-wide array
+//    indexed with the register number would be placed in private memory, turning every operand into a scratch
+//    round trip).
+struct RegFile1 {
+  uint32_t v[EW_MAX_REGS];
+  __device__ __forceinline__ void load(int r, uint32_t* out) const { out[0] = v[r]; }
+  __device__ __forceinline__ void store(int r, const uint32_t* in) { v[r] = in[0]; }
+  __device__ __forceinline__ uint32_t get(int r) const { return v[r]; }
 };
+
+template <int V>
+struct SwitchRegFile {
+  // twelve named rows held as vector values and selected by a uniform switch: the merged switch arms become phis of
+  // values, which stay in VGPRs (rows kept as arrays would be merged into a phi of pointers and spilled to private
+  // memory)
+  static_assert(EW_MAX_REGS == 12, "SwitchRegFile names twelve registers");
+  typedef uint32_t row_t __attribute__((ext_vector_type(V)));
+  row_t r0, r1, r2, r3, r4, r5, r6, r7, r8, r9, r10, r11;
+#define RF_ROWS(X) X(0) X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8) X(9) X(10) X(11)
+  __device__ __forceinline__ void load(int r, uint32_t* out) const {
+    row_t v = r0;
+    switch (r) {
+#define RF_LOAD(i) case i: v = r##i; break;
+      RF_ROWS(RF_LOAD)
+#undef RF_LOAD
+      default: break;
+    }
+#pragma unroll
+    for (int e = 0; e < V; ++e) out[e] = v[e];
+  }
+  __device__ __forceinline__ void store(int r, const uint32_t* in) {
+    row_t v;
+#pragma unroll
+    for (int e = 0; e < V; ++e) v[e] = in[e];
+    switch (r) {
+#define RF_STORE(i) case i: r##i = v; break;
+      RF_ROWS(RF_STORE)
+#undef RF_STORE
+      default: break;
+    }
+  }
+#undef RF_ROWS
+};
+
+// Number of register operands an instruction reads.
+__device__ __forceinline__ int ew_nsrc(int op) {
+  if (op == EW_LOAD || op == EW_CONST || op == EW_IOTA || op == EW_ACC) return 0;
+  if (op == EW_SELECT || op == EW_FCLAMP || op == EW_ICLAMP) return 3;
+  if (op >= EW_ADD) return 2;
+  return 1;
+}
 
 // Runs the program on V consecutive elements of the innermost dimension (linear indices lin .. lin+V-1, all in one
 // innermost row; `coord` are the coordinates of `lin`). `acc` holds the GEMM accumulators (bits) for EW_ACC (V = 1
-// only). Results land in R (register, element). The instruction dispatch is uniform across the wave, so its cost
-// is paid once per V elements.
-template <int V>
+// only). Results land in the register file R. The instruction dispatch is uniform across the wave, so its cost is
+// paid once per V elements.
+template <int V, typename RF>
 __device__ __forceinline__ void ew_run_v(const EwProgram& P, int64_t lin, const int32_t* coord, const uint32_t* acc,
-                                         RegFile<V>& R) {
+                                         RF& R) {
 #define EW_FOR _Pragma("unroll") for (int e = 0; e < V; ++e)
-#define EW_FA __uint_as_float(R.get(I.a, e))
-#define EW_FB __uint_as_float(R.get(I.b, e))
-#define EW_IA ((int32_t)R.get(I.a, e))
-#define EW_IB ((int32_t)R.get(I.b, e))
-#define EW_UA (R.get(I.a, e))
-#define EW_UB (R.get(I.b, e))
+#define EW_FA __uint_as_float(ra[e])
+#define EW_FB __uint_as_float(rb[e])
+#define EW_IA ((int32_t)ra[e])
+#define EW_IB ((int32_t)rb[e])
+#define EW_UA (ra[e])
+#define EW_UB (rb[e])
 #define EW_F(OP, EXPR) case OP: EW_FOR r[e] = __float_as_uint(EXPR); break;
 #define EW_U(OP, EXPR) case OP: EW_FOR r[e] = (uint32_t)(EXPR); break;
+  EwInstr next = P.instr[0];
   for (int pc = 0; pc < P.n_instr; ++pc) {
-    const EwInstr I = P.instr[pc];
-    uint32_t r[V];
+    const EwInstr I = next;
+    if (pc + 1 < P.n_instr) next = P.instr[pc + 1];  // requested while this instruction executes
+    uint32_t r[V], ra[V], rb[V], rc[V];
+    const int nsrc = ew_nsrc(I.op);
+    if (nsrc >= 1) R.load(I.a, ra);
+    if (nsrc >= 2) R.load(I.b, rb);
+    if (nsrc >= 3) R.load(I.c, rc);
     switch (I.op) {
       case EW_LOAD: load_leaf<V>(P.leaves[I.a], lin, coord, P.rank, r); break;
       EW_U(EW_CONST, I.imm.u)
@@ -339,9 +394,9 @@ __device__ __forceinline__ void ew_run_v(const EwProgram& P, int64_t lin, const 
       EW_U(EW_FCMP, cmp_f(EW_FA, EW_FB, I.imm.i))
       EW_U(EW_ICMP, cmp_i<int32_t>(EW_IA, EW_IB, I.imm.i))
       EW_U(EW_UCMP, cmp_i<uint32_t>(EW_UA, EW_UB, I.imm.i))
-      EW_U(EW_SELECT, EW_UA ? EW_UB : R.get(I.c, e))
-      EW_F(EW_FCLAMP, fminf(fmaxf(EW_FB, EW_FA), __uint_as_float(R.get(I.c, e))))
-      EW_U(EW_ICLAMP, EW_IB < EW_IA ? EW_IA : (EW_IB > (int32_t)R.get(I.c, e) ? (int32_t)R.get(I.c, e) : EW_IB))
+      EW_U(EW_SELECT, EW_UA ? EW_UB : rc[e])
+      EW_F(EW_FCLAMP, fminf(fmaxf(EW_FB, EW_FA), __uint_as_float(rc[e])))
+      EW_U(EW_ICLAMP, EW_IB < EW_IA ? EW_IA : (EW_IB > (int32_t)rc[e] ? (int32_t)rc[e] : EW_IB))
       default: EW_FOR r[e] = 0; break;
     }
     // per-op rounding to the StableHLO result element type
@@ -352,7 +407,7 @@ __device__ __forceinline__ void ew_run_v(const EwProgram& P, int64_t lin, const 
         EW_FOR r[e] = (uint32_t)wrap_int((int32_t)r[e], I.round);
       }
     }
-    EW_FOR R.set(I.dst, e, r[e]);
+    R.store(I.dst, r);
   }
 #undef EW_FOR
 #undef EW_FA
@@ -367,7 +422,7 @@ __device__ __forceinline__ void ew_run_v(const EwProgram& P, int64_t lin, const 
 
 // Scalar form (one element): used by the generic GEMM epilogue and the unvectorised kernels.
 __device__ __forceinline__ void ew_run(const EwProgram& P, int64_t lin, const int32_t* coord, const uint32_t* acc,
-                                       RegFile<1>& R) {
+                                       RegFile1& R) {
   ew_run_v<1>(P, lin, coord, acc, R);
 }
 

@@ -57,9 +57,9 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& G, int b, int m, i
         }
       }
       uint32_t acc[2] = {raw, __float_as_uint(acc1)};
-      RegFile<1> R;
+      RegFile1 R;
       ew_run(P, lin, coord, acc, R);
-      store_bits(G.out_ptr[0], lin, P.out_dtype[0], R.get(P.out_reg[0], 0), (P.out_float_mask & 1) != 0);
+      store_bits(G.out_ptr[0], lin, P.out_dtype[0], R.get(P.out_reg[0]), (P.out_float_mask & 1) != 0);
       if (G.n_out > 1) store_bits(G.out_ptr[1], lin, G.out_dtype[1], raw, !INT_ACC);
       break;
     }

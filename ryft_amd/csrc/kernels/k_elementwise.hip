@@ -1,9 +1,10 @@
 // Elementwise programs and reductions (HBM-bound). Each thread evaluates the program's instruction list on VEC = 8
 // consecutive elements of the innermost dimension at once, so the (uniform) instruction dispatch is paid once per 8
-// elements and contiguous leaves / outputs move as 8- to 32-byte vectors; shapes whose innermost dimension is not a
-// multiple of 8 run the same program one element per thread. Reductions give each output row 256 threads (long
-// rows, e.g. RMSNorm's 4096) or one wavefront (shorter rows), combine within the thread, across lanes with
-// shuffles and across wavefronts through LDS; the init value enters once at the end.
+// elements and contiguous leaves / outputs move as 8- to 32-byte vectors; the program's registers stay in VGPRs.
+// Shapes whose innermost dimension is not a multiple of 8 run the same program one element per thread (registers in
+// VGPRs). Reductions give each output row a workgroup (long rows, e.g. RMSNorm's 4096) or one wavefront (shorter
+// rows), combine within the thread, across lanes with shuffles and across wavefronts through LDS; the init value
+// enters once at the end.
 #include <hip/hip_runtime.h>
 
 #include <string>
@@ -20,49 +21,50 @@ __global__ void __launch_bounds__(256) ew_kernel(const EwProgram P) {
   for (int64_t lin = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; lin < P.total; lin += stride) {
     int32_t coord[EW_MAX_RANK];
     if (COORDS) decompose(lin, P, coord);
-    RegFile<1> R;
+    RegFile1 R;
     ew_run(P, lin, coord, nullptr, R);
     for (int o = 0; o < P.n_out; ++o)
-      store_bits(P.out_ptr[o], lin, P.out_dtype[o], R.get(P.out_reg[o], 0), (P.out_float_mask >> o) & 1);
+      store_bits(P.out_ptr[o], lin, P.out_dtype[o], R.get(P.out_reg[o]), (P.out_float_mask >> o) & 1);
   }
 }
 
-constexpr int VEC = 8;
+constexpr int VEC = 8;    // elements per thread in the vectorised kernels
+constexpr int VNT = 256;  // threads per workgroup there
+using VRegs = SwitchRegFile<VEC>;
 
 // Stores V consecutive register values (float bits if `is_float`, else int32) as `dtype` at out[lin..lin+V).
 template <int V>
 __device__ __forceinline__ void store_vec(void* out, int64_t lin, int dtype, const uint32_t* v, bool is_float) {
-  static_assert(V == 8, "vector stores are written for 8 elements");
+  static_assert(V == 4 || V == 8, "vector stores are written for 4 or 8 elements");
   char* p = (char*)out;
   switch (dtype) {
-    case DT_F32: {
-      uint32_t w[8];
+    case DT_F32: case DT_S32: case DT_U32: {
+      uint32_t w[V];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) w[e] = is_float ? v[e] : __float_as_uint((float)(int32_t)v[e]);
+      for (int e = 0; e < V; ++e) w[e] = (dtype != DT_F32 || is_float) ? v[e] : __float_as_uint((float)(int32_t)v[e]);
       *(u32x4v*)(p + lin * 4) = u32x4v{w[0], w[1], w[2], w[3]};
-      *(u32x4v*)(p + lin * 4 + 16) = u32x4v{w[4], w[5], w[6], w[7]};
+      if constexpr (V == 8) *(u32x4v*)(p + lin * 4 + 16) = u32x4v{w[4], w[5], w[6], w[7]};
       break;
     }
-    case DT_S32: case DT_U32:
-      *(u32x4v*)(p + lin * 4) = u32x4v{v[0], v[1], v[2], v[3]};
-      *(u32x4v*)(p + lin * 4 + 16) = u32x4v{v[4], v[5], v[6], v[7]};
-      break;
     case DT_BF16: case DT_F16: {
-      uint32_t w[4];
+      uint32_t w[V / 2];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
+      for (int q = 0; q < V / 2; ++q) {
         const float a = is_float ? __uint_as_float(v[2 * q]) : (float)(int32_t)v[2 * q];
         const float b = is_float ? __uint_as_float(v[2 * q + 1]) : (float)(int32_t)v[2 * q + 1];
         if (dtype == DT_BF16) w[q] = f32x2_to_bf16x2_bits(a, b);
         else w[q] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)a) | ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)b) << 16);
       }
-      *(u32x4v*)(p + lin * 2) = u32x4v{w[0], w[1], w[2], w[3]};
+      if constexpr (V == 8) *(u32x4v*)(p + lin * 2) = u32x4v{w[0], w[1], w[2], w[3]};
+      else *(u32x2v*)(p + lin * 2) = u32x2v{w[0], w[1]};
       break;
     }
     case DT_F8E4M3FN: case DT_F8E5M2: case DT_S8: case DT_U8: case DT_PRED: {
-      uint32_t w[2] = {0u, 0u};
+      uint32_t w[V / 4];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
+      for (int q = 0; q < V / 4; ++q) w[q] = 0u;
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
         const float f = is_float ? __uint_as_float(v[e]) : (float)(int32_t)v[e];
         uint32_t byte;
         if (dtype == DT_F8E4M3FN) byte = f32_to_e4m3fn_bits(f);
@@ -71,12 +73,13 @@ __device__ __forceinline__ void store_vec(void* out, int64_t lin, int dtype, con
         else byte = is_float ? (uint32_t)f2i_sat(f, dtype) & 0xffu : v[e] & 0xffu;
         w[e >> 2] |= byte << (8 * (e & 3));
       }
-      *(u32x2v*)(p + lin) = u32x2v{w[0], w[1]};
+      if constexpr (V == 8) *(u32x2v*)(p + lin) = u32x2v{w[0], w[1]};
+      else *(uint32_t*)(p + lin) = w[0];
       break;
     }
     default:
 #pragma unroll
-      for (int e = 0; e < 8; ++e) store_bits(out, lin + e, dtype, v[e], is_float);
+      for (int e = 0; e < V; ++e) store_bits(out, lin + e, dtype, v[e], is_float);
       break;
   }
 }
@@ -96,19 +99,18 @@ __device__ __forceinline__ void decompose_fast(int64_t lin, const EwProgram& P, 
 }
 
 template <bool COORDS>
-__global__ void __launch_bounds__(256) ew_kernel_vec(const EwProgram P) {
+__global__ void __launch_bounds__(VNT) ew_kernel_vec(const EwProgram P) {
+  VRegs R;
   const int64_t chunks = P.total / VEC;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < chunks; c += stride) {
     const int64_t lin = c * VEC;
     int32_t coord[EW_MAX_RANK];
     if (COORDS) decompose_fast(lin, P, coord);
-    RegFile<VEC> R;
     ew_run_v<VEC>(P, lin, coord, nullptr, R);
     for (int o = 0; o < P.n_out; ++o) {
       uint32_t v[VEC];
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) v[e] = R.get(P.out_reg[o], e);
+      R.load(P.out_reg[o], v);
       store_vec<VEC>(P.out_ptr[o], lin, P.out_dtype[o], v, (P.out_float_mask >> o) & 1);
     }
   }
@@ -161,7 +163,7 @@ void launch_elementwise(const EwProgram& p, hipStream_t stream) {
   if (p.total == 0) return;
   EwProgram v = p;
   if (prepare_vec(v, true)) {
-    dim3 grid(grid_for(v.total / VEC, 256)), block(256);
+    dim3 grid(grid_for(v.total / VEC, VNT)), block(VNT);
     if (v.needs_coords) hipLaunchKernelGGL(ew_kernel_vec<true>, grid, block, 0, stream, v);
     else hipLaunchKernelGGL(ew_kernel_vec<false>, grid, block, 0, stream, v);
   } else {
@@ -219,9 +221,9 @@ __global__ void __launch_bounds__(256) reduce_kernel(const ReduceArgs A) {
       int64_t lin = o * A.inner + r;
       int32_t coord[EW_MAX_RANK];
       if (COORDS) decompose(lin, P, coord);
-      RegFile<1> R;
+      RegFile1 R;
       ew_run(P, lin, coord, nullptr, R);
-      acc = red_combine(acc, R.get(P.out_reg[0], 0), A.kind, fl);
+      acc = red_combine(acc, R.get(P.out_reg[0]), A.kind, fl);
     }
     for (int off = 32; off > 0; off >>= 1) {
       uint32_t other = (uint32_t)__shfl_xor((int)acc, off, 64);
@@ -241,17 +243,18 @@ __device__ __forceinline__ uint32_t red_identity(int kind, bool fl) {
   }
 }
 
-// G threads per output row (256: one workgroup, 64: one wavefront); each thread folds VEC-element chunks.
+// G threads per output row (VNT: one workgroup, 64: one wavefront); each thread folds VEC-element chunks.
 template <int G, bool COORDS>
-__global__ void __launch_bounds__(256) reduce_kernel_vec(const ReduceArgs A) {
+__global__ void __launch_bounds__(VNT) reduce_kernel_vec(const ReduceArgs A) {
+  __shared__ uint32_t part[VNT / 64];
+  VRegs R;
   const EwProgram& P = A.prologue;
-  constexpr int RB = 256 / G;  // rows per workgroup
+  constexpr int RB = VNT / G;  // rows per workgroup
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = threadIdx.x / G, t = threadIdx.x % G;
   const bool fl = A.is_float != 0;
   const uint32_t init = A.init_ptr ? load_bits(A.init_ptr, 0, A.init_dtype) : (uint32_t)A.init.i;
   const uint32_t ident = red_identity(A.kind, fl);
-  __shared__ uint32_t part[4];
   const int64_t chunks = A.inner / VEC;
   for (int64_t o = (int64_t)blockIdx.x * RB + g; o < A.outer; o += (int64_t)gridDim.x * RB) {
     uint32_t acc = ident;
@@ -259,18 +262,19 @@ __global__ void __launch_bounds__(256) reduce_kernel_vec(const ReduceArgs A) {
       const int64_t lin = o * A.inner + c * VEC;
       int32_t coord[EW_MAX_RANK];
       if (COORDS) decompose_fast(lin, P, coord);
-      RegFile<VEC> R;
       ew_run_v<VEC>(P, lin, coord, nullptr, R);
+      uint32_t v[VEC];
+      R.load(P.out_reg[0], v);
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) acc = red_combine(acc, R.get(P.out_reg[0], e), A.kind, fl);
+      for (int e = 0; e < VEC; ++e) acc = red_combine(acc, v[e], A.kind, fl);
     }
     for (int off = 32; off > 0; off >>= 1) acc = red_combine(acc, (uint32_t)__shfl_xor((int)acc, off, 64), A.kind, fl);
-    if constexpr (G == 256) {
+    if constexpr (G == VNT) {
       if (lane == 0) part[wave] = acc;
       __syncthreads();
       if (threadIdx.x == 0) {
         uint32_t r = part[0];
-        for (int w = 1; w < 4; ++w) r = red_combine(r, part[w], A.kind, fl);
+        for (int w = 1; w < VNT / 64; ++w) r = red_combine(r, part[w], A.kind, fl);
         store_bits(P.out_ptr[0], o, P.out_dtype[0], red_combine(r, init, A.kind, fl), fl);
       }
       __syncthreads();  // part[] is reused by the next row
@@ -285,14 +289,14 @@ void launch_reduce(const ReduceArgs& a, hipStream_t stream) {
   ReduceArgs v = a;
   if (a.inner % VEC == 0 && prepare_vec(v.prologue, false)) {
     const bool coords = v.prologue.needs_coords != 0;
-    if (a.inner / VEC >= 128) {  // long rows: a workgroup per row
-      dim3 grid((unsigned)(a.outer < 256 * 8 ? a.outer : 256 * 8)), block(256);
-      if (coords) hipLaunchKernelGGL((reduce_kernel_vec<256, true>), grid, block, 0, stream, v);
-      else hipLaunchKernelGGL((reduce_kernel_vec<256, false>), grid, block, 0, stream, v);
+    if (a.inner / VEC >= 2 * VNT) {  // long rows: a workgroup per row
+      dim3 grid((unsigned)(a.outer < 256 * 16 ? a.outer : 256 * 16)), block(VNT);
+      if (coords) hipLaunchKernelGGL((reduce_kernel_vec<VNT, true>), grid, block, 0, stream, v);
+      else hipLaunchKernelGGL((reduce_kernel_vec<VNT, false>), grid, block, 0, stream, v);
     } else {  // a wavefront per row
-      int64_t blocks = (a.outer + 3) / 4;
+      int64_t blocks = (a.outer + VNT / 64 - 1) / (VNT / 64);
       if (blocks > 256 * 16) blocks = 256 * 16;
-      dim3 grid((unsigned)blocks), block(256);
+      dim3 grid((unsigned)blocks), block(VNT);
       if (coords) hipLaunchKernelGGL((reduce_kernel_vec<64, true>), grid, block, 0, stream, v);
       else hipLaunchKernelGGL((reduce_kernel_vec<64, false>), grid, block, 0, stream, v);
     }
