@@ -201,6 +201,45 @@ struct TileLoader {
   }
 };
 
+// One row-contiguous operand tile (BK k-rows × R elements) global → registers → LDS, copied unchanged ([k][R] rows
+// of LDB bytes), read later with transposing LDS reads.
+template <int ESIZE, int R, int BK, int THREADS>
+struct TileCopyLoader {
+  static constexpr int VE = 16 / ESIZE;
+  static constexpr int NTOT = BK * (R / VE);
+  static constexpr int NVEC = NTOT / THREADS;
+  static_assert(NTOT % THREADS == 0, "uneven tile split");
+  u32x4 regs[NVEC];
+  __device__ __forceinline__ void load(const char* base, int64_t sr, int64_t sk, int tid) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, -1, 0x00020000);
+    (void)sr;  // row-contiguous: the element stride along R is 1
+#pragma unroll
+    for (int i = 0; i < NVEC; ++i) {
+      const int v = tid + i * THREADS;
+      const int k = v / (R / VE), c = v % (R / VE);
+      regs[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(((int64_t)k * sk + (int64_t)c * VE) * ESIZE), 0, 0);
+    }
+  }
+  template <int LDB>
+  __device__ __forceinline__ void store(char* lds, int tid) {
+#pragma unroll
+    for (int i = 0; i < NVEC; ++i) {
+      const int v = tid + i * THREADS;
+      const int k = v / (R / VE), c = v % (R / VE);
+      *(u32x4*)(lds + k * LDB + c * 16) = regs[i];
+    }
+  }
+};
+
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+// ds_read_b64_tr_b16. Within each group of 16 lanes, lane i receives element i % 4 of the 8-byte chunks addressed by
+// lanes i/4, i/4 + 4, i/4 + 8, i/4 + 12 of the group (lane layout measured on gfx950). So when lane s of a group
+// addresses row k0 + s/4, column c0 + 4·(s % 4) of a [k][n] tile, lane i receives B[k0 .. k0+3][c0 + i].
+__device__ __forceinline__ uint2 lds_read_tr16(const char* p) {
+  const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4_t*)p);
+  return __builtin_bit_cast(uint2, v);
+}
+
 template <int KIND, int BM, int BN, int BK, int WM, int WN, bool A_R, bool B_R, bool DUAL>
 struct MfmaCfg {
   using M = Mma<KIND>;
@@ -209,7 +248,13 @@ struct MfmaCfg {
   static constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
   static constexpr int LDK = BK * ESIZE + 16;  // LDS row pitch in bytes (16-byte pad)
   static constexpr int NB = DUAL ? 2 : 1;
-  static constexpr int STAGE = (BM + NB * BN) * LDK;
+  // BTR: an n-contiguous 16-bit B operand is copied into LDS unchanged, [k][n] rows of pitch LDB (≡ 64 bytes mod 256
+  // so the 8 rows one transposing read touches fall in distinct banks), and its fragments are read with
+  // ds_read_b64_tr_b16; otherwise B is K-packed like A ([n][k] rows of pitch LDK, transposed in registers on the way)
+  static constexpr bool BTR = B_R && ESIZE == 2;
+  static constexpr int LDB = BN * ESIZE + 64;
+  static constexpr int BREG = BTR ? BK * LDB : BN * LDK;  // bytes of one B operand tile
+  static constexpr int STAGE = BM * LDK + NB * BREG;
   static constexpr int LDS_BYTES = 2 * STAGE;
   static_assert(BK % MK == 0, "BK must be a multiple of the MFMA K");
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32");
@@ -434,9 +479,10 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_mfma_kernel(const GemmArgs 
 
   // One register stage of global prefetch: tile kt + 2 is requested at the start of k-tile kt (right after tile
   // kt + 1 went from registers to LDS), so each load has a whole k-tile of MFMA work to arrive in. Two LDS stages.
+  using BLoader = std::conditional_t<C::BTR, TileCopyLoader<ES, BN, BK, C::THREADS>, TileLoader<ES, BN, BK, C::THREADS, B_R>>;
   TileLoader<ES, BM, BK, C::THREADS, A_R> la;
-  TileLoader<ES, BN, BK, C::THREADS, B_R> lb;
-  TileLoader<ES, BN, BK, C::THREADS, B_R> lb2;
+  BLoader lb;
+  BLoader lb2;
 
   Acc acc[C::TM][C::TN];
   Acc acc2[DUAL ? C::TM : 1][DUAL ? C::TN : 1];
@@ -458,8 +504,9 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_mfma_kernel(const GemmArgs 
   auto lstore = [&](int buf) {
     char* s = smem + buf * C::STAGE;
     la.template store<C::LDK>(s, tid);
-    lb.template store<C::LDK>(s + BM * C::LDK, tid);
-    if constexpr (DUAL) lb2.template store<C::LDK>(s + (BM + BN) * C::LDK, tid);
+    constexpr int BP = C::BTR ? C::LDB : C::LDK;
+    lb.template store<BP>(s + BM * C::LDK, tid);
+    if constexpr (DUAL) lb2.template store<BP>(s + BM * C::LDK + C::BREG, tid);
   };
 
   // Fragments of MFMA k-step s live in register slot s & 1: step s + 1 is read from LDS while step s multiplies.
@@ -469,17 +516,33 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_mfma_kernel(const GemmArgs 
   const int lrow = lane & 31;
   const int lk = (lane >> 5) * C::KPACK * ES;  // byte offset of this lane's k-pack within an MFMA k-step
   const int a_off = (wm * C::WTM + lrow) * C::LDK + lk;
-  const int b_off = BM * C::LDK + (wn * C::WTN + lrow) * C::LDK + lk;
+  // K-packed B: row n, k-pack of this lane. Transposed-read B: lane s of each 16-lane group addresses k-row
+  // 8·(lane/32) + s/4 and column 16·((lane/16) % 2) + 4·(s % 4), so the pair of reads (k-rows +0 and +4) delivers
+  // B[8·(lane/32) .. +7][lane % 32] — the MFMA operand fragment.
+  const int b_off = C::BTR ? BM * C::LDK + (8 * (lane >> 5) + ((lane & 15) >> 2)) * C::LDB +
+                                 (wn * C::WTN + 16 * ((lane >> 4) & 1) + 4 * (lane & 3)) * ES
+                           : BM * C::LDK + (wn * C::WTN + lrow) * C::LDK + lk;
+  auto bfrag = [&](const char* p) -> typename F::T {
+    if constexpr (C::BTR) {
+      const uint2 lo = lds_read_tr16(p), hi = lds_read_tr16(p + 4 * C::LDB);
+      return u32x4{lo.x, lo.y, hi.x, hi.y};
+    } else {
+      return F::load(p);
+    }
+  };
   auto lfrag = [&](int buf, auto s, auto slot) {
     constexpr int SL = decltype(slot)::value;
     constexpr int ko = decltype(s)::value * C::MK * ES;
+    // B fragment j / k-step offset: K-packed rows are n (32 per tile) with k along the row; transposed rows are k
+    constexpr int bko = C::BTR ? decltype(s)::value * C::MK * C::LDB : ko;
+    constexpr int bjo = C::BTR ? 32 * ES : 32 * C::LDK;
     const char* st = smem + buf * C::STAGE;
 #pragma unroll
     for (int i = 0; i < C::TM; ++i) fa[SL][i] = F::load(st + a_off + i * 32 * C::LDK + ko);
 #pragma unroll
     for (int j = 0; j < C::TN; ++j) {
-      fb[SL][j] = F::load(st + b_off + j * 32 * C::LDK + ko);
-      if constexpr (DUAL) fb2[SL][j] = F::load(st + b_off + BN * C::LDK + j * 32 * C::LDK + ko);
+      fb[SL][j] = bfrag(st + b_off + j * bjo + bko);
+      if constexpr (DUAL) fb2[SL][j] = bfrag(st + b_off + C::BREG + j * bjo + bko);
     }
   };
 
