@@ -239,6 +239,14 @@ __device__ __forceinline__ uint2 lds_read_tr16(const char* p) {
   const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4_t*)p);
   return __builtin_bit_cast(uint2, v);
 }
+typedef int i32x2_t __attribute__((ext_vector_type(2)));
+// ds_read_b64_tr_b8. Within each group of 16 lanes, lane i receives byte i % 8 of the 8-byte chunks addressed by
+// lanes 2j + i/8 (j = 0..7) of the group (measured on gfx950). So when lane s of a group addresses row k0 + s/2,
+// column c0 + 8·(s % 2) of a [k][n] byte tile, lane i receives B[k0 .. k0+7][c0 + i].
+__device__ __forceinline__ uint2 lds_read_tr8(const char* p) {
+  const i32x2_t v = __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) i32x2_t*)p);
+  return __builtin_bit_cast(uint2, v);
+}
 
 template <int KIND, int BM, int BN, int BK, int WM, int WN, bool A_R, bool B_R, bool DUAL>
 struct MfmaCfg {
@@ -248,11 +256,12 @@ struct MfmaCfg {
   static constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
   static constexpr int LDK = BK * ESIZE + 16;  // LDS row pitch in bytes (16-byte pad)
   static constexpr int NB = DUAL ? 2 : 1;
-  // BTR: an n-contiguous 16-bit B operand is copied into LDS unchanged, [k][n] rows of pitch LDB (≡ 64 bytes mod 256
-  // so the 8 rows one transposing read touches fall in distinct banks), and its fragments are read with
-  // ds_read_b64_tr_b16; otherwise B is K-packed like A ([n][k] rows of pitch LDK, transposed in registers on the way)
-  static constexpr bool BTR = B_R && ESIZE == 2;
-  static constexpr int LDB = BN * ESIZE + 64;
+  // BTR: an n-contiguous 16- or 8-bit B operand is copied into LDS unchanged, [k][n] rows of pitch LDB (≡ 64 resp.
+  // 32·odd bytes mod 256, so the rows one transposing read touches fall in distinct banks), and its fragments are read
+  // with ds_read_b64_tr_b16 / _b8; otherwise B is K-packed like A ([n][k] rows of pitch LDK, transposed in registers
+  // on the way)
+  static constexpr bool BTR = B_R && ESIZE <= 2;
+  static constexpr int LDB = BN * ESIZE + (ESIZE == 2 ? 64 : 32);
   static constexpr int BREG = BTR ? BK * LDB : BN * LDK;  // bytes of one B operand tile
   static constexpr int STAGE = BM * LDK + NB * BREG;
   static constexpr int LDS_BYTES = 2 * STAGE;
@@ -519,15 +528,26 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_mfma_kernel(const GemmArgs 
   // K-packed B: row n, k-pack of this lane. Transposed-read B: lane s of each 16-lane group addresses k-row
   // 8·(lane/32) + s/4 and column 16·((lane/16) % 2) + 4·(s % 4), so the pair of reads (k-rows +0 and +4) delivers
   // B[8·(lane/32) .. +7][lane % 32] — the MFMA operand fragment.
-  const int b_off = C::BTR ? BM * C::LDK + (8 * (lane >> 5) + ((lane & 15) >> 2)) * C::LDB +
-                                 (wn * C::WTN + 16 * ((lane >> 4) & 1) + 4 * (lane & 3)) * ES
-                           : BM * C::LDK + (wn * C::WTN + lrow) * C::LDK + lk;
+  // (8-bit: lane s addresses k-row KPACK·(lane/32) + s/2 and column 16·((lane/16) % 2) + 8·(s % 2); each read
+  // delivers 8 consecutive k, KPACK / 8 reads make the fragment.)
+  const int b_off = !C::BTR ? BM * C::LDK + (wn * C::WTN + lrow) * C::LDK + lk
+                    : ES == 2 ? BM * C::LDK + (8 * (lane >> 5) + ((lane & 15) >> 2)) * C::LDB +
+                                    (wn * C::WTN + 16 * ((lane >> 4) & 1) + 4 * (lane & 3)) * ES
+                              : BM * C::LDK + (C::KPACK * (lane >> 5) + ((lane & 15) >> 1)) * C::LDB +
+                                    (wn * C::WTN + 16 * ((lane >> 4) & 1) + 8 * (lane & 1)) * ES;
   auto bfrag = [&](const char* p) -> typename F::T {
-    if constexpr (C::BTR) {
+    if constexpr (!C::BTR) {
+      return F::load(p);
+    } else if constexpr (ES == 2) {
       const uint2 lo = lds_read_tr16(p), hi = lds_read_tr16(p + 4 * C::LDB);
       return u32x4{lo.x, lo.y, hi.x, hi.y};
+    } else if constexpr (C::KPACK == 16) {
+      const uint2 a = lds_read_tr8(p), b = lds_read_tr8(p + 8 * C::LDB);
+      return u32x4{a.x, a.y, b.x, b.y};
     } else {
-      return F::load(p);
+      const uint2 a = lds_read_tr8(p), b = lds_read_tr8(p + 8 * C::LDB), c = lds_read_tr8(p + 16 * C::LDB),
+                  d = lds_read_tr8(p + 24 * C::LDB);
+      return u32x8{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
     }
   };
   auto lfrag = [&](int buf, auto s, auto slot) {
