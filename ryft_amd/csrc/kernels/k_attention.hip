@@ -5,8 +5,8 @@
 // transposed, Sᵀ = K·Qᵀ, so that the 32×32 MFMA accumulator puts one query in each lane (lanes l and l+32 share a
 // query and split its keys): the running max / sum of the online softmax then need no cross-lane reductions except
 // one swap between the two half-waves, and the rescaling of the output Oᵀ = Vᵀ·Pᵀ is a per-lane multiply. P never
-// leaves registers: the Sᵀ accumulator, rounded to bf16, is directly the B operand of the P·V MFMA, with the
-// matching key order obtained by storing Vᵀ in LDS in that permuted order. Row maxima are taken on the raw
+// leaves registers: the Sᵀ accumulator, rounded to bf16, is directly the B operand of the P·V MFMA; V stays [key][d]
+// in LDS and its transposed fragments, in the matching key order, come from transposing LDS reads. Row maxima are taken on the raw
 // scores and each probability costs one FMA and one v_exp_f32 (2^x). Two workgroups share a CU (≤ 256 registers
 // per lane), so one wave's softmax overlaps another's MFMAs. The [S, S] score matrix is never materialised.
 #include <hip/hip_runtime.h>
@@ -35,6 +35,13 @@ __device__ __forceinline__ f32x16_a mma_bf16(const u32x4a& a, const u32x4a& b, f
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_a, a), __builtin_bit_cast(bf16x8_a, b), c, 0, 0, 0);
 }
 
+typedef short s16x4_a __attribute__((ext_vector_type(4)));
+// ds_read_b64_tr_b16 (lane layout measured on gfx950; see the P·V loop)
+__device__ __forceinline__ uint2 lds_read_tr16(const char* p) {
+  const s16x4_a v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4_a*)p);
+  return __builtin_bit_cast(uint2, v);
+}
+
 typedef __bf16 bf16x2_a __attribute__((ext_vector_type(2)));
 typedef float f32x2_a __attribute__((ext_vector_type(2)));
 
@@ -45,10 +52,12 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
 
 template <int D>
 struct AttnCfg {
-  static constexpr int KP = D * 2 + 16;    // K row pitch (bytes): [key][d]
-  static constexpr int VP = BKV * 2 + 16;  // Vᵀ row pitch (bytes): [d][key]
+  static constexpr int KP = D * 2 + 16;  // K row pitch (bytes): [key][d]
+  // V row pitch (bytes): [key][d] rows as in memory, ≡ 64 mod 256 so the 4 rows of one transposing read fall in
+  // distinct banks
+  static constexpr int VP = D * 2 + 64;
   static constexpr int KBYTES = BKV * KP;
-  static constexpr int VBYTES = D * VP;
+  static constexpr int VBYTES = BKV * VP;
   static constexpr int STAGE = KBYTES + VBYTES;
   static constexpr int OP = D * 4 + 16;     // output staging pitch (f32)
   static constexpr int LDS = 2 * STAGE > BQ * OP ? 2 * STAGE : BQ * OP;
@@ -92,11 +101,9 @@ __global__ void __launch_bounds__(256, 2) attention_fwd_kernel(const AttnArgs A)
     if (lim < nkv) nkv = lim;
   }
 
-  // K block: 64 keys × D → 4·(D/128)... vectors of 16 B per thread; Vᵀ block: 8×8 transposes by threads < 8·D/8
-  constexpr int KVEC = BKV * D / 8 / 256;  // 16-byte vectors of K per thread
-  constexpr int VBLK = (BKV / 8) * (D / 8); // 8×8 blocks of V
-  u32x4a kreg[KVEC];
-  u32x4a vreg[8];
+  // K and V blocks (64 keys × D) are copied into LDS unchanged, 16 bytes per thread per load
+  constexpr int KVEC = BKV * D / 8 / 256;  // 16-byte vectors of K (and of V) per thread
+  u32x4a kreg[KVEC], vreg[KVEC];
   // Buffer loads with the KV block origin in the scalar resource: the per-lane byte offsets are loop-invariant
   // 32-bit values (the launcher checks the extents), so no address registers are rewritten each block — with
   // 64-bit address registers the allocator reuses them while the loads are in flight and the MFMAs then wait for
@@ -111,11 +118,7 @@ __global__ void __launch_bounds__(256, 2) attention_fwd_kernel(const AttnArgs A)
       int v = tid + i * 256;
       int row = v / (D / 8), c = v % (D / 8);
       kreg[i] = __builtin_amdgcn_raw_buffer_load_b128(kr, (row * ks2 + c * 8) * 2, 0, 0);
-    }
-    if (tid < VBLK) {
-      int kb = tid % (BKV / 8), dv = tid / (BKV / 8);  // lanes spread over k-blocks: conflict-free LDS stores
-#pragma unroll
-      for (int q = 0; q < 8; ++q) vreg[q] = __builtin_amdgcn_raw_buffer_load_b128(vr, ((kb * 8 + q) * vs2 + dv * 8) * 2, 0, 0);
+      vreg[i] = __builtin_amdgcn_raw_buffer_load_b128(vr, (row * vs2 + c * 8) * 2, 0, 0);
     }
   };
   auto lstore = [&](int buf) {
@@ -126,29 +129,7 @@ __global__ void __launch_bounds__(256, 2) attention_fwd_kernel(const AttnArgs A)
       int v = tid + i * 256;
       int row = v / (D / 8), c = v % (D / 8);
       *(u32x4a*)(sK + row * C::KP + c * 16) = kreg[i];
-    }
-    if (tid < VBLK) {
-      int kb = tid % (BKV / 8), dv = tid / (BKV / 8);  // lanes spread over k-blocks: conflict-free LDS stores
-      uint32_t w[8][4];
-#pragma unroll
-      for (int q = 0; q < 8; ++q) { w[q][0] = vreg[q].x; w[q][1] = vreg[q].y; w[q][2] = vreg[q].z; w[q][3] = vreg[q].w; }
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        u32x4a lo, hi;
-        lo.x = __builtin_amdgcn_perm(w[1][t], w[0][t], 0x05040100u); hi.x = __builtin_amdgcn_perm(w[1][t], w[0][t], 0x07060302u);
-        lo.y = __builtin_amdgcn_perm(w[3][t], w[2][t], 0x05040100u); hi.y = __builtin_amdgcn_perm(w[3][t], w[2][t], 0x07060302u);
-        lo.z = __builtin_amdgcn_perm(w[5][t], w[4][t], 0x05040100u); hi.z = __builtin_amdgcn_perm(w[5][t], w[4][t], 0x07060302u);
-        lo.w = __builtin_amdgcn_perm(w[7][t], w[6][t], 0x05040100u); hi.w = __builtin_amdgcn_perm(w[7][t], w[6][t], 0x07060302u);
-        // Within each 16-key group, key 8a + 4h + i is stored at position 8h + 4a + i, so that the 8 keys one lane
-        // multiplies in a k-step (h = lane / 32: keys 4h..4h+3 and 8+4h..8+4h+3) are contiguous: the P·V loop then
-        // reads them with one conflict-free 16-byte read. This lane's 8 keys are group kb / 2, a = kb % 2.
-        char* r0 = sV + (dv * 8 + 2 * t) * C::VP + (kb >> 1) * 32 + (kb & 1) * 8;
-        char* r1 = r0 + C::VP;
-        *(uint2*)r0 = uint2{lo.x, lo.y};
-        *(uint2*)(r0 + 16) = uint2{lo.z, lo.w};
-        *(uint2*)r1 = uint2{hi.x, hi.y};
-        *(uint2*)(r1 + 16) = uint2{hi.z, hi.w};
-      }
+      *(u32x4a*)(sV + row * C::VP + c * 16) = vreg[i];
     }
   };
 
@@ -215,13 +196,19 @@ __global__ void __launch_bounds__(256, 2) attention_fwd_kernel(const AttnArgs A)
       pf[2 * t + 1] = u32x4a{pack_bf16(p[8], p[9]), pack_bf16(p[10], p[11]), pack_bf16(p[12], p[13]), pack_bf16(p[14], p[15])};
     }
     // Oᵀ[d, q] += Σ_key Vᵀ[d, key] · P[q, key]; k-step s covers keys [16s, 16s+16) in the accumulator's key order:
-    // element e of lane l ↔ key 16s + 8·(e/4) + 4·(l/32) + e%4
+    // element e of lane l ↔ key 16s + 8·(e/4) + 4·(l/32) + e%4. The Vᵀ fragment (row d = l % 32) is read from the
+    // [key][d] tile with two ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i % 4 of the
+    // 8-byte chunks addressed by lanes i/4 + 4m (m = 0..3), so lane i addresses key row k0 + i/4 and column
+    // c0 + 4·(i % 4), and receives keys k0 .. k0+3 of column c0 + i — with k0 = 16s + 4·(l/32) and k0 + 8, exactly
+    // the accumulator's key order.
+    const int v_off = (4 * (lane >> 5) + ((lane & 15) >> 2)) * C::VP + (16 * ((lane >> 4) & 1) + 4 * (lane & 3)) * 2;
 #pragma unroll
     for (int s = 0; s < BKV / 16; ++s) {
 #pragma unroll
       for (int dt = 0; dt < D / 32; ++dt) {
-        const u32x4a vf = *(const u32x4a*)(sV + (dt * 32 + (lane & 31)) * C::VP + (s * 16 + 8 * half) * 2);
-        o[dt] = mma_bf16(vf, pf[s], o[dt]);
+        const char* vp = sV + v_off + 16 * s * C::VP + dt * 64;
+        const uint2 lo = lds_read_tr16(vp), hi = lds_read_tr16(vp + 8 * C::VP);
+        o[dt] = mma_bf16(u32x4a{lo.x, lo.y, hi.x, hi.y}, pf[s], o[dt]);
       }
     }
     if (j + 1 < nkv) lstore(cur ^ 1);
