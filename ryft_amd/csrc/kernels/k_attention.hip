@@ -154,32 +154,43 @@ __global__ void __launch_bounds__(256, 2) attention_fwd_kernel(const AttnArgs A)
         st[t] = mma_bf16(kf, qf[s], st[t]);
       }
     }
-    // mask and block max on the unscaled scores (the scale is positive, so maxima commute with it)
+    // mask and block max on the unscaled scores (the scale is positive, so maxima commute with it); only blocks that
+    // reach past this wave's first query need the causal mask (a wave-uniform branch between two copies)
     const int kbase = j * BKV;
     const bool need_mask = A.causal && (kbase + BKV - 1 > q0 + wave * 32 + A.causal_offset);
     float mloc = -INFINITY;
+    if (need_mask) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float v = st[t][r];
-        if (need_mask) {
-          int key = kbase + t * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-          if (key > myq + A.causal_offset) v = -INFINITY;
+        for (int r = 0; r < 16; ++r) {
+          const int key = kbase + t * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+          const float v = key > myq + A.causal_offset ? -INFINITY : st[t][r];
+          st[t][r] = v;
+          mloc = fmaxf(mloc, v);
         }
-        st[t][r] = v;
-        mloc = fmaxf(mloc, v);
-      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, st[t][r]);
+    }
     mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-    const float m_new = fmaxf(m_run, mloc);
+    // Lazy rescaling: the exponent reference m_run only moves when this block's maximum exceeds it by more than 8 in
+    // log2 units (probabilities then stay ≤ 2^8; o and l share the reference, so o / l is unchanged), and the
+    // rescale of o is skipped when no lane moved its reference.
+    const bool raise = (mloc - m_run) * sl2 > 8.0f || (m_run == -INFINITY && mloc != -INFINITY);
+    const float m_new = raise ? mloc : m_run;
     const float m_use = m_new == -INFINITY ? 0.f : m_new;  // a fully masked row keeps p = 0
-    const float alpha = __builtin_amdgcn_exp2f((m_run - m_use) * sl2);
+    if (__builtin_amdgcn_ballot_w64(raise)) {
+      const float alpha = __builtin_amdgcn_exp2f((m_run - m_use) * sl2);  // 1 where the reference did not move
+      l_run *= alpha;
+#pragma unroll
+      for (int t = 0; t < D / 32; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
+    }
     m_run = m_new;
-    l_run *= alpha;
-#pragma unroll
-    for (int t = 0; t < D / 32; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
     // P = 2^((s - m)·scale·log2 e) with one FMA and v_exp_f32 per score, packed to bf16 (round to nearest even) as
     // the B operand of Oᵀ = Vᵀ·Pᵀ
     const float mb = -m_use * sl2;
