@@ -69,9 +69,12 @@ __global__ void __launch_bounds__(256, 2) attention_fwd_kernel(const AttnArgs A)
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nq = A.Sq / BQ;
-  // heaviest (latest) query blocks first under a causal mask
-  const int qb = A.causal ? nq - 1 - (int)(blockIdx.x % nq) : (int)(blockIdx.x % nq);
-  const int bh = blockIdx.x / nq;
+  // Under a causal mask the work of a query block grows with its index. Workgroups are dispatched in blockIdx order,
+  // so the query block is the slow index and runs heaviest first across all heads (longest-first scheduling): the
+  // short blocks fill the tail instead of one head's long blocks finishing last.
+  const int nbh = (int)gridDim.x / nq;
+  const int qb = A.causal ? nq - 1 - (int)(blockIdx.x / nbh) : (int)(blockIdx.x / nbh);
+  const int bh = blockIdx.x % nbh;
   const int b = bh / A.H, h = bh % A.H;
   const int q0 = qb * BQ;
   const uint16_t* Qg = (const uint16_t*)A.q + (int64_t)b * A.qs[0] + (int64_t)h * A.qs[1];
