@@ -1,7 +1,8 @@
 // Fused softmax attention forward for gfx950 (bf16 in, f32 softmax statistics, bf16 P·V, bf16/f32 out).
 //
 // A workgroup owns 128 queries of one (batch, head); each of its 4 wavefronts owns 32 queries. Key/value blocks of
-// 64 rows stream through LDS (double-buffered: block j+1 is fetched while block j is consumed). Scores are computed
+// 64 rows stream through LDS (double-buffered: block j+1 is fetched while block j is consumed), loaded from global
+// memory directly into a swizzled LDS layout without passing through registers. Scores are computed
 // transposed, Sᵀ = K·Qᵀ, so that the 32×32 MFMA accumulator puts one query in each lane (lanes l and l+32 share a
 // query and split its keys): the running max / sum of the online softmax then need no cross-lane reductions except
 // one swap between the two half-waves, and the rescaling of the output Oᵀ = Vᵀ·Pᵀ is a per-lane multiply. P never
@@ -50,18 +51,33 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_a{lo, hi}, bf16x2_a));
 }
 
+typedef __attribute__((address_space(3))) void lds_void;
+// One wave-wide 16-byte-per-lane load from a buffer straight into LDS: lane l's 16 bytes land at lds + 16·l (lds is
+// wave-uniform; it goes to M0).
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, char* lds, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds, 16, voff, 0, 0, 0);
+}
+
 template <int D>
 struct AttnCfg {
-  static constexpr int KP = D * 2 + 16;  // K row pitch (bytes): [key][d]
-  // V row pitch (bytes): [key][d] rows as in memory, ≡ 64 mod 256 so the 4 rows of one transposing read fall in
-  // distinct banks
-  static constexpr int VP = D * 2 + 64;
-  static constexpr int KBYTES = BKV * KP;
-  static constexpr int VBYTES = BKV * VP;
-  static constexpr int STAGE = KBYTES + VBYTES;
-  static constexpr int OP = D * 4 + 16;     // output staging pitch (f32)
+  static constexpr int RB = D * 2;             // bytes per key row of a K or V block in LDS (unpadded, swizzled)
+  static constexpr int KBYTES = BKV * RB;      // one K (or V) block
+  static constexpr int STAGE = 2 * KBYTES;     // K block, then V block
+  static constexpr int PIECES = KBYTES / 1024;  // 1 KB pieces per block: one wave-wide 16-byte-per-lane DMA each
+  static constexpr int OP = D * 4 + 16;        // output staging pitch (f32)
   static constexpr int LDS = 2 * STAGE > BQ * OP ? 2 * STAGE : BQ * OP;
 };
+
+// LDS swizzle of K and V blocks: the 16-byte chunk c of key row r sits at chunk position c ^ kv_swz(r). Chosen for
+// the two read patterns (64 banks of 4 bytes): the K fragment reads (ds_read_b128, 16 lanes on 16 consecutive rows,
+// one chunk) need a bijection of r mod 16; the transposing V reads (ds_read_b64_tr_b16, 32 lanes on 4 consecutive
+// rows × 4 consecutive chunks) need the 4 rows of a group to land their chunk quads on distinct quads.
+template <int D>
+__device__ __forceinline__ int kv_swz(int r) {
+  if constexpr (D == 128) return ((r & 3) << 2) | ((r >> 2) & 3);  // 16 chunks per row
+  else return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);            // 8 chunks per row: bank quad also picks r & 1
+}
+
 
 template <int D>
 __global__ void __launch_bounds__(256, 2) attention_fwd_kernel(const AttnArgs A) {
@@ -104,47 +120,53 @@ __global__ void __launch_bounds__(256, 2) attention_fwd_kernel(const AttnArgs A)
     if (lim < nkv) nkv = lim;
   }
 
-  // K and V blocks (64 keys × D) are copied into LDS unchanged, 16 bytes per thread per load
-  constexpr int KVEC = BKV * D / 8 / 256;  // 16-byte vectors of K (and of V) per thread
-  u32x4a kreg[KVEC], vreg[KVEC];
-  // Buffer loads with the KV block origin in the scalar resource: the per-lane byte offsets are loop-invariant
-  // 32-bit values (the launcher checks the extents), so no address registers are rewritten each block — with
-  // 64-bit address registers the allocator reuses them while the loads are in flight and the MFMAs then wait for
-  // the prefetch.
+  // K and V blocks (64 keys × D) go from global memory straight into LDS (buffer_load … lds, 16 bytes per lane):
+  // each wave-wide load fills one contiguous 1 KB piece, lane l writing bytes [16l, 16l+16) of it, so the swizzle is
+  // applied on the global side — the lane that fills chunk position c' of row r loads chunk c' ^ kv_swz(r). No
+  // registers hold the blocks in flight and no LDS stores are issued. The block origin is in the scalar resource
+  // and the per-lane byte offsets are loop-invariant (the launcher checks that they fit 32 bits).
   const int ks2 = (int)A.ks[2], vs2 = (int)A.vs[2];
-  auto gload = [&](int j) {
+  constexpr int PPW = C::PIECES / 4;  // pieces per wave per tensor
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  int koff[PPW], voff[PPW];
+#pragma unroll
+  for (int i = 0; i < PPW; ++i) {
+    const int byte = (i * 4 + wave_u) * 1024 + lane * 16;
+    const int r = byte / C::RB, c = ((byte % C::RB) / 16) ^ kv_swz<D>(r);
+    koff[i] = r * ks2 * 2 + c * 16;
+    voff[i] = r * vs2 * 2 + c * 16;
+  }
+  auto dma = [&](int j, int buf) {
     const int k0 = j * BKV;
     const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc((void*)(Kg + (int64_t)k0 * ks2 * 2), (short)0, -1, 0x00020000);
     const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc((void*)(Vg + (int64_t)k0 * vs2 * 2), (short)0, -1, 0x00020000);
+    char* sK = smem + buf * C::STAGE;
 #pragma unroll
-    for (int i = 0; i < KVEC; ++i) {
-      int v = tid + i * 256;
-      int row = v / (D / 8), c = v % (D / 8);
-      kreg[i] = __builtin_amdgcn_raw_buffer_load_b128(kr, (row * ks2 + c * 8) * 2, 0, 0);
-      vreg[i] = __builtin_amdgcn_raw_buffer_load_b128(vr, (row * vs2 + c * 8) * 2, 0, 0);
+    for (int i = 0; i < PPW; ++i) {
+      lds_dma16(kr, sK + (i * 4 + wave_u) * 1024, koff[i]);
+      lds_dma16(vr, sK + C::KBYTES + (i * 4 + wave_u) * 1024, voff[i]);
     }
   };
-  auto lstore = [&](int buf) {
-    char* sK = smem + buf * C::STAGE;
-    char* sV = sK + C::KBYTES;
-#pragma unroll
-    for (int i = 0; i < KVEC; ++i) {
-      int v = tid + i * 256;
-      int row = v / (D / 8), c = v % (D / 8);
-      *(u32x4a*)(sK + row * C::KP + c * 16) = kreg[i];
-      *(u32x4a*)(sV + row * C::VP + c * 16) = vreg[i];
-    }
+  // wait for this wave's block loads, then for every wave's
+  auto dma_wait_sync = [&]() {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();
   };
 
-  if (nkv > 0) {
-    gload(0);
-    lstore(0);
-  }
-  __syncthreads();
   const int half = lane >> 5;
+  // K fragment: row t·32 + l % 32, chunk 2s + l/32 → byte (l % 32)·RB + 16·((2s + l/32) ^ sw) = k_lane ^ 32s
+  const int k_lane = (lane & 31) * C::RB + 16 * (kv_swz<D>(lane & 15) ^ half);
+  // V fragment rows 16s + vr0 (+ 8), chunk 4·dt + vcl: byte = v_lane[hi] ^ 64·dt, plus 16s·RB
+  const int vr0 = 4 * (lane >> 5) + ((lane & 15) >> 2);
+  const int vcl = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+  const int v_lo = vr0 * C::RB + 16 * (vcl ^ kv_swz<D>(vr0)) + 8 * (lane & 1);
+  const int v_hi = (vr0 + 8) * C::RB + 16 * (vcl ^ kv_swz<D>(vr0 + 8)) + 8 * (lane & 1);
+
+  if (nkv > 0) dma(0, 0);
+  dma_wait_sync();
   for (int j = 0; j < nkv; ++j) {
     const int cur = j & 1;
-    if (j + 1 < nkv) gload(j + 1);
+    if (j + 1 < nkv) dma(j + 1, cur ^ 1);
     const char* sK = smem + cur * C::STAGE;
     const char* sV = sK + C::KBYTES;
     // Sᵀ tiles: keys [32t, 32t+32) × this wave's 32 queries
@@ -153,7 +175,7 @@ __global__ void __launch_bounds__(256, 2) attention_fwd_kernel(const AttnArgs A)
     for (int s = 0; s < D / 16; ++s) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        u32x4a kf = *(const u32x4a*)(sK + (t * 32 + (lane & 31)) * C::KP + (s * 16 + 8 * half) * 2);
+        u32x4a kf = *(const u32x4a*)(sK + t * 32 * C::RB + (k_lane ^ (32 * s)));
         st[t] = mma_bf16(kf, qf[s], st[t]);
       }
     }
@@ -215,18 +237,16 @@ __global__ void __launch_bounds__(256, 2) attention_fwd_kernel(const AttnArgs A)
     // 8-byte chunks addressed by lanes i/4 + 4m (m = 0..3), so lane i addresses key row k0 + i/4 and column
     // c0 + 4·(i % 4), and receives keys k0 .. k0+3 of column c0 + i — with k0 = 16s + 4·(l/32) and k0 + 8, exactly
     // the accumulator's key order.
-    const int v_off = (4 * (lane >> 5) + ((lane & 15) >> 2)) * C::VP + (16 * ((lane >> 4) & 1) + 4 * (lane & 3)) * 2;
 #pragma unroll
     for (int s = 0; s < BKV / 16; ++s) {
 #pragma unroll
       for (int dt = 0; dt < D / 32; ++dt) {
-        const char* vp = sV + v_off + 16 * s * C::VP + dt * 64;
-        const uint2 lo = lds_read_tr16(vp), hi = lds_read_tr16(vp + 8 * C::VP);
+        const char* vs = sV + 16 * s * C::RB;
+        const uint2 lo = lds_read_tr16(vs + (v_lo ^ (64 * dt))), hi = lds_read_tr16(vs + (v_hi ^ (64 * dt)));
         o[dt] = mma_bf16(u32x4a{lo.x, lo.y, hi.x, hi.y}, pf[s], o[dt]);
       }
     }
-    if (j + 1 < nkv) lstore(cur ^ 1);
-    __syncthreads();
+    dma_wait_sync();
   }
 
   // normalise and write out through LDS (lane-per-query layout → row-major rows)
