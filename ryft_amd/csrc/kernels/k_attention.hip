@@ -13,6 +13,7 @@
 #include <hip/hip_runtime.h>
 
 #include <string>
+#include <type_traits>
 
 #include "../common.h"
 #include "ew_device.h"
@@ -36,11 +37,23 @@ __device__ __forceinline__ f32x16_a mma_bf16(const u32x4a& a, const u32x4a& b, f
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_a, a), __builtin_bit_cast(bf16x8_a, b), c, 0, 0, 0);
 }
 
-typedef short s16x4_a __attribute__((ext_vector_type(4)));
-// ds_read_b64_tr_b16 (lane layout measured on gfx950; see the P·V loop)
-__device__ __forceinline__ uint2 lds_read_tr16(const char* p) {
-  const s16x4_a v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4_a*)p);
-  return __builtin_bit_cast(uint2, v);
+typedef uint32_t u32x2a __attribute__((ext_vector_type(2)));
+// ds_read_b64_tr_b16 (lane layout measured on gfx950; see the P·V loop) as inline assembly. The compiler sees
+// neither its LDS access nor its completion: it does not make it wait for the LDS-DMA loads of the next block (which
+// it cannot tell apart from the stage being read, and would otherwise wait for before the first P·V read), and the
+// caller waits (lgkmcnt) through tr16_wait before using the result.
+template <int OFF>
+__device__ __forceinline__ u32x2a lds_read_tr16_asm(uint32_t addr) {
+  u32x2a r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+  return r;
+}
+// waits for all outstanding LDS reads; the fragments pass through the statement so that their uses follow it
+__device__ __forceinline__ void tr16_wait(u32x2a (&f)[8]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]), "+v"(f[6]), "+v"(f[7]));
+}
+__device__ __forceinline__ void tr16_wait(u32x2a (&f)[4]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]));
 }
 
 typedef __bf16 bf16x2_a __attribute__((ext_vector_type(2)));
@@ -52,10 +65,18 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
 }
 
 typedef __attribute__((address_space(3))) void lds_void;
-// One wave-wide 16-byte-per-lane load from a buffer straight into LDS: lane l's 16 bytes land at lds + 16·l (lds is
-// wave-uniform; it goes to M0).
-__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, char* lds, int voff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds, 16, voff, 0, 0, 0);
+// One wave-wide 16-byte-per-lane load from a buffer straight into LDS: lane l's 16 bytes (buffer bytes voff + soff)
+// land at lds + 16·l (lds and soff are wave-uniform: M0 and the scalar offset).
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, char* lds, int voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds, 16, voff, soff, 0, 0);
+}
+
+template <class F>
+__device__ __forceinline__ void static_for4(F&& f) {
+  f(std::integral_constant<int, 0>{});
+  f(std::integral_constant<int, 1>{});
+  f(std::integral_constant<int, 2>{});
+  f(std::integral_constant<int, 3>{});
 }
 
 template <int D>
@@ -77,7 +98,6 @@ __device__ __forceinline__ int kv_swz(int r) {
   if constexpr (D == 128) return ((r & 3) << 2) | ((r >> 2) & 3);  // 16 chunks per row
   else return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);            // 8 chunks per row: bank quad also picks r & 1
 }
-
 
 template <int D>
 __global__ void __launch_bounds__(256, 2) attention_fwd_kernel(const AttnArgs A) {
@@ -128,14 +148,12 @@ __global__ void __launch_bounds__(256, 2) attention_fwd_kernel(const AttnArgs A)
   const int ks2 = (int)A.ks[2], vs2 = (int)A.vs[2];
   constexpr int PPW = C::PIECES / 4;  // pieces per wave per tensor
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  int koff[PPW], voff[PPW];
-#pragma unroll
-  for (int i = 0; i < PPW; ++i) {
-    const int byte = (i * 4 + wave_u) * 1024 + lane * 16;
-    const int r = byte / C::RB, c = ((byte % C::RB) / 16) ^ kv_swz<D>(r);
-    koff[i] = r * ks2 * 2 + c * 16;
-    voff[i] = r * vs2 * 2 + c * 16;
-  }
+  // the swizzle depends on the row modulo 16 only, which is the same for all pieces of a wave: piece i is piece 0
+  // moved down 4096 / RB rows, a scalar offset
+  const int r0 = (wave_u * 1024 + lane * 16) / C::RB;
+  const int c0 = ((lane * 16) % C::RB / 16) ^ kv_swz<D>(r0);
+  const int koff = r0 * ks2 * 2 + c0 * 16, voff = r0 * vs2 * 2 + c0 * 16;
+  constexpr int PROWS = 4096 / C::RB;  // rows between a wave's consecutive pieces
   auto dma = [&](int j, int buf) {
     const int k0 = j * BKV;
     const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc((void*)(Kg + (int64_t)k0 * ks2 * 2), (short)0, -1, 0x00020000);
@@ -143,8 +161,8 @@ __global__ void __launch_bounds__(256, 2) attention_fwd_kernel(const AttnArgs A)
     char* sK = smem + buf * C::STAGE;
 #pragma unroll
     for (int i = 0; i < PPW; ++i) {
-      lds_dma16(kr, sK + (i * 4 + wave_u) * 1024, koff[i]);
-      lds_dma16(vr, sK + C::KBYTES + (i * 4 + wave_u) * 1024, voff[i]);
+      lds_dma16(kr, sK + (i * 4 + wave_u) * 1024, koff, i * PROWS * ks2 * 2);
+      lds_dma16(vr, sK + C::KBYTES + (i * 4 + wave_u) * 1024, voff, i * PROWS * vs2 * 2);
     }
   };
   // wait for this wave's block loads, then for every wave's
@@ -237,15 +255,28 @@ __global__ void __launch_bounds__(256, 2) attention_fwd_kernel(const AttnArgs A)
     // 8-byte chunks addressed by lanes i/4 + 4m (m = 0..3), so lane i addresses key row k0 + i/4 and column
     // c0 + 4·(i % 4), and receives keys k0 .. k0+3 of column c0 + i — with k0 = 16s + 4·(l/32) and k0 + 8, exactly
     // the accumulator's key order.
-#pragma unroll
-    for (int s = 0; s < BKV / 16; ++s) {
+    // Fragments of k-step s + 1 are read while the MFMAs of k-step s run (two register sets).
+    const uint32_t vaddr = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const char*)sV;
+    u32x2a vf[2][2 * (D / 32)];
+    auto vread = [&](auto sc, u32x2a (&f)[2 * (D / 32)]) {
+      constexpr int S = decltype(sc)::value;
 #pragma unroll
       for (int dt = 0; dt < D / 32; ++dt) {
-        const char* vs = sV + 16 * s * C::RB;
-        const uint2 lo = lds_read_tr16(vs + (v_lo ^ (64 * dt))), hi = lds_read_tr16(vs + (v_hi ^ (64 * dt)));
-        o[dt] = mma_bf16(u32x4a{lo.x, lo.y, hi.x, hi.y}, pf[s], o[dt]);
+        f[2 * dt] = lds_read_tr16_asm<16 * S * C::RB>(vaddr + (v_lo ^ (64 * dt)));
+        f[2 * dt + 1] = lds_read_tr16_asm<16 * S * C::RB>(vaddr + (v_hi ^ (64 * dt)));
       }
-    }
+    };
+    vread(std::integral_constant<int, 0>{}, vf[0]);
+    static_for4([&](auto sc) {
+      constexpr int S = decltype(sc)::value;
+      tr16_wait(vf[S & 1]);
+      if constexpr (S + 1 < BKV / 16) vread(std::integral_constant<int, S + 1>{}, vf[(S + 1) & 1]);
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt) {
+        const u32x2a lo = vf[S & 1][2 * dt], hi = vf[S & 1][2 * dt + 1];
+        o[dt] = mma_bf16(u32x4a{lo.x, lo.y, hi.x, hi.y}, pf[S], o[dt]);
+      }
+    });
     dma_wait_sync();
   }
 
