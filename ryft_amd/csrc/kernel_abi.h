@@ -95,6 +95,45 @@ struct ReduceArgs {
   const void* init_ptr;  // non-null: the init value is a device scalar (a program argument)
 };
 
+// ------------------------------------------------------------------------------------------------ row fusion
+// Reductions over the innermost dimension whose results are broadcast back along that dimension into an elementwise
+// consumer over the same [rows, inner] space (RMSNorm, LayerNorm, an unfused softmax), run as one kernel: each row
+// is reduced n_red times in sequence and then mapped, without the per-row values ever reaching HBM.
+// One program holds every phase: instructions [phase_end[k-1], phase_end[k]) compute the value reduced by reduction
+// k (k < n_red; they may read the earlier row values through EW_ACC j < k), and [phase_end[n_red-1], phase_end[n_red])
+// the consumer (which reads row value j through EW_ACC j). No register value crosses a phase boundary.
+#define ROW_MAX_RED 2
+
+// Fast path of a row-fused step whose program the planner recognised as a scaled root-mean-square normalisation:
+// out[r, i] = convert(round_mid(x[r, i] · rsqrt(t(Σ_i x[r, i]²) + eps) · w[i])), t(s) = s·alpha (or s / alpha),
+// all arithmetic in f32 in the program's own operation order; x contiguous rows, w (optional) one row shared by all.
+struct RowNormArgs {
+  const void* x;
+  const void* w;    // null: no weight factor
+  void* out;
+  int32_t x_dtype, w_dtype, out_dtype;
+  int32_t mid_round;  // element type the product is rounded to before the output conversion (0: none)
+  float alpha, eps;
+  int32_t alpha_div;  // 1: t(s) = s / alpha
+  int32_t pad;
+};
+enum RowFast : int32_t { ROW_FAST_NONE = 0, ROW_FAST_NORM = 1 };
+
+struct RowArgs {
+  EwProgram prog;  // iteration space [rows..., inner]; out_ptr: the consumer's outputs (contiguous)
+  int64_t rows;    // product of the outer dims
+  int64_t inner;   // innermost extent (the reduced one)
+  int32_t n_red;
+  int32_t phase_end[ROW_MAX_RED + 1];
+  int32_t red_reg[ROW_MAX_RED];    // register holding the value folded by reduction k at the end of its phase
+  int32_t kind[ROW_MAX_RED];       // ReduceKind
+  int32_t is_float[ROW_MAX_RED];
+  uint32_t init[ROW_MAX_RED];      // init value bits (f32 bits for float class)
+  int32_t red_dtype[ROW_MAX_RED];  // element type the row value is rounded to (the reduce's result type)
+  int32_t fast;                    // RowFast: a specialised kernel computes the same step
+  RowNormArgs norm;                // ROW_FAST_NORM operands
+};
+
 // ------------------------------------------------------------------------------------------------ GEMM
 // C[b, m, n] = Σ_k A[b, m, k] · B[b, n, k]   (B is addressed as [n, k]; its strides say which one is contiguous)
 struct GemmOperand {

@@ -182,7 +182,9 @@ __device__ __forceinline__ int64_t leaf_offset(const EwLeaf& L, int64_t lin, con
   if (L.kind == EW_LEAF_IDENTITY) return L.offset + lin;
   if (L.kind == EW_LEAF_SCALAR) return L.offset;
   int64_t off = L.offset;
-  for (int d = 0; d < rank; ++d) off += (int64_t)coord[d] * L.strides[d];
+#pragma unroll
+  for (int d = 0; d < EW_MAX_RANK; ++d)  // constant indices: the leaf and coordinates stay in registers
+    if (d < rank) off += (int64_t)coord[d] * L.strides[d];
   return off;
 }
 
@@ -191,6 +193,23 @@ __device__ __forceinline__ void decompose(int64_t lin, const EwProgram& P, int32
     int64_t s = P.shape[d];
     coord[d] = (int32_t)(lin % s);
     lin /= s;
+  }
+}
+
+// B bytes (4, 8, 16 or 32; B-aligned) into the first B/4 words of w.
+template <int B>
+__device__ __forceinline__ void load_words(const char* p, uint32_t* w) {
+  if constexpr (B >= 16) {
+#pragma unroll
+    for (int q = 0; q < B / 16; ++q) {
+      const u32x4v a = *(const u32x4v*)(p + 16 * q);
+      w[4 * q] = a.x, w[4 * q + 1] = a.y, w[4 * q + 2] = a.z, w[4 * q + 3] = a.w;
+    }
+  } else if constexpr (B == 8) {
+    const u32x2v a = *(const u32x2v*)p;
+    w[0] = a.x, w[1] = a.y;
+  } else {
+    w[0] = *(const uint32_t*)p;
   }
 }
 
@@ -206,54 +225,58 @@ __device__ __forceinline__ void load_leaf(const EwLeaf& L, int64_t lin, const in
 #pragma unroll
       for (int e = 0; e < V; ++e) r[e] = x;
     } else if (L.vmode == EW_VEC_CONTIG) {
-      // V elements of ≤ 4 bytes, aligned to V·size (checked by the launcher); read as 4-byte words
+      // V elements of ≤ 4 bytes, aligned to V·size (checked by the launcher); one switch on the element type, then
+      // straight-line decoding of the V elements (no per-element branches)
       static_assert(V == 4 || V == 8, "vector leaf loads are written for 4 or 8 elements");
       const char* p = (const char*)L.ptr;
-      const int es = L.dtype == DT_F32 || L.dtype == DT_S32 || L.dtype == DT_U32 ? 4
-                     : (L.dtype == DT_BF16 || L.dtype == DT_F16 || L.dtype == DT_S16 || L.dtype == DT_U16 ? 2 : 1);
-      uint32_t w[V];  // the first V·es/4 words hold the elements
-      if (es == 4) {
-        const u32x4v a = *(const u32x4v*)(p + off * 4);
-        w[0] = a.x, w[1] = a.y, w[2] = a.z, w[3] = a.w;
-        if constexpr (V == 8) {
-          const u32x4v b = *(const u32x4v*)(p + off * 4 + 16);
-          w[4] = b.x, w[5] = b.y, w[6] = b.z, w[7] = b.w;
-        }
-      } else if (es == 2) {
-        if constexpr (V == 8) {
-          const u32x4v a = *(const u32x4v*)(p + off * 2);
-          w[0] = a.x, w[1] = a.y, w[2] = a.z, w[3] = a.w;
-        } else {
-          const u32x2v a = *(const u32x2v*)(p + off * 2);
-          w[0] = a.x, w[1] = a.y;
-        }
-      } else {
-        if constexpr (V == 8) {
-          const u32x2v a = *(const u32x2v*)(p + off);
-          w[0] = a.x, w[1] = a.y;
-        } else {
-          w[0] = *(const uint32_t*)(p + off);
-        }
-      }
+      uint32_t w[V];
+      switch (L.dtype) {
+        case DT_F32: case DT_S32: case DT_U32:
+          load_words<V * 4>(p + off * 4, w);
 #pragma unroll
-      for (int e = 0; e < V; ++e) {
-        if (es == 4) {
-          r[e] = w[e];
-        } else if (es == 2) {
-          const uint32_t h = (w[e >> 1] >> (16 * (e & 1))) & 0xffffu;
-          if (L.dtype == DT_BF16) r[e] = h << 16;
-          else if (L.dtype == DT_F16) r[e] = __float_as_uint((float)__builtin_bit_cast(_Float16, (uint16_t)h));
-          else if (L.dtype == DT_S16) r[e] = (uint32_t)(int32_t)(int16_t)h;
-          else r[e] = h;
-        } else {
-          const uint32_t byte = (w[e >> 2] >> (8 * (e & 3))) & 0xffu;
-          switch (L.dtype) {
-            case DT_F8E4M3FN: r[e] = __float_as_uint(e4m3fn_bits_to_f32(byte)); break;
-            case DT_F8E5M2: r[e] = __float_as_uint(e5m2_bits_to_f32(byte)); break;
-            case DT_S8: r[e] = (uint32_t)(int32_t)(int8_t)byte; break;
-            default: r[e] = byte; break;
-          }
-        }
+          for (int e = 0; e < V; ++e) r[e] = w[e];
+          break;
+        case DT_BF16:
+          load_words<V * 2>(p + off * 2, w);
+#pragma unroll
+          for (int e = 0; e < V; ++e) r[e] = (e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16);
+          break;
+        case DT_F16:
+          load_words<V * 2>(p + off * 2, w);
+#pragma unroll
+          for (int e = 0; e < V; ++e)
+            r[e] = __float_as_uint((float)__builtin_bit_cast(_Float16, (uint16_t)(w[e >> 1] >> (16 * (e & 1)))));
+          break;
+        case DT_S16:
+          load_words<V * 2>(p + off * 2, w);
+#pragma unroll
+          for (int e = 0; e < V; ++e) r[e] = (uint32_t)(int32_t)(int16_t)(w[e >> 1] >> (16 * (e & 1)));
+          break;
+        case DT_U16:
+          load_words<V * 2>(p + off * 2, w);
+#pragma unroll
+          for (int e = 0; e < V; ++e) r[e] = (w[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+          break;
+        case DT_F8E4M3FN:
+          load_words<V>(p + off, w);
+#pragma unroll
+          for (int e = 0; e < V; ++e) r[e] = __float_as_uint(e4m3fn_bits_to_f32((w[e >> 2] >> (8 * (e & 3))) & 0xffu));
+          break;
+        case DT_F8E5M2:
+          load_words<V>(p + off, w);
+#pragma unroll
+          for (int e = 0; e < V; ++e) r[e] = __float_as_uint(e5m2_bits_to_f32((w[e >> 2] >> (8 * (e & 3))) & 0xffu));
+          break;
+        case DT_S8:
+          load_words<V>(p + off, w);
+#pragma unroll
+          for (int e = 0; e < V; ++e) r[e] = (uint32_t)(int32_t)(int8_t)(w[e >> 2] >> (8 * (e & 3)));
+          break;
+        default:  // u8, pred
+          load_words<V>(p + off, w);
+#pragma unroll
+          for (int e = 0; e < V; ++e) r[e] = (w[e >> 2] >> (8 * (e & 3))) & 0xffu;
+          break;
       }
     } else {
 #pragma unroll
@@ -316,13 +339,66 @@ __device__ __forceinline__ int ew_nsrc(int op) {
   return 1;
 }
 
+// Operations with long instruction sequences, evaluated one element at a time from a single copy of their code (the
+// interpreter's other operations are unrolled over its V elements).
+__device__ __noinline__ uint32_t ew_heavy(int op, uint32_t a, uint32_t b, int round) {
+  const float fa = __uint_as_float(a), fb = __uint_as_float(b);
+  const int32_t ia = (int32_t)a, ib = (int32_t)b;
+  switch (op) {
+    case EW_LOG: return __float_as_uint(logf(fa));
+    case EW_TANH: return __float_as_uint(tanhf(fa));
+    case EW_EXPM1: return __float_as_uint(expm1f(fa));
+    case EW_LOG1P: return __float_as_uint(log1pf(fa));
+    case EW_CVT_F2I: return (uint32_t)f2i_sat(fa, round);
+    case EW_POW: return __float_as_uint(powf(fa, fb));
+    case EW_REM: return __float_as_uint(fmodf(fa, fb));
+    case EW_IDIV: return (uint32_t)(ib == 0 ? -1 : (ia == (int32_t)0x80000000 && ib == -1) ? ia : ia / ib);
+    case EW_IREM: return (uint32_t)(ib == 0 ? ia : (ib == -1 ? 0 : ia % ib));
+    case EW_UDIV: return b == 0 ? 0xffffffffu : a / b;
+    case EW_UREM: return b == 0 ? a : a % b;
+    default: return 0u;
+  }
+}
+
 // Runs the program on V consecutive elements of the innermost dimension (linear indices lin .. lin+V-1, all in one
 // innermost row; `coord` are the coordinates of `lin`). `acc` holds the GEMM accumulators (bits) for EW_ACC (V = 1
-// only). Results land in the register file R. The instruction dispatch is uniform across the wave, so its cost is
+// only unless the values are row-uniform). Instructions [pc_begin, pc_end) run (pc_end < 0: to the end). Results
+// land in the register file R. The instruction dispatch is uniform across the wave, so its cost is
 // paid once per V elements.
+// The instruction and leaf tables of a program staged in LDS by the kernels that interpret it many times: a
+// uniform LDS read (then readfirstlane into scalar registers) per instruction instead of a scalar load from the
+// kernel-argument segment, whose latency the interpreter's dependent dispatch chain cannot hide.
+struct EwTables {
+  EwInstr instr[EW_MAX_INSTR];
+  EwLeaf leaves[EW_MAX_LEAVES];
+};
+
+// Copies P's tables into `T` (LDS); every thread of the workgroup takes part, the caller synchronises.
+__device__ __forceinline__ void stage_tables(const EwProgram& P, EwTables* T) {
+  static_assert(sizeof(EwInstr) % 4 == 0 && sizeof(EwLeaf) % 4 == 0, "tables are copied as 32-bit words");
+  const uint32_t* si = (const uint32_t*)P.instr;
+  uint32_t* di = (uint32_t*)T->instr;
+  const int ni = P.n_instr * (int)(sizeof(EwInstr) / 4);
+  for (int i = threadIdx.x; i < ni; i += blockDim.x) di[i] = si[i];
+  const uint32_t* sl = (const uint32_t*)P.leaves;
+  uint32_t* dl = (uint32_t*)T->leaves;
+  const int nl = P.n_leaves * (int)(sizeof(EwLeaf) / 4);
+  for (int i = threadIdx.x; i < nl; i += blockDim.x) dl[i] = sl[i];
+}
+
+template <typename T>
+__device__ __forceinline__ T uniform_read(const T* p) {
+  static_assert(sizeof(T) % 4 == 0, "uniform reads move 32-bit words");
+  struct W { uint32_t w[sizeof(T) / 4]; } v;
+  const uint32_t* s = (const uint32_t*)p;
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(T) / 4); ++i) v.w[i] = __builtin_amdgcn_readfirstlane(s[i]);
+  return __builtin_bit_cast(T, v);
+}
+
 template <int V, typename RF>
 __device__ __forceinline__ void ew_run_v(const EwProgram& P, int64_t lin, const int32_t* coord, const uint32_t* acc,
-                                         RF& R) {
+                                         RF& R, int pc_begin = 0, int pc_end = -1, const EwTables* T = nullptr) {
 #define EW_FOR _Pragma("unroll") for (int e = 0; e < V; ++e)
 #define EW_FA __uint_as_float(ra[e])
 #define EW_FB __uint_as_float(rb[e])
@@ -332,39 +408,44 @@ __device__ __forceinline__ void ew_run_v(const EwProgram& P, int64_t lin, const 
 #define EW_UB (rb[e])
 #define EW_F(OP, EXPR) case OP: EW_FOR r[e] = __float_as_uint(EXPR); break;
 #define EW_U(OP, EXPR) case OP: EW_FOR r[e] = (uint32_t)(EXPR); break;
-  EwInstr next = P.instr[0];
-  for (int pc = 0; pc < P.n_instr; ++pc) {
+#define EW_HEAVY(OP) case OP: _Pragma("unroll 1") for (int e = 0; e < V; ++e) r[e] = ew_heavy(OP, ra[e], rb[e], I.round); break;
+  const int end = pc_end < 0 ? P.n_instr : pc_end;
+  EwInstr next = T ? uniform_read(&T->instr[pc_begin]) : P.instr[pc_begin];
+  for (int pc = pc_begin; pc < end; ++pc) {
     const EwInstr I = next;
-    if (pc + 1 < P.n_instr) next = P.instr[pc + 1];  // requested while this instruction executes
+    if (pc + 1 < end) next = T ? uniform_read(&T->instr[pc + 1]) : P.instr[pc + 1];  // requested while I executes
     uint32_t r[V], ra[V], rb[V], rc[V];
     const int nsrc = ew_nsrc(I.op);
     if (nsrc >= 1) R.load(I.a, ra);
     if (nsrc >= 2) R.load(I.b, rb);
     if (nsrc >= 3) R.load(I.c, rc);
     switch (I.op) {
-      case EW_LOAD: load_leaf<V>(P.leaves[I.a], lin, coord, P.rank, r); break;
+      case EW_LOAD:
+        if (T) load_leaf<V>(uniform_read(&T->leaves[I.a]), lin, coord, P.rank, r);
+        else load_leaf<V>(P.leaves[I.a], lin, coord, P.rank, r);
+        break;
       EW_U(EW_CONST, I.imm.u)
       EW_U(EW_IOTA, coord[I.a] + (I.a == P.rank - 1 ? e : 0))
       EW_U(EW_ACC, acc[I.a])
       EW_F(EW_NEG, -EW_FA)
       EW_F(EW_ABS, fabsf(EW_FA))
       EW_F(EW_EXP, expf(EW_FA))
-      EW_F(EW_LOG, logf(EW_FA))
+      EW_HEAVY(EW_LOG)
       EW_F(EW_RSQRT, 1.0f / sqrtf(EW_FA))
       EW_F(EW_SQRT, sqrtf(EW_FA))
-      EW_F(EW_TANH, tanhf(EW_FA))
+      EW_HEAVY(EW_TANH)
       EW_F(EW_LOGISTIC, 1.0f / (1.0f + expf(-EW_FA)))
       EW_F(EW_FLOOR, floorf(EW_FA))
       EW_F(EW_CEIL, ceilf(EW_FA))
       EW_F(EW_SIGN, EW_FA != EW_FA ? EW_FA : (EW_FA > 0.f ? 1.f : (EW_FA < 0.f ? -1.f : EW_FA)))
-      EW_F(EW_EXPM1, expm1f(EW_FA))
-      EW_F(EW_LOG1P, log1pf(EW_FA))
+      EW_HEAVY(EW_EXPM1)
+      EW_HEAVY(EW_LOG1P)
       EW_U(EW_INEG, -EW_IA)
       EW_U(EW_IABS, EW_IA < 0 ? -EW_IA : EW_IA)
       EW_U(EW_NOT, (I.round == DT_PRED) ? (uint32_t)(EW_IA == 0) : ~EW_UA)
       EW_U(EW_ISIGN, EW_IA > 0 ? 1 : (EW_IA < 0 ? -1 : 0))
       EW_F(EW_CVT_F2F, EW_FA)
-      EW_U(EW_CVT_F2I, f2i_sat(EW_FA, I.round))
+      EW_HEAVY(EW_CVT_F2I)
       EW_F(EW_CVT_I2F, I.imm.i ? (float)EW_UA : (float)EW_IA)  // imm: source unsigned
       EW_U(EW_CVT_I2I, EW_UA)
       EW_U(EW_CVT_F2P, EW_FA != 0.0f)
@@ -375,15 +456,15 @@ __device__ __forceinline__ void ew_run_v(const EwProgram& P, int64_t lin, const 
       EW_F(EW_DIV, EW_FA / EW_FB)
       EW_F(EW_MAX, (EW_FA != EW_FA || EW_FB != EW_FB) ? __uint_as_float(0x7fc00000u) : fmaxf(EW_FA, EW_FB))
       EW_F(EW_MIN, (EW_FA != EW_FA || EW_FB != EW_FB) ? __uint_as_float(0x7fc00000u) : fminf(EW_FA, EW_FB))
-      EW_F(EW_POW, powf(EW_FA, EW_FB))
-      EW_F(EW_REM, fmodf(EW_FA, EW_FB))
+      EW_HEAVY(EW_POW)
+      EW_HEAVY(EW_REM)
       EW_U(EW_IADD, EW_IA + EW_IB)
       EW_U(EW_ISUB, EW_IA - EW_IB)
       EW_U(EW_IMUL, EW_IA * EW_IB)
-      EW_U(EW_IDIV, EW_IB == 0 ? -1 : (EW_IA == (int32_t)0x80000000 && EW_IB == -1) ? EW_IA : EW_IA / EW_IB)
-      EW_U(EW_IREM, EW_IB == 0 ? EW_IA : (EW_IB == -1 ? 0 : EW_IA % EW_IB))
-      EW_U(EW_UDIV, EW_UB == 0 ? 0xffffffffu : EW_UA / EW_UB)
-      EW_U(EW_UREM, EW_UB == 0 ? EW_UA : EW_UA % EW_UB)
+      EW_HEAVY(EW_IDIV)
+      EW_HEAVY(EW_IREM)
+      EW_HEAVY(EW_UDIV)
+      EW_HEAVY(EW_UREM)
       EW_U(EW_IMAX, EW_IA > EW_IB ? EW_IA : EW_IB)
       EW_U(EW_IMIN, EW_IA < EW_IB ? EW_IA : EW_IB)
       EW_U(EW_UMAX, EW_UA > EW_UB ? EW_UA : EW_UB)
@@ -400,12 +481,29 @@ __device__ __forceinline__ void ew_run_v(const EwProgram& P, int64_t lin, const 
       default: EW_FOR r[e] = 0; break;
     }
     // per-op rounding to the StableHLO result element type
-    if (I.round) {
-      if (dt_is_float(I.round)) {
-        EW_FOR r[e] = __float_as_uint(round_float(__uint_as_float(r[e]), I.round));
-      } else {
-        EW_FOR r[e] = (uint32_t)wrap_int((int32_t)r[e], I.round);
-      }
+    // (one switch on the type, then straight-line code over the V elements)
+    switch (I.round) {
+      case 0: case DT_F32: case DT_S32: case DT_U32: break;
+      case DT_BF16:
+        if constexpr (V % 2 == 0) {
+#pragma unroll
+          for (int e = 0; e < V; e += 2) {
+            const uint32_t pk = f32x2_to_bf16x2_bits(__uint_as_float(r[e]), __uint_as_float(r[e + 1]));
+            r[e] = pk << 16, r[e + 1] = pk & 0xffff0000u;
+          }
+        } else {
+          EW_FOR r[e] = (uint32_t)f32_to_bf16_bits(__uint_as_float(r[e])) << 16;
+        }
+        break;
+      case DT_F16: EW_FOR r[e] = __float_as_uint((float)(_Float16)__uint_as_float(r[e])); break;
+      case DT_F8E4M3FN: EW_FOR r[e] = __float_as_uint(e4m3fn_bits_to_f32(f32_to_e4m3fn_bits(__uint_as_float(r[e])))); break;
+      case DT_F8E5M2: EW_FOR r[e] = __float_as_uint(e5m2_bits_to_f32(f32_to_e5m2_bits(__uint_as_float(r[e])))); break;
+      case DT_S8: EW_FOR r[e] = (uint32_t)(int32_t)(int8_t)r[e]; break;
+      case DT_S16: EW_FOR r[e] = (uint32_t)(int32_t)(int16_t)r[e]; break;
+      case DT_U8: EW_FOR r[e] = r[e] & 0xffu; break;
+      case DT_U16: EW_FOR r[e] = r[e] & 0xffffu; break;
+      case DT_PRED: EW_FOR r[e] = r[e] != 0u; break;
+      default: break;
     }
     R.store(I.dst, r);
   }
@@ -418,6 +516,7 @@ __device__ __forceinline__ void ew_run_v(const EwProgram& P, int64_t lin, const 
 #undef EW_UB
 #undef EW_F
 #undef EW_U
+#undef EW_HEAVY
 }
 
 // Scalar form (one element): used by the generic GEMM epilogue and the unvectorised kernels.

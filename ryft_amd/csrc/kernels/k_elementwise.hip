@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <string>
+#include <type_traits>
 
 #include "../common.h"
 #include "ew_device.h"
@@ -100,6 +101,9 @@ __device__ __forceinline__ void decompose_fast(int64_t lin, const EwProgram& P, 
 
 template <bool COORDS>
 __global__ void __launch_bounds__(VNT) ew_kernel_vec(const EwProgram P) {
+  __shared__ EwTables T;
+  stage_tables(P, &T);
+  __syncthreads();
   VRegs R;
   const int64_t chunks = P.total / VEC;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -107,7 +111,7 @@ __global__ void __launch_bounds__(VNT) ew_kernel_vec(const EwProgram P) {
     const int64_t lin = c * VEC;
     int32_t coord[EW_MAX_RANK];
     if (COORDS) decompose_fast(lin, P, coord);
-    ew_run_v<VEC>(P, lin, coord, nullptr, R);
+    ew_run_v<VEC>(P, lin, coord, nullptr, R, 0, -1, &T);
     for (int o = 0; o < P.n_out; ++o) {
       uint32_t v[VEC];
       R.load(P.out_reg[o], v);
@@ -247,8 +251,11 @@ __device__ __forceinline__ uint32_t red_identity(int kind, bool fl) {
 template <int G, bool COORDS>
 __global__ void __launch_bounds__(VNT) reduce_kernel_vec(const ReduceArgs A) {
   __shared__ uint32_t part[VNT / 64];
+  __shared__ EwTables T;
   VRegs R;
   const EwProgram& P = A.prologue;
+  stage_tables(P, &T);
+  __syncthreads();
   constexpr int RB = VNT / G;  // rows per workgroup
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = threadIdx.x / G, t = threadIdx.x % G;
@@ -262,7 +269,7 @@ __global__ void __launch_bounds__(VNT) reduce_kernel_vec(const ReduceArgs A) {
       const int64_t lin = o * A.inner + c * VEC;
       int32_t coord[EW_MAX_RANK];
       if (COORDS) decompose_fast(lin, P, coord);
-      ew_run_v<VEC>(P, lin, coord, nullptr, R);
+      ew_run_v<VEC>(P, lin, coord, nullptr, R, 0, -1, &T);
       uint32_t v[VEC];
       R.load(P.out_reg[0], v);
 #pragma unroll
@@ -309,6 +316,229 @@ void launch_reduce(const ReduceArgs& a, hipStream_t stream) {
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) fail(PJRT_Error_Code_INTERNAL, std::string("reduce launch failed: ") + hipGetErrorString(e));
+}
+
+}  // namespace ryft
+
+namespace ryft {
+
+// ------------------------------------------------------------------------------------------------ row fusion
+// G threads per row (VNT: a workgroup per row, for long rows; 64: a wavefront per row), V consecutive elements per
+// program run. Each reduction folds its phase's value over the row within the thread, across lanes with shuffles and
+// across wavefronts through LDS; every thread of the row then holds the same row value (one association order,
+// broadcast from lane 0 / read from LDS in wave order), combines the init value and rounds to the reduce's type.
+// The consumer phase reads the row values through EW_ACC. Rows are short enough to stay in L2 between phases.
+template <int G, int V, bool COORDS>
+__global__ void __launch_bounds__(VNT) row_kernel(const RowArgs A) {
+  __shared__ uint32_t part[VNT / 64];
+  __shared__ EwTables T;
+  typename std::conditional<V == 1, RegFile1, SwitchRegFile<V>>::type R;
+  const EwProgram& P = A.prog;
+  stage_tables(P, &T);
+  __syncthreads();
+  constexpr int RB = VNT / G;  // rows per workgroup
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = threadIdx.x / G, t = threadIdx.x % G;
+  const int64_t chunks = A.inner / V;
+  for (int64_t o = (int64_t)blockIdx.x * RB + g; o < A.rows; o += (int64_t)gridDim.x * RB) {
+    uint32_t rv[ROW_MAX_RED] = {0u, 0u};
+    // passes 0 .. n_red-1 fold the reductions, pass n_red runs the consumer; one program-run site keeps the
+    // interpreter's code once in the instruction cache
+    for (int k = 0; k <= A.n_red; ++k) {
+      const bool red = k < A.n_red;
+      const bool fl = red && A.is_float[k] != 0;
+      const int kind = red ? A.kind[k] : 0;
+      const int pb = k == 0 ? 0 : A.phase_end[k - 1], pe = A.phase_end[k];
+      uint32_t acc = red ? red_identity(kind, fl) : 0u;
+      for (int64_t c = t; c < chunks; c += G) {
+        const int64_t lin = o * A.inner + c * V;
+        int32_t coord[EW_MAX_RANK];
+        if (COORDS) decompose_fast(lin, P, coord);
+        ew_run_v<V>(P, lin, coord, rv, R, pb, pe, &T);
+        if (red) {
+          uint32_t v[V];
+          R.load(A.red_reg[k], v);
+#pragma unroll
+          for (int e = 0; e < V; ++e) acc = red_combine(acc, v[e], kind, fl);
+        } else {
+          for (int q = 0; q < P.n_out; ++q) {
+            uint32_t v[V];
+            R.load(P.out_reg[q], v);
+            if constexpr (V == 1) store_bits(P.out_ptr[q], lin, P.out_dtype[q], v[0], (P.out_float_mask >> q) & 1);
+            else store_vec<V>(P.out_ptr[q], lin, P.out_dtype[q], v, (P.out_float_mask >> q) & 1);
+          }
+        }
+      }
+      if (!red) break;
+      for (int off = 32; off > 0; off >>= 1) acc = red_combine(acc, (uint32_t)__shfl_xor((int)acc, off, 64), kind, fl);
+      acc = (uint32_t)__shfl((int)acc, 0, 64);
+      if constexpr (G == VNT) {
+        if (lane == 0) part[wave] = acc;
+        __syncthreads();
+        acc = part[0];
+        for (int w = 1; w < VNT / 64; ++w) acc = red_combine(acc, part[w], kind, fl);
+        __syncthreads();  // part[] is reused by the next reduction
+      }
+      acc = red_combine(acc, A.init[k], kind, fl);
+      const uint32_t val = fl ? __float_as_uint(round_float(__uint_as_float(acc), A.red_dtype[k]))
+                              : (uint32_t)wrap_int((int32_t)acc, A.red_dtype[k]);
+      if (k == 0) rv[0] = val;
+      else rv[1] = val;
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------ row-norm path
+// Eight consecutive elements of a float row as f32 (f32, bf16 or f16 storage; 16-byte aligned groups).
+__device__ __forceinline__ void load8_f32(const void* p, int64_t i, int dt, float* v) {
+  const char* c = (const char*)p;
+  if (dt == DT_F32) {
+    const u32x4v a = *(const u32x4v*)(c + i * 4), b = *(const u32x4v*)(c + i * 4 + 16);
+    v[0] = __uint_as_float(a.x), v[1] = __uint_as_float(a.y), v[2] = __uint_as_float(a.z), v[3] = __uint_as_float(a.w);
+    v[4] = __uint_as_float(b.x), v[5] = __uint_as_float(b.y), v[6] = __uint_as_float(b.z), v[7] = __uint_as_float(b.w);
+  } else {
+    const u32x4v a = *(const u32x4v*)(c + i * 2);
+    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (dt == DT_BF16) {
+        v[2 * q] = __uint_as_float(w[q] << 16), v[2 * q + 1] = __uint_as_float(w[q] & 0xffff0000u);
+      } else {
+        v[2 * q] = (float)__builtin_bit_cast(_Float16, (uint16_t)w[q]);
+        v[2 * q + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[q] >> 16));
+      }
+    }
+  }
+}
+
+// One workgroup per row. A thread owns chunks t, t + 256, ... of 8 elements; with NC > 0 (rows of at most NC·2048
+// elements) it loads them — and the matching weight chunks — once, up front, and keeps them in registers; NC = 0
+// reads the row again (from L2) for the scaling pass. Σx² is folded per thread in element order, then across lanes
+// and wavefronts in the same order as the interpreted row kernel, so both paths give the same bits. Products and
+// sums are separately rounded f32 operations (no contraction into FMAs), as the program specifies.
+template <int NC>
+__global__ void __launch_bounds__(VNT) rownorm_kernel(const RowArgs A) {
+#pragma clang fp contract(off)
+  __shared__ float part[VNT / 64];
+  const RowNormArgs& N = A.norm;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t chunks = A.inner / 8;
+  const float init = __uint_as_float(A.init[0]);
+  for (int64_t o = blockIdx.x; o < A.rows; o += gridDim.x) {
+    const int64_t base = o * A.inner;
+    float acc = 0.0f;
+    float xs[NC > 0 ? NC : 1][8], ws[NC > 0 ? NC : 1][8];
+    if constexpr (NC > 0) {
+#pragma unroll
+      for (int q = 0; q < NC; ++q) {
+        const int64_t c = threadIdx.x + (int64_t)q * VNT;
+        if (c < chunks) {
+          load8_f32(N.x, base + c * 8, N.x_dtype, xs[q]);
+          if (N.w) load8_f32(N.w, c * 8, N.w_dtype, ws[q]);
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < NC; ++q)
+        if (threadIdx.x + (int64_t)q * VNT < chunks) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc = acc + xs[q][e] * xs[q][e];
+        }
+    } else {
+      for (int64_t c = threadIdx.x; c < chunks; c += VNT) {
+        float v[8];
+        load8_f32(N.x, base + c * 8, N.x_dtype, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc = acc + v[e] * v[e];
+      }
+    }
+    for (int off = 32; off > 0; off >>= 1) acc = acc + __shfl_xor(acc, off, 64);
+    acc = __shfl(acc, 0, 64);
+    if (lane == 0) part[wave] = acc;
+    __syncthreads();
+    acc = part[0];
+    for (int w = 1; w < VNT / 64; ++w) acc = acc + part[w];
+    __syncthreads();
+    acc = acc + init;
+    float t = N.alpha_div ? acc / N.alpha : acc * N.alpha;
+    t = t + N.eps;
+    const float s = 1.0f / sqrtf(t);
+    auto emit = [&](int64_t c, const float* v, const float* wv) {
+      uint32_t b[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float y = v[e] * s;
+        if (N.w) y = y * wv[e];
+        b[e] = __float_as_uint(round_float(y, N.mid_round));
+      }
+      store_vec<8>(N.out, base + c * 8, N.out_dtype, b, true);
+    };
+    if constexpr (NC > 0) {
+#pragma unroll
+      for (int q = 0; q < NC; ++q) {
+        const int64_t c = threadIdx.x + (int64_t)q * VNT;
+        if (c < chunks) emit(c, xs[q], ws[q]);
+      }
+    } else {
+      for (int64_t c = threadIdx.x; c < chunks; c += VNT) {
+        float v[8], wv[8];
+        load8_f32(N.x, base + c * 8, N.x_dtype, v);
+        if (N.w) load8_f32(N.w, c * 8, N.w_dtype, wv);
+        emit(c, v, wv);
+      }
+    }
+  }
+}
+
+static bool rownorm_launchable(const RowArgs& a) {
+  const RowNormArgs& n = a.norm;
+  auto float_ok = [](int dt) { return dt == DT_F32 || dt == DT_BF16 || dt == DT_F16; };
+  auto aligned = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+  return a.inner % 8 == 0 && float_ok(n.x_dtype) && (!n.w || float_ok(n.w_dtype)) && aligned(n.x) &&
+         (!n.w || aligned(n.w)) && ((uintptr_t)n.out % (uintptr_t)(8 * elem_size(n.out_dtype))) == 0 &&
+         (n.out_dtype == DT_F32 || n.out_dtype == DT_BF16 || n.out_dtype == DT_F16 || n.out_dtype == DT_F8E4M3FN ||
+          n.out_dtype == DT_F8E5M2);
+}
+
+template <int G, int V>
+static void launch_row_g(const RowArgs& a, hipStream_t stream) {
+  constexpr int RB = VNT / G;
+  int64_t blocks = (a.rows + RB - 1) / RB;
+  if (blocks > 256 * 16) blocks = 256 * 16;
+  dim3 grid((unsigned)blocks), block(VNT);
+  if (a.prog.needs_coords) hipLaunchKernelGGL((row_kernel<G, V, true>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((row_kernel<G, V, false>), grid, block, 0, stream, a);
+}
+
+void launch_row(const RowArgs& a, hipStream_t stream) {
+  if (a.rows == 0 || a.inner == 0) return;
+  if (a.n_red < 1 || a.n_red > ROW_MAX_RED || a.prog.rank < 1 || a.prog.shape[a.prog.rank - 1] != a.inner ||
+      a.rows * a.inner != a.prog.total)
+    fail(PJRT_Error_Code_INTERNAL, "row-fused step: arguments do not describe a [rows, inner] space");
+  for (int k = 0; k <= a.n_red; ++k)
+    if (a.phase_end[k] < (k ? a.phase_end[k - 1] : 0) || a.phase_end[k] > a.prog.n_instr)
+      fail(PJRT_Error_Code_INTERNAL, "row-fused step: phase bounds outside the program");
+  if (a.fast == ROW_FAST_NORM && rownorm_launchable(a)) {
+    const int64_t blocks = a.rows < 256 * 16 ? a.rows : 256 * 16;
+    const int64_t per_thread = (a.inner / 8 + VNT - 1) / VNT;
+    const dim3 grid((unsigned)blocks), block(VNT);
+    if (per_thread <= 1) hipLaunchKernelGGL(rownorm_kernel<1>, grid, block, 0, stream, a);
+    else if (per_thread <= 2) hipLaunchKernelGGL(rownorm_kernel<2>, grid, block, 0, stream, a);
+    else if (per_thread <= 4) hipLaunchKernelGGL(rownorm_kernel<4>, grid, block, 0, stream, a);
+    else hipLaunchKernelGGL(rownorm_kernel<0>, grid, block, 0, stream, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) fail(PJRT_Error_Code_INTERNAL, std::string("row-norm launch failed: ") + hipGetErrorString(e));
+    return;
+  }
+  RowArgs v = a;
+  if (prepare_vec(v.prog, true)) {
+    if (a.inner / VEC >= VNT) launch_row_g<VNT, VEC>(v, stream);
+    else launch_row_g<64, VEC>(v, stream);
+  } else {
+    if (a.inner >= 4 * VNT) launch_row_g<VNT, 1>(a, stream);
+    else launch_row_g<64, 1>(a, stream);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) fail(PJRT_Error_Code_INTERNAL, std::string("row-fused launch failed: ") + hipGetErrorString(e));
 }
 
 }  // namespace ryft

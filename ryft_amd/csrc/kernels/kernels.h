@@ -10,6 +10,7 @@ namespace ryft {
 
 void launch_elementwise(const EwProgram& p, hipStream_t stream);
 void launch_reduce(const ReduceArgs& a, hipStream_t stream);
+void launch_row(const RowArgs& a, hipStream_t stream);
 void launch_gemm(const GemmArgs& a, hipStream_t stream);
 void launch_attention(const AttnArgs& a, hipStream_t stream);
 

@@ -208,18 +208,22 @@ PJRT_Error* Client_Create(PJRT_Client_Create_Args* args) {
   NEED_ARGS(PJRT_Client_Create_Args, client);
   API_TRY
   // Recognised options: visible_devices (int64 list, as GpuClientOptions, clients.rs:453-573) and compile_only
-  // (bool, plugin-specific: plans are built but nothing runs). Others are ignored.
+  // (bool, plugin-specific: plans are built but nothing runs), fast_paths (bool, plugin-specific, default true:
+  // false runs every row-fused step through the interpreted kernel, for cross-checks). Others are ignored.
   std::vector<int> visible;
-  bool compile_only = false;
+  bool compile_only = false, fast_paths = true;
   for (size_t i = 0; i < args->num_options; ++i) {
     const PJRT_NamedValue& o = args->create_options[i];
     std::string name(o.name, o.name_size);
     if (name == "visible_devices" && o.type == PJRT_NamedValue_kInt64List)
       for (size_t k = 0; k < o.value_size; ++k) visible.push_back((int)o.int64_array_value[k]);
     if (name == "compile_only" && o.type == PJRT_NamedValue_kBool) compile_only = o.bool_value;
+    if (name == "fast_paths" && o.type == PJRT_NamedValue_kBool) fast_paths = o.bool_value;
   }
   std::lock_guard<std::mutex> lk(g_client_mu);
-  args->client = to<PJRT_Client>(new Client(visible, compile_only));
+  Client* c = new Client(visible, compile_only);
+  c->fast_paths = fast_paths;
+  args->client = to<PJRT_Client>(c);
   API_CATCH
 }
 PJRT_Error* Client_Destroy(PJRT_Client_Destroy_Args* args) {

@@ -87,6 +87,8 @@ class ExprBuilder {
   struct Val { int instr; bool is_float; };
 
   std::map<int, int> acc_nodes;  // nodes read as GEMM accumulators (epilogues)
+  std::map<int, int> row_nodes;  // reduce nodes read as row value k (row fusion), through the mapping row_src
+  std::vector<int> row_src;
   bool dry = false;              // dry run: record leaves, materialize nothing
   std::vector<std::pair<int, std::vector<int>>> dry_leaves;
   std::set<int> inner_nodes;     // elementwise nodes computed inside the program
@@ -95,6 +97,14 @@ class ExprBuilder {
   void add_output(Val v, DType dtype) { outputs_.push_back({v.instr, dtype}); }
   EwProgram finish();
   const std::vector<Leaf>& leaves() const { return leaves_; }
+  // Phases (row fusion): values computed in one phase are never read in another; `v` must stay in its register
+  // until the phase ends. Returns the index one past the phase's last instruction.
+  void begin_phase() { memo_.clear(); }
+  int end_phase(Val v) {
+    keep_.push_back({v.instr, (int)instrs_.size()});
+    return (int)instrs_.size();
+  }
+  int reg_of(Val v) const { return reg_.at(v.instr); }
   // expression structure, for epilogue classification
   const std::vector<EwInstr>& raw_instrs() const { return instrs_; }
   const std::vector<std::vector<int>>& raw_srcs() const { return srcs_; }
@@ -114,11 +124,13 @@ class ExprBuilder {
   std::map<std::pair<int, std::vector<int>>, Val> memo_;
   std::vector<std::pair<int, DType>> outputs_;
   std::vector<int> ident_;
+  std::vector<std::pair<int, int>> keep_;  // (instruction, keep its register until this instruction index)
+  std::vector<int> reg_;                   // register of each instruction (after finish)
 };
 
 class Planner {
  public:
-  explicit Planner(const Graph& g) : g_(g), users_(g.users()) {
+  Planner(const Graph& g, const PlanOptions& opts) : g_(g), opts_(opts), users_(g.users()) {
     for (int r : g.results) results_.insert(r);
   }
 
@@ -141,6 +153,9 @@ class Planner {
   int materialize(int node, int target = -1);
   void emit_elementwise_root(int node, int target);
   void emit_reduce(int node, int target);
+  bool try_row_fusion(int node, int target);
+  void classify_row(Step& st);
+  bool row_reducible(int reduce, const TensorType& space);
   void emit_dot(const std::vector<int>& dots, int target, int root);
   bool try_attention(int d2, int target, DType out_dtype, int root);
   void emit_copy(int src_slot, int64_t src_off, int dst_slot, size_t bytes);
@@ -153,6 +168,7 @@ class Planner {
   void classify_epilogue(Step& st, const std::vector<int>& unused);
 
   const Graph& g_;
+  PlanOptions opts_;
   std::vector<std::vector<int>> users_;
   std::set<int> results_;
   Plan plan_;
@@ -216,10 +232,16 @@ ExprBuilder::Val ExprBuilder::emit(int node, const std::vector<int>& src) {
   bool fl = float_class(dt);
   Val out;
   auto acc_it = acc_nodes.find(node);
+  auto row_it = row_nodes.find(node);
   if (acc_it != acc_nodes.end() && src == ident_) {
     EwInstr ins{};
     ins.op = EW_ACC;
     ins.a = (uint8_t)acc_it->second;
+    out = {push(ins, fl, {}), fl};
+  } else if (row_it != row_nodes.end() && src == row_src) {
+    EwInstr ins{};
+    ins.op = EW_ACC;
+    ins.a = (uint8_t)row_it->second;
     out = {push(ins, fl, {}), fl};
   } else if (n.op == Op::Constant && n.splat) {
     EwInstr ins{};
@@ -339,6 +361,7 @@ EwProgram ExprBuilder::finish() {
   for (int i = 0; i < n; ++i)
     for (int s : srcs_[i]) last[s] = std::max(last[s], i);
   for (auto& o : outputs_) last[o.first] = n + 1;
+  for (auto& k : keep_) last[k.first] = std::max(last[k.first], k.second);
   std::vector<int> reg(n, -1);
   std::vector<std::vector<int>> free_at(n + 2);
   std::vector<int> free_regs;
@@ -351,6 +374,7 @@ EwProgram ExprBuilder::finish() {
     int l = last[i] < 0 ? i + 1 : last[i];
     if (l <= n) free_at[l].push_back(i);
   }
+  reg_ = reg;
   p.n_instr = n;
   p.needs_coords = 0;
   for (int i = 0; i < n; ++i) {
@@ -528,6 +552,9 @@ void Planner::emit_elementwise_root(int node, int target) {
     }
   }
 
+  // Reductions over the innermost dim broadcast back into this expression → one row-fused launch.
+  if (try_row_fusion(node, target)) return;
+
   // Plain elementwise kernel; split the expression at its operands if it does not fit one program.
   for (int attempt = 0; attempt < 2; ++attempt) {
     try {
@@ -620,6 +647,241 @@ void Planner::emit_reduce(int node, int target) {
       materialize(x);
     }
   }
+}
+
+// A reduce that row fusion can run inside a consumer over `space`: it folds exactly the innermost dim of an operand
+// shaped like the consumer, starts from a constant init, and yields a 32-bit register type.
+bool Planner::row_reducible(int reduce, const TensorType& space) {
+  const Node& r = g_.nodes[reduce];
+  if (r.op != Op::Reduce || materialized(reduce) || r.operands.size() != 2) return false;
+  const Node& x = g_.nodes[r.operands[0]];
+  const int rank = space.rank();
+  if (x.type.shape != space.shape || r.dims.size() != 1 || r.dims[0] != rank - 1) return false;
+  double init;
+  if (!splat_value(r.operands[1], &init)) return false;
+  const DType t = r.type.dtype;
+  if (t == DType::F64 || t == DType::S64 || t == DType::U64) return false;
+  return float_class(x.type.dtype) == float_class(t);
+}
+
+// Row fusion: `node` (shape [rows..., inner]) reads reduce results over its innermost dim through a broadcast along
+// that dim. Those reductions (and the ones their operands read the same way, dependencies first, at most
+// ROW_MAX_RED) run in the same kernel as `node`, one row at a time.
+bool Planner::try_row_fusion(int node, int target) {
+  const Node& n = g_.nodes[node];
+  const int rank = n.type.rank();
+  if (rank < 1 || n.type.elements() == 0 || n.type.shape[rank - 1] < 2) return false;
+  std::vector<int> ident(rank), outer(rank - 1);
+  for (int d = 0; d < rank; ++d) ident[d] = d;
+  for (int d = 0; d + 1 < rank; ++d) outer[d] = d;
+  auto candidates = [&](int root) {
+    ExprBuilder dry(*this, n.type.shape);
+    dry.dry = true;
+    dry.emit(root, ident);
+    std::vector<int> out;
+    for (auto& l : dry.dry_leaves)
+      if (l.second == outer && row_reducible(l.first, n.type) &&
+          std::find(out.begin(), out.end(), l.first) == out.end())
+        out.push_back(l.first);
+    return out;
+  };
+  std::vector<int> order;
+  std::function<void(int, int)> visit = [&](int r, int depth) {
+    if (std::find(order.begin(), order.end(), r) != order.end() || depth > 8) return;
+    for (int r2 : candidates(g_.nodes[r].operands[0])) visit(r2, depth + 1);
+    if (std::find(order.begin(), order.end(), r) == order.end()) order.push_back(r);
+  };
+  for (int r : candidates(node)) visit(r, 0);
+  if (order.empty()) return false;
+  if (order.size() > ROW_MAX_RED) order.resize(ROW_MAX_RED);  // dependencies come first; the rest are leaves
+
+  try {
+    ExprBuilder b(*this, n.type.shape);
+    b.row_src = outer;
+    RowArgs ra{};
+    std::vector<ExprBuilder::Val> vals;
+    for (size_t k = 0; k < order.size(); ++k) {
+      const Node& r = g_.nodes[order[k]];
+      const Node& x = g_.nodes[r.operands[0]];
+      b.begin_phase();
+      ExprBuilder::Val v = b.emit(r.operands[0], ident);
+      ra.phase_end[k] = b.end_phase(v);
+      vals.push_back(v);
+      double init = 0;
+      splat_value(r.operands[1], &init);
+      ra.is_float[k] = float_class(x.type.dtype);
+      if (ra.is_float[k]) {
+        float f = (float)init;
+        memcpy(&ra.init[k], &f, 4);
+      } else {
+        ra.init[k] = (uint32_t)(int32_t)(int64_t)init;
+      }
+      switch (r.reduce_body) {
+        case ReduceBody::Add: ra.kind[k] = RED_ADD; break;
+        case ReduceBody::Max: ra.kind[k] = RED_MAX; break;
+        case ReduceBody::Min: ra.kind[k] = RED_MIN; break;
+        case ReduceBody::Mul: ra.kind[k] = RED_MUL; break;
+        case ReduceBody::And: ra.kind[k] = RED_AND; break;
+        case ReduceBody::Or: ra.kind[k] = RED_OR; break;
+      }
+      ra.red_dtype[k] = (int32_t)r.type.dtype;
+      b.row_nodes[order[k]] = (int)k;
+    }
+    b.begin_phase();
+    ExprBuilder::Val v = b.emit(node, ident);
+    b.add_output(v, n.type.dtype);
+    ra.phase_end[order.size()] = b.end_phase(v);
+    EwProgram p = b.finish();
+    ra.prog = p;
+    ra.n_red = (int32_t)order.size();
+    for (size_t k = 0; k < order.size(); ++k) ra.red_reg[k] = b.reg_of(vals[k]);
+    ra.inner = n.type.shape[rank - 1];
+    ra.rows = n.type.elements() / ra.inner;
+    int out = temp_or(target, n.type);
+    Step st{};
+    st.kind = Step::ROW;
+    st.name = "row_fused";
+    st.row = ra;
+    push_program_patches(st, offsetof(RowArgs, prog), p, b.leaves(), {out});
+    st.bytes = leaf_bytes(plan_, b.leaves()) + (double)n.type.bytes();
+    if (opts_.fast_paths) classify_row(st);
+    if (st.row.fast == ROW_FAST_NORM) st.name = "row_norm";
+    plan_.steps.push_back(std::move(st));
+    mat_[node] = out;
+    return true;
+  } catch (const Status& s) {
+    if (s.code != PJRT_Error_Code_RESOURCE_EXHAUSTED) throw;
+    return false;  // does not fit one program: the reductions run as their own launches
+  }
+}
+
+// Recognises a row-fused program of the form convert(x · rsqrt(Σx² · α + ε) · w) (RMSNorm: one f32 sum of squares
+// of the row being scaled, α and ε constants, w an optional row vector shared by all rows, f32 products, optional
+// rounding to a narrower float type before the output conversion) and points the step at the specialised kernel.
+// The interpreted program stays in the step; the launcher falls back to it when the fast path's alignment or type
+// requirements are not met.
+void Planner::classify_row(Step& st) {
+  RowArgs& A = st.row;
+  const EwProgram& p = A.prog;
+  float init;
+  memcpy(&init, &A.init[0], 4);
+  if (A.n_red != 1 || A.kind[0] != RED_ADD || !A.is_float[0] || A.red_dtype[0] != (int32_t)DType::F32 ||
+      p.n_out != 1 || init != 0.0f)
+    return;
+  struct E { int op; int a = -1, b = -1; int round = 0; int leaf = -1; int acc = -1; float imm = 0; };
+  std::vector<E> ex;
+  int regmap[EW_MAX_REGS];
+  for (auto& r : regmap) r = -1;
+  int v0 = -1;
+  for (int i = 0; i < p.n_instr; ++i) {
+    const EwInstr& I = p.instr[i];
+    E e;
+    e.op = I.op;
+    e.round = I.round;
+    if (I.op == EW_LOAD) e.leaf = I.a;
+    else if (I.op == EW_ACC) e.acc = I.a;
+    else if (I.op == EW_CONST) e.imm = I.imm.f;
+    else if (I.op == EW_IOTA) return;
+    else e.a = regmap[I.a], e.b = regmap[I.b];
+    ex.push_back(e);
+    regmap[I.dst] = (int)ex.size() - 1;
+    if (i + 1 == A.phase_end[0]) v0 = regmap[A.red_reg[0]];
+  }
+  if (v0 < 0) return;
+  const int root = regmap[p.out_reg[0]];
+  // x: an identity-mapped float leaf, read as f32 (possibly through an exact widening convert)
+  auto float_leaf = [&](int e) -> int {
+    if (ex[e].op == EW_CVT_F2F && ex[e].round == 0) e = ex[e].a;
+    if (ex[e].op != EW_LOAD) return -1;
+    const int dt = p.leaves[ex[e].leaf].dtype;
+    if (dt != (int)DType::F32 && dt != (int)DType::BF16 && dt != (int)DType::F16) return -1;
+    return ex[e].leaf;
+  };
+  if (ex[v0].op != EW_MUL || ex[v0].round != 0 || ex[v0].a != ex[v0].b) return;
+  const int lx = float_leaf(ex[v0].a);
+  if (lx < 0 || p.leaves[lx].kind != EW_LEAF_IDENTITY || p.leaves[lx].offset != 0) return;
+  // output conversions
+  int top = root, mid = 0;
+  if (ex[top].op == EW_CVT_F2F && (ex[top].round == p.out_dtype[0] || ex[top].round == 0)) top = ex[top].a;
+  if (ex[top].op == EW_CVT_F2F && ex[top].round != 0) { mid = ex[top].round; top = ex[top].a; }
+  while (ex[top].op == EW_CVT_F2F && ex[top].round == 0) top = ex[top].a;  // f32 → f32
+  // product x · s · w (any association of f32 products)
+  std::vector<int> fs;
+  std::function<void(int)> factors = [&](int e) {
+    if (ex[e].op == EW_MUL && ex[e].round == 0) { factors(ex[e].a); factors(ex[e].b); return; }
+    fs.push_back(e);
+  };
+  factors(top);
+  int sx = -1, ss = -1, sw = -1;
+  float alpha = 1.0f, eps = 0.0f;
+  int alpha_div = 0;
+  const int rank = p.rank;
+  for (int f : fs) {
+    if (sx < 0 && float_leaf(f) == lx) { sx = f; continue; }
+    if (ss < 0 && ex[f].op == EW_RSQRT && ex[f].round == 0) {
+      const E& add = ex[ex[f].a];
+      if (add.op != EW_ADD || add.round != 0) return;
+      int c = ex[add.a].op == EW_CONST ? add.a : (ex[add.b].op == EW_CONST ? add.b : -1);
+      if (c < 0) return;
+      eps = ex[c].imm;
+      const E& t = ex[c == add.a ? add.b : add.a];
+      if (t.op == EW_ACC && t.acc == 0) {
+        alpha = 1.0f;
+      } else if ((t.op == EW_MUL || t.op == EW_DIV) && t.round == 0) {
+        const bool acc_a = ex[t.a].op == EW_ACC && ex[t.a].acc == 0;
+        const bool acc_b = t.op == EW_MUL && ex[t.b].op == EW_ACC && ex[t.b].acc == 0;
+        const int k = acc_a ? t.b : (acc_b ? t.a : -1);
+        if (k < 0 || ex[k].op != EW_CONST) return;
+        alpha = ex[k].imm;
+        alpha_div = t.op == EW_DIV;
+      } else {
+        return;
+      }
+      ss = f;
+      continue;
+    }
+    const int lw = float_leaf(f);
+    if (sw < 0 && lw >= 0) {
+      // a row vector shared by every row: stride 1 along the innermost dim, 0 along the others
+      const EwLeaf& L = p.leaves[lw];
+      bool ok = L.strides[rank - 1] == 1;
+      for (int d = 0; d + 1 < rank; ++d) ok = ok && (L.strides[d] == 0 || p.shape[d] == 1);
+      if (!ok) return;
+      sw = f;
+      continue;
+    }
+    return;
+  }
+  if (sx < 0 || ss < 0) return;
+  const int lw = sw >= 0 ? float_leaf(sw) : -1;
+  // operands: slots of the leaves (from the program's pointer patches) and of the output
+  auto leaf_slot = [&](int li) {
+    const size_t field = offsetof(RowArgs, prog) + offsetof(EwProgram, leaves) + li * sizeof(EwLeaf) + offsetof(EwLeaf, ptr);
+    for (auto& pt : st.patches)
+      if (pt.first == field) return pt.second;
+    return -1;
+  };
+  int out_slot = -1;
+  for (auto& pt : st.patches)
+    if (pt.first == offsetof(RowArgs, prog) + offsetof(EwProgram, out_ptr)) out_slot = pt.second;
+  const int xs = leaf_slot(lx), ws = lw >= 0 ? leaf_slot(lw) : -1;
+  if (xs < 0 || out_slot < 0 || (lw >= 0 && ws < 0)) return;
+  RowNormArgs& N = A.norm;
+  N = RowNormArgs{};
+  N.x_dtype = p.leaves[lx].dtype;
+  N.w_dtype = lw >= 0 ? p.leaves[lw].dtype : 0;
+  N.out_dtype = p.out_dtype[0];
+  N.mid_round = mid;
+  N.alpha = alpha;
+  N.eps = eps;
+  N.alpha_div = alpha_div;
+  N.x = nullptr;
+  N.w = lw >= 0 ? (const void*)(uintptr_t)(p.leaves[lw].offset * (int64_t)dtype_size((DType)N.w_dtype)) : nullptr;
+  N.out = nullptr;
+  st.patches.push_back({offsetof(RowArgs, norm) + offsetof(RowNormArgs, x), xs});
+  if (lw >= 0) st.patches.push_back({offsetof(RowArgs, norm) + offsetof(RowNormArgs, w), ws});
+  st.patches.push_back({offsetof(RowArgs, norm) + offsetof(RowNormArgs, out), out_slot});
+  A.fast = ROW_FAST_NORM;
 }
 
 int Planner::canonical_copy(int node, const std::vector<int64_t>& order) {
@@ -1238,6 +1500,9 @@ std::string Plan::describe() const {
       os << " instrs=" << s.ew.n_instr << " leaves=" << s.ew.n_leaves << " elems=" << s.ew.total;
     } else if (s.kind == Step::REDUCE) {
       os << " outer=" << s.red.outer << " inner=" << s.red.inner;
+    } else if (s.kind == Step::ROW) {
+      os << " rows=" << s.row.rows << " inner=" << s.row.inner << " reductions=" << s.row.n_red
+         << " instrs=" << s.row.prog.n_instr << " leaves=" << s.row.prog.n_leaves;
     } else if (s.kind == Step::ATTENTION) {
       os << " B=" << s.attn.B << " H=" << s.attn.H << " S=" << s.attn.Sq << " D=" << s.attn.D << " causal=" << s.attn.causal;
     }
@@ -1246,8 +1511,8 @@ std::string Plan::describe() const {
   return os.str();
 }
 
-Plan build_plan(const Graph& g) {
-  Planner p(g);
+Plan build_plan(const Graph& g, const PlanOptions& opts) {
+  Planner p(g, opts);
   return p.run();
 }
 

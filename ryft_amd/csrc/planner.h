@@ -17,12 +17,13 @@ struct Slot {
 };
 
 struct Step {
-  enum Kind { ELEMENTWISE, REDUCE, GEMM, ATTENTION, COPY } kind;
+  enum Kind { ELEMENTWISE, REDUCE, GEMM, ATTENTION, COPY, ROW } kind;
   std::string name;  // kernel family, for profiling ("gemm_bf16_mfma", "attention_fwd", ...)
   EwProgram ew;
   ReduceArgs red;
   GemmArgs gemm;
   AttnArgs attn;
+  RowArgs row;
   struct { int64_t bytes; } copy;
   // Pointer fields inside the args block that refer to slots: (byte offset of the pointer field, slot). The
   // field's initial value is a byte offset into the slot's buffer.
@@ -35,6 +36,7 @@ struct Step {
       case REDUCE: return &red;
       case GEMM: return &gemm;
       case ATTENTION: return &attn;
+      case ROW: return &row;
       default: return nullptr;
     }
   }
@@ -50,6 +52,9 @@ struct Plan {
   std::string describe() const;
 };
 
-Plan build_plan(const Graph& g);
+struct PlanOptions {
+  bool fast_paths = true;  // recognise programs that specialised kernels compute (row norm); false: interpret them
+};
+Plan build_plan(const Graph& g, const PlanOptions& opts = PlanOptions());
 
 }  // namespace ryft

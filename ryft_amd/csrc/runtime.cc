@@ -431,7 +431,9 @@ std::shared_ptr<Executable> compile_program(Client* c, const std::string& code, 
     unimplemented("MLIR bytecode input is not supported yet; pass the module as MLIR text");
   auto exe = std::make_shared<Executable>();
   Graph g = parse_mlir_text(code, "main");
-  exe->plan = build_plan(g);
+  PlanOptions po;
+  po.fast_paths = c->fast_paths;
+  exe->plan = build_plan(g, po);
   exe->name = "main";
   exe->fingerprint = fnv_hex(code, options);
   exe->program_text = code;
@@ -517,7 +519,9 @@ EventPtr execute(LoadedExecutable* le, Device* d, Buffer* const* args, size_t nu
       std::lock_guard<std::mutex> pl(c->prof_mu);
       prof = c->profiling;
     }
-    alignas(64) static thread_local unsigned char block[sizeof(GemmArgs) > sizeof(ReduceArgs) ? sizeof(GemmArgs) + 64 : sizeof(ReduceArgs) + 64];
+    constexpr size_t kBlock = std::max({sizeof(EwProgram), sizeof(ReduceArgs), sizeof(GemmArgs), sizeof(RowArgs),
+                                        sizeof(AttnArgs)});
+    alignas(64) static thread_local unsigned char block[kBlock + 64];
     for (const Step& step : plan.steps) {
       StepTiming tm;
       if (prof) {
@@ -536,6 +540,7 @@ EventPtr execute(LoadedExecutable* le, Device* d, Buffer* const* args, size_t nu
         size_t sz = step.kind == Step::ELEMENTWISE ? sizeof(EwProgram)
                     : step.kind == Step::REDUCE    ? sizeof(ReduceArgs)
                     : step.kind == Step::GEMM      ? sizeof(GemmArgs)
+                    : step.kind == Step::ROW       ? sizeof(RowArgs)
                                                    : sizeof(AttnArgs);
         memcpy(block, const_cast<Step&>(step).args_block(), sz);
         for (auto& p : step.patches) {
@@ -545,6 +550,7 @@ EventPtr execute(LoadedExecutable* le, Device* d, Buffer* const* args, size_t nu
         switch (step.kind) {
           case Step::ELEMENTWISE: launch_elementwise(*(EwProgram*)block, st); break;
           case Step::REDUCE: launch_reduce(*(ReduceArgs*)block, st); break;
+          case Step::ROW: launch_row(*(RowArgs*)block, st); break;
           case Step::GEMM: launch_gemm(*(GemmArgs*)block, st); break;
           case Step::ATTENTION: launch_attention(*(AttnArgs*)block, st); break;
           default: break;

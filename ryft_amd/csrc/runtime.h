@@ -182,6 +182,7 @@ struct Client {  // PJRT_Client
   std::vector<std::unique_ptr<Memory>> memories;
   std::vector<Memory*> memory_ptrs;
   PinnedPool pinned;
+  bool fast_paths = true;  // planner option (PlanOptions::fast_paths)
 
   // completion worker: fires OnReady callbacks / host-side copy completions in stream order
   std::mutex q_mu;

@@ -9,6 +9,7 @@ import subprocess
 
 import pytest
 
+from tests import row_programs
 from ryft_amd import configs, pjrt
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -78,7 +79,7 @@ def _plan(client, program):
     ("c2", {}, ["gemm_bf16_mfma_256x256"]),
     ("c3", {}, ["gemm_i8_mfma_256x256"]),
     ("c4", {}, ["attention_fwd"]),
-    ("c5", {}, ["reduce", "elementwise", "gemm_fp8_mfma_dual_128x128", "gemm_fp8_mfma_64x128"]),
+    ("c5", {}, ["row_norm", "gemm_fp8_mfma_dual_128x128", "gemm_fp8_mfma_64x128"]),
 ])
 def test_full_size_plans(compile_client, name, kw, expect):
     w = configs.CONFIGS[name](**kw)
@@ -224,3 +225,50 @@ def test_attention_not_fused_when_intermediate_escapes(compile_client):
     exe, kernels = _plan(compile_client, prog)
     assert "attention_fwd" not in kernels
     assert exe.executable().output_count() == 2
+
+
+@pytest.mark.parametrize("name,build,reductions", [
+    ("rmsnorm", lambda: row_programs.rmsnorm((16, 4096), "bf16"), 1),
+    ("softmax", lambda: row_programs.softmax((4, 8, 200)), 2),
+    ("layernorm", lambda: row_programs.layernorm((8, 33)), 2),
+    ("int_row_max", lambda: row_programs.int_row_max_gap((8, 64)), 1),
+])
+def test_row_fusion_plans(compile_client, name, build, reductions):
+    # a reduction over the innermost dim broadcast back into its consumer runs in the consumer's launch
+    exe, kernels = _plan(compile_client, build())
+    fused = "row_norm" if name == "rmsnorm" else "row_fused"  # RMSNorm has a specialised kernel
+    assert fused in kernels, kernels
+    assert f"reductions={reductions}" in exe.describe_plan()
+    if name == "int_row_max":  # the row maxima are also a result: a reduce launch of their own writes them
+        assert sorted(kernels) == ["reduce", "row_fused"]
+    else:
+        assert kernels == [fused]
+
+
+def test_rmsnorm_fast_path_recognition(plugin):
+    # scaled sum-of-squares normalisations run on the row-norm kernel; the fast_paths=false client option keeps them
+    # on the interpreted row kernel; near misses (an extra offset) stay interpreted
+    fast = plugin.client({"compile_only": True})
+    slow = plugin.client({"compile_only": True, "fast_paths": False})
+    for prog in (row_programs.rmsnorm((512, 4096), "bf16", quant="f8E4M3FN"), row_programs.rmsnorm((3, 5, 64))):
+        assert _plan(fast, prog)[1] == ["row_norm"]
+        assert _plan(slow, prog)[1] == ["row_fused"]
+    near = row_programs.rmsnorm((8, 64)).replace("%12 = stablehlo.multiply %9, %11", "%12 = stablehlo.add %9, %11")
+    assert _plan(fast, near)[1] == ["row_fused"]
+
+
+def test_row_fusion_skips_non_innermost_reductions(compile_client):
+    # a reduction over dim 0 is not a row reduction: it stays a reduce launch feeding an elementwise one
+    T, R = "tensor<64x32xf32>", "tensor<32xf32>"
+    prog = f"""module {{
+  func.func @main(%arg0: {T}) -> {T} {{
+    %cst = stablehlo.constant dense<0.000000e+00> : tensor<f32>
+    %0 = stablehlo.reduce(%arg0 init: %cst) applies stablehlo.add across dimensions = [0] : ({T}, tensor<f32>) -> {R}
+    %1 = stablehlo.broadcast_in_dim %0, dims = [1] : ({R}) -> {T}
+    %2 = stablehlo.divide %arg0, %1 : {T}
+    return %2 : {T}
+  }}
+}}
+"""
+    _, kernels = _plan(compile_client, prog)
+    assert kernels == ["reduce", "elementwise"]
