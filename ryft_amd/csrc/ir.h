@@ -87,8 +87,9 @@ struct Graph {
 
 // Front-end: StableHLO MLIR text (pretty or generic syntax) → Graph. Throws Status on malformed or unsupported input.
 Graph parse_mlir_text(const std::string& text, const std::string& entry = "main");
-// MLIR bytecode (the `MLïR` magic) is recognised and rejected with UNIMPLEMENTED.
+// MLIR bytecode (the `ML\xEFR` magic) → Graph, for the same op set (mlir_bytecode.cc).
 bool is_mlir_bytecode(const char* data, size_t size);
+Graph parse_mlir_bytecode(const std::string& bytes, const std::string& entry = "main");
 
 // Literal helpers: constant element as double / int64 (splat or index 0).
 double literal_as_double(const Node& n, int64_t index = 0);

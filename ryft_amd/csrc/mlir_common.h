@@ -1,0 +1,23 @@
+// Internal interface between the two StableHLO front-ends (MLIR text in mlir_text.cc, MLIR bytecode in
+// mlir_bytecode.cc): textual type / attribute forms and the node checks both apply.
+#pragma once
+
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "ir.h"
+
+namespace ryft {
+
+DType mlir_element_type(const std::string& t);                      // "f32", "bf16", "i8", "f8E4M3FN", ...
+TensorType mlir_type_text(const std::string& text);                 // "tensor<2x3xf32>" or a scalar element type
+std::vector<int64_t> mlir_int_list_text(const std::string& raw);    // "[0, 1]", "array<i64: 0, 1>", "dense<...>"
+void mlir_dense_text(const std::string& text, const TensorType& tt, Node& n);  // "dense<...>" → n.literal / n.splat
+CmpDir mlir_cmp_dir_text(const std::string& raw);                   // text containing EQ / NE / GE / GT / LE / LT
+CmpType mlir_cmp_type_text(const std::string& raw);                 // text containing FLOAT / SIGNED / ...
+void validate_node(const Graph& g, Node& n);                        // operand counts, shapes, dimension ranges
+// StableHLO op names (no dialect prefix) that map to one Op and carry no attributes ("add" → Op::Add, ...).
+const std::unordered_map<std::string, Op>& mlir_simple_ops();
+
+}  // namespace ryft

@@ -15,8 +15,28 @@
 #include <unordered_map>
 
 #include "ir.h"
+#include "mlir_common.h"
 
 namespace ryft {
+
+void validate_node(const Graph& g, Node& n);
+
+// StableHLO op names (without the dialect prefix) that map to one Op with no attributes.
+const std::unordered_map<std::string, Op>& mlir_simple_ops() {
+  static const std::unordered_map<std::string, Op> m = {
+      {"negate", Op::Negate},       {"abs", Op::Abs},         {"exponential", Op::Exp},
+      {"log", Op::Log},             {"rsqrt", Op::Rsqrt},     {"sqrt", Op::Sqrt},
+      {"tanh", Op::Tanh},           {"logistic", Op::Logistic}, {"not", Op::Not},
+      {"convert", Op::Convert},     {"floor", Op::Floor},     {"ceil", Op::Ceil},
+      {"sign", Op::Sign},           {"exponential_minus_one", Op::Expm1}, {"log_plus_one", Op::Log1p},
+      {"add", Op::Add},             {"subtract", Op::Subtract}, {"multiply", Op::Multiply},
+      {"divide", Op::Divide},       {"maximum", Op::Maximum}, {"minimum", Op::Minimum},
+      {"power", Op::Power},         {"remainder", Op::Remainder}, {"and", Op::And},
+      {"or", Op::Or},               {"xor", Op::Xor},         {"select", Op::Select},
+      {"clamp", Op::Clamp},         {"reshape", Op::Reshape}, {"bitcast_convert", Op::Convert},
+  };
+  return m;
+}
 
 std::string TensorType::str() const {
   std::ostringstream os;
@@ -778,6 +798,7 @@ class Parser {
     os.type = parse_fn_or_types(c_);
   }
 
+ public:
   static CmpDir parse_dir(const std::string& raw) {
     static const char* names[] = {"EQ", "NE", "GE", "GT", "LE", "LT"};
     for (int i = 0; i < 6; ++i)
@@ -792,6 +813,8 @@ class Parser {
     return CmpType::NOTYPE;
   }
 
+ private:
+
   // Result type of an op: explicit fn-type result, or (for `op %a, %b : tensor<..>`) the single listed type.
   TensorType result_type(const OpSyntax& os) {
     if (!os.type.results.empty()) return os.type.results[0];
@@ -800,18 +823,7 @@ class Parser {
   }
 
   void build(const OpSyntax& os) {
-    static const std::unordered_map<std::string, Op> simple = {
-        {"negate", Op::Negate},       {"abs", Op::Abs},         {"exponential", Op::Exp},
-        {"log", Op::Log},             {"rsqrt", Op::Rsqrt},     {"sqrt", Op::Sqrt},
-        {"tanh", Op::Tanh},           {"logistic", Op::Logistic}, {"not", Op::Not},
-        {"convert", Op::Convert},     {"floor", Op::Floor},     {"ceil", Op::Ceil},
-        {"sign", Op::Sign},           {"exponential_minus_one", Op::Expm1}, {"log_plus_one", Op::Log1p},
-        {"add", Op::Add},             {"subtract", Op::Subtract}, {"multiply", Op::Multiply},
-        {"divide", Op::Divide},       {"maximum", Op::Maximum}, {"minimum", Op::Minimum},
-        {"power", Op::Power},         {"remainder", Op::Remainder}, {"and", Op::And},
-        {"or", Op::Or},               {"xor", Op::Xor},         {"select", Op::Select},
-        {"clamp", Op::Clamp},         {"reshape", Op::Reshape}, {"bitcast_convert", Op::Convert},
-    };
+    const auto& simple = mlir_simple_ops();
     Node n;
     n.debug = os.results.empty() ? std::string() : os.results[0];
     for (auto& o : os.operands) n.operands.push_back(value(o));
@@ -909,77 +921,7 @@ class Parser {
     for (auto& r : os.results) names_[r] = id;
   }
 
-  void validate(Node& n) {
-    auto& g = graph_;
-    auto opt = [&](int i) -> const TensorType& { return g.nodes[n.operands.at(i)].type; };
-    auto need = [&](size_t k) {
-      if (n.operands.size() != k) invalid(std::string(op_name(n.op)) + " expects " + std::to_string(k) + " operands");
-    };
-    switch (n.op) {
-      case Op::BroadcastInDim:
-        need(1);
-        if (n.dims.size() != opt(0).shape.size()) invalid("broadcast_in_dim: dims size must equal operand rank");
-        for (size_t i = 0; i < n.dims.size(); ++i) {
-          int64_t d = n.dims[i];
-          if (d < 0 || d >= n.type.rank()) invalid("broadcast_in_dim: dimension out of range");
-          if (opt(0).shape[i] != 1 && opt(0).shape[i] != n.type.shape[d]) invalid("broadcast_in_dim: incompatible shape");
-        }
-        break;
-      case Op::Transpose:
-        need(1);
-        if ((int)n.dims.size() != opt(0).rank()) invalid("transpose: permutation size must equal rank");
-        for (size_t i = 0; i < n.dims.size(); ++i)
-          if (n.type.shape[i] != opt(0).shape[n.dims[i]]) invalid("transpose: result shape mismatch");
-        break;
-      case Op::Reshape:
-        need(1);
-        if (opt(0).elements() != n.type.elements()) invalid("reshape: element count mismatch");
-        break;
-      case Op::DotGeneral: {
-        need(2);
-        auto& L = opt(0);
-        auto& R = opt(1);
-        if (n.dot.lhs_batch.size() != n.dot.rhs_batch.size() || n.dot.lhs_contract.size() != n.dot.rhs_contract.size())
-          invalid("dot_general: mismatched dimension lists");
-        for (size_t i = 0; i < n.dot.lhs_batch.size(); ++i)
-          if (L.shape.at(n.dot.lhs_batch[i]) != R.shape.at(n.dot.rhs_batch[i])) invalid("dot_general: batch size mismatch");
-        for (size_t i = 0; i < n.dot.lhs_contract.size(); ++i)
-          if (L.shape.at(n.dot.lhs_contract[i]) != R.shape.at(n.dot.rhs_contract[i]))
-            invalid("dot_general: contracting size mismatch");
-        break;
-      }
-      case Op::Reduce: {
-        auto& in = opt(0);
-        std::vector<int64_t> out;
-        for (int d = 0; d < in.rank(); ++d) {
-          bool red = false;
-          for (auto r : n.dims) red |= (r == d);
-          if (!red) out.push_back(in.shape[d]);
-        }
-        if (out != n.type.shape) invalid("reduce: result shape mismatch");
-        if (opt(1).rank() != 0) invalid("reduce: init value must be a scalar");
-        break;
-      }
-      case Op::Select:
-        need(3);
-        if (opt(0).dtype != DType::PRED) invalid("select: predicate must be i1");
-        break;
-      case Op::Iota:
-        if (n.iota_dim < 0 || n.iota_dim >= n.type.rank()) invalid("iota: dimension out of range");
-        break;
-      default:
-        if (op_is_elementwise(n.op)) {
-          for (size_t i = 0; i < n.operands.size(); ++i) {
-            auto& t = opt(i);
-            bool scalar_ok = (n.op == Op::Select && i == 0) || n.op == Op::Clamp;
-            if (t.shape != n.type.shape && !(scalar_ok && t.rank() == 0))
-              invalid(std::string(op_name(n.op)) + ": operand shape " + shape_str(t.shape) + " does not match result " +
-                      shape_str(n.type.shape));
-          }
-        }
-        break;
-    }
-  }
+  void validate(Node& n) { validate_node(graph_, n); }
 
   Cursor c_;
   Graph graph_;
@@ -988,6 +930,97 @@ class Parser {
 };
 
 }  // namespace
+
+// ------------------------------------------------------------------------------------------------ shared
+// Pieces of the text front-end the bytecode front-end reuses (declared in mlir_common.h): textual type and attribute
+// forms (MLIR bytecode keeps types and attributes without a binary encoding as their assembly text), and the
+// per-op checks both front-ends apply to the nodes they build.
+DType mlir_element_type(const std::string& t) { return parse_element_type(t); }
+TensorType mlir_type_text(const std::string& text) {
+  Cursor c(text);
+  return parse_type(c);
+}
+std::vector<int64_t> mlir_int_list_text(const std::string& raw) { return parse_int_list_text(raw); }
+void mlir_dense_text(const std::string& text, const TensorType& tt, Node& n) {
+  size_t d = text.find("dense<");
+  if (d == std::string::npos) unimplemented("constant value '" + text + "' is not a dense literal");
+  Cursor vc(text);
+  vc.set_pos(d + 6);
+  parse_dense(vc.angle_body(), tt, n);
+}
+CmpDir mlir_cmp_dir_text(const std::string& raw) { return Parser::parse_dir(raw); }
+CmpType mlir_cmp_type_text(const std::string& raw) { return Parser::parse_cmp_type(raw); }
+
+void validate_node(const Graph& g, Node& n) {
+  auto opt = [&](int i) -> const TensorType& { return g.nodes[n.operands.at(i)].type; };
+  auto need = [&](size_t k) {
+    if (n.operands.size() != k) invalid(std::string(op_name(n.op)) + " expects " + std::to_string(k) + " operands");
+  };
+  switch (n.op) {
+    case Op::BroadcastInDim:
+      need(1);
+      if (n.dims.size() != opt(0).shape.size()) invalid("broadcast_in_dim: dims size must equal operand rank");
+      for (size_t i = 0; i < n.dims.size(); ++i) {
+        int64_t d = n.dims[i];
+        if (d < 0 || d >= n.type.rank()) invalid("broadcast_in_dim: dimension out of range");
+        if (opt(0).shape[i] != 1 && opt(0).shape[i] != n.type.shape[d]) invalid("broadcast_in_dim: incompatible shape");
+      }
+      break;
+    case Op::Transpose:
+      need(1);
+      if ((int)n.dims.size() != opt(0).rank()) invalid("transpose: permutation size must equal rank");
+      for (size_t i = 0; i < n.dims.size(); ++i)
+        if (n.type.shape[i] != opt(0).shape[n.dims[i]]) invalid("transpose: result shape mismatch");
+      break;
+    case Op::Reshape:
+      need(1);
+      if (opt(0).elements() != n.type.elements()) invalid("reshape: element count mismatch");
+      break;
+    case Op::DotGeneral: {
+      need(2);
+      auto& L = opt(0);
+      auto& R = opt(1);
+      if (n.dot.lhs_batch.size() != n.dot.rhs_batch.size() || n.dot.lhs_contract.size() != n.dot.rhs_contract.size())
+        invalid("dot_general: mismatched dimension lists");
+      for (size_t i = 0; i < n.dot.lhs_batch.size(); ++i)
+        if (L.shape.at(n.dot.lhs_batch[i]) != R.shape.at(n.dot.rhs_batch[i])) invalid("dot_general: batch size mismatch");
+      for (size_t i = 0; i < n.dot.lhs_contract.size(); ++i)
+        if (L.shape.at(n.dot.lhs_contract[i]) != R.shape.at(n.dot.rhs_contract[i]))
+          invalid("dot_general: contracting size mismatch");
+      break;
+    }
+    case Op::Reduce: {
+      auto& in = opt(0);
+      std::vector<int64_t> out;
+      for (int d = 0; d < in.rank(); ++d) {
+        bool red = false;
+        for (auto r : n.dims) red |= (r == d);
+        if (!red) out.push_back(in.shape[d]);
+      }
+      if (out != n.type.shape) invalid("reduce: result shape mismatch");
+      if (opt(1).rank() != 0) invalid("reduce: init value must be a scalar");
+      break;
+    }
+    case Op::Select:
+      need(3);
+      if (opt(0).dtype != DType::PRED) invalid("select: predicate must be i1");
+      break;
+    case Op::Iota:
+      if (n.iota_dim < 0 || n.iota_dim >= n.type.rank()) invalid("iota: dimension out of range");
+      break;
+    default:
+      if (op_is_elementwise(n.op)) {
+        for (size_t i = 0; i < n.operands.size(); ++i) {
+          auto& t = opt(i);
+          bool scalar_ok = (n.op == Op::Select && i == 0) || n.op == Op::Clamp;
+          if (t.shape != n.type.shape && !(scalar_ok && t.rank() == 0))
+            invalid(std::string(op_name(n.op)) + ": operand shape " + shape_str(t.shape) + " does not match result " +
+                    shape_str(n.type.shape));
+        }
+      }
+      break;
+  }
+}
 
 Graph parse_mlir_text(const std::string& text, const std::string& entry) {
   Parser p(text);

@@ -427,10 +427,8 @@ static std::string fnv_hex(const std::string& a, const std::string& b) {
 std::shared_ptr<Executable> compile_program(Client* c, const std::string& code, const std::string& format,
                                             const std::string& options) {
   if (format != "mlir") unimplemented("program format '" + format + "' is not supported; pass StableHLO as \"mlir\"");
-  if (is_mlir_bytecode(code.data(), code.size()))
-    unimplemented("MLIR bytecode input is not supported yet; pass the module as MLIR text");
   auto exe = std::make_shared<Executable>();
-  Graph g = parse_mlir_text(code, "main");
+  Graph g = is_mlir_bytecode(code.data(), code.size()) ? parse_mlir_bytecode(code, "main") : parse_mlir_text(code, "main");
   PlanOptions po;
   po.fast_paths = c->fast_paths;
   exe->plan = build_plan(g, po);

@@ -175,10 +175,10 @@ def test_printer_golden_forms_compile(compile_client, name):
     assert exe.executable().output_count() == 1
 
 
-def test_bytecode_is_rejected_clearly(compile_client):
+def test_malformed_bytecode_is_invalid_argument(compile_client):
     with pytest.raises(pjrt.PjrtError) as e:
-        compile_client.compile(pjrt.Program.mlir(b"ML\xefR\x00\x05rest-of-bytecode"))
-    assert e.value.code == pjrt.ErrorCode.UNIMPLEMENTED
+        compile_client.compile(pjrt.Program.mlir(b"ML\xefR\x0dMLIR\x00\x05rest-of-bytecode"))
+    assert e.value.code == pjrt.ErrorCode.INVALID_ARGUMENT
     assert "bytecode" in e.value.message
 
 
