@@ -173,6 +173,12 @@ struct GemmArgs {
   float alpha;
   int32_t raw_out;      // EPI_SCALE: also store the raw accumulator into out[1]
   int32_t mid_round;    // EPI_SCALE / EPI_SWIGLU: round the value to this dtype before the output conversion
+  // Split-K (MFMA kernels, epilogues other than EPI_PROGRAM): splits > 1 divides K into `splits` equal ranges; the
+  // workgroups of range s write their raw f32 / i32 accumulators to ws[s][acc][batch][M][N] (acc: 0, and 1 for the
+  // second dot of a dual GEMM), and a reduction kernel sums the ranges in order and applies the epilogue.
+  int32_t splits;
+  int32_t pad_splits;
+  void* ws;
   // EPI_PROGRAM: iteration space = the dot result's dims; epi_groups = #dims in (batch, lhs-free, rhs-free)
   int32_t epi_groups[3];
   EwProgram epi;

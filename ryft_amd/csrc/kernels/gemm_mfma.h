@@ -472,7 +472,10 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_mfma_kernel(const GemmArgs 
   const int tiles_n = G.N / BN, tiles_m = G.M / BM;
   const int per_batch = tiles_n * tiles_m;
   const int total = per_batch * G.batch;
-  int bid = blockIdx.x;
+  // split-K: the K range is the slow index of the grid, so the tile order below (and its XCD mapping) is the same
+  // within every range
+  const int split = G.splits > 1 ? (int)(blockIdx.x / total) : 0;
+  int bid = G.splits > 1 ? (int)(blockIdx.x % total) : (int)blockIdx.x;
   if ((total & 7) == 0) bid = (bid & 7) * (total >> 3) + (bid >> 3);
   const int b = bid / per_batch, t = bid % per_batch;
   const int GM = tiles_m < 8 ? tiles_m : 8;
@@ -503,9 +506,10 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_mfma_kernel(const GemmArgs 
       if constexpr (DUAL) acc2[i][j] = Acc{};
     }
 
-  const int KT = G.K / BK;
+  const int KT = G.splits > 1 ? G.K / BK / G.splits : G.K / BK;  // k-tiles of this workgroup's K range
+  const int kt0 = split * KT;
   auto gload = [&](int kt) {
-    const int64_t ko = (int64_t)kt * BK;
+    const int64_t ko = (int64_t)(kt0 + kt) * BK;
     la.load(Ab + ko * G.A.sk * ES, G.A.sr, G.A.sk, tid);
     lb.load(Bb + ko * G.B.sk * ES, G.B.sr, G.B.sk, tid);
     if constexpr (DUAL) lb2.load(B2b + ko * G.B2.sk * ES, G.B2.sr, G.B2.sk, tid);
@@ -657,8 +661,18 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_mfma_kernel(const GemmArgs 
     // The region is private to this wave, and one wave's LDS operations execute in order: keeping the compiler from
     // moving the reads above the writes is all the ordering needed (a memory fence would also wait for the stores).
     __asm__ __volatile__("" ::: "memory");
-    epi_round<M::INT, DUAL, C::WTN, PITCH, EPI_ROWS * 32>(G, b, m0 + wm * C::WTM + round * EPI_ROWS * 32,
-                                                         n0 + wn * C::WTN, patch, patch + REGION, lane);
+    const int em0 = m0 + wm * C::WTM + round * EPI_ROWS * 32, en0 = n0 + wn * C::WTN;
+    if (G.splits > 1) {  // raw partial sums of this K range
+      constexpr int PDT = M::INT ? DT_S32 : DT_F32;
+      const int64_t slice = (int64_t)G.batch * G.M * G.N * 4;
+      char* ws = (char*)G.ws + (int64_t)split * C::NB * slice;
+      epi_pass<EPI_STORE, PDT, M::INT, false, C::WTN, PITCH, EPI_ROWS * 32>(G, ws, b, em0, en0, patch, nullptr, lane);
+      if constexpr (DUAL)
+        epi_pass<EPI_STORE, PDT, M::INT, false, C::WTN, PITCH, EPI_ROWS * 32>(G, ws + slice, b, em0, en0, patch + REGION,
+                                                                             nullptr, lane);
+    } else {
+      epi_round<M::INT, DUAL, C::WTN, PITCH, EPI_ROWS * 32>(G, b, em0, en0, patch, patch + REGION, lane);
+    }
     if constexpr (round + 1 < C::TM / EPI_ROWS) __asm__ __volatile__("" ::: "memory");  // reads before next writes
   });
 }

@@ -4,6 +4,7 @@
 // and type mixes the MFMA instantiations do not cover.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <string>
 #include <type_traits>
 
@@ -81,6 +82,78 @@ __global__ void __launch_bounds__(256) gemm_generic_kernel(const GemmArgs G) {
 }
 
 // ------------------------------------------------------------------------------------------------ dispatch
+// ------------------------------------------------------------------------------------------------ split-K
+// Sums the K ranges' partial accumulators in range order and applies the epilogue, with the same per-element
+// arithmetic (and operation order) as the MFMA kernels' epilogue passes. Each thread owns 4 consecutive columns.
+template <bool INT, bool DUAL>
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(const GemmArgs G) {
+  const int64_t quads = (int64_t)G.batch * G.M * G.N / 4;
+  const int64_t slice = (int64_t)G.batch * G.M * G.N;  // elements of one accumulator set
+  const int nb = DUAL ? 2 : 1;
+  for (int64_t qd = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; qd < quads; qd += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t e0 = qd * 4;
+    const int n = (int)(e0 % G.N);
+    const int64_t bm = e0 / G.N;
+    const int m = (int)(bm % G.M), b = (int)(bm / G.M);
+    uint32_t v[4], v2[4];
+    {
+      const u32x4 w = *(const u32x4*)((const uint32_t*)G.ws + e0);
+      v[0] = w.x, v[1] = w.y, v[2] = w.z, v[3] = w.w;
+      if (DUAL) {
+        const u32x4 w2 = *(const u32x4*)((const uint32_t*)G.ws + slice + e0);
+        v2[0] = w2.x, v2[1] = w2.y, v2[2] = w2.z, v2[3] = w2.w;
+      }
+    }
+    for (int s = 1; s < G.splits; ++s) {
+      const u32x4 w = *(const u32x4*)((const uint32_t*)G.ws + (int64_t)s * nb * slice + e0);
+      const uint32_t x[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        v[e] = INT ? (uint32_t)((int32_t)v[e] + (int32_t)x[e]) : __float_as_uint(__uint_as_float(v[e]) + __uint_as_float(x[e]));
+      if (DUAL) {
+        const u32x4 w2 = *(const u32x4*)((const uint32_t*)G.ws + ((int64_t)s * nb + 1) * slice + e0);
+        const uint32_t x2[4] = {w2.x, w2.y, w2.z, w2.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v2[e] = __float_as_uint(__uint_as_float(v2[e]) + __uint_as_float(x2[e]));
+      }
+    }
+    uint32_t raw[4] = {v[0], v[1], v[2], v[3]};
+    bool is_float = !INT;
+    if (G.epilogue == EPI_SCALE) {
+      float rs = G.alpha;
+      if (G.row) rs *= G.row[(int64_t)b * G.row_sb + (int64_t)m * G.row_sm];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float cs = G.col ? G.col[(int64_t)b * G.col_sb + (int64_t)(n + e) * G.col_sn] : 1.0f;
+        float x = INT ? (float)(int32_t)v[e] : __uint_as_float(v[e]);
+        x = x * rs * cs;
+        if (G.mid_round) x = G.mid_round == DT_BF16 ? bf16_bits_to_f32(f32_to_bf16_bits(x)) : (float)(_Float16)x;
+        v[e] = __float_as_uint(x);
+      }
+      is_float = true;
+    } else if (DUAL && G.epilogue == EPI_SWIGLU) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float c1 = G.col ? G.col[(int64_t)b * G.col_sb + (int64_t)(n + e) * G.col_sn] : 1.0f;
+        const float c2 = G.col2 ? G.col2[(int64_t)b * G.col2_sb + (int64_t)(n + e) * G.col2_sn] : 1.0f;
+        const float a = __uint_as_float(v[e]) * c1;
+        const float u = __uint_as_float(v2[e]) * c2;
+        const float lg = 1.0f / (1.0f + expf(-a));
+        float x = (a * lg) * u;
+        if (G.mid_round) x = G.mid_round == DT_BF16 ? bf16_bits_to_f32(f32_to_bf16_bits(x)) : (float)(_Float16)x;
+        v[e] = __float_as_uint(x);
+      }
+      is_float = true;
+    }
+    const int64_t o = e0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) store_bits(G.out_ptr[0], o + e, G.out_dtype[0], v[e], is_float);
+    if (G.epilogue == EPI_SCALE && G.raw_out)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) store_bits(G.out_ptr[1], o + e, G.out_dtype[1], raw[e], !INT);
+  }
+}
+
 static int mma_kind(const GemmArgs& g) {
   auto t = [](int d) { return d; };
   if (g.dual && g.B2.dtype != g.B.dtype) return -1;
@@ -144,6 +217,31 @@ const char* gemm_kernel_name(const GemmArgs& a) {
   return "gemm_generic";
 }
 
+int gemm_plan_splits(const GemmArgs& a) {
+  GemmArgs g = a;
+  g.splits = 1;
+  Choice c;
+  if (!pick_mfma(g, &c)) return 1;
+  const int64_t tiles = (int64_t)(g.M / c.bm) * (g.N / c.bn) * g.batch;
+  const bool f32 = g.A.dtype == DT_F32;
+  // the 64-row tile (chosen when 128×128 tiles would not cover the chip) reads twice the operand bytes per FLOP of a
+  // 128×128 tile, from L2 as well as LDS: splitting K over 128×128 tiles beats it
+  const bool small_tile = !f32 && c.bm < 128;
+  if (tiles >= 192 && !small_tile) return 1;  // the chip (256 CUs) is already covered well enough
+  // the split tile: 128×128 (64×64 for f32) over each K range; at least 4 k-tiles per range
+  const int tm = f32 ? 64 : 128, tk = f32 ? 16 : (g.A.dtype == DT_BF16 || g.A.dtype == DT_F16 ? 64 : 128);
+  if (g.M % tm || g.N % tm || g.dual) return 1;
+  const int64_t tiles_s = (int64_t)(g.M / tm) * (g.N / tm) * g.batch;
+  int best = 1;
+  for (int s = 2; s <= 16; s *= 2) {
+    if (tiles_s * s > 256 || g.K % (tk * s) || g.K / (tk * s) < 4) break;
+    best = s;
+  }
+  if (best < 2 || (!small_tile && tiles_s * best <= tiles)) return 1;
+  g.splits = best;
+  return pick_mfma(g, &c) ? best : 1;
+}
+
 void launch_gemm(const GemmArgs& g, hipStream_t stream) {
   if (g.M == 0 || g.N == 0 || g.batch == 0) return;
   Choice c;
@@ -155,10 +253,20 @@ void launch_gemm(const GemmArgs& g, hipStream_t stream) {
       e = hipFuncSetAttribute(c.fn, hipFuncAttributeMaxDynamicSharedMemorySize, c.lds);
       if (e != hipSuccess) fail(PJRT_Error_Code_INTERNAL, std::string("LDS attribute failed: ") + hipGetErrorString(e));
     }
-    int64_t blocks = (int64_t)(g.M / c.bm) * (g.N / c.bn) * g.batch;
+    const int splits = g.splits > 1 ? g.splits : 1;
+    if (splits > 1 && (!g.ws || g.K % (splits * 16))) fail(PJRT_Error_Code_INTERNAL, "split-K without a workspace");
+    int64_t blocks = (int64_t)(g.M / c.bm) * (g.N / c.bn) * g.batch * splits;
     if (blocks > INT32_MAX) fail(PJRT_Error_Code_UNIMPLEMENTED, "too many GEMM tiles");
     void* args[] = {(void*)&g};
     e = hipLaunchKernel(c.fn, dim3((unsigned)blocks), dim3(c.threads), args, (size_t)c.lds, stream);
+    if (e == hipSuccess && splits > 1) {
+      const int64_t quads = (int64_t)g.batch * g.M * g.N / 4;
+      const unsigned rb = (unsigned)std::min<int64_t>((quads + 255) / 256, 256 * 16);
+      if (g.acc_is_int) hipLaunchKernelGGL((splitk_reduce_kernel<true, false>), dim3(rb), dim3(256), 0, stream, g);
+      else if (g.dual) hipLaunchKernelGGL((splitk_reduce_kernel<false, true>), dim3(rb), dim3(256), 0, stream, g);
+      else hipLaunchKernelGGL((splitk_reduce_kernel<false, false>), dim3(rb), dim3(256), 0, stream, g);
+      e = hipGetLastError();
+    }
   } else {
     dim3 grid((g.N + 63) / 64, (g.M + 63) / 64, g.batch), block(256);
     if (g.batch > 65535) fail(PJRT_Error_Code_UNIMPLEMENTED, "batch too large for the generic GEMM");

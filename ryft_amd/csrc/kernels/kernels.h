@@ -16,6 +16,9 @@ void launch_attention(const AttnArgs& a, hipStream_t stream);
 
 // Name of the GEMM kernel launch_gemm() picks for these arguments (used for profiling labels).
 const char* gemm_kernel_name(const GemmArgs& a);
+// Number of K ranges launch_gemm splits these arguments into when given a workspace of
+// splits × (dual ? 2 : 1) × batch × M × N 4-byte accumulators (1: no split).
+int gemm_plan_splits(const GemmArgs& a);
 // Head dims the fused attention kernel supports.
 bool attention_supported(int head_dim);
 

@@ -166,6 +166,7 @@ class Planner {
   bool splat_value(int node, double* v);
   int iota_axis(int node, int rank);
   void classify_epilogue(Step& st, const std::vector<int>& unused);
+  void plan_split_k(Step& st);
 
   const Graph& g_;
   PlanOptions opts_;
@@ -1044,6 +1045,7 @@ void Planner::emit_dot(const std::vector<int>& dots_in, int target, int root) {
     st.patches.push_back({offsetof(GemmArgs, out_ptr), out});
     st.bytes += (double)d.type.bytes();
     st.name = gemm_kernel_name(G);
+    plan_split_k(st);
     plan_.steps.push_back(std::move(st));
     mat_[dots[0]] = out;
     return;
@@ -1110,9 +1112,27 @@ void Planner::emit_dot(const std::vector<int>& dots_in, int target, int root) {
     }
   }
   st.name = gemm_kernel_name(G);
+  plan_split_k(st);
   plan_.steps.push_back(std::move(st));
   mat_[root] = out;
   if (acc_slot >= 0) mat_[dots[0]] = acc_slot;
+}
+
+// Split-K for GEMMs whose tiles would leave much of the chip idle (few output tiles, long K): the kernel library
+// picks the split; the plan provides the workspace of per-range partial sums (a temporary, reused across
+// executions by the allocator's cache).
+void Planner::plan_split_k(Step& st) {
+  GemmArgs& G = st.gemm;
+  if (G.epilogue == EPI_PROGRAM) return;
+  const int s = gemm_plan_splits(G);
+  if (s <= 1) return;
+  TensorType wt;
+  wt.dtype = DType::F32;
+  wt.shape = {(int64_t)s * (G.dual ? 2 : 1) * G.batch * G.M * G.N};
+  const int ws = new_slot(Slot::TEMP, wt);
+  G.splits = s;
+  st.patches.push_back({offsetof(GemmArgs, ws), ws});
+  st.name = std::string(gemm_kernel_name(G)) + "_splitk" + std::to_string(s);
 }
 
 // Replace a generic epilogue program by a specialised epilogue when its expression has one of the shapes the GEMM

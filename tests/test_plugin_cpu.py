@@ -75,11 +75,11 @@ def _plan(client, program):
 
 
 @pytest.mark.parametrize("name,kw,expect", [
-    ("c1", {}, ["gemm_f32_mfma_64x64"]),
+    ("c1", {}, ["gemm_f32_mfma_64x64_splitk8"]),
     ("c2", {}, ["gemm_bf16_mfma_256x256"]),
     ("c3", {}, ["gemm_i8_mfma_256x256"]),
     ("c4", {}, ["attention_fwd"]),
-    ("c5", {}, ["row_norm", "gemm_fp8_mfma_dual_128x128", "gemm_fp8_mfma_64x128"]),
+    ("c5", {}, ["row_norm", "gemm_fp8_mfma_dual_128x128", "gemm_fp8_mfma_128x128_splitk2"]),
 ])
 def test_full_size_plans(compile_client, name, kw, expect):
     w = configs.CONFIGS[name](**kw)
@@ -272,3 +272,16 @@ def test_row_fusion_skips_non_innermost_reductions(compile_client):
 """
     _, kernels = _plan(compile_client, prog)
     assert kernels == ["reduce", "elementwise"]
+
+
+@pytest.mark.parametrize("name,kw,kernel", [
+    ("c2", {"batch": 1, "m": 256, "k": 4096, "n": 256}, "gemm_bf16_mfma_128x128_splitk16"),
+    ("c3", {"m": 256, "k": 8192, "n": 256}, "gemm_i8_mfma_128x128_splitk16"),
+    ("c3", {"m": 4096, "k": 4096, "n": 4096}, "gemm_i8_mfma_256x256"),
+])
+def test_split_k_plans(compile_client, name, kw, kernel):
+    # few output tiles over a long K: the K range is split over 128×128 tiles (partial sums in a workspace, then one
+    # reduction launch applies the epilogue); tile counts that cover the chip keep one pass
+    w = configs.CONFIGS[name](**kw)
+    _, kernels = _plan(compile_client, w.program)
+    assert kernels == [kernel]
