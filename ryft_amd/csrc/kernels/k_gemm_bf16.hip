@@ -16,8 +16,9 @@ bool pick_bf16(const GemmArgs& g, bool br, Choice* c) {
       return true;
     }
     if (fits(256, 256, 64) && tiles256 >= 128) {
-      *c = br ? make_choice<MMA_BF16, 256, 256, 64, 2, 2, false, true, false>("gemm_bf16_mfma_256x256")
-              : make_choice<MMA_BF16, 256, 256, 64, 2, 2, false, false, false>("gemm_bf16_mfma_256x256");
+      // eight waves (two per SIMD, 128×64 each): one wave's LDS waits and barrier overlap the other's MFMAs
+      *c = br ? make_choice<MMA_BF16, 256, 256, 64, 2, 4, false, true, false>("gemm_bf16_mfma_256x256")
+              : make_choice<MMA_BF16, 256, 256, 64, 2, 4, false, false, false>("gemm_bf16_mfma_256x256");
       return true;
     }
     if (fits(128, 128, 64)) {
