@@ -218,11 +218,17 @@ __global__ void __launch_bounds__(256, 2) attention_fwd_kernel(const AttnArgs A)
 #pragma unroll
         for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, st[t][r]);
     }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+    // the other half-wave's maximum, by a lane swap across the halves (no LDS round trip): one of the swap's two
+    // results holds it, the other this lane's own value
+    {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mloc), __float_as_uint(mloc), false, false);
+      mloc = fmaxf(mloc, fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])));
+    }
     // Lazy rescaling: the exponent reference m_run only moves when this block's maximum exceeds it by more than 8 in
     // log2 units (probabilities then stay ≤ 2^8; o and l share the reference, so o / l is unchanged), and the
     // rescale of o is skipped when no lane moved its reference.
-    const bool raise = (mloc - m_run) * sl2 > 8.0f || (m_run == -INFINITY && mloc != -INFINITY);
+    // (bitwise operators: a short-circuit would become a divergent branch)
+    const bool raise = ((mloc - m_run) * sl2 > 8.0f) | ((m_run == -INFINITY) & (mloc != -INFINITY));
     const float m_new = raise ? mloc : m_run;
     const float m_use = m_new == -INFINITY ? 0.f : m_new;  // a fully masked row keeps p = 0
     if (__builtin_amdgcn_ballot_w64(raise)) {
