@@ -18,6 +18,7 @@
 #include "../common.h"
 #include "ew_device.h"
 #include "kernels.h"
+#include "launch.h"
 
 namespace ryft {
 
@@ -316,7 +317,7 @@ __global__ void __launch_bounds__(256, 2) attention_fwd_kernel(const AttnArgs A)
 
 }  // namespace
 
-void launch_attention(const AttnArgs& a, hipStream_t stream) {
+void launch_attention(const AttnArgs& a, hipStream_t stream, hipEvent_t done) {
   if (!attention_supported(a.D)) fail(PJRT_Error_Code_UNIMPLEMENTED, "attention head dim " + std::to_string(a.D));
   if (a.Sq % BQ || a.Sk % BKV) fail(PJRT_Error_Code_UNIMPLEMENTED, "attention sequence lengths must be multiples of 128 / 64");
   if (a.qs[3] != 1 || a.ks[3] != 1 || a.vs[3] != 1 || a.os[3] != 1)
@@ -328,7 +329,7 @@ void launch_attention(const AttnArgs& a, hipStream_t stream) {
   if (a.ks[2] > (1 << 20) || a.vs[2] > (1 << 20))
     fail(PJRT_Error_Code_UNIMPLEMENTED, "attention key/value row stride too large");
   int64_t blocks = (int64_t)a.B * a.H * (a.Sq / BQ);
-  if (blocks == 0) return;
+  if (blocks == 0) return record_done(done, stream);
   hipError_t e;
   if (a.D == 128) {
     int lds = AttnCfg<128>::LDS;
@@ -338,7 +339,7 @@ void launch_attention(const AttnArgs& a, hipStream_t stream) {
       if (e != hipSuccess) fail(PJRT_Error_Code_INTERNAL, std::string("attention LDS attribute: ") + hipGetErrorString(e));
       attr128 = true;
     }
-    hipLaunchKernelGGL(attention_fwd_kernel<128>, dim3((unsigned)blocks), dim3(256), lds, stream, a);
+    launch_k(done, attention_fwd_kernel<128>, dim3((unsigned)blocks), dim3(256), (uint32_t)lds, stream, a);
   } else {
     int lds = AttnCfg<64>::LDS;
     static bool attr64 = false;
@@ -347,7 +348,7 @@ void launch_attention(const AttnArgs& a, hipStream_t stream) {
       if (e != hipSuccess) fail(PJRT_Error_Code_INTERNAL, std::string("attention LDS attribute: ") + hipGetErrorString(e));
       attr64 = true;
     }
-    hipLaunchKernelGGL(attention_fwd_kernel<64>, dim3((unsigned)blocks), dim3(256), lds, stream, a);
+    launch_k(done, attention_fwd_kernel<64>, dim3((unsigned)blocks), dim3(256), (uint32_t)lds, stream, a);
   }
   e = hipGetLastError();
   if (e != hipSuccess) fail(PJRT_Error_Code_INTERNAL, std::string("attention launch failed: ") + hipGetErrorString(e));

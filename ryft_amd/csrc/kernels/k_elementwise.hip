@@ -13,6 +13,7 @@
 #include "../common.h"
 #include "ew_device.h"
 #include "kernels.h"
+#include "launch.h"
 
 namespace ryft {
 
@@ -163,17 +164,17 @@ static bool prepare_vec(EwProgram& p, bool check_outputs) {
   return true;
 }
 
-void launch_elementwise(const EwProgram& p, hipStream_t stream) {
-  if (p.total == 0) return;
+void launch_elementwise(const EwProgram& p, hipStream_t stream, hipEvent_t done) {
+  if (p.total == 0) return record_done(done, stream);
   EwProgram v = p;
   if (prepare_vec(v, true)) {
     dim3 grid(grid_for(v.total / VEC, VNT)), block(VNT);
-    if (v.needs_coords) hipLaunchKernelGGL(ew_kernel_vec<true>, grid, block, 0, stream, v);
-    else hipLaunchKernelGGL(ew_kernel_vec<false>, grid, block, 0, stream, v);
+    if (v.needs_coords) launch_k(done, ew_kernel_vec<true>, grid, block, 0, stream, v);
+    else launch_k(done, ew_kernel_vec<false>, grid, block, 0, stream, v);
   } else {
     dim3 grid(grid_for(p.total, 256)), block(256);
-    if (p.needs_coords) hipLaunchKernelGGL(ew_kernel<true>, grid, block, 0, stream, p);
-    else hipLaunchKernelGGL(ew_kernel<false>, grid, block, 0, stream, p);
+    if (p.needs_coords) launch_k(done, ew_kernel<true>, grid, block, 0, stream, p);
+    else launch_k(done, ew_kernel<false>, grid, block, 0, stream, p);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) fail(PJRT_Error_Code_INTERNAL, std::string("elementwise launch failed: ") + hipGetErrorString(e));
@@ -291,28 +292,28 @@ __global__ void __launch_bounds__(VNT) reduce_kernel_vec(const ReduceArgs A) {
   }
 }
 
-void launch_reduce(const ReduceArgs& a, hipStream_t stream) {
-  if (a.outer == 0) return;
+void launch_reduce(const ReduceArgs& a, hipStream_t stream, hipEvent_t done) {
+  if (a.outer == 0) return record_done(done, stream);
   ReduceArgs v = a;
   if (a.inner % VEC == 0 && prepare_vec(v.prologue, false)) {
     const bool coords = v.prologue.needs_coords != 0;
     if (a.inner / VEC >= 2 * VNT) {  // long rows: a workgroup per row
       dim3 grid((unsigned)(a.outer < 256 * 16 ? a.outer : 256 * 16)), block(VNT);
-      if (coords) hipLaunchKernelGGL((reduce_kernel_vec<VNT, true>), grid, block, 0, stream, v);
-      else hipLaunchKernelGGL((reduce_kernel_vec<VNT, false>), grid, block, 0, stream, v);
+      if (coords) launch_k(done, reduce_kernel_vec<VNT, true>, grid, block, 0, stream, v);
+      else launch_k(done, reduce_kernel_vec<VNT, false>, grid, block, 0, stream, v);
     } else {  // a wavefront per row
       int64_t blocks = (a.outer + VNT / 64 - 1) / (VNT / 64);
       if (blocks > 256 * 16) blocks = 256 * 16;
       dim3 grid((unsigned)blocks), block(VNT);
-      if (coords) hipLaunchKernelGGL((reduce_kernel_vec<64, true>), grid, block, 0, stream, v);
-      else hipLaunchKernelGGL((reduce_kernel_vec<64, false>), grid, block, 0, stream, v);
+      if (coords) launch_k(done, reduce_kernel_vec<64, true>, grid, block, 0, stream, v);
+      else launch_k(done, reduce_kernel_vec<64, false>, grid, block, 0, stream, v);
     }
   } else {
     int64_t blocks = (a.outer + 3) / 4;
     if (blocks > 256 * 16) blocks = 256 * 16;
     dim3 grid((unsigned)blocks), block(256);
-    if (a.prologue.needs_coords) hipLaunchKernelGGL(reduce_kernel<true>, grid, block, 0, stream, a);
-    else hipLaunchKernelGGL(reduce_kernel<false>, grid, block, 0, stream, a);
+    if (a.prologue.needs_coords) launch_k(done, reduce_kernel<true>, grid, block, 0, stream, a);
+    else launch_k(done, reduce_kernel<false>, grid, block, 0, stream, a);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) fail(PJRT_Error_Code_INTERNAL, std::string("reduce launch failed: ") + hipGetErrorString(e));
@@ -500,17 +501,17 @@ static bool rownorm_launchable(const RowArgs& a) {
 }
 
 template <int G, int V>
-static void launch_row_g(const RowArgs& a, hipStream_t stream) {
+static void launch_row_g(const RowArgs& a, hipStream_t stream, hipEvent_t done) {
   constexpr int RB = VNT / G;
   int64_t blocks = (a.rows + RB - 1) / RB;
   if (blocks > 256 * 16) blocks = 256 * 16;
   dim3 grid((unsigned)blocks), block(VNT);
-  if (a.prog.needs_coords) hipLaunchKernelGGL((row_kernel<G, V, true>), grid, block, 0, stream, a);
-  else hipLaunchKernelGGL((row_kernel<G, V, false>), grid, block, 0, stream, a);
+  if (a.prog.needs_coords) launch_k(done, row_kernel<G, V, true>, grid, block, 0, stream, a);
+  else launch_k(done, row_kernel<G, V, false>, grid, block, 0, stream, a);
 }
 
-void launch_row(const RowArgs& a, hipStream_t stream) {
-  if (a.rows == 0 || a.inner == 0) return;
+void launch_row(const RowArgs& a, hipStream_t stream, hipEvent_t done) {
+  if (a.rows == 0 || a.inner == 0) return record_done(done, stream);
   if (a.n_red < 1 || a.n_red > ROW_MAX_RED || a.prog.rank < 1 || a.prog.shape[a.prog.rank - 1] != a.inner ||
       a.rows * a.inner != a.prog.total)
     fail(PJRT_Error_Code_INTERNAL, "row-fused step: arguments do not describe a [rows, inner] space");
@@ -521,21 +522,21 @@ void launch_row(const RowArgs& a, hipStream_t stream) {
     const int64_t blocks = a.rows < 256 * 16 ? a.rows : 256 * 16;
     const int64_t per_thread = (a.inner / 8 + VNT - 1) / VNT;
     const dim3 grid((unsigned)blocks), block(VNT);
-    if (per_thread <= 1) hipLaunchKernelGGL(rownorm_kernel<1>, grid, block, 0, stream, a);
-    else if (per_thread <= 2) hipLaunchKernelGGL(rownorm_kernel<2>, grid, block, 0, stream, a);
-    else if (per_thread <= 4) hipLaunchKernelGGL(rownorm_kernel<4>, grid, block, 0, stream, a);
-    else hipLaunchKernelGGL(rownorm_kernel<0>, grid, block, 0, stream, a);
+    if (per_thread <= 1) launch_k(done, rownorm_kernel<1>, grid, block, 0, stream, a);
+    else if (per_thread <= 2) launch_k(done, rownorm_kernel<2>, grid, block, 0, stream, a);
+    else if (per_thread <= 4) launch_k(done, rownorm_kernel<4>, grid, block, 0, stream, a);
+    else launch_k(done, rownorm_kernel<0>, grid, block, 0, stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) fail(PJRT_Error_Code_INTERNAL, std::string("row-norm launch failed: ") + hipGetErrorString(e));
     return;
   }
   RowArgs v = a;
   if (prepare_vec(v.prog, true)) {
-    if (a.inner / VEC >= VNT) launch_row_g<VNT, VEC>(v, stream);
-    else launch_row_g<64, VEC>(v, stream);
+    if (a.inner / VEC >= VNT) launch_row_g<VNT, VEC>(v, stream, done);
+    else launch_row_g<64, VEC>(v, stream, done);
   } else {
-    if (a.inner >= 4 * VNT) launch_row_g<VNT, 1>(a, stream);
-    else launch_row_g<64, 1>(a, stream);
+    if (a.inner >= 4 * VNT) launch_row_g<VNT, 1>(a, stream, done);
+    else launch_row_g<64, 1>(a, stream, done);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) fail(PJRT_Error_Code_INTERNAL, std::string("row-fused launch failed: ") + hipGetErrorString(e));

@@ -12,6 +12,7 @@
 #include "gemm_epilogue.h"
 #include "gemm_mfma.h"
 #include "kernels.h"
+#include "launch.h"
 
 namespace ryft {
 
@@ -242,8 +243,8 @@ int gemm_plan_splits(const GemmArgs& a) {
   return pick_mfma(g, &c) ? best : 1;
 }
 
-void launch_gemm(const GemmArgs& g, hipStream_t stream) {
-  if (g.M == 0 || g.N == 0 || g.batch == 0) return;
+void launch_gemm(const GemmArgs& g, hipStream_t stream, hipEvent_t done) {
+  if (g.M == 0 || g.N == 0 || g.batch == 0) return record_done(done, stream);
   Choice c;
   hipError_t e;
   if (g.K > 0 && pick_mfma(g, &c)) {
@@ -258,13 +259,16 @@ void launch_gemm(const GemmArgs& g, hipStream_t stream) {
     int64_t blocks = (int64_t)(g.M / c.bm) * (g.N / c.bn) * g.batch * splits;
     if (blocks > INT32_MAX) fail(PJRT_Error_Code_UNIMPLEMENTED, "too many GEMM tiles");
     void* args[] = {(void*)&g};
-    e = hipLaunchKernel(c.fn, dim3((unsigned)blocks), dim3(c.threads), args, (size_t)c.lds, stream);
+    hipEvent_t main_done = splits > 1 ? nullptr : done;  // split-K: the reduction launch carries it
+    e = main_done ? hipExtLaunchKernel(c.fn, dim3((unsigned)blocks), dim3(c.threads), args, (size_t)c.lds, stream,
+                                       nullptr, main_done, 0)
+                  : hipLaunchKernel(c.fn, dim3((unsigned)blocks), dim3(c.threads), args, (size_t)c.lds, stream);
     if (e == hipSuccess && splits > 1) {
       const int64_t quads = (int64_t)g.batch * g.M * g.N / 4;
       const unsigned rb = (unsigned)std::min<int64_t>((quads + 255) / 256, 256 * 16);
-      if (g.acc_is_int) hipLaunchKernelGGL((splitk_reduce_kernel<true, false>), dim3(rb), dim3(256), 0, stream, g);
-      else if (g.dual) hipLaunchKernelGGL((splitk_reduce_kernel<false, true>), dim3(rb), dim3(256), 0, stream, g);
-      else hipLaunchKernelGGL((splitk_reduce_kernel<false, false>), dim3(rb), dim3(256), 0, stream, g);
+      if (g.acc_is_int) launch_k(done, splitk_reduce_kernel<true, false>, dim3(rb), dim3(256), 0, stream, g);
+      else if (g.dual) launch_k(done, splitk_reduce_kernel<false, true>, dim3(rb), dim3(256), 0, stream, g);
+      else launch_k(done, splitk_reduce_kernel<false, false>, dim3(rb), dim3(256), 0, stream, g);
       e = hipGetLastError();
     }
   } else {
@@ -272,11 +276,11 @@ void launch_gemm(const GemmArgs& g, hipStream_t stream) {
     if (g.batch > 65535) fail(PJRT_Error_Code_UNIMPLEMENTED, "batch too large for the generic GEMM");
     if (g.acc_is_int) {
       if (g.dual) fail(PJRT_Error_Code_UNIMPLEMENTED, "integer dual GEMM");
-      hipLaunchKernelGGL((gemm_generic_kernel<true, false>), grid, block, 0, stream, g);
+      launch_k(done, gemm_generic_kernel<true, false>, grid, block, 0, stream, g);
     } else if (g.dual) {
-      hipLaunchKernelGGL((gemm_generic_kernel<false, true>), grid, block, 0, stream, g);
+      launch_k(done, gemm_generic_kernel<false, true>, grid, block, 0, stream, g);
     } else {
-      hipLaunchKernelGGL((gemm_generic_kernel<false, false>), grid, block, 0, stream, g);
+      launch_k(done, gemm_generic_kernel<false, false>, grid, block, 0, stream, g);
     }
     e = hipGetLastError();
   }

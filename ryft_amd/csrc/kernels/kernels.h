@@ -8,11 +8,12 @@
 
 namespace ryft {
 
-void launch_elementwise(const EwProgram& p, hipStream_t stream);
-void launch_reduce(const ReduceArgs& a, hipStream_t stream);
-void launch_row(const RowArgs& a, hipStream_t stream);
-void launch_gemm(const GemmArgs& a, hipStream_t stream);
-void launch_attention(const AttnArgs& a, hipStream_t stream);
+// `done` (optional): an event the launcher records on `stream` after its last kernel, as part of that launch.
+void launch_elementwise(const EwProgram& p, hipStream_t stream, hipEvent_t done = nullptr);
+void launch_reduce(const ReduceArgs& a, hipStream_t stream, hipEvent_t done = nullptr);
+void launch_row(const RowArgs& a, hipStream_t stream, hipEvent_t done = nullptr);
+void launch_gemm(const GemmArgs& a, hipStream_t stream, hipEvent_t done = nullptr);
+void launch_attention(const AttnArgs& a, hipStream_t stream, hipEvent_t done = nullptr);
 
 // Name of the GEMM kernel launch_gemm() picks for these arguments (used for profiling labels).
 const char* gemm_kernel_name(const GemmArgs& a);

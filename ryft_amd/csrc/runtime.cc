@@ -520,7 +520,15 @@ EventPtr execute(LoadedExecutable* le, Device* d, Buffer* const* args, size_t nu
     constexpr size_t kBlock = std::max({sizeof(EwProgram), sizeof(ReduceArgs), sizeof(GemmArgs), sizeof(RowArgs),
                                         sizeof(AttnArgs)});
     alignas(64) static thread_local unsigned char block[kBlock + 64];
-    for (const Step& step : plan.steps) {
+    // The execution's completion event rides on its last kernel launch when it can (no separate marker packet
+    // between consecutive executions); otherwise it is recorded after the last step.
+    done = std::make_shared<EventState>();
+    HIP_CHECK(hipEventCreateWithFlags(&done->hip_event, hipEventDisableTiming));
+    bool recorded = false;
+    for (size_t si = 0; si < plan.steps.size(); ++si) {
+      const Step& step = plan.steps[si];
+      hipEvent_t carry = (!prof && si + 1 == plan.steps.size() && step.kind != Step::COPY) ? done->hip_event : nullptr;
+      recorded |= carry != nullptr;
       StepTiming tm;
       if (prof) {
         tm.name = step.name;
@@ -546,12 +554,12 @@ EventPtr execute(LoadedExecutable* le, Device* d, Buffer* const* args, size_t nu
           *f = (char*)ptr[p.second] + (uintptr_t)(*f);
         }
         switch (step.kind) {
-          case Step::ELEMENTWISE: launch_elementwise(*(EwProgram*)block, st); break;
-          case Step::REDUCE: launch_reduce(*(ReduceArgs*)block, st); break;
-          case Step::ROW: launch_row(*(RowArgs*)block, st); break;
-          case Step::GEMM: launch_gemm(*(GemmArgs*)block, st); break;
-          case Step::ATTENTION: launch_attention(*(AttnArgs*)block, st); break;
-          default: break;
+          case Step::ELEMENTWISE: launch_elementwise(*(EwProgram*)block, st, carry); break;
+          case Step::REDUCE: launch_reduce(*(ReduceArgs*)block, st, carry); break;
+          case Step::ROW: launch_row(*(RowArgs*)block, st, carry); break;
+          case Step::GEMM: launch_gemm(*(GemmArgs*)block, st, carry); break;
+          case Step::ATTENTION: launch_attention(*(AttnArgs*)block, st, carry); break;
+          default: recorded = false; break;
         }
       }
       if (prof) {
@@ -560,7 +568,8 @@ EventPtr execute(LoadedExecutable* le, Device* d, Buffer* const* args, size_t nu
         c->timings.push_back(tm);
       }
     }
-    done = c->record_event(d);
+    if (!recorded) HIP_CHECK(hipEventRecord(done->hip_event, st));
+    c->enqueue_completion(done);
   }
   outputs->clear();
   for (size_t i = 0; i < plan.output_slots.size(); ++i) {
