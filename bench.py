@@ -40,6 +40,7 @@ def _cpu_baseline(name, seconds):
         "c4": (configs.c4_causal_attention, {"b": 1, "h": 2}, "2 of the 128 heads of C4"),
         "c5": (configs.c5_swiglu_fp8, {"m": 64}, "64 of the 512 tokens of C5"),
         "copy": (configs.hbm_copy_f32, {}, "the full copy calibration vector"),
+        "rmsnorm": (configs.rmsnorm_fp8_rows, {"m": 1024}, "1024 of the 16384 rows"),
     }
     fn, kw, desc = samples[name]
     w = fn(**kw)
@@ -65,7 +66,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "copy"],
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "copy", "rmsnorm"],
                     help="c1..c5: the BASELINE configs (c2 is the headline); copy: the HBM calibration kernel")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")

@@ -284,6 +284,44 @@ def hbm_copy_f32(n=64 * 1024 * 1024, seed=0xCC) -> Workload:
                     compute_dtype="f32", tolerance=0.0)
 
 
+def rmsnorm_fp8_rows(m=16384, d=4096, seed=0xCD) -> Workload:
+    """Calibration workload, not a BASELINE config: C5's normalise-and-quantise step (RMSNorm over 4096 bf16 values
+    with eps 1e-6 and a bf16 weight, result rounded to bf16 and converted to f8E4M3FN) on m rows — large enough for
+    HBM bandwidth, not launch latency, to bound the row-norm kernel (2 bytes read and 1 written per element)."""
+    xt, wt, xf, rf, wf = _t((m, d), "bf16"), _t((d,), "bf16"), _t((m, d), "f32"), _t((m,), "f32"), _t((d,), "f32")
+    qt = _t((m, d), "f8E4M3FN")
+    prog = f"""module {{
+  func.func @main(%arg0: {xt}, %arg1: {wt}) -> {qt} {{
+    %0 = stablehlo.convert %arg0 : ({xt}) -> {xf}
+    %1 = stablehlo.multiply %0, %0 : {xf}
+    %cst = stablehlo.constant dense<0.000000e+00> : tensor<f32>
+    %2 = stablehlo.reduce(%1 init: %cst) applies stablehlo.add across dimensions = [1] : ({xf}, tensor<f32>) -> {rf}
+    %cst_0 = stablehlo.constant dense<{_f32_literal(1.0 / d)}> : tensor<f32>
+    %3 = stablehlo.broadcast_in_dim %cst_0, dims = [] : (tensor<f32>) -> {rf}
+    %4 = stablehlo.multiply %2, %3 : {rf}
+    %cst_1 = stablehlo.constant dense<{_f32_literal(1e-6)}> : tensor<f32>
+    %5 = stablehlo.broadcast_in_dim %cst_1, dims = [] : (tensor<f32>) -> {rf}
+    %6 = stablehlo.add %4, %5 : {rf}
+    %7 = stablehlo.rsqrt %6 : {rf}
+    %8 = stablehlo.broadcast_in_dim %7, dims = [0] : ({rf}) -> {xf}
+    %9 = stablehlo.multiply %0, %8 : {xf}
+    %10 = stablehlo.convert %arg1 : ({wt}) -> {wf}
+    %11 = stablehlo.broadcast_in_dim %10, dims = [1] : ({wf}) -> {xf}
+    %12 = stablehlo.multiply %9, %11 : {xf}
+    %13 = stablehlo.convert %12 : ({xf}) -> {xt}
+    %14 = stablehlo.convert %13 : ({xt}) -> {qt}
+    return %14 : {qt}
+  }}
+}}
+"""
+    s16 = seed * 16
+    x = hd.f32_to_bf16_bits(hd.normal(s16 + 0, (m, d)))
+    w = hd.f32_to_bf16_bits(hd.normal(s16 + 1, (d,), 1.0, 0.02))
+    ins = [HostInput(x, BufferType.BF16, (m, d)), HostInput(w, BufferType.BF16, (d,))]
+    return Workload("rmsnorm_fp8_rows", prog, ins, flops=0.0, bytes=3.0 * m * d + 2.0 * d, compute_dtype="bf16",
+                    tolerance=3e-2)
+
+
 CONFIGS: Dict[str, Callable[..., Workload]] = {
     "c1": c1_f32_dot,
     "c2": c2_bf16_batched_dot,
@@ -291,4 +329,5 @@ CONFIGS: Dict[str, Callable[..., Workload]] = {
     "c4": c4_causal_attention,
     "c5": c5_swiglu_fp8,
     "copy": hbm_copy_f32,
+    "rmsnorm": rmsnorm_fp8_rows,
 }

@@ -42,6 +42,18 @@ __device__ __forceinline__ uint8_t f32_to_e4m3fn_bits(float f) {
   if (f != f) code = ((__float_as_uint(f) >> 24) & 0x80u) | 0x7fu;
   return (uint8_t)code;
 }
+// Four floats → four f8E4M3FN bytes (a, b, c, d from the low byte up): two v_cvt_pk_fp8_f32, each converting a pair.
+// Only NaN inputs need more (their sign back), and the instruction writes those as 0xff: a word with no byte of 0x7f
+// or 0xff (one zero-byte test on the low seven bits of each byte) is final, any other takes the per-element rule.
+__device__ __forceinline__ uint32_t f32x4_to_e4m3fn_bits(float a, float b, float c, float d) {
+  uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, (int)w, true);
+  const uint32_t t = ~w & 0x7f7f7f7fu;
+  if ((t - 0x01010101u) & ~t & 0x80808080u)
+    w = (uint32_t)f32_to_e4m3fn_bits(a) | ((uint32_t)f32_to_e4m3fn_bits(b) << 8) |
+        ((uint32_t)f32_to_e4m3fn_bits(c) << 16) | ((uint32_t)f32_to_e4m3fn_bits(d) << 24);
+  return w;
+}
 __device__ __forceinline__ float e4m3fn_bits_to_f32(uint32_t v) {
   uint32_t s = (v & 0x80u) << 24, e = (v >> 3) & 15u, m = v & 7u;
   float r;
@@ -213,6 +225,64 @@ __device__ __forceinline__ void load_words(const char* p, uint32_t* w) {
   }
 }
 
+// Raw words of V contiguous elements of a leaf starting at element `off` (V·size bytes, V·size-aligned): the first
+// V·size/4 words of w.
+template <int V>
+__device__ __forceinline__ void fetch_contig(const EwLeaf& L, int64_t off, uint32_t* w) {
+  static_assert(V == 4 || V == 8, "vector leaf loads are written for 4 or 8 elements");
+  const char* p = (const char*)L.ptr;
+  switch (L.dtype) {
+    case DT_F32: case DT_S32: case DT_U32: load_words<V * 4>(p + off * 4, w); break;
+    case DT_BF16: case DT_F16: case DT_S16: case DT_U16: load_words<V * 2>(p + off * 2, w); break;
+    default: load_words<V>(p + off, w); break;
+  }
+}
+
+// V register values (f32 bits / int32) from the raw words fetch_contig returned: one switch on the element type,
+// then straight-line decoding of the V elements (no per-element branches).
+template <int V>
+__device__ __forceinline__ void decode_contig(int dtype, const uint32_t* w, uint32_t* r) {
+  switch (dtype) {
+    case DT_F32: case DT_S32: case DT_U32:
+#pragma unroll
+      for (int e = 0; e < V; ++e) r[e] = w[e];
+      break;
+    case DT_BF16:
+#pragma unroll
+      for (int e = 0; e < V; ++e) r[e] = (e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16);
+      break;
+    case DT_F16:
+#pragma unroll
+      for (int e = 0; e < V; ++e)
+        r[e] = __float_as_uint((float)__builtin_bit_cast(_Float16, (uint16_t)(w[e >> 1] >> (16 * (e & 1)))));
+      break;
+    case DT_S16:
+#pragma unroll
+      for (int e = 0; e < V; ++e) r[e] = (uint32_t)(int32_t)(int16_t)(w[e >> 1] >> (16 * (e & 1)));
+      break;
+    case DT_U16:
+#pragma unroll
+      for (int e = 0; e < V; ++e) r[e] = (w[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+      break;
+    case DT_F8E4M3FN:
+#pragma unroll
+      for (int e = 0; e < V; ++e) r[e] = __float_as_uint(e4m3fn_bits_to_f32((w[e >> 2] >> (8 * (e & 3))) & 0xffu));
+      break;
+    case DT_F8E5M2:
+#pragma unroll
+      for (int e = 0; e < V; ++e) r[e] = __float_as_uint(e5m2_bits_to_f32((w[e >> 2] >> (8 * (e & 3))) & 0xffu));
+      break;
+    case DT_S8:
+#pragma unroll
+      for (int e = 0; e < V; ++e) r[e] = (uint32_t)(int32_t)(int8_t)(w[e >> 2] >> (8 * (e & 3)));
+      break;
+    default:  // u8, pred
+#pragma unroll
+      for (int e = 0; e < V; ++e) r[e] = (w[e >> 2] >> (8 * (e & 3))) & 0xffu;
+      break;
+  }
+}
+
 // Element bits of a leaf at V consecutive innermost positions starting at linear index `lin` (coordinates `coord`).
 template <int V>
 __device__ __forceinline__ void load_leaf(const EwLeaf& L, int64_t lin, const int32_t* coord, int rank, uint32_t* r) {
@@ -225,59 +295,10 @@ __device__ __forceinline__ void load_leaf(const EwLeaf& L, int64_t lin, const in
 #pragma unroll
       for (int e = 0; e < V; ++e) r[e] = x;
     } else if (L.vmode == EW_VEC_CONTIG) {
-      // V elements of ≤ 4 bytes, aligned to V·size (checked by the launcher); one switch on the element type, then
-      // straight-line decoding of the V elements (no per-element branches)
-      static_assert(V == 4 || V == 8, "vector leaf loads are written for 4 or 8 elements");
-      const char* p = (const char*)L.ptr;
+      // V elements of ≤ 4 bytes, aligned to V·size (checked by the launcher)
       uint32_t w[V];
-      switch (L.dtype) {
-        case DT_F32: case DT_S32: case DT_U32:
-          load_words<V * 4>(p + off * 4, w);
-#pragma unroll
-          for (int e = 0; e < V; ++e) r[e] = w[e];
-          break;
-        case DT_BF16:
-          load_words<V * 2>(p + off * 2, w);
-#pragma unroll
-          for (int e = 0; e < V; ++e) r[e] = (e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16);
-          break;
-        case DT_F16:
-          load_words<V * 2>(p + off * 2, w);
-#pragma unroll
-          for (int e = 0; e < V; ++e)
-            r[e] = __float_as_uint((float)__builtin_bit_cast(_Float16, (uint16_t)(w[e >> 1] >> (16 * (e & 1)))));
-          break;
-        case DT_S16:
-          load_words<V * 2>(p + off * 2, w);
-#pragma unroll
-          for (int e = 0; e < V; ++e) r[e] = (uint32_t)(int32_t)(int16_t)(w[e >> 1] >> (16 * (e & 1)));
-          break;
-        case DT_U16:
-          load_words<V * 2>(p + off * 2, w);
-#pragma unroll
-          for (int e = 0; e < V; ++e) r[e] = (w[e >> 1] >> (16 * (e & 1))) & 0xffffu;
-          break;
-        case DT_F8E4M3FN:
-          load_words<V>(p + off, w);
-#pragma unroll
-          for (int e = 0; e < V; ++e) r[e] = __float_as_uint(e4m3fn_bits_to_f32((w[e >> 2] >> (8 * (e & 3))) & 0xffu));
-          break;
-        case DT_F8E5M2:
-          load_words<V>(p + off, w);
-#pragma unroll
-          for (int e = 0; e < V; ++e) r[e] = __float_as_uint(e5m2_bits_to_f32((w[e >> 2] >> (8 * (e & 3))) & 0xffu));
-          break;
-        case DT_S8:
-          load_words<V>(p + off, w);
-#pragma unroll
-          for (int e = 0; e < V; ++e) r[e] = (uint32_t)(int32_t)(int8_t)(w[e >> 2] >> (8 * (e & 3)));
-          break;
-        default:  // u8, pred
-          load_words<V>(p + off, w);
-#pragma unroll
-          for (int e = 0; e < V; ++e) r[e] = (w[e >> 2] >> (8 * (e & 3))) & 0xffu;
-          break;
-      }
+      fetch_contig<V>(L, off, w);
+      decode_contig<V>(L.dtype, w, r);
     } else {
 #pragma unroll
       for (int e = 0; e < V; ++e) r[e] = load_bits(L.ptr, off + (int64_t)e * L.vstride, L.dtype);
@@ -287,9 +308,10 @@ __device__ __forceinline__ void load_leaf(const EwLeaf& L, int64_t lin, const in
 
 // Register files of the VM. Operands are moved as whole rows of V elements.
 //  * RegFile1: one element per thread in a VGPR array (indexed with the uniform register number: indirect moves).
-//  * SwitchRegFile<V>: V elements per thread in twelve named VGPR rows picked by a uniform switch (a V-wide array
-//    indexed with the register number would be placed in private memory, turning every operand into a scratch
-//    round trip).
+//  * SwitchRegFile<V, NR>: V elements per thread in NR (≤ twelve) named VGPR rows picked by a uniform switch (a
+//    V-wide array indexed with the register number would be placed in private memory, turning every operand into a
+//    scratch round trip). Programs that use only the first NR registers run with the smaller file, which leaves VGPRs
+//    for more waves per SIMD.
 struct RegFile1 {
   uint32_t v[EW_MAX_REGS];
   __device__ __forceinline__ void load(int r, uint32_t* out) const { out[0] = v[r]; }
@@ -297,19 +319,19 @@ struct RegFile1 {
   __device__ __forceinline__ uint32_t get(int r) const { return v[r]; }
 };
 
-template <int V>
+template <int V, int NR = EW_MAX_REGS>
 struct SwitchRegFile {
   // twelve named rows held as vector values and selected by a uniform switch: the merged switch arms become phis of
   // values, which stay in VGPRs (rows kept as arrays would be merged into a phi of pointers and spilled to private
   // memory)
-  static_assert(EW_MAX_REGS == 12, "SwitchRegFile names twelve registers");
+  static_assert(EW_MAX_REGS == 12 && NR >= 1 && NR <= 12, "SwitchRegFile names up to twelve registers");
   typedef uint32_t row_t __attribute__((ext_vector_type(V)));
   row_t r0, r1, r2, r3, r4, r5, r6, r7, r8, r9, r10, r11;
 #define RF_ROWS(X) X(0) X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8) X(9) X(10) X(11)
   __device__ __forceinline__ void load(int r, uint32_t* out) const {
     row_t v = r0;
     switch (r) {
-#define RF_LOAD(i) case i: v = r##i; break;
+#define RF_LOAD(i) case i: if constexpr (i < NR) v = r##i; break;
       RF_ROWS(RF_LOAD)
 #undef RF_LOAD
       default: break;
@@ -322,7 +344,7 @@ struct SwitchRegFile {
 #pragma unroll
     for (int e = 0; e < V; ++e) v[e] = in[e];
     switch (r) {
-#define RF_STORE(i) case i: r##i = v; break;
+#define RF_STORE(i) case i: if constexpr (i < NR) r##i = v; break;
       RF_ROWS(RF_STORE)
 #undef RF_STORE
       default: break;
@@ -332,7 +354,7 @@ struct SwitchRegFile {
 };
 
 // Number of register operands an instruction reads.
-__device__ __forceinline__ int ew_nsrc(int op) {
+__host__ __device__ __forceinline__ int ew_nsrc(int op) {
   if (op == EW_LOAD || op == EW_CONST || op == EW_IOTA || op == EW_ACC) return 0;
   if (op == EW_SELECT || op == EW_FCLAMP || op == EW_ICLAMP) return 3;
   if (op >= EW_ADD) return 2;

@@ -62,19 +62,38 @@ __device__ __forceinline__ void store_vec(void* out, int64_t lin, int dtype, con
       break;
     }
     case DT_F8E4M3FN: case DT_F8E5M2: case DT_S8: case DT_U8: case DT_PRED: {
+      // one uniform branch per vector, then straight-line conversion of its V elements
+      if (dtype == DT_F8E4M3FN && is_float) {
+        uint32_t w[V / 4];
+#pragma unroll
+        for (int q = 0; q < V / 4; ++q)
+          w[q] = f32x4_to_e4m3fn_bits(__uint_as_float(v[4 * q]), __uint_as_float(v[4 * q + 1]),
+                                      __uint_as_float(v[4 * q + 2]), __uint_as_float(v[4 * q + 3]));
+        if constexpr (V == 8) *(u32x2v*)(p + lin) = u32x2v{w[0], w[1]};
+        else *(uint32_t*)(p + lin) = w[0];
+        break;
+      }
+      uint32_t byte[V];
+      if (dtype == DT_F8E4M3FN) {
+#pragma unroll
+        for (int e = 0; e < V; ++e) byte[e] = f32_to_e4m3fn_bits(is_float ? __uint_as_float(v[e]) : (float)(int32_t)v[e]);
+      } else if (dtype == DT_F8E5M2) {
+#pragma unroll
+        for (int e = 0; e < V; ++e) byte[e] = f32_to_e5m2_bits(is_float ? __uint_as_float(v[e]) : (float)(int32_t)v[e]);
+      } else if (dtype == DT_PRED) {
+#pragma unroll
+        for (int e = 0; e < V; ++e) byte[e] = v[e] != 0;
+      } else if (is_float) {
+#pragma unroll
+        for (int e = 0; e < V; ++e) byte[e] = (uint32_t)f2i_sat(__uint_as_float(v[e]), dtype) & 0xffu;
+      } else {
+#pragma unroll
+        for (int e = 0; e < V; ++e) byte[e] = v[e] & 0xffu;
+      }
       uint32_t w[V / 4];
 #pragma unroll
-      for (int q = 0; q < V / 4; ++q) w[q] = 0u;
-#pragma unroll
-      for (int e = 0; e < V; ++e) {
-        const float f = is_float ? __uint_as_float(v[e]) : (float)(int32_t)v[e];
-        uint32_t byte;
-        if (dtype == DT_F8E4M3FN) byte = f32_to_e4m3fn_bits(f);
-        else if (dtype == DT_F8E5M2) byte = f32_to_e5m2_bits(f);
-        else if (dtype == DT_PRED) byte = v[e] != 0;
-        else byte = is_float ? (uint32_t)f2i_sat(f, dtype) & 0xffu : v[e] & 0xffu;
-        w[e >> 2] |= byte << (8 * (e & 3));
-      }
+      for (int q = 0; q < V / 4; ++q)
+        w[q] = byte[4 * q] | (byte[4 * q + 1] << 8) | (byte[4 * q + 2] << 16) | (byte[4 * q + 3] << 24);
       if constexpr (V == 8) *(u32x2v*)(p + lin) = u32x2v{w[0], w[1]};
       else *(uint32_t*)(p + lin) = w[0];
       break;
@@ -100,12 +119,12 @@ __device__ __forceinline__ void decompose_fast(int64_t lin, const EwProgram& P, 
   }
 }
 
-template <bool COORDS>
+template <bool COORDS, int NR>
 __global__ void __launch_bounds__(VNT) ew_kernel_vec(const EwProgram P) {
   __shared__ EwTables T;
   stage_tables(P, &T);
   __syncthreads();
-  VRegs R;
+  SwitchRegFile<VEC, NR> R;
   const int64_t chunks = P.total / VEC;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < chunks; c += stride) {
@@ -119,6 +138,22 @@ __global__ void __launch_bounds__(VNT) ew_kernel_vec(const EwProgram P) {
       store_vec<VEC>(P.out_ptr[o], lin, P.out_dtype[o], v, (P.out_float_mask >> o) & 1);
     }
   }
+}
+
+// Registers a program touches (one past the highest register it reads or writes).
+constexpr int EW_SMALL_REGS = 4;
+static int program_regs(const EwProgram& p) {
+  int n = 0;
+  for (int i = 0; i < p.n_instr; ++i) {
+    const EwInstr& I = p.instr[i];
+    n = std::max(n, (int)I.dst + 1);
+    const int src = ew_nsrc(I.op);
+    if (src >= 1) n = std::max(n, (int)I.a + 1);
+    if (src >= 2) n = std::max(n, (int)I.b + 1);
+    if (src >= 3) n = std::max(n, (int)I.c + 1);
+  }
+  for (int o = 0; o < p.n_out; ++o) n = std::max(n, (int)p.out_reg[o] + 1);
+  return n;
 }
 
 static int grid_for(int64_t total, int threads) {
@@ -169,8 +204,14 @@ void launch_elementwise(const EwProgram& p, hipStream_t stream, hipEvent_t done)
   EwProgram v = p;
   if (prepare_vec(v, true)) {
     dim3 grid(grid_for(v.total / VEC, VNT)), block(VNT);
-    if (v.needs_coords) launch_k(done, ew_kernel_vec<true>, grid, block, 0, stream, v);
-    else launch_k(done, ew_kernel_vec<false>, grid, block, 0, stream, v);
+    const bool small = program_regs(v) <= EW_SMALL_REGS;
+    if (v.needs_coords) {
+      if (small) launch_k(done, ew_kernel_vec<true, EW_SMALL_REGS>, grid, block, 0, stream, v);
+      else launch_k(done, ew_kernel_vec<true, EW_MAX_REGS>, grid, block, 0, stream, v);
+    } else {
+      if (small) launch_k(done, ew_kernel_vec<false, EW_SMALL_REGS>, grid, block, 0, stream, v);
+      else launch_k(done, ew_kernel_vec<false, EW_MAX_REGS>, grid, block, 0, stream, v);
+    }
   } else {
     dim3 grid(grid_for(p.total, 256)), block(256);
     if (p.needs_coords) launch_k(done, ew_kernel<true>, grid, block, 0, stream, p);
@@ -391,44 +432,188 @@ __global__ void __launch_bounds__(VNT) row_kernel(const RowArgs A) {
 
 // ------------------------------------------------------------------------------------------------ row-norm path
 // Eight consecutive elements of a float row as f32 (f32, bf16 or f16 storage; 16-byte aligned groups).
-__device__ __forceinline__ void load8_f32(const void* p, int64_t i, int dt, float* v) {
+// Raw words of 8 consecutive f32 / bf16 / f16 elements (8 words for f32, 4 for the 16-bit types).
+__device__ __forceinline__ void load8_raw(const void* p, int64_t i, int dt, uint32_t* w) {
   const char* c = (const char*)p;
   if (dt == DT_F32) {
     const u32x4v a = *(const u32x4v*)(c + i * 4), b = *(const u32x4v*)(c + i * 4 + 16);
-    v[0] = __uint_as_float(a.x), v[1] = __uint_as_float(a.y), v[2] = __uint_as_float(a.z), v[3] = __uint_as_float(a.w);
-    v[4] = __uint_as_float(b.x), v[5] = __uint_as_float(b.y), v[6] = __uint_as_float(b.z), v[7] = __uint_as_float(b.w);
+    w[0] = a.x, w[1] = a.y, w[2] = a.z, w[3] = a.w, w[4] = b.x, w[5] = b.y, w[6] = b.z, w[7] = b.w;
   } else {
     const u32x4v a = *(const u32x4v*)(c + i * 2);
-    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+    w[0] = a.x, w[1] = a.y, w[2] = a.z, w[3] = a.w;
+  }
+}
+
+__device__ __forceinline__ void decode8_f32(int dt, const uint32_t* w, float* v) {
+  if (dt == DT_F32) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = __uint_as_float(w[e]);
+  } else if (dt == DT_BF16) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[2 * q] = __uint_as_float(w[q] << 16), v[2 * q + 1] = __uint_as_float(w[q] & 0xffff0000u);
+  } else {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      if (dt == DT_BF16) {
-        v[2 * q] = __uint_as_float(w[q] << 16), v[2 * q + 1] = __uint_as_float(w[q] & 0xffff0000u);
-      } else {
-        v[2 * q] = (float)__builtin_bit_cast(_Float16, (uint16_t)w[q]);
-        v[2 * q + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[q] >> 16));
-      }
+      v[2 * q] = (float)__builtin_bit_cast(_Float16, (uint16_t)w[q]);
+      v[2 * q + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[q] >> 16));
     }
   }
 }
 
-// One workgroup per row. A thread owns chunks t, t + 256, ... of 8 elements; with NC > 0 (rows of at most NC·2048
-// elements) it loads them — and the matching weight chunks — once, up front, and keeps them in registers; NC = 0
-// reads the row again (from L2) for the scaling pass. Σx² is folded per thread in element order, then across lanes
-// and wavefronts in the same order as the interpreted row kernel, so both paths give the same bits. Products and
-// sums are separately rounded f32 operations (no contraction into FMAs), as the program specifies.
+__device__ __forceinline__ void load8_f32(const void* p, int64_t i, int dt, float* v) {
+  uint32_t w[8];
+  load8_raw(p, i, dt, w);
+  decode8_f32(dt, w, v);
+}
+
+// Rounds 8 floats to the precision of `dtype` (a no-op for f32): one switch, straight-line element work.
+__device__ __forceinline__ void round8(float* y, int dtype) {
+  switch (dtype) {
+    case DT_BF16:
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const uint32_t pk = f32x2_to_bf16x2_bits(y[e], y[e + 1]);
+        y[e] = __uint_as_float(pk << 16), y[e + 1] = __uint_as_float(pk & 0xffff0000u);
+      }
+      break;
+    case DT_F16:
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] = round_float(y[e], DT_F16);
+      break;
+    case DT_F8E4M3FN:
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] = round_float(y[e], DT_F8E4M3FN);
+      break;
+    case DT_F8E5M2:
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] = round_float(y[e], DT_F8E5M2);
+      break;
+    default: break;
+  }
+}
+
+// The scale 1/√(Σx²·α + ε) of a row from its folded Σx² (the init value enters last, as in the interpreted kernel).
+__device__ __forceinline__ float rownorm_scale(const RowArgs& A, float acc) {
+  const RowNormArgs& N = A.norm;
+  acc = acc + __uint_as_float(A.init[0]);
+  float t = N.alpha_div ? acc / N.alpha : acc * N.alpha;
+  t = t + N.eps;
+  return 1.0f / sqrtf(t);
+}
+
+// y = round(x·s·w) for 8 elements, stored as the output type; uniform branches once per vector of 8, straight-line
+// element work inside each.
+__device__ __forceinline__ void rownorm_emit(const RowNormArgs& N, int64_t lin, const float* v, const float* wv, float s,
+                                             int out_dtype) {
+#pragma clang fp contract(off)
+  float y[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) y[e] = v[e] * s;
+  if (N.w) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) y[e] = y[e] * wv[e];
+  }
+  round8(y, N.mid_round);
+  uint32_t b[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) b[e] = __float_as_uint(y[e]);
+  store_vec<8>(N.out, lin, out_dtype, b, true);
+}
+
+// RMSNorm rows of at most 64·8·NCW elements, one wavefront per row: lane l owns chunks l, l + 64, ... of 8
+// elements, loads them all at once (raw words, XB bytes per element) and keeps them in registers, folds Σx² in
+// element order, then across lanes by shuffles and a broadcast from lane 0 — the order of the interpreted row kernel
+// for such rows, so both paths give the same bits. No barrier sits between rows, so a compute unit has as many rows
+// in flight as it holds waves. The weight row, shared by all rows, is staged once per workgroup in LDS. Products
+// and sums are separately rounded f32 operations (no contraction into FMAs), as the program specifies.
+template <int NCW, int XB>
+__global__ void __launch_bounds__(VNT) rownorm_wave_kernel(const RowArgs A) {
+#pragma clang fp contract(off)
+  extern __shared__ __attribute__((aligned(16))) char wrow[];
+  const RowNormArgs& N = A.norm;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t chunks = A.inner / 8;
+  if (N.w) {
+    const int64_t nbytes = A.inner * (N.w_dtype == DT_F32 ? 4 : 2);
+    for (int64_t b = threadIdx.x * 16; b < nbytes; b += VNT * 16)
+      *(u32x4v*)(wrow + b) = *(const u32x4v*)((const char*)N.w + b);
+  }
+  __syncthreads();
+  constexpr int W = XB * 2;  // raw words per chunk
+  auto decode_x = [&](const uint32_t* w, float* v) {
+    if constexpr (XB == 4) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = __uint_as_float(w[e]);
+    } else {
+      decode8_f32(N.x_dtype, w, v);
+    }
+  };
+  for (int64_t o = (int64_t)blockIdx.x * (VNT / 64) + wave; o < A.rows; o += (int64_t)gridDim.x * (VNT / 64)) {
+    const char* xrow = (const char*)N.x + o * A.inner * XB;
+    uint32_t xr[NCW][W];
+#pragma unroll
+    for (int q = 0; q < NCW; ++q) {
+      const int c = lane + 64 * q;
+      if (c < chunks) {
+#pragma unroll
+        for (int h = 0; h < W / 4; ++h) {
+          const u32x4v a = *(const u32x4v*)(xrow + (int64_t)c * 8 * XB + 16 * h);
+          xr[q][4 * h] = a.x, xr[q][4 * h + 1] = a.y, xr[q][4 * h + 2] = a.z, xr[q][4 * h + 3] = a.w;
+        }
+      }
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NCW; ++q)
+      if (lane + 64 * q < chunks) {
+        float v[8];
+        decode_x(xr[q], v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc = acc + v[e] * v[e];
+      }
+    for (int off = 32; off > 0; off >>= 1) acc = acc + __shfl_xor(acc, off, 64);
+    acc = __shfl(acc, 0, 64);
+    const float s = rownorm_scale(A, acc);
+    // one loop per output type, so each unrolled loop body holds that type's conversion only
+    auto emit_all = [&](auto odt) {
+#pragma unroll
+      for (int q = 0; q < NCW; ++q) {
+        const int c = lane + 64 * q;
+        if (c < chunks) {
+          float v[8], wv[8];
+          decode_x(xr[q], v);
+          if (N.w) load8_f32(wrow, (int64_t)c * 8, N.w_dtype, wv);
+          rownorm_emit(N, o * A.inner + (int64_t)c * 8, v, wv, s, decltype(odt)::value);
+        }
+      }
+    };
+    switch (N.out_dtype) {
+      case DT_F32: emit_all(std::integral_constant<int, DT_F32>{}); break;
+      case DT_BF16: emit_all(std::integral_constant<int, DT_BF16>{}); break;
+      case DT_F16: emit_all(std::integral_constant<int, DT_F16>{}); break;
+      case DT_F8E4M3FN: emit_all(std::integral_constant<int, DT_F8E4M3FN>{}); break;
+      default: emit_all(std::integral_constant<int, DT_F8E5M2>{}); break;
+    }
+  }
+}
+
+// One workgroup per row (rows too long for a wavefront, or too few rows to fill the chip that way). A thread owns
+// chunks t, t + 256, ... of 8 elements; with NC > 0 (rows of at most NC·2048 elements) it loads them — and the
+// matching weight chunks — once, up front, and keeps them in registers; NC = 0 reads the row again (from L2) for the
+// scaling pass. Σx² is folded per thread in element order, then across lanes and wavefronts (through LDS) in the
+// order of the interpreted row kernel for such rows.
 template <int NC>
-__global__ void __launch_bounds__(VNT) rownorm_kernel(const RowArgs A) {
+__global__ void __launch_bounds__(VNT) rownorm_block_kernel(const RowArgs A) {
 #pragma clang fp contract(off)
   __shared__ float part[VNT / 64];
   const RowNormArgs& N = A.norm;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t chunks = A.inner / 8;
-  const float init = __uint_as_float(A.init[0]);
+  constexpr int NQ = NC > 0 ? NC : 1;
   for (int64_t o = blockIdx.x; o < A.rows; o += gridDim.x) {
     const int64_t base = o * A.inner;
     float acc = 0.0f;
-    float xs[NC > 0 ? NC : 1][8], ws[NC > 0 ? NC : 1][8];
+    float xs[NQ][8], ws[NQ][8];
     if constexpr (NC > 0) {
 #pragma unroll
       for (int q = 0; q < NC; ++q) {
@@ -459,35 +644,32 @@ __global__ void __launch_bounds__(VNT) rownorm_kernel(const RowArgs A) {
     acc = part[0];
     for (int w = 1; w < VNT / 64; ++w) acc = acc + part[w];
     __syncthreads();
-    acc = acc + init;
-    float t = N.alpha_div ? acc / N.alpha : acc * N.alpha;
-    t = t + N.eps;
-    const float s = 1.0f / sqrtf(t);
-    auto emit = [&](int64_t c, const float* v, const float* wv) {
-      uint32_t b[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float y = v[e] * s;
-        if (N.w) y = y * wv[e];
-        b[e] = __float_as_uint(round_float(y, N.mid_round));
-      }
-      store_vec<8>(N.out, base + c * 8, N.out_dtype, b, true);
-    };
+    const float s = rownorm_scale(A, acc);
     if constexpr (NC > 0) {
 #pragma unroll
       for (int q = 0; q < NC; ++q) {
         const int64_t c = threadIdx.x + (int64_t)q * VNT;
-        if (c < chunks) emit(c, xs[q], ws[q]);
+        if (c < chunks) rownorm_emit(N, base + c * 8, xs[q], ws[q], s, N.out_dtype);
       }
     } else {
       for (int64_t c = threadIdx.x; c < chunks; c += VNT) {
         float v[8], wv[8];
         load8_f32(N.x, base + c * 8, N.x_dtype, v);
         if (N.w) load8_f32(N.w, c * 8, N.w_dtype, wv);
-        emit(c, v, wv);
+        rownorm_emit(N, base + c * 8, v, wv, s, N.out_dtype);
       }
     }
   }
+}
+
+// Whether a [rows, inner] row step gives each row one wavefront (else one workgroup), in the interpreted row kernel
+// and in the RMSNorm kernels alike, so both fold a row's sums in the same order: short rows always; rows of up to
+// ROW_WAVE_CHUNKS 8-element vectors when there are enough of them to keep every compute unit's waves busy (with few
+// rows, splitting each row over a workgroup's four waves finishes sooner).
+constexpr int64_t ROW_WAVE_CHUNKS = 64 * 16;
+constexpr int64_t ROW_WAVE_MIN_ROWS = 2048;
+static bool row_per_wave(int64_t rows, int64_t inner) {
+  return inner / VEC < VNT || (inner / VEC <= ROW_WAVE_CHUNKS && rows >= ROW_WAVE_MIN_ROWS);
 }
 
 static bool rownorm_launchable(const RowArgs& a) {
@@ -519,21 +701,45 @@ void launch_row(const RowArgs& a, hipStream_t stream, hipEvent_t done) {
     if (a.phase_end[k] < (k ? a.phase_end[k - 1] : 0) || a.phase_end[k] > a.prog.n_instr)
       fail(PJRT_Error_Code_INTERNAL, "row-fused step: phase bounds outside the program");
   if (a.fast == ROW_FAST_NORM && rownorm_launchable(a)) {
-    const int64_t blocks = a.rows < 256 * 16 ? a.rows : 256 * 16;
-    const int64_t per_thread = (a.inner / 8 + VNT - 1) / VNT;
-    const dim3 grid((unsigned)blocks), block(VNT);
-    if (per_thread <= 1) launch_k(done, rownorm_kernel<1>, grid, block, 0, stream, a);
-    else if (per_thread <= 2) launch_k(done, rownorm_kernel<2>, grid, block, 0, stream, a);
-    else if (per_thread <= 4) launch_k(done, rownorm_kernel<4>, grid, block, 0, stream, a);
-    else launch_k(done, rownorm_kernel<0>, grid, block, 0, stream, a);
+    const int64_t chunks = a.inner / 8;
+    const dim3 block(VNT);
+    if (row_per_wave(a.rows, a.inner)) {
+      // a wavefront per row, four rows per workgroup, the weight row in dynamic LDS
+      int64_t blocks = (a.rows + 3) / 4;
+      if (blocks > 256 * 64) blocks = 256 * 64;
+      const dim3 grid((unsigned)blocks);
+      const uint32_t lds = a.norm.w ? (uint32_t)(a.inner * (a.norm.w_dtype == DT_F32 ? 4 : 2)) : 0u;
+      const int ncw = (int)((chunks + 63) / 64);
+      auto go = [&](auto kernel) { launch_k(done, kernel, grid, block, lds, stream, a); };
+      if (a.norm.x_dtype == DT_F32) {
+        if (ncw <= 1) go(rownorm_wave_kernel<1, 4>);
+        else if (ncw <= 2) go(rownorm_wave_kernel<2, 4>);
+        else if (ncw <= 4) go(rownorm_wave_kernel<4, 4>);
+        else if (ncw <= 8) go(rownorm_wave_kernel<8, 4>);
+        else go(rownorm_wave_kernel<16, 4>);
+      } else {
+        if (ncw <= 1) go(rownorm_wave_kernel<1, 2>);
+        else if (ncw <= 2) go(rownorm_wave_kernel<2, 2>);
+        else if (ncw <= 4) go(rownorm_wave_kernel<4, 2>);
+        else if (ncw <= 8) go(rownorm_wave_kernel<8, 2>);
+        else go(rownorm_wave_kernel<16, 2>);
+      }
+    } else {
+      const dim3 grid((unsigned)(a.rows < 256 * 16 ? a.rows : 256 * 16));
+      const int64_t per_thread = (chunks + VNT - 1) / VNT;
+      if (per_thread <= 1) launch_k(done, rownorm_block_kernel<1>, grid, block, 0, stream, a);
+      else if (per_thread <= 2) launch_k(done, rownorm_block_kernel<2>, grid, block, 0, stream, a);
+      else if (per_thread <= 4) launch_k(done, rownorm_block_kernel<4>, grid, block, 0, stream, a);
+      else launch_k(done, rownorm_block_kernel<0>, grid, block, 0, stream, a);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) fail(PJRT_Error_Code_INTERNAL, std::string("row-norm launch failed: ") + hipGetErrorString(e));
     return;
   }
   RowArgs v = a;
   if (prepare_vec(v.prog, true)) {
-    if (a.inner / VEC >= VNT) launch_row_g<VNT, VEC>(v, stream, done);
-    else launch_row_g<64, VEC>(v, stream, done);
+    if (row_per_wave(a.rows, a.inner)) launch_row_g<64, VEC>(v, stream, done);
+    else launch_row_g<VNT, VEC>(v, stream, done);
   } else {
     if (a.inner >= 4 * VNT) launch_row_g<VNT, 1>(a, stream, done);
     else launch_row_g<64, 1>(a, stream, done);

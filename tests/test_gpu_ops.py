@@ -7,7 +7,7 @@ workgroup-per-row reduction."""
 import numpy as np
 import pytest
 
-from oracle import stablehlo as sh
+from oracle import numerics, stablehlo as sh
 from ryft_amd import configs, hostdata as hd, pjrt
 from tests.helpers import check, oracle_outputs, run_pjrt
 
@@ -87,6 +87,32 @@ def test_convert_chain_bf16_f8(gpu_client, shape):
         # conversions are exact: compare bits
         assert np.array_equal(np.asarray(o).view(np.uint8), sh.to_raw(w[0], w[1]).view(np.uint8)) or \
             np.array_equal(np.isnan(sh.from_raw(o, w[1])), np.isnan(w[0])), f"convert output {i}"
+
+
+@pytest.mark.parametrize("shape", [(4, 64), (8, 33)])
+def test_convert_f32_to_f8e4m3fn_special_values_bits(gpu_client, shape):
+    # every special value in every byte position of a packed 4-byte group (the 8-wide store converts pairs and fixes
+    # NaN signs only for groups holding a 0x7f / 0xff byte): NaNs of both signs, infinities, the overflow boundary
+    # (464 rounds to 448, anything above is NaN), ±0, subnormals and their ties, mixed with ordinary values
+    specials = np.array([0x7fc00000, 0xffc00000, 0x7f800001, 0x7f800000, 0xff800000], np.uint32).view(np.float32)
+    specials = np.concatenate([specials, np.array([448, 449, 463.99, 464, 464.01, -464, -465, 0.0, -0.0, 2.0 ** -9,
+                                                   2.0 ** -10, 3 * 2.0 ** -10, -2.0 ** -10, 1e-30, 1.5, -2.5],
+                                                  np.float32)])
+    n = shape[0] * shape[1]
+    x = hd.normal(7, (n,), 0, 50).astype(np.float32)
+    for i, v in enumerate(specials):  # special i at 13·i + 5·j, j = 0..3: once in each byte position of a 4-group
+        for j in range(4):
+            pos = (i * 13 + j * 5) % n
+            x[pos] = v
+    T, E = _t(shape), _t(shape, "f8E4M3FN")
+    prog = _mod([T], [E], f"    %0 = stablehlo.convert %arg0 : ({T}) -> {E}\n    return %0 : {E}")
+    ins = [configs.HostInput(x.reshape(shape), pjrt.BufferType.F32, shape)]
+    outs, _ = run_pjrt(gpu_client, prog, ins)
+    got = np.asarray(outs[0]).view(np.uint8).reshape(-1)
+    # the oracle's encoder on the f32 inputs (its decoded float64 values would not keep a NaN's sign)
+    ref = numerics._encode(x.astype(np.float64), "f8E4M3FN").astype(np.uint8)
+    bad = np.nonzero(got != ref)[0]
+    assert bad.size == 0, [(float(x[i]), hex(got[i]), hex(ref[i])) for i in bad[:8]]
 
 
 @pytest.mark.parametrize("shape", SHAPES + [(5, 2048)])

@@ -49,11 +49,15 @@ def test_rmsnorm(gpu_client, shape, dt):
 
 @pytest.mark.parametrize("shape,dt,quant", [((512, 4096), "bf16", "f8E4M3FN"), ((16, 4096), "f32", None),
                                             ((8, 256), "bf16", None), ((2, 3, 4096), "bf16", "f8E4M3FN"),
-                                            ((4, 8192), "f32", None), ((3, 16400), "bf16", None)])
+                                            ((4, 8192), "f32", None), ((3, 16400), "bf16", None),
+                                            ((2048, 4096), "bf16", "f8E4M3FN"), ((2048, 4096), "f32", None),
+                                            ((2048, 8192), "f32", None), ((2049, 1016), "f32", None)])
 def test_rmsnorm_fast_path_matches_interpreter(gpu_client, interp_client, shape, dt, quant):
-    # the row-norm kernel and the interpreted row kernel fold in the same order: identical bits, and both match the
-    # oracle (C5's normalise-and-quantise step at its full size is the first case; rows of ≤ 2048, ≤ 4096, ≤ 8192
-    # and longer elements cover the one-, two-, four-chunk register-resident and the re-reading variants)
+    # the row-norm kernels and the interpreted row kernel fold in the same order: identical bits, and both match the
+    # oracle. C5's normalise-and-quantise step at its full size is the first case. With few rows a workgroup takes a
+    # row: rows of ≤ 2048, ≤ 4096, ≤ 8192 and longer elements cover the one-, two-, four-chunk register-resident and
+    # the re-reading variants. Short rows, and rows of ≤ 8192 elements when there are ≥ 2048 of them, take a
+    # wavefront each (8 and 16 chunks per lane, 16- and 32-bit inputs, a ragged last chunk column).
     d = shape[-1]
     mk = _f32 if dt == "f32" else _bf16
     ins = [mk(51, shape), mk(52, (d,), 1.0, 0.02)]
