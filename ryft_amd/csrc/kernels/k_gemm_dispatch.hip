@@ -260,9 +260,10 @@ void launch_gemm(const GemmArgs& g, hipStream_t stream, hipEvent_t done) {
     if (blocks > INT32_MAX) fail(PJRT_Error_Code_UNIMPLEMENTED, "too many GEMM tiles");
     void* args[] = {(void*)&g};
     hipEvent_t main_done = splits > 1 ? nullptr : done;  // split-K: the reduction launch carries it
-    e = main_done ? hipExtLaunchKernel(c.fn, dim3((unsigned)blocks), dim3(c.threads), args, (size_t)c.lds, stream,
-                                       nullptr, main_done, 0)
-                  : hipLaunchKernel(c.fn, dim3((unsigned)blocks), dim3(c.threads), args, (size_t)c.lds, stream);
+    hipEvent_t start = take_start();
+    e = main_done || start ? hipExtLaunchKernel(c.fn, dim3((unsigned)blocks), dim3(c.threads), args, (size_t)c.lds,
+                                                stream, start, main_done, 0)
+                           : hipLaunchKernel(c.fn, dim3((unsigned)blocks), dim3(c.threads), args, (size_t)c.lds, stream);
     if (e == hipSuccess && splits > 1) {
       const int64_t quads = (int64_t)g.batch * g.M * g.N / 4;
       const unsigned rb = (unsigned)std::min<int64_t>((quads + 255) / 256, 256 * 16);

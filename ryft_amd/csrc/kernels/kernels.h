@@ -8,6 +8,10 @@
 
 namespace ryft {
 
+// Start event for the calling thread's next kernel launch (null: none); see launch.h.
+hipEvent_t& pending_start();
+
+
 // `done` (optional): an event the launcher records on `stream` after its last kernel, as part of that launch.
 void launch_elementwise(const EwProgram& p, hipStream_t stream, hipEvent_t done = nullptr);
 void launch_reduce(const ReduceArgs& a, hipStream_t stream, hipEvent_t done = nullptr);

@@ -15,6 +15,12 @@
 
 namespace ryft {
 
+hipEvent_t& pending_start() {
+  static thread_local hipEvent_t e = nullptr;
+  return e;
+}
+
+
 PJRT_Error* make_pjrt_error(PJRT_Error_Code code, const std::string& msg);  // pjrt_api.cc
 
 // ------------------------------------------------------------------------------------------------ events
@@ -536,7 +542,9 @@ EventPtr execute(LoadedExecutable* le, Device* d, Buffer* const* args, size_t nu
         tm.bytes = step.bytes;
         HIP_CHECK(hipEventCreate(&tm.start));
         HIP_CHECK(hipEventCreate(&tm.stop));
-        HIP_CHECK(hipEventRecord(tm.start, st));
+        // kernel steps: the first launch records the start, the last the stop (the kernels' own duration)
+        if (step.kind == Step::COPY) HIP_CHECK(hipEventRecord(tm.start, st));
+        else pending_start() = tm.start;
       }
       if (step.kind == Step::COPY) {
         void* src = ptr[step.patches[0].second];
@@ -553,17 +561,22 @@ EventPtr execute(LoadedExecutable* le, Device* d, Buffer* const* args, size_t nu
           void** f = (void**)(block + p.first);
           *f = (char*)ptr[p.second] + (uintptr_t)(*f);
         }
+        hipEvent_t last = prof ? tm.stop : carry;
         switch (step.kind) {
-          case Step::ELEMENTWISE: launch_elementwise(*(EwProgram*)block, st, carry); break;
-          case Step::REDUCE: launch_reduce(*(ReduceArgs*)block, st, carry); break;
-          case Step::ROW: launch_row(*(RowArgs*)block, st, carry); break;
-          case Step::GEMM: launch_gemm(*(GemmArgs*)block, st, carry); break;
-          case Step::ATTENTION: launch_attention(*(AttnArgs*)block, st, carry); break;
+          case Step::ELEMENTWISE: launch_elementwise(*(EwProgram*)block, st, last); break;
+          case Step::REDUCE: launch_reduce(*(ReduceArgs*)block, st, last); break;
+          case Step::ROW: launch_row(*(RowArgs*)block, st, last); break;
+          case Step::GEMM: launch_gemm(*(GemmArgs*)block, st, last); break;
+          case Step::ATTENTION: launch_attention(*(AttnArgs*)block, st, last); break;
           default: recorded = false; break;
+        }
+        if (hipEvent_t unused = pending_start()) {  // no launch took it
+          pending_start() = nullptr;
+          HIP_CHECK(hipEventRecord(unused, st));
         }
       }
       if (prof) {
-        HIP_CHECK(hipEventRecord(tm.stop, st));
+        if (step.kind == Step::COPY) HIP_CHECK(hipEventRecord(tm.stop, st));
         std::lock_guard<std::mutex> pl(c->prof_mu);
         c->timings.push_back(tm);
       }
