@@ -576,6 +576,18 @@ typedef struct PJRT_Buffer_ToHostBuffer_Args {
 } PJRT_Buffer_ToHostBuffer_Args;
 typedef PJRT_Error* PJRT_Buffer_ToHostBuffer(PJRT_Buffer_ToHostBuffer_Args* args);
 
+/* Buffer_CopyRawToHost: buffers.rs:2931-2958 (caller: Buffer::copy_raw_to_host_buffer, buffers.rs:1318-1340). Copies
+ * transfer_size bytes starting at byte `offset` of the buffer's on-device bytes; the event completes when dst holds them. */
+typedef struct PJRT_Buffer_CopyRawToHost_Args {
+  PJRT_ARGS_HEAD;
+  PJRT_Buffer* buffer;
+  void* dst;
+  int64_t offset;
+  int64_t transfer_size;
+  PJRT_Event* event; /* out */
+} PJRT_Buffer_CopyRawToHost_Args;
+typedef PJRT_Error* PJRT_Buffer_CopyRawToHost(PJRT_Buffer_CopyRawToHost_Args* args);
+
 typedef struct PJRT_Buffer_IsOnCpu_Args {
   PJRT_ARGS_HEAD;
   PJRT_Buffer* buffer;
@@ -931,6 +943,88 @@ typedef struct PJRT_LoadedExecutable_AddressableDeviceLogicalIds_Args {
 typedef PJRT_Error* PJRT_LoadedExecutable_AddressableDeviceLogicalIds(
     PJRT_LoadedExecutable_AddressableDeviceLogicalIds_Args* args);
 
+/* Executable_Serialize: programs.rs:1916-1943 (caller: Executable::serialize, programs.rs:404-423). The bytes stay
+ * valid until the deleter is called on serialized_executable. */
+typedef struct PJRT_Executable_Serialize_Args {
+  PJRT_ARGS_HEAD;
+  const PJRT_Executable* executable;
+  const char* serialized_bytes;                    /* out */
+  size_t serialized_bytes_size;                    /* out */
+  PJRT_SerializedExecutable* serialized_executable; /* out */
+  void (*serialized_executable_deleter)(PJRT_SerializedExecutable* exec); /* out */
+} PJRT_Executable_Serialize_Args;
+typedef PJRT_Error* PJRT_Executable_Serialize(PJRT_Executable_Serialize_Args* args);
+
+/* Executable_DeserializeAndLoad: programs.rs:2234-2269 (caller: Client::deserialize_and_load_executable,
+ * programs.rs:1303-1330). */
+typedef struct PJRT_Executable_DeserializeAndLoad_Args {
+  PJRT_ARGS_HEAD;
+  PJRT_Client* client;
+  const char* serialized_executable;
+  size_t serialized_executable_size;
+  PJRT_LoadedExecutable* loaded_executable; /* out */
+  const char* overridden_serialized_compile_options;
+  size_t overridden_serialized_compile_options_size;
+} PJRT_Executable_DeserializeAndLoad_Args;
+typedef PJRT_Error* PJRT_Executable_DeserializeAndLoad(PJRT_Executable_DeserializeAndLoad_Args* args);
+
+/* LoadedExecutable_GetDeviceAssignment: programs.rs:2052-2080 (caller: LoadedExecutable::device_assignment,
+ * programs.rs:704-736). The bytes are a serialized xla.DeviceAssignmentProto (ryft-xla-sys/src/protos.rs:2318-2352). */
+typedef struct PJRT_LoadedExecutable_GetDeviceAssignment_Args {
+  PJRT_ARGS_HEAD;
+  PJRT_LoadedExecutable* executable;
+  const char* serialized_bytes;                                /* out */
+  size_t serialized_bytes_size;                                /* out */
+  PJRT_DeviceAssignmentSerialized* serialized_device_assignment; /* out */
+  void (*serialized_device_assignment_deleter)(PJRT_DeviceAssignmentSerialized* da); /* out */
+} PJRT_LoadedExecutable_GetDeviceAssignment_Args;
+typedef PJRT_Error* PJRT_LoadedExecutable_GetDeviceAssignment(PJRT_LoadedExecutable_GetDeviceAssignment_Args* args);
+
+/* Executable_GetCompiledMemoryStats: programs.rs (struct PJRT_Executable_GetCompiledMemoryStats_Args; caller
+ * Executable::memory_statistics, programs.rs:318-360). */
+typedef struct PJRT_Executable_GetCompiledMemoryStats_Args {
+  PJRT_ARGS_HEAD;
+  PJRT_Executable* executable;
+  int64_t generated_code_size_in_bytes;      /* out */
+  int64_t argument_size_in_bytes;            /* out */
+  int64_t output_size_in_bytes;              /* out */
+  int64_t alias_size_in_bytes;               /* out */
+  int64_t temp_size_in_bytes;                /* out */
+  int64_t host_generated_code_size_in_bytes; /* out */
+  int64_t host_argument_size_in_bytes;       /* out */
+  int64_t host_output_size_in_bytes;         /* out */
+  int64_t host_alias_size_in_bytes;          /* out */
+  int64_t host_temp_size_in_bytes;           /* out */
+  int64_t peak_memory_in_bytes;              /* out */
+  int64_t total_size_in_bytes;               /* out */
+  int64_t total_allocation_bytes;            /* out */
+  int64_t indefinite_allocations;            /* out */
+  int64_t peak_unpadded_heap_bytes;          /* out */
+} PJRT_Executable_GetCompiledMemoryStats_Args;
+typedef PJRT_Error* PJRT_Executable_GetCompiledMemoryStats(PJRT_Executable_GetCompiledMemoryStats_Args* args);
+
+/* Executable_ParameterMemoryKinds: programs.rs:1606-1630 (caller: Executable::input_memory_kinds, programs.rs:127-145). */
+typedef struct PJRT_Executable_ParameterMemoryKinds_Args {
+  PJRT_ARGS_HEAD;
+  PJRT_Executable* executable;
+  size_t num_parameters;             /* out */
+  const char* const* memory_kinds;   /* out */
+  const size_t* memory_kind_sizes;   /* out */
+} PJRT_Executable_ParameterMemoryKinds_Args;
+typedef PJRT_Error* PJRT_Executable_ParameterMemoryKinds(PJRT_Executable_ParameterMemoryKinds_Args* args);
+
+/* ExecuteContext_Create / _Destroy: programs.rs:2311-2345 (caller: Api::execution_context, programs.rs:1476-1481). */
+typedef struct PJRT_ExecuteContext_Create_Args {
+  PJRT_ARGS_HEAD;
+  PJRT_ExecuteContext* context; /* out */
+} PJRT_ExecuteContext_Create_Args;
+typedef PJRT_Error* PJRT_ExecuteContext_Create(PJRT_ExecuteContext_Create_Args* args);
+typedef struct PJRT_ExecuteContext_Destroy_Args {
+  PJRT_ARGS_HEAD;
+  PJRT_ExecuteContext* context;
+} PJRT_ExecuteContext_Destroy_Args;
+typedef PJRT_Error* PJRT_ExecuteContext_Destroy(PJRT_ExecuteContext_Destroy_Args* args);
+
 typedef struct PJRT_SendCallbackInfo PJRT_SendCallbackInfo;
 typedef struct PJRT_RecvCallbackInfo PJRT_RecvCallbackInfo;
 
@@ -1022,14 +1116,14 @@ typedef struct PJRT_Api {
   PJRT_SLOT(PJRT_Executable_GetCostAnalysis);
   PJRT_SLOT(PJRT_Executable_OutputMemoryKinds);
   PJRT_SLOT(PJRT_Executable_OptimizedProgram);
-  PJRT_NOSLOT(PJRT_Executable_Serialize);
+  PJRT_SLOT(PJRT_Executable_Serialize);
   PJRT_SLOT(PJRT_LoadedExecutable_Destroy);
   PJRT_SLOT(PJRT_LoadedExecutable_GetExecutable);
   PJRT_SLOT(PJRT_LoadedExecutable_AddressableDevices);
   PJRT_SLOT(PJRT_LoadedExecutable_Delete);
   PJRT_SLOT(PJRT_LoadedExecutable_IsDeleted);
   PJRT_SLOT(PJRT_LoadedExecutable_Execute);
-  PJRT_NOSLOT(PJRT_Executable_DeserializeAndLoad);
+  PJRT_SLOT(PJRT_Executable_DeserializeAndLoad);
   PJRT_SLOT(PJRT_LoadedExecutable_Fingerprint);
   PJRT_SLOT(PJRT_Buffer_Destroy);
   PJRT_SLOT(PJRT_Buffer_ElementType);
@@ -1069,11 +1163,11 @@ typedef struct PJRT_Api {
   PJRT_NOSLOT(PJRT_Client_CreateViewOfDeviceBuffer);
   PJRT_SLOT(PJRT_Executable_Fingerprint);
   PJRT_NOSLOT(PJRT_Client_TopologyDescription);
-  PJRT_NOSLOT(PJRT_Executable_GetCompiledMemoryStats);
+  PJRT_SLOT(PJRT_Executable_GetCompiledMemoryStats);
   PJRT_SLOT(PJRT_Memory_Kind_Id);
-  PJRT_NOSLOT(PJRT_ExecuteContext_Create);
-  PJRT_NOSLOT(PJRT_ExecuteContext_Destroy);
-  PJRT_NOSLOT(PJRT_Buffer_CopyRawToHost);
+  PJRT_SLOT(PJRT_ExecuteContext_Create);
+  PJRT_SLOT(PJRT_ExecuteContext_Destroy);
+  PJRT_SLOT(PJRT_Buffer_CopyRawToHost);
   PJRT_NOSLOT(PJRT_AsyncHostToDeviceTransferManager_Destroy);
   PJRT_NOSLOT(PJRT_AsyncHostToDeviceTransferManager_TransferData);
   PJRT_NOSLOT(PJRT_Client_CreateBuffersForAsyncHostToDevice);
@@ -1090,7 +1184,7 @@ typedef struct PJRT_Api {
   PJRT_NOSLOT(PJRT_TopologyDescription_Deserialize);
   PJRT_NOSLOT(PJRT_Client_CreateAliasBuffer);
   PJRT_NOSLOT(PJRT_Client_FulfillAliasBuffer);
-  PJRT_NOSLOT(PJRT_LoadedExecutable_GetDeviceAssignment);
+  PJRT_SLOT(PJRT_LoadedExecutable_GetDeviceAssignment);
   PJRT_NOSLOT(PJRT_Client_CreateErrorBuffer);
   PJRT_NOSLOT(PJRT_AsyncHostToDeviceTransferManager_TransferLiteral);
   PJRT_NOSLOT(PJRT_Buffer_CopyRawToHostFuture);
@@ -1107,7 +1201,7 @@ typedef struct PJRT_Api {
   PJRT_NOSLOT(PJRT_Buffer_Bitcast);
   PJRT_SLOT(PJRT_Error_ForEachPayload);
   PJRT_NOSLOT(PJRT_TopologyDescription_Fingerprint);
-  PJRT_NOSLOT(PJRT_Executable_ParameterMemoryKinds);
+  PJRT_SLOT(PJRT_Executable_ParameterMemoryKinds);
 } PJRT_Api;
 
 #undef PJRT_SLOT
@@ -1148,6 +1242,17 @@ PJRT_ASSERT(sizeof(PJRT_Event_Set_Args) == 48, "PJRT_Event_Set_Args");
 PJRT_ASSERT(sizeof(PJRT_Device_MemoryStats_Args) == 192, "PJRT_Device_MemoryStats_Args");
 PJRT_ASSERT(sizeof(PJRT_Executable_OutputDimensions_Args) == 48, "PJRT_Executable_OutputDimensions_Args");
 PJRT_ASSERT(sizeof(PJRT_Executable_GetCompileOptions_Args) == 56, "PJRT_Executable_GetCompileOptions_Args");
+PJRT_ASSERT(sizeof(PJRT_Executable_Serialize_Args) == 56, "PJRT_Executable_Serialize_Args");
+PJRT_ASSERT(sizeof(PJRT_Executable_DeserializeAndLoad_Args) == 64, "PJRT_Executable_DeserializeAndLoad_Args");
+PJRT_ASSERT(offsetof(PJRT_Executable_DeserializeAndLoad_Args, loaded_executable) == 40,
+            "PJRT_Executable_DeserializeAndLoad_Args.loaded_executable");
+PJRT_ASSERT(sizeof(PJRT_LoadedExecutable_GetDeviceAssignment_Args) == 56, "PJRT_LoadedExecutable_GetDeviceAssignment_Args");
+PJRT_ASSERT(sizeof(PJRT_Executable_GetCompiledMemoryStats_Args) == 144, "PJRT_Executable_GetCompiledMemoryStats_Args");
+PJRT_ASSERT(offsetof(PJRT_Executable_GetCompiledMemoryStats_Args, peak_memory_in_bytes) == 104,
+            "PJRT_Executable_GetCompiledMemoryStats_Args.peak_memory_in_bytes");
+PJRT_ASSERT(sizeof(PJRT_Executable_ParameterMemoryKinds_Args) == 48, "PJRT_Executable_ParameterMemoryKinds_Args");
+PJRT_ASSERT(sizeof(PJRT_ExecuteContext_Create_Args) == 24, "PJRT_ExecuteContext_Create_Args");
+PJRT_ASSERT(sizeof(PJRT_Buffer_CopyRawToHost_Args) == 56, "PJRT_Buffer_CopyRawToHost_Args");
 #undef PJRT_ASSERT
 
 #ifdef __cplusplus

@@ -297,6 +297,18 @@ PJRT_Error* Client_AddressableMemories(PJRT_Client_AddressableMemories_Args* arg
   args->num_addressable_memories = c->memory_ptrs.size();
   return nullptr;
 }
+// One replica, one partition, on the client's first device (none on a compile-only client).
+LoadedExecutable* load_executable(Client* c, std::shared_ptr<Executable> exe) {
+  auto le = new LoadedExecutable();
+  le->client = c;
+  le->exe = std::move(exe);
+  if (!c->device_ptrs.empty()) {
+    le->devices = {c->device_ptrs.at(0)};
+    le->logical_ids = {PJRT_LogicalDeviceIds{0, 0}};
+  }
+  return le;
+}
+
 PJRT_Error* Client_Compile(PJRT_Client_Compile_Args* args) {
   NEED_ARGS(PJRT_Client_Compile_Args, executable);
   NEED(args->client, "client");
@@ -307,19 +319,7 @@ PJRT_Error* Client_Compile(PJRT_Client_Compile_Args* args) {
   std::string format = p->format ? std::string(p->format, p->format_size) : std::string("mlir");
   std::string code(p->code ? p->code : "", p->code ? p->code_size : 0);
   std::string opts(args->compile_options ? args->compile_options : "", args->compile_options ? args->compile_options_size : 0);
-  auto le = new LoadedExecutable();
-  le->client = c;
-  try {
-    le->exe = compile_program(c, code, format, opts);
-  } catch (...) {
-    delete le;
-    throw;
-  }
-  if (!c->device_ptrs.empty()) {
-    le->devices = {c->device_ptrs.at(0)};
-    le->logical_ids = {PJRT_LogicalDeviceIds{0, 0}};
-  }
-  args->executable = to<PJRT_LoadedExecutable>(le);
+  args->executable = to<PJRT_LoadedExecutable>(load_executable(c, compile_program(c, code, format, opts)));
   API_CATCH
 }
 PJRT_Error* Client_DefaultDeviceAssignment(PJRT_Client_DefaultDeviceAssignment_Args* args) {
@@ -636,6 +636,93 @@ PJRT_Error* Executable_GetCompileOptions(PJRT_Executable_GetCompileOptions_Args*
   return nullptr;
 }
 
+PJRT_Error* Executable_Serialize(PJRT_Executable_Serialize_Args* args) {
+  NEED_ARGS(PJRT_Executable_Serialize_Args, serialized_executable_deleter);
+  NEED(args->executable, "executable");
+  API_TRY
+  auto& e = exe_of(const_cast<PJRT_Executable*>(args->executable));
+  auto* blob = new std::string(serialize_executable(e));
+  args->serialized_bytes = blob->data();
+  args->serialized_bytes_size = blob->size();
+  args->serialized_executable = reinterpret_cast<PJRT_SerializedExecutable*>(blob);
+  args->serialized_executable_deleter = [](PJRT_SerializedExecutable* p) { delete reinterpret_cast<std::string*>(p); };
+  API_CATCH
+}
+PJRT_Error* Executable_DeserializeAndLoad(PJRT_Executable_DeserializeAndLoad_Args* args) {
+  NEED_ARGS(PJRT_Executable_DeserializeAndLoad_Args, loaded_executable);
+  NEED(args->client, "client");
+  API_TRY
+  Client* c = from<Client>(args->client);
+  std::string override_opts;
+  const std::string* opts = nullptr;
+  const bool has_override =
+      args->struct_size >= offsetof(PJRT_Executable_DeserializeAndLoad_Args, overridden_serialized_compile_options_size) +
+                               sizeof(size_t) &&
+      args->overridden_serialized_compile_options && args->overridden_serialized_compile_options_size > 0;
+  if (has_override) {
+    override_opts.assign(args->overridden_serialized_compile_options, args->overridden_serialized_compile_options_size);
+    opts = &override_opts;
+  }
+  auto exe = deserialize_executable(c, args->serialized_executable, args->serialized_executable_size, opts);
+  args->loaded_executable = to<PJRT_LoadedExecutable>(load_executable(c, std::move(exe)));
+  API_CATCH
+}
+PJRT_Error* Executable_GetCompiledMemoryStats(PJRT_Executable_GetCompiledMemoryStats_Args* args) {
+  NEED_ARGS(PJRT_Executable_GetCompiledMemoryStats_Args, peak_memory_in_bytes);
+  NEED(args->executable, "executable");
+  auto& e = exe_of(args->executable);
+  int64_t arg = 0, out = 0, temp = 0, cst = 0;
+  for (const Slot& sl : e.plan.slots) {
+    const int64_t n = (int64_t)sl.type.bytes();
+    if (sl.kind == Slot::PARAM) arg += n;
+    else if (sl.kind == Slot::OUTPUT) out += n;
+    else if (sl.kind == Slot::TEMP) temp += n;
+    else cst += n;
+  }
+  // kernels are compiled into the plugin; the executable's device memory is its arguments, outputs, planned
+  // temporaries and uploaded constants
+  args->generated_code_size_in_bytes = 0;
+  args->argument_size_in_bytes = arg;
+  args->output_size_in_bytes = out;
+  args->alias_size_in_bytes = 0;
+  args->temp_size_in_bytes = temp;
+  args->host_generated_code_size_in_bytes = 0;
+  args->host_argument_size_in_bytes = 0;
+  args->host_output_size_in_bytes = 0;
+  args->host_alias_size_in_bytes = 0;
+  args->host_temp_size_in_bytes = 0;
+  args->peak_memory_in_bytes = arg + out + temp + cst;
+  auto fits = [&](size_t off) { return args->struct_size >= off + sizeof(int64_t); };
+  if (fits(offsetof(PJRT_Executable_GetCompiledMemoryStats_Args, total_size_in_bytes)))
+    args->total_size_in_bytes = arg + out + temp + cst;
+  if (fits(offsetof(PJRT_Executable_GetCompiledMemoryStats_Args, total_allocation_bytes)))
+    args->total_allocation_bytes = out + temp + cst;
+  if (fits(offsetof(PJRT_Executable_GetCompiledMemoryStats_Args, indefinite_allocations)))
+    args->indefinite_allocations = 0;
+  if (fits(offsetof(PJRT_Executable_GetCompiledMemoryStats_Args, peak_unpadded_heap_bytes)))
+    args->peak_unpadded_heap_bytes = arg + out + temp + cst;
+  return nullptr;
+}
+PJRT_Error* Executable_ParameterMemoryKinds(PJRT_Executable_ParameterMemoryKinds_Args* args) {
+  NEED_ARGS(PJRT_Executable_ParameterMemoryKinds_Args, memory_kind_sizes);
+  NEED(args->executable, "executable");
+  auto& e = exe_of(args->executable);
+  args->num_parameters = e.param_memory_kinds.size();
+  args->memory_kinds = e.param_memory_kinds.data();
+  args->memory_kind_sizes = e.param_memory_kind_sizes.data();
+  return nullptr;
+}
+PJRT_Error* ExecuteContext_Create(PJRT_ExecuteContext_Create_Args* args) {
+  NEED_ARGS(PJRT_ExecuteContext_Create_Args, context);
+  args->context = to<PJRT_ExecuteContext>(new ExecuteContext());
+  return nullptr;
+}
+PJRT_Error* ExecuteContext_Destroy(PJRT_ExecuteContext_Destroy_Args* args) {
+  NEED_ARGS(PJRT_ExecuteContext_Destroy_Args, context);
+  delete from<ExecuteContext>(args->context);
+  return nullptr;
+}
+
 PJRT_Error* LoadedExecutable_Destroy(PJRT_LoadedExecutable_Destroy_Args* args) {
   NEED_ARGS(PJRT_LoadedExecutable_Destroy_Args, executable);
   delete from<LoadedExecutable>(args->executable);
@@ -661,6 +748,43 @@ PJRT_Error* LoadedExecutable_AddressableDeviceLogicalIds(PJRT_LoadedExecutable_A
   auto* le = from<LoadedExecutable>(args->executable);
   args->addressable_device_logical_ids = le->logical_ids.data();
   args->num_addressable_device_logical_ids = le->logical_ids.size();
+  return nullptr;
+}
+// A serialized xla.DeviceAssignmentProto: replica_count = 1 (field 1), computation_count = 1 (field 2), one
+// computation_devices entry (field 3) whose packed replica_device_ids (field 1) hold the executable's device id.
+PJRT_Error* LoadedExecutable_GetDeviceAssignment(PJRT_LoadedExecutable_GetDeviceAssignment_Args* args) {
+  NEED_ARGS(PJRT_LoadedExecutable_GetDeviceAssignment_Args, serialized_device_assignment_deleter);
+  NEED(args->executable, "executable");
+  auto* le = from<LoadedExecutable>(args->executable);
+  if (le->devices.empty())
+    return make_pjrt_error(PJRT_Error_Code_FAILED_PRECONDITION, "a compile-only client has no device assignment");
+  auto varint = [](std::string& o, uint64_t v) {
+    do {
+      uint8_t byte = v & 0x7f;
+      v >>= 7;
+      o.push_back((char)(byte | (v ? 0x80 : 0)));
+    } while (v);
+  };
+  std::string ids;
+  varint(ids, (uint64_t)(int64_t)le->devices[0]->id);
+  std::string comp;
+  comp.push_back(0x0a);  // replica_device_ids, packed
+  varint(comp, ids.size());
+  comp += ids;
+  auto* blob = new std::string();
+  blob->push_back(0x08);  // replica_count
+  varint(*blob, 1);
+  blob->push_back(0x10);  // computation_count
+  varint(*blob, 1);
+  blob->push_back(0x1a);  // computation_devices
+  varint(*blob, comp.size());
+  *blob += comp;
+  args->serialized_bytes = blob->data();
+  args->serialized_bytes_size = blob->size();
+  args->serialized_device_assignment = reinterpret_cast<PJRT_DeviceAssignmentSerialized*>(blob);
+  args->serialized_device_assignment_deleter = [](PJRT_DeviceAssignmentSerialized* p) {
+    delete reinterpret_cast<std::string*>(p);
+  };
   return nullptr;
 }
 PJRT_Error* LoadedExecutable_Delete(PJRT_LoadedExecutable_Delete_Args* args) {
@@ -830,6 +954,13 @@ PJRT_Error* Buffer_ToHostBuffer(PJRT_Buffer_ToHostBuffer_Args* args) {
   args->event = wrap_event(buffer_to_host(b, args->dst, args->dst_size));
   API_CATCH
 }
+PJRT_Error* Buffer_CopyRawToHost(PJRT_Buffer_CopyRawToHost_Args* args) {
+  NEED_ARGS(PJRT_Buffer_CopyRawToHost_Args, event);
+  NEED(args->buffer, "buffer");
+  API_TRY
+  args->event = wrap_event(buffer_raw_to_host(buf(args->buffer), args->dst, args->offset, args->transfer_size));
+  API_CATCH
+}
 PJRT_Error* Buffer_IsOnCpu(PJRT_Buffer_IsOnCpu_Args* args) {
   NEED_ARGS(PJRT_Buffer_IsOnCpu_Args, is_on_cpu);
   args->is_on_cpu = false;
@@ -973,6 +1104,14 @@ PJRT_Api make_api() {
   SET(Executable_OutputElementTypes);
   SET(Executable_OutputDimensions);
   SET(Executable_GetCompileOptions);
+  SET(Executable_Serialize);
+  SET(Executable_DeserializeAndLoad);
+  SET(Executable_GetCompiledMemoryStats);
+  SET(Executable_ParameterMemoryKinds);
+  SET(ExecuteContext_Create);
+  SET(ExecuteContext_Destroy);
+  SET(LoadedExecutable_GetDeviceAssignment);
+  SET(Buffer_CopyRawToHost);
   SET(LoadedExecutable_Destroy);
   SET(LoadedExecutable_GetExecutable);
   SET(LoadedExecutable_AddressableDevices);

@@ -402,6 +402,33 @@ EventPtr buffer_to_host(Buffer* b, void* dst, size_t dst_size) {
   });
 }
 
+EventPtr buffer_raw_to_host(Buffer* b, void* dst, int64_t offset, int64_t size) {
+  if (b->deleted) fail(PJRT_Error_Code_FAILED_PRECONDITION, "CopyRawToHost on a deleted buffer");
+  const int64_t bytes = (int64_t)b->bytes();
+  if (offset < 0 || size < 0 || offset > bytes || size > bytes - offset)
+    invalid("CopyRawToHost: bytes [" + std::to_string(offset) + ", " + std::to_string(offset) + " + " +
+            std::to_string(size) + ") are outside the buffer's " + std::to_string(bytes) + " bytes");
+  if (size > 0 && !dst) invalid("CopyRawToHost: dst is null");
+  Client* c = b->client;
+  Device* d = b->device;
+  if (size == 0) return ready_event();
+  std::lock_guard<std::recursive_mutex> lk(d->launch_mu);
+  HIP_CHECK(hipSetDevice(d->hip_ordinal));
+  auto* chunk = c->pinned.acquire((size_t)size);
+  hipError_t e = hipMemcpyAsync(chunk->ptr, (const char*)b->mem->ptr + offset, (size_t)size, hipMemcpyDeviceToHost,
+                                d->stream);
+  if (e != hipSuccess) {
+    c->pinned.release_now(chunk);
+    fail(PJRT_Error_Code_INTERNAL, std::string("device-to-host copy failed: ") + hipGetErrorString(e));
+  }
+  auto mem = b->mem;  // keep the source alive until the copy completes
+  PinnedPool* pool = &c->pinned;
+  return c->record_event(d, [chunk, dst, size, mem, pool] {
+    memcpy(dst, chunk->ptr, (size_t)size);
+    pool->release_now(chunk);
+  });
+}
+
 Buffer* copy_buffer(Buffer* src, Device* d) {
   if (src->deleted) fail(PJRT_Error_Code_FAILED_PRECONDITION, "copy of a deleted buffer");
   if (d != src->device) unimplemented("copies between devices are not supported");
@@ -450,6 +477,11 @@ std::shared_ptr<Executable> compile_program(Client* c, const std::string& code, 
     exe->output_memory_kinds.push_back(kDevice);
     exe->output_memory_kind_sizes.push_back(6);
   }
+  for (size_t i = 0; i < exe->plan.param_types.size(); ++i) {
+    static const char* kDevice = "device";
+    exe->param_memory_kinds.push_back(kDevice);
+    exe->param_memory_kind_sizes.push_back(6);
+  }
   static const char* kFlops = "flops";
   static const char* kBytes = "bytes accessed";
   PJRT_NamedValue f{};
@@ -481,6 +513,42 @@ std::shared_ptr<Executable> compile_program(Client* c, const std::string& code, 
     exe->constants[s] = m;
   }
   return exe;
+}
+
+// Serialized executable: "RYFTEXE1", then the program bytes and the compile-options bytes, each after its u64
+// length. Deserialisation compiles the program again (plans are cheap to rebuild; the kernels live in the plugin).
+static const char kExeMagic[8] = {'R', 'Y', 'F', 'T', 'E', 'X', 'E', '1'};
+
+std::string serialize_executable(const Executable& e) {
+  std::string out(kExeMagic, sizeof(kExeMagic));
+  auto put = [&](const std::string& v) {
+    uint64_t n = v.size();
+    out.append((const char*)&n, sizeof(n));
+    out.append(v);
+  };
+  put(e.program_text);
+  put(e.compile_options);
+  return out;
+}
+
+std::shared_ptr<Executable> deserialize_executable(Client* c, const char* data, size_t size, const std::string* options) {
+  if (!data || size < sizeof(kExeMagic) || memcmp(data, kExeMagic, sizeof(kExeMagic)) != 0)
+    invalid("not a serialized executable of this plugin (bad header)");
+  size_t pos = sizeof(kExeMagic);
+  auto get = [&](const char* what) {
+    uint64_t n = 0;
+    if (size - pos < sizeof(n)) invalid(std::string("serialized executable is truncated (") + what + " length)");
+    memcpy(&n, data + pos, sizeof(n));
+    pos += sizeof(n);
+    if (n > size - pos) invalid(std::string("serialized executable is truncated (") + what + ")");
+    std::string v(data + pos, (size_t)n);
+    pos += (size_t)n;
+    return v;
+  };
+  std::string code = get("program");
+  std::string opts = get("compile options");
+  if (pos != size) invalid("serialized executable has trailing bytes");
+  return compile_program(c, code, "mlir", options ? *options : opts);
 }
 
 // ------------------------------------------------------------------------------------------------ execute

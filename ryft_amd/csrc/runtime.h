@@ -151,9 +151,13 @@ struct Executable {  // PJRT_Executable (shared by the loaded executable and eve
   std::vector<size_t> output_ranks;
   std::vector<const char*> output_memory_kinds;
   std::vector<size_t> output_memory_kind_sizes;
+  std::vector<const char*> param_memory_kinds;
+  std::vector<size_t> param_memory_kind_sizes;
   std::vector<PJRT_NamedValue> cost_properties;
   std::vector<std::shared_ptr<DeviceMem>> constants;  // by slot (null for non-constant slots)
 };
+
+struct ExecuteContext {};  // PJRT_ExecuteContext: carries nothing the plugin reads
 
 struct ExecutableView {  // what PJRT_Executable* points to
   std::shared_ptr<Executable> exe;
@@ -209,6 +213,12 @@ Buffer* buffer_from_host(Client* c, Device* d, const void* data, DType t, const 
 // Starts a device → host copy into `dst`; returns the completion event.
 EventPtr buffer_to_host(Buffer* b, void* dst, size_t dst_size);
 // Compiles a StableHLO program.
+// Executable bytes for PJRT_Executable_Serialize, and the executable they describe (compiled again on this client;
+// `options`, when given, replaces the serialized compile options).
+std::string serialize_executable(const Executable& e);
+std::shared_ptr<Executable> deserialize_executable(Client* c, const char* data, size_t size, const std::string* options);
+// A byte range of a buffer's device bytes → host memory; the event completes when `dst` holds the bytes.
+EventPtr buffer_raw_to_host(Buffer* b, void* dst, int64_t offset, int64_t size);
 std::shared_ptr<Executable> compile_program(Client* c, const std::string& code, const std::string& format,
                                             const std::string& options);
 // Enqueues one execution; fills outputs and returns the completion event.

@@ -260,6 +260,30 @@ for _n, _f in {
     "PJRT_Buffer_IsOnCpu": [("buffer", _vp), ("is_on_cpu", C.c_bool)],
     "PJRT_Buffer_ReadyEvent": [("buffer", _vp), ("event", _vp)],
     "PJRT_Buffer_CopyToDevice": [("buffer", _vp), ("dst_device", _vp), ("dst_buffer", _vp)],
+    "PJRT_Buffer_CopyRawToHost": [("buffer", _vp), ("dst", _vp), ("offset", C.c_int64), ("transfer_size", C.c_int64),
+                                  ("event", _vp)],
+    "PJRT_Executable_Serialize": [("executable", _vp), ("serialized_bytes", _vp), ("serialized_bytes_size", _sz),
+                                  ("serialized_executable", _vp),
+                                  ("serialized_executable_deleter", C.CFUNCTYPE(None, _vp))],
+    "PJRT_Executable_DeserializeAndLoad": [("client", _vp), ("serialized_executable", _vp),
+                                           ("serialized_executable_size", _sz), ("loaded_executable", _vp),
+                                           ("overridden_serialized_compile_options", _vp),
+                                           ("overridden_serialized_compile_options_size", _sz)],
+    "PJRT_LoadedExecutable_GetDeviceAssignment": [("executable", _vp), ("serialized_bytes", _vp),
+                                                  ("serialized_bytes_size", _sz),
+                                                  ("serialized_device_assignment", _vp),
+                                                  ("serialized_device_assignment_deleter", C.CFUNCTYPE(None, _vp))],
+    "PJRT_Executable_GetCompiledMemoryStats": [("executable", _vp)] + [(f, C.c_int64) for f in (
+        "generated_code_size_in_bytes", "argument_size_in_bytes", "output_size_in_bytes", "alias_size_in_bytes",
+        "temp_size_in_bytes", "host_generated_code_size_in_bytes", "host_argument_size_in_bytes",
+        "host_output_size_in_bytes", "host_alias_size_in_bytes", "host_temp_size_in_bytes", "peak_memory_in_bytes",
+        "total_size_in_bytes", "total_allocation_bytes", "indefinite_allocations", "peak_unpadded_heap_bytes")],
+    "PJRT_Executable_ParameterMemoryKinds": [("executable", _vp), ("num_parameters", _sz),
+                                             ("memory_kinds", C.POINTER(_vp)), ("memory_kind_sizes", C.POINTER(_sz))],
+    "PJRT_Executable_OutputMemoryKinds": [("executable", _vp), ("num_outputs", _sz),
+                                          ("memory_kinds", C.POINTER(_vp)), ("memory_kind_sizes", C.POINTER(_sz))],
+    "PJRT_ExecuteContext_Create": [("context", _vp)],
+    "PJRT_ExecuteContext_Destroy": [("context", _vp)],
 }.items():
     A[_n] = _args(_n + "_Args", _f)
 
@@ -584,6 +608,14 @@ class Buffer:
         a = self.api.call("PJRT_Buffer_ToHostBuffer", src=self.handle, dst=C.cast(out, _vp), dst_size=size)
         return Event(self.api, a.event, lambda: bytes(out)[:size])
 
+    def copy_raw_to_host(self, size: int, offset: int = 0) -> Event:
+        """Buffer::copy_raw_to_host_buffer (buffers.rs:1318-1340): `size` bytes of the on-device bytes from `offset`;
+        the event's value is those bytes."""
+        out = (C.c_uint8 * max(size, 1))()
+        a = self.api.call("PJRT_Buffer_CopyRawToHost", buffer=self.handle, dst=C.cast(out, _vp), offset=offset,
+                          transfer_size=size)
+        return Event(self.api, a.event, lambda: bytes(out)[:size])
+
     def copy_to_device(self, device: Device) -> "Buffer":
         a = self.api.call("PJRT_Buffer_CopyToDevice", buffer=self.handle, dst_device=device.handle)
         return Buffer(self.client, a.dst_buffer)
@@ -653,6 +685,91 @@ class CompilationOptions:
         return out
 
 
+def _read_varint(data: bytes, pos: int):
+    n, shift = 0, 0
+    while True:
+        if pos >= len(data):
+            raise PjrtError(ErrorCode.INVALID_ARGUMENT, "truncated varint")
+        b = data[pos]
+        pos += 1
+        n |= (b & 0x7F) << shift
+        shift += 7
+        if not b & 0x80:
+            return n, pos
+
+
+def _proto_fields(data: bytes):
+    """(field number, wire type, value) of a protobuf message (varint and length-delimited fields)."""
+    pos, out = 0, []
+    while pos < len(data):
+        key, pos = _read_varint(data, pos)
+        num, wt = key >> 3, key & 7
+        if wt == 0:
+            v, pos = _read_varint(data, pos)
+        elif wt == 2:
+            n, pos = _read_varint(data, pos)
+            v, pos = data[pos:pos + n], pos + n
+        else:
+            raise PjrtError(ErrorCode.INVALID_ARGUMENT, f"unsupported protobuf wire type {wt}")
+        out.append((num, wt, v))
+    return out
+
+
+@dataclass
+class DeviceAssignment:
+    """devices.rs:517-540: `assignment[replica * computation_count + computation]` = device id."""
+
+    replica_count: int
+    computation_count: int
+    assignment: List[int]
+
+    @staticmethod
+    def decode(data: bytes) -> "DeviceAssignment":
+        """xla.DeviceAssignmentProto (ryft-xla-sys/src/protos.rs:2318-2352), read as devices.rs:674-688 does."""
+        replicas = computations = 0
+        columns: List[List[int]] = []
+        for num, wt, v in _proto_fields(data):
+            if num == 1 and wt == 0:
+                replicas = v
+            elif num == 2 and wt == 0:
+                computations = v
+            elif num == 3 and wt == 2:
+                ids: List[int] = []
+                for n2, w2, v2 in _proto_fields(v):
+                    if n2 == 1 and w2 == 2:  # packed int64
+                        pos = 0
+                        while pos < len(v2):
+                            x, pos = _read_varint(v2, pos)
+                            ids.append(x - (1 << 64) if x >> 63 else x)
+                    elif n2 == 1 and w2 == 0:
+                        ids.append(v2)
+                columns.append(ids)
+        out = []
+        for r in range(replicas):
+            for c in range(computations):
+                if c >= len(columns) or r >= len(columns[c]):
+                    raise PjrtError(ErrorCode.INVALID_ARGUMENT, "invalid device assignment")
+                out.append(columns[c][r])
+        return DeviceAssignment(replicas, computations, out)
+
+
+class ExecutionContext:
+    """PJRT_ExecuteContext (programs.rs:1190-1235)."""
+
+    def __init__(self, api: Api, handle: int):
+        if not handle:
+            raise PjrtError(ErrorCode.INVALID_ARGUMENT, "the provided PJRT execute context handle is a null pointer")
+        self.api, self.handle = api, handle
+
+    def __del__(self):
+        try:
+            if self.handle:
+                self.api.call("PJRT_ExecuteContext_Destroy", context=self.handle)
+                self.handle = None
+        except Exception:
+            pass
+
+
 class Executable:
     def __init__(self, api: Api, handle: int):
         self.api, self.handle = api, handle
@@ -697,6 +814,26 @@ class Executable:
         a.serialized_compile_options_deleter(a.serialized_compile_options)
         return data
 
+    def serialize(self) -> bytes:
+        """Executable::serialize (programs.rs:404-423): the plugin's bytes for this executable."""
+        a = self.api.call("PJRT_Executable_Serialize", executable=self.handle)
+        data = C.string_at(a.serialized_bytes, a.serialized_bytes_size)
+        a.serialized_executable_deleter(a.serialized_executable)
+        return data
+
+    def memory_statistics(self) -> Dict[str, int]:
+        """Executable::memory_statistics (programs.rs:318-360)."""
+        a = self.api.call("PJRT_Executable_GetCompiledMemoryStats", executable=self.handle)
+        return {name: int(getattr(a, name)) for name, _ in a._fields_[3:]}
+
+    def input_memory_kinds(self) -> List[str]:
+        a = self.api.call("PJRT_Executable_ParameterMemoryKinds", executable=self.handle)
+        return [_str(a.memory_kinds[i], a.memory_kind_sizes[i]) for i in range(a.num_parameters)]
+
+    def output_memory_kinds(self) -> List[str]:
+        a = self.api.call("PJRT_Executable_OutputMemoryKinds", executable=self.handle)
+        return [_str(a.memory_kinds[i], a.memory_kind_sizes[i]) for i in range(a.num_outputs)]
+
     def __del__(self):
         try:
             if self.handle:
@@ -735,6 +872,13 @@ class LoadedExecutable:
     def executable(self) -> Executable:
         a = self.api.call("PJRT_LoadedExecutable_GetExecutable", loaded_executable=self.handle)
         return Executable(self.api, a.executable)
+
+    def device_assignment(self) -> DeviceAssignment:
+        """LoadedExecutable::device_assignment (programs.rs:704-736; decoding as devices.rs:674-688)."""
+        a = self.api.call("PJRT_LoadedExecutable_GetDeviceAssignment", executable=self.handle)
+        data = C.string_at(a.serialized_bytes, a.serialized_bytes_size)
+        a.serialized_device_assignment_deleter(a.serialized_device_assignment)
+        return DeviceAssignment.decode(data)
 
     def execute(self, inputs: Sequence[Sequence], launch_id: int = 0) -> List[ExecutionDeviceOutputs]:
         """LoadedExecutable::execute (programs.rs:769-963): one input list per addressable device."""
@@ -880,6 +1024,21 @@ class Client:
         a = self.api.call("PJRT_Client_Compile", client=self.handle, program=C.pointer(p),
                           compile_options=C.cast(ob, _vp), compile_options_size=len(opts))
         return LoadedExecutable(self, a.executable)
+
+    def deserialize_and_load_executable(self, data: bytes, options: Optional[CompilationOptions] = None
+                                        ) -> LoadedExecutable:
+        """Client::deserialize_and_load_executable (programs.rs:1303-1330)."""
+        blob = C.create_string_buffer(bytes(data), len(data))
+        opts = options.encode() if options is not None else b""
+        ob = C.create_string_buffer(opts, max(len(opts), 1))
+        a = self.api.call("PJRT_Executable_DeserializeAndLoad", client=self.handle, serialized_executable=C.cast(blob, _vp),
+                          serialized_executable_size=len(data),
+                          overridden_serialized_compile_options=C.cast(ob, _vp) if opts else None,
+                          overridden_serialized_compile_options_size=len(opts))
+        return LoadedExecutable(self, a.loaded_executable)
+
+    def execution_context(self) -> "ExecutionContext":
+        return ExecutionContext(self.api, self.api.call("PJRT_ExecuteContext_Create").context)
 
     def buffer(self, data, element_type: BufferType, dims: Sequence[int], byte_strides: Optional[Sequence[int]] = None,
                device: Optional[Device] = None, memory: Optional[Memory] = None) -> Buffer:

@@ -1,0 +1,84 @@
+"""GPU checks of the executable and buffer entry points around the hot path: the sequence of ryft-pjrt's
+test_client_compile (programs.rs:2576-2623) against a device client, serialized executables that run like the
+original (test_client_deserialize_and_load_executable, programs.rs:2691-2723), and raw byte-range copies to the host
+(Buffer::copy_raw_to_host_buffer, buffers.rs:1318-1340)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from ryft_amd import configs, hostdata as hd, pjrt
+from tests.helpers import run_pjrt
+
+pytestmark = pytest.mark.gpu
+
+ADD_PROGRAM = """module {
+  func.func @main(%arg0: tensor<2x1xi32>, %arg1: tensor<2x1xi32>) -> tensor<2x1xi32> {
+    %0 = stablehlo.add %arg0, %arg1 : tensor<2x1xi32>
+    return %0 : tensor<2x1xi32>
+  }
+}
+"""
+
+
+def test_client_compile_sequence(gpu_client):
+    opts = pjrt.CompilationOptions()
+    le = gpu_client.compile(pjrt.Program.mlir(ADD_PROGRAM), opts)
+    assert le.addressable_devices() == gpu_client.addressable_devices()[:1]
+    assert le.device_assignment() == pjrt.DeviceAssignment(1, 1, [0])
+    e = le.executable()
+    assert e.name() == "main"
+    assert (e.replica_count(), e.computation_count(), e.output_count()) == (1, 1, 1)
+    assert e.output_element_types() == [pjrt.BufferType.S32]
+    assert e.output_dimensions() == [[2, 1]]
+    assert e.input_memory_kinds() == ["device", "device"]
+    assert e.output_memory_kinds() == ["device"]
+    assert e.fingerprint()
+    assert e.compile_options() == opts.encode()
+    assert e.memory_statistics()["argument_size_in_bytes"] == 16
+    assert e.serialize()
+    # the i32 add known answer (programs.rs:2823-2827)
+    ins = [configs.HostInput(np.array([[7], [-50]], np.int32), pjrt.BufferType.S32, (2, 1)),
+           configs.HostInput(np.array([[35], [8]], np.int32), pjrt.BufferType.S32, (2, 1))]
+    outs, _ = run_pjrt(gpu_client, ADD_PROGRAM, ins)
+    assert outs[0].reshape(-1).tolist() == [42, -42]
+
+
+@pytest.mark.parametrize("cfg,kw", [("c2", {"batch": 2, "m": 256, "k": 256, "n": 256}),
+                                    ("c3", {"m": 256, "k": 512, "n": 256}),
+                                    ("c4", {"b": 1, "h": 2, "s": 256})])
+def test_deserialized_executable_runs_like_the_original(gpu_client, cfg, kw):
+    w = {"c2": configs.c2_bf16_batched_dot, "c3": configs.c3_int8_gemm, "c4": configs.c4_causal_attention}[cfg](**kw)
+    le = gpu_client.compile(pjrt.Program.mlir(w.program))
+    le2 = gpu_client.deserialize_and_load_executable(le.executable().serialize())
+    assert le2.device_assignment() == le.device_assignment()
+    dev = gpu_client.addressable_devices()[0]
+    bufs = [gpu_client.buffer(x.data, x.type, x.dims, device=dev) for x in w.inputs]
+    a = le.execute([bufs])[0]
+    b = le2.execute([bufs])[0]
+    a.done.await_()
+    b.done.await_()
+    for x, y in zip(a.outputs, b.outputs):
+        assert np.array_equal(x.to_numpy(), y.to_numpy())
+
+
+def test_copy_raw_to_host_ranges(gpu_client):
+    dev = gpu_client.addressable_devices()[0]
+    x = hd.int_uniform(5, (1000,), -2 ** 31, 2 ** 31 - 1).astype(np.int32)
+    b = gpu_client.buffer(x, pjrt.BufferType.S32, (1000,), device=dev)
+    b.ready_event().await_()
+    raw = x.tobytes()
+    assert b.copy_raw_to_host(4000).await_() == raw
+    for off, size in [(0, 1), (8, 100), (3, 17), (3999, 1), (4000, 0), (0, 0)]:
+        assert b.copy_raw_to_host(size, off).await_() == raw[off:off + size], (off, size)
+    # ranges outside the buffer are rejected before anything is copied (the host array is large enough either way)
+    dst = (ctypes.c_uint8 * 8192)()
+    for off, size in [(0, 4001), (4000, 1), (-1, 4), (10, -2)]:
+        with pytest.raises(pjrt.PjrtError) as e:
+            b.api.call("PJRT_Buffer_CopyRawToHost", buffer=b.handle, dst=ctypes.cast(dst, ctypes.c_void_p), offset=off,
+                       transfer_size=size)
+        assert e.value.code == pjrt.ErrorCode.INVALID_ARGUMENT, (off, size)
+    b.delete()
+    with pytest.raises(pjrt.PjrtError) as e:
+        b.copy_raw_to_host(4)
+    assert e.value.code == pjrt.ErrorCode.FAILED_PRECONDITION

@@ -40,7 +40,13 @@ def test_api_table(plugin):
     for name in ["PJRT_Client_Create", "PJRT_Client_Compile", "PJRT_Client_BufferFromHostBuffer",
                  "PJRT_LoadedExecutable_Execute", "PJRT_LoadedExecutable_GetExecutable", "PJRT_Executable_NumOutputs",
                  "PJRT_Executable_Destroy", "PJRT_Buffer_ToHostBuffer", "PJRT_Event_Await", "PJRT_Event_OnReady",
-                 "PJRT_Device_DefaultMemory", "PJRT_Error_Destroy"]:
+                 "PJRT_Device_DefaultMemory", "PJRT_Error_Destroy",
+                 # the rest of what ryft-pjrt's test_client_compile calls (programs.rs:2576-2623), executable
+                 # serialization, raw copies and execution contexts
+                 "PJRT_LoadedExecutable_GetDeviceAssignment", "PJRT_Executable_GetCompiledMemoryStats",
+                 "PJRT_Executable_ParameterMemoryKinds", "PJRT_Executable_OutputMemoryKinds",
+                 "PJRT_Executable_Serialize", "PJRT_Executable_DeserializeAndLoad", "PJRT_Buffer_CopyRawToHost",
+                 "PJRT_ExecuteContext_Create", "PJRT_ExecuteContext_Destroy"]:
         assert api.fn(name) is not None
     with pytest.raises(pjrt.PjrtError) as e:
         api.fn("PJRT_Compile")
@@ -214,6 +220,78 @@ def test_compile_options_round_trip(compile_client):
     exe = compile_client.compile(pjrt.Program.mlir(GOLDENS["iota"]), opts)
     assert exe.executable().compile_options() == opts.encode()
     assert len(exe.executable().fingerprint()) == 16
+
+
+def test_serialize_deserialize_round_trip(compile_client):
+    # as ryft-pjrt's test_client_deserialize_and_load_executable (programs.rs:2691-2723): the deserialized executable
+    # reports the same name, counts, output types / dims / memory kinds, fingerprint and compile options
+    opts = pjrt.CompilationOptions()
+    le = compile_client.compile(pjrt.Program.mlir(configs.c3_int8_gemm(m=256, k=256, n=256).program), opts)
+    e = le.executable()
+    blob = e.serialize()
+    le2 = compile_client.deserialize_and_load_executable(blob, opts)
+    e2 = le2.executable()
+    assert e2.name() == e.name() == "main"
+    assert (e2.replica_count(), e2.computation_count()) == (e.replica_count(), e.computation_count()) == (1, 1)
+    assert e2.output_count() == e.output_count() == 2
+    assert e2.output_element_types() == e.output_element_types() == [pjrt.BufferType.S32, pjrt.BufferType.F32]
+    assert e2.output_dimensions() == e.output_dimensions() == [[256, 256], [256, 256]]
+    assert e2.output_memory_kinds() == e.output_memory_kinds() == ["device", "device"]
+    assert e2.fingerprint() == e.fingerprint()
+    assert e2.compile_options() == opts.encode()
+    assert e2.cost_analysis() == e.cost_analysis()
+    assert le2.describe_plan() == le.describe_plan()
+    # serializing the deserialized executable gives the same bytes; without override options the serialized
+    # ones are used
+    assert e2.serialize() == blob
+    assert compile_client.deserialize_and_load_executable(blob).executable().compile_options() == opts.encode()
+
+
+@pytest.mark.parametrize("mutate", ["magic", "truncate_length", "truncate_payload", "trailing"])
+def test_malformed_serialized_executable_is_invalid_argument(compile_client, mutate):
+    blob = compile_client.compile(pjrt.Program.mlir(GOLDENS["iota"])).executable().serialize()
+    bad = {"magic": b"XXXX" + blob[4:], "truncate_length": blob[:12], "truncate_payload": blob[:-3],
+           "trailing": blob + b"\0"}[mutate]
+    with pytest.raises(pjrt.PjrtError) as e:
+        compile_client.deserialize_and_load_executable(bad)
+    assert e.value.code == pjrt.ErrorCode.INVALID_ARGUMENT
+
+
+def test_memory_statistics_and_memory_kinds(compile_client):
+    # C1 plans an 8-range split-K: the f32 partial sums are the executable's only temporary (8 × 256 × 256 × 4 B)
+    e = compile_client.compile(pjrt.Program.mlir(configs.c1_f32_dot().program)).executable()
+    st = e.memory_statistics()
+    assert st["argument_size_in_bytes"] == 2 * 256 * 512 * 4
+    assert st["output_size_in_bytes"] == 256 * 256 * 4
+    assert st["temp_size_in_bytes"] == 8 * 256 * 256 * 4
+    assert st["generated_code_size_in_bytes"] == 0 and st["alias_size_in_bytes"] == 0
+    assert st["peak_memory_in_bytes"] == st["argument_size_in_bytes"] + st["output_size_in_bytes"] + st["temp_size_in_bytes"]
+    assert e.input_memory_kinds() == ["device", "device"]
+    assert e.output_memory_kinds() == ["device"]
+
+
+def test_execution_context_create_destroy(compile_client):
+    ctx = compile_client.execution_context()
+    assert ctx.handle
+    del ctx
+
+
+def test_device_assignment_needs_a_device(compile_client):
+    le = compile_client.compile(pjrt.Program.mlir(GOLDENS["iota"]))
+    with pytest.raises(pjrt.PjrtError) as e:
+        le.device_assignment()
+    assert e.value.code == pjrt.ErrorCode.FAILED_PRECONDITION
+
+
+def test_device_assignment_proto_decoding():
+    # xla.DeviceAssignmentProto{replica_count: 2, computation_count: 1, computation_devices: [{replica_device_ids:
+    # [3, 5]}]} in both the packed and the unpacked repeated encodings, read as devices.rs:674-688 does
+    packed = bytes([0x08, 2, 0x10, 1, 0x1a, 4, 0x0a, 2, 3, 5])
+    unpacked = bytes([0x08, 2, 0x10, 1, 0x1a, 4, 0x08, 3, 0x08, 5])
+    for data in (packed, unpacked):
+        assert pjrt.DeviceAssignment.decode(data) == pjrt.DeviceAssignment(2, 1, [3, 5])
+    with pytest.raises(pjrt.PjrtError):
+        pjrt.DeviceAssignment.decode(bytes([0x08, 2, 0x10, 1, 0x1a, 3, 0x0a, 1, 3]))  # one id for two replicas
 
 
 def test_attention_not_fused_when_intermediate_escapes(compile_client):
