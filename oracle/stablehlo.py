@@ -247,6 +247,40 @@ def _eval_op(op: str, rest: str, env, dot_precision: str) -> Tuple[np.ndarray, s
     if op == "reshape":
         (x, dt), = _operands(rest, 1, env)
         return np.asarray(x).reshape(out_shape), dt
+    if op == "slice":
+        # manipulation.rs:840-917: result[i] = operand[start + i·stride] for start ≤ index < limit, per dimension
+        m = re.match(r"(%[\w.$-]+)\s*\[(.*?)\]", rest)
+        x, dt = env[m.group(1)]
+        sl = []
+        for part in [p for p in m.group(2).split(",") if p.strip()]:
+            f = [int(v) for v in part.split(":")]
+            sl.append(slice(f[0], f[1], f[2] if len(f) > 2 else 1))
+        return np.asarray(x)[tuple(sl)].copy(), dt
+    if op == "concatenate":
+        # manipulation.rs:778-822: the inputs one after another along `dim`, in operand order
+        head = rest.split(":")[0]
+        d = int(re.search(r"dim\s*=\s*(\d+)", head).group(1))
+        names = re.findall(r"%[\w.$-]+", head)
+        vals = [env[x] for x in names]
+        return np.concatenate([np.asarray(v) for v, _ in vals], axis=d), vals[0][1]
+    if op == "pad":
+        # manipulation.rs:530-560: result[lo + i·(interior + 1)] = operand[i] where that index lies in the result,
+        # the padding value elsewhere (negative edge padding removes elements; interior padding comes first)
+        (x, dt), (v, _) = _operands(rest, 2, env)
+        lo = _ints(re.search(r"low\s*=\s*\[(.*?)\]", rest).group(1))
+        hi = _ints(re.search(r"high\s*=\s*\[(.*?)\]", rest).group(1))
+        it = _ints(re.search(r"interior\s*=\s*\[(.*?)\]", rest).group(1))
+        x = np.asarray(x)
+        pv = np.asarray(v).reshape(())
+        # interior padding first, then the edges: positive edges add padding, negative ones cut elements off
+        inner = np.full([k + (k - 1) * it[d] if k > 0 else 0 for d, k in enumerate(x.shape)], pv, dtype=x.dtype)
+        inner[tuple(slice(None, None, it[d] + 1) for d in range(x.ndim))] = x
+        cut = tuple(slice(max(0, -lo[d]), inner.shape[d] - max(0, -hi[d]) if inner.shape[d] - max(0, -hi[d]) > 0
+                          else 0) for d in range(x.ndim))
+        inner = inner[cut]
+        out = np.pad(inner, [(max(0, lo[d]), max(0, hi[d])) for d in range(x.ndim)], constant_values=pv)
+        assert list(out.shape) == list(out_shape), (out.shape, out_shape)
+        return out, dt
     if op == "compare":
         # comparison.rs:44-135
         m = re.match(r"(\w+)\s*,\s*(%[\w.$-]+)\s*,\s*(%[\w.$-]+)", rest)

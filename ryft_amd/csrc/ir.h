@@ -41,7 +41,7 @@ enum class Op : uint8_t {
   // elementwise, ternary
   Select, Clamp,
   // data movement
-  BroadcastInDim, Transpose, Reshape, Iota,
+  BroadcastInDim, Transpose, Reshape, Iota, Slice, Concatenate, Pad,
   // contractions and reductions
   DotGeneral, Reduce,
 };
@@ -62,6 +62,9 @@ struct Node {
   std::vector<int> operands;
   // attributes (meaning depends on op)
   std::vector<int64_t> dims;  // broadcast_dimensions / permutation / reduce dimensions
+  // slice: start / limit / stride per dim; pad: edge_padding_low / edge_padding_high / interior_padding
+  std::vector<int64_t> lo, hi, step;
+  int64_t axis = 0;  // concatenate dimension
   int64_t iota_dim = 0;
   CmpDir cmp = CmpDir::EQ;
   CmpType cmp_type = CmpType::NOTYPE;

@@ -76,6 +76,12 @@ struct EwProgram {
   void* out_ptr[EW_MAX_OUT];        // contiguous row-major over `shape` (elementwise kernels)
   int32_t needs_coords;             // any GENERAL leaf or IOTA
   int32_t out_float_mask;           // bit o set: output o's register holds float bits
+  // out_strided = 1: the (single) output is written at out_offset + Σ coord[d]·out_strides[d] elements instead of
+  // contiguously (a region of a larger tensor: concatenate's operands, pad's interior); elementwise kernels only
+  int32_t out_strided;
+  int32_t pad_;
+  int64_t out_offset;
+  int64_t out_strides[EW_MAX_RANK];
   EwLeaf leaves[EW_MAX_LEAVES];
   EwInstr instr[EW_MAX_INSTR];
 };

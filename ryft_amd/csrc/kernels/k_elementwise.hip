@@ -25,6 +25,12 @@ __global__ void __launch_bounds__(256) ew_kernel(const EwProgram P) {
     if (COORDS) decompose(lin, P, coord);
     RegFile1 R;
     ew_run(P, lin, coord, nullptr, R);
+    if (COORDS && P.out_strided) {
+      int64_t off = P.out_offset;
+      for (int d = 0; d < P.rank; ++d) off += (int64_t)coord[d] * P.out_strides[d];
+      store_bits(P.out_ptr[0], off, P.out_dtype[0], R.get(P.out_reg[0]), P.out_float_mask & 1);
+      continue;
+    }
     for (int o = 0; o < P.n_out; ++o)
       store_bits(P.out_ptr[o], lin, P.out_dtype[o], R.get(P.out_reg[o]), (P.out_float_mask >> o) & 1);
   }
@@ -201,8 +207,10 @@ static bool prepare_vec(EwProgram& p, bool check_outputs) {
 
 void launch_elementwise(const EwProgram& p, hipStream_t stream, hipEvent_t done) {
   if (p.total == 0) return record_done(done, stream);
+  if (p.out_strided && (p.n_out != 1 || !p.needs_coords))
+    fail(PJRT_Error_Code_INTERNAL, "strided-output elementwise step needs one output and coordinates");
   EwProgram v = p;
-  if (prepare_vec(v, true)) {
+  if (!p.out_strided && prepare_vec(v, true)) {
     dim3 grid(grid_for(v.total / VEC, VNT)), block(VNT);
     const bool small = program_regs(v) <= EW_SMALL_REGS;
     if (v.needs_coords) {

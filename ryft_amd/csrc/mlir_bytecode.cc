@@ -581,6 +581,11 @@ class BytecodeParser {
         {"stablehlo.broadcast_in_dim", {{"broadcast_dimensions", true, {BAttr::DENSE_ARRAY}}}},
         {"stablehlo.transpose", {{"permutation", true, {BAttr::DENSE_ARRAY}}}},
         {"stablehlo.reduce", {{"dimensions", true, {BAttr::DENSE_ARRAY}}}},
+        {"stablehlo.slice", {{"limit_indices", true, {BAttr::DENSE_ARRAY}}, {"start_indices", true, {BAttr::DENSE_ARRAY}},
+                             {"strides", true, {BAttr::DENSE_ARRAY}}}},
+        {"stablehlo.concatenate", {{"dimension", true, {BAttr::INT}}}},
+        {"stablehlo.pad", {{"edge_padding_high", true, {BAttr::DENSE_ARRAY}}, {"edge_padding_low", true, {BAttr::DENSE_ARRAY}},
+                           {"interior_padding", true, {BAttr::DENSE_ARRAY}}}},
         {"stablehlo.compare",
          {{"compare_type", false, {BAttr::CMP_TYPE}}, {"comparison_direction", true, {BAttr::CMP_DIR}}}},
         {"stablehlo.dot_general",
@@ -602,6 +607,7 @@ class BytecodeParser {
     if (op == "func.func") return pick({"sym_name", "function_type", "sym_visibility", "arg_attrs", "res_attrs"});
     if (op == "stablehlo.compare") return pick({"comparison_direction", "compare_type"});
     if (op == "stablehlo.dot_general") return pick({"dot_dimension_numbers", "precision_config", "algorithm"});
+    // (slice and pad: three fields of one kind, so another order could not be told apart; sorted only)
     return sorted;
   }
 
@@ -885,6 +891,20 @@ class BytecodeParser {
       } else if (nm == "transpose") {
         n.op = Op::Transpose;
         n.dims = int_list(op, "permutation");
+      } else if (nm == "slice") {
+        n.op = Op::Slice;
+        n.lo = int_list(op, "start_indices");
+        n.hi = int_list(op, "limit_indices");
+        n.step = int_list(op, "strides");
+      } else if (nm == "concatenate") {
+        n.op = Op::Concatenate;
+        const BAttr& a = need(op, "dimension");
+        n.axis = a.kind == BAttr::INT ? a.i : mlir_int_list_text(a.str).at(0);
+      } else if (nm == "pad") {
+        n.op = Op::Pad;
+        n.lo = int_list(op, "edge_padding_low");
+        n.hi = int_list(op, "edge_padding_high");
+        n.step = int_list(op, "interior_padding");
       } else if (nm == "compare") {
         n.op = Op::Compare;
         const BAttr& d = need(op, "comparison_direction");

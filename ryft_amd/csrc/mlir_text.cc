@@ -7,6 +7,7 @@
 //   broadcast_in_dim  .../manipulation.rs:2154        select    .../control_flow.rs:596
 //   iota              .../miscellaneous.rs:1181       convert   .../casting.rs:456
 //   compare           .../comparison.rs:500, control_flow.rs:534
+//   slice / concatenate / pad  .../manipulation.rs:2438, 2388, 2257
 #include <cctype>
 #include <cmath>
 #include <cstdlib>
@@ -82,6 +83,9 @@ const char* op_name(Op op) {
     case Op::BroadcastInDim: return "broadcast_in_dim";
     case Op::Transpose: return "transpose";
     case Op::Reshape: return "reshape";
+    case Op::Slice: return "slice";
+    case Op::Concatenate: return "concatenate";
+    case Op::Pad: return "pad";
     case Op::Iota: return "iota";
     case Op::DotGeneral: return "dot_general";
     case Op::Reduce: return "reduce";
@@ -761,6 +765,34 @@ class Parser {
       }
       return;
     }
+    if (n == "slice") {
+      // stablehlo.slice %x [start:limit(:stride), ...] : fn
+      os.operands.push_back(c_.sigil_name('%'));
+      c_.expect("[");
+      std::string st, li, sp;
+      c_.skip_ws();
+      if (c_.peek_raw() != ']') {
+        for (;;) {
+          const int64_t a = c_.integer();
+          c_.expect(":");
+          const int64_t b = c_.integer();
+          int64_t k = 1;
+          if (c_.try_consume(":")) k = c_.integer();
+          st += (st.empty() ? "" : ", ") + std::to_string(a);
+          li += (li.empty() ? "" : ", ") + std::to_string(b);
+          sp += (sp.empty() ? "" : ", ") + std::to_string(k);
+          if (!c_.try_consume(",")) break;
+        }
+      }
+      c_.expect("]");
+      os.attrs["start_indices"] = "[" + st + "]";
+      os.attrs["limit_indices"] = "[" + li + "]";
+      os.attrs["strides"] = "[" + sp + "]";
+      if (c_.try_consume("{")) parse_attr_dict(os.attrs);
+      c_.expect(":");
+      os.type = parse_fn_or_types(c_);
+      return;
+    }
     if (n == "compare") {
       os.attrs["comparison_direction"] = c_.ident();
       c_.expect(",");
@@ -859,6 +891,22 @@ class Parser {
       std::string d = get("dims");
       if (d.empty()) d = get("permutation");
       n.dims = parse_int_list_text(d);
+    } else if (nm == "slice") {
+      n.op = Op::Slice;
+      n.lo = parse_int_list_text(get("start_indices"));
+      n.hi = parse_int_list_text(get("limit_indices"));
+      n.step = parse_int_list_text(get("strides"));
+    } else if (nm == "concatenate") {
+      n.op = Op::Concatenate;
+      std::string d = get("dim");
+      if (d.empty()) d = get("dimension");
+      n.axis = parse_int_list_text(d).at(0);
+    } else if (nm == "pad") {
+      n.op = Op::Pad;
+      std::string l = get("low"), h = get("high"), in = get("interior");
+      n.lo = parse_int_list_text(l.empty() ? get("edge_padding_low") : l);
+      n.hi = parse_int_list_text(h.empty() ? get("edge_padding_high") : h);
+      n.step = parse_int_list_text(in.empty() ? get("interior_padding") : in);
     } else if (nm == "compare") {
       n.op = Op::Compare;
       n.cmp = parse_dir(get("comparison_direction"));
@@ -976,6 +1024,49 @@ void validate_node(const Graph& g, Node& n) {
       need(1);
       if (opt(0).elements() != n.type.elements()) invalid("reshape: element count mismatch");
       break;
+    case Op::Slice: {
+      need(1);
+      const int r = opt(0).rank();
+      if ((int)n.lo.size() != r || (int)n.hi.size() != r || (int)n.step.size() != r)
+        invalid("slice: start / limit / stride lists must have one entry per dimension");
+      for (int d = 0; d < r; ++d) {
+        if (n.step[d] < 1) invalid("slice: strides must be positive");
+        if (n.lo[d] < 0 || n.lo[d] > n.hi[d] || n.hi[d] > opt(0).shape[d]) invalid("slice: indices out of range");
+        if (n.type.shape[d] != (n.hi[d] - n.lo[d] + n.step[d] - 1) / n.step[d]) invalid("slice: result shape mismatch");
+      }
+      if (n.type.dtype != opt(0).dtype) invalid("slice: element type mismatch");
+      break;
+    }
+    case Op::Concatenate: {
+      if (n.operands.empty()) invalid("concatenate expects at least one operand");
+      const int r = n.type.rank();
+      if (n.axis < 0 || n.axis >= r) invalid("concatenate: dimension out of range");
+      int64_t total = 0;
+      for (size_t i = 0; i < n.operands.size(); ++i) {
+        const TensorType& t = opt((int)i);
+        if (t.rank() != r || t.dtype != n.type.dtype) invalid("concatenate: operand rank or type mismatch");
+        for (int d = 0; d < r; ++d)
+          if (d != n.axis && t.shape[d] != n.type.shape[d]) invalid("concatenate: operand shape mismatch");
+        total += t.shape[n.axis];
+      }
+      if (total != n.type.shape[n.axis]) invalid("concatenate: result shape mismatch");
+      break;
+    }
+    case Op::Pad: {
+      need(2);
+      const int r = opt(0).rank();
+      if ((int)n.lo.size() != r || (int)n.hi.size() != r || (int)n.step.size() != r)
+        invalid("pad: padding lists must have one entry per dimension");
+      if (opt(1).rank() != 0 || opt(1).dtype != opt(0).dtype || n.type.dtype != opt(0).dtype)
+        invalid("pad: padding value must be a scalar of the operand's type");
+      for (int d = 0; d < r; ++d) {
+        if (n.step[d] < 0) invalid("pad: interior padding must be non-negative");
+        const int64_t k = opt(0).shape[d];
+        const int64_t want = n.lo[d] + n.hi[d] + k + (k > 0 ? (k - 1) * n.step[d] : 0);
+        if (want < 0 || n.type.shape[d] != want) invalid("pad: result shape mismatch");
+      }
+      break;
+    }
     case Op::DotGeneral: {
       need(2);
       auto& L = opt(0);

@@ -94,6 +94,8 @@ class ExprBuilder {
   std::set<int> inner_nodes;     // elementwise nodes computed inside the program
 
   Val emit(int node, const std::vector<int>& src);
+  // A load of a materialized view read along the iteration space (view dim d ↔ space dim d), `extra` elements on.
+  Val load_view(const View& v, int64_t extra, DType dtype);
   void add_output(Val v, DType dtype) { outputs_.push_back({v.instr, dtype}); }
   EwProgram finish();
   const std::vector<Leaf>& leaves() const { return leaves_; }
@@ -160,6 +162,10 @@ class Planner {
   bool try_attention(int d2, int target, DType out_dtype, int root);
   void emit_copy(int src_slot, int64_t src_off, int dst_slot, size_t bytes);
   bool dot_operand(int dot, int which, GemmOperand* op, int* slot, int force_copy);
+  void emit_concatenate(int node, int target);
+  void emit_pad(int node, int target);
+  void push_strided_step(ExprBuilder& b, const char* name, int out, int64_t out_offset,
+                         const std::vector<int64_t>& out_strides, double in_bytes, double out_bytes);
   int canonical_copy(int node, const std::vector<int64_t>& order);
   void push_program_patches(Step& st, size_t base, const EwProgram& p, const std::vector<Leaf>& leaves,
                             const std::vector<int>& out_slots);
@@ -206,6 +212,19 @@ ExprBuilder::Val ExprBuilder::leaf_load(int node, const std::vector<int>& src, D
   l.strides.assign(space_.size(), 0);
   for (size_t d = 0; d < src.size(); ++d)
     if (src[d] >= 0) l.strides[src[d]] += v.strides[d];
+  ins.op = EW_LOAD;
+  ins.a = (uint8_t)std::min(leaf_index(l), 255);
+  return {push(ins, float_class(dtype), {}), float_class(dtype)};
+}
+
+ExprBuilder::Val ExprBuilder::load_view(const View& v, int64_t extra, DType dtype) {
+  Leaf l;
+  l.slot = v.slot;
+  l.dtype = v.dtype;
+  l.offset = v.offset + extra;
+  l.strides = v.strides;
+  l.strides.resize(space_.size(), 0);
+  EwInstr ins{};
   ins.op = EW_LOAD;
   ins.a = (uint8_t)std::min(leaf_index(l), 255);
   return {push(ins, float_class(dtype), {}), float_class(dtype)};
@@ -270,6 +289,9 @@ ExprBuilder::Val ExprBuilder::emit(int node, const std::vector<int>& src) {
     std::vector<int> s2(o.type.rank());
     for (size_t i = 0; i < n.dims.size(); ++i) s2[n.dims[i]] = src[i];
     out = emit(n.operands[0], s2);
+  } else if (n.op == Op::Slice) {
+    // a slice is a view of its operand: offset by the start indices, strides scaled by the slice strides
+    out = leaf_load(node, src, dt);
   } else if (op_is_elementwise(n.op)) {
     inner_nodes.insert(node);
     std::vector<Val> ops;
@@ -444,6 +466,15 @@ View Planner::view_of(int node) {
     v.strides = row_major_strides(n.type.shape);
     return v;
   }
+  if (n.op == Op::Slice && !materialized(node)) {
+    View b = view_of(n.operands[0]);
+    v = b;
+    for (int d = 0; d < n.type.rank(); ++d) {
+      v.offset += n.lo[d] * b.strides[d];
+      v.strides[d] = b.strides[d] * n.step[d];
+    }
+    return v;
+  }
   v.slot = materialize(node);
   v.dtype = plan_.slots[v.slot].type.dtype;
   v.strides = row_major_strides(n.type.shape);
@@ -490,6 +521,12 @@ int Planner::materialize(int node, int target) {
       break;
     case Op::Reduce:
       emit_reduce(node, target);
+      break;
+    case Op::Concatenate:
+      emit_concatenate(node, target);
+      break;
+    case Op::Pad:
+      emit_pad(node, target);
       break;
     case Op::Reshape: {
       int s = materialize(n.operands[0]);
@@ -571,6 +608,7 @@ void Planner::emit_elementwise_root(int node, int target) {
         st.kind = Step::COPY;
         st.name = "copy";
         st.copy.bytes = (int64_t)n.type.bytes();
+        st.copy.src_offset = b.leaves()[0].offset * (int64_t)dtype_size(n.type.dtype);
         st.patches = {{0, b.leaves()[0].slot}, {1, out}};
         st.bytes = 2.0 * (double)n.type.bytes();
       } else {
@@ -588,6 +626,110 @@ void Planner::emit_elementwise_root(int node, int target) {
       for (int o : n.operands) materialize(o);
     }
   }
+}
+
+// One elementwise step whose single output is a region of `out`: element c of the program's space is written at
+// out_offset + Σ c[d]·out_strides[d].
+void Planner::push_strided_step(ExprBuilder& b, const char* name, int out, int64_t out_offset,
+                                const std::vector<int64_t>& out_strides, double in_bytes, double out_bytes) {
+  EwProgram p = b.finish();
+  p.out_strided = 1;
+  p.needs_coords = 1;
+  p.out_offset = out_offset;
+  for (int d = 0; d < p.rank; ++d) p.out_strides[d] = out_strides[d];
+  Step st{};
+  st.kind = Step::ELEMENTWISE;
+  st.name = name;
+  st.ew = p;
+  push_program_patches(st, 0, p, b.leaves(), {out});
+  st.bytes = in_bytes + out_bytes;
+  plan_.steps.push_back(std::move(st));
+}
+
+// concatenate (manipulation.rs:778-822): each operand's expression is computed straight into its region of the
+// result (the operands' producers fuse into those steps).
+void Planner::emit_concatenate(int node, int target) {
+  const Node& n = g_.nodes[node];
+  const int out = temp_or(target, n.type);
+  const auto rm = row_major_strides(n.type.shape);
+  int64_t at = 0;
+  for (int o : n.operands) {
+    const Node& on = g_.nodes[o];
+    const int64_t len = on.type.shape[n.axis];
+    if (on.type.elements() > 0) {
+      std::vector<int> ident(on.type.rank());
+      for (int d = 0; d < on.type.rank(); ++d) ident[d] = d;
+      for (int attempt = 0; attempt < 2; ++attempt) {
+        try {
+          ExprBuilder b(*this, on.type.shape);
+          b.add_output(b.emit(o, ident), n.type.dtype);
+          push_strided_step(b, "concatenate", out, at * rm[n.axis], rm, leaf_bytes(plan_, b.leaves()),
+                            (double)on.type.bytes());
+          break;
+        } catch (const Status& s) {
+          if (s.code != PJRT_Error_Code_RESOURCE_EXHAUSTED || attempt == 1) throw;
+          materialize(o);
+        }
+      }
+    }
+    at += len;
+  }
+  mat_[node] = out;
+}
+
+// pad (manipulation.rs:530-642): result[lo + i·(interior + 1)] = operand[i] where that index is inside the result,
+// the padding value everywhere else. One step fills the result; a second writes the operand elements that land
+// inside it (negative edge padding drops operand elements, interior padding spaces the writes).
+void Planner::emit_pad(int node, int target) {
+  const Node& n = g_.nodes[node];
+  const Node& xn = g_.nodes[n.operands[0]];
+  const int r = n.type.rank();
+  const int out = temp_or(target, n.type);
+  if (n.type.elements() == 0) {
+    mat_[node] = out;
+    return;
+  }
+  {
+    ExprBuilder b(*this, n.type.shape);
+    b.add_output(b.emit(n.operands[1], std::vector<int>()), n.type.dtype);
+    EwProgram p = b.finish();
+    Step st{};
+    st.kind = Step::ELEMENTWISE;
+    st.name = "pad_fill";
+    st.ew = p;
+    push_program_patches(st, 0, p, b.leaves(), {out});
+    st.bytes = (double)n.type.bytes();
+    plan_.steps.push_back(std::move(st));
+  }
+  const auto rm = row_major_strides(n.type.shape);
+  std::vector<int64_t> first(r), count(r), ostr(r);
+  int64_t out_offset = 0;
+  bool any = xn.type.elements() > 0;
+  for (int d = 0; d < r && any; ++d) {
+    const int64_t s = n.step[d] + 1, lo = n.lo[d], k = xn.type.shape[d], od = n.type.shape[d];
+    const int64_t i0 = lo >= 0 ? 0 : (-lo + s - 1) / s;                      // first operand index landing at ≥ 0
+    const int64_t i1 = od - 1 - lo < 0 ? -1 : std::min(k - 1, (od - 1 - lo) / s);  // last one landing < od
+    if (i1 < i0) {
+      any = false;
+      break;
+    }
+    first[d] = i0;
+    count[d] = i1 - i0 + 1;
+    ostr[d] = rm[d] * s;
+    out_offset += (lo + i0 * s) * rm[d];
+  }
+  if (any) {
+    View v = view_of(n.operands[0]);
+    int64_t extra = 0;
+    for (int d = 0; d < r; ++d) extra += first[d] * v.strides[d];
+    ExprBuilder b(*this, count);
+    b.add_output(b.load_view(v, extra, xn.type.dtype), n.type.dtype);
+    int64_t elems = 1;
+    for (auto c : count) elems *= c;
+    const double bytes = (double)elems * (double)dtype_size(n.type.dtype);
+    push_strided_step(b, "pad", out, out_offset, ostr, bytes, bytes);
+  }
+  mat_[node] = out;
 }
 
 void Planner::emit_reduce(int node, int target) {

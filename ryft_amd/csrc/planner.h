@@ -24,7 +24,7 @@ struct Step {
   GemmArgs gemm;
   AttnArgs attn;
   RowArgs row;
-  struct { int64_t bytes; } copy;
+  struct { int64_t bytes; int64_t src_offset; } copy;  // src_offset: bytes into the source slot
   // Pointer fields inside the args block that refer to slots: (byte offset of the pointer field, slot). The
   // field's initial value is a byte offset into the slot's buffer.
   std::vector<std::pair<size_t, int>> patches;

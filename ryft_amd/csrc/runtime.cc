@@ -615,7 +615,7 @@ EventPtr execute(LoadedExecutable* le, Device* d, Buffer* const* args, size_t nu
         else pending_start() = tm.start;
       }
       if (step.kind == Step::COPY) {
-        void* src = ptr[step.patches[0].second];
+        void* src = (char*)ptr[step.patches[0].second] + step.copy.src_offset;
         void* dst = ptr[step.patches[1].second];
         if (step.copy.bytes) HIP_CHECK(hipMemcpyAsync(dst, src, (size_t)step.copy.bytes, hipMemcpyDeviceToDevice, st));
       } else {

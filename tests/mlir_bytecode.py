@@ -158,6 +158,17 @@ def _parse_op(res: str, name: str, rest: str) -> Op:
             attrs["compare_type"] = ("cmp_type", parts[3])
         ins, outs = _types_after_colon(ty)
         return Op(name, parts[1:3], [res], outs, attrs)
+    if short == "slice":
+        m = re.fullmatch(r"(%\w+) \[(.*?)\] : (.*)", rest.strip())
+        starts, limits, strides = [], [], []
+        for part in [x for x in m.group(2).split(",") if x.strip()]:
+            f = [int(v) for v in part.split(":")]
+            starts.append(f[0])
+            limits.append(f[1])
+            strides.append(f[2] if len(f) > 2 else 1)
+        ins, outs = _types_after_colon(m.group(3))
+        return Op(name, [m.group(1)], [res], outs, {"start_indices": ("i64s", starts), "limit_indices": ("i64s", limits),
+                                                    "strides": ("i64s", strides)})
     body, ty = rest.split(" : ", 1)
     ins, outs = _types_after_colon(ty)
     items = _split_top(body)
@@ -167,6 +178,13 @@ def _parse_op(res: str, name: str, rest: str) -> Op:
         key = "broadcast_dimensions" if short == "broadcast_in_dim" else "permutation"
         kv = [x for x in items if x.startswith("dims")][0]
         attrs[key] = ("i64s", _ints(kv.split("=", 1)[1]))
+    if short == "concatenate":
+        kv = [x for x in items if x.startswith("dim")][0]
+        attrs["dimension"] = ("i64", int(kv.split("=", 1)[1]))
+    if short == "pad":
+        for key, attr in (("low", "edge_padding_low"), ("high", "edge_padding_high"), ("interior", "interior_padding")):
+            kv = [x for x in items if x.startswith(key)][0]
+            attrs[attr] = ("i64s", _ints(kv.split("=", 1)[1]))
     if short == "dot_general":
         dd = {"lhs_batch": [], "rhs_batch": [], "lhs_contract": [], "rhs_contract": []}
         for x in items:
@@ -188,15 +206,22 @@ SORTED = {
     "func.func": ["arg_attrs", "function_type", "res_attrs", "sym_name", "sym_visibility"],
     "stablehlo.compare": ["compare_type", "comparison_direction"],
     "stablehlo.dot_general": ["algorithm", "dot_dimension_numbers", "precision_config"],
+    "stablehlo.slice": ["limit_indices", "start_indices", "strides"],
+    "stablehlo.pad": ["edge_padding_high", "edge_padding_low", "interior_padding"],
 }
 # ... and in declaration order
 DECLARED = {
     "func.func": ["sym_name", "function_type", "sym_visibility", "arg_attrs", "res_attrs"],
     "stablehlo.compare": ["comparison_direction", "compare_type"],
     "stablehlo.dot_general": ["dot_dimension_numbers", "precision_config", "algorithm"],
+    # slice and pad: written sorted in every variant (three fields of one kind: a reader could not tell another
+    # order apart)
+    "stablehlo.slice": ["limit_indices", "start_indices", "strides"],
+    "stablehlo.pad": ["edge_padding_high", "edge_padding_low", "interior_padding"],
 }
 REQUIRED = {"function_type", "sym_name", "comparison_direction", "dot_dimension_numbers", "value", "iota_dimension",
-            "broadcast_dimensions", "permutation", "dimensions"}
+            "broadcast_dimensions", "permutation", "dimensions", "start_indices", "limit_indices", "strides",
+            "dimension", "edge_padding_low", "edge_padding_high", "interior_padding"}
 
 
 class Writer:

@@ -27,6 +27,19 @@ def _config_program(name):
     return configs.CONFIGS[name]().program  # (generates the inputs too: once per config)
 
 
+SLICE_CONCAT_PAD = """module {
+  func.func @main(%arg0: tensor<6x8xf32>, %arg1: tensor<f32>) -> (tensor<6x12xf32>, tensor<9x8xf32>) {
+    %0 = stablehlo.slice %arg0 [0:6, 1:8:2] : (tensor<6x8xf32>) -> tensor<6x4xf32>
+    %1 = stablehlo.concatenate %arg0, %0, dim = 1 : (tensor<6x8xf32>, tensor<6x4xf32>) -> tensor<6x12xf32>
+    %2 = stablehlo.pad %arg0, %arg1, low = [2, -1], high = [-1, 0], interior = [1, 0] : (tensor<6x8xf32>, tensor<f32>) -> tensor<12x7xf32>
+    %3 = stablehlo.slice %2 [3:12, 0:7] : (tensor<12x7xf32>) -> tensor<9x7xf32>
+    %4 = stablehlo.concatenate %3, %3, dim = 1 : (tensor<9x7xf32>, tensor<9x7xf32>) -> tensor<9x14xf32>
+    %5 = stablehlo.slice %4 [0:9, 3:11] : (tensor<9x14xf32>) -> tensor<9x8xf32>
+    return %1, %5 : tensor<6x12xf32>, tensor<9x8xf32>
+  }
+}
+"""
+
 PROGRAMS = {
     "c1": lambda: _config_program("c1"),
     "c2": lambda: _config_program("c2"),
@@ -35,6 +48,7 @@ PROGRAMS = {
     "c5": lambda: _config_program("c5"),
     "layernorm": lambda: row_programs.layernorm((8, 33)),
     "int_row_max": lambda: row_programs.int_row_max_gap((8, 64)),
+    "slice_concatenate_pad": lambda: SLICE_CONCAT_PAD,
 }
 
 

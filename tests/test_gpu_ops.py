@@ -200,3 +200,80 @@ def test_mfma_bf16_with_generic_epilogue(gpu_client):
     outs, exe = run_pjrt(gpu_client, prog, ins)
     assert "gemm_bf16_mfma" in exe.describe_plan()
     check(outs[0], oracle_outputs(prog, ins)[0], 1e-4, "bf16+tanh")
+
+
+# slice / concatenate / pad (manipulation.rs:530-917): slices are views read in place, concatenate writes each
+# operand's expression into its region, pad fills and then writes the kept operand elements
+def _ints_input(seed, shape, dt="i32"):
+    x = hd.int_uniform(seed, shape, -1000, 1000).astype(np.int32)
+    return configs.HostInput(x, pjrt.BufferType.S32, shape)
+
+
+@pytest.mark.parametrize("case", ["strided_f32", "outer_rows_bf16", "golden_i32"])
+def test_slice_views(gpu_client, case):
+    if case == "strided_f32":
+        prog = _mod(["tensor<8x33xf32>"], ["tensor<6x11xf32>"], """    %0 = stablehlo.slice %arg0 [1:7, 2:33:3] : (tensor<8x33xf32>) -> tensor<6x11xf32>
+    %1 = stablehlo.negate %0 : tensor<6x11xf32>
+    return %1 : tensor<6x11xf32>""")
+        ins = _f32_inputs(1, (8, 33))
+    elif case == "outer_rows_bf16":
+        # contiguous rows: the plan copies bytes from an offset into the operand
+        prog = _mod(["tensor<4x64xbf16>"], ["tensor<2x64xbf16>"], """    %0 = stablehlo.slice %arg0 [1:3, 0:64] : (tensor<4x64xbf16>) -> tensor<2x64xbf16>
+    return %0 : tensor<2x64xbf16>""")
+        x = hd.f32_to_bf16_bits(hd.normal(3, (4, 64)))
+        ins = [configs.HostInput(x, pjrt.BufferType.BF16, (4, 64))]
+    else:
+        prog = _mod(["tensor<3x4x5xi32>"], ["tensor<2x2x3xi32>"], """    %0 = stablehlo.slice %arg0 [0:2, 1:3, 0:5:2] : (tensor<3x4x5xi32>) -> tensor<2x2x3xi32>
+    return %0 : tensor<2x2x3xi32>""")
+        ins = [_ints_input(4, (3, 4, 5))]
+    outs, _ = run_pjrt(gpu_client, prog, ins)
+    for o, w in zip(outs, oracle_outputs(prog, ins)):
+        check(o, w, 0, case)
+
+
+def test_slice_feeds_gemm_in_place(gpu_client):
+    prog = _mod(["tensor<64x256xbf16>", "tensor<128x64xbf16>"], ["tensor<64x64xf32>"], """    %0 = stablehlo.slice %arg0 [0:64, 128:256] : (tensor<64x256xbf16>) -> tensor<64x128xbf16>
+    %1 = stablehlo.dot_general %0, %arg1, contracting_dims = [1] x [0] : (tensor<64x128xbf16>, tensor<128x64xbf16>) -> tensor<64x64xf32>
+    return %1 : tensor<64x64xf32>""")
+    ins = [configs.HostInput(hd.f32_to_bf16_bits(hd.normal(5, (64, 256))), pjrt.BufferType.BF16, (64, 256)),
+           configs.HostInput(hd.f32_to_bf16_bits(hd.normal(6, (128, 64))), pjrt.BufferType.BF16, (128, 64))]
+    outs, exe = run_pjrt(gpu_client, prog, ins)
+    assert exe.describe_plan().split()[1].startswith("gemm")
+    check(outs[0], oracle_outputs(prog, ins)[0], 1e-5, "slice·B")  # bf16 products are exact in f32
+
+
+def test_concatenate_with_fused_producers(gpu_client):
+    prog = _mod(["tensor<8x16xf32>", "tensor<8x16xf32>"], ["tensor<8x40xf32>", "tensor<24x16xf32>"], """    %0 = stablehlo.slice %arg0 [0:8, 4:12] : (tensor<8x16xf32>) -> tensor<8x8xf32>
+    %1 = stablehlo.slice %arg1 [0:8, 0:16:2] : (tensor<8x16xf32>) -> tensor<8x8xf32>
+    %2 = stablehlo.add %0, %1 : tensor<8x8xf32>
+    %3 = stablehlo.negate %arg1 : tensor<8x16xf32>
+    %4 = stablehlo.concatenate %3, %2, %arg0, dim = 1 : (tensor<8x16xf32>, tensor<8x8xf32>, tensor<8x16xf32>) -> tensor<8x40xf32>
+    %5 = stablehlo.concatenate %arg0, %3, %arg1, dim = 0 : (tensor<8x16xf32>, tensor<8x16xf32>, tensor<8x16xf32>) -> tensor<24x16xf32>
+    return %4, %5 : tensor<8x40xf32>, tensor<24x16xf32>""")
+    ins = _f32_inputs(2, (8, 16))
+    outs, _ = run_pjrt(gpu_client, prog, ins)
+    for i, (o, w) in enumerate(zip(outs, oracle_outputs(prog, ins))):
+        check(o, w, 0, f"concatenate {i}")
+
+
+@pytest.mark.parametrize("shape,lo,hi,interior", [((2, 3), (0, 1), (2, 1), (1, 2)), ((8, 16), (1, -1), (3, 2), (0, 0)),
+                                                  ((5, 7), (-3, 2), (-4, -2), (2, 1)),
+                                                  ((3, 4), (-3, 0), (1, 0), (0, 0))])  # last: all operand rows cut
+def test_pad(gpu_client, shape, lo, hi, interior):
+    out_shape = tuple(l + h + k + (k - 1) * it for k, l, h, it in zip(shape, lo, hi, interior))
+    t, ot = _t(shape, "i32"), _t(out_shape, "i32")
+    prog = _mod([t, "tensor<i32>"], [ot], f"""    %0 = stablehlo.pad %arg0, %arg1, low = {list(lo)}, high = {list(hi)}, interior = {list(interior)} : ({t}, tensor<i32>) -> {ot}
+    return %0 : {ot}""")
+    ins = [_ints_input(7, shape), configs.HostInput(np.array(-5, np.int32), pjrt.BufferType.S32, ())]
+    outs, _ = run_pjrt(gpu_client, prog, ins)
+    check(outs[0], oracle_outputs(prog, ins)[0], 0, "pad")
+
+
+def test_pad_float_with_computed_value(gpu_client):
+    prog = _mod(["tensor<6x8xf32>", "tensor<f32>"], ["tensor<9x10xf32>"], """    %0 = stablehlo.exponential %arg1 : tensor<f32>
+    %1 = stablehlo.pad %arg0, %0, low = [2, 1], high = [-1, 1], interior = [0, 0] : (tensor<6x8xf32>, tensor<f32>) -> tensor<7x10xf32>
+    %2 = stablehlo.pad %1, %arg1, low = [1, 0], high = [1, 0], interior = [0, 0] : (tensor<7x10xf32>, tensor<f32>) -> tensor<9x10xf32>
+    return %2 : tensor<9x10xf32>""")
+    ins = _f32_inputs(1, (6, 8)) + [configs.HostInput(np.array(0.5, np.float32), pjrt.BufferType.F32, ())]
+    outs, _ = run_pjrt(gpu_client, prog, ins)
+    check(outs[0], oracle_outputs(prog, ins)[0], 1e-6, "pad f32")

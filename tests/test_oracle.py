@@ -165,3 +165,45 @@ def test_broadcast_in_dim_permuting_dims():
     (out, _), = sh.evaluate(prog, [np.array([[1, 2, 3]])])
     want = np.array([[[1, 1], [2, 2], [3, 3]], [[1, 1], [2, 2], [3, 3]]])
     assert np.array_equal(out, want)
+
+
+def test_pad_concatenate_slice_reference_examples():
+    # the worked examples in ryft-mlir's documentation of each builder (manipulation.rs:549-570, 772-781, 848-864)
+    pad = _mod(["tensor<2x3xi32>", "tensor<i32>"], "tensor<5x9xi32>", """
+    %0 = stablehlo.pad %arg0, %arg1, low = [0, 1], high = [2, 1], interior = [1, 2] : (tensor<2x3xi32>, tensor<i32>) -> tensor<5x9xi32>
+    return %0 : tensor<5x9xi32>""")
+    (out, _), = sh.evaluate(pad, [np.array([[1, 2, 3], [4, 5, 6]]), np.array(0)])
+    assert out.tolist() == [[0, 1, 0, 0, 2, 0, 0, 3, 0], [0] * 9, [0, 4, 0, 0, 5, 0, 0, 6, 0], [0] * 9, [0] * 9]
+    cat = _mod(["tensor<3x2xi64>", "tensor<1x2xi64>"], "tensor<4x2xi64>", """
+    %0 = stablehlo.concatenate %arg0, %arg1, dim = 0 : (tensor<3x2xi64>, tensor<1x2xi64>) -> tensor<4x2xi64>
+    return %0 : tensor<4x2xi64>""")
+    (out, _), = sh.evaluate(cat, [np.array([[1, 2], [3, 4], [5, 6]]), np.array([[7, 8]])])
+    assert out.tolist() == [[1, 2], [3, 4], [5, 6], [7, 8]]
+    sl = _mod(["tensor<3x4xi64>"], "tensor<2x2xi64>", """
+    %0 = stablehlo.slice %arg0 [1:3, 2:4] : (tensor<3x4xi64>) -> tensor<2x2xi64>
+    return %0 : tensor<2x2xi64>""")
+    (out, _), = sh.evaluate(sl, [np.array([[0, 0, 0, 0], [0, 0, 1, 1], [0, 0, 1, 1]])])
+    assert out.tolist() == [[1, 1], [1, 1]]
+
+
+@pytest.mark.parametrize("shape,lo,hi,interior", [((3, 4), (2, -1), (-2, 3), (0, 1)), ((5,), (-3,), (-4,), (2,)),
+                                                  ((2, 3, 2), (1, 0, -1), (0, 2, -1), (1, 0, 3)),
+                                                  ((4, 1), (-4, 0), (1, 0), (0, 0))])
+def test_pad_matches_the_index_formula(shape, lo, hi, interior):
+    # the builder documentation's definition (manipulation.rs:544-546): result[lo + i·(interior + 1)] = operand[i]
+    # where that index lies in the result, the padding value elsewhere; checked element by element against the
+    # oracle's interior-then-edges construction, including negative edges that cut interior padding
+    out_shape = tuple(l + h + k + (k - 1) * it for k, l, h, it in zip(shape, lo, hi, interior))
+    t = "tensor<" + "x".join(map(str, shape)) + "xi32>"
+    ot = "tensor<" + "x".join(map(str, out_shape)) + "xi32>"
+    prog = _mod([t, "tensor<i32>"], ot, f"""
+    %0 = stablehlo.pad %arg0, %arg1, low = {list(lo)}, high = {list(hi)}, interior = {list(interior)} : ({t}, tensor<i32>) -> {ot}
+    return %0 : {ot}""")
+    x = np.arange(1, 1 + int(np.prod(shape))).reshape(shape)
+    (out, _), = sh.evaluate(prog, [x, np.array(-7)])
+    want = np.full(out_shape, -7)
+    for idx in np.ndindex(*shape):
+        pos = tuple(l + i * (it + 1) for l, i, it in zip(lo, idx, interior))
+        if all(0 <= p < n for p, n in zip(pos, out_shape)):
+            want[pos] = x[idx]
+    assert np.array_equal(out, want)

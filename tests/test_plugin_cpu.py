@@ -159,6 +159,25 @@ GOLDENS = {
     return %0 : tensor<3xi1>
   }
 }""",
+    # manipulation.rs:2257-2265, 2388-2389, 2438 (joined lines, entry renamed @main)
+    "pad": """module {
+  func.func @main(%arg0: tensor<2x3xi32>, %arg1: tensor<i32>) -> tensor<5x5xi32> {
+    %0 = stablehlo.pad %arg0, %arg1, low = [0, 1], high = [2, 1], interior = [1, 0] : (tensor<2x3xi32>, tensor<i32>) -> tensor<5x5xi32>
+    return %0 : tensor<5x5xi32>
+  }
+}""",
+    "concatenate": """module {
+  func.func @main(%arg0: tensor<3x2xi64>, %arg1: tensor<1x2xi64>) -> tensor<4x2xi64> {
+    %0 = stablehlo.concatenate %arg0, %arg1, dim = 0 : (tensor<3x2xi64>, tensor<1x2xi64>) -> tensor<4x2xi64>
+    return %0 : tensor<4x2xi64>
+  }
+}""",
+    "slice": """module {
+  func.func @main(%arg0: tensor<3x4x5xi32>) -> tensor<2x2x3xi32> {
+    %0 = stablehlo.slice %arg0 [0:2, 1:3, 0:5:2] : (tensor<3x4x5xi32>) -> tensor<2x2x3xi32>
+    return %0 : tensor<2x2x3xi32>
+  }
+}""",
     # README.md example (programs.rs test program shape) with the reduce region form and generic syntax
     "generic_forms": """module @jit_f attributes {mhlo.num_partitions = 1 : i32} {
   func.func public @main(%arg0: tensor<4x8xf32> {mhlo.sharding = "{replicated}"}) -> (tensor<4xf32> {jax.result_info = ""}) {
@@ -292,6 +311,50 @@ def test_device_assignment_proto_decoding():
         assert pjrt.DeviceAssignment.decode(data) == pjrt.DeviceAssignment(2, 1, [3, 5])
     with pytest.raises(pjrt.PjrtError):
         pjrt.DeviceAssignment.decode(bytes([0x08, 2, 0x10, 1, 0x1a, 3, 0x0a, 1, 3]))  # one id for two replicas
+
+
+def test_slice_concatenate_pad_plans(compile_client):
+    # a slice is a view (no step of its own: the slice of a parameter feeding an add is one elementwise step, and a
+    # bf16 slice feeding a dot is read by the GEMM in place); concatenate writes each operand's expression into its
+    # region (one step per operand); pad is a fill plus one strided write
+    prog = """module {
+  func.func @main(%arg0: tensor<8x16xf32>, %arg1: tensor<8x16xf32>, %arg2: tensor<f32>) -> (tensor<8x8xf32>, tensor<8x40xf32>, tensor<12x17xf32>) {
+    %0 = stablehlo.slice %arg0 [0:8, 4:12] : (tensor<8x16xf32>) -> tensor<8x8xf32>
+    %1 = stablehlo.slice %arg1 [0:8, 0:16:2] : (tensor<8x16xf32>) -> tensor<8x8xf32>
+    %2 = stablehlo.add %0, %1 : tensor<8x8xf32>
+    %3 = stablehlo.negate %arg1 : tensor<8x16xf32>
+    %4 = stablehlo.concatenate %3, %2, %arg0, dim = 1 : (tensor<8x16xf32>, tensor<8x8xf32>, tensor<8x16xf32>) -> tensor<8x40xf32>
+    %5 = stablehlo.pad %arg0, %arg2, low = [1, -1], high = [3, 2], interior = [0, 0] : (tensor<8x16xf32>, tensor<f32>) -> tensor<12x17xf32>
+    return %2, %4, %5 : tensor<8x8xf32>, tensor<8x40xf32>, tensor<12x17xf32>
+  }
+}"""
+    with pytest.raises(pjrt.PjrtError) as e:  # 12x17 is the pad's shape; 11x18 is not
+        compile_client.compile(pjrt.Program.mlir(prog.replace("tensor<12x17xf32>", "tensor<11x18xf32>")))
+    assert e.value.code == pjrt.ErrorCode.INVALID_ARGUMENT
+    exe, kinds = _plan(compile_client, prog)
+    assert kinds.count("elementwise") == 1
+    assert kinds.count("concatenate") == 3
+    assert kinds.count("pad_fill") == 1 and kinds.count("pad") == 1
+    dot = """module {
+  func.func @main(%arg0: tensor<64x256xbf16>, %arg1: tensor<128x64xbf16>) -> tensor<64x64xf32> {
+    %0 = stablehlo.slice %arg0 [0:64, 128:256] : (tensor<64x256xbf16>) -> tensor<64x128xbf16>
+    %1 = stablehlo.dot_general %0, %arg1, contracting_dims = [1] x [0] : (tensor<64x128xbf16>, tensor<128x64xbf16>) -> tensor<64x64xf32>
+    return %1 : tensor<64x64xf32>
+  }
+}"""
+    _, kinds = _plan(compile_client, dot)
+    assert len(kinds) == 1 and kinds[0].startswith("gemm"), kinds
+
+
+@pytest.mark.parametrize("bad", [
+    ("slice %arg0 [0:2, 1:3, 0:5:2]", "slice %arg0 [0:2, 1:5, 0:5:2]"),      # limit past the dimension
+    ("slice %arg0 [0:2, 1:3, 0:5:2]", "slice %arg0 [0:2, 1:3, 0:5:0]"),      # zero stride
+    ("slice %arg0 [0:2, 1:3, 0:5:2]", "slice %arg0 [0:2, 1:3]"),             # one entry per dimension
+])
+def test_slice_validation_errors(compile_client, bad):
+    with pytest.raises(pjrt.PjrtError) as e:
+        compile_client.compile(pjrt.Program.mlir(GOLDENS["slice"].replace(*bad)))
+    assert e.value.code == pjrt.ErrorCode.INVALID_ARGUMENT
 
 
 def test_attention_not_fused_when_intermediate_escapes(compile_client):
