@@ -1058,6 +1058,75 @@ typedef struct PJRT_LoadedExecutable_Execute_Args {
 } PJRT_LoadedExecutable_Execute_Args;
 typedef PJRT_Error* PJRT_LoadedExecutable_Execute(PJRT_LoadedExecutable_Execute_Args* args);
 
+/* ---------------------------------------------------------------- layouts extension (extensions/layouts.rs:590-808) */
+/* Version 4 (PJRT_API_LAYOUTS_EXTENSION_VERSION, layouts.rs:599), type PJRT_Extension_Type_Layouts. Layouts returned
+ * by Client_GetDefaultLayout and Buffer_MemoryLayout belong to the caller (MemoryLayout_Destroy); those returned by
+ * the executable functions belong to the executable (layouts.rs:245-290 marks them borrowed). */
+typedef struct PJRT_Layouts_MemoryLayout PJRT_Layouts_MemoryLayout;
+typedef struct PJRT_Layouts_SerializedLayout PJRT_Layouts_SerializedLayout;
+
+typedef struct PJRT_Layouts_MemoryLayout_Destroy_Args {
+  PJRT_ARGS_HEAD;
+  PJRT_Layouts_MemoryLayout* layout;
+} PJRT_Layouts_MemoryLayout_Destroy_Args;
+typedef PJRT_Error* PJRT_Layouts_MemoryLayout_Destroy(PJRT_Layouts_MemoryLayout_Destroy_Args* args);
+
+typedef struct PJRT_Layouts_MemoryLayout_Serialize_Args {
+  PJRT_ARGS_HEAD;
+  PJRT_Layouts_MemoryLayout* layout;
+  const char* serialized_bytes;                      /* out */
+  size_t serialized_bytes_size;                      /* out */
+  PJRT_Layouts_SerializedLayout* serialized_layout;  /* out */
+  void (*serialized_layout_deleter)(PJRT_Layouts_SerializedLayout* s_layout); /* out */
+} PJRT_Layouts_MemoryLayout_Serialize_Args;
+typedef PJRT_Error* PJRT_Layouts_MemoryLayout_Serialize(PJRT_Layouts_MemoryLayout_Serialize_Args* args);
+
+typedef struct PJRT_Layouts_PJRT_Client_GetDefaultLayout_Args {
+  PJRT_ARGS_HEAD;
+  PJRT_Client* client;
+  PJRT_Buffer_Type element_type;
+  const int64_t* dims;
+  size_t num_dims;
+  PJRT_Layouts_MemoryLayout* layout; /* out */
+} PJRT_Layouts_PJRT_Client_GetDefaultLayout_Args;
+typedef PJRT_Error* PJRT_Layouts_PJRT_Client_GetDefaultLayout(PJRT_Layouts_PJRT_Client_GetDefaultLayout_Args* args);
+
+typedef struct PJRT_Layouts_PJRT_Buffer_MemoryLayout_Args {
+  PJRT_ARGS_HEAD;
+  PJRT_Buffer* buffer;
+  PJRT_Layouts_MemoryLayout* layout; /* out */
+} PJRT_Layouts_PJRT_Buffer_MemoryLayout_Args;
+typedef PJRT_Error* PJRT_Layouts_PJRT_Buffer_MemoryLayout(PJRT_Layouts_PJRT_Buffer_MemoryLayout_Args* args);
+
+typedef struct PJRT_Layouts_PJRT_Executable_GetOutputLayouts_Args {
+  PJRT_ARGS_HEAD;
+  PJRT_Executable* executable;
+  size_t num_outputs;                    /* out */
+  PJRT_Layouts_MemoryLayout** layouts;   /* out */
+} PJRT_Layouts_PJRT_Executable_GetOutputLayouts_Args;
+typedef PJRT_Error* PJRT_Layouts_PJRT_Executable_GetOutputLayouts(PJRT_Layouts_PJRT_Executable_GetOutputLayouts_Args* args);
+
+typedef struct PJRT_Layouts_PJRT_Executable_GetParameterLayouts_Args {
+  PJRT_ARGS_HEAD;
+  PJRT_Executable* executable;
+  size_t num_parameters;                 /* out */
+  PJRT_Layouts_MemoryLayout** layouts;   /* out */
+} PJRT_Layouts_PJRT_Executable_GetParameterLayouts_Args;
+typedef PJRT_Error* PJRT_Layouts_PJRT_Executable_GetParameterLayouts(
+    PJRT_Layouts_PJRT_Executable_GetParameterLayouts_Args* args);
+
+#define PJRT_API_LAYOUTS_EXTENSION_VERSION 4
+typedef struct PJRT_Layouts_Extension {
+  PJRT_Extension_Base base;
+  PJRT_Layouts_MemoryLayout_Destroy* PJRT_Layouts_MemoryLayout_Destroy;
+  PJRT_Layouts_MemoryLayout_Serialize* PJRT_Layouts_MemoryLayout_Serialize;
+  PJRT_Layouts_PJRT_Client_GetDefaultLayout* PJRT_Layouts_PJRT_Client_GetDefaultLayout;
+  PJRT_Layouts_PJRT_Buffer_MemoryLayout* PJRT_Layouts_PJRT_Buffer_MemoryLayout;
+  PJRT_Unimplemented_Fn PJRT_Layouts_PJRT_Topology_GetDefaultLayout; /* no topology descriptions */
+  PJRT_Layouts_PJRT_Executable_GetOutputLayouts* PJRT_Layouts_PJRT_Executable_GetOutputLayouts;
+  PJRT_Layouts_PJRT_Executable_GetParameterLayouts* PJRT_Layouts_PJRT_Executable_GetParameterLayouts;
+} PJRT_Layouts_Extension;
+
 /* ---------------------------------------------------------------- the table (lib.rs:214-364) */
 #define PJRT_SLOT(name) name* name
 #define PJRT_NOSLOT(name) PJRT_Unimplemented_Fn name
@@ -1243,6 +1312,11 @@ PJRT_ASSERT(sizeof(PJRT_Device_MemoryStats_Args) == 192, "PJRT_Device_MemoryStat
 PJRT_ASSERT(sizeof(PJRT_Executable_OutputDimensions_Args) == 48, "PJRT_Executable_OutputDimensions_Args");
 PJRT_ASSERT(sizeof(PJRT_Executable_GetCompileOptions_Args) == 56, "PJRT_Executable_GetCompileOptions_Args");
 PJRT_ASSERT(sizeof(PJRT_Executable_Serialize_Args) == 56, "PJRT_Executable_Serialize_Args");
+PJRT_ASSERT(sizeof(PJRT_Layouts_Extension) == 24 + 7 * 8, "PJRT_Layouts_Extension");
+PJRT_ASSERT(sizeof(PJRT_Layouts_PJRT_Client_GetDefaultLayout_Args) == 56, "PJRT_Layouts_PJRT_Client_GetDefaultLayout_Args");
+PJRT_ASSERT(offsetof(PJRT_Layouts_PJRT_Client_GetDefaultLayout_Args, dims) == 32, "GetDefaultLayout.dims");
+PJRT_ASSERT(sizeof(PJRT_Layouts_MemoryLayout_Serialize_Args) == 56, "PJRT_Layouts_MemoryLayout_Serialize_Args");
+PJRT_ASSERT(sizeof(PJRT_Layouts_PJRT_Executable_GetOutputLayouts_Args) == 40, "GetOutputLayouts_Args");
 PJRT_ASSERT(sizeof(PJRT_Executable_DeserializeAndLoad_Args) == 64, "PJRT_Executable_DeserializeAndLoad_Args");
 PJRT_ASSERT(offsetof(PJRT_Executable_DeserializeAndLoad_Args, loaded_executable) == 40,
             "PJRT_Executable_DeserializeAndLoad_Args.loaded_executable");

@@ -1030,8 +1030,75 @@ PJRT_Error* Ext_DescribePlan(PJRT_LoadedExecutable* executable, const char** tex
   API_CATCH
 }
 
+// ------------------------------------------------------------------------------------------------ layouts extension
+// Buffers are dense and row-major: every layout is {rank-1, ..., 0} with no tiles, written as XLA prints a layout.
+PJRT_Error* Layouts_MemoryLayout_Destroy(PJRT_Layouts_MemoryLayout_Destroy_Args* args) {
+  NEED_ARGS(PJRT_Layouts_MemoryLayout_Destroy_Args, layout);
+  delete from<MemoryLayout>(args->layout);
+  return nullptr;
+}
+PJRT_Error* Layouts_MemoryLayout_Serialize(PJRT_Layouts_MemoryLayout_Serialize_Args* args) {
+  NEED_ARGS(PJRT_Layouts_MemoryLayout_Serialize_Args, serialized_layout_deleter);
+  NEED(args->layout, "layout");
+  const MemoryLayout* l = from<MemoryLayout>(args->layout);
+  auto* text = new std::string("{");
+  for (size_t i = 0; i < l->minor_to_major.size(); ++i) *text += (i ? "," : "") + std::to_string(l->minor_to_major[i]);
+  *text += "}";
+  args->serialized_bytes = text->data();
+  args->serialized_bytes_size = text->size();
+  args->serialized_layout = reinterpret_cast<PJRT_Layouts_SerializedLayout*>(text);
+  args->serialized_layout_deleter = [](PJRT_Layouts_SerializedLayout* p) { delete reinterpret_cast<std::string*>(p); };
+  return nullptr;
+}
+PJRT_Error* Layouts_Client_GetDefaultLayout(PJRT_Layouts_PJRT_Client_GetDefaultLayout_Args* args) {
+  NEED_ARGS(PJRT_Layouts_PJRT_Client_GetDefaultLayout_Args, layout);
+  NEED(args->client, "client");
+  if (args->num_dims && !args->dims) return make_pjrt_error(PJRT_Error_Code_INVALID_ARGUMENT, "dims is null");
+  for (size_t i = 0; i < args->num_dims; ++i)
+    if (args->dims[i] < 0) return make_pjrt_error(PJRT_Error_Code_INVALID_ARGUMENT, "negative dimension");
+  auto* l = new MemoryLayout();
+  for (size_t i = 0; i < args->num_dims; ++i) l->minor_to_major.push_back((int64_t)(args->num_dims - 1 - i));
+  args->layout = to<PJRT_Layouts_MemoryLayout>(l);
+  return nullptr;
+}
+PJRT_Error* Layouts_Buffer_MemoryLayout(PJRT_Layouts_PJRT_Buffer_MemoryLayout_Args* args) {
+  NEED_ARGS(PJRT_Layouts_PJRT_Buffer_MemoryLayout_Args, layout);
+  NEED(args->buffer, "buffer");
+  auto* l = new MemoryLayout();
+  l->minor_to_major = buf(args->buffer)->minor_to_major;
+  args->layout = to<PJRT_Layouts_MemoryLayout>(l);
+  return nullptr;
+}
+PJRT_Error* Layouts_Executable_GetOutputLayouts(PJRT_Layouts_PJRT_Executable_GetOutputLayouts_Args* args) {
+  NEED_ARGS(PJRT_Layouts_PJRT_Executable_GetOutputLayouts_Args, layouts);
+  NEED(args->executable, "executable");
+  auto& e = exe_of(args->executable);
+  args->num_outputs = e.output_layout_ptrs.size();
+  args->layouts = reinterpret_cast<PJRT_Layouts_MemoryLayout**>(e.output_layout_ptrs.data());
+  return nullptr;
+}
+PJRT_Error* Layouts_Executable_GetParameterLayouts(PJRT_Layouts_PJRT_Executable_GetParameterLayouts_Args* args) {
+  NEED_ARGS(PJRT_Layouts_PJRT_Executable_GetParameterLayouts_Args, layouts);
+  NEED(args->executable, "executable");
+  auto& e = exe_of(args->executable);
+  args->num_parameters = e.param_layout_ptrs.size();
+  args->layouts = reinterpret_cast<PJRT_Layouts_MemoryLayout**>(e.param_layout_ptrs.data());
+  return nullptr;
+}
+
+PJRT_Layouts_Extension g_layouts_extension = {
+    {sizeof(PJRT_Layouts_Extension), PJRT_Extension_Type_Layouts, nullptr},
+    Layouts_MemoryLayout_Destroy,
+    Layouts_MemoryLayout_Serialize,
+    Layouts_Client_GetDefaultLayout,
+    Layouts_Buffer_MemoryLayout,
+    nullptr,
+    Layouts_Executable_GetOutputLayouts,
+    Layouts_Executable_GetParameterLayouts,
+};
+
 RYFT_MI355X_Extension g_extension = {
-    {sizeof(RYFT_MI355X_Extension), (PJRT_Extension_Type)RYFT_MI355X_EXTENSION_TYPE, nullptr},
+    {sizeof(RYFT_MI355X_Extension), (PJRT_Extension_Type)RYFT_MI355X_EXTENSION_TYPE, &g_layouts_extension.base},
     Ext_SetKernelTiming,
     Ext_KernelTiming,
     Ext_DescribePlan,

@@ -477,6 +477,19 @@ std::shared_ptr<Executable> compile_program(Client* c, const std::string& code, 
     exe->output_memory_kinds.push_back(kDevice);
     exe->output_memory_kind_sizes.push_back(6);
   }
+  auto row_major_layout = [](size_t rank) {
+    auto l = std::make_unique<MemoryLayout>();
+    for (size_t i = 0; i < rank; ++i) l->minor_to_major.push_back((int64_t)(rank - 1 - i));
+    return l;
+  };
+  for (auto& t : exe->plan.param_types) {
+    exe->param_layouts.push_back(row_major_layout(t.shape.size()));
+    exe->param_layout_ptrs.push_back(exe->param_layouts.back().get());
+  }
+  for (auto& t : exe->plan.output_types) {
+    exe->output_layouts.push_back(row_major_layout(t.shape.size()));
+    exe->output_layout_ptrs.push_back(exe->output_layouts.back().get());
+  }
   for (size_t i = 0; i < exe->plan.param_types.size(); ++i) {
     static const char* kDevice = "device";
     exe->param_memory_kinds.push_back(kDevice);

@@ -140,6 +140,10 @@ struct Buffer {  // PJRT_Buffer
 };
 
 // ------------------------------------------------------------------------------------------------ executables
+struct MemoryLayout {  // PJRT_Layouts_MemoryLayout: dense, untiled
+  std::vector<int64_t> minor_to_major;
+};
+
 struct Executable {  // PJRT_Executable (shared by the loaded executable and every view handed out)
   std::string name;
   std::string fingerprint;
@@ -153,6 +157,9 @@ struct Executable {  // PJRT_Executable (shared by the loaded executable and eve
   std::vector<size_t> output_memory_kind_sizes;
   std::vector<const char*> param_memory_kinds;
   std::vector<size_t> param_memory_kind_sizes;
+  // row-major layouts of the parameters and results, owned here (the layouts extension lends them out)
+  std::vector<std::unique_ptr<MemoryLayout>> param_layouts, output_layouts;
+  std::vector<MemoryLayout*> param_layout_ptrs, output_layout_ptrs;
   std::vector<PJRT_NamedValue> cost_properties;
   std::vector<std::shared_ptr<DeviceMem>> constants;  // by slot (null for non-constant slots)
 };

@@ -309,6 +309,77 @@ class _RyftExtension(C.Structure):
                 ("describe_plan", C.CFUNCTYPE(_vp, _vp, C.POINTER(_vp), C.POINTER(_sz)))]
 
 
+PJRT_EXTENSION_TYPE_LAYOUTS = 4
+_LAYOUT_ARGS = {
+    "PJRT_Layouts_MemoryLayout_Destroy": [("layout", _vp)],
+    "PJRT_Layouts_MemoryLayout_Serialize": [("layout", _vp), ("serialized_bytes", _vp), ("serialized_bytes_size", _sz),
+                                            ("serialized_layout", _vp),
+                                            ("serialized_layout_deleter", C.CFUNCTYPE(None, _vp))],
+    "PJRT_Layouts_PJRT_Client_GetDefaultLayout": [("client", _vp), ("element_type", C.c_uint),
+                                                  ("dims", C.POINTER(C.c_int64)), ("num_dims", _sz), ("layout", _vp)],
+    "PJRT_Layouts_PJRT_Buffer_MemoryLayout": [("buffer", _vp), ("layout", _vp)],
+    "PJRT_Layouts_PJRT_Executable_GetOutputLayouts": [("executable", _vp), ("num_outputs", _sz),
+                                                      ("layouts", C.POINTER(_vp))],
+    "PJRT_Layouts_PJRT_Executable_GetParameterLayouts": [("executable", _vp), ("num_parameters", _sz),
+                                                         ("layouts", C.POINTER(_vp))],
+}
+for _n, _f in _LAYOUT_ARGS.items():
+    A[_n] = _args(_n + "_Args", _f)
+# the extension's function table after its PJRT_Extension_Base (extensions/layouts.rs:798-807)
+_LAYOUT_SLOTS = ["PJRT_Layouts_MemoryLayout_Destroy", "PJRT_Layouts_MemoryLayout_Serialize",
+                 "PJRT_Layouts_PJRT_Client_GetDefaultLayout", "PJRT_Layouts_PJRT_Buffer_MemoryLayout",
+                 "PJRT_Layouts_PJRT_Topology_GetDefaultLayout", "PJRT_Layouts_PJRT_Executable_GetOutputLayouts",
+                 "PJRT_Layouts_PJRT_Executable_GetParameterLayouts"]
+
+
+class LayoutsExtension:
+    """PJRT_Layouts_Extension (extensions/layouts.rs:20-60): calls go through its own function table."""
+
+    def __init__(self, api: "Api", address: int):
+        self.api, self.address = api, address
+        self.struct_size = C.c_size_t.from_address(address).value
+
+    def call(self, name: str, **kw):
+        off = 24 + 8 * _LAYOUT_SLOTS.index(name)
+        fp = C.c_void_p.from_address(self.address + off).value if self.struct_size >= off + 8 else None
+        if not fp:
+            raise PjrtError(ErrorCode.UNIMPLEMENTED, f"{name} is not implemented by the loaded plugin")
+        args = self.api.new_args(name, **kw)
+        err = self.api.error(C.CFUNCTYPE(_vp, _vp)(fp)(C.addressof(args)))
+        if err is not None:
+            raise err
+        return args
+
+
+class Layout:
+    """A PJRT memory layout (extensions/layouts.rs:95-195); borrowed ones belong to their executable."""
+
+    def __init__(self, ext: LayoutsExtension, handle: int, borrowed: bool):
+        if not handle:
+            raise PjrtError(ErrorCode.INVALID_ARGUMENT, "the provided PJRT layout handle is a null pointer")
+        self.ext, self.handle, self.borrowed = ext, handle, borrowed
+
+    def serialize(self) -> str:
+        a = self.ext.call("PJRT_Layouts_MemoryLayout_Serialize", layout=self.handle)
+        text = _str(a.serialized_bytes, a.serialized_bytes_size)
+        a.serialized_layout_deleter(a.serialized_layout)
+        return text
+
+    def __eq__(self, other) -> bool:
+        return isinstance(other, Layout) and self.serialize() == other.serialize()
+
+    def __repr__(self) -> str:
+        return f"Layout[{self.serialize()}]"
+
+    def __del__(self):
+        try:
+            if self.handle and not self.borrowed:
+                self.ext.call("PJRT_Layouts_MemoryLayout_Destroy", layout=self.handle)
+                self.handle = None
+        except Exception:
+            pass
+
+
 def _str(ptr, size) -> str:
     if not ptr or size == 0:
         return ""
@@ -397,6 +468,12 @@ class Api:
                 return p
             p = C.cast(base.next, C.c_void_p).value
         return None
+
+    def layouts_extension(self) -> LayoutsExtension:
+        p = self.extension(PJRT_EXTENSION_TYPE_LAYOUTS)
+        if not p:
+            raise PjrtError(ErrorCode.UNIMPLEMENTED, "the loaded plugin has no layouts extension")
+        return LayoutsExtension(self, p)
 
     def attributes(self) -> Dict[str, object]:
         a = self.call("PJRT_Plugin_Attributes")
@@ -600,6 +677,10 @@ class Buffer:
 
     def ready_event(self) -> Event:
         return Event(self.api, self.api.call("PJRT_Buffer_ReadyEvent", buffer=self.handle).event)
+
+    def memory_layout(self) -> Layout:
+        ext = self.api.layouts_extension()
+        return Layout(ext, ext.call("PJRT_Layouts_PJRT_Buffer_MemoryLayout", buffer=self.handle).layout, False)
 
     def copy_to_host(self) -> Event:
         """ToHostBuffer twice: size query with dst=null, then the copy (buffers.rs:1237-1266)."""
@@ -821,6 +902,17 @@ class Executable:
         a.serialized_executable_deleter(a.serialized_executable)
         return data
 
+    def input_layouts(self) -> List[Layout]:
+        """Executable::input_layouts (extensions/layouts.rs:245-263): borrowed from the executable."""
+        ext = self.api.layouts_extension()
+        a = ext.call("PJRT_Layouts_PJRT_Executable_GetParameterLayouts", executable=self.handle)
+        return [Layout(ext, a.layouts[i], True) for i in range(a.num_parameters)]
+
+    def output_layouts(self) -> List[Layout]:
+        ext = self.api.layouts_extension()
+        a = ext.call("PJRT_Layouts_PJRT_Executable_GetOutputLayouts", executable=self.handle)
+        return [Layout(ext, a.layouts[i], True) for i in range(a.num_outputs)]
+
     def memory_statistics(self) -> Dict[str, int]:
         """Executable::memory_statistics (programs.rs:318-360)."""
         a = self.api.call("PJRT_Executable_GetCompiledMemoryStats", executable=self.handle)
@@ -1036,6 +1128,14 @@ class Client:
                           overridden_serialized_compile_options=C.cast(ob, _vp) if opts else None,
                           overridden_serialized_compile_options_size=len(opts))
         return LoadedExecutable(self, a.loaded_executable)
+
+    def default_layout(self, element_type: BufferType, dims: Sequence[int]) -> Layout:
+        """Client::default_layout (extensions/layouts.rs:198-217)."""
+        ext = self.api.layouts_extension()
+        d = (C.c_int64 * max(len(dims), 1))(*dims)
+        a = ext.call("PJRT_Layouts_PJRT_Client_GetDefaultLayout", client=self.handle, element_type=int(element_type),
+                     dims=d, num_dims=len(dims))
+        return Layout(ext, a.layout, False)
 
     def execution_context(self) -> "ExecutionContext":
         return ExecutionContext(self.api, self.api.call("PJRT_ExecuteContext_Create").context)

@@ -82,3 +82,15 @@ def test_copy_raw_to_host_ranges(gpu_client):
     with pytest.raises(pjrt.PjrtError) as e:
         b.copy_raw_to_host(4)
     assert e.value.code == pjrt.ErrorCode.FAILED_PRECONDITION
+
+
+def test_buffer_memory_layout(gpu_client):
+    # buffers are dense row-major; the layout handed out is the caller's (destroyed when dropped)
+    dev = gpu_client.addressable_devices()[0]
+    for dims in [(3, 4, 5), (7,), ()]:
+        x = np.zeros(dims, np.float32)
+        b = gpu_client.buffer(x, pjrt.BufferType.F32, dims, device=dev)
+        layout = b.memory_layout()
+        assert layout.serialize() == "{" + ",".join(str(len(dims) - 1 - i) for i in range(len(dims))) + "}"
+        assert not layout.borrowed
+        assert layout == gpu_client.default_layout(pjrt.BufferType.F32, list(dims))

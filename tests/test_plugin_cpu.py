@@ -65,7 +65,43 @@ def test_plugin_attributes(plugin):
 
 def test_extension_chain(plugin):
     assert plugin.api().extension(pjrt.RYFT_MI355X_EXTENSION_TYPE) is not None
-    assert plugin.api().extension(4) is None  # no layouts extension: ryft-pjrt reports Unimplemented
+    assert plugin.api().extension(pjrt.PJRT_EXTENSION_TYPE_LAYOUTS) is not None
+    assert plugin.api().extension(6) is None  # no memory-descriptions extension: ryft-pjrt reports Unimplemented
+
+
+def test_layouts_extension_default_layouts(compile_client):
+    # as ryft-pjrt's test_layout (extensions/layouts.rs:829-841): the default layout of an f32 [2, 3, 4] buffer is
+    # the dense row-major {2,1,0}, and equal layouts serialize equally
+    layout = compile_client.default_layout(pjrt.BufferType.F32, [2, 3, 4])
+    assert layout.serialize() == "{2,1,0}"
+    assert repr(layout) == "Layout[{2,1,0}]"
+    assert layout == compile_client.default_layout(pjrt.BufferType.BF16, [7, 1, 9])
+    assert compile_client.default_layout(pjrt.BufferType.S32, []).serialize() == "{}"
+    assert compile_client.default_layout(pjrt.BufferType.S8, [5]).serialize() == "{0}"
+    with pytest.raises(pjrt.PjrtError) as e:
+        compile_client.default_layout(pjrt.BufferType.F32, [2, -1])
+    assert e.value.code == pjrt.ErrorCode.INVALID_ARGUMENT
+
+
+def test_layouts_extension_executable_layouts(compile_client):
+    # ryft-pjrt's test_executable_layouts (extensions/layouts.rs:944-1000): two [2, 1] i32 parameters and one result,
+    # all {1,0}; the layouts belong to the executable (borrowed, never destroyed by the caller)
+    e = compile_client.compile(pjrt.Program.mlir(ADD_2X1)).executable()
+    ins, outs = e.input_layouts(), e.output_layouts()
+    assert [x.serialize() for x in ins] == ["{1,0}", "{1,0}"]
+    assert len(outs) == e.output_count() and [x.serialize() for x in outs] == ["{1,0}"]
+    assert all(x.borrowed for x in ins + outs)
+    e2 = compile_client.compile(pjrt.Program.mlir(configs.c4_causal_attention(b=1, h=2, s=128).program)).executable()
+    assert [x.serialize() for x in e2.input_layouts()] == ["{3,2,1,0}"] * 3
+
+
+ADD_2X1 = """module {
+  func.func @main(%arg0: tensor<2x1xi32>, %arg1: tensor<2x1xi32>) -> tensor<2x1xi32> {
+    %0 = stablehlo.add %arg0, %arg1 : tensor<2x1xi32>
+    return %0 : tensor<2x1xi32>
+  }
+}
+"""
 
 
 def test_compile_only_client(compile_client):
