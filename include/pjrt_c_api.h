@@ -1127,6 +1127,35 @@ typedef struct PJRT_Layouts_Extension {
   PJRT_Layouts_PJRT_Executable_GetParameterLayouts* PJRT_Layouts_PJRT_Executable_GetParameterLayouts;
 } PJRT_Layouts_Extension;
 
+/* ---------------------------------------------------------------- memory descriptions extension
+ * (extensions/memory_descriptions.rs:209-285; version 1, type PJRT_Extension_Type_MemoryDescriptions) */
+typedef struct PJRT_MemoryDescription PJRT_MemoryDescription;
+
+typedef struct PJRT_DeviceDescription_MemoryDescriptions_Args {
+  PJRT_ARGS_HEAD;
+  PJRT_DeviceDescription* device_description;
+  const PJRT_MemoryDescription* const* memory_descriptions; /* out, owned by the description */
+  size_t num_memory_descriptions;                           /* out */
+  ptrdiff_t default_memory_index;                           /* out; -1: none */
+} PJRT_DeviceDescription_MemoryDescriptions_Args;
+typedef PJRT_Error* PJRT_DeviceDescription_MemoryDescriptions(PJRT_DeviceDescription_MemoryDescriptions_Args* args);
+
+typedef struct PJRT_MemoryDescription_Kind_Args {
+  PJRT_ARGS_HEAD;
+  const PJRT_MemoryDescription* memory_description;
+  const char* kind;  /* out */
+  size_t kind_size;  /* out */
+  int kind_id;       /* out */
+} PJRT_MemoryDescription_Kind_Args;
+typedef PJRT_Error* PJRT_MemoryDescription_Kind(PJRT_MemoryDescription_Kind_Args* args);
+
+#define PJRT_API_MEMORY_DESCRIPTIONS_EXTENSION_VERSION 1
+typedef struct PJRT_MemoryDescriptions_Extension {
+  PJRT_Extension_Base base;
+  PJRT_DeviceDescription_MemoryDescriptions* PJRT_DeviceDescription_MemoryDescriptions;
+  PJRT_MemoryDescription_Kind* PJRT_MemoryDescription_Kind;
+} PJRT_MemoryDescriptions_Extension;
+
 /* ---------------------------------------------------------------- the table (lib.rs:214-364) */
 #define PJRT_SLOT(name) name* name
 #define PJRT_NOSLOT(name) PJRT_Unimplemented_Fn name
@@ -1313,6 +1342,9 @@ PJRT_ASSERT(sizeof(PJRT_Executable_OutputDimensions_Args) == 48, "PJRT_Executabl
 PJRT_ASSERT(sizeof(PJRT_Executable_GetCompileOptions_Args) == 56, "PJRT_Executable_GetCompileOptions_Args");
 PJRT_ASSERT(sizeof(PJRT_Executable_Serialize_Args) == 56, "PJRT_Executable_Serialize_Args");
 PJRT_ASSERT(sizeof(PJRT_Layouts_Extension) == 24 + 7 * 8, "PJRT_Layouts_Extension");
+PJRT_ASSERT(sizeof(PJRT_MemoryDescriptions_Extension) == 24 + 2 * 8, "PJRT_MemoryDescriptions_Extension");
+PJRT_ASSERT(sizeof(PJRT_DeviceDescription_MemoryDescriptions_Args) == 48, "MemoryDescriptions_Args");
+PJRT_ASSERT(sizeof(PJRT_MemoryDescription_Kind_Args) == 48, "PJRT_MemoryDescription_Kind_Args");
 PJRT_ASSERT(sizeof(PJRT_Layouts_PJRT_Client_GetDefaultLayout_Args) == 56, "PJRT_Layouts_PJRT_Client_GetDefaultLayout_Args");
 PJRT_ASSERT(offsetof(PJRT_Layouts_PJRT_Client_GetDefaultLayout_Args, dims) == 32, "GetDefaultLayout.dims");
 PJRT_ASSERT(sizeof(PJRT_Layouts_MemoryLayout_Serialize_Args) == 56, "PJRT_Layouts_MemoryLayout_Serialize_Args");

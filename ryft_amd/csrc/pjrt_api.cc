@@ -494,9 +494,12 @@ PJRT_Error* Memory_Kind(PJRT_Memory_Kind_Args* args) {
   args->kind_size = m->kind.size();
   return nullptr;
 }
+// The id XLA's PJRT plugins report for the "device" memory kind (ryft-pjrt's memories.rs:354 pins it).
+constexpr int kDeviceMemoryKindId = 42097224;
+
 PJRT_Error* Memory_Kind_Id(PJRT_Memory_Kind_Id_Args* args) {
   NEED_ARGS(PJRT_Memory_Kind_Id_Args, kind_id);
-  args->kind_id = 0;
+  args->kind_id = kDeviceMemoryKindId;
   return nullptr;
 }
 PJRT_Error* Memory_DebugString(PJRT_Memory_DebugString_Args* args) {
@@ -1086,8 +1089,41 @@ PJRT_Error* Layouts_Executable_GetParameterLayouts(PJRT_Layouts_PJRT_Executable_
   return nullptr;
 }
 
+// ------------------------------------------------------------------------------------------------ memory descriptions
+// Every device has one memory, HBM, of kind "device"; it is the default.
+struct MemoryDescriptionObj {
+  const char* kind;
+  int kind_id;
+};
+const MemoryDescriptionObj g_device_memory_description = {"device", kDeviceMemoryKindId};
+const MemoryDescriptionObj* const g_memory_descriptions[1] = {&g_device_memory_description};
+
+PJRT_Error* MemDesc_DeviceDescription_MemoryDescriptions(PJRT_DeviceDescription_MemoryDescriptions_Args* args) {
+  NEED_ARGS(PJRT_DeviceDescription_MemoryDescriptions_Args, default_memory_index);
+  NEED(args->device_description, "device_description");
+  args->memory_descriptions = reinterpret_cast<const PJRT_MemoryDescription* const*>(g_memory_descriptions);
+  args->num_memory_descriptions = 1;
+  args->default_memory_index = 0;
+  return nullptr;
+}
+PJRT_Error* MemDesc_MemoryDescription_Kind(PJRT_MemoryDescription_Kind_Args* args) {
+  NEED_ARGS(PJRT_MemoryDescription_Kind_Args, kind_id);
+  NEED(args->memory_description, "memory_description");
+  auto* d = reinterpret_cast<const MemoryDescriptionObj*>(args->memory_description);
+  args->kind = d->kind;
+  args->kind_size = strlen(d->kind);
+  args->kind_id = d->kind_id;
+  return nullptr;
+}
+
+PJRT_MemoryDescriptions_Extension g_memory_descriptions_extension = {
+    {sizeof(PJRT_MemoryDescriptions_Extension), PJRT_Extension_Type_MemoryDescriptions, nullptr},
+    MemDesc_DeviceDescription_MemoryDescriptions,
+    MemDesc_MemoryDescription_Kind,
+};
+
 PJRT_Layouts_Extension g_layouts_extension = {
-    {sizeof(PJRT_Layouts_Extension), PJRT_Extension_Type_Layouts, nullptr},
+    {sizeof(PJRT_Layouts_Extension), PJRT_Extension_Type_Layouts, &g_memory_descriptions_extension.base},
     Layouts_MemoryLayout_Destroy,
     Layouts_MemoryLayout_Serialize,
     Layouts_Client_GetDefaultLayout,

@@ -220,6 +220,7 @@ for _n, _f in {
     "PJRT_Device_DefaultMemory": [("device", _vp), ("memory", _vp)],
     "PJRT_Memory_Id": [("memory", _vp), ("id", C.c_int)],
     "PJRT_Memory_Kind": [("memory", _vp), ("kind", _vp), ("kind_size", _sz)],
+    "PJRT_Memory_Kind_Id": [("memory", _vp), ("kind_id", C.c_int)],
     "PJRT_Memory_ToString": [("memory", _vp), ("to_string", _vp), ("to_string_size", _sz)],
     "PJRT_Memory_AddressableByDevices": [("memory", _vp), ("devices", C.POINTER(_vp)), ("num_devices", _sz)],
     "PJRT_Executable_Destroy": [("executable", _vp)],
@@ -378,6 +379,29 @@ class Layout:
                 self.handle = None
         except Exception:
             pass
+
+
+PJRT_EXTENSION_TYPE_MEMORY_DESCRIPTIONS = 6
+A["PJRT_DeviceDescription_MemoryDescriptions"] = _args(
+    "PJRT_DeviceDescription_MemoryDescriptions_Args",
+    [("device_description", _vp), ("memory_descriptions", C.POINTER(_vp)), ("num_memory_descriptions", _sz),
+     ("default_memory_index", C.c_ssize_t)])
+A["PJRT_MemoryDescription_Kind"] = _args(
+    "PJRT_MemoryDescription_Kind_Args", [("memory_description", _vp), ("kind", _vp), ("kind_size", _sz),
+                                         ("kind_id", C.c_int)])
+
+
+def _ext_call(api: "Api", address: int, slots: List[str], name: str, **kw):
+    """Call `name` through an extension's function table (the slots after its PJRT_Extension_Base)."""
+    off = 24 + 8 * slots.index(name)
+    fp = C.c_void_p.from_address(address + off).value if C.c_size_t.from_address(address).value >= off + 8 else None
+    if not fp:
+        raise PjrtError(ErrorCode.UNIMPLEMENTED, f"{name} is not implemented by the loaded plugin")
+    args = api.new_args(name, **kw)
+    err = api.error(C.CFUNCTYPE(_vp, _vp)(fp)(C.addressof(args)))
+    if err is not None:
+        raise err
+    return args
 
 
 def _str(ptr, size) -> str:
@@ -558,6 +582,9 @@ class Memory:
         a = self.client.api.call("PJRT_Memory_Kind", memory=self.handle)
         return _str(a.kind, a.kind_size)
 
+    def kind_id(self) -> int:
+        return self.client.api.call("PJRT_Memory_Kind_Id", memory=self.handle).kind_id
+
     def __str__(self) -> str:
         a = self.client.api.call("PJRT_Memory_ToString", memory=self.handle)
         return _str(a.to_string, a.to_string_size)
@@ -583,6 +610,22 @@ class Device:
     def attributes(self) -> Dict[str, object]:
         a = self.client.api.call("PJRT_DeviceDescription_Attributes", device_description=self._desc())
         return _named_values(a.attributes, a.num_attributes)
+
+    def memory_descriptions(self):
+        """DeviceDescription::memory_descriptions (extensions/memory_descriptions.rs:130-205): [(kind, kind_id)] and
+        the index of the default one (None if the plugin names none)."""
+        api = self.client.api
+        p = api.extension(PJRT_EXTENSION_TYPE_MEMORY_DESCRIPTIONS)
+        if not p:
+            raise PjrtError(ErrorCode.UNIMPLEMENTED, "the loaded plugin has no memory descriptions extension")
+        slots = ["PJRT_DeviceDescription_MemoryDescriptions", "PJRT_MemoryDescription_Kind"]
+        a = _ext_call(api, p, slots, "PJRT_DeviceDescription_MemoryDescriptions", device_description=self._desc())
+        out = []
+        for i in range(a.num_memory_descriptions):
+            k = _ext_call(api, p, slots, "PJRT_MemoryDescription_Kind", memory_description=a.memory_descriptions[i])
+            out.append((_str(k.kind, k.kind_size), int(k.kind_id)))
+        idx = a.default_memory_index
+        return out, (idx if 0 <= idx < len(out) else None)
 
     def local_hardware_id(self) -> int:
         return self.client.api.call("PJRT_Device_LocalHardwareId", device=self.handle).local_hardware_id

@@ -94,3 +94,15 @@ def test_buffer_memory_layout(gpu_client):
         assert layout.serialize() == "{" + ",".join(str(len(dims) - 1 - i) for i in range(len(dims))) + "}"
         assert not layout.borrowed
         assert layout == gpu_client.default_layout(pjrt.BufferType.F32, list(dims))
+
+
+def test_device_memory_descriptions(gpu_client):
+    # ryft-pjrt's test_device_memory_descriptions (extensions/memory_descriptions.rs:297-316): non-empty kinds,
+    # non-zero kind ids, a default; the one memory is HBM, kind "device", with the kind id XLA's plugins use for it
+    # (memories.rs:354), the same one Memory_Kind_Id reports
+    device = gpu_client.addressable_devices()[0]
+    descs, default = device.memory_descriptions()
+    assert descs == [("device", 42097224)] and default == 0
+    mem = device.default_memory()
+    assert mem.kind() == "device"
+    assert mem.kind_id() == 42097224

@@ -66,7 +66,8 @@ def test_plugin_attributes(plugin):
 def test_extension_chain(plugin):
     assert plugin.api().extension(pjrt.RYFT_MI355X_EXTENSION_TYPE) is not None
     assert plugin.api().extension(pjrt.PJRT_EXTENSION_TYPE_LAYOUTS) is not None
-    assert plugin.api().extension(6) is None  # no memory-descriptions extension: ryft-pjrt reports Unimplemented
+    assert plugin.api().extension(pjrt.PJRT_EXTENSION_TYPE_MEMORY_DESCRIPTIONS) is not None
+    assert plugin.api().extension(1) is None  # no profiler extension: ryft-pjrt reports Unimplemented
 
 
 def test_layouts_extension_default_layouts(compile_client):
