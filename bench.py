@@ -6,9 +6,13 @@ back to back (async dispatch, like a JAX-style caller) and the timed region ends
 ready; the per-step latency with an await after every execute is reported alongside. Kernel durations come from
 HIP events recorded on the plugin's stream around each launch (the plugin's timing extension), in a separate pass.
 
+The cyclic garbage collector is paused during the timed region (as `timeit` does); the plugin's own work is
+unchanged.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2] [--cpu-seconds 10]
 """
 import argparse
+import gc
 import json
 import os
 import sys
@@ -93,13 +97,19 @@ def main():
     for _ in range(args.warmup):
         step().done.await_()
 
-    # timed region: K steps enqueued back to back, ending when the last one is done
+    # timed region: K steps enqueued back to back, ending when the last one is done. Python's cyclic garbage
+    # collector is paused while the steps are timed (as timeit does): one full collection stalls the enqueueing
+    # thread for about a millisecond, which would be billed to the steps, not to the plugin or its kernels.
+    gc.collect()
+    gc.disable()
     t0 = time.perf_counter()
     last = None
     for _ in range(args.steps):
         last = step()
+    t_enqueued = time.perf_counter()
     last.done.await_()
     elapsed = time.perf_counter() - t0
+    gc.enable()
     ms_per_step = elapsed / args.steps * 1e3
 
     # per-step latency with an await after each execute (the README's call pattern)
@@ -160,6 +170,7 @@ def main():
         "data": "synthetic (seeded splitmix64 inputs with the BASELINE.json distributions)",
         "config": {"workload": w.name, "input_shapes": shapes, "flops_per_step": w.flops,
                    "bytes_per_step": w.bytes, "ms_per_step_await_each": round(ms_sync, 4),
+                   "host_enqueue_us_per_step": round((t_enqueued - t0) / args.steps * 1e6, 2),
                    "pcie_inclusive": {"ms_per_step": round(ms_pcie, 3),
                                       "value": round((w.flops or w.bytes) / (ms_pcie * 1e-3) / (1e12 if w.flops else 1e9), 2),
                                       "steps": pcie_steps,

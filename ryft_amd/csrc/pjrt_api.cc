@@ -171,12 +171,18 @@ PJRT_Error* Event_OnReady(PJRT_Event_OnReady_Args* args) {
   NEED(args->event, "event");
   NEED(args->callback, "callback");
   auto st = from<Event>(args->event)->state;
-  bool run_now = false;
+  bool run_now = false, hand_to_worker = false;
   {
     std::lock_guard<std::mutex> lk(st->mu);
-    if (st->ready) run_now = true;
-    else st->callbacks.push_back({args->callback, args->user_arg});
+    if (st->ready) {
+      run_now = true;
+    } else {
+      st->callbacks.push_back({args->callback, args->user_arg});
+      hand_to_worker = st->lazy_owner && !st->queued;
+      st->queued |= hand_to_worker;
+    }
   }
+  if (hand_to_worker) st->lazy_owner->enqueue_completion(st);
   if (run_now) {
     // each callback receives its own error object; the callee destroys it (events.rs:100-108)
     args->callback(st->code == PJRT_Error_Code_OK ? nullptr : make_pjrt_error(st->code, st->message), args->user_arg);

@@ -9,6 +9,9 @@
 #include <algorithm>
 #include <chrono>
 #include <cstdio>
+#include <cstdlib>
+#include <mutex>
+#include <set>
 #include <sstream>
 
 #include "kernels/kernels.h"
@@ -181,6 +184,8 @@ void PinnedPool::release_now(Chunk* c) {
 }
 
 // ------------------------------------------------------------------------------------------------ client
+static void register_live_client(Client* c);
+
 Client::Client(const std::vector<int>& visible, bool compile_only) {
   if (compile_only) {
     // no device is touched: programs compile to plans (inspectable through the extension) but cannot execute
@@ -264,9 +269,34 @@ Client::Client(const std::vector<int>& visible, bool compile_only) {
       e->wait();
     }
   });
+  register_live_client(this);
 }
 
-Client::~Client() {
+// Clients alive in this process. A host that exits without destroying its clients (a garbage-collected
+// wrapper whose finalizer never ran, for one) would leave each client's completion worker running, possibly
+// inside a HIP call, while the HIP runtime tears itself down at exit. The exit hook below is registered after the
+// first client has initialised HIP, so it runs before the runtime's own exit-time teardown: it stops every live
+// client's worker and drains its streams.
+static std::mutex& live_clients_mu() {
+  static std::mutex m;
+  return m;
+}
+static std::set<Client*>& live_clients() {
+  static std::set<Client*> s;
+  return s;
+}
+static void quiesce_live_clients() {
+  std::lock_guard<std::mutex> lk(live_clients_mu());
+  for (Client* c : live_clients()) c->stop_worker();
+}
+static void register_live_client(Client* c) {
+  static std::once_flag hook;
+  std::lock_guard<std::mutex> lk(live_clients_mu());  // constructs the registry before the hook is registered
+  live_clients().insert(c);
+  std::call_once(hook, [] { std::atexit(quiesce_live_clients); });
+}
+
+void Client::stop_worker() {
   {
     std::lock_guard<std::mutex> lk(q_mu);
     stopping = true;
@@ -277,6 +307,14 @@ Client::~Client() {
     (void)hipSetDevice(d->hip_ordinal);
     (void)hipStreamSynchronize(d->stream);
   }
+}
+
+Client::~Client() {
+  {
+    std::lock_guard<std::mutex> lk(live_clients_mu());
+    live_clients().erase(this);
+  }
+  stop_worker();
   {
     std::lock_guard<std::mutex> lk(prof_mu);
     for (auto& t : timings) {
@@ -663,7 +701,9 @@ EventPtr execute(LoadedExecutable* le, Device* d, Buffer* const* args, size_t nu
       }
     }
     if (!recorded) HIP_CHECK(hipEventRecord(done->hip_event, st));
-    c->enqueue_completion(done);
+    // Nothing runs on this event's completion unless a callback is registered, so it is not queued on the
+    // completion worker.
+    done->lazy_owner = c;
   }
   outputs->clear();
   for (size_t i = 0; i < plan.output_slots.size(); ++i) {

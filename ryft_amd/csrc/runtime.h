@@ -39,6 +39,10 @@ struct EventState {
   std::vector<std::pair<PJRT_Event_OnReadyCallback, void*>> callbacks;
   hipEvent_t hip_event = nullptr;  // completion marker on the device stream (null for host events)
   std::function<void()> on_complete;  // host work run before the event turns ready (e.g. staging → user copy)
+  // Execution completion events are resolved on demand (await, query) rather than by the client's completion
+  // worker; the first OnReady callback registered before completion hands the event to `lazy_owner`'s worker.
+  struct Client* lazy_owner = nullptr;
+  bool queued = false;
 
   ~EventState();
   // Marks the event ready (idempotent) and runs the registered callbacks on this thread.
@@ -208,6 +212,9 @@ struct Client {  // PJRT_Client
   std::vector<StepTiming> timings;
 
   Client(const std::vector<int>& visible, bool compile_only);
+  // Drains the completion worker (it exits once its queue is empty) and the device streams. Called by the
+  // destructor, and at process exit for clients the host never destroyed.
+  void stop_worker();
   ~Client();
   void enqueue_completion(const EventPtr& e);
   EventPtr record_event(Device* d, std::function<void()> on_complete = nullptr);

@@ -19,10 +19,12 @@ Names and argument meaning follow ryft-pjrt; Python spellings replace Rust ones 
 """
 from __future__ import annotations
 
+import atexit
 import ctypes as C
 import enum
 import os
 import re
+import weakref
 from dataclasses import dataclass, field
 from typing import Callable, Dict, List, Optional, Sequence, Tuple
 
@@ -333,6 +335,29 @@ _LAYOUT_SLOTS = ["PJRT_Layouts_MemoryLayout_Destroy", "PJRT_Layouts_MemoryLayout
                  "PJRT_Layouts_PJRT_Executable_GetParameterLayouts"]
 
 
+# Wrappers that own a plugin object destroy it in __del__. At interpreter exit CPython clears module globals
+# (this module's and ctypes') before it finalizes the objects still referenced from __main__, so those finalizers
+# could no longer call into the plugin and clients would stay alive, with their streams, device memory and pinned
+# host memory, into the HIP runtime's own exit-time teardown. Every owning wrapper is therefore tracked, and an
+# exit hook destroys the live ones while the interpreter is intact: clients last, after everything they own.
+_LIVE: "weakref.WeakValueDictionary" = weakref.WeakValueDictionary()  # id → wrapper (some define __eq__)
+
+
+class _Owned:
+    _exit_order = 0  # clients are destroyed after the objects that belong to them
+
+    def __new__(cls, *args, **kwargs):
+        obj = super().__new__(cls)
+        _LIVE[id(obj)] = obj
+        return obj
+
+
+@atexit.register
+def _destroy_live_objects():
+    for obj in sorted(list(_LIVE.values()), key=lambda o: o._exit_order):
+        obj.__del__()
+
+
 class LayoutsExtension:
     """PJRT_Layouts_Extension (extensions/layouts.rs:20-60): calls go through its own function table."""
 
@@ -352,7 +377,7 @@ class LayoutsExtension:
         return args
 
 
-class Layout:
+class Layout(_Owned):
     """A PJRT memory layout (extensions/layouts.rs:95-195); borrowed ones belong to their executable."""
 
     def __init__(self, ext: LayoutsExtension, handle: int, borrowed: bool):
@@ -645,7 +670,7 @@ class Device:
 
 
 # ----------------------------------------------------------------------------------------------- events
-class Event:
+class Event(_Owned):
     """PJRT_Event wrapper (events.rs); `await_` blocks, `on_ready` registers a callback."""
 
     def __init__(self, api: Api, handle: int, value=None):
@@ -678,7 +703,7 @@ class Event:
 
 
 # ----------------------------------------------------------------------------------------------- buffers
-class Buffer:
+class Buffer(_Owned):
     def __init__(self, client: "Client", handle: int):
         if not handle:
             raise PjrtError(ErrorCode.INVALID_ARGUMENT, "the provided PJRT buffer handle is a null pointer")
@@ -877,7 +902,7 @@ class DeviceAssignment:
         return DeviceAssignment(replicas, computations, out)
 
 
-class ExecutionContext:
+class ExecutionContext(_Owned):
     """PJRT_ExecuteContext (programs.rs:1190-1235)."""
 
     def __init__(self, api: Api, handle: int):
@@ -894,7 +919,7 @@ class ExecutionContext:
             pass
 
 
-class Executable:
+class Executable(_Owned):
     def __init__(self, api: Api, handle: int):
         self.api, self.handle = api, handle
 
@@ -990,7 +1015,7 @@ class ExecutionDeviceOutputs:
     done: Event
 
 
-class LoadedExecutable:
+class LoadedExecutable(_Owned):
     def __init__(self, client: "Client", handle: int):
         if not handle:
             raise PjrtError(ErrorCode.INVALID_ARGUMENT, "the provided PJRT loaded executable handle is a null pointer")
@@ -1017,7 +1042,10 @@ class LoadedExecutable:
 
     def execute(self, inputs: Sequence[Sequence], launch_id: int = 0) -> List[ExecutionDeviceOutputs]:
         """LoadedExecutable::execute (programs.rs:769-963): one input list per addressable device."""
-        device_count = len(self.addressable_devices())
+        counts = self.__dict__.get("_counts")
+        if counts is None:  # fixed for a loaded executable: queried once, not on every execution
+            counts = self._counts = (len(self.addressable_devices()), self.executable().output_count())
+        device_count, output_count = counts
         if len(inputs) != device_count:
             raise PjrtError(ErrorCode.INVALID_ARGUMENT,
                             f"expected inputs for {device_count} device(s) but got inputs for {len(inputs)} device(s)")
@@ -1036,7 +1064,6 @@ class LoadedExecutable:
         opts.num_non_donatable_input_indices = len(non_donatable)
         arg_arrays = [(_vp * max(input_count, 1))(*[x.buffer.handle for x in dev]) for dev in norm]
         arg_lists = (C.POINTER(_vp) * device_count)(*[C.cast(a, C.POINTER(_vp)) for a in arg_arrays])
-        output_count = self.executable().output_count()  # GetExecutable → NumOutputs → Destroy, every call
         out_arrays = [(_vp * max(output_count, 1))() for _ in range(device_count)]
         out_lists = (C.POINTER(_vp) * device_count)(*[C.cast(a, C.POINTER(_vp)) for a in out_arrays])
         events = (_vp * device_count)()
@@ -1068,7 +1095,9 @@ class LoadedExecutable:
 
 
 # ----------------------------------------------------------------------------------------------- client
-class Client:
+class Client(_Owned):
+    _exit_order = 1
+
     def __init__(self, plugin: Plugin, handle: int):
         if not handle:
             raise PjrtError(ErrorCode.INVALID_ARGUMENT, "the provided PJRT client handle is a null pointer")

@@ -5,6 +5,8 @@ Tolerances (normwise relative error): f32 1e-4; bf16 1e-2; int8â†
 output 1e-5; causal attention 2e-2; fp8 SwiGLU 3e-2. Full BASELINE sizes run for C1, C2, C3 and C5; C4 at full size
 is checked on sampled heads plus size-independent properties (finite output, row 0 equals V[0]).
 """
+import time
+
 import numpy as np
 import pytest
 
@@ -96,6 +98,30 @@ def test_add_kat(gpu_client):
     out.done.await_()
     assert out.outputs[0].to_numpy().tolist() == [42, -42]
     assert out.done.is_ready()
+    deadline = time.time() + 10
+    while not seen and time.time() < deadline:  # the callback may run on the completion worker
+        time.sleep(0.001)
+    assert seen == [None]
+
+
+def test_execution_event_callbacks_without_await(gpu_client):
+    """Callbacks registered on a pending execution event fire once, with no error, when nothing awaits it
+    (events.rs:90-120 `on_ready`); later registrations on the ready event run at once."""
+    import threading
+    w = configs.c2_bf16_batched_dot(batch=2, m=256, k=256, n=256)
+    exe = gpu_client.compile(pjrt.Program.mlir(w.program))
+    bufs = [gpu_client.buffer(x.data, x.type, x.dims) for x in w.inputs]
+    fired = threading.Event()
+    seen = []
+    outs = [exe.execute([bufs])[0] for _ in range(4)]
+    outs[-1].done.on_ready(lambda err: (seen.append(err), fired.set()))
+    assert fired.wait(30), "OnReady callback of an execution event never ran"
+    assert seen == [None] and outs[-1].done.is_ready()
+    late = []
+    outs[-1].done.on_ready(lambda err: late.append(err))
+    assert late == [None]
+    for o in outs[:-1]:
+        o.done.await_()
 
 
 def test_execute_validates_arguments(gpu_client):

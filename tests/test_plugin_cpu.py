@@ -463,3 +463,26 @@ def test_split_k_plans(compile_client, name, kw, kernel):
     w = configs.CONFIGS[name](**kw)
     _, kernels = _plan(compile_client, w.program)
     assert kernels == [kernel]
+
+
+_EXIT_SCRIPT = r'''
+import atexit, sys
+sys.path.insert(0, sys.argv[1])
+state = {}
+atexit.register(lambda: print("after hook:", state["client"].handle is None, state["exe"].handle is None, flush=True))
+from ryft_amd import pjrt  # its exit hook is registered after the one above, so it runs first
+client = pjrt.load_plugin().client({"compile_only": True})
+exe = client.compile(pjrt.Program.mlir(sys.argv[2]))
+state.update(client=client, exe=exe)
+print("compiled", flush=True)
+'''
+
+
+def test_wrappers_alive_at_interpreter_exit_are_destroyed():
+    """Objects still referenced from __main__ at exit are destroyed by the module's exit hook (executables before
+    their client) while ctypes is intact, instead of reaching finalizers that can no longer call the plugin."""
+    import sys
+    r = subprocess.run([sys.executable, "-c", _EXIT_SCRIPT, ROOT, ADD_2X1], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, r.stderr
+    assert r.stdout.split() == ["compiled", "after", "hook:", "True", "True"], r.stdout + r.stderr
