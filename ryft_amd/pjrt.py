@@ -1055,19 +1055,24 @@ class LoadedExecutable(_Owned):
             if len(dev) != input_count:
                 raise PjrtError(ErrorCode.INVALID_ARGUMENT,
                                 f"expected {input_count} input(s) for each device but got {len(dev)} for device {d}")
-        non_donatable = [i for i, x in enumerate(norm[0])] if norm else []
-        nd = (C.c_int64 * max(len(non_donatable), 1))(*non_donatable)
-        opts = ExecuteOptions()
-        opts.struct_size = C.sizeof(opts)
-        opts.launch_id = launch_id
-        opts.non_donatable_input_indices = nd
-        opts.num_non_donatable_input_indices = len(non_donatable)
+        # the options (every input non-donatable) depend only on the input count and launch id: built once each
+        key = (input_count, launch_id)
+        cached = self.__dict__.setdefault("_options", {}).get(key)
+        if cached is None:
+            nd = (C.c_int64 * max(input_count, 1))(*range(input_count))
+            opts = ExecuteOptions()
+            opts.struct_size = C.sizeof(opts)
+            opts.launch_id = launch_id
+            opts.non_donatable_input_indices = nd
+            opts.num_non_donatable_input_indices = input_count
+            cached = self._options[key] = (nd, opts, C.pointer(opts))
+        opts_ptr = cached[2]
         arg_arrays = [(_vp * max(input_count, 1))(*[x.buffer.handle for x in dev]) for dev in norm]
         arg_lists = (C.POINTER(_vp) * device_count)(*[C.cast(a, C.POINTER(_vp)) for a in arg_arrays])
         out_arrays = [(_vp * max(output_count, 1))() for _ in range(device_count)]
         out_lists = (C.POINTER(_vp) * device_count)(*[C.cast(a, C.POINTER(_vp)) for a in out_arrays])
         events = (_vp * device_count)()
-        self.api.call("PJRT_LoadedExecutable_Execute", executable=self.handle, options=C.pointer(opts),
+        self.api.call("PJRT_LoadedExecutable_Execute", executable=self.handle, options=opts_ptr,
                       argument_lists=arg_lists, num_devices=device_count, num_args=input_count,
                       output_lists=out_lists, device_complete_events=events, execute_device=None)
         results = []
