@@ -43,6 +43,7 @@ def _cpu_baseline(name, seconds):
         "c3": (configs.c3_int8_gemm, {"m": 512}, "512 of the 4096 rows of C3"),
         "c4": (configs.c4_causal_attention, {"b": 1, "h": 2}, "2 of the 128 heads of C4"),
         "c5": (configs.c5_swiglu_fp8, {"m": 64}, "64 of the 512 tokens of C5"),
+        "c5x": (configs.c5x_swiglu_fp8_activations, {"m": 64}, "64 of the 512 tokens of C5 (fp8 activations)"),
         "copy": (configs.hbm_copy_f32, {}, "the full copy calibration vector"),
         "rmsnorm": (configs.rmsnorm_fp8_rows, {"m": 1024}, "1024 of the 16384 rows"),
     }
@@ -70,7 +71,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "copy", "rmsnorm"],
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "c5x", "copy", "rmsnorm"],
                     help="c1..c5: the BASELINE configs (c2 is the headline); copy: the HBM calibration kernel")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")

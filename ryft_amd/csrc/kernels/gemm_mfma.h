@@ -15,6 +15,8 @@
 //   bf16  v_mfma_f32_32x32x16_bf16      f16  v_mfma_f32_32x32x16_f16
 //   i8    v_mfma_i32_32x32x32_i8        fp8  v_mfma_f32_32x32x64_f8f6f4 (e4m3 × e4m3, unit scales)
 //   f32   v_mfma_f32_32x32x2_f32
+//   bf16 × f8E4M3FN (weight-only quantised B): B is read from HBM as f8E4M3FN bytes and widened exactly to bf16
+//   (v_cvt_scalef32_pk_bf16_fp8, unit scale) between its registers and LDS; the MFMA is the bf16 one
 //
 // Generic path: a 64×64 LDS-tiled FMA kernel that reads any element type through any strides (bounds-checked); it
 // serves shapes and type mixes the MFMA instantiations do not cover.
@@ -40,7 +42,7 @@ typedef int i32x8_t __attribute__((__vector_size__(8 * sizeof(int))));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // ------------------------------------------------------------------------------------------------ MFMA GEMM
-enum MmaKind { MMA_BF16 = 0, MMA_F16 = 1, MMA_I8 = 2, MMA_FP8 = 3, MMA_F32 = 4 };
+enum MmaKind { MMA_BF16 = 0, MMA_F16 = 1, MMA_I8 = 2, MMA_FP8 = 3, MMA_F32 = 4, MMA_BF16_F8 = 5 };
 
 template <int KIND> struct Mma;
 template <> struct Mma<MMA_BF16> {
@@ -84,6 +86,11 @@ template <> struct Mma<MMA_F32> {
   static constexpr bool INT = false;
   __device__ static Acc mma(float a, float b, Acc c) { return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0); }
 };
+// bf16 activations × f8E4M3FN weights: the bf16 MFMA on B tiles widened to bf16 in LDS.
+template <> struct Mma<MMA_BF16_F8> : Mma<MMA_BF16> {};
+
+// Element size of B in HBM (differs from the LDS / MFMA element size only for widened B operands).
+template <int KIND> constexpr int b_hbm_size() { return KIND == MMA_BF16_F8 ? 1 : Mma<KIND>::ESIZE; }
 
 // Fragment type and LDS read for KPACK·ESIZE bytes per lane.
 template <int BYTES> struct Frag;
@@ -231,6 +238,82 @@ struct TileCopyLoader {
   }
 };
 
+// f8E4M3FN → bf16, 16 values: v_cvt_scalef32_pk_bf16_fp8 widens two bytes of a word per instruction. Exact: every
+// f8E4M3FN value (subnormals included) is a bf16 value and the unit scale multiplies exactly; NaN stays NaN.
+typedef __bf16 bf16x2_g __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void f8x16_to_bf16(const u32x4& v, u32x4& lo, u32x4& hi) {
+#define RYFT_W(x, s) __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((x), 1.0f, (s)))
+  lo = u32x4{RYFT_W(v.x, false), RYFT_W(v.x, true), RYFT_W(v.y, false), RYFT_W(v.y, true)};
+  hi = u32x4{RYFT_W(v.z, false), RYFT_W(v.z, true), RYFT_W(v.w, false), RYFT_W(v.w, true)};
+#undef RYFT_W
+}
+
+// A row-contiguous f8E4M3FN operand tile (BK k-rows × R bytes in HBM) → bf16 [k][R] rows of LDB bytes in LDS (the
+// layout TileCopyLoader gives a 16-bit operand, read the same way with transposing LDS reads).
+template <int R, int BK, int THREADS>
+struct TileWidenCopyLoader {
+  static constexpr int NTOT = BK * (R / 16);
+  static constexpr int NVEC = NTOT / THREADS;
+  static_assert(NTOT % THREADS == 0, "uneven tile split");
+  u32x4 regs[NVEC];
+  __device__ __forceinline__ void load(const char* base, int64_t sr, int64_t sk, int tid) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, -1, 0x00020000);
+    (void)sr;
+#pragma unroll
+    for (int i = 0; i < NVEC; ++i) {
+      const int v = tid + i * THREADS;
+      const int k = v / (R / 16), c = v % (R / 16);
+      regs[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)((int64_t)k * sk + (int64_t)c * 16), 0, 0);
+    }
+  }
+  template <int LDB>
+  __device__ __forceinline__ void store(char* lds, int tid) {
+#pragma unroll
+    for (int i = 0; i < NVEC; ++i) {
+      const int v = tid + i * THREADS;
+      const int k = v / (R / 16), c = v % (R / 16);
+      u32x4 lo, hi;
+      f8x16_to_bf16(regs[i], lo, hi);
+      *(u32x4*)(lds + k * LDB + c * 32) = lo;
+      *(u32x4*)(lds + k * LDB + c * 32 + 16) = hi;
+    }
+  }
+};
+
+// A K-contiguous f8E4M3FN operand tile (R rows × BK bytes in HBM) → K-packed bf16 rows of LDK bytes in LDS.
+template <int R, int BK, int THREADS>
+struct TileWidenLoader {
+  static constexpr int NTOT = R * BK / 16;
+  static constexpr int NVEC = (NTOT + THREADS - 1) / THREADS;
+  static constexpr bool PARTIAL = (NTOT % THREADS) != 0;
+  static_assert(!PARTIAL || NVEC == 1, "uneven tile split");
+  u32x4 regs[NVEC];
+  __device__ __forceinline__ void load(const char* base, int64_t sr, int64_t sk, int tid) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, -1, 0x00020000);
+    (void)sk;
+#pragma unroll
+    for (int i = 0; i < NVEC; ++i) {
+      const int v = tid + i * THREADS;
+      if (PARTIAL && v >= NTOT) break;
+      const int row = v / (BK / 16), kv = v % (BK / 16);
+      regs[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)((int64_t)row * sr + (int64_t)kv * 16), 0, 0);
+    }
+  }
+  template <int LDK>
+  __device__ __forceinline__ void store(char* lds, int tid) {
+#pragma unroll
+    for (int i = 0; i < NVEC; ++i) {
+      const int v = tid + i * THREADS;
+      if (PARTIAL && v >= NTOT) break;
+      const int row = v / (BK / 16), kv = v % (BK / 16);
+      u32x4 lo, hi;
+      f8x16_to_bf16(regs[i], lo, hi);
+      *(u32x4*)(lds + row * LDK + kv * 32) = lo;
+      *(u32x4*)(lds + row * LDK + kv * 32 + 16) = hi;
+    }
+  }
+};
+
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 // ds_read_b64_tr_b16. Within each group of 16 lanes, lane i receives element i % 4 of the 8-byte chunks addressed by
 // lanes i/4, i/4 + 4, i/4 + 8, i/4 + 12 of the group (lane layout measured on gfx950). So when lane s of a group
@@ -252,6 +335,7 @@ template <int KIND, int BM, int BN, int BK, int WM, int WN, bool A_R, bool B_R, 
 struct MfmaCfg {
   using M = Mma<KIND>;
   static constexpr int ESIZE = M::ESIZE, KPACK = M::KPACK, MK = 2 * KPACK;
+  static constexpr int BES = b_hbm_size<KIND>();  // B's element size in HBM (1: f8 widened to bf16 in LDS)
   static constexpr int THREADS = 64 * WM * WN;
   static constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
   static constexpr int LDK = BK * ESIZE + 16;  // LDS row pitch in bytes (16-byte pad)
@@ -486,12 +570,15 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_mfma_kernel(const GemmArgs 
   const int m0 = tm * BM, n0 = tn * BN;
 
   const char* Ab = (const char*)G.A.ptr + ((int64_t)b * G.A.sb + (int64_t)m0 * G.A.sr) * ES;
-  const char* Bb = (const char*)G.B.ptr + ((int64_t)b * G.B.sb + (int64_t)n0 * G.B.sr) * ES;
-  const char* B2b = DUAL ? (const char*)G.B2.ptr + ((int64_t)b * G.B2.sb + (int64_t)n0 * G.B2.sr) * ES : nullptr;
+  constexpr int BES = C::BES;
+  const char* Bb = (const char*)G.B.ptr + ((int64_t)b * G.B.sb + (int64_t)n0 * G.B.sr) * BES;
+  const char* B2b = DUAL ? (const char*)G.B2.ptr + ((int64_t)b * G.B2.sb + (int64_t)n0 * G.B2.sr) * BES : nullptr;
 
   // One register stage of global prefetch: tile kt + 2 is requested at the start of k-tile kt (right after tile
   // kt + 1 went from registers to LDS), so each load has a whole k-tile of MFMA work to arrive in. Two LDS stages.
-  using BLoader = std::conditional_t<C::BTR, TileCopyLoader<ES, BN, BK, C::THREADS>, TileLoader<ES, BN, BK, C::THREADS, B_R>>;
+  using BLoader = std::conditional_t<
+      BES != ES, std::conditional_t<C::BTR, TileWidenCopyLoader<BN, BK, C::THREADS>, TileWidenLoader<BN, BK, C::THREADS>>,
+      std::conditional_t<C::BTR, TileCopyLoader<ES, BN, BK, C::THREADS>, TileLoader<ES, BN, BK, C::THREADS, B_R>>>;
   TileLoader<ES, BM, BK, C::THREADS, A_R> la;
   BLoader lb;
   BLoader lb2;
@@ -511,8 +598,8 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_mfma_kernel(const GemmArgs 
   auto gload = [&](int kt) {
     const int64_t ko = (int64_t)(kt0 + kt) * BK;
     la.load(Ab + ko * G.A.sk * ES, G.A.sr, G.A.sk, tid);
-    lb.load(Bb + ko * G.B.sk * ES, G.B.sr, G.B.sk, tid);
-    if constexpr (DUAL) lb2.load(B2b + ko * G.B2.sk * ES, G.B2.sr, G.B2.sk, tid);
+    lb.load(Bb + ko * G.B.sk * BES, G.B.sr, G.B.sk, tid);
+    if constexpr (DUAL) lb2.load(B2b + ko * G.B2.sk * BES, G.B2.sr, G.B2.sk, tid);
   };
   auto lstore = [&](int buf) {
     char* s = smem + buf * C::STAGE;
@@ -706,5 +793,6 @@ bool pick_f16(const GemmArgs& g, bool br, Choice* c);
 bool pick_i8(const GemmArgs& g, bool br, Choice* c);
 bool pick_fp8(const GemmArgs& g, bool br, Choice* c);
 bool pick_f32(const GemmArgs& g, bool br, Choice* c);
+bool pick_bf16f8(const GemmArgs& g, bool br, Choice* c);
 
 }  // namespace ryft

@@ -156,9 +156,10 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const GemmArgs G) {
 }
 
 static int mma_kind(const GemmArgs& g) {
-  auto t = [](int d) { return d; };
   if (g.dual && g.B2.dtype != g.B.dtype) return -1;
-  if (t(g.A.dtype) != t(g.B.dtype)) return -1;
+  // bf16 × f8E4M3FN (weight-only quantisation): f8 widens exactly to bf16, so the bf16 MFMA computes the same dot
+  if (g.A.dtype == DT_BF16 && g.B.dtype == DT_F8E4M3FN) return g.acc_is_int ? -1 : MMA_BF16_F8;
+  if (g.A.dtype != g.B.dtype) return -1;
   switch (g.A.dtype) {
     case DT_BF16: return g.acc_is_int ? -1 : MMA_BF16;
     case DT_F16: return g.acc_is_int ? -1 : MMA_F16;
@@ -183,31 +184,29 @@ static bool pick_mfma(const GemmArgs& g, Choice* c) {
     return false;
   if (g.epilogue != EPI_STORE && !mfma_mid_round_supported(g.mid_round, g.raw_out != 0)) return false;
   if (g.epilogue == EPI_STORE && g.mid_round) return false;
-  const int es = kind == MMA_BF16 || kind == MMA_F16 ? 2 : (kind == MMA_F32 ? 4 : 1);
-  const int ve = 16 / es;
-  // operand layouts: K-contiguous (sk == 1) or row-contiguous (sr == 1)
-  auto layout = [&](const GemmOperand& o, int rows, int* r) -> bool {
+  const int es = kind == MMA_BF16 || kind == MMA_F16 || kind == MMA_BF16_F8 ? 2 : (kind == MMA_F32 ? 4 : 1);
+  const int bes = kind == MMA_BF16_F8 ? 1 : es;  // B's element size in HBM
+  // operand layouts: K-contiguous (sk == 1) or row-contiguous (sr == 1), in 16-byte vectors of `oes`-byte elements
+  auto layout = [&](const GemmOperand& o, int oes, int* r) -> bool {
+    const int ve = 16 / oes;
     if (((uintptr_t)o.ptr & 15) != 0) return false;
     // tiles (≤ 256 rows / k-rows) are read through 32-bit buffer offsets from the tile origin
-    if ((o.sr > o.sk ? o.sr : o.sk) * (int64_t)es * 256 >= ((int64_t)1 << 31)) return false;
+    if ((o.sr > o.sk ? o.sr : o.sk) * (int64_t)oes * 256 >= ((int64_t)1 << 31)) return false;
     if (o.sk == 1 && (o.sr % ve) == 0 && (o.sb % ve) == 0) { *r = 0; return true; }
     if (o.sr == 1 && (o.sk % ve) == 0 && (o.sb % ve) == 0) { *r = 1; return true; }
-    (void)rows;
     return false;
   };
   int ar, br, br2 = -1;
-  if (!layout(g.A, g.M, &ar) || !layout(g.B, g.N, &br)) return false;
-  if (g.dual && (!layout(g.B2, g.N, &br2) || br2 != br)) return false;
+  if (!layout(g.A, es, &ar) || !layout(g.B, bes, &br)) return false;
+  if (g.dual && (!layout(g.B2, bes, &br2) || br2 != br)) return false;
   if (ar != 0) return false;  // m-contiguous A tiles are not instantiated
-  auto fits = [&](int bm, int bn, int bk) { return g.M % bm == 0 && g.N % bn == 0 && g.K % bk == 0; };
-  const bool dual = g.dual != 0;
-  const int64_t tiles256 = (int64_t)(g.M / 256) * (g.N / 256) * g.batch;
   switch (kind) {
     case MMA_BF16: return pick_bf16(g, br, c);
     case MMA_F16: return pick_f16(g, br, c);
     case MMA_I8: return pick_i8(g, br, c);
     case MMA_FP8: return pick_fp8(g, br, c);
     case MMA_F32: return pick_f32(g, br, c);
+    case MMA_BF16_F8: return pick_bf16f8(g, br, c);
   }
   return false;
 }

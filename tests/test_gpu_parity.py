@@ -183,17 +183,80 @@ def test_c4_attention_full_sampled(gpu_client):
         assert err <= w.tolerance
 
 
-@pytest.mark.parametrize("kw", [dict(m=128, d=256, f=512), dict(m=64, d=256, f=384)])
-def test_c5_swiglu_small(gpu_client, kw):
-    _run_and_check(gpu_client, configs.c5_swiglu_fp8(**kw))
+@pytest.mark.parametrize("kw,kernel", [(dict(m=256, d=512, f=1024), "gemm_bf16f8_mfma_dual_256x128"),
+                                       (dict(m=128, d=256, f=512), "gemm_bf16f8_mfma_dual_128x128"),
+                                       (dict(m=64, d=256, f=384), "gemm_generic")])
+def test_c5_swiglu_small(gpu_client, kw, kernel):
+    outs, exe = _run_and_check(gpu_client, configs.c5_swiglu_fp8(**kw))
+    assert kernel in exe.describe_plan()
 
 
-def test_c5_swiglu_weight_only_bf16(gpu_client):
-    _run_and_check(gpu_client, configs.c5_swiglu_fp8(m=64, d=256, f=512, activations="bf16"))
+def test_c5_swiglu_direct_f8_operands(gpu_client):
+    # the dot_generals take the f8E4M3FN weights as operands (mixed operand types) instead of converted copies
+    outs, exe = _run_and_check(gpu_client, configs.c5_swiglu_fp8(m=256, d=512, f=1024, weights="direct"))
+    assert "gemm_bf16f8_mfma_dual_256x128" in exe.describe_plan()
 
 
 def test_c5_swiglu_full(gpu_client):
-    _run_and_check(gpu_client, configs.c5_swiglu_fp8())
+    # C5 as BASELINE.json states it: bf16 activations × f8E4M3FN weights, on the bf16 MFMA (no generic kernel)
+    w = configs.c5_swiglu_fp8()
+    outs, exe = _run_and_check(gpu_client, w)
+    plan = exe.describe_plan()
+    assert "gemm_generic" not in plan and "gemm_bf16f8_mfma_dual" in plan, plan
+
+
+def test_c5x_fp8_activations_full(gpu_client):
+    # not a BASELINE config: activations quantized to f8E4M3FN too (fp8 × fp8 MFMA), checked against its own graph
+    w = configs.c5x_swiglu_fp8_activations()
+    outs, exe = _run_and_check(gpu_client, w)
+    assert "gemm_fp8_mfma_dual" in exe.describe_plan()
+
+
+def _widen_program(k_contiguous):
+    if k_contiguous:  # rhs stored [n, k]
+        return """module {
+  func.func @main(%arg0: tensor<256x256xbf16>, %arg1: tensor<256x256xf8E4M3FN>) -> tensor<256x256xf32> {
+    %0 = stablehlo.dot_general %arg0, %arg1, contracting_dims = [1] x [1] : (tensor<256x256xbf16>, tensor<256x256xf8E4M3FN>) -> tensor<256x256xf32>
+    return %0 : tensor<256x256xf32>
+  }
+}"""
+    return """module {
+  func.func @main(%arg0: tensor<256x256xbf16>, %arg1: tensor<256x256xf8E4M3FN>) -> tensor<256x256xf32> {
+    %0 = stablehlo.dot_general %arg0, %arg1, contracting_dims = [1] x [0] : (tensor<256x256xbf16>, tensor<256x256xf8E4M3FN>) -> tensor<256x256xf32>
+    return %0 : tensor<256x256xf32>
+  }
+}"""
+
+
+@pytest.mark.parametrize("k_contiguous", [False, True])
+def test_bf16_f8_widening_every_code(gpu_client, k_contiguous):
+    """The bf16 × f8E4M3FN GEMM widens every f8 code exactly: identity lhs, rhs holding all 254 finite codes in
+    every row and column (subnormals and signed zeros included), f32 result equal to the decoded codes
+    (StableHLO convert f8E4M3FN → bf16 is exact, casting.rs:75-122). A column holding a NaN code is NaN in every
+    row (0 · NaN = NaN), the other columns unchanged."""
+    eye = nm.encode_bits(np.eye(256), "bf16")
+    idx = (np.arange(256)[:, None] + np.arange(256)[None, :]) % 256
+    codes = idx.astype(np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0x00  # finite codes only
+    nan_codes = codes.copy()
+    nan_codes[17, 3] = 0x7F
+    nan_codes[200, 250] = 0xFF
+    exe = gpu_client.compile(pjrt.Program.mlir(_widen_program(k_contiguous)))
+    assert "gemm_bf16f8_mfma" in exe.describe_plan(), exe.describe_plan()
+    decoded = nm.decode_bits(codes, "f8E4M3FN").astype(np.float32)
+    for rhs, nan_cols in ((codes, []), (nan_codes, [3, 250])):
+        stored = np.ascontiguousarray(rhs.T) if k_contiguous else rhs  # k-contiguous: the [n, k] layout
+        ins = [configs.HostInput(eye, pjrt.BufferType.BF16, (256, 256)),
+               configs.HostInput(stored, pjrt.BufferType.F8E4M3FN, (256, 256))]
+        outs, _ = run_pjrt(gpu_client, "", ins, executable=exe)
+        got = outs[0].view(np.float32).reshape(256, 256)
+        want = decoded  # C = I · B = B in both layouts
+        ok = np.ones(256, bool)
+        ok[nan_cols] = False
+        # values, not bits: the diagonal's -0 product summed with +0 products is +0
+        assert np.array_equal(got[:, ok], want[:, ok])
+        for c in nan_cols:
+            assert np.all(np.isnan(got[:, c]))
 
 
 def test_repeated_execution_is_deterministic(gpu_client):

@@ -34,8 +34,14 @@ def test_bf16_split_k(gpu_client):
 
 
 def test_fp8_split_k_scaled_epilogue(gpu_client):
-    # C5 at 128 tokens: the down projection (M=128, N=1024, K=2048) runs split-K with the per-column scale epilogue
-    _run(gpu_client, configs.c5_swiglu_fp8(m=128, d=1024, f=2048), "gemm_fp8_mfma_128x128")
+    # C5 with fp8 activations at 128 tokens: the down projection (M=128, N=1024, K=2048) runs split-K with the
+    # per-column scale epilogue
+    _run(gpu_client, configs.c5x_swiglu_fp8_activations(m=128, d=1024, f=2048), "gemm_fp8_mfma_128x128")
+
+
+def test_bf16_f8_split_k_scaled_epilogue(gpu_client):
+    # C5 as stated (bf16 activations, f8 weights) at 128 tokens: the same split on the widening bf16 kernel
+    _run(gpu_client, configs.c5_swiglu_fp8(m=128, d=1024, f=2048), "gemm_bf16f8_mfma_128x128")
 
 
 def test_f32_split_k(gpu_client):
