@@ -122,9 +122,14 @@ def c3_int8_gemm(m=4096, k=4096, n=4096, seed=0xC3) -> Workload:
 
 
 # ----------------------------------------------------------------------------------------------- C4
-def c4_causal_attention(b=4, h=32, s=2048, d=128, seed=0xC4) -> Workload:
+def c4_causal_attention(b=4, h=32, s=2048, d=128, seed=0xC4, mask="GE", fill="0xFF800000", p_type="bf16") -> Workload:
     """Causal softmax attention written as plain StableHLO: dot → scale → iota/compare/select mask → reduce-max →
-    subtract → exp → reduce-sum → divide → convert → dot → convert."""
+    subtract → exp → reduce-sum → divide → convert → dot → convert.
+
+    The defaults are BASELINE.json's C4. Variants for tests: `mask` is the comparison direction of row (query) index
+    against column (key) index ("GT": a strict mask, query 0 sees no key); `fill` the select's fill for masked
+    scores (an MLIR float literal); p_type="f32" feeds the f32 probabilities to the second dot_general directly
+    (f32 × bf16 operands, no convert)."""
     qt = _t((b, h, s, d), "bf16")
     sf = _t((b, h, s, s), "f32")
     sb = _t((b, h, s, s), "bf16")
@@ -134,6 +139,14 @@ def c4_causal_attention(b=4, h=32, s=2048, d=128, seed=0xC4) -> Workload:
     rf = _t((b, h, s), "f32")
     of = _t((b, h, s, d), "f32")
     scale = _f32_literal(1.0 / math.sqrt(d))
+    if fill == "0xFF800000":
+        fill_cst, fill_ref = "", "%cst_0"
+    else:
+        fill_cst, fill_ref = f"    %cst_f = stablehlo.constant dense<{fill}> : tensor<f32>\n", "%cst_f"
+    if p_type == "bf16":
+        p_line, p_ref, p_ty = f"    %16 = stablehlo.convert %15 : ({sf}) -> {sb}\n", "%16", sb
+    else:
+        p_line, p_ref, p_ty = "", "%15", sf
     prog = f"""module {{
   func.func @main(%arg0: {qt}, %arg1: {qt}, %arg2: {qt}) -> {qt} {{
     %0 = stablehlo.dot_general %arg0, %arg1, batching_dims = [0, 1] x [0, 1], contracting_dims = [3] x [3] : ({qt}, {qt}) -> {sf}
@@ -142,10 +155,10 @@ def c4_causal_attention(b=4, h=32, s=2048, d=128, seed=0xC4) -> Workload:
     %2 = stablehlo.multiply %0, %1 : {sf}
     %3 = stablehlo.iota dim = 0 : {mi}
     %4 = stablehlo.iota dim = 1 : {mi}
-    %5 = stablehlo.compare  GE, %3, %4,  SIGNED : ({mi}, {mi}) -> {mp}
+    %5 = stablehlo.compare  {mask}, %3, %4,  SIGNED : ({mi}, {mi}) -> {mp}
     %6 = stablehlo.broadcast_in_dim %5, dims = [2, 3] : ({mp}) -> {pi}
     %cst_0 = stablehlo.constant dense<0xFF800000> : tensor<f32>
-    %7 = stablehlo.broadcast_in_dim %cst_0, dims = [] : (tensor<f32>) -> {sf}
+{fill_cst}    %7 = stablehlo.broadcast_in_dim {fill_ref}, dims = [] : (tensor<f32>) -> {sf}
     %8 = stablehlo.select %6, %2, %7 : {pi}, {sf}
     %9 = stablehlo.reduce(%8 init: %cst_0) applies stablehlo.maximum across dimensions = [3] : ({sf}, tensor<f32>) -> {rf}
     %10 = stablehlo.broadcast_in_dim %9, dims = [0, 1, 2] : ({rf}) -> {sf}
@@ -155,8 +168,7 @@ def c4_causal_attention(b=4, h=32, s=2048, d=128, seed=0xC4) -> Workload:
     %13 = stablehlo.reduce(%12 init: %cst_1) applies stablehlo.add across dimensions = [3] : ({sf}, tensor<f32>) -> {rf}
     %14 = stablehlo.broadcast_in_dim %13, dims = [0, 1, 2] : ({rf}) -> {sf}
     %15 = stablehlo.divide %12, %14 : {sf}
-    %16 = stablehlo.convert %15 : ({sf}) -> {sb}
-    %17 = stablehlo.dot_general %16, %arg2, batching_dims = [0, 1] x [0, 1], contracting_dims = [3] x [2] : ({sb}, {qt}) -> {of}
+{p_line}    %17 = stablehlo.dot_general {p_ref}, %arg2, batching_dims = [0, 1] x [0, 1], contracting_dims = [3] x [2] : ({p_ty}, {qt}) -> {of}
     %18 = stablehlo.convert %17 : ({of}) -> {qt}
     return %18 : {qt}
   }}

@@ -317,17 +317,26 @@ __global__ void __launch_bounds__(256, 2) attention_fwd_kernel(const AttnArgs A)
 
 }  // namespace
 
-void launch_attention(const AttnArgs& a, hipStream_t stream, hipEvent_t done) {
-  if (!attention_supported(a.D)) fail(PJRT_Error_Code_UNIMPLEMENTED, "attention head dim " + std::to_string(a.D));
-  if (a.Sq % BQ || a.Sk % BKV) fail(PJRT_Error_Code_UNIMPLEMENTED, "attention sequence lengths must be multiples of 128 / 64");
+const char* attention_unsupported(const AttnArgs& a) {
+  if (!attention_supported(a.D)) return "attention head dim must be 64 or 128";
+  if (a.Sq <= 0 || a.Sk <= 0 || a.Sq % BQ || a.Sk % BKV) return "attention sequence lengths must be multiples of 128 / 64";
   if (a.qs[3] != 1 || a.ks[3] != 1 || a.vs[3] != 1 || a.os[3] != 1)
-    fail(PJRT_Error_Code_UNIMPLEMENTED, "attention operands must be contiguous along the head dim");
-  if (!(a.out_dtype == DT_BF16 || a.out_dtype == DT_F32)) fail(PJRT_Error_Code_UNIMPLEMENTED, "attention output type");
+    return "attention operands must be contiguous along the head dim";
+  if (!(a.out_dtype == DT_BF16 || a.out_dtype == DT_F32)) return "attention output type must be bf16 or f32";
+  if (a.p_dtype != DT_BF16) return "attention probabilities must be rounded to bf16 before P·V";
+  // a row with no visible key (strict mask) is NaN under StableHLO's -inf fill; the kernel does not produce it
+  if (a.causal && a.causal_offset < 0) return "attention causal mask must keep the diagonal";
   if (((uintptr_t)a.q | (uintptr_t)a.k | (uintptr_t)a.v | (uintptr_t)a.o) & 15)
-    fail(PJRT_Error_Code_UNIMPLEMENTED, "attention operands must be 16-byte aligned");
-  // K / V blocks are read through 32-bit byte offsets from the block origin
-  if (a.ks[2] > (1 << 20) || a.vs[2] > (1 << 20))
-    fail(PJRT_Error_Code_UNIMPLEMENTED, "attention key/value row stride too large");
+    return "attention operands must be 16-byte aligned";
+  // Q rows are read 16 bytes at a time, K / V blocks through 32-bit byte offsets from the block origin
+  for (int i = 0; i < 3; ++i)
+    if ((a.qs[i] | a.ks[i] | a.vs[i] | a.os[i]) & 7) return "attention strides must be multiples of 8 elements";
+  if (a.ks[2] > (1 << 20) || a.vs[2] > (1 << 20)) return "attention key/value row stride too large";
+  return nullptr;
+}
+
+void launch_attention(const AttnArgs& a, hipStream_t stream, hipEvent_t done) {
+  if (const char* why = attention_unsupported(a)) fail(PJRT_Error_Code_UNIMPLEMENTED, why);
   int64_t blocks = (int64_t)a.B * a.H * (a.Sq / BQ);
   if (blocks == 0) return record_done(done, stream);
   hipError_t e;

@@ -26,5 +26,8 @@ const char* gemm_kernel_name(const GemmArgs& a);
 int gemm_plan_splits(const GemmArgs& a);
 // Head dims the fused attention kernel supports.
 bool attention_supported(int head_dim);
+// Why the fused attention kernel cannot run these arguments (null: it can). The planner calls it with the operands'
+// byte offsets from their (256-byte aligned) slots in place of pointers, and fuses only when it returns null.
+const char* attention_unsupported(const AttnArgs& a);
 
 }  // namespace ryft

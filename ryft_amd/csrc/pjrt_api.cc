@@ -7,6 +7,7 @@
 //   ToHostBuffer with dst == null only reports dst_size (buffers.rs:1242-1253).
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <cstddef>
 #include <cstring>
 #include <mutex>
@@ -827,19 +828,26 @@ PJRT_Error* LoadedExecutable_Execute(PJRT_LoadedExecutable_Execute_Args* args) {
   size_t nd = args->num_devices;
   if (args->execute_device) {
     if (nd != 1) return make_pjrt_error(PJRT_Error_Code_INVALID_ARGUMENT, "execute_device requires exactly one argument list");
+    // constants and plans live on the executable's devices only
+    Device* want = from<Device>(args->execute_device);
+    if (std::find(le->devices.begin(), le->devices.end(), want) == le->devices.end())
+      return make_pjrt_error(PJRT_Error_Code_INVALID_ARGUMENT, "execute_device is not a device of this executable");
   } else if (nd != le->devices.size()) {
     return make_pjrt_error(PJRT_Error_Code_INVALID_ARGUMENT,
                            "expected argument lists for " + std::to_string(le->devices.size()) + " device(s) but got " +
                                std::to_string(nd));
   }
+  // outputs are created by the execution: without somewhere to put them they could never be destroyed
+  if (!args->output_lists) return make_pjrt_error(PJRT_Error_Code_INVALID_ARGUMENT, "output_lists is null");
+  for (size_t d = 0; d < nd; ++d)
+    if (!args->output_lists[d]) return make_pjrt_error(PJRT_Error_Code_INVALID_ARGUMENT, "output list is null");
   for (size_t d = 0; d < nd; ++d) {
     Device* dev = args->execute_device ? from<Device>(args->execute_device) : le->devices[d];
     std::vector<Buffer*> outs;
     Buffer* const* argv = reinterpret_cast<Buffer* const*>(args->argument_lists ? args->argument_lists[d] : nullptr);
     if (!argv && args->num_args) return make_pjrt_error(PJRT_Error_Code_INVALID_ARGUMENT, "argument list is null");
     EventPtr done = execute(le, dev, argv, args->num_args, &outs);
-    if (args->output_lists && args->output_lists[d])
-      for (size_t o = 0; o < outs.size(); ++o) args->output_lists[d][o] = to<PJRT_Buffer>(outs[o]);
+    for (size_t o = 0; o < outs.size(); ++o) args->output_lists[d][o] = to<PJRT_Buffer>(outs[o]);
     if (args->device_complete_events) args->device_complete_events[d] = wrap_event(done);
   }
   API_CATCH

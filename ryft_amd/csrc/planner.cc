@@ -1521,8 +1521,10 @@ bool Planner::try_attention(int d2, int target, DType out_dtype, int root) {
   int causal = 0, causal_offset = 0;
   const Node& Mn = g_.nodes[m];
   if (Mn.op == Op::Select) {
+    // only a -inf fill: the kernel gives masked scores probability exactly 0, which a finite fill matches only
+    // while it stays far below the row maximum
     double fill;
-    if (!splat_value(Mn.operands[2], &fill) || !(fill < -1e30)) return false;
+    if (!splat_value(Mn.operands[2], &fill) || !(std::isinf(fill) && fill < 0)) return false;
     // the predicate is compare(iota, iota), possibly computed at lower rank and broadcast up to the scores
     int pred = Mn.operands[0];
     std::vector<int64_t> axis_map = {0, 1, 2, 3};  // axis of the current predicate space → score axis
@@ -1582,11 +1584,10 @@ bool Planner::try_attention(int d2, int target, DType out_dtype, int root) {
   int64_t B = Qt.shape[0], H = Qt.shape[1], Sq = Qt.shape[2], Dh = Qt.shape[3], Sk = Kt.shape[2];
   if (Vt.shape[3] != Dh || Vt.shape[2] != Sk || !attention_supported((int)Dh)) return false;
   if (!(out_dtype == DType::BF16 || out_dtype == DType::F32)) return false;
-  if (!(p_dtype == DType::BF16 || p_dtype == DType::F32)) return false;
+  if (p_dtype != DType::BF16) return false;  // the kernel rounds P to bf16 for the P·V MFMA
 
   View vq = view_of(q), vk = view_of(k), vv = view_of(vnode);
   const Node& rn = g_.nodes[root];
-  int out = temp_or(target, rn.type);
   Step st{};
   st.kind = Step::ATTENTION;
   st.name = "attention_fwd";
@@ -1604,6 +1605,10 @@ bool Planner::try_attention(int d2, int target, DType out_dtype, int root) {
   A.q = (const void*)(uintptr_t)(vq.offset * 2);
   A.k = (const void*)(uintptr_t)(vk.offset * 2);
   A.v = (const void*)(uintptr_t)(vv.offset * 2);
+  // the launcher's preconditions, checked here on the operands' offsets (slots are 256-byte aligned) so that a
+  // graph the kernel cannot run takes the unfused path instead of failing at execute time
+  if (attention_unsupported(A)) return false;
+  int out = temp_or(target, rn.type);
   st.patches = {{offsetof(AttnArgs, q), vq.slot}, {offsetof(AttnArgs, k), vk.slot}, {offsetof(AttnArgs, v), vv.slot},
                 {offsetof(AttnArgs, o), out}};
   double pairs = causal ? (double)Sq * (double)(Sk + 1) / 2.0 : (double)Sq * (double)Sk;  // Sq == Sk for causal

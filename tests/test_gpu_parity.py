@@ -183,6 +183,30 @@ def test_c4_attention_full_sampled(gpu_client):
         assert err <= w.tolerance
 
 
+@pytest.mark.parametrize("kw", [dict(s=200), dict(s=96, d=64), dict(fill="-3.40282347E+38"), dict(p_type="f32")])
+def test_c4_attention_graphs_the_kernel_declines(gpu_client, kw):
+    """Attention graphs outside the fused kernel's preconditions run unfused and match the oracle."""
+    base = dict(b=1, h=2, s=256, d=128)
+    base.update(kw)
+    outs, exe = _run_and_check(gpu_client, configs.c4_causal_attention(**base))
+    assert "attention_fwd" not in exe.describe_plan()
+
+
+def test_c4_strict_mask_first_row_is_nan(gpu_client):
+    """A strict causal mask (key < query) leaves query 0 with no visible key: with the -inf fill its reduce-max is
+    -inf, exp(-inf - -inf) is NaN, so StableHLO gives a NaN row; every other row matches the oracle."""
+    w = configs.c4_causal_attention(b=1, h=2, s=256, d=128, mask="GT")
+    outs, exe = run_pjrt(gpu_client, w.program, w.inputs)
+    assert "attention_fwd" not in exe.describe_plan()
+    (want, dt), = oracle_outputs(w.program, w.inputs)
+    got = sh.from_raw(outs[0], dt)
+    assert np.all(np.isnan(want[:, :, 0])) and np.all(np.isnan(got[:, :, 0]))
+    assert np.all(np.isfinite(got[:, :, 1:]))
+    err = sh.rel_error(got[:, :, 1:], want[:, :, 1:])
+    print(f"[parity] c4 strict mask rows 1.. error {err:.3e}", flush=True)
+    assert err <= w.tolerance
+
+
 @pytest.mark.parametrize("kw,kernel", [(dict(m=256, d=512, f=1024), "gemm_bf16f8_mfma_dual_256x128"),
                                        (dict(m=128, d=256, f=512), "gemm_bf16f8_mfma_dual_128x128"),
                                        (dict(m=64, d=256, f=384), "gemm_generic")])

@@ -407,6 +407,25 @@ def test_attention_not_fused_when_intermediate_escapes(compile_client):
     assert exe.executable().output_count() == 2
 
 
+@pytest.mark.parametrize("name,kw", [
+    ("s200", dict(s=200)),                        # not a multiple of the 128-query block
+    ("s96", dict(s=96)),
+    ("strict_mask", dict(mask="GT")),             # query 0 sees no key: NaN under the -inf fill
+    ("finite_fill", dict(fill="-3.40282347E+38")),
+    ("f32_probabilities", dict(p_type="f32")),    # P·V asks for f32 P; the kernel rounds P to bf16
+])
+def test_attention_declined_when_the_kernel_cannot_run_it(compile_client, name, kw):
+    """The fused kernel's preconditions are checked when planning: a graph it cannot run (or would compute
+    differently) plans to the unfused steps instead of failing or deviating at execute time."""
+    base = dict(b=1, h=2, s=256, d=128)
+    base.update(kw)
+    w = configs.c4_causal_attention(**base)
+    exe, kernels = _plan(compile_client, w.program)
+    assert "attention_fwd" not in kernels, (name, kernels)
+    _, kernels = _plan(compile_client, configs.c4_causal_attention(b=1, h=2, s=256, d=128).program)
+    assert "attention_fwd" in kernels
+
+
 @pytest.mark.parametrize("name,build,reductions", [
     ("rmsnorm", lambda: row_programs.rmsnorm((16, 4096), "bf16"), 1),
     ("softmax", lambda: row_programs.softmax((4, 8, 200)), 2),
