@@ -1,15 +1,23 @@
-"""Benchmark: one StableHLO workload through the MI355X PJRT plugin (client.compile → resident input buffers →
-execute → await), reported as whole-job TFLOP/s plus the dominant kernel's roofline fraction.
+"""Benchmark: the BASELINE StableHLO graphs through the MI355X PJRT plugin (client.compile → resident input
+buffers → execute → await), reported as whole-job TFLOP/s (GB/s for the memory-bound calibrations) plus each
+graph's dominant kernel against its roofline.
 
-A step is one execution of the config's StableHLO module on inputs already resident in HBM. Steps are enqueued
-back to back (async dispatch, like a JAX-style caller) and the timed region ends when the last step's done event is
-ready; the per-step latency with an await after every execute is reported alongside. Kernel durations come from
-HIP events recorded on the plugin's stream around each launch (the plugin's timing extension), in a separate pass.
+A step is one execution of a graph's StableHLO module on inputs already resident in HBM. Steps are enqueued back to
+back (async dispatch, like a JAX-style caller) and the timed region ends when the last step's done event is ready;
+the per-step latency with an await after every execute is reported alongside. Kernel durations come from HIP events
+recorded on the plugin's stream by each step's first and last kernel launch (the plugin's timing extension), in a
+separate pass; the roofline uses their median.
+
+With no --config every graph runs: C5 (the largest, by FLOPs) is the headline line's `value`, and `per_graph`
+holds C1–C5 plus the two HBM calibrations (copy, rmsnorm), each with its own value, kernels, roofline and CPU
+baseline. HBM traffic and MFMA utilisation come from rocprofv3 counter runs committed under profiles/
+(counters_<workload>.json): MFMA busy = (SQ_VALU_MFMA_BUSY_CYCLES / 1024 SIMDs) / (SQ_BUSY_CU_CYCLES / 256 CUs).
 
 The cyclic garbage collector is paused during the timed region (as `timeit` does); the plugin's own work is
 unchanged.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2] [--cpu-seconds 10]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config all|c1|c2|c3|c4|c5|c5x|copy|rmsnorm]
+                       [--cpu-seconds S] [--no-cpu-baseline]
 """
 import argparse
 import gc
@@ -22,6 +30,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "TFLOP/s and % of MFMA/HBM roofline per StableHLO graph on 1 MI355X vs XLA CPU"
+HEADLINE = "c5"
+ALL = ["c5", "c1", "c2", "c3", "c4", "copy", "rmsnorm"]
+CHOICES = ["all", "c1", "c2", "c3", "c4", "c5", "c5x", "copy", "rmsnorm"]
 
 
 def _workload(name):
@@ -29,10 +40,31 @@ def _workload(name):
     return configs.CONFIGS[name]()
 
 
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _blas_threads():
+    try:
+        from threadpoolctl import threadpool_info
+        n = [p["num_threads"] for p in threadpool_info() if p.get("user_api") == "blas"]
+        if n:
+            return max(n)
+    except Exception:
+        pass
+    return int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+
+
 def _cpu_baseline(name, seconds):
     """The oracle (a numpy port of the StableHLO semantics, dots as f32 GEMMs the way XLA's CPU backend upcasts
     bf16) timed on a bounded sample of the same workload on this host's cores."""
-    import numpy as np
     from oracle import stablehlo as sh
     from ryft_amd import configs
     from tests.helpers import MLIR_DT
@@ -58,35 +90,29 @@ def _cpu_baseline(name, seconds):
         el = time.perf_counter() - t0
         if el >= seconds or reps >= 1000:
             break
-    cores = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    threads = _blas_threads()
+    what = (f"{desc}, {reps} evaluation(s) in {el:.1f} s (numpy oracle: f32 dots on {threads} BLAS threads, "
+            f"other ops single-threaded; host {_cpu_model()}, {os.cpu_count()} logical CPUs visible)")
     if not w.flops:
-        return {"value": w.bytes * reps / el / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
-                "sample": f"{desc}, {reps} evaluation(s) in {el:.1f} s (numpy oracle)"}
-    return {"value": w.flops * reps / el / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
-            "sample": f"{desc}, {reps} evaluation(s) in {el:.1f} s (numpy oracle, f32 dots)"}
+        return {"value": round(w.bytes * reps / el / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+                "sample": what}
+    return {"value": round(w.flops * reps / el / 1e12, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": what}
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "c5x", "copy", "rmsnorm"],
-                    help="c1..c5: the BASELINE configs (c2 is the headline); copy: the HBM calibration kernel")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported in this build "
-              "(no multi-GPU path; see the sharding notes in DESIGN.md)", file=sys.stderr)
-        sys.exit(2)
+def _counters(workload_name, kernel):
+    """HBM bytes per launch, MFMA busy fraction and shader clock of `kernel` from the committed counter runs."""
+    path = os.path.join(ROOT, "profiles", f"counters_{workload_name}.json")
+    if not os.path.exists(path):
+        return {}
+    with open(path) as f:
+        return json.load(f).get(kernel, {})
 
+
+def measure(name, steps, warmup, cpu_seconds, client, dev):
     from ryft_amd import configs, pjrt
 
-    w = _workload(args.config)
-    plugin = pjrt.load_plugin()
-    client = plugin.client()
-    dev = client.addressable_devices()[0]
+    w = _workload(name)
     exe = client.compile(pjrt.Program.mlir(w.program))
     bufs = [client.buffer(x.data, x.type, x.dims, device=dev) for x in w.inputs]
     for b in bufs:
@@ -98,7 +124,7 @@ def main():
     # warm-up in the timed pattern (back to back), so the allocator already caches the output blocks that
     # overlapping steps hold
     last = None
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         last = step()
     if last is not None:
         last.done.await_()
@@ -110,22 +136,22 @@ def main():
     gc.disable()
     t0 = time.perf_counter()
     last = None
-    for _ in range(args.steps):
+    for _ in range(steps):
         last = step()
     t_enqueued = time.perf_counter()
     last.done.await_()
     elapsed = time.perf_counter() - t0
     gc.enable()
-    ms_per_step = elapsed / args.steps * 1e3
+    ms_per_step = elapsed / steps * 1e3
 
     # per-step latency with an await after each execute (the README's call pattern)
     t1 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         step().done.await_()
-    ms_sync = (time.perf_counter() - t1) / args.steps * 1e3
+    ms_sync = (time.perf_counter() - t1) / steps * 1e3
 
     # PCIe-inclusive rate (not the headline): host inputs → device buffers → execute → results back to host
-    pcie_steps = max(1, min(args.steps, 5))
+    pcie_steps = max(1, min(steps, 3))
     t2 = time.perf_counter()
     for _ in range(pcie_steps):
         hb = [client.buffer(x.data, x.type, x.dims, device=dev) for x in w.inputs]
@@ -135,9 +161,9 @@ def main():
             o.to_numpy()
     ms_pcie = (time.perf_counter() - t2) / pcie_steps * 1e3
 
-    # kernel timing pass (HIP events on the plugin stream)
+    # kernel timing pass (HIP events on the plugin stream, carried by the launches themselves)
     client.set_kernel_timing(True)
-    for _ in range(args.steps):
+    for _ in range(steps):
         last = step()
     last.done.await_()
     kernels = client.kernel_timing()
@@ -145,47 +171,104 @@ def main():
 
     dom_name, dom = max(kernels.items(), key=lambda kv: kv[1]["total_ms"])
     mfma = dom["flops"] > 0
+    med_s = dom["median_us"] * 1e-6
     if mfma:
-        achieved = dom["flops"] / (dom["avg_us"] * 1e-6) / 1e12
+        achieved = dom["flops"] / med_s / 1e12
         peak = configs.PEAK_TFLOPS[w.compute_dtype]
         unit = "TFLOP/s"
     else:
-        achieved = dom["bytes"] / (dom["avg_us"] * 1e-6) / 1e9
+        achieved = dom["bytes"] / med_s / 1e9
         peak = configs.PEAK_HBM_GBS
         unit = "GB/s"
-    traffic = None
-    tf = os.path.join(ROOT, "profiles", f"traffic_{w.name}.json")
-    if os.path.exists(tf):
-        with open(tf) as f:
-            traffic = json.load(f).get(dom_name)
+    ctr = _counters(w.name, dom_name)
     roofline = {"bound": "mfma" if mfma else "hbm", "achieved": round(achieved, 2), "peak": peak, "unit": unit,
-                "frac": round(achieved / peak, 4), "traffic": traffic, "kernel": dom_name,
-                "kernel_avg_us": round(dom["avg_us"], 2), "work_per_launch": dom["flops"] if mfma else dom["bytes"]}
+                "frac": round(achieved / peak, 4), "traffic": ctr.get("hbm_bytes"), "kernel": dom_name,
+                "kernel_median_us": round(dom["median_us"], 2), "kernel_avg_us": round(dom["avg_us"], 2),
+                "work_per_launch": dom["flops"] if mfma else dom["bytes"]}
+    mdt = w.info.get("mfma_dtype")
+    if mfma and mdt and mdt != w.compute_dtype:  # C5: fp8 weights on the bf16 MFMA (exact widening)
+        roofline["frac_vs_" + mdt + "_peak"] = round(achieved / configs.PEAK_TFLOPS[mdt], 4)
+        roofline["mfma_dtype"] = mdt
+    if "mfma_busy" in ctr:
+        roofline["mfma_busy"] = ctr["mfma_busy"]
+    if "shader_mhz" in ctr:
+        roofline["shader_mhz"] = ctr["shader_mhz"]
 
-    cpu = None if args.no_cpu_baseline else _cpu_baseline(args.config, args.cpu_seconds)
     if w.flops:
         value, vunit = w.flops / (ms_per_step * 1e-3) / 1e12, "TFLOP/s"
-    else:  # the copy calibration workload is priced in bytes
+    else:  # the calibration workloads are priced in bytes
         value, vunit = w.bytes / (ms_per_step * 1e-3) / 1e9, "GB/s"
-    dtype = {"f32": "f32", "bf16": "bf16", "int8": "int8", "fp8": "fp8"}[w.compute_dtype]
-    shapes = {x_i: list(x.dims) for x_i, x in enumerate(w.inputs)}
-    line = {
-        "metric": METRIC, "value": round(value, 2), "unit": vunit, "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": dtype,
-        "data": "synthetic (seeded splitmix64 inputs with the BASELINE.json distributions)",
-        "config": {"workload": w.name, "input_shapes": shapes, "flops_per_step": w.flops,
-                   "bytes_per_step": w.bytes, "ms_per_step_await_each": round(ms_sync, 4),
-                   "host_enqueue_us_per_step": round((t_enqueued - t0) / args.steps * 1e6, 2),
-                   "pcie_inclusive": {"ms_per_step": round(ms_pcie, 3),
-                                      "value": round((w.flops or w.bytes) / (ms_pcie * 1e-3) / (1e12 if w.flops else 1e9), 2),
-                                      "steps": pcie_steps,
-                                      "what": "host buffers uploaded, executed, outputs copied back to host memory"},
-                   "kernels": {k: {"avg_us": round(v["avg_us"], 2), "count_per_step": v["count"] / args.steps}
-                               for k, v in kernels.items()}},
+    dtype = {"f32": "f32", "bf16": "bf16", "int8": "int8", "fp8": "fp8"}[mdt or w.compute_dtype]
+    result = {
+        "value": round(value, 2), "unit": vunit, "ms_per_step": round(ms_per_step, 4), "dtype": dtype,
+        "workload": w.name, "input_shapes": {i: list(x.dims) for i, x in enumerate(w.inputs)},
+        "flops_per_step": w.flops, "bytes_per_step": w.bytes, "ms_per_step_await_each": round(ms_sync, 4),
+        "host_enqueue_us_per_step": round((t_enqueued - t0) / steps * 1e6, 2),
+        "pcie_inclusive": {"ms_per_step": round(ms_pcie, 3),
+                           "value": round((w.flops or w.bytes) / (ms_pcie * 1e-3) / (1e12 if w.flops else 1e9), 3),
+                           "steps": pcie_steps,
+                           "what": "host buffers uploaded, executed, outputs copied back to host memory"},
+        "kernels": {k: {"median_us": round(v["median_us"], 2), "avg_us": round(v["avg_us"], 2),
+                        "count_per_step": v["count"] / steps} for k, v in kernels.items()},
         "roofline": roofline,
-        "cpu_baseline": cpu,
+        "cpu_baseline": None if cpu_seconds <= 0 else _cpu_baseline(name, cpu_seconds),
     }
+    if w.info.get("baseline_config") is False or name in ("copy", "rmsnorm"):
+        result["note"] = "calibration / extra workload, not a BASELINE config"
+    del exe, bufs
+    return result
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="all", choices=CHOICES,
+                    help="all (default): every BASELINE graph plus the HBM calibrations, C5 as the headline; "
+                         "or one workload, which then is the headline")
+    ap.add_argument("--cpu-seconds", type=float, default=4.0, help="CPU baseline sample length per graph")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported in this build "
+              "(no multi-GPU path; see the sharding notes in DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    if args.steps < 1:
+        print("--steps must be at least 1", file=sys.stderr)
+        sys.exit(2)
+
+    from ryft_amd import pjrt
+
+    names = ALL if args.config == "all" else [args.config]
+    head = HEADLINE if args.config == "all" else args.config
+    plugin = pjrt.load_plugin()
+    client = plugin.client()
+    dev = client.addressable_devices()[0]
+    cpu_s = 0.0 if args.no_cpu_baseline else args.cpu_seconds
+    per = {}
+    for n in names:
+        t = time.perf_counter()
+        per[n] = measure(n, args.steps, args.warmup, cpu_s, client, dev)
+        print(f"[bench] {n}: {per[n]['value']} {per[n]['unit']}, kernel {per[n]['roofline']['kernel']} "
+              f"frac {per[n]['roofline']['frac']} ({time.perf_counter() - t:.1f} s)", file=sys.stderr, flush=True)
+
+    h = per[head]
+    config = {k: h[k] for k in ("workload", "input_shapes", "flops_per_step", "bytes_per_step",
+                                "ms_per_step_await_each", "host_enqueue_us_per_step", "pcie_inclusive", "kernels")}
+    if head == "c5":
+        config["weights_dtype"] = "f8E4M3FN (widened exactly to bf16 for the bf16 MFMA)"
+    line = {
+        "metric": METRIC, "value": h["value"], "unit": h["unit"], "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": h["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": h["dtype"],
+        "data": "synthetic (seeded splitmix64 inputs with the BASELINE.json distributions)",
+        "config": config,
+        "roofline": h["roofline"],
+        "cpu_baseline": h["cpu_baseline"],
+    }
+    if len(names) > 1:
+        line["per_graph"] = {n: {k: v for k, v in r.items() if k != "input_shapes"} for n, r in per.items()}
     print(json.dumps(line), flush=True)
 
 

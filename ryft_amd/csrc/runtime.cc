@@ -603,6 +603,64 @@ std::shared_ptr<Executable> deserialize_executable(Client* c, const char* data, 
 }
 
 // ------------------------------------------------------------------------------------------------ execute
+bool enqueue_steps(Client* c, const Plan& plan, void* const* ptr, hipStream_t st, hipEvent_t done, bool prof) {
+  constexpr size_t kBlock = std::max({sizeof(EwProgram), sizeof(ReduceArgs), sizeof(GemmArgs), sizeof(RowArgs),
+                                      sizeof(AttnArgs)});
+  alignas(64) static thread_local unsigned char block[kBlock + 64];
+  bool recorded = false;
+  for (size_t si = 0; si < plan.steps.size(); ++si) {
+    const Step& step = plan.steps[si];
+    hipEvent_t carry = (!prof && si + 1 == plan.steps.size() && step.kind != Step::COPY) ? done : nullptr;
+    recorded |= carry != nullptr;
+    StepTiming tm;
+    if (prof) {
+      tm.name = step.name;
+      tm.flops = step.flops;
+      tm.bytes = step.bytes;
+      HIP_CHECK(hipEventCreate(&tm.start));
+      HIP_CHECK(hipEventCreate(&tm.stop));
+      // kernel steps: the first launch records the start, the last the stop (the kernels' own duration)
+      if (step.kind == Step::COPY) HIP_CHECK(hipEventRecord(tm.start, st));
+      else pending_start() = tm.start;
+    }
+    if (step.kind == Step::COPY) {
+      void* src = (char*)ptr[step.patches[0].second] + step.copy.src_offset;
+      void* dst = ptr[step.patches[1].second];
+      if (step.copy.bytes) HIP_CHECK(hipMemcpyAsync(dst, src, (size_t)step.copy.bytes, hipMemcpyDeviceToDevice, st));
+    } else {
+      size_t sz = step.kind == Step::ELEMENTWISE ? sizeof(EwProgram)
+                  : step.kind == Step::REDUCE    ? sizeof(ReduceArgs)
+                  : step.kind == Step::GEMM      ? sizeof(GemmArgs)
+                  : step.kind == Step::ROW       ? sizeof(RowArgs)
+                                                 : sizeof(AttnArgs);
+      memcpy(block, const_cast<Step&>(step).args_block(), sz);
+      for (auto& p : step.patches) {
+        void** f = (void**)(block + p.first);
+        *f = (char*)ptr[p.second] + (uintptr_t)(*f);
+      }
+      hipEvent_t last = prof ? tm.stop : carry;
+      switch (step.kind) {
+        case Step::ELEMENTWISE: launch_elementwise(*(EwProgram*)block, st, last); break;
+        case Step::REDUCE: launch_reduce(*(ReduceArgs*)block, st, last); break;
+        case Step::ROW: launch_row(*(RowArgs*)block, st, last); break;
+        case Step::GEMM: launch_gemm(*(GemmArgs*)block, st, last); break;
+        case Step::ATTENTION: launch_attention(*(AttnArgs*)block, st, last); break;
+        default: recorded = false; break;
+      }
+      if (hipEvent_t unused = pending_start()) {  // no launch took it
+        pending_start() = nullptr;
+        HIP_CHECK(hipEventRecord(unused, st));
+      }
+    }
+    if (prof) {
+      if (step.kind == Step::COPY) HIP_CHECK(hipEventRecord(tm.stop, st));
+      std::lock_guard<std::mutex> pl(c->prof_mu);
+      c->timings.push_back(tm);
+    }
+  }
+  return recorded;
+}
+
 EventPtr execute(LoadedExecutable* le, Device* d, Buffer* const* args, size_t num_args, std::vector<Buffer*>* outputs) {
   Executable& exe = *le->exe;
   const Plan& plan = exe.plan;
@@ -642,64 +700,11 @@ EventPtr execute(LoadedExecutable* le, Device* d, Buffer* const* args, size_t nu
       std::lock_guard<std::mutex> pl(c->prof_mu);
       prof = c->profiling;
     }
-    constexpr size_t kBlock = std::max({sizeof(EwProgram), sizeof(ReduceArgs), sizeof(GemmArgs), sizeof(RowArgs),
-                                        sizeof(AttnArgs)});
-    alignas(64) static thread_local unsigned char block[kBlock + 64];
     // The execution's completion event rides on its last kernel launch when it can (no separate marker packet
     // between consecutive executions); otherwise it is recorded after the last step.
     done = std::make_shared<EventState>();
     HIP_CHECK(hipEventCreateWithFlags(&done->hip_event, hipEventDisableTiming));
-    bool recorded = false;
-    for (size_t si = 0; si < plan.steps.size(); ++si) {
-      const Step& step = plan.steps[si];
-      hipEvent_t carry = (!prof && si + 1 == plan.steps.size() && step.kind != Step::COPY) ? done->hip_event : nullptr;
-      recorded |= carry != nullptr;
-      StepTiming tm;
-      if (prof) {
-        tm.name = step.name;
-        tm.flops = step.flops;
-        tm.bytes = step.bytes;
-        HIP_CHECK(hipEventCreate(&tm.start));
-        HIP_CHECK(hipEventCreate(&tm.stop));
-        // kernel steps: the first launch records the start, the last the stop (the kernels' own duration)
-        if (step.kind == Step::COPY) HIP_CHECK(hipEventRecord(tm.start, st));
-        else pending_start() = tm.start;
-      }
-      if (step.kind == Step::COPY) {
-        void* src = (char*)ptr[step.patches[0].second] + step.copy.src_offset;
-        void* dst = ptr[step.patches[1].second];
-        if (step.copy.bytes) HIP_CHECK(hipMemcpyAsync(dst, src, (size_t)step.copy.bytes, hipMemcpyDeviceToDevice, st));
-      } else {
-        size_t sz = step.kind == Step::ELEMENTWISE ? sizeof(EwProgram)
-                    : step.kind == Step::REDUCE    ? sizeof(ReduceArgs)
-                    : step.kind == Step::GEMM      ? sizeof(GemmArgs)
-                    : step.kind == Step::ROW       ? sizeof(RowArgs)
-                                                   : sizeof(AttnArgs);
-        memcpy(block, const_cast<Step&>(step).args_block(), sz);
-        for (auto& p : step.patches) {
-          void** f = (void**)(block + p.first);
-          *f = (char*)ptr[p.second] + (uintptr_t)(*f);
-        }
-        hipEvent_t last = prof ? tm.stop : carry;
-        switch (step.kind) {
-          case Step::ELEMENTWISE: launch_elementwise(*(EwProgram*)block, st, last); break;
-          case Step::REDUCE: launch_reduce(*(ReduceArgs*)block, st, last); break;
-          case Step::ROW: launch_row(*(RowArgs*)block, st, last); break;
-          case Step::GEMM: launch_gemm(*(GemmArgs*)block, st, last); break;
-          case Step::ATTENTION: launch_attention(*(AttnArgs*)block, st, last); break;
-          default: recorded = false; break;
-        }
-        if (hipEvent_t unused = pending_start()) {  // no launch took it
-          pending_start() = nullptr;
-          HIP_CHECK(hipEventRecord(unused, st));
-        }
-      }
-      if (prof) {
-        if (step.kind == Step::COPY) HIP_CHECK(hipEventRecord(tm.stop, st));
-        std::lock_guard<std::mutex> pl(c->prof_mu);
-        c->timings.push_back(tm);
-      }
-    }
+    const bool recorded = enqueue_steps(c, plan, ptr.data(), st, done->hip_event, prof);
     if (!recorded) HIP_CHECK(hipEventRecord(done->hip_event, st));
     // Nothing runs on this event's completion unless a callback is registered, so it is not queued on the
     // completion worker.
@@ -726,7 +731,11 @@ std::string kernel_timing_json(Client* c) {
     (void)hipSetDevice(d->hip_ordinal);
     HIP_CHECK(hipStreamSynchronize(d->stream));
   }
-  struct Agg { int64_t count = 0; double ms = 0, min_ms = 1e30, max_ms = 0, flops = 0, bytes = 0; };
+  struct Agg {
+    int64_t count = 0;
+    double ms = 0, min_ms = 1e30, max_ms = 0, flops = 0, bytes = 0;
+    std::vector<double> samples;
+  };
   std::map<std::string, Agg> agg;
   std::vector<std::string> order;
   {
@@ -740,6 +749,7 @@ std::string kernel_timing_json(Client* c) {
       a.ms += ms;
       a.min_ms = std::min(a.min_ms, (double)ms);
       a.max_ms = std::max(a.max_ms, (double)ms);
+      a.samples.push_back(ms);
       a.flops += t.flops;
       a.bytes += t.bytes;
       (void)hipEventDestroy(t.start);
@@ -752,7 +762,11 @@ std::string kernel_timing_json(Client* c) {
   bool first = true;
   for (auto& n : order) {
     Agg& a = agg[n];
+    std::sort(a.samples.begin(), a.samples.end());
+    const size_t h = a.samples.size() / 2;
+    const double median = a.samples.size() % 2 ? a.samples[h] : 0.5 * (a.samples[h - 1] + a.samples[h]);
     os << (first ? "" : ",") << "\"" << n << "\":{\"count\":" << a.count << ",\"total_ms\":" << a.ms
+       << ",\"median_us\":" << 1e3 * median
        << ",\"avg_us\":" << 1e3 * a.ms / a.count << ",\"min_us\":" << 1e3 * a.min_ms << ",\"max_us\":" << 1e3 * a.max_ms
        << ",\"flops\":" << a.flops / a.count << ",\"bytes\":" << a.bytes / a.count << "}";
     first = false;

@@ -237,6 +237,10 @@ std::shared_ptr<Executable> compile_program(Client* c, const std::string& code, 
                                             const std::string& options);
 // Enqueues one execution; fills outputs and returns the completion event.
 EventPtr execute(LoadedExecutable* le, Device* d, Buffer* const* args, size_t num_args, std::vector<Buffer*>* outputs);
+// Enqueues every step of `plan` on `st`, slot s living at ptr[s] (the caller has made the plan's device current).
+// `done` (optional) is recorded by the last kernel launch when it can; returns whether it was. With `prof`, each
+// step's first and last launch record timing events appended to c->timings. Allocates no device memory.
+bool enqueue_steps(Client* c, const Plan& plan, void* const* ptr, hipStream_t st, hipEvent_t done, bool prof);
 // Copies a buffer to another buffer on the same device.
 Buffer* copy_buffer(Buffer* src, Device* d);
 
