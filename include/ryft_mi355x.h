@@ -38,6 +38,28 @@ typedef struct RYFT_MI355X_Extension {
   PJRT_Error* (*describe_plan)(PJRT_LoadedExecutable* executable, const char** text, size_t* text_size);
 } RYFT_MI355X_Extension;
 
+/*
+ * Allocation-free execution. No counterpart in the reference (ryft-pjrt's execute path is
+ * PJRT_LoadedExecutable_Execute, crates/ryft-pjrt/src/programs.rs:769-963, which allocates its results); it is for
+ * callers that cannot allocate device memory: code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc.
+ *
+ * Enqueues one execution of `executable` (a PJRT_LoadedExecutable of this plugin, on its first device) on `stream`
+ * (a hipStream_t of that device; null = the device's null stream) and returns without waiting. The caller passes
+ * the device memory of every parameter (`inputs[i]`, `input_sizes[i]` bytes, dense row-major) and every result
+ * (`outputs[o]`, `output_sizes[o]` bytes); sizes must equal the program's and pointers be 256-byte aligned. The
+ * plan's intermediates live in a per-GPU scratch array of 64 MiB that the library holds until the process ends;
+ * an executable needing more is rejected with RESOURCE_EXHAUSTED. Nothing is allocated on the device (no hipMalloc,
+ * no hipFree) and no event is created. Calls that overlap on one GPU share that scratch and race; the caller orders
+ * the producers of the inputs before the call and waits on `stream` before reading the outputs.
+ *
+ * Returns 0 on success, else a PJRT_Error_Code; `*error_message` (if non-null) then points at a description that
+ * stays valid until the calling thread's next call.
+ */
+int RyftMi355x_ExecuteNoAlloc(PJRT_LoadedExecutable* executable, const void* const* inputs, const size_t* input_sizes,
+                              size_t num_inputs, void* const* outputs, const size_t* output_sizes, size_t num_outputs,
+                              void* stream, const char** error_message);
+
 #ifdef __cplusplus
 }
 #endif

@@ -221,6 +221,7 @@ Client::Client(const std::vector<int>& visible, bool compile_only) {
     d->attribute_strings = {"device_vendor", "AMD", "gfx_arch", arch, "core_count"};
     HIP_CHECK(hipSetDevice(o));
     HIP_CHECK(hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking));
+    (void)noalloc_scratch(o);  // set-up of the allocation-free entry point on this device (retried on its first call)
     d->allocator = std::make_unique<DeviceAllocator>(o);
     auto m = std::make_unique<Memory>();
     m->client = this;

@@ -241,6 +241,10 @@ EventPtr execute(LoadedExecutable* le, Device* d, Buffer* const* args, size_t nu
 // `done` (optional) is recorded by the last kernel launch when it can; returns whether it was. With `prof`, each
 // step's first and last launch record timing events appended to c->timings. Allocates no device memory.
 bool enqueue_steps(Client* c, const Plan& plan, void* const* ptr, hipStream_t st, hipEvent_t done, bool prof);
+// Device address of the allocation-free entry point's scratch array on a GPU (looked up once per device, with
+// that device current; null if the lookup fails), and its size.
+void* noalloc_scratch(int hip_ordinal);
+size_t noalloc_scratch_bytes();
 // Copies a buffer to another buffer on the same device.
 Buffer* copy_buffer(Buffer* src, Device* d);
 

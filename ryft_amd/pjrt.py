@@ -249,6 +249,11 @@ for _n, _f in {
                                       ("argument_lists", C.POINTER(C.POINTER(_vp))), ("num_devices", _sz),
                                       ("num_args", _sz), ("output_lists", C.POINTER(C.POINTER(_vp))),
                                       ("device_complete_events", C.POINTER(_vp)), ("execute_device", _vp)],
+    "PJRT_Client_CreateUninitializedBuffer": [("client", _vp), ("shape_dims", C.POINTER(C.c_int64)),
+                                              ("shape_num_dims", _sz), ("shape_element_type", C.c_uint),
+                                              ("shape_layout", _vp), ("device", _vp), ("memory", _vp),
+                                              ("buffer", _vp)],
+    "PJRT_Buffer_UnsafePointer": [("buffer", _vp), ("buffer_pointer", C.c_size_t)],
     "PJRT_Buffer_Destroy": [("buffer", _vp)],
     "PJRT_Buffer_ElementType": [("buffer", _vp), ("type", C.c_uint)],
     "PJRT_Buffer_Dimensions": [("buffer", _vp), ("dims", C.POINTER(C.c_int64)), ("num_dims", _sz)],
@@ -750,6 +755,10 @@ class Buffer(_Owned):
         ext = self.api.layouts_extension()
         return Layout(ext, ext.call("PJRT_Layouts_PJRT_Buffer_MemoryLayout", buffer=self.handle).layout, False)
 
+    def unsafe_pointer(self) -> int:
+        """Buffer::unsafe_pointer (buffers.rs:1500-1505): the device address of the buffer's bytes."""
+        return int(self.api.call("PJRT_Buffer_UnsafePointer", buffer=self.handle).buffer_pointer)
+
     def copy_to_host(self) -> Event:
         """ToHostBuffer twice: size query with dst=null, then the copy (buffers.rs:1237-1266)."""
         size = self.api.call("PJRT_Buffer_ToHostBuffer", src=self.handle, dst=None).dst_size
@@ -1241,6 +1250,18 @@ class Client(_Owned):
                           device=None, memory=memory.handle, device_layout=None, **kw)
         if a.done_with_host_buffer:
             Event(self.api, a.done_with_host_buffer)  # dropped, as ryft-pjrt does
+        return Buffer(self, a.buffer)
+
+    def uninitialized_buffer(self, element_type: BufferType, dims: Sequence[int],
+                             memory: Optional[Memory] = None) -> Buffer:
+        """Client::uninitialized_buffer (buffers.rs:2229-2252): a device buffer of the given type and dimensions whose
+        bytes are unspecified, placed in `memory` (default: the first device's default memory); device = null."""
+        if memory is None:
+            memory = self.addressable_devices()[0].default_memory()
+        dims_arr = (C.c_int64 * max(len(dims), 1))(*dims)
+        a = self.api.call("PJRT_Client_CreateUninitializedBuffer", client=self.handle, shape_dims=dims_arr,
+                          shape_num_dims=len(dims), shape_element_type=int(element_type), shape_layout=None,
+                          device=None, memory=memory.handle)
         return Buffer(self, a.buffer)
 
     # --- plugin extension: kernel timing on the device stream

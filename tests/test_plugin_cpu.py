@@ -15,18 +15,19 @@ from ryft_amd import configs, pjrt
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def test_library_exports_only_get_pjrt_api():
+def test_library_exports_only_its_entry_points():
+    # GetPjrtApi (what load_plugin resolves) and the allocation-free execute entry point; nothing else
     out = subprocess.run(["nm", "-D", "--defined-only", pjrt.DEFAULT_PLUGIN_PATH], capture_output=True, text=True,
                          check=True).stdout
     syms = sorted({ln.split()[-1].split("@")[0] for ln in out.splitlines() if ln.strip()})
-    assert syms == ["GetPjrtApi"]
+    assert syms == ["GetPjrtApi", "RyftMi355x_ExecuteNoAlloc"]
 
 
 def test_header_declares_what_the_library_exports():
     header = open(os.path.join(ROOT, "include", "ryft_mi355x.h")).read()
-    decls = re.findall(r"^\s*(?:const\s+)?\w+\*?\s+(\w+)\(void\);", header, re.M)
+    decls = re.findall(r"^(?:const\s+)?\w+\*?\s+(\w+)\(", header, re.M)
     lib = ctypes.CDLL(pjrt.DEFAULT_PLUGIN_PATH)
-    assert decls == ["GetPjrtApi"]
+    assert decls == ["GetPjrtApi", "RyftMi355x_ExecuteNoAlloc"]
     for d in decls:
         assert hasattr(lib, d)
 
