@@ -238,79 +238,56 @@ struct TileCopyLoader {
   }
 };
 
-// f8E4M3FN → bf16, 16 values: v_cvt_scalef32_pk_bf16_fp8 widens two bytes of a word per instruction. Exact: every
-// f8E4M3FN value (subnormals included) is a bf16 value and the unit scale multiplies exactly; NaN stays NaN.
-typedef __bf16 bf16x2_g __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ void f8x16_to_bf16(const u32x4& v, u32x4& lo, u32x4& hi) {
+// f8E4M3FN → bf16, 8 values (one 8-byte piece → one 16-byte chunk): v_cvt_scalef32_pk_bf16_fp8 widens two bytes of
+// a word per instruction. Exact: every f8E4M3FN value (subnormals included) is a bf16 value and the unit scale
+// multiplies exactly; NaN stays NaN.
+typedef uint32_t u32x2w __attribute__((__vector_size__(2 * sizeof(uint32_t))));
+__device__ __forceinline__ u32x4 f8x8_to_bf16(const u32x2w& v) {
 #define RYFT_W(x, s) __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((x), 1.0f, (s)))
-  lo = u32x4{RYFT_W(v.x, false), RYFT_W(v.x, true), RYFT_W(v.y, false), RYFT_W(v.y, true)};
-  hi = u32x4{RYFT_W(v.z, false), RYFT_W(v.z, true), RYFT_W(v.w, false), RYFT_W(v.w, true)};
+  return u32x4{RYFT_W(v[0], false), RYFT_W(v[0], true), RYFT_W(v[1], false), RYFT_W(v[1], true)};
 #undef RYFT_W
 }
 
-// A row-contiguous f8E4M3FN operand tile (BK k-rows × R bytes in HBM) → bf16 [k][R] rows of LDB bytes in LDS (the
-// layout TileCopyLoader gives a 16-bit operand, read the same way with transposing LDS reads).
-template <int R, int BK, int THREADS>
-struct TileWidenCopyLoader {
-  static constexpr int NTOT = BK * (R / 16);
-  static constexpr int NVEC = NTOT / THREADS;
-  static_assert(NTOT % THREADS == 0, "uneven tile split");
-  u32x4 regs[NVEC];
-  __device__ __forceinline__ void load(const char* base, int64_t sr, int64_t sk, int tid) {
+// An f8E4M3FN operand tile widened to bf16 on its way into LDS, in 8-byte pieces (one 16-byte bf16 chunk each):
+// consecutive lanes take consecutive pieces of one LDS row, so each 16-lane group of a store writes 256 contiguous
+// bytes (conflict-free) and each global read covers whole rows. ROWS rows of PIECES pieces. Used for a K-contiguous
+// B (R n-rows × BK k in HBM → K-packed bf16 rows of LDK bytes, like a 16-bit K-packed operand); an n-contiguous f8 B
+// is copied into LDS unchanged and widened after its transposing read.
+template <int ROWS, int PIECES, int THREADS>
+struct TileWidenPieces {
+  static constexpr int NTOT = ROWS * PIECES;
+  static constexpr int NVEC = (NTOT + THREADS - 1) / THREADS;
+  static constexpr bool PARTIAL = (NTOT % THREADS) != 0;
+  static_assert(!PARTIAL || NVEC == 1, "uneven tile split");
+  u32x2w regs[NVEC];
+  // stride_row: HBM bytes between consecutive LDS rows of the tile (sk for [k][n] tiles, sr for [n][k] tiles)
+  __device__ __forceinline__ void load(const char* base, int64_t stride_row, int tid) {
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, -1, 0x00020000);
-    (void)sr;
 #pragma unroll
     for (int i = 0; i < NVEC; ++i) {
       const int v = tid + i * THREADS;
-      const int k = v / (R / 16), c = v % (R / 16);
-      regs[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)((int64_t)k * sk + (int64_t)c * 16), 0, 0);
+      if (PARTIAL && v >= NTOT) break;
+      const int r = v / PIECES, c = v % PIECES;
+      regs[i] = __builtin_amdgcn_raw_buffer_load_b64(rs, (int)((int64_t)r * stride_row + (int64_t)c * 8), 0, 0);
     }
   }
-  template <int LDB>
+  template <int PITCH>
   __device__ __forceinline__ void store(char* lds, int tid) {
 #pragma unroll
     for (int i = 0; i < NVEC; ++i) {
       const int v = tid + i * THREADS;
-      const int k = v / (R / 16), c = v % (R / 16);
-      u32x4 lo, hi;
-      f8x16_to_bf16(regs[i], lo, hi);
-      *(u32x4*)(lds + k * LDB + c * 32) = lo;
-      *(u32x4*)(lds + k * LDB + c * 32 + 16) = hi;
+      if (PARTIAL && v >= NTOT) break;
+      const int r = v / PIECES, c = v % PIECES;
+      *(u32x4*)(lds + r * PITCH + c * 16) = f8x8_to_bf16(regs[i]);
     }
   }
 };
 
-// A K-contiguous f8E4M3FN operand tile (R rows × BK bytes in HBM) → K-packed bf16 rows of LDK bytes in LDS.
 template <int R, int BK, int THREADS>
-struct TileWidenLoader {
-  static constexpr int NTOT = R * BK / 16;
-  static constexpr int NVEC = (NTOT + THREADS - 1) / THREADS;
-  static constexpr bool PARTIAL = (NTOT % THREADS) != 0;
-  static_assert(!PARTIAL || NVEC == 1, "uneven tile split");
-  u32x4 regs[NVEC];
+struct TileWidenLoader : TileWidenPieces<R, BK / 8, THREADS> {
   __device__ __forceinline__ void load(const char* base, int64_t sr, int64_t sk, int tid) {
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, -1, 0x00020000);
-    (void)sk;
-#pragma unroll
-    for (int i = 0; i < NVEC; ++i) {
-      const int v = tid + i * THREADS;
-      if (PARTIAL && v >= NTOT) break;
-      const int row = v / (BK / 16), kv = v % (BK / 16);
-      regs[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)((int64_t)row * sr + (int64_t)kv * 16), 0, 0);
-    }
-  }
-  template <int LDK>
-  __device__ __forceinline__ void store(char* lds, int tid) {
-#pragma unroll
-    for (int i = 0; i < NVEC; ++i) {
-      const int v = tid + i * THREADS;
-      if (PARTIAL && v >= NTOT) break;
-      const int row = v / (BK / 16), kv = v % (BK / 16);
-      u32x4 lo, hi;
-      f8x16_to_bf16(regs[i], lo, hi);
-      *(u32x4*)(lds + row * LDK + kv * 32) = lo;
-      *(u32x4*)(lds + row * LDK + kv * 32 + 16) = hi;
-    }
+    (void)sk;  // K-contiguous
+    TileWidenPieces<R, BK / 8, THREADS>::load(base, sr, tid);
   }
 };
 
@@ -335,7 +312,7 @@ template <int KIND, int BM, int BN, int BK, int WM, int WN, bool A_R, bool B_R, 
 struct MfmaCfg {
   using M = Mma<KIND>;
   static constexpr int ESIZE = M::ESIZE, KPACK = M::KPACK, MK = 2 * KPACK;
-  static constexpr int BES = b_hbm_size<KIND>();  // B's element size in HBM (1: f8 widened to bf16 in LDS)
+  static constexpr int BES = b_hbm_size<KIND>();  // B's element size in HBM (1: f8 for the bf16 MFMA)
   static constexpr int THREADS = 64 * WM * WN;
   static constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
   static constexpr int LDK = BK * ESIZE + 16;  // LDS row pitch in bytes (16-byte pad)
@@ -345,14 +322,18 @@ struct MfmaCfg {
   // with ds_read_b64_tr_b16 / _b8; otherwise B is K-packed like A ([n][k] rows of pitch LDK, transposed in registers
   // on the way)
   static constexpr bool BTR = B_R && ESIZE <= 2;
-  static constexpr int LDB = BN * ESIZE + (ESIZE == 2 ? 64 : 32);
+  // element size of B in LDS: an n-contiguous f8 B for the bf16 MFMA stays f8 in LDS (half the LDS bytes written
+  // and read) and is widened in registers after its transposing read; a K-contiguous one is widened on its way in
+  static constexpr int BLES = BTR ? BES : ESIZE;
+  static constexpr int LDB = BN * BLES + (BLES == 2 ? 64 : 32);
   static constexpr int BREG = BTR ? BK * LDB : BN * LDK;  // bytes of one B operand tile
   static constexpr int STAGE = BM * LDK + NB * BREG;
-  static constexpr int LDS_BYTES = 2 * STAGE;
   static_assert(BK % MK == 0, "BK must be a multiple of the MFMA K");
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32");
-  // epilogue rounds: the largest number of 32-row tile-rows (dividing TM) whose f32 patches fit in the LDS
+  // epilogue rounds: the largest number of 32-row tile-rows (dividing TM) whose f32 patches fit in the LDS the two
+  // stages occupy (at least one round's worth)
   static constexpr int epi_bytes(int rows) { return WM * WN * NB * rows * 32 * (WTN + 4) * 4; }
+  static constexpr int LDS_BYTES = 2 * STAGE > epi_bytes(1) ? 2 * STAGE : epi_bytes(1);
   static constexpr int EPI_ROWS = (TM % 4 == 0 && epi_bytes(4) <= LDS_BYTES)   ? 4
                                   : (TM % 2 == 0 && epi_bytes(2) <= LDS_BYTES) ? 2
                                                                                : 1;
@@ -577,8 +558,8 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_mfma_kernel(const GemmArgs 
   // One register stage of global prefetch: tile kt + 2 is requested at the start of k-tile kt (right after tile
   // kt + 1 went from registers to LDS), so each load has a whole k-tile of MFMA work to arrive in. Two LDS stages.
   using BLoader = std::conditional_t<
-      BES != ES, std::conditional_t<C::BTR, TileWidenCopyLoader<BN, BK, C::THREADS>, TileWidenLoader<BN, BK, C::THREADS>>,
-      std::conditional_t<C::BTR, TileCopyLoader<ES, BN, BK, C::THREADS>, TileLoader<ES, BN, BK, C::THREADS, B_R>>>;
+      C::BTR, TileCopyLoader<C::BLES, BN, BK, C::THREADS>,
+      std::conditional_t<BES != ES, TileWidenLoader<BN, BK, C::THREADS>, TileLoader<ES, BN, BK, C::THREADS, B_R>>>;
   TileLoader<ES, BM, BK, C::THREADS, A_R> la;
   BLoader lb;
   BLoader lb2;
@@ -612,7 +593,12 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_mfma_kernel(const GemmArgs 
   // Fragments of MFMA k-step s live in register slot s & 1: step s + 1 is read from LDS while step s multiplies.
   constexpr int S = BK / C::MK;
   static_assert(S % 2 == 0, "k-steps per tile must be even (fragment slots alternate)");
-  typename F::T fa[2][C::TM], fb[2][C::TN], fb2[2][DUAL ? C::TN : 1];
+  // f8 B in LDS for the bf16 MFMA: B fragments are kept as the raw bytes of their transposing read and widened
+  // right before the MFMAs that use them, so their LDS reads stay in flight across the previous step's MFMAs
+  constexpr bool BWIDEN = C::BTR && C::BLES == 1 && ES == 2;
+  using BF = std::conditional_t<BWIDEN, u32x2w, typename F::T>;
+  typename F::T fa[2][C::TM];
+  BF fb[2][C::TN], fb2[2][DUAL ? C::TN : 1];
   const int lrow = lane & 31;
   const int lk = (lane >> 5) * C::KPACK * ES;  // byte offset of this lane's k-pack within an MFMA k-step
   const int a_off = (wm * C::WTM + lrow) * C::LDK + lk;
@@ -622,16 +608,19 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_mfma_kernel(const GemmArgs 
   // (8-bit: lane s addresses k-row KPACK·(lane/32) + s/2 and column 16·((lane/16) % 2) + 8·(s % 2); each read
   // delivers 8 consecutive k, KPACK / 8 reads make the fragment.)
   const int b_off = !C::BTR ? BM * C::LDK + (wn * C::WTN + lrow) * C::LDK + lk
-                    : ES == 2 ? BM * C::LDK + (8 * (lane >> 5) + ((lane & 15) >> 2)) * C::LDB +
-                                    (wn * C::WTN + 16 * ((lane >> 4) & 1) + 4 * (lane & 3)) * ES
-                              : BM * C::LDK + (C::KPACK * (lane >> 5) + ((lane & 15) >> 1)) * C::LDB +
-                                    (wn * C::WTN + 16 * ((lane >> 4) & 1) + 8 * (lane & 1)) * ES;
-  auto bfrag = [&](const char* p) -> typename F::T {
+                    : C::BLES == 2 ? BM * C::LDK + (8 * (lane >> 5) + ((lane & 15) >> 2)) * C::LDB +
+                                         (wn * C::WTN + 16 * ((lane >> 4) & 1) + 4 * (lane & 3)) * 2
+                                   : BM * C::LDK + (C::KPACK * (lane >> 5) + ((lane & 15) >> 1)) * C::LDB +
+                                         (wn * C::WTN + 16 * ((lane >> 4) & 1) + 8 * (lane & 1));
+  auto bfrag = [&](const char* p) -> BF {
     if constexpr (!C::BTR) {
       return F::load(p);
-    } else if constexpr (ES == 2) {
+    } else if constexpr (C::BLES == 2) {
       const uint2 lo = lds_read_tr16(p), hi = lds_read_tr16(p + 4 * C::LDB);
       return u32x4{lo.x, lo.y, hi.x, hi.y};
+    } else if constexpr (BWIDEN) {  // one transposing read gives the 8 k of the fragment
+      const uint2 a = lds_read_tr8(p);
+      return u32x2w{a.x, a.y};
     } else if constexpr (C::KPACK == 16) {
       const uint2 a = lds_read_tr8(p), b = lds_read_tr8(p + 8 * C::LDB);
       return u32x4{a.x, a.y, b.x, b.y};
@@ -646,7 +635,7 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_mfma_kernel(const GemmArgs 
     constexpr int ko = decltype(s)::value * C::MK * ES;
     // B fragment j / k-step offset: K-packed rows are n (32 per tile) with k along the row; transposed rows are k
     constexpr int bko = C::BTR ? decltype(s)::value * C::MK * C::LDB : ko;
-    constexpr int bjo = C::BTR ? 32 * ES : 32 * C::LDK;
+    constexpr int bjo = C::BTR ? 32 * C::BLES : 32 * C::LDK;
     const char* st = smem + buf * C::STAGE;
 #pragma unroll
     for (int i = 0; i < C::TM; ++i) fa[SL][i] = F::load(st + a_off + i * 32 * C::LDK + ko);
@@ -685,12 +674,23 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_mfma_kernel(const GemmArgs 
         lfrag(cur ^ 1, int_c<0>{}, int_c<0>{});
       }
       __builtin_amdgcn_sched_barrier(0);
+      typename F::T wb[C::TN], wb2[DUAL ? C::TN : 1];
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j) {
+        if constexpr (BWIDEN) {
+          wb[j] = f8x8_to_bf16(fb[SS & 1][j]);
+          if constexpr (DUAL) wb2[j] = f8x8_to_bf16(fb2[SS & 1][j]);
+        } else {
+          wb[j] = fb[SS & 1][j];
+          if constexpr (DUAL) wb2[j] = fb2[SS & 1][j];
+        }
+      }
 #pragma unroll
       for (int i = 0; i < C::TM; ++i)
 #pragma unroll
         for (int j = 0; j < C::TN; ++j) {
-          acc[i][j] = M::mma(fb[SS & 1][j], fa[SS & 1][i], acc[i][j]);
-          if constexpr (DUAL) acc2[i][j] = M::mma(fb2[SS & 1][j], fa[SS & 1][i], acc2[i][j]);
+          acc[i][j] = M::mma(wb[j], fa[SS & 1][i], acc[i][j]);
+          if constexpr (DUAL) acc2[i][j] = M::mma(wb2[j], fa[SS & 1][i], acc2[i][j]);
         }
       // The LDS store of tile kt + 1 (step 0) and the loads of tile kt + 2 (step 1) are spread between this step's
       // MFMAs, one memory instruction per MFMA: issued as a burst they would queue in the memory pipeline and stall
@@ -770,7 +770,7 @@ struct Choice {
   const void* fn = nullptr;
   int threads = 256;
   int lds = 0;
-  int bm = 0, bn = 0;
+  int bm = 0, bn = 0, bk = 0;
   const char* name = "gemm_generic";
 };
 
@@ -783,11 +783,13 @@ Choice make_choice(const char* name) {
   c.lds = C::LDS_BYTES;
   c.bm = BM;
   c.bn = BN;
+  c.bk = BK;
   c.name = name;
   return c;
 }
 
 // Per-type instantiation pickers (one translation unit each, so the build parallelises). `br`: B is n-contiguous.
+// With g.splits > 1 a picker returns the tile it runs over each of the K ranges (or false if K does not divide).
 bool pick_bf16(const GemmArgs& g, bool br, Choice* c);
 bool pick_f16(const GemmArgs& g, bool br, Choice* c);
 bool pick_i8(const GemmArgs& g, bool br, Choice* c);

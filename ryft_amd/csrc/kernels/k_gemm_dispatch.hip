@@ -228,13 +228,16 @@ int gemm_plan_splits(const GemmArgs& a) {
   // 128×128 tile, from L2 as well as LDS: splitting K over 128×128 tiles beats it
   const bool small_tile = !f32 && c.bm < 128;
   if (tiles >= 192 && !small_tile) return 1;  // the chip (256 CUs) is already covered well enough
-  // the split tile: 128×128 (64×64 for f32) over each K range; at least 4 k-tiles per range
-  const int tm = f32 ? 64 : 128, tk = f32 ? 16 : (g.A.dtype == DT_BF16 || g.A.dtype == DT_F16 ? 64 : 128);
-  if (g.M % tm || g.N % tm || g.dual) return 1;
-  const int64_t tiles_s = (int64_t)(g.M / tm) * (g.N / tm) * g.batch;
+  if (g.dual) return 1;
+  // the split tile: the one the picker runs over each K range (probed with two ranges); at least 4 k-tiles per range
+  GemmArgs probe = g;
+  probe.splits = 2;
+  Choice sc;
+  if (!pick_mfma(probe, &sc)) return 1;
+  const int64_t tiles_s = (int64_t)(g.M / sc.bm) * (g.N / sc.bn) * g.batch;
   int best = 1;
   for (int s = 2; s <= 16; s *= 2) {
-    if (tiles_s * s > 256 || g.K % (tk * s) || g.K / (tk * s) < 4) break;
+    if (tiles_s * s > 256 || g.K % (sc.bk * s) || g.K / (sc.bk * s) < 4) break;
     best = s;
   }
   if (best < 2 || (!small_tile && tiles_s * best <= tiles)) return 1;

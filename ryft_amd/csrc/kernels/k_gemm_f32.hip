@@ -5,13 +5,10 @@ namespace ryft {
 
 bool pick_f32(const GemmArgs& g, bool br, Choice* c) {
   auto fits = [&](int bm, int bn, int bk) { return g.M % bm == 0 && g.N % bn == 0 && g.K % bk == 0; };
-  const bool dual = g.dual != 0;
-  const int64_t tiles256 = (int64_t)(g.M / 256) * (g.N / 256) * g.batch;
-  (void)dual; (void)tiles256;
-    if (dual || !fits(64, 64, 16 * (g.splits > 1 ? g.splits : 1))) return false;
-    *c = br ? make_choice<MMA_F32, 64, 64, 16, 2, 2, false, true, false>("gemm_f32_mfma_64x64")
-            : make_choice<MMA_F32, 64, 64, 16, 2, 2, false, false, false>("gemm_f32_mfma_64x64");
-    return true;
+  if (g.dual || !fits(64, 64, 16 * (g.splits > 1 ? g.splits : 1))) return false;
+  *c = br ? make_choice<MMA_F32, 64, 64, 16, 2, 2, false, true, false>("gemm_f32_mfma_64x64")
+          : make_choice<MMA_F32, 64, 64, 16, 2, 2, false, false, false>("gemm_f32_mfma_64x64");
+  return true;
 }
 
 }  // namespace ryft

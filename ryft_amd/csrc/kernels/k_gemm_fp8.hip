@@ -5,32 +5,29 @@ namespace ryft {
 
 bool pick_fp8(const GemmArgs& g, bool br, Choice* c) {
   auto fits = [&](int bm, int bn, int bk) { return g.M % bm == 0 && g.N % bn == 0 && g.K % bk == 0; };
-  const bool dual = g.dual != 0;
-  const int64_t tiles256 = (int64_t)(g.M / 256) * (g.N / 256) * g.batch;
-  (void)dual; (void)tiles256;
-    if (g.splits > 1) {  // split-K runs the 128×128 tile over each K range
-      if (dual || !fits(128, 128, 128 * g.splits)) return false;
-      *c = br ? make_choice<MMA_FP8, 128, 128, 128, 2, 2, false, true, false>("gemm_fp8_mfma_128x128")
-              : make_choice<MMA_FP8, 128, 128, 128, 2, 2, false, false, false>("gemm_fp8_mfma_128x128");
-      return true;
-    }
-    if (dual) {
-      if (!fits(128, 128, 128)) return false;
-      *c = br ? make_choice<MMA_FP8, 128, 128, 128, 2, 2, false, true, true>("gemm_fp8_mfma_dual_128x128")
-              : make_choice<MMA_FP8, 128, 128, 128, 2, 2, false, false, true>("gemm_fp8_mfma_dual_128x128");
-      return true;
-    }
-    if (fits(128, 128, 128) && (int64_t)(g.M / 128) * (g.N / 128) * g.batch >= 256) {
-      *c = br ? make_choice<MMA_FP8, 128, 128, 128, 2, 2, false, true, false>("gemm_fp8_mfma_128x128")
-              : make_choice<MMA_FP8, 128, 128, 128, 2, 2, false, false, false>("gemm_fp8_mfma_128x128");
-      return true;
-    }
-    if (fits(64, 128, 128)) {
-      *c = br ? make_choice<MMA_FP8, 64, 128, 128, 2, 2, false, true, false>("gemm_fp8_mfma_64x128")
-              : make_choice<MMA_FP8, 64, 128, 128, 2, 2, false, false, false>("gemm_fp8_mfma_64x128");
-      return true;
-    }
-    return false;
+  if (g.splits > 1) {  // split-K runs the 128×128 tile over each K range
+    if (g.dual || !fits(128, 128, 128 * g.splits)) return false;
+    *c = br ? make_choice<MMA_FP8, 128, 128, 128, 2, 2, false, true, false>("gemm_fp8_mfma_128x128")
+            : make_choice<MMA_FP8, 128, 128, 128, 2, 2, false, false, false>("gemm_fp8_mfma_128x128");
+    return true;
+  }
+  if (g.dual) {
+    if (!fits(128, 128, 128)) return false;
+    *c = br ? make_choice<MMA_FP8, 128, 128, 128, 2, 2, false, true, true>("gemm_fp8_mfma_dual_128x128")
+            : make_choice<MMA_FP8, 128, 128, 128, 2, 2, false, false, true>("gemm_fp8_mfma_dual_128x128");
+    return true;
+  }
+  if (fits(128, 128, 128) && (int64_t)(g.M / 128) * (g.N / 128) * g.batch >= 256) {
+    *c = br ? make_choice<MMA_FP8, 128, 128, 128, 2, 2, false, true, false>("gemm_fp8_mfma_128x128")
+            : make_choice<MMA_FP8, 128, 128, 128, 2, 2, false, false, false>("gemm_fp8_mfma_128x128");
+    return true;
+  }
+  if (fits(64, 128, 128)) {
+    *c = br ? make_choice<MMA_FP8, 64, 128, 128, 2, 2, false, true, false>("gemm_fp8_mfma_64x128")
+            : make_choice<MMA_FP8, 64, 128, 128, 2, 2, false, false, false>("gemm_fp8_mfma_64x128");
+    return true;
+  }
+  return false;
 }
 
 }  // namespace ryft

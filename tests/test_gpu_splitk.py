@@ -41,7 +41,7 @@ def test_fp8_split_k_scaled_epilogue(gpu_client):
 
 def test_bf16_f8_split_k_scaled_epilogue(gpu_client):
     # C5 as stated (bf16 activations, f8 weights) at 128 tokens: the same split on the widening bf16 kernel
-    _run(gpu_client, configs.c5_swiglu_fp8(m=128, d=1024, f=2048), "gemm_bf16f8_mfma_128x128")
+    _run(gpu_client, configs.c5_swiglu_fp8(m=128, d=1024, f=2048), "gemm_bf16f8_mfma_128x256")
 
 
 def test_f32_split_k(gpu_client):

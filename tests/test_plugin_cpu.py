@@ -123,8 +123,8 @@ def _plan(client, program):
     ("c2", {}, ["gemm_bf16_mfma_256x256"]),
     ("c3", {}, ["gemm_i8_mfma_256x256"]),
     ("c4", {}, ["attention_fwd"]),
-    ("c5", {}, ["row_norm", "gemm_bf16f8_mfma_dual_256x128", "gemm_bf16f8_mfma_128x128_splitk2"]),
-    ("c5", {"weights": "direct"}, ["row_norm", "gemm_bf16f8_mfma_dual_256x128", "gemm_bf16f8_mfma_128x128_splitk2"]),
+    ("c5", {}, ["row_norm", "gemm_bf16f8_mfma_dual_256x128", "gemm_bf16f8_mfma_128x256_splitk4"]),
+    ("c5", {"weights": "direct"}, ["row_norm", "gemm_bf16f8_mfma_dual_256x128", "gemm_bf16f8_mfma_128x256_splitk4"]),
     ("c5x", {}, ["row_norm", "gemm_fp8_mfma_dual_128x128", "gemm_fp8_mfma_128x128_splitk2"]),
 ])
 def test_full_size_plans(compile_client, name, kw, expect):
