@@ -331,7 +331,9 @@ def _eval_op(op: str, rest: str, env, dot_precision: str) -> Tuple[np.ndarray, s
             r = {"exponential": lambda: np.exp(x), "log": lambda: np.log(x), "rsqrt": lambda: 1.0 / np.sqrt(x),
                  "sqrt": lambda: np.sqrt(x), "tanh": lambda: np.tanh(x),
                  "logistic": lambda: 1.0 / (1.0 + np.exp(-x)), "negate": lambda: -x, "abs": lambda: np.abs(x),
-                 "floor": lambda: np.floor(x), "ceil": lambda: np.ceil(x), "sign": lambda: np.sign(x),
+                 "floor": lambda: np.floor(x), "ceil": lambda: np.ceil(x),
+                 # arithmetic.rs:15-25: NaN and signed zeros are their own sign
+                 "sign": lambda: np.where(np.isnan(x) | (x == 0), x, np.sign(x)),
                  "exponential_minus_one": lambda: np.expm1(x), "log_plus_one": lambda: np.log1p(x)}[op]()
         return normalize(r, dt), dt
     if op == "dot_general":

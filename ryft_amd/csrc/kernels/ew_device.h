@@ -498,7 +498,10 @@ __device__ __forceinline__ void ew_run_v(const EwProgram& P, int64_t lin, const 
       EW_U(EW_ICMP, cmp_i<int32_t>(EW_IA, EW_IB, I.imm.i))
       EW_U(EW_UCMP, cmp_i<uint32_t>(EW_UA, EW_UB, I.imm.i))
       EW_U(EW_SELECT, EW_UA ? EW_UB : rc[e])
-      EW_F(EW_FCLAMP, fminf(fmaxf(EW_FB, EW_FA), __uint_as_float(rc[e])))
+      // clamp(min, x, max) = minimum(maximum(x, min), max), both NaN-propagating
+      EW_F(EW_FCLAMP, (EW_FA != EW_FA || EW_FB != EW_FB || __uint_as_float(rc[e]) != __uint_as_float(rc[e]))
+                          ? __uint_as_float(0x7fc00000u)
+                          : fminf(fmaxf(EW_FB, EW_FA), __uint_as_float(rc[e])))
       EW_U(EW_ICLAMP, EW_IB < EW_IA ? EW_IA : (EW_IB > (int32_t)rc[e] ? (int32_t)rc[e] : EW_IB))
       default: EW_FOR r[e] = 0; break;
     }

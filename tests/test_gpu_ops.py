@@ -277,3 +277,66 @@ def test_pad_float_with_computed_value(gpu_client):
     ins = _f32_inputs(1, (6, 8)) + [configs.HostInput(np.array(0.5, np.float32), pjrt.BufferType.F32, ())]
     outs, _ = run_pjrt(gpu_client, prog, ins)
     check(outs[0], oracle_outputs(prog, ins)[0], 1e-6, "pad f32")
+
+
+# ----------------------------------------------------------------------------------------------- op semantics
+from tests.ref_examples import EXAMPLES, TRANSCENDENTAL, check_values  # noqa: E402
+
+_BT = {"f32": pjrt.BufferType.F32, "i32": pjrt.BufferType.S32, "i8": pjrt.BufferType.S8, "i1": pjrt.BufferType.PRED}
+_NP = {"f32": np.float32, "i32": np.int32, "i8": np.int8, "i1": np.bool_}
+
+
+@pytest.mark.parametrize("ex", EXAMPLES, ids=[e.name for e in EXAMPLES])
+def test_reference_worked_examples(gpu_client, ex):
+    """The reference's documented example of each op (tests/ref_examples.py) on the GPU: bit-exact, except 2 ulps of
+    slack for power / expm1 / log1p (device libm)."""
+    ins = [configs.HostInput(np.asarray(v, dtype=np.float64).astype(_NP[t]), _BT[t], ex.shape)
+           for v, t in zip(ex.inputs, ex.in_types)]
+    outs, _ = run_pjrt(gpu_client, ex.program(), ins)
+    check_values(outs[0], ex, ulps=2 if ex.op in TRANSCENDENTAL else 0)
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_clamp_f32_and_i32(gpu_client, shape):
+    """clamp(min, x, max) with per-element bounds (NaN in any operand gives NaN), scalar bounds, and i32."""
+    T, I, S = _t(shape), _t(shape, "i32"), "tensor<f32>"
+    lo = hd.normal(21, shape) - 0.5
+    hi = lo + np.abs(hd.normal(22, shape))
+    x = hd.normal(23, shape) * 2
+    for arr, idx in ((x, 0), (lo, 7), (hi, 13)):
+        arr.reshape(-1)[idx] = np.nan
+    body = f"""    %0 = stablehlo.clamp %arg0, %arg1, %arg2 : {T}
+    %1 = stablehlo.clamp %arg3, %arg1, %arg4 : ({S}, {T}, {S}) -> {T}
+    %2 = stablehlo.convert %arg1 : ({T}) -> {I}
+    %3 = stablehlo.constant dense<-1> : {I}
+    %4 = stablehlo.constant dense<2> : {I}
+    %5 = stablehlo.clamp %3, %2, %4 : {I}
+    return %0, %1, %5 : {T}, {T}, {I}"""
+    prog = _mod([T, T, T, S, S], [T, T, I], body)
+    ins = [configs.HostInput(v.astype(np.float32), pjrt.BufferType.F32, shape) for v in (lo, x, hi)] + [
+        configs.HostInput(np.float32(-0.25), pjrt.BufferType.F32, ()), configs.HostInput(np.float32(0.75),
+                                                                                       pjrt.BufferType.F32, ())]
+    outs, _ = run_pjrt(gpu_client, prog, ins)
+    want = oracle_outputs(prog, ins)
+    got0 = outs[0].astype(np.float64)
+    assert np.isnan(got0.reshape(-1)[[0, 7, 13]]).all()
+    for o, w, name in zip(outs, want, ("clamp", "clamp_scalar_bounds", "clamp_i32")):
+        g, v = sh.from_raw(o, w[1]), w[0]
+        assert np.array_equal(np.isnan(g), np.isnan(v)), name
+        ok = ~np.isnan(v)
+        assert np.array_equal(g[ok], v[ok]), name
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_power_and_remainder_f32(gpu_client, shape):
+    T = _t(shape)
+    body = f"""    %0 = stablehlo.abs %arg0 : {T}
+    %1 = stablehlo.power %0, %arg1 : {T}
+    %2 = stablehlo.remainder %arg0, %arg1 : {T}
+    return %1, %2 : {T}, {T}"""
+    prog = _mod([T, T], [T, T], body)
+    ins = _f32_inputs(2, shape, seed=31)
+    outs, _ = run_pjrt(gpu_client, prog, ins)
+    want = oracle_outputs(prog, ins)
+    check(outs[0], want[0], 1e-5, "power")
+    check(outs[1], want[1], 0, "remainder")  # fmod is exact

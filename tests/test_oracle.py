@@ -9,6 +9,12 @@ Each oracle function is checked against something a plausible mistake would fail
   * softmax attention  torch scaled_dot_product_attention(is_causal=True) in float64; rows of P sum to one.
   * RMSNorm + SwiGLU   closed form in float64 numpy (independent code path).
   * reduce / broadcast / transpose / iota / compare / select   closed forms on small inputs.
+  * op semantics  the reference's documented example of each elementwise op (tests/ref_examples.py: sign of -0.0,
+                  remainder signs, power's NaN and overflow, ceil / floor, not / and / or / xor, expm1 / log1p,
+                  maximum / minimum, compare); clamp's operand order with all three operands distinct; integer
+                  divide / remainder against exact integer arithmetic; float remainder's sign; float → int
+                  truncation and int → float rounding; reduce with every body and a non-neutral init; compare in
+                  every direction with a NaN operand.
 """
 import math
 
@@ -207,3 +213,113 @@ def test_pad_matches_the_index_formula(shape, lo, hi, interior):
         if all(0 <= p < n for p, n in zip(pos, out_shape)):
             want[pos] = x[idx]
     assert np.array_equal(out, want)
+
+
+# ----------------------------------------------------------------------------------------------- op semantics
+from tests.ref_examples import EXAMPLES, check_values, oracle_inputs  # noqa: E402
+
+
+@pytest.mark.parametrize("ex", EXAMPLES, ids=[e.name for e in EXAMPLES])
+def test_reference_worked_examples(ex):
+    """The reference's documented example of each op (tests/ref_examples.py cites file:line) gives the documented
+    result: pins sign conventions (remainder, sign of -0.0, ceil of small negatives), operand order of the binary
+    ops, NaN production (power of a negative base) and overflow (10000^10 in f32)."""
+    (out, dt), = sh.evaluate(ex.program(), oracle_inputs(ex))
+    assert dt == ex.out_type
+    check_values(out, ex)
+
+
+def _eval1(prog, *vals):
+    (out, dt), = sh.evaluate(prog, [np.asarray(v) for v in vals])
+    return out
+
+
+def test_clamp_operand_order():
+    # comparison.rs:166-176: `clamp %min, %operand, %max` bounds the middle operand. With min / operand / max all
+    # different, swapping any two of them changes the result.
+    T = "tensor<3xi32>"
+    prog = _mod([T, T, T], T, f"    %0 = stablehlo.clamp %arg0, %arg1, %arg2 : {T}\n    return %0 : {T}")
+    assert _eval1(prog, [5, 10, 15], [3, 13, 23], [10, 15, 20]).tolist() == [5, 13, 20]
+    F, S = "tensor<4xf32>", "tensor<f32>"
+    prog = _mod([S, F, S], F, f"    %0 = stablehlo.clamp %arg0, %arg1, %arg2 : ({S}, {F}, {S}) -> {F}\n    return %0 : {F}")
+    out = _eval1(prog, np.float64(-1.0), [-3.0, -0.5, 0.5, 3.0], np.float64(1.0))
+    assert out.tolist() == [-1.0, -0.5, 0.5, 1.0]
+
+
+def test_integer_divide_and_remainder_truncate_toward_zero():
+    # brute force against Python's exact integer arithmetic: q = sign(a)·sign(b)·(|a| // |b|), r = a - q·b
+    T = "tensor<451xi32>"
+    a, b = np.meshgrid(np.arange(-20, 21), np.array([v for v in range(-6, 7) if v != 0]))
+    a, b = a.ravel()[:451], b.ravel()[:451]
+    q_prog = _mod([T, T], T, f"    %0 = stablehlo.divide %arg0, %arg1 : {T}\n    return %0 : {T}")
+    r_prog = _mod([T, T], T, f"    %0 = stablehlo.remainder %arg0, %arg1 : {T}\n    return %0 : {T}")
+    q, r = _eval1(q_prog, a, b), _eval1(r_prog, a, b)
+    for x, y, qq, rr in zip(a.tolist(), b.tolist(), q.tolist(), r.tolist()):
+        want_q = (1 if (x >= 0) == (y > 0) else -1) * (abs(x) // abs(y))
+        assert qq == want_q and rr == x - want_q * y, (x, y, qq, rr)
+    # i32 wraparound of the one overflowing quotient, INT_MIN / -1
+    T1 = "tensor<1xi32>"
+    prog = _mod([T1, T1], T1, f"    %0 = stablehlo.divide %arg0, %arg1 : {T1}\n    return %0 : {T1}")
+    assert _eval1(prog, [-2 ** 31], [-1]).tolist() == [-2 ** 31]
+
+
+def test_float_remainder_sign_follows_dividend():
+    # the result has the dividend's sign and a magnitude below the divisor's (fmod), not IEEE round-to-nearest
+    # remainder: 17.1 rem 3 is 2.1, never -0.9
+    T = "tensor<4xf32>"
+    prog = _mod([T, T], T, f"    %0 = stablehlo.remainder %arg0, %arg1 : {T}\n    return %0 : {T}")
+    a = np.float32([17.1, -17.1, 17.1, -17.1]).astype(np.float64)
+    out = _eval1(prog, a, [3.0, 3.0, -3.0, -3.0])
+    want = np.float32(np.float32(17.1) - np.float32(15.0))  # exact: 15 is a multiple of 3 below 17.1
+    assert out.tolist() == [want, -want, want, -want]
+
+
+def test_convert_float_to_int_truncates_toward_zero():
+    F, I = "tensor<6xf32>", "tensor<6xi32>"
+    prog = _mod([F], I, f"    %0 = stablehlo.convert %arg0 : ({F}) -> {I}\n    return %0 : {I}")
+    assert _eval1(prog, [-2.7, -0.5, -0.0, 0.5, 2.7, 100.9]).tolist() == [-2, 0, 0, 0, 2, 100]
+    # integer → f32 rounds to nearest even: 2^24 + 1 is halfway between 2^24 and 2^24 + 2
+    I1, F1 = "tensor<2xi32>", "tensor<2xf32>"
+    prog = _mod([I1], F1, f"    %0 = stablehlo.convert %arg0 : ({I1}) -> {F1}\n    return %0 : {F1}")
+    assert _eval1(prog, [2 ** 24 + 1, 2 ** 24 + 3]).tolist() == [2.0 ** 24, 2.0 ** 24 + 4]
+
+
+def test_reduce_bodies_and_init_values():
+    # functional.rs:121-129: [[0, 1, 2, 3, 4, 5]] summed from 0 is [15]
+    def red(body, init, vals, dt="i32"):
+        T, R, S = f"tensor<1x{len(vals)}x{dt}>", f"tensor<1x{dt}>", f"tensor<{dt}>"
+        prog = _mod([T, S], R, f"    %0 = stablehlo.reduce(%arg0 init: %arg1) applies stablehlo.{body} across "
+                               f"dimensions = [1] : ({T}, {S}) -> {R}\n    return %0 : {R}")
+        return _eval1(prog, np.asarray([vals]), np.asarray(init)).tolist()[0]
+    assert red("add", 0, [0, 1, 2, 3, 4, 5]) == 15
+    assert red("add", 100, [0, 1, 2, 3, 4, 5]) == 115           # the init value takes part
+    assert red("multiply", 1, [1, 2, 3, 4, 5]) == 120
+    assert red("multiply", 2, [1, 2, 3, 4, 5]) == 240
+    assert red("maximum", 0, [-5, -3, -9]) == 0                  # init above every element
+    assert red("maximum", -100, [-5, -3, -9]) == -3
+    assert red("minimum", 0, [5, 3, 9]) == 0
+    assert red("minimum", 100, [5, 3, 9]) == 3
+    assert red("and", -1, [0b1110, 0b0111]) == 0b0110
+    assert red("and", 0b0010, [0b1110, 0b0111]) == 0b0010
+    assert red("or", 0, [0b1000, 0b0001]) == 0b1001
+    assert red("or", 0b0100, [0b1000, 0b0001]) == 0b1101
+    assert red("multiply", 1.0, [2.0, -0.5, 3.0], "f32") == -3.0
+
+
+def test_compare_directions_and_nan():
+    T, P = "tensor<4xf32>", "tensor<4xi1>"
+    a, b = [1.0, 2.0, 3.0, float("nan")], [2.0, 2.0, 2.0, 2.0]
+    want = {"EQ": [0, 1, 0, 0], "NE": [1, 0, 1, 1], "LT": [1, 0, 0, 0], "LE": [1, 1, 0, 0], "GT": [0, 0, 1, 0],
+            "GE": [0, 1, 1, 0]}
+    for d, w in want.items():
+        prog = _mod([T, T], P, f"    %0 = stablehlo.compare  {d}, %arg0, %arg1,  FLOAT : ({T}, {T}) -> {P}\n"
+                               f"    return %0 : {P}")
+        assert _eval1(prog, a, b).tolist() == w, d
+
+
+def test_sign_of_integers_and_not_of_bits():
+    I = "tensor<5xi32>"
+    prog = _mod([I], I, f"    %0 = stablehlo.sign %arg0 : {I}\n    return %0 : {I}")
+    assert _eval1(prog, [-7, -1, 0, 1, 9]).tolist() == [-1, -1, 0, 1, 1]
+    prog = _mod([I], I, f"    %0 = stablehlo.not %arg0 : {I}\n    return %0 : {I}")
+    assert _eval1(prog, [0, -1, 5, 2 ** 31 - 1, -2 ** 31]).tolist() == [-1, 0, -6, -2 ** 31, 2 ** 31 - 1]
