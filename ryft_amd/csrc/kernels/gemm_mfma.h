@@ -115,6 +115,17 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel)
   return __builtin_amdgcn_perm(hi, lo, sel);
 }
 
+// Bounds of one k-tile's loads in the edge kernels (shapes that are not tile multiples): the buffer resource covers
+// `nrec` bytes from the tile origin (rows past the operand's last byte read as zero instead of faulting), and the k
+// positions at or beyond `kvalid` are loaded as zeros (an offset past `nrec`, which the hardware returns as 0), so the
+// last, partial k-tile contributes nothing beyond K. Rows past M / N inside the operand's memory only feed output rows
+// / columns that are never stored.
+struct LoadBounds {
+  int nrec = -1;     // bytes from the tile origin (-1: unchecked)
+  int kvalid = 1 << 30;
+};
+__device__ __forceinline__ int masked_off(int64_t off, bool valid) { return valid ? (int)off : (int)0x80000000u; }
+
 // One operand tile (R rows × BK k) global → registers → LDS (K-packed rows of LDK bytes).
 template <int ESIZE, int R, int BK, int THREADS, bool RCONTIG>
 struct TileLoader {
@@ -130,23 +141,28 @@ struct TileLoader {
   // base: element pointer of (row 0, k 0) of this tile; sr / sk: element strides. Loads go through a buffer
   // resource whose base is this k-tile's origin (scalar registers), so the per-lane byte offsets are loop-invariant
   // 32-bit values (the host checks that one tile spans less than 2 GiB).
-  __device__ __forceinline__ void load(const char* base, int64_t sr, int64_t sk, int tid) {
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, -1, 0x00020000);
+  template <bool EDGE = false>
+  __device__ __forceinline__ void load(const char* base, int64_t sr, int64_t sk, int tid, LoadBounds lb = {}) {
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, EDGE ? lb.nrec : -1, 0x00020000);
 #pragma unroll
     for (int i = 0; i < NVEC; ++i) {
       int v = tid + i * THREADS;
       if (PARTIAL && v >= NTOT) break;
       if (!RCONTIG) {
         int row = v / (BK / VE), kv = v % (BK / VE);
-        regs[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(((int64_t)row * sr + (int64_t)kv * VE) * ESIZE), 0, 0);
+        const int64_t off = ((int64_t)row * sr + (int64_t)kv * VE) * ESIZE;
+        regs[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, EDGE ? masked_off(off, kv * VE < lb.kvalid) : (int)off, 0, 0);
       } else {
         // consecutive lanes take consecutive k-blocks of one row group: their transposed LDS stores then land in
         // distinct banks (lanes 8 rows apart would share banks), and each global row is still read in 128-byte runs
         int kb = v % (BK / KP), rv = v / (BK / KP);
 #pragma unroll
-        for (int q = 0; q < KP; ++q)
+        for (int q = 0; q < KP; ++q) {
+          const int64_t off = ((int64_t)(kb * KP + q) * sk + (int64_t)rv * VE) * ESIZE;
           regs[i * KP + q] = __builtin_amdgcn_raw_buffer_load_b128(
-              rs, (int)(((int64_t)(kb * KP + q) * sk + (int64_t)rv * VE) * ESIZE), 0, 0);
+              rs, EDGE ? masked_off(off, kb * KP + q < lb.kvalid) : (int)off, 0, 0);
+        }
       }
     }
   }
@@ -217,14 +233,17 @@ struct TileCopyLoader {
   static constexpr int NVEC = NTOT / THREADS;
   static_assert(NTOT % THREADS == 0, "uneven tile split");
   u32x4 regs[NVEC];
-  __device__ __forceinline__ void load(const char* base, int64_t sr, int64_t sk, int tid) {
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, -1, 0x00020000);
+  template <bool EDGE = false>
+  __device__ __forceinline__ void load(const char* base, int64_t sr, int64_t sk, int tid, LoadBounds lb = {}) {
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, EDGE ? lb.nrec : -1, 0x00020000);
     (void)sr;  // row-contiguous: the element stride along R is 1
 #pragma unroll
     for (int i = 0; i < NVEC; ++i) {
       const int v = tid + i * THREADS;
       const int k = v / (R / VE), c = v % (R / VE);
-      regs[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(((int64_t)k * sk + (int64_t)c * VE) * ESIZE), 0, 0);
+      const int64_t off = ((int64_t)k * sk + (int64_t)c * VE) * ESIZE;
+      regs[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, EDGE ? masked_off(off, k < lb.kvalid) : (int)off, 0, 0);
     }
   }
   template <int LDB>
@@ -260,15 +279,18 @@ struct TileWidenPieces {
   static constexpr bool PARTIAL = (NTOT % THREADS) != 0;
   static_assert(!PARTIAL || NVEC == 1, "uneven tile split");
   u32x2w regs[NVEC];
-  // stride_row: HBM bytes between consecutive LDS rows of the tile (sk for [k][n] tiles, sr for [n][k] tiles)
-  __device__ __forceinline__ void load(const char* base, int64_t stride_row, int tid) {
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, -1, 0x00020000);
+  // stride_row: HBM bytes between consecutive LDS rows of the tile ([n][k] tiles: sr); pieces run along k
+  template <bool EDGE = false>
+  __device__ __forceinline__ void load(const char* base, int64_t stride_row, int tid, LoadBounds lb = {}) {
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, EDGE ? lb.nrec : -1, 0x00020000);
 #pragma unroll
     for (int i = 0; i < NVEC; ++i) {
       const int v = tid + i * THREADS;
       if (PARTIAL && v >= NTOT) break;
       const int r = v / PIECES, c = v % PIECES;
-      regs[i] = __builtin_amdgcn_raw_buffer_load_b64(rs, (int)((int64_t)r * stride_row + (int64_t)c * 8), 0, 0);
+      const int64_t off = (int64_t)r * stride_row + (int64_t)c * 8;
+      regs[i] = __builtin_amdgcn_raw_buffer_load_b64(rs, EDGE ? masked_off(off, c * 8 < lb.kvalid) : (int)off, 0, 0);
     }
   }
   template <int PITCH>
@@ -285,9 +307,10 @@ struct TileWidenPieces {
 
 template <int R, int BK, int THREADS>
 struct TileWidenLoader : TileWidenPieces<R, BK / 8, THREADS> {
-  __device__ __forceinline__ void load(const char* base, int64_t sr, int64_t sk, int tid) {
+  template <bool EDGE = false>
+  __device__ __forceinline__ void load(const char* base, int64_t sr, int64_t sk, int tid, LoadBounds lb = {}) {
     (void)sk;  // K-contiguous
-    TileWidenPieces<R, BK / 8, THREADS>::load(base, sr, tid);
+    TileWidenPieces<R, BK / 8, THREADS>::template load<EDGE>(base, sr, tid, lb);
   }
 };
 
@@ -384,7 +407,7 @@ __device__ __forceinline__ uint32_t out_bits(uint32_t x, bool is_float) {
 // KIND is EPI_STORE / EPI_SCALE / EPI_SWIGLU; the output type, the epilogue kind and the trip count are
 // compile-time, so each pass is a short unrolled loop whose LDS reads can be issued ahead of the conversions. MIDR:
 // the value is rounded to G.mid_round (bf16 or f16) before the output conversion.
-template <int KIND, int DT, bool INT, bool MIDR, int WTN, int PITCH, int ROWS>
+template <int KIND, int DT, bool INT, bool MIDR, int WTN, int PITCH, int ROWS, bool EDGE = false>
 __device__ __forceinline__ void epi_pass(const GemmArgs& G, void* out, int b, int m0, int n0, const uint32_t* reg,
                                          const uint32_t* reg2, int lane) {
   constexpr int OS = out_size<DT>();
@@ -394,23 +417,27 @@ __device__ __forceinline__ void epi_pass(const GemmArgs& G, void* out, int b, in
   constexpr int RSTEP = 64 / CPR, ITER = ROWS * CPR / 64;
   const int row0 = lane / CPR, col = (lane % CPR) * VPC;
   const int n = n0 + col;
+  // partial edge tiles: chunks past N (N is a multiple of 16, so a chunk is all in or all out) and rows past M are
+  // neither read from the per-row / per-column operands nor stored
+  const bool col_ok = !EDGE || n < G.N;
   char* optr = (char*)out + (((int64_t)b * G.M + m0 + row0) * (int64_t)G.N + n) * OS;
   const int64_t ostep = (int64_t)RSTEP * G.N * OS;
   // per-column operands are the same for every row this lane visits
   float cs[VPC], cs2[VPC];
   if constexpr (KIND == EPI_SCALE || KIND == EPI_SWIGLU) {
-    const float* cp = G.col ? G.col + (int64_t)b * G.col_sb + (int64_t)n * G.col_sn : nullptr;
+    const float* cp = G.col && col_ok ? G.col + (int64_t)b * G.col_sb + (int64_t)n * G.col_sn : nullptr;
 #pragma unroll
     for (int e = 0; e < VPC; ++e) cs[e] = cp ? cp[(int64_t)e * G.col_sn] : 1.0f;
   }
   if constexpr (KIND == EPI_SWIGLU) {
-    const float* cp = G.col2 ? G.col2 + (int64_t)b * G.col2_sb + (int64_t)n * G.col2_sn : nullptr;
+    const float* cp = G.col2 && col_ok ? G.col2 + (int64_t)b * G.col2_sb + (int64_t)n * G.col2_sn : nullptr;
 #pragma unroll
     for (int e = 0; e < VPC; ++e) cs2[e] = cp ? cp[(int64_t)e * G.col2_sn] : 1.0f;
   }
 #pragma unroll 4
   for (int it = 0; it < ITER; ++it) {
     const int row = row0 + it * RSTEP;
+    if (EDGE && (!col_ok || m0 + row >= G.M)) continue;
     uint32_t v[VPC];
 #pragma unroll
     for (int q = 0; q < VPC / 4; ++q) {
@@ -479,10 +506,10 @@ __host__ __device__ inline bool mfma_out_supported(int dt, bool int_acc, int epi
 
 // Epilogue of one staged round: dispatch (uniform) on the epilogue kind, the intermediate rounding and the output
 // type to one compact pass.
-template <bool INT, bool DUAL, bool MIDR, int WTN, int PITCH, int ROWS>
+template <bool INT, bool DUAL, bool MIDR, int WTN, int PITCH, int ROWS, bool EDGE>
 __device__ __forceinline__ void epi_round_mr(const GemmArgs& G, int b, int m0, int n0, const uint32_t* reg,
                                              const uint32_t* reg2, int lane) {
-#define RYFT_EPI(K, DT, OUT) epi_pass<K, DT, INT, MIDR, WTN, PITCH, ROWS>(G, OUT, b, m0, n0, reg, reg2, lane)
+#define RYFT_EPI(K, DT, OUT) epi_pass<K, DT, INT, MIDR, WTN, PITCH, ROWS, EDGE>(G, OUT, b, m0, n0, reg, reg2, lane)
   const int dt = G.out_dtype[0];
   if (!MIDR && G.epilogue == EPI_STORE) {
     if (INT && dt == DT_S32) RYFT_EPI(EPI_STORE, DT_S32, G.out_ptr[0]);
@@ -510,14 +537,16 @@ __device__ __forceinline__ void epi_round_mr(const GemmArgs& G, int b, int m0, i
 #undef RYFT_EPI
 }
 
-template <bool INT, bool DUAL, int WTN, int PITCH, int ROWS>
+template <bool INT, bool DUAL, int WTN, int PITCH, int ROWS, bool EDGE>
 __device__ __forceinline__ void epi_round(const GemmArgs& G, int b, int m0, int n0, const uint32_t* reg,
                                           const uint32_t* reg2, int lane) {
-  if (G.mid_round) epi_round_mr<INT, DUAL, true, WTN, PITCH, ROWS>(G, b, m0, n0, reg, reg2, lane);
-  else epi_round_mr<INT, DUAL, false, WTN, PITCH, ROWS>(G, b, m0, n0, reg, reg2, lane);
+  if (G.mid_round) epi_round_mr<INT, DUAL, true, WTN, PITCH, ROWS, EDGE>(G, b, m0, n0, reg, reg2, lane);
+  else epi_round_mr<INT, DUAL, false, WTN, PITCH, ROWS, EDGE>(G, b, m0, n0, reg, reg2, lane);
 }
 
-template <int KIND, int BM, int BN, int BK, int WM, int WN, bool A_R, bool B_R, bool DUAL>
+// EDGE: any M, N (partial tiles at the edges: bounded loads, masked stores) and any K that is a multiple of the
+// 16-byte vector (the last k-tile loads zeros past K); no split-K.
+template <int KIND, int BM, int BN, int BK, int WM, int WN, bool A_R, bool B_R, bool DUAL, bool EDGE>
 __global__ void __launch_bounds__(64 * WM * WN) gemm_mfma_kernel(const GemmArgs G) {
   using C = MfmaCfg<KIND, BM, BN, BK, WM, WN, A_R, B_R, DUAL>;
   using M = typename C::M;
@@ -534,7 +563,7 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_mfma_kernel(const GemmArgs 
   // each XCD owns a contiguous run of tile ids; within a batch, ids run column-major through groups of up to 8
   // tile-rows, so one XCD's run covers a compact block of tiles and each A row-panel / B column-panel is fetched
   // into that XCD's L2 by few XCDs (with a row-major order every XCD would stream every B panel).
-  const int tiles_n = G.N / BN, tiles_m = G.M / BM;
+  const int tiles_n = EDGE ? (G.N + BN - 1) / BN : G.N / BN, tiles_m = EDGE ? (G.M + BM - 1) / BM : G.M / BM;
   const int per_batch = tiles_n * tiles_m;
   const int total = per_batch * G.batch;
   // split-K: the K range is the slow index of the grid, so the tile order below (and its XCD mapping) is the same
@@ -574,13 +603,40 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_mfma_kernel(const GemmArgs 
       if constexpr (DUAL) acc2[i][j] = Acc{};
     }
 
-  const int KT = G.splits > 1 ? G.K / BK / G.splits : G.K / BK;  // k-tiles of this workgroup's K range
+  // k-tiles of this workgroup's K range
+  const int KT = EDGE ? (G.K + BK - 1) / BK : (G.splits > 1 ? G.K / BK / G.splits : G.K / BK);
   const int kt0 = split * KT;
+  // edge kernels: the last byte of each operand (its loads are bounded to it), as an address
+  auto op_end = [&](const GemmOperand& o, int rows, int es) -> const char* {
+    return (const char*)o.ptr +
+           ((int64_t)(G.batch - 1) * o.sb + (int64_t)(rows - 1) * o.sr + (int64_t)(G.K - 1) * o.sk + 1) * es;
+  };
+  const char* const a_end = EDGE ? op_end(G.A, G.M, ES) : nullptr;
+  const char* const b_end = EDGE ? op_end(G.B, G.N, BES) : nullptr;
+  const char* const b2_end = EDGE && DUAL ? op_end(G.B2, G.N, BES) : nullptr;
+  auto bounds = [&](const char* p, const char* end, int kvalid) {
+    LoadBounds r;
+    r.nrec = (int)min((int64_t)(end - p), (int64_t)0x7fffffff);
+    r.kvalid = kvalid;
+    return r;
+  };
   auto gload = [&](int kt) {
     const int64_t ko = (int64_t)(kt0 + kt) * BK;
-    la.load(Ab + ko * G.A.sk * ES, G.A.sr, G.A.sk, tid);
-    lb.load(Bb + ko * G.B.sk * BES, G.B.sr, G.B.sk, tid);
-    if constexpr (DUAL) lb2.load(B2b + ko * G.B2.sk * BES, G.B2.sr, G.B2.sk, tid);
+    const char* pa = Ab + ko * G.A.sk * ES;
+    const char* pb = Bb + ko * G.B.sk * BES;
+    if constexpr (EDGE) {
+      const int kvalid = G.K - (int)ko;
+      la.template load<true>(pa, G.A.sr, G.A.sk, tid, bounds(pa, a_end, kvalid));
+      lb.template load<true>(pb, G.B.sr, G.B.sk, tid, bounds(pb, b_end, kvalid));
+      if constexpr (DUAL) {
+        const char* pb2 = B2b + ko * G.B2.sk * BES;
+        lb2.template load<true>(pb2, G.B2.sr, G.B2.sk, tid, bounds(pb2, b2_end, kvalid));
+      }
+    } else {
+      la.load(pa, G.A.sr, G.A.sk, tid);
+      lb.load(pb, G.B.sr, G.B.sk, tid);
+      if constexpr (DUAL) lb2.load(B2b + ko * G.B2.sk * BES, G.B2.sr, G.B2.sk, tid);
+    }
   };
   auto lstore = [&](int buf) {
     char* s = smem + buf * C::STAGE;
@@ -758,7 +814,7 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_mfma_kernel(const GemmArgs 
         epi_pass<EPI_STORE, PDT, M::INT, false, C::WTN, PITCH, EPI_ROWS * 32>(G, ws + slice, b, em0, en0, patch + REGION,
                                                                              nullptr, lane);
     } else {
-      epi_round<M::INT, DUAL, C::WTN, PITCH, EPI_ROWS * 32>(G, b, em0, en0, patch, patch + REGION, lane);
+      epi_round<M::INT, DUAL, C::WTN, PITCH, EPI_ROWS * 32, EDGE>(G, b, em0, en0, patch, patch + REGION, lane);
     }
     if constexpr (round + 1 < C::TM / EPI_ROWS) __asm__ __volatile__("" ::: "memory");  // reads before next writes
   });
@@ -771,14 +827,16 @@ struct Choice {
   int threads = 256;
   int lds = 0;
   int bm = 0, bn = 0, bk = 0;
+  bool edge = false;  // partial tiles allowed (grid rounds up)
   const char* name = "gemm_generic";
 };
 
-template <int KIND, int BM, int BN, int BK, int WM, int WN, bool A_R, bool B_R, bool DUAL>
+template <int KIND, int BM, int BN, int BK, int WM, int WN, bool A_R, bool B_R, bool DUAL, bool EDGE = false>
 Choice make_choice(const char* name) {
   using C = MfmaCfg<KIND, BM, BN, BK, WM, WN, A_R, B_R, DUAL>;
   Choice c;
-  c.fn = (const void*)&gemm_mfma_kernel<KIND, BM, BN, BK, WM, WN, A_R, B_R, DUAL>;
+  c.fn = (const void*)&gemm_mfma_kernel<KIND, BM, BN, BK, WM, WN, A_R, B_R, DUAL, EDGE>;
+  c.edge = EDGE;
   c.threads = C::THREADS;
   c.lds = C::LDS_BYTES;
   c.bm = BM;
@@ -788,13 +846,24 @@ Choice make_choice(const char* name) {
   return c;
 }
 
-// Per-type instantiation pickers (one translation unit each, so the build parallelises). `br`: B is n-contiguous.
-// With g.splits > 1 a picker returns the tile it runs over each of the K ranges (or false if K does not divide).
-bool pick_bf16(const GemmArgs& g, bool br, Choice* c);
-bool pick_f16(const GemmArgs& g, bool br, Choice* c);
-bool pick_i8(const GemmArgs& g, bool br, Choice* c);
-bool pick_fp8(const GemmArgs& g, bool br, Choice* c);
-bool pick_f32(const GemmArgs& g, bool br, Choice* c);
-bool pick_bf16f8(const GemmArgs& g, bool br, Choice* c);
+// The edge instantiation of a tile for either layout of A (ar: m-contiguous) and B (br: n-contiguous).
+template <int KIND, int BM, int BN, int BK, int WM, int WN, bool DUAL>
+Choice edge_choice(bool ar, bool br, const char* name) {
+  if (ar) return br ? make_choice<KIND, BM, BN, BK, WM, WN, true, true, DUAL, true>(name)
+                    : make_choice<KIND, BM, BN, BK, WM, WN, true, false, DUAL, true>(name);
+  return br ? make_choice<KIND, BM, BN, BK, WM, WN, false, true, DUAL, true>(name)
+            : make_choice<KIND, BM, BN, BK, WM, WN, false, false, DUAL, true>(name);
+}
+
+// Per-type instantiation pickers (one translation unit each, so the build parallelises). `ar`: A is m-contiguous,
+// `br`: B is n-contiguous. Tile-multiple shapes with a K-contiguous A get the full-tile kernels; any other shape (and
+// an m-contiguous A) gets the edge kernel of a 128×128 tile (64×64 for f32). With g.splits > 1 a picker returns the
+// tile it runs over each of the K ranges, or false (split-K runs full tiles only).
+bool pick_bf16(const GemmArgs& g, bool ar, bool br, Choice* c);
+bool pick_f16(const GemmArgs& g, bool ar, bool br, Choice* c);
+bool pick_i8(const GemmArgs& g, bool ar, bool br, Choice* c);
+bool pick_fp8(const GemmArgs& g, bool ar, bool br, Choice* c);
+bool pick_f32(const GemmArgs& g, bool ar, bool br, Choice* c);
+bool pick_bf16f8(const GemmArgs& g, bool ar, bool br, Choice* c);
 
 }  // namespace ryft

@@ -3,8 +3,8 @@
 
 namespace ryft {
 
-bool pick_bf16(const GemmArgs& g, bool br, Choice* c) {
-  auto fits = [&](int bm, int bn, int bk) { return g.M % bm == 0 && g.N % bn == 0 && g.K % bk == 0; };
+bool pick_bf16(const GemmArgs& g, bool ar, bool br, Choice* c) {
+  auto fits = [&](int bm, int bn, int bk) { return !ar && g.M % bm == 0 && g.N % bn == 0 && g.K % bk == 0; };
   if (g.dual) return false;
   if (g.splits > 1) {  // split-K runs the 128×128 tile over each K range
     if (!fits(128, 128, 64 * g.splits)) return false;
@@ -24,14 +24,20 @@ bool pick_bf16(const GemmArgs& g, bool br, Choice* c) {
             : make_choice<MMA_BF16, 128, 128, 64, 2, 2, false, false, false>("gemm_bf16_mfma_128x128");
     return true;
   }
-  return false;
+  *c = edge_choice<MMA_BF16, 128, 128, 64, 2, 2, false>(ar, br, "gemm_bf16_mfma_edge_128x128");
+  return true;
 }
 
-bool pick_f16(const GemmArgs& g, bool br, Choice* c) {
-  auto fits = [&](int bm, int bn, int bk) { return g.M % bm == 0 && g.N % bn == 0 && g.K % bk == 0; };
-  if (g.dual || !fits(128, 128, 64 * (g.splits > 1 ? g.splits : 1))) return false;
-  *c = br ? make_choice<MMA_F16, 128, 128, 64, 2, 2, false, true, false>("gemm_f16_mfma_128x128")
-          : make_choice<MMA_F16, 128, 128, 64, 2, 2, false, false, false>("gemm_f16_mfma_128x128");
+bool pick_f16(const GemmArgs& g, bool ar, bool br, Choice* c) {
+  auto fits = [&](int bm, int bn, int bk) { return !ar && g.M % bm == 0 && g.N % bn == 0 && g.K % bk == 0; };
+  if (g.dual) return false;
+  if (fits(128, 128, 64 * (g.splits > 1 ? g.splits : 1))) {
+    *c = br ? make_choice<MMA_F16, 128, 128, 64, 2, 2, false, true, false>("gemm_f16_mfma_128x128")
+            : make_choice<MMA_F16, 128, 128, 64, 2, 2, false, false, false>("gemm_f16_mfma_128x128");
+    return true;
+  }
+  if (g.splits > 1) return false;
+  *c = edge_choice<MMA_F16, 128, 128, 64, 2, 2, false>(ar, br, "gemm_f16_mfma_edge_128x128");
   return true;
 }
 

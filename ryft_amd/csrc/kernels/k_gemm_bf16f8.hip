@@ -4,8 +4,8 @@
 
 namespace ryft {
 
-bool pick_bf16f8(const GemmArgs& g, bool br, Choice* c) {
-  auto fits = [&](int bm, int bn, int bk) { return g.M % bm == 0 && g.N % bn == 0 && g.K % bk == 0; };
+bool pick_bf16f8(const GemmArgs& g, bool ar, bool br, Choice* c) {
+  auto fits = [&](int bm, int bn, int bk) { return !ar && g.M % bm == 0 && g.N % bn == 0 && g.K % bk == 0; };
   if (g.splits > 1) {  // split-K: 128×256 tiles (eight waves of 64×64) over each K range, else 128×128
     if (g.dual) return false;
     if (fits(128, 256, 64 * g.splits)) {
@@ -30,7 +30,8 @@ bool pick_bf16f8(const GemmArgs& g, bool br, Choice* c) {
               : make_choice<MMA_BF16_F8, 128, 128, 64, 2, 2, false, false, true>("gemm_bf16f8_mfma_dual_128x128");
       return true;
     }
-    return false;
+    *c = edge_choice<MMA_BF16_F8, 128, 128, 64, 2, 2, true>(ar, br, "gemm_bf16f8_mfma_dual_edge_128x128");
+    return true;
   }
   const int64_t tiles256 = (int64_t)(g.M / 256) * (g.N / 256) * g.batch;
   if (fits(256, 256, 64) && tiles256 >= 128) {
@@ -43,7 +44,8 @@ bool pick_bf16f8(const GemmArgs& g, bool br, Choice* c) {
             : make_choice<MMA_BF16_F8, 128, 128, 64, 2, 2, false, false, false>("gemm_bf16f8_mfma_128x128");
     return true;
   }
-  return false;
+  *c = edge_choice<MMA_BF16_F8, 128, 128, 64, 2, 2, false>(ar, br, "gemm_bf16f8_mfma_edge_128x128");
+  return true;
 }
 
 }  // namespace ryft

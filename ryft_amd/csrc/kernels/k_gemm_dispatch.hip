@@ -186,29 +186,39 @@ static bool pick_mfma(const GemmArgs& g, Choice* c) {
   if (g.epilogue == EPI_STORE && g.mid_round) return false;
   const int es = kind == MMA_BF16 || kind == MMA_F16 || kind == MMA_BF16_F8 ? 2 : (kind == MMA_F32 ? 4 : 1);
   const int bes = kind == MMA_BF16_F8 ? 1 : es;  // B's element size in HBM
-  // operand layouts: K-contiguous (sk == 1) or row-contiguous (sr == 1), in 16-byte vectors of `oes`-byte elements
-  auto layout = [&](const GemmOperand& o, int oes, int* r) -> bool {
-    const int ve = 16 / oes;
+  // operand layouts: K-contiguous (sk == 1) or row-contiguous (sr == 1), read in 16-byte vectors of `oes`-byte
+  // elements (`kbytes`-byte pieces along k for a K-contiguous f8 B widened to bf16)
+  auto layout = [&](const GemmOperand& o, int oes, int kbytes, int* r) -> bool {
+    const int ve = 16 / oes, vk = kbytes / oes;
     if (((uintptr_t)o.ptr & 15) != 0) return false;
     // tiles (≤ 256 rows / k-rows) are read through 32-bit buffer offsets from the tile origin
     if ((o.sr > o.sk ? o.sr : o.sk) * (int64_t)oes * 256 >= ((int64_t)1 << 31)) return false;
-    if (o.sk == 1 && (o.sr % ve) == 0 && (o.sb % ve) == 0) { *r = 0; return true; }
+    if (o.sk == 1 && (o.sr % vk) == 0 && (o.sb % vk) == 0) { *r = 0; return true; }
     if (o.sr == 1 && (o.sk % ve) == 0 && (o.sb % ve) == 0) { *r = 1; return true; }
     return false;
   };
+  const int bkb = kind == MMA_BF16_F8 ? 8 : 16;
   int ar, br, br2 = -1;
-  if (!layout(g.A, es, &ar) || !layout(g.B, bes, &br)) return false;
-  if (g.dual && (!layout(g.B2, bes, &br2) || br2 != br)) return false;
-  if (ar != 0) return false;  // m-contiguous A tiles are not instantiated
+  if (!layout(g.A, es, 16, &ar) || !layout(g.B, bes, bkb, &br)) return false;
+  if (g.dual && (!layout(g.B2, bes, bkb, &br2) || br2 != br)) return false;
+  bool ok = false;
   switch (kind) {
-    case MMA_BF16: return pick_bf16(g, br, c);
-    case MMA_F16: return pick_f16(g, br, c);
-    case MMA_I8: return pick_i8(g, br, c);
-    case MMA_FP8: return pick_fp8(g, br, c);
-    case MMA_F32: return pick_f32(g, br, c);
-    case MMA_BF16_F8: return pick_bf16f8(g, br, c);
+    case MMA_BF16: ok = pick_bf16(g, ar, br, c); break;
+    case MMA_F16: ok = pick_f16(g, ar, br, c); break;
+    case MMA_I8: ok = pick_i8(g, ar, br, c); break;
+    case MMA_FP8: ok = pick_fp8(g, ar, br, c); break;
+    case MMA_F32: ok = pick_f32(g, ar, br, c); break;
+    case MMA_BF16_F8: ok = pick_bf16f8(g, ar, br, c); break;
   }
-  return false;
+  if (ok && c->edge) {
+    // the edge kernels zero k positions past K a load at a time: K must end on a load boundary of each
+    // K-contiguous operand (16-byte vectors; 8-byte pieces for a widened f8 B)
+    int kgran = 1;
+    if (ar == 0) kgran = 16 / es;
+    if (br == 0) kgran = std::max(kgran, kind == MMA_BF16_F8 ? 8 : 16 / bes);
+    if (g.K % kgran) ok = false;
+  }
+  return ok;
 }
 
 const char* gemm_kernel_name(const GemmArgs& a) {
@@ -222,7 +232,7 @@ int gemm_plan_splits(const GemmArgs& a) {
   g.splits = 1;
   Choice c;
   if (!pick_mfma(g, &c)) return 1;
-  const int64_t tiles = (int64_t)(g.M / c.bm) * (g.N / c.bn) * g.batch;
+  const int64_t tiles = (int64_t)((g.M + c.bm - 1) / c.bm) * ((g.N + c.bn - 1) / c.bn) * g.batch;
   const bool f32 = g.A.dtype == DT_F32;
   // the 64-row tile (chosen when 128×128 tiles would not cover the chip) reads twice the operand bytes per FLOP of a
   // 128×128 tile, from L2 as well as LDS: splitting K over 128×128 tiles beats it
@@ -251,14 +261,15 @@ void launch_gemm(const GemmArgs& g, hipStream_t stream, hipEvent_t done) {
   hipError_t e;
   if (g.K > 0 && pick_mfma(g, &c)) {
     // shape invariants the MFMA kernels rely on (checked again here, right before the launch)
-    if (g.M % c.bm || g.N % c.bn) fail(PJRT_Error_Code_INTERNAL, "gemm tile mismatch");
+    if (!c.edge && (g.M % c.bm || g.N % c.bn)) fail(PJRT_Error_Code_INTERNAL, "gemm tile mismatch");
     if (c.lds > 65536) {
       e = hipFuncSetAttribute(c.fn, hipFuncAttributeMaxDynamicSharedMemorySize, c.lds);
       if (e != hipSuccess) fail(PJRT_Error_Code_INTERNAL, std::string("LDS attribute failed: ") + hipGetErrorString(e));
     }
     const int splits = g.splits > 1 ? g.splits : 1;
-    if (splits > 1 && (!g.ws || g.K % (splits * 16))) fail(PJRT_Error_Code_INTERNAL, "split-K without a workspace");
-    int64_t blocks = (int64_t)(g.M / c.bm) * (g.N / c.bn) * g.batch * splits;
+    if (splits > 1 && (!g.ws || g.K % (splits * 16) || c.edge))
+      fail(PJRT_Error_Code_INTERNAL, "split-K without a workspace or on partial tiles");
+    int64_t blocks = (int64_t)((g.M + c.bm - 1) / c.bm) * ((g.N + c.bn - 1) / c.bn) * g.batch * splits;
     if (blocks > INT32_MAX) fail(PJRT_Error_Code_UNIMPLEMENTED, "too many GEMM tiles");
     void* args[] = {(void*)&g};
     hipEvent_t main_done = splits > 1 ? nullptr : done;  // split-K: the reduction launch carries it

@@ -3,8 +3,8 @@
 
 namespace ryft {
 
-bool pick_i8(const GemmArgs& g, bool br, Choice* c) {
-  auto fits = [&](int bm, int bn, int bk) { return g.M % bm == 0 && g.N % bn == 0 && g.K % bk == 0; };
+bool pick_i8(const GemmArgs& g, bool ar, bool br, Choice* c) {
+  auto fits = [&](int bm, int bn, int bk) { return !ar && g.M % bm == 0 && g.N % bn == 0 && g.K % bk == 0; };
   if (g.dual) return false;
   if (g.splits > 1) {  // split-K runs the 128×128 tile over each K range
     if (!fits(128, 128, 128 * g.splits)) return false;
@@ -24,7 +24,8 @@ bool pick_i8(const GemmArgs& g, bool br, Choice* c) {
             : make_choice<MMA_I8, 128, 128, 128, 2, 2, false, false, false>("gemm_i8_mfma_128x128");
     return true;
   }
-  return false;
+  *c = edge_choice<MMA_I8, 128, 128, 128, 2, 2, false>(ar, br, "gemm_i8_mfma_edge_128x128");
+  return true;
 }
 
 }  // namespace ryft

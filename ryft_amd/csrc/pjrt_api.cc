@@ -310,7 +310,7 @@ LoadedExecutable* load_executable(Client* c, std::shared_ptr<Executable> exe) {
   le->client = c;
   le->exe = std::move(exe);
   if (!c->device_ptrs.empty()) {
-    le->devices = {c->device_ptrs.at(0)};
+    le->devices = {c->device_ptrs.at(le->exe->device_index)};
     le->logical_ids = {PJRT_LogicalDeviceIds{0, 0}};
   }
   return le;

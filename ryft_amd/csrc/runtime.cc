@@ -500,6 +500,8 @@ std::shared_ptr<Executable> compile_program(Client* c, const std::string& code, 
                                             const std::string& options) {
   if (format != "mlir") unimplemented("program format '" + format + "' is not supported; pass StableHLO as \"mlir\"");
   auto exe = std::make_shared<Executable>();
+  exe->options = decode_compile_options(options);
+  exe->device_index = choose_device(exe->options, c->device_ptrs.size());
   Graph g = is_mlir_bytecode(code.data(), code.size()) ? parse_mlir_bytecode(code, "main") : parse_mlir_text(code, "main");
   PlanOptions po;
   po.fast_paths = c->fast_paths;
@@ -548,10 +550,10 @@ std::shared_ptr<Executable> compile_program(Client* c, const std::string& code, 
   by.name_size = strlen(kBytes);
   by.float_value = (float)exe->plan.total_bytes;
   exe->cost_properties = {f, by};
-  // upload non-splat constants once, to the client's device
+  // upload non-splat constants once, to the executable's device
   exe->constants.resize(exe->plan.slots.size());
   if (c->device_ptrs.empty()) return exe;  // compile-only client
-  Device* d = c->device_ptrs.at(0);
+  Device* d = c->device_ptrs.at(exe->device_index);
   for (size_t s = 0; s < exe->plan.slots.size(); ++s) {
     const Slot& sl = exe->plan.slots[s];
     if (sl.kind != Slot::CONSTANT) continue;

@@ -148,11 +148,30 @@ struct MemoryLayout {  // PJRT_Layouts_MemoryLayout: dense, untiled
   std::vector<int64_t> minor_to_major;
 };
 
+// The CompileOptionsProto fields the plugin acts on (crates/ryft-xla-sys/src/protos.rs:3298-3346, 2391-2530).
+struct CompileOptions {
+  int64_t device_ordinal = -1;  // -1: the client's first device
+  int64_t replica_count = 1, partition_count = 1;
+  bool use_spmd_partitioning = false;
+  bool tupled_arguments = false;
+  bool portable = false;
+  int precision = 0;  // matrix_unit_operand_precision: 0 default, 1 high, 2 highest (f32 dots run f32 MFMAs always)
+  int64_t assignment_replicas = 0, assignment_computations = 0;
+  std::vector<int64_t> assignment_ids;  // device ids of an explicit device assignment (empty: none)
+};
+// Decodes serialized compile options (empty bytes: the defaults). Malformed bytes are INVALID_ARGUMENT; more than one
+// replica or partition, tupled parameters or a multi-device assignment are UNIMPLEMENTED.
+CompileOptions decode_compile_options(const std::string& bytes);
+// Index of the client device an executable with these options runs on (num_devices 0: compile-only, unchecked).
+int choose_device(const CompileOptions& o, size_t num_devices);
+
 struct Executable {  // PJRT_Executable (shared by the loaded executable and every view handed out)
   std::string name;
   std::string fingerprint;
   std::string program_text;
   std::string compile_options;
+  CompileOptions options;
+  int device_index = 0;  // the client device it was compiled for (constants live there)
   Plan plan;
   std::vector<PJRT_Buffer_Type> output_types;
   std::vector<int64_t> output_dims_flat;

@@ -1188,8 +1188,10 @@ class Client(_Owned):
                       num_partitions=partitions, default_assignment_size=n, default_assignment=arr)
         return list(arr)[:n]
 
-    def compile(self, program: Program, options: Optional[CompilationOptions] = None) -> LoadedExecutable:
-        opts = (options or CompilationOptions()).encode()
+    def compile(self, program: Program, options=None) -> LoadedExecutable:
+        """Client::compile (programs.rs:1245-1263). `options`: CompilationOptions, or already-serialized
+        CompileOptionsProto bytes."""
+        opts = bytes(options) if isinstance(options, (bytes, bytearray)) else (options or CompilationOptions()).encode()
         code = C.create_string_buffer(program.code, len(program.code))
         fmt = C.create_string_buffer(program.format.encode(), len(program.format))
         p = Program_()

@@ -106,3 +106,18 @@ def test_device_memory_descriptions(gpu_client):
     mem = device.default_memory()
     assert mem.kind() == "device"
     assert mem.kind_id() == 42097224
+
+
+def test_compile_options_choose_the_device(gpu_client):
+    """device_ordinal / a one-device assignment pick the executable's device; a device the client does not have is
+    INVALID_ARGUMENT at compile time; an explicit device_ordinal 0 runs like the default."""
+    n = len(gpu_client.addressable_devices())
+    with pytest.raises(pjrt.PjrtError) as e:
+        gpu_client.compile(pjrt.Program.mlir(ADD_PROGRAM), pjrt.CompilationOptions(device_ordinal=n))
+    assert e.value.code == pjrt.ErrorCode.INVALID_ARGUMENT
+    le = gpu_client.compile(pjrt.Program.mlir(ADD_PROGRAM), pjrt.CompilationOptions(device_ordinal=0))
+    assert le.addressable_devices() == gpu_client.addressable_devices()[:1]
+    a = configs.HostInput(np.array([[7], [-1]], np.int32), pjrt.BufferType.S32, (2, 1))
+    b = configs.HostInput(np.array([[35], [-41]], np.int32), pjrt.BufferType.S32, (2, 1))
+    outs, _ = run_pjrt(gpu_client, "", [a, b], executable=le)
+    assert outs[0].ravel().tolist() == [42, -42]

@@ -281,6 +281,52 @@ def test_compile_options_round_trip(compile_client):
     assert len(exe.executable().fingerprint()) == 16
 
 
+def _ebo(*fields):
+    """CompileOptionsProto bytes whose executable_build_options (field 3) holds `fields` (raw encoded fields)."""
+    body = b"".join(fields)
+    return b"\x1a" + bytes([len(body)]) + body
+
+
+@pytest.mark.parametrize("name,opts,code", [
+    ("two_replicas", pjrt.CompilationOptions(replica_count=2).encode(), pjrt.ErrorCode.UNIMPLEMENTED),
+    ("two_partitions", pjrt.CompilationOptions(partition_count=2).encode(), pjrt.ErrorCode.UNIMPLEMENTED),
+    ("tupled_parameters", b"\x10\x01", pjrt.ErrorCode.UNIMPLEMENTED),
+    # device assignment {replica_count 2, computation_count 1, ids [0, 1]}
+    ("two_device_assignment", _ebo(b"\x4a\x0a\x08\x02\x10\x01\x1a\x04\x0a\x02\x00\x01"), pjrt.ErrorCode.UNIMPLEMENTED),
+    ("assignment_size_mismatch", _ebo(b"\x4a\x09\x08\x02\x10\x01\x1a\x03\x0a\x01\x00"), pjrt.ErrorCode.INVALID_ARGUMENT),
+    ("truncated_build_options", b"\x1a\x05\x08", pjrt.ErrorCode.INVALID_ARGUMENT),
+    ("truncated_varint", b"\x50\x80", pjrt.ErrorCode.INVALID_ARGUMENT),
+    ("group_wire_type", b"\x0b", pjrt.ErrorCode.INVALID_ARGUMENT),
+    ("unknown_precision", b"\x50\x03", pjrt.ErrorCode.INVALID_ARGUMENT),
+    ("negative_device_ordinal", _ebo(b"\x08" + b"\xfe" + b"\xff" * 8 + b"\x01"), pjrt.ErrorCode.INVALID_ARGUMENT),
+])
+def test_compile_options_rejected(compile_client, name, opts, code):
+    """CompileOptionsProto decoding (protos.rs:3298-3346, 2391-2530): what one executable of this plugin cannot be
+    (several replicas / partitions / devices, tupled parameters) is UNIMPLEMENTED; malformed bytes are
+    INVALID_ARGUMENT."""
+    with pytest.raises(pjrt.PjrtError) as e:
+        compile_client.compile(pjrt.Program.mlir(GOLDENS["iota"]), opts)
+    assert e.value.code == code, (name, e.value)
+
+
+@pytest.mark.parametrize("name,opts", [
+    ("empty", b""),
+    ("defaults", pjrt.CompilationOptions().encode()),
+    ("highest_precision", pjrt.CompilationOptions(matrix_unit_operand_precision=2).encode()),
+    ("device_ordinal_0", pjrt.CompilationOptions(device_ordinal=0).encode()),
+    # one-device assignment {1, 1, [0]}, packed and unpacked id encodings
+    ("one_device_assignment", _ebo(b"\x4a\x08\x08\x01\x10\x01\x1a\x02\x08\x00")),
+    ("one_device_assignment_packed", _ebo(b"\x4a\x09\x08\x01\x10\x01\x1a\x03\x0a\x01\x00")),
+    # fields the plugin does not act on are skipped by wire type: portable (4), profile_version (5), multi-slice
+    # config bytes (6), an unknown fixed64 (15) and fixed32 (16) field, debug options inside the build options
+    ("skipped_fields", b"\x20\x01\x28\x07\x32\x02ab\x79" + b"\x00" * 8 + b"\x85\x01" + b"\x00" * 4 +
+     _ebo(b"\x1a\x02\x08\x01", b"\x20\x01")),
+])
+def test_compile_options_accepted(compile_client, name, opts):
+    exe = compile_client.compile(pjrt.Program.mlir(GOLDENS["iota"]), opts)
+    assert exe.executable().compile_options() == opts
+
+
 def test_serialize_deserialize_round_trip(compile_client):
     # as ryft-pjrt's test_client_deserialize_and_load_executable (programs.rs:2691-2723): the deserialized executable
     # reports the same name, counts, output types / dims / memory kinds, fingerprint and compile options
@@ -425,6 +471,14 @@ def test_attention_declined_when_the_kernel_cannot_run_it(compile_client, name, 
     assert "attention_fwd" not in kernels, (name, kernels)
     _, kernels = _plan(compile_client, configs.c4_causal_attention(b=1, h=2, s=256, d=128).program)
     assert "attention_fwd" in kernels
+
+
+def test_edge_tile_plans(compile_client):
+    # shapes that are not tile multiples, and m-contiguous lhs operands, plan to the edge MFMA kernels
+    from tests.edge_programs import CASES
+    for (name, prog, _), kernel, _ in CASES:
+        _, kernels = _plan(compile_client, prog)
+        assert kernels == [kernel], (name, kernels)
 
 
 @pytest.mark.parametrize("name,build,reductions", [
