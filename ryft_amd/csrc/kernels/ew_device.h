@@ -418,7 +418,21 @@ __device__ __forceinline__ T uniform_read(const T* p) {
   return __builtin_bit_cast(T, v);
 }
 
-template <int V, typename RF>
+// Ops evaluated out of line (ew_heavy).
+__host__ __device__ inline bool ew_is_heavy(int op) {
+  switch (op) {
+    case EW_LOG: case EW_TANH: case EW_EXPM1: case EW_LOG1P: case EW_CVT_F2I: case EW_POW: case EW_REM:
+    case EW_IDIV: case EW_IREM: case EW_UDIV: case EW_UREM:
+      return true;
+    default:
+      return false;
+  }
+}
+
+// PRE: the program's leaves (at most two, contiguous) were fetched ahead by the caller as raw words (fetch_contig),
+// at acc[leaf · V ..]; EW_LOAD decodes them instead of reading memory (streaming kernels issue several chunks' loads
+// before computing any of them).
+template <int V, typename RF, bool PRE = false>
 __device__ __forceinline__ void ew_run_v(const EwProgram& P, int64_t lin, const int32_t* coord, const uint32_t* acc,
                                          RF& R, int pc_begin = 0, int pc_end = -1, const EwTables* T = nullptr) {
 #define EW_FOR _Pragma("unroll") for (int e = 0; e < V; ++e)
@@ -430,7 +444,9 @@ __device__ __forceinline__ void ew_run_v(const EwProgram& P, int64_t lin, const 
 #define EW_UB (rb[e])
 #define EW_F(OP, EXPR) case OP: EW_FOR r[e] = __float_as_uint(EXPR); break;
 #define EW_U(OP, EXPR) case OP: EW_FOR r[e] = (uint32_t)(EXPR); break;
-#define EW_HEAVY(OP) case OP: _Pragma("unroll 1") for (int e = 0; e < V; ++e) r[e] = ew_heavy(OP, ra[e], rb[e], I.round); break;
+// (PRE: the out-of-line heavy ops are compiled out; the launcher streams only programs without them, and a call in
+// the loop would force the prefetched words out of registers)
+#define EW_HEAVY(OP) case OP: if constexpr (!PRE) { _Pragma("unroll 1") for (int e = 0; e < V; ++e) r[e] = ew_heavy(OP, ra[e], rb[e], I.round); } break;
   const int end = pc_end < 0 ? P.n_instr : pc_end;
   EwInstr next = T ? uniform_read(&T->instr[pc_begin]) : P.instr[pc_begin];
   for (int pc = pc_begin; pc < end; ++pc) {
@@ -443,12 +459,18 @@ __device__ __forceinline__ void ew_run_v(const EwProgram& P, int64_t lin, const 
     if (nsrc >= 3) R.load(I.c, rc);
     switch (I.op) {
       case EW_LOAD:
-        if (T) load_leaf<V>(uniform_read(&T->leaves[I.a]), lin, coord, P.rank, r);
-        else load_leaf<V>(P.leaves[I.a], lin, coord, P.rank, r);
+        if constexpr (PRE) {
+          uint32_t w[V];
+          EW_FOR w[e] = I.a == 0 ? acc[e] : acc[V + e];
+          decode_contig<V>(T ? uniform_read(&T->leaves[I.a].dtype) : P.leaves[I.a].dtype, w, r);
+        } else {
+          if (T) load_leaf<V>(uniform_read(&T->leaves[I.a]), lin, coord, P.rank, r);
+          else load_leaf<V>(P.leaves[I.a], lin, coord, P.rank, r);
+        }
         break;
       EW_U(EW_CONST, I.imm.u)
       EW_U(EW_IOTA, coord[I.a] + (I.a == P.rank - 1 ? e : 0))
-      EW_U(EW_ACC, acc[I.a])
+      EW_U(EW_ACC, PRE ? 0u : acc[I.a])  // (a runtime index into acc would keep PRE's words out of registers)
       EW_F(EW_NEG, -EW_FA)
       EW_F(EW_ABS, fabsf(EW_FA))
       EW_F(EW_EXP, expf(EW_FA))

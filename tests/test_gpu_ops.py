@@ -340,3 +340,29 @@ def test_power_and_remainder_f32(gpu_client, shape):
     want = oracle_outputs(prog, ins)
     check(outs[0], want[0], 1e-5, "power")
     check(outs[1], want[1], 0, "remainder")  # fmod is exact
+
+
+@pytest.mark.parametrize("dt,bt", [("bf16", pjrt.BufferType.BF16), ("f8E4M3FN", pjrt.BufferType.F8E4M3FN),
+                                   ("i8", pjrt.BufferType.S8), ("f32", pjrt.BufferType.F32)])
+def test_streaming_maps_by_element_size(gpu_client, dt, bt):
+    """Maps over one or two contiguous leaves run the streaming kernel, whose fetches are specialised by element size
+    (4, 2 and 1 bytes): a unary map and a binary map of the same type, checked bit-exactly against the oracle."""
+    shape = (16, 4096)
+    T, F = _t(shape, dt), _t(shape, "f32")
+    body = f"""    %0 = stablehlo.convert %arg0 : ({T}) -> {F}
+    %1 = stablehlo.negate %0 : {F}
+    %2 = stablehlo.add %arg0, %arg1 : {T}
+    return %1, %2 : {F}, {T}"""
+    prog = _mod([T, T], [F, T], body)
+    if dt == "i8":
+        raw = [hd.int_uniform(41 + i, shape, -60, 60).astype(np.int8) for i in range(2)]
+    elif dt == "f32":
+        raw = [hd.normal(41 + i, shape).astype(np.float32) for i in range(2)]
+    elif dt == "bf16":
+        raw = [hd.f32_to_bf16_bits(hd.normal(41 + i, shape)) for i in range(2)]
+    else:
+        raw = [hd.f32_to_e4m3fn_bits(hd.normal(41 + i, shape)) for i in range(2)]
+    ins = [configs.HostInput(r, bt, shape) for r in raw]
+    outs, exe = run_pjrt(gpu_client, prog, ins)
+    for o, w, name in zip(outs, oracle_outputs(prog, ins), ("convert-negate", "add")):
+        check(o, w, 0.0, f"{dt} {name}")
