@@ -1156,6 +1156,91 @@ typedef struct PJRT_MemoryDescriptions_Extension {
   PJRT_MemoryDescription_Kind* PJRT_MemoryDescription_Kind;
 } PJRT_MemoryDescriptions_Extension;
 
+/* ---------------------------------------------------------------- profiler extension (extensions/profiler.rs:345-520)
+ * Errors of this API are its own type (PLUGIN_Profiler_Error), released with its own Error_Destroy. */
+#define PJRT_API_PROFILER_EXTENSION_VERSION 1
+typedef struct PLUGIN_Profiler_Error PLUGIN_Profiler_Error;
+typedef struct PLUGIN_Profiler PLUGIN_Profiler;
+
+typedef struct PLUGIN_Profiler_Error_Message_Args {
+  size_t struct_size;
+  void* state;
+  const PLUGIN_Profiler_Error* error;
+  const char* message; /* out */
+  size_t message_size; /* out */
+} PLUGIN_Profiler_Error_Message_Args;
+typedef void PLUGIN_Profiler_Error_Message(PLUGIN_Profiler_Error_Message_Args* args);
+
+typedef struct PLUGIN_Profiler_Error_GetCode_Args {
+  size_t struct_size;
+  void* state;
+  const PLUGIN_Profiler_Error* error;
+  int code; /* out */
+} PLUGIN_Profiler_Error_GetCode_Args;
+typedef PLUGIN_Profiler_Error* PLUGIN_Profiler_Error_GetCode(PLUGIN_Profiler_Error_GetCode_Args* args);
+
+typedef struct PLUGIN_Profiler_Error_Destroy_Args {
+  size_t struct_size;
+  void* state;
+  PLUGIN_Profiler_Error* error;
+} PLUGIN_Profiler_Error_Destroy_Args;
+typedef void PLUGIN_Profiler_Error_Destroy(PLUGIN_Profiler_Error_Destroy_Args* args);
+
+typedef struct PLUGIN_Profiler_Create_Args {
+  size_t struct_size;
+  const char* options; /* serialized tensorflow.ProfileOptions */
+  size_t options_size;
+  PLUGIN_Profiler* profiler; /* out */
+} PLUGIN_Profiler_Create_Args;
+typedef PLUGIN_Profiler_Error* PLUGIN_Profiler_Create(PLUGIN_Profiler_Create_Args* args);
+
+typedef struct PLUGIN_Profiler_Destroy_Args {
+  size_t struct_size;
+  PLUGIN_Profiler* profiler;
+} PLUGIN_Profiler_Destroy_Args;
+typedef PLUGIN_Profiler_Error* PLUGIN_Profiler_Destroy(PLUGIN_Profiler_Destroy_Args* args);
+
+typedef struct PLUGIN_Profiler_Start_Args {
+  size_t struct_size;
+  PLUGIN_Profiler* profiler;
+} PLUGIN_Profiler_Start_Args;
+typedef PLUGIN_Profiler_Error* PLUGIN_Profiler_Start(PLUGIN_Profiler_Start_Args* args);
+
+typedef struct PLUGIN_Profiler_Stop_Args {
+  size_t struct_size;
+  PLUGIN_Profiler* profiler;
+} PLUGIN_Profiler_Stop_Args;
+typedef PLUGIN_Profiler_Error* PLUGIN_Profiler_Stop(PLUGIN_Profiler_Stop_Args* args);
+
+/* A call with a null buffer serializes the session's XSpace into storage the session owns (valid until Destroy) and
+ * returns it with its size (one trailing NUL included); a call with a non-null buffer does nothing. */
+typedef struct PLUGIN_Profiler_CollectData_Args {
+  size_t struct_size;
+  PLUGIN_Profiler* profiler;
+  uint8_t* buffer;             /* in/out */
+  size_t buffer_size_in_bytes; /* out */
+} PLUGIN_Profiler_CollectData_Args;
+typedef PLUGIN_Profiler_Error* PLUGIN_Profiler_CollectData(PLUGIN_Profiler_CollectData_Args* args);
+
+typedef struct PLUGIN_Profiler_Api {
+  size_t struct_size;
+  void* state;
+  PLUGIN_Profiler_Error_Destroy* PLUGIN_Profiler_Error_Destroy;
+  PLUGIN_Profiler_Error_Message* PLUGIN_Profiler_Error_Message;
+  PLUGIN_Profiler_Error_GetCode* PLUGIN_Profiler_Error_GetCode;
+  PLUGIN_Profiler_Create* PLUGIN_Profiler_Create;
+  PLUGIN_Profiler_Destroy* PLUGIN_Profiler_Destroy;
+  PLUGIN_Profiler_Start* PLUGIN_Profiler_Start;
+  PLUGIN_Profiler_Stop* PLUGIN_Profiler_Stop;
+  PLUGIN_Profiler_CollectData* PLUGIN_Profiler_CollectData;
+} PLUGIN_Profiler_Api;
+
+typedef struct PJRT_Profiler_Extension {
+  PJRT_Extension_Base base;
+  PLUGIN_Profiler_Api* profiler_api;
+  int64_t trace_me_context_id;
+} PJRT_Profiler_Extension;
+
 /* ---------------------------------------------------------------- the table (lib.rs:214-364) */
 #define PJRT_SLOT(name) name* name
 #define PJRT_NOSLOT(name) PJRT_Unimplemented_Fn name
@@ -1343,6 +1428,12 @@ PJRT_ASSERT(sizeof(PJRT_Executable_GetCompileOptions_Args) == 56, "PJRT_Executab
 PJRT_ASSERT(sizeof(PJRT_Executable_Serialize_Args) == 56, "PJRT_Executable_Serialize_Args");
 PJRT_ASSERT(sizeof(PJRT_Layouts_Extension) == 24 + 7 * 8, "PJRT_Layouts_Extension");
 PJRT_ASSERT(sizeof(PJRT_MemoryDescriptions_Extension) == 24 + 2 * 8, "PJRT_MemoryDescriptions_Extension");
+PJRT_ASSERT(sizeof(PJRT_Profiler_Extension) == 24 + 2 * 8, "PJRT_Profiler_Extension");
+PJRT_ASSERT(sizeof(PLUGIN_Profiler_Api) == 10 * 8, "PLUGIN_Profiler_Api");
+PJRT_ASSERT(sizeof(PLUGIN_Profiler_Error_Message_Args) == 40, "PLUGIN_Profiler_Error_Message_Args");
+PJRT_ASSERT(sizeof(PLUGIN_Profiler_Error_GetCode_Args) == 32, "PLUGIN_Profiler_Error_GetCode_Args");
+PJRT_ASSERT(sizeof(PLUGIN_Profiler_Create_Args) == 32, "PLUGIN_Profiler_Create_Args");
+PJRT_ASSERT(sizeof(PLUGIN_Profiler_CollectData_Args) == 32, "PLUGIN_Profiler_CollectData_Args");
 PJRT_ASSERT(sizeof(PJRT_DeviceDescription_MemoryDescriptions_Args) == 48, "MemoryDescriptions_Args");
 PJRT_ASSERT(sizeof(PJRT_MemoryDescription_Kind_Args) == 48, "PJRT_MemoryDescription_Kind_Args");
 PJRT_ASSERT(sizeof(PJRT_Layouts_PJRT_Client_GetDefaultLayout_Args) == 56, "PJRT_Layouts_PJRT_Client_GetDefaultLayout_Args");

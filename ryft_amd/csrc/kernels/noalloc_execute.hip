@@ -145,7 +145,8 @@ extern "C" int RyftMi355x_ExecuteNoAlloc(PJRT_LoadedExecutable* executable, cons
     std::lock_guard<std::recursive_mutex> lk(d->launch_mu);
     if (hipSetDevice(d->hip_ordinal) != hipSuccess)
       return report(PJRT_Error_Code_INTERNAL, "cannot make device %d current", d->hip_ordinal);
-    enqueue_steps(le->client, plan, ptr, (hipStream_t)stream, nullptr, false);
+    // (never timed, not even for a started profiler session: timing creates events)
+    enqueue_steps(le->client, plan, ptr, (hipStream_t)stream, nullptr, false, d->id, false);
   } catch (const Status& st) {
     return report(st.code, "%s", st.what());
   }

@@ -1131,7 +1131,7 @@ PJRT_Error* MemDesc_MemoryDescription_Kind(PJRT_MemoryDescription_Kind_Args* arg
 }
 
 PJRT_MemoryDescriptions_Extension g_memory_descriptions_extension = {
-    {sizeof(PJRT_MemoryDescriptions_Extension), PJRT_Extension_Type_MemoryDescriptions, nullptr},
+    {sizeof(PJRT_MemoryDescriptions_Extension), PJRT_Extension_Type_MemoryDescriptions, &g_profiler_extension.base},
     MemDesc_DeviceDescription_MemoryDescriptions,
     MemDesc_MemoryDescription_Kind,
 };

@@ -318,10 +318,7 @@ Client::~Client() {
   stop_worker();
   {
     std::lock_guard<std::mutex> lk(prof_mu);
-    for (auto& t : timings) {
-      if (t.start) (void)hipEventDestroy(t.start);
-      if (t.stop) (void)hipEventDestroy(t.stop);
-    }
+    timings.clear();
   }
   for (auto& d : devices) {
     d->allocator.reset();
@@ -499,6 +496,15 @@ static std::string fnv_hex(const std::string& a, const std::string& b) {
 std::shared_ptr<Executable> compile_program(Client* c, const std::string& code, const std::string& format,
                                             const std::string& options) {
   if (format != "mlir") unimplemented("program format '" + format + "' is not supported; pass StableHLO as \"mlir\"");
+  struct CompileSpan {  // the compilation's host span, for started profiler sessions
+    int64_t begin = wall_clock_ns();
+    ~CompileSpan() {
+      try {
+        if (profiler_sessions_active()) profiler_record_host("compile main", begin, wall_clock_ns());
+      } catch (...) {
+      }
+    }
+  } span;
   auto exe = std::make_shared<Executable>();
   exe->options = decode_compile_options(options);
   exe->device_index = choose_device(exe->options, c->device_ptrs.size());
@@ -606,25 +612,38 @@ std::shared_ptr<Executable> deserialize_executable(Client* c, const char* data, 
 }
 
 // ------------------------------------------------------------------------------------------------ execute
-bool enqueue_steps(Client* c, const Plan& plan, void* const* ptr, hipStream_t st, hipEvent_t done, bool prof) {
+TimingEvents::TimingEvents() {
+  HIP_CHECK(hipEventCreate(&start));
+  HIP_CHECK(hipEventCreate(&stop));
+}
+TimingEvents::~TimingEvents() {
+  if (start) (void)hipEventDestroy(start);
+  if (stop) (void)hipEventDestroy(stop);
+}
+
+bool enqueue_steps(Client* c, const Plan& plan, void* const* ptr, hipStream_t st, hipEvent_t done, bool prof,
+                   int device_id, bool profilable) {
+  const bool record = profilable && profiler_sessions_active();  // started profiler sessions take the events too
+  const bool timed = prof || record;
   constexpr size_t kBlock = std::max({sizeof(EwProgram), sizeof(ReduceArgs), sizeof(GemmArgs), sizeof(RowArgs),
                                       sizeof(AttnArgs)});
   alignas(64) static thread_local unsigned char block[kBlock + 64];
   bool recorded = false;
   for (size_t si = 0; si < plan.steps.size(); ++si) {
     const Step& step = plan.steps[si];
-    hipEvent_t carry = (!prof && si + 1 == plan.steps.size() && step.kind != Step::COPY) ? done : nullptr;
+    hipEvent_t carry = (!timed && si + 1 == plan.steps.size() && step.kind != Step::COPY) ? done : nullptr;
     recorded |= carry != nullptr;
     StepTiming tm;
-    if (prof) {
+    if (timed) {
       tm.name = step.name;
       tm.flops = step.flops;
       tm.bytes = step.bytes;
-      HIP_CHECK(hipEventCreate(&tm.start));
-      HIP_CHECK(hipEventCreate(&tm.stop));
+      tm.device = device_id;
+      tm.host_ns = wall_clock_ns();
+      tm.ev = std::make_shared<TimingEvents>();
       // kernel steps: the first launch records the start, the last the stop (the kernels' own duration)
-      if (step.kind == Step::COPY) HIP_CHECK(hipEventRecord(tm.start, st));
-      else pending_start() = tm.start;
+      if (step.kind == Step::COPY) HIP_CHECK(hipEventRecord(tm.ev->start, st));
+      else pending_start() = tm.ev->start;
     }
     if (step.kind == Step::COPY) {
       void* src = (char*)ptr[step.patches[0].second] + step.copy.src_offset;
@@ -641,7 +660,7 @@ bool enqueue_steps(Client* c, const Plan& plan, void* const* ptr, hipStream_t st
         void** f = (void**)(block + p.first);
         *f = (char*)ptr[p.second] + (uintptr_t)(*f);
       }
-      hipEvent_t last = prof ? tm.stop : carry;
+      hipEvent_t last = timed ? tm.ev->stop : carry;
       switch (step.kind) {
         case Step::ELEMENTWISE: launch_elementwise(*(EwProgram*)block, st, last); break;
         case Step::REDUCE: launch_reduce(*(ReduceArgs*)block, st, last); break;
@@ -655,16 +674,20 @@ bool enqueue_steps(Client* c, const Plan& plan, void* const* ptr, hipStream_t st
         HIP_CHECK(hipEventRecord(unused, st));
       }
     }
-    if (prof) {
-      if (step.kind == Step::COPY) HIP_CHECK(hipEventRecord(tm.stop, st));
-      std::lock_guard<std::mutex> pl(c->prof_mu);
-      c->timings.push_back(tm);
+    if (timed) {
+      if (step.kind == Step::COPY) HIP_CHECK(hipEventRecord(tm.ev->stop, st));
+      if (record) profiler_record_step(tm);
+      if (prof) {
+        std::lock_guard<std::mutex> pl(c->prof_mu);
+        c->timings.push_back(tm);
+      }
     }
   }
   return recorded;
 }
 
 EventPtr execute(LoadedExecutable* le, Device* d, Buffer* const* args, size_t num_args, std::vector<Buffer*>* outputs) {
+  const int64_t host_begin = wall_clock_ns();
   Executable& exe = *le->exe;
   const Plan& plan = exe.plan;
   Client* c = le->client;
@@ -707,7 +730,7 @@ EventPtr execute(LoadedExecutable* le, Device* d, Buffer* const* args, size_t nu
     // between consecutive executions); otherwise it is recorded after the last step.
     done = std::make_shared<EventState>();
     HIP_CHECK(hipEventCreateWithFlags(&done->hip_event, hipEventDisableTiming));
-    const bool recorded = enqueue_steps(c, plan, ptr.data(), st, done->hip_event, prof);
+    const bool recorded = enqueue_steps(c, plan, ptr.data(), st, done->hip_event, prof, d->id);
     if (!recorded) HIP_CHECK(hipEventRecord(done->hip_event, st));
     // Nothing runs on this event's completion unless a callback is registered, so it is not queued on the
     // completion worker.
@@ -726,6 +749,7 @@ EventPtr execute(LoadedExecutable* le, Device* d, Buffer* const* args, size_t nu
     b->ready = done;
     outputs->push_back(b.release());
   }
+  if (profiler_sessions_active()) profiler_record_host("execute " + exe.name, host_begin, wall_clock_ns());
   return done;
 }
 
@@ -745,7 +769,7 @@ std::string kernel_timing_json(Client* c) {
     std::lock_guard<std::mutex> lk(c->prof_mu);
     for (auto& t : c->timings) {
       float ms = 0;
-      HIP_CHECK(hipEventElapsedTime(&ms, t.start, t.stop));
+      HIP_CHECK(hipEventElapsedTime(&ms, t.ev->start, t.ev->stop));
       if (!agg.count(t.name)) order.push_back(t.name);
       Agg& a = agg[t.name];
       a.count++;
@@ -755,8 +779,6 @@ std::string kernel_timing_json(Client* c) {
       a.samples.push_back(ms);
       a.flops += t.flops;
       a.bytes += t.bytes;
-      (void)hipEventDestroy(t.start);
-      (void)hipEventDestroy(t.stop);
     }
     c->timings.clear();
   }

@@ -202,11 +202,31 @@ struct LoadedExecutable {  // PJRT_LoadedExecutable
 };
 
 // ------------------------------------------------------------------------------------------------ client
+// HIP events recorded by a plan step's first and last kernel launch (destroyed with the last holder).
+struct TimingEvents {
+  hipEvent_t start = nullptr, stop = nullptr;
+  TimingEvents();
+  ~TimingEvents();
+  TimingEvents(const TimingEvents&) = delete;
+  TimingEvents& operator=(const TimingEvents&) = delete;
+};
+
 struct StepTiming {
   std::string name;
   double flops = 0, bytes = 0;
-  hipEvent_t start = nullptr, stop = nullptr;
+  int device = 0;        // PJRT device id
+  int64_t host_ns = 0;   // wall clock when the step was enqueued
+  std::shared_ptr<TimingEvents> ev;
 };
+
+// ------------------------------------------------------------------------------------------------ profiler
+// Sessions of the PJRT profiler extension (profiler.cc). While at least one is started, executions record their
+// steps' HIP events (and their own host spans) into every started session.
+bool profiler_sessions_active();
+void profiler_record_step(const StepTiming& t);
+void profiler_record_host(const std::string& name, int64_t begin_ns, int64_t end_ns);
+int64_t wall_clock_ns();
+extern PJRT_Profiler_Extension g_profiler_extension;  // the extension's table (chained into the PJRT_Api)
 
 struct Client {  // PJRT_Client
   std::string platform_name = "rocm";
@@ -258,8 +278,11 @@ std::shared_ptr<Executable> compile_program(Client* c, const std::string& code, 
 EventPtr execute(LoadedExecutable* le, Device* d, Buffer* const* args, size_t num_args, std::vector<Buffer*>* outputs);
 // Enqueues every step of `plan` on `st`, slot s living at ptr[s] (the caller has made the plan's device current).
 // `done` (optional) is recorded by the last kernel launch when it can; returns whether it was. With `prof`, each
-// step's first and last launch record timing events appended to c->timings. Allocates no device memory.
-bool enqueue_steps(Client* c, const Plan& plan, void* const* ptr, hipStream_t st, hipEvent_t done, bool prof);
+// step's first and last launch record timing events appended to c->timings; while a profiler session is started,
+// they are recorded for it too (device_id names the device in its trace) unless `profilable` is false. Allocates no
+// device memory; creates no HIP object unless timing.
+bool enqueue_steps(Client* c, const Plan& plan, void* const* ptr, hipStream_t st, hipEvent_t done, bool prof,
+                   int device_id = 0, bool profilable = true);
 // Device address of the allocation-free entry point's scratch array on a GPU (looked up once per device, with
 // that device current; null if the lookup fails), and its size.
 void* noalloc_scratch(int hip_ordinal);

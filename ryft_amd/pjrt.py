@@ -589,6 +589,16 @@ class Plugin:
     def client(self, options: Optional[Dict[str, object]] = None) -> "Client":
         return Client._create(self, options or {})
 
+    def profiler_extension(self):
+        """Plugin::profiler_extension (extensions/profiler.rs:103-125)."""
+        from . import profiler
+        return profiler.extension(self.api())
+
+    def profiler(self, options=None):
+        """Plugin::profiler (extensions/profiler.rs:127-145): a profiler session of this plugin."""
+        from . import profiler
+        return self.profiler_extension().profiler(options or profiler.ProfileOptions())
+
 
 def load_plugin(path: str = DEFAULT_PLUGIN_PATH) -> Plugin:
     """Loads (once per canonical path) the plugin at `path` (plugins.rs:91-106, 120-122)."""
@@ -1146,6 +1156,15 @@ class Client(_Owned):
                 nv.type, nv.string_value, nv.value_size = 0, C.cast(C.c_char_p(sb), _vp), len(sb)
         a = api.call("PJRT_Client_Create", create_options=vals, num_options=len(options))
         return Client(plugin, a.client)
+
+    def profiler_extension(self):
+        """Client::profiler_extension (extensions/profiler.rs:26-60)."""
+        return self.plugin.profiler_extension()
+
+    def profiler(self, options=None):
+        """Client::profiler (extensions/profiler.rs:62-80): a profiler session; it records the work of every client
+        of the plugin while started."""
+        return self.plugin.profiler(options)
 
     def platform_name(self) -> str:
         a = self.api.call("PJRT_Client_PlatformName", client=self.handle)

@@ -7,7 +7,7 @@ import ctypes
 import numpy as np
 import pytest
 
-from ryft_amd import configs, hostdata as hd, pjrt
+from ryft_amd import configs, hostdata as hd, pjrt, profiler
 from tests.helpers import run_pjrt
 
 pytestmark = pytest.mark.gpu
@@ -121,3 +121,55 @@ def test_compile_options_choose_the_device(gpu_client):
     b = configs.HostInput(np.array([[35], [-41]], np.int32), pjrt.BufferType.S32, (2, 1))
     outs, _ = run_pjrt(gpu_client, "", [a, b], executable=le)
     assert outs[0].ravel().tolist() == [42, -42]
+
+
+def test_profiler(gpu_client):
+    """ryft-pjrt's test_profiler (extensions/profiler.rs:552-628): profile compiling and running the i32 add known
+    answer; the results hold no errors, the host plane the compilation and the execution, and the device plane the
+    add's kernel step with its algorithmic bytes."""
+    opts = profiler.ProfileOptions(version=1, device_type=1, host_tracing_level=2, device_tracing_level=1)
+    prof = gpu_client.profiler(opts)
+    other = gpu_client.profiler(opts)  # two sessions started together both record
+    prof.start()
+    other.start()
+    ins = [configs.HostInput(np.array([[7], [-1]], np.int32), pjrt.BufferType.S32, (2, 1)),
+           configs.HostInput(np.array([[35], [-41]], np.int32), pjrt.BufferType.S32, (2, 1))]
+    outs, _ = run_pjrt(gpu_client, ADD_PROGRAM, ins)
+    assert outs[0].reshape(-1).tolist() == [42, -42]
+    prof.stop()
+    other.stop()
+    space = prof.results()
+    assert space.errors == []
+    host = [e.name for e in space.plane("/host:CPU").lines[0].events]
+    assert "compile main" in host and "execute main" in host
+    dev = space.plane("/device:GPU:0")
+    assert dev is not None
+    (line,) = dev.lines
+    assert len(line.events) >= 1
+    for ev in line.events:
+        assert ev.duration_ps > 0 and ev.offset_ps >= 0
+    assert sum(ev.stats["bytes accessed"] for ev in line.events) == 24  # two 8-byte operands, one 8-byte result
+    assert [e.name for e in other.results().plane("/device:GPU:0").lines[0].events] == [e.name for e in line.events]
+
+
+def test_profiler_device_events_time_the_gemm(gpu_client):
+    """A bf16 batched GEMM under the profiler: one device event per plan step, named by its kernel, with the step's
+    algorithmic flops, lasting about what the plugin's own kernel timing reports for the same steps."""
+    w = configs.c2_bf16_batched_dot(batch=4, m=512, k=512, n=512)
+    le = gpu_client.compile(pjrt.Program.mlir(w.program))
+    dev = gpu_client.addressable_devices()[0]
+    bufs = [gpu_client.buffer(x.data, x.type, x.dims, device=dev) for x in w.inputs]
+    le.execute([bufs])[0].done.await_()  # warm
+    prof = gpu_client.profiler()
+    prof.start()
+    for _ in range(3):
+        le.execute([bufs])[0].done.await_()
+    prof.stop()
+    line = prof.results().plane("/device:GPU:0").lines[0]
+    gemm = [e for e in line.events if e.name.startswith("gemm_bf16")]
+    assert len(gemm) == 3, [e.name for e in line.events]
+    for e in gemm:
+        assert e.stats["flops"] == 2.0 * 4 * 512 * 512 * 512
+        assert 1e6 < e.duration_ps < 5e9  # 1 µs .. 5 ms
+    offs = [e.offset_ps for e in gemm]
+    assert offs == sorted(offs) and offs[0] >= 0

@@ -10,7 +10,7 @@ import subprocess
 import pytest
 
 from tests import row_programs
-from ryft_amd import configs, pjrt
+from ryft_amd import configs, pjrt, profiler
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
@@ -68,7 +68,74 @@ def test_extension_chain(plugin):
     assert plugin.api().extension(pjrt.RYFT_MI355X_EXTENSION_TYPE) is not None
     assert plugin.api().extension(pjrt.PJRT_EXTENSION_TYPE_LAYOUTS) is not None
     assert plugin.api().extension(pjrt.PJRT_EXTENSION_TYPE_MEMORY_DESCRIPTIONS) is not None
-    assert plugin.api().extension(1) is None  # no profiler extension: ryft-pjrt reports Unimplemented
+    assert plugin.api().extension(profiler.PJRT_EXTENSION_TYPE_PROFILER) is not None
+
+
+def test_profiler_extension(plugin, compile_client):
+    # as ryft-pjrt's test_profiler_extension (extensions/profiler.rs:536-550) for the GPU plugins
+    assert plugin.profiler_extension().trace_me_context_id == 0
+    assert compile_client.profiler_extension().table == plugin.profiler_extension().table
+
+
+def test_profiler_session_records_compilation(compile_client):
+    """Create → start → compile → stop → results on a compile-only client: a host plane with the compilation's span,
+    no device plane (nothing ran) and no errors."""
+    prof = compile_client.profiler(profiler.ProfileOptions(version=1, device_type=1, host_tracing_level=2,
+                                                           device_tracing_level=1))
+    prof.start()
+    compile_client.compile(pjrt.Program.mlir(ADD_2X1))
+    prof.stop()
+    space = prof.results()
+    assert space.errors == []
+    host = space.plane("/host:CPU")
+    assert host is not None and [p.name for p in space.planes] == ["/host:CPU"]
+    (line,) = host.lines
+    assert [e.name for e in line.events] == ["compile main"]
+    assert line.events[0].duration_ps > 0 and line.timestamp_ns > 0
+    assert prof.results_bytes() == prof.results_bytes()  # serialization is deterministic
+
+
+def test_profiler_session_errors_and_levels(compile_client, plugin):
+    prof = plugin.profiler()
+    with pytest.raises(pjrt.PjrtError) as e:
+        prof.stop()  # never started
+    assert e.value.code == pjrt.ErrorCode.FAILED_PRECONDITION
+    prof.start()
+    with pytest.raises(pjrt.PjrtError) as e:
+        prof.start()
+    assert e.value.code == pjrt.ErrorCode.FAILED_PRECONDITION
+    with pytest.raises(pjrt.PjrtError) as e:
+        prof.results()  # still running
+    assert e.value.code == pjrt.ErrorCode.FAILED_PRECONDITION
+    prof.stop()
+    assert prof.results().errors == []
+    # host tracing level 0: no host plane; compilations after stop are not recorded by a stopped session
+    quiet = compile_client.profiler(profiler.ProfileOptions(host_tracing_level=0))
+    quiet.start()
+    compile_client.compile(pjrt.Program.mlir(ADD_2X1))
+    quiet.stop()
+    assert quiet.results().planes == []
+    compile_client.compile(pjrt.Program.mlir(ADD_2X1))
+    assert [e.name for e in prof.results().plane("/host:CPU").lines[0].events] == []
+    # version 0 stands for the default session, whatever the levels say
+    default = compile_client.profiler(profiler.ProfileOptions(version=0, host_tracing_level=0))
+    default.start()
+    compile_client.compile(pjrt.Program.mlir(ADD_2X1))
+    default.stop()
+    assert [p.name for p in default.results().planes] == ["/host:CPU"]
+    ext = plugin.profiler_extension()
+    bad = (ctypes.c_ubyte * 2)(0x10, 0x80)  # field 2, varint truncated
+    args = profiler._CreateArgs(0, ctypes.cast(bad, ctypes.c_void_p), 2, None)
+    with pytest.raises(pjrt.PjrtError) as e:
+        ext.call("PLUGIN_Profiler_Create", args)
+    assert e.value.code == pjrt.ErrorCode.INVALID_ARGUMENT and "profile options" in str(e.value)
+
+
+def test_profile_options_encoding():
+    # field numbers of tensorflow.ProfileOptions (protos.rs:3423-3490)
+    enc = profiler.ProfileOptions(version=1, device_type=1, host_tracing_level=2, device_tracing_level=1).encode()
+    assert enc == bytes([0x10, 2, 0x18, 1, 0x28, 1, 0x30, 1])
+    assert profiler.ProfileOptions(version=0, host_tracing_level=0, device_tracing_level=0).encode() == b""
 
 
 def test_layouts_extension_default_layouts(compile_client):
@@ -545,20 +612,23 @@ _EXIT_SCRIPT = r'''
 import atexit, sys
 sys.path.insert(0, sys.argv[1])
 state = {}
-atexit.register(lambda: print("after hook:", state["client"].handle is None, state["exe"].handle is None, flush=True))
+atexit.register(lambda: print("after hook:", state["client"].handle is None, state["exe"].handle is None,
+                              state["prof"].handle is None, flush=True))
 from ryft_amd import pjrt  # its exit hook is registered after the one above, so it runs first
 client = pjrt.load_plugin().client({"compile_only": True})
+prof = client.profiler()
+prof.start()  # left started
 exe = client.compile(pjrt.Program.mlir(sys.argv[2]))
-state.update(client=client, exe=exe)
+state.update(client=client, exe=exe, prof=prof)
 print("compiled", flush=True)
 '''
 
 
 def test_wrappers_alive_at_interpreter_exit_are_destroyed():
-    """Objects still referenced from __main__ at exit are destroyed by the module's exit hook (executables before
-    their client) while ctypes is intact, instead of reaching finalizers that can no longer call the plugin."""
+    """Objects still referenced from __main__ at exit are destroyed by the module's exit hook (executables and a
+    started profiler session before their client) while ctypes is intact, instead of reaching finalizers that can no longer call the plugin."""
     import sys
     r = subprocess.run([sys.executable, "-c", _EXIT_SCRIPT, ROOT, ADD_2X1], capture_output=True, text=True,
                        timeout=120)
     assert r.returncode == 0, r.stderr
-    assert r.stdout.split() == ["compiled", "after", "hook:", "True", "True"], r.stdout + r.stderr
+    assert r.stdout.split() == ["compiled", "after", "hook:", "True", "True", "True"], r.stdout + r.stderr
