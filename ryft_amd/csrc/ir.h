@@ -83,6 +83,11 @@ struct Graph {
   std::vector<Node> nodes;
   std::vector<int> params;   // node ids, in argument order
   std::vector<int> results;  // node ids, in return order
+  // Input/output aliasing declared on the parameters (func argument attributes): `tf.aliasing_output = k` names the
+  // result the parameter's buffer may become when donated; `jax.buffer_donor = true` lets the compiler pick one.
+  // Empty, or one entry per parameter.
+  std::vector<int> param_alias;     // result index or -1
+  std::vector<bool> param_donor;
   std::string name = "main";
   std::vector<std::vector<int>> users() const;
   std::string dump() const;

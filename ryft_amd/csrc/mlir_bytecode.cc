@@ -856,6 +856,26 @@ class BytecodeParser {
       g.params.push_back(id);
       node_of[body.args[k]] = id;
     }
+    // parameters' aliasing attributes (arg_attrs: one dictionary per argument)
+    g.param_alias.assign(body.args.size(), -1);
+    g.param_donor.assign(body.args.size(), false);
+    if (const BAttr* aa = get(fn, "arg_attrs")) {
+      if (aa->kind == BAttr::ARRAY && aa->elems.size() == body.args.size()) {
+        for (size_t k = 0; k < aa->elems.size(); ++k) {
+          const BAttr& d = attr(aa->elems[k]);
+          if (d.kind != BAttr::DICT) continue;
+          for (auto& [name, idx] : d.dict) {
+            const BAttr& v = attr(idx);
+            if (name == "tf.aliasing_output") {
+              if (v.kind != BAttr::INT || v.i < 0) invalid("tf.aliasing_output must be a result index");
+              g.param_alias[k] = (int)v.i;
+            } else if (name == "jax.buffer_donor") {
+              g.param_donor[k] = v.kind == BAttr::UNIT || (v.kind == BAttr::INT && v.i != 0);
+            }
+          }
+        }
+      }
+    }
     auto value = [&](int64_t v) {
       auto it = node_of.find(v);
       if (it == node_of.end()) unimplemented("an operand is not produced by a supported op");

@@ -507,7 +507,9 @@ class Parser {
         std::string nm = c_.sigil_name('%');
         c_.expect(":");
         TensorType tt = parse_type(c_);
-        if (c_.peek() == '{') { c_.expect("{"); c_.skip_balanced('{', '}'); }
+        std::map<std::string, std::string> attrs;
+        if (c_.try_consume("{")) parse_attr_dict(attrs);
+        record_aliasing(attrs);
         Node n;
         n.op = Op::Parameter;
         n.type = tt;
@@ -533,6 +535,24 @@ class Parser {
       }
     }
     if (c_.try_consume("attributes")) { c_.expect("{"); c_.skip_balanced('{', '}'); }
+  }
+
+  // A parameter's aliasing attributes: `tf.aliasing_output = k : i32`, `jax.buffer_donor = true`.
+  void record_aliasing(const std::map<std::string, std::string>& attrs) {
+    int alias = -1;
+    bool donor = false;
+    auto it = attrs.find("tf.aliasing_output");
+    if (it != attrs.end()) {
+      const std::string v = it->second.substr(0, it->second.find(':'));
+      char* end = nullptr;
+      const long k = strtol(v.c_str(), &end, 10);
+      if (end == v.c_str() || k < 0 || k > (1 << 20)) c_.error("tf.aliasing_output must be a result index");
+      alias = (int)k;
+    }
+    it = attrs.find("jax.buffer_donor");
+    if (it != attrs.end()) donor = it->second.empty() || it->second.find("true") != std::string::npos;
+    graph_.param_alias.push_back(alias);
+    graph_.param_donor.push_back(donor);
   }
 
   int add(Node n) {
@@ -583,7 +603,8 @@ class Parser {
     // after '{' or '<{' consumed; parse `name = value, ...` up to the closing '}'
     for (;;) {
       if (c_.try_consume("}")) return;
-      std::string key = c_.ident();
+      c_.skip_ws();
+      std::string key = c_.peek_raw() == '"' ? c_.quoted() : c_.ident();
       std::string val;
       if (c_.try_consume("=")) val = raw_attr_value();
       attrs[key] = val;

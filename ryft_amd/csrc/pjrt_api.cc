@@ -689,12 +689,15 @@ PJRT_Error* Executable_GetCompiledMemoryStats(PJRT_Executable_GetCompiledMemoryS
     else if (sl.kind == Slot::TEMP) temp += n;
     else cst += n;
   }
+  int64_t alias = 0;  // results that can take over a donated argument's memory
+  for (size_t o = 0; o < e.plan.output_alias.size(); ++o)
+    if (e.plan.output_alias[o] >= 0) alias += (int64_t)e.plan.output_types[o].bytes();
   // kernels are compiled into the plugin; the executable's device memory is its arguments, outputs, planned
   // temporaries and uploaded constants
   args->generated_code_size_in_bytes = 0;
   args->argument_size_in_bytes = arg;
   args->output_size_in_bytes = out;
-  args->alias_size_in_bytes = 0;
+  args->alias_size_in_bytes = alias;
   args->temp_size_in_bytes = temp;
   args->host_generated_code_size_in_bytes = 0;
   args->host_argument_size_in_bytes = 0;
@@ -846,7 +849,9 @@ PJRT_Error* LoadedExecutable_Execute(PJRT_LoadedExecutable_Execute_Args* args) {
     std::vector<Buffer*> outs;
     Buffer* const* argv = reinterpret_cast<Buffer* const*>(args->argument_lists ? args->argument_lists[d] : nullptr);
     if (!argv && args->num_args) return make_pjrt_error(PJRT_Error_Code_INVALID_ARGUMENT, "argument list is null");
-    EventPtr done = execute(le, dev, argv, args->num_args, &outs);
+    const PJRT_ExecuteOptions* o = args->options;
+    EventPtr done = execute(le, dev, argv, args->num_args, &outs, o ? o->non_donatable_input_indices : nullptr,
+                            o ? o->num_non_donatable_input_indices : 0);
     for (size_t o = 0; o < outs.size(); ++o) args->output_lists[d][o] = to<PJRT_Buffer>(outs[o]);
     if (args->device_complete_events) args->device_complete_events[d] = wrap_event(done);
   }

@@ -137,6 +137,8 @@ class Planner {
   }
 
   Plan run();
+  void plan_aliasing();
+  bool in_place(int param_slot, int output_slot) const;
 
   View view_of(int node);
   bool materialized(int node) const { return mat_.count(node) > 0; }
@@ -1646,7 +1648,86 @@ Plan Planner::run() {
     plan_.total_flops += st.flops;
     plan_.total_bytes += st.bytes;
   }
+  plan_aliasing();
   return std::move(plan_);
+}
+
+// Aliasing declared on the parameters (tf.aliasing_output, jax.buffer_donor), checked as XLA's alias config is:
+// result index in range, one parameter per result, identical types.
+void Planner::plan_aliasing() {
+  const size_t np = g_.params.size(), no = g_.results.size();
+  plan_.output_alias.assign(no, -1);
+  plan_.output_in_place.assign(no, false);
+  auto type_text = [](const TensorType& t) { return t.str(); };
+  for (size_t p = 0; p < np && p < g_.param_alias.size(); ++p) {
+    const int o = g_.param_alias[p];
+    if (o < 0) continue;
+    if ((size_t)o >= no)
+      invalid("parameter " + std::to_string(p) + " is aliased to result " + std::to_string(o) + " but the function has " +
+              std::to_string(no) + " result(s)");
+    if (plan_.output_alias[o] >= 0)
+      invalid("result " + std::to_string(o) + " is aliased to both parameter " + std::to_string(plan_.output_alias[o]) +
+              " and parameter " + std::to_string(p));
+    if (!(plan_.param_types[p] == plan_.output_types[o]))
+      invalid("parameter " + std::to_string(p) + " (" + type_text(plan_.param_types[p]) + ") cannot alias result " +
+              std::to_string(o) + " (" + type_text(plan_.output_types[o]) + "): the types differ");
+    plan_.output_alias[o] = (int)p;
+  }
+  // buffer donors take the first result of their type that no parameter claims
+  for (size_t p = 0; p < np && p < g_.param_donor.size(); ++p) {
+    if (!g_.param_donor[p] || (p < g_.param_alias.size() && g_.param_alias[p] >= 0)) continue;
+    for (size_t o = 0; o < no; ++o)
+      if (plan_.output_alias[o] < 0 && plan_.param_types[p] == plan_.output_types[o]) {
+        plan_.output_alias[o] = (int)p;
+        break;
+      }
+  }
+  for (size_t o = 0; o < no; ++o)
+    if (plan_.output_alias[o] >= 0)
+      plan_.output_in_place[o] = in_place(plan_.param_slots[plan_.output_alias[o]], plan_.output_slots[o]);
+}
+
+// Whether the result slot `os` can live in the parameter slot `ps`'s memory: one step writes the result, no later step
+// reads the parameter, and that step reads the parameter only at the element it writes (an elementwise step whose
+// parameter leaves are identity views, or a whole-buffer copy of the parameter).
+bool Planner::in_place(int ps, int os) const {
+  const auto& steps = plan_.steps;
+  int writer = -1;
+  for (size_t i = 0; i < steps.size(); ++i)
+    for (auto& pt : steps[i].patches)
+      if (pt.second == os) {
+        if (writer >= 0 && writer != (int)i) return false;
+        writer = (int)i;
+      }
+  if (writer < 0) return false;
+  for (size_t i = writer + 1; i < steps.size(); ++i)
+    for (auto& pt : steps[i].patches)
+      if (pt.second == ps) return false;
+  const Step& st = steps[writer];
+  const int64_t bytes = plan_.slots[os].type.bytes();
+  if (st.kind == Step::COPY)
+    return st.patches.size() == 2 && st.patches[0].second == ps && st.patches[1].second == os &&
+           st.copy.src_offset == 0 && st.copy.bytes == bytes;
+  if (st.kind != Step::ELEMENTWISE) return false;
+  const EwProgram& e = st.ew;
+  if (e.out_strided || e.total != num_elements(plan_.slots[ps].type.shape)) return false;
+  for (auto& pt : st.patches) {
+    bool ok = false;
+    if (pt.second == ps) {
+      for (int l = 0; l < e.n_leaves; ++l) {
+        const EwLeaf& L = e.leaves[l];
+        if (pt.first == offsetof(EwProgram, leaves) + l * sizeof(EwLeaf) + offsetof(EwLeaf, ptr))
+          ok = L.kind == EW_LEAF_IDENTITY && L.offset == 0 && (uintptr_t)L.ptr == 0;
+      }
+    } else if (pt.second == os) {
+      for (int k = 0; k < e.n_out; ++k)
+        if (pt.first == offsetof(EwProgram, out_ptr) + k * sizeof(void*)) ok = (uintptr_t)e.out_ptr[k] == 0;
+    } else {
+      ok = true;
+    }
+    if (!ok) return false;
+  }
+  return true;
 }
 
 }  // namespace
@@ -1675,6 +1756,10 @@ std::string Plan::describe() const {
     }
     os << " flops=" << s.flops << " bytes=" << s.bytes << "\n";
   }
+  for (size_t o = 0; o < output_alias.size(); ++o)
+    if (output_alias[o] >= 0)
+      os << "alias: result " << o << " <- parameter " << output_alias[o]
+         << (output_in_place[o] ? " (in place)" : " (own buffer)") << "\n";
   return os.str();
 }
 

@@ -48,6 +48,11 @@ struct Plan {
   std::vector<int> param_slots;   // per graph parameter
   std::vector<int> output_slots;  // per graph result
   std::vector<TensorType> param_types, output_types;
+  // Input/output aliasing, per result: the parameter whose buffer the result takes over when that argument is
+  // donated (-1: none), and whether the steps can compute the result straight into the donated buffer (else the
+  // result gets a buffer of its own and the donated one is released after the execution).
+  std::vector<int> output_alias;
+  std::vector<bool> output_in_place;
   double total_flops = 0, total_bytes = 0;
   std::string describe() const;
 };

@@ -648,7 +648,8 @@ bool enqueue_steps(Client* c, const Plan& plan, void* const* ptr, hipStream_t st
     if (step.kind == Step::COPY) {
       void* src = (char*)ptr[step.patches[0].second] + step.copy.src_offset;
       void* dst = ptr[step.patches[1].second];
-      if (step.copy.bytes) HIP_CHECK(hipMemcpyAsync(dst, src, (size_t)step.copy.bytes, hipMemcpyDeviceToDevice, st));
+      if (step.copy.bytes && dst != src)  // (a result computed in place over its donated parameter: nothing to copy)
+        HIP_CHECK(hipMemcpyAsync(dst, src, (size_t)step.copy.bytes, hipMemcpyDeviceToDevice, st));
     } else {
       size_t sz = step.kind == Step::ELEMENTWISE ? sizeof(EwProgram)
                   : step.kind == Step::REDUCE    ? sizeof(ReduceArgs)
@@ -686,7 +687,8 @@ bool enqueue_steps(Client* c, const Plan& plan, void* const* ptr, hipStream_t st
   return recorded;
 }
 
-EventPtr execute(LoadedExecutable* le, Device* d, Buffer* const* args, size_t num_args, std::vector<Buffer*>* outputs) {
+EventPtr execute(LoadedExecutable* le, Device* d, Buffer* const* args, size_t num_args, std::vector<Buffer*>* outputs,
+                 const int64_t* non_donatable, size_t num_non_donatable) {
   const int64_t host_begin = wall_clock_ns();
   Executable& exe = *le->exe;
   const Plan& plan = exe.plan;
@@ -703,6 +705,27 @@ EventPtr execute(LoadedExecutable* le, Device* d, Buffer* const* args, size_t nu
       invalid("argument " + std::to_string(i) + " has type " + TensorType{b->dtype, b->dims}.str() + " but the program expects " + t.str());
     if (b->device != d) invalid("argument " + std::to_string(i) + " lives on another device");
   }
+  // donation (XLA's aliasing semantics): an argument aliased to a result is donated unless the caller marked it
+  // non-donatable, in which case the result simply gets a buffer of its own
+  std::vector<int> donated_to(num_args, -1);  // argument → result
+  for (size_t o = 0; o < plan.output_alias.size(); ++o) {
+    const int p = plan.output_alias[o];
+    if (p < 0) continue;
+    bool keep = false;
+    for (size_t k = 0; k < num_non_donatable; ++k) {
+      if (non_donatable[k] < 0 || (size_t)non_donatable[k] >= num_args)
+        invalid("non-donatable input index " + std::to_string(non_donatable[k]) + " is out of range");
+      keep |= non_donatable[k] == p;
+    }
+    if (keep) continue;
+    Buffer* b = args[p];
+    if (b->external_refs.load() > 0)
+      invalid("argument " + std::to_string(p) + " is donated but has external references");
+    for (size_t i = 0; i < num_args; ++i)
+      if (i != (size_t)p && args[i] == b)
+        invalid("argument " + std::to_string(p) + " is donated but the same buffer is also argument " + std::to_string(i));
+    donated_to[p] = (int)o;
+  }
   std::vector<void*> ptr(plan.slots.size(), nullptr);
   std::vector<std::shared_ptr<DeviceMem>> hold(plan.slots.size());
   for (size_t s = 0; s < plan.slots.size(); ++s) {
@@ -710,7 +733,18 @@ EventPtr execute(LoadedExecutable* le, Device* d, Buffer* const* args, size_t nu
     switch (sl.kind) {
       case Slot::PARAM: ptr[s] = args[sl.index]->mem->ptr; break;
       case Slot::CONSTANT: ptr[s] = exe.constants[s]->ptr; break;
-      case Slot::OUTPUT: case Slot::TEMP:
+      case Slot::OUTPUT: {
+        const int p = plan.output_alias.empty() ? -1 : plan.output_alias[sl.index];
+        if (p >= 0 && donated_to[p] == sl.index && plan.output_in_place[sl.index]) {
+          hold[s] = args[p]->mem;  // computed straight into the donated buffer
+          ptr[s] = hold[s]->ptr;
+          break;
+        }
+        hold[s] = c->allocate(d, sl.type.bytes());
+        ptr[s] = hold[s]->ptr;
+        break;
+      }
+      case Slot::TEMP:
         hold[s] = c->allocate(d, sl.type.bytes());
         ptr[s] = hold[s]->ptr;
         break;
@@ -749,6 +783,13 @@ EventPtr execute(LoadedExecutable* le, Device* d, Buffer* const* args, size_t nu
     b->ready = done;
     outputs->push_back(b.release());
   }
+  // donated arguments are gone; their memory lives on in the result that took it over, or returns to the allocator
+  // (ordered after this execution's reads on the device's one stream)
+  for (size_t i = 0; i < num_args; ++i)
+    if (donated_to[i] >= 0) {
+      args[i]->deleted = true;
+      args[i]->mem.reset();
+    }
   if (profiler_sessions_active()) profiler_record_host("execute " + exe.name, host_begin, wall_clock_ns());
   return done;
 }

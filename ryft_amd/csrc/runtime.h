@@ -274,8 +274,11 @@ std::shared_ptr<Executable> deserialize_executable(Client* c, const char* data, 
 EventPtr buffer_raw_to_host(Buffer* b, void* dst, int64_t offset, int64_t size);
 std::shared_ptr<Executable> compile_program(Client* c, const std::string& code, const std::string& format,
                                             const std::string& options);
-// Enqueues one execution; fills outputs and returns the completion event.
-EventPtr execute(LoadedExecutable* le, Device* d, Buffer* const* args, size_t num_args, std::vector<Buffer*>* outputs);
+// Enqueues one execution; fills outputs and returns the completion event. Arguments that the program aliases to a
+// result are donated unless their index is in `non_donatable`: the result takes over (or replaces) the argument's
+// device memory and the argument buffer is marked deleted.
+EventPtr execute(LoadedExecutable* le, Device* d, Buffer* const* args, size_t num_args, std::vector<Buffer*>* outputs,
+                 const int64_t* non_donatable = nullptr, size_t num_non_donatable = 0);
 // Enqueues every step of `plan` on `st`, slot s living at ptr[s] (the caller has made the plan's device current).
 // `done` (optional) is recorded by the last kernel launch when it can; returns whether it was. With `prof`, each
 // step's first and last launch record timing events appended to c->timings; while a profiler session is started,

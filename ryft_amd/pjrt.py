@@ -1074,16 +1074,23 @@ class LoadedExecutable(_Owned):
             if len(dev) != input_count:
                 raise PjrtError(ErrorCode.INVALID_ARGUMENT,
                                 f"expected {input_count} input(s) for each device but got {len(dev)} for device {d}")
-        # the options (every input non-donatable) depend only on the input count and launch id: built once each
-        key = (input_count, launch_id)
+        donatable = tuple(x.donatable for x in norm[0]) if norm else ()
+        for d, dev in enumerate(norm):
+            for i, x in enumerate(dev):
+                if x.donatable != donatable[i]:
+                    raise PjrtError(ErrorCode.INVALID_ARGUMENT, f"input {i} is not marked consistently across all "
+                                                                "devices as donatable or non-donatable")
+        # the options depend only on which inputs are donatable and the launch id: built once each
+        key = (donatable, launch_id)
         cached = self.__dict__.setdefault("_options", {}).get(key)
         if cached is None:
-            nd = (C.c_int64 * max(input_count, 1))(*range(input_count))
+            keep = [i for i, dn in enumerate(donatable) if not dn]
+            nd = (C.c_int64 * max(len(keep), 1))(*keep)
             opts = ExecuteOptions()
             opts.struct_size = C.sizeof(opts)
             opts.launch_id = launch_id
             opts.non_donatable_input_indices = nd
-            opts.num_non_donatable_input_indices = input_count
+            opts.num_non_donatable_input_indices = len(keep)
             cached = self._options[key] = (nd, opts, C.pointer(opts))
         opts_ptr = cached[2]
         arg_arrays = [(_vp * max(input_count, 1))(*[x.buffer.handle for x in dev]) for dev in norm]

@@ -60,9 +60,9 @@ def parse_tensor(t: str) -> Tuple[Tuple[int, ...], str]:
 def _split_top(s: str, sep: str = ",") -> List[str]:
     out, depth, cur = [], 0, ""
     for ch in s:
-        if ch in "<[(":
+        if ch in "<[({":
             depth += 1
-        elif ch in ">])":
+        elif ch in ">])}":
             depth -= 1
         if ch == sep and depth == 0:
             out.append(cur)
@@ -113,7 +113,7 @@ def parse_module(text: str):
     assert m, "no func.func @main"
     args = [a.strip() for a in _split_top(m.group(1))]
     arg_names = [a.split(":")[0].strip() for a in args]
-    arg_types = [a.split(":", 1)[1].strip() for a in args]
+    arg_types = [a.split(":", 1)[1].split("{")[0].strip() for a in args]  # (argument attributes: arg_attr_dicts)
     res = m.group(2).strip()
     res_types = _split_top(res[1:-1]) if res.startswith("(") else [res]
     body = text[m.end():]
@@ -134,6 +134,23 @@ def parse_module(text: str):
             name, rest = "stablehlo.reduce", rhs[len("stablehlo.reduce"):]
         ops.append(_parse_op(lhs, name, rest))
     return arg_names, arg_types, res_types, ops, returned
+
+
+def arg_attr_dicts(text: str) -> List[Dict[str, Tuple[str, str]]]:
+    """Per argument of `func.func @main`, its attribute dictionary: name → (value, type), e.g.
+    {"tf.aliasing_output": ("0", "i32")}; a value without a type is a bool ("true") or a unit attribute ("")."""
+    m = re.search(r"func\.func\s+(?:public\s+)?@main\((.*?)\)\s*->", text, re.S)
+    out = []
+    for a in _split_top(m.group(1)):
+        d = {}
+        if "{" in a:
+            body = a[a.index("{") + 1:a.rindex("}")]
+            for item in _split_top(body):
+                k, _, v = item.partition("=")
+                val, _, ty = v.partition(":")
+                d[k.strip().strip('"')] = (val.strip(), ty.strip())
+        out.append(d)
+    return out
 
 
 def _parse_op(res: str, name: str, rest: str) -> Op:
@@ -424,6 +441,21 @@ class Writer:
         fbody = varint(1) + varint(n_func_values) + self._block([self.tensor(t) for t in arg_types], body_ops)
         fattrs = {"sym_name": self.string_attr("main"),
                   "function_type": self.attr(("type", self.fn_type(arg_types, res_types)))}
+        dicts = arg_attr_dicts(text)
+        if any(dicts):  # arg_attrs: ArrayAttr of DictionaryAttr (builtin codes 0 and 1)
+            elems = []
+            for d in dicts:
+                entries = b""
+                for k, (val, ty) in sorted(d.items()):
+                    if ty:
+                        v = self.battr(varint(8) + varint(self.elem(ty)) + svarint(int(val)))
+                    elif val in ("true", "false"):
+                        v = self.battr(varint(8) + varint(self.elem("i1")) + bytes([val == "true"]))
+                    else:
+                        v = self.battr(varint(7))
+                    entries += varint(self.string_attr(k)) + varint(v)
+                elems.append(self.battr(varint(1) + varint(len(d)) + entries))
+            fattrs["arg_attrs"] = self.battr(varint(0) + varint(len(elems)) + b"".join(varint(e) for e in elems))
         func = self._op("func.func", fattrs, [], [], fbody, True, 1)
         mbody = varint(1) + varint(0) + self._block([], [func])
         module = self._op("builtin.module", {}, [], [], mbody, True, 1)

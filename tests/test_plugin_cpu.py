@@ -632,3 +632,42 @@ def test_wrappers_alive_at_interpreter_exit_are_destroyed():
                        timeout=120)
     assert r.returncode == 0, r.stderr
     assert r.stdout.split() == ["compiled", "after", "hook:", "True", "True", "True"], r.stdout + r.stderr
+
+
+# ----------------------------------------------------------------------------------------------- input donation
+@pytest.mark.parametrize("name,expect", [
+    ("SGD", ["alias: result 0 <- parameter 0 (in place)"]),
+    ("GEMM", ["alias: result 0 <- parameter 0 (own buffer)"]),
+    ("TRANSPOSED", ["alias: result 0 <- parameter 0 (own buffer)"]),
+    ("PASSTHROUGH", ["alias: result 1 <- parameter 0 (in place)"]),
+    ("DONOR", ["alias: result 1 <- parameter 0 (in place)"]),
+])
+@pytest.mark.parametrize("form", ["text", "bytecode"])
+def test_aliasing_plans(compile_client, name, expect, form):
+    """Aliasing declared on func arguments (text attribute dictionaries, or bytecode arg_attrs) reaches the plan; a
+    result is computed in place over its donated parameter only when no step reads the parameter after (or, in the
+    writing step, apart from) the element being written."""
+    from tests import donation_programs as dp, mlir_bytecode
+    text = getattr(dp, name)
+    code = text if form == "text" else mlir_bytecode.to_bytecode(text)
+    le = compile_client.compile(pjrt.Program.mlir(code))
+    lines = [ln for ln in le.describe_plan().splitlines() if ln.startswith("alias:")]
+    assert lines == expect
+    st = le.executable().memory_statistics()
+    nbytes = {"SGD": 4 << 16, "GEMM": 2 * 256 * 256, "TRANSPOSED": 4 * 64 * 64, "PASSTHROUGH": 4096, "DONOR": 2048}
+    assert st["alias_size_in_bytes"] == nbytes[name]
+
+
+def test_no_aliasing_without_attributes(compile_client):
+    le = compile_client.compile(pjrt.Program.mlir(ADD_2X1))
+    assert "alias:" not in le.describe_plan()
+    assert le.executable().memory_statistics()["alias_size_in_bytes"] == 0
+
+
+@pytest.mark.parametrize("name", ["result_out_of_range", "type_mismatch", "two_parameters_one_result"])
+def test_malformed_aliasing_is_invalid_argument(compile_client, name):
+    from tests import donation_programs as dp
+    program, fragment = dp.BAD[name]
+    with pytest.raises(pjrt.PjrtError) as e:
+        compile_client.compile(pjrt.Program.mlir(program))
+    assert e.value.code == pjrt.ErrorCode.INVALID_ARGUMENT and fragment in str(e.value), str(e.value)
