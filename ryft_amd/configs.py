@@ -122,20 +122,25 @@ def c3_int8_gemm(m=4096, k=4096, n=4096, seed=0xC3) -> Workload:
 
 
 # ----------------------------------------------------------------------------------------------- C4
-def c4_causal_attention(b=4, h=32, s=2048, d=128, seed=0xC4, mask="GE", fill="0xFF800000", p_type="bf16") -> Workload:
+def c4_causal_attention(b=4, h=32, s=2048, d=128, seed=0xC4, mask="GE", fill="0xFF800000", p_type="bf16",
+                        sk=None) -> Workload:
     """Causal softmax attention written as plain StableHLO: dot → scale → iota/compare/select mask → reduce-max →
     subtract → exp → reduce-sum → divide → convert → dot → convert.
 
     The defaults are BASELINE.json's C4. Variants for tests: `mask` is the comparison direction of row (query) index
     against column (key) index ("GT": a strict mask, query 0 sees no key); `fill` the select's fill for masked
     scores (an MLIR float literal); p_type="f32" feeds the f32 probabilities to the second dot_general directly
-    (f32 × bf16 operands, no convert)."""
+    (f32 × bf16 operands, no convert); mask=None drops the mask (plain softmax attention), and `sk` then sets a key /
+    value length of its own."""
+    sk = s if sk is None else sk
+    assert sk == s or mask is None
     qt = _t((b, h, s, d), "bf16")
-    sf = _t((b, h, s, s), "f32")
-    sb = _t((b, h, s, s), "bf16")
-    pi = _t((b, h, s, s), "i1")
-    mi = _t((s, s), "i32")
-    mp = _t((s, s), "i1")
+    kt = _t((b, h, sk, d), "bf16")
+    sf = _t((b, h, s, sk), "f32")
+    sb = _t((b, h, s, sk), "bf16")
+    pi = _t((b, h, s, sk), "i1")
+    mi = _t((s, sk), "i32")
+    mp = _t((s, sk), "i1")
     rf = _t((b, h, s), "f32")
     of = _t((b, h, s, d), "f32")
     scale = _f32_literal(1.0 / math.sqrt(d))
@@ -147,20 +152,25 @@ def c4_causal_attention(b=4, h=32, s=2048, d=128, seed=0xC4, mask="GE", fill="0x
         p_line, p_ref, p_ty = f"    %16 = stablehlo.convert %15 : ({sf}) -> {sb}\n", "%16", sb
     else:
         p_line, p_ref, p_ty = "", "%15", sf
-    prog = f"""module {{
-  func.func @main(%arg0: {qt}, %arg1: {qt}, %arg2: {qt}) -> {qt} {{
-    %0 = stablehlo.dot_general %arg0, %arg1, batching_dims = [0, 1] x [0, 1], contracting_dims = [3] x [3] : ({qt}, {qt}) -> {sf}
-    %cst = stablehlo.constant dense<{scale}> : tensor<f32>
-    %1 = stablehlo.broadcast_in_dim %cst, dims = [] : (tensor<f32>) -> {sf}
-    %2 = stablehlo.multiply %0, %1 : {sf}
-    %3 = stablehlo.iota dim = 0 : {mi}
+    scaled = "%2" if mask is not None else "%8"  # the scaled scores (unmasked: the softmax's input itself)
+    if mask is None:
+        mask_lines = "    %cst_0 = stablehlo.constant dense<0xFF800000> : tensor<f32>\n"
+    else:
+        mask_lines = f"""    %3 = stablehlo.iota dim = 0 : {mi}
     %4 = stablehlo.iota dim = 1 : {mi}
     %5 = stablehlo.compare  {mask}, %3, %4,  SIGNED : ({mi}, {mi}) -> {mp}
     %6 = stablehlo.broadcast_in_dim %5, dims = [2, 3] : ({mp}) -> {pi}
     %cst_0 = stablehlo.constant dense<0xFF800000> : tensor<f32>
 {fill_cst}    %7 = stablehlo.broadcast_in_dim {fill_ref}, dims = [] : (tensor<f32>) -> {sf}
     %8 = stablehlo.select %6, %2, %7 : {pi}, {sf}
-    %9 = stablehlo.reduce(%8 init: %cst_0) applies stablehlo.maximum across dimensions = [3] : ({sf}, tensor<f32>) -> {rf}
+"""
+    prog = f"""module {{
+  func.func @main(%arg0: {qt}, %arg1: {kt}, %arg2: {kt}) -> {qt} {{
+    %0 = stablehlo.dot_general %arg0, %arg1, batching_dims = [0, 1] x [0, 1], contracting_dims = [3] x [3] : ({qt}, {kt}) -> {sf}
+    %cst = stablehlo.constant dense<{scale}> : tensor<f32>
+    %1 = stablehlo.broadcast_in_dim %cst, dims = [] : (tensor<f32>) -> {sf}
+    {scaled} = stablehlo.multiply %0, %1 : {sf}
+{mask_lines}    %9 = stablehlo.reduce(%8 init: %cst_0) applies stablehlo.maximum across dimensions = [3] : ({sf}, tensor<f32>) -> {rf}
     %10 = stablehlo.broadcast_in_dim %9, dims = [0, 1, 2] : ({rf}) -> {sf}
     %11 = stablehlo.subtract %8, %10 : {sf}
     %12 = stablehlo.exponential %11 : {sf}
@@ -168,15 +178,16 @@ def c4_causal_attention(b=4, h=32, s=2048, d=128, seed=0xC4, mask="GE", fill="0x
     %13 = stablehlo.reduce(%12 init: %cst_1) applies stablehlo.add across dimensions = [3] : ({sf}, tensor<f32>) -> {rf}
     %14 = stablehlo.broadcast_in_dim %13, dims = [0, 1, 2] : ({rf}) -> {sf}
     %15 = stablehlo.divide %12, %14 : {sf}
-{p_line}    %17 = stablehlo.dot_general {p_ref}, %arg2, batching_dims = [0, 1] x [0, 1], contracting_dims = [3] x [2] : ({p_ty}, {qt}) -> {of}
+{p_line}    %17 = stablehlo.dot_general {p_ref}, %arg2, batching_dims = [0, 1] x [0, 1], contracting_dims = [3] x [2] : ({p_ty}, {kt}) -> {of}
     %18 = stablehlo.convert %17 : ({of}) -> {qt}
     return %18 : {qt}
   }}
 }}
 """
-    ins = [HostInput(hd.f32_to_bf16_bits(hd.normal(seed * 16 + i, (b, h, s, d))), BufferType.BF16, (b, h, s, d))
-           for i in range(3)]
-    flops = 4.0 * b * h * d * s * (s + 1) / 2.0  # unmasked (k <= q) pairs only
+    ins = [HostInput(hd.f32_to_bf16_bits(hd.normal(seed * 16 + i, (b, h, n, d))), BufferType.BF16, (b, h, n, d))
+           for i, n in enumerate((s, sk, sk))]
+    # unmasked (k <= q) pairs only
+    flops = 4.0 * b * h * d * s * (s + 1) / 2.0 if mask is not None else 4.0 * b * h * d * s * sk
     return Workload("c4_causal_attention", prog, ins, flops=flops, bytes=2.0 * 4 * b * h * s * d,
                     compute_dtype="bf16", tolerance=2e-2,
                     info={"full_square_flops": 4.0 * b * h * s * s * d, "exps": b * h * s * (s + 1) / 2})

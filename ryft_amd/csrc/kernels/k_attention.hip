@@ -105,41 +105,28 @@ __global__ void __launch_bounds__(256, 2) attention_fwd_kernel(const AttnArgs A)
   using C = AttnCfg<D>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  // Query blocks of 128. Under a causal mask the work of a block grows with its index, so a workgroup takes the
+  // blocks p and nq-1-p (the larger first): every workgroup then has the same work. The workgroups of one (batch,
+  // head) are consecutive on one XCD (workgroup x runs on XCD x mod 8), so they run together and share that XCD's
+  // L2 for the head's keys and values.
   const int nq = A.Sq / BQ;
-  // Under a causal mask the work of a query block grows with its index. Workgroups are dispatched in blockIdx order,
-  // so the query block is the slow index and runs heaviest first across all heads (longest-first scheduling): the
-  // short blocks fill the tail instead of one head's long blocks finishing last.
-  const int nbh = (int)gridDim.x / nq;
-  const int qb = A.causal ? nq - 1 - (int)(blockIdx.x / nbh) : (int)(blockIdx.x / nbh);
-  const int bh = blockIdx.x % nbh;
+  const bool pairs = A.causal && nq > 1;
+  const int W = pairs ? (nq + 1) / 2 : nq;  // workgroups per (batch, head)
+  const int nbh = A.B * A.H;
+  int bh, p;
+  if (nbh % 8 == 0) {
+    const int slot = (int)blockIdx.x >> 3;
+    bh = (slot / W) * 8 + ((int)blockIdx.x & 7);
+    p = slot % W;
+  } else {
+    bh = (int)blockIdx.x / W;
+    p = (int)blockIdx.x % W;
+  }
   const int b = bh / A.H, h = bh % A.H;
-  const int q0 = qb * BQ;
   const uint16_t* Qg = (const uint16_t*)A.q + (int64_t)b * A.qs[0] + (int64_t)h * A.qs[1];
   const char* Kg = (const char*)A.k + ((int64_t)b * A.ks[0] + (int64_t)h * A.ks[1]) * 2;
   const char* Vg = (const char*)A.v + ((int64_t)b * A.vs[0] + (int64_t)h * A.vs[1]) * 2;
-
-  // Q fragments (B operand of Sᵀ = K·Qᵀ): lane holds Q[q][s·16 + 8·(lane/32) .. +8] for its query q
-  const int myq = q0 + wave * 32 + (lane & 31);
-  u32x4a qf[D / 16];
-#pragma unroll
-  for (int s = 0; s < D / 16; ++s)
-    qf[s] = *(const u32x4a*)(Qg + (int64_t)myq * A.qs[2] + s * 16 + 8 * (lane >> 5));
-  // complete the Q loads here: waited for at their first use inside the loop, the wait would run every iteration
-  // and stall on the next KV block's prefetch (vmcnt(0), expcnt / lgkmcnt left open)
-  __builtin_amdgcn_s_waitcnt(0x0F70);
-
-  const float sl2 = A.scale * 1.4426950408889634f;  // logits in the log2 domain
-  float m_run = -INFINITY, l_run = 0.f;
-  f32x16_a o[D / 32];
-#pragma unroll
-  for (int t = 0; t < D / 32; ++t) o[t] = f32x16_a{};
-
-  int nkv = A.Sk / BKV;
-  if (A.causal) {
-    int last_key = q0 + BQ - 1 + A.causal_offset;  // largest key any query of this block may see
-    int lim = last_key < 0 ? 0 : last_key / BKV + 1;
-    if (lim < nkv) nkv = lim;
-  }
 
   // K and V blocks (64 keys × D) go from global memory straight into LDS (buffer_load … lds, 16 bytes per lane):
   // each wave-wide load fills one contiguous 1 KB piece, lane l writing bytes [16l, 16l+16) of it, so the swizzle is
@@ -148,7 +135,6 @@ __global__ void __launch_bounds__(256, 2) attention_fwd_kernel(const AttnArgs A)
   // and the per-lane byte offsets are loop-invariant (the launcher checks that they fit 32 bits).
   const int ks2 = (int)A.ks[2], vs2 = (int)A.vs[2];
   constexpr int PPW = C::PIECES / 4;  // pieces per wave per tensor
-  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   // the swizzle depends on the row modulo 16 only, which is the same for all pieces of a wave: piece i is piece 0
   // moved down 4096 / RB rows, a scalar offset
   const int r0 = (wave_u * 1024 + lane * 16) / C::RB;
@@ -181,137 +167,193 @@ __global__ void __launch_bounds__(256, 2) attention_fwd_kernel(const AttnArgs A)
   const int v_lo = vr0 * C::RB + 16 * (vcl ^ kv_swz<D>(vr0)) + 8 * (lane & 1);
   const int v_hi = (vr0 + 8) * C::RB + 16 * (vcl ^ kv_swz<D>(vr0 + 8)) + 8 * (lane & 1);
 
-  if (nkv > 0) dma(0, 0);
-  dma_wait_sync();
-  for (int j = 0; j < nkv; ++j) {
-    const int cur = j & 1;
-    if (j + 1 < nkv) dma(j + 1, cur ^ 1);
-    const char* sK = smem + cur * C::STAGE;
-    const char* sV = sK + C::KBYTES;
-    // Sᵀ tiles: keys [32t, 32t+32) × this wave's 32 queries
-    f32x16_a st[2] = {f32x16_a{}, f32x16_a{}};
+  const float sl2 = A.scale * 1.4426950408889634f;  // logits in the log2 domain
+  const int ntiles = pairs && 2 * p + 1 != nq ? 2 : 1;
+  for (int ti = 0; ti < ntiles; ++ti) {
+    const int qb = pairs ? (ti == 0 ? nq - 1 - p : p) : p;
+    const int q0 = qb * BQ;
+    // Q fragments (B operand of Sᵀ = K·Qᵀ): lane holds Q[q][s·16 + 8·(lane/32) .. +8] for its query q
+    const int myq = q0 + wave * 32 + (lane & 31);
+    u32x4a qf[D / 16];
 #pragma unroll
-    for (int s = 0; s < D / 16; ++s) {
+    for (int s = 0; s < D / 16; ++s)
+      qf[s] = *(const u32x4a*)(Qg + (int64_t)myq * A.qs[2] + s * 16 + 8 * (lane >> 5));
+    // complete the Q loads here: waited for at their first use inside the loop, the wait would run every iteration
+    // and stall on the next KV block's prefetch (vmcnt(0), expcnt / lgkmcnt left open)
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    // Q·scale·log2 e, rounded to bf16 (a relative error of 2^-9 per element, about 1e-3 in a probability): the
+    // score MFMAs then yield logits in the log2 domain, and with the accumulator started at -m (the lane's exponent
+    // reference) they yield the exponents themselves, so that a probability costs one v_exp_f32 and no FMA
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        u32x4a kf = *(const u32x4a*)(sK + t * 32 * C::RB + (k_lane ^ (32 * s)));
-        st[t] = mma_bf16(kf, qf[s], st[t]);
+    for (int s = 0; s < D / 16; ++s)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t w = qf[s][k];
+        qf[s][k] = pack_bf16(__uint_as_float(w << 16) * sl2, __uint_as_float(w & 0xFFFF0000u) * sl2);
       }
+
+    // m_run: the lane's exponent reference in the log2 domain (-inf until its first visible score), cinit its
+    // negation (0 while there is none), the score accumulators' start
+    float m_run = -INFINITY, l_run = 0.f;
+    f32x16_a cinit = f32x16_a{};
+    f32x16_a o[D / 32];
+#pragma unroll
+    for (int t = 0; t < D / 32; ++t) o[t] = f32x16_a{};
+
+    int nkv = A.Sk / BKV;
+    if (A.causal) {
+      int last_key = q0 + BQ - 1 + A.causal_offset;  // largest key any query of this block may see
+      int lim = last_key < 0 ? 0 : last_key / BKV + 1;
+      if (lim < nkv) nkv = lim;
     }
-    // mask and block max on the unscaled scores (the scale is positive, so maxima commute with it); only blocks that
-    // reach past this wave's first query need the causal mask (a wave-uniform branch between two copies)
-    const int kbase = j * BKV;
-    const bool need_mask = A.causal && (kbase + BKV - 1 > q0 + wave * 32 + A.causal_offset);
-    float mloc = -INFINITY;
-    if (need_mask) {
+
+    if (nkv > 0) dma(0, 0);
+    dma_wait_sync();
+    for (int j = 0; j < nkv; ++j) {
+      const int cur = j & 1;
+      if (j + 1 < nkv) dma(j + 1, cur ^ 1);
+      const char* sK = smem + cur * C::STAGE;
+      const char* sV = sK + C::KBYTES;
+      // Sᵀ tiles: keys [32t, 32t+32) × this wave's 32 queries
+      f32x16_a st[2] = {cinit, cinit};
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int s = 0; s < D / 16; ++s) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kbase + t * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-          const float v = key > myq + A.causal_offset ? -INFINITY : st[t][r];
-          st[t][r] = v;
-          mloc = fmaxf(mloc, v);
+        for (int t = 0; t < 2; ++t) {
+          u32x4a kf = *(const u32x4a*)(sK + t * 32 * C::RB + (k_lane ^ (32 * s)));
+          st[t] = mma_bf16(kf, qf[s], st[t]);
         }
-    } else {
+      }
+      // mask and block max on the exponents (logits relative to the reference); only blocks that reach past this
+      // wave's first query need the causal mask (a wave-uniform branch between two copies)
+      const int kbase = j * BKV;
+      const bool need_mask = A.causal && (kbase + BKV - 1 > q0 + wave * 32 + A.causal_offset);
+      float mloc = -INFINITY;
+      if (need_mask) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, st[t][r]);
+          for (int r = 0; r < 16; ++r) {
+            const int key = kbase + t * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+            const float v = key > myq + A.causal_offset ? -INFINITY : st[t][r];
+            st[t][r] = v;
+            mloc = fmaxf(mloc, v);
+          }
+      } else {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, st[t][r]);
+      }
+      // the other half-wave's maximum, by a lane swap across the halves (no LDS round trip): one of the swap's two
+      // results holds it, the other this lane's own value
+      {
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mloc), __float_as_uint(mloc), false, false);
+        mloc = fmaxf(mloc, fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])));
+      }
+      // Lazy rescaling: the exponent reference m_run only moves when this block's maximum exceeds it by more than 8
+      // (probabilities then stay ≤ 2^8; o and l share the reference, so o / l is unchanged), and the rescale of o
+      // runs only when some lane moved its reference; otherwise P = 2^exponent with no further arithmetic.
+      // (bitwise operators: a short-circuit would become a divergent branch)
+      const bool raise = (mloc > 8.0f) | ((m_run == -INFINITY) & (mloc != -INFINITY));
+      u32x4a pf[4];
+      // P packed to bf16 (round to nearest even) as the B operand of Oᵀ = Vᵀ·Pᵀ; l sums the packed probabilities
+      // (one v_dot2 against (1, 1) per pair), so that o / l weighs V by exactly the probabilities P·V uses
+      auto probs = [&]() {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          float p[16];
+#pragma unroll
+          for (int r = 0; r < 16; ++r) p[r] = __builtin_amdgcn_exp2f(st[t][r]);
+          uint32_t w[8];
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            w[k] = pack_bf16(p[2 * k], p[2 * k + 1]);
+            l_run = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_a, w[k]),
+                                                    __builtin_bit_cast(bf16x2_a, 0x3F803F80u), l_run, false);
+          }
+          pf[2 * t] = u32x4a{w[0], w[1], w[2], w[3]};
+          pf[2 * t + 1] = u32x4a{w[4], w[5], w[6], w[7]};
+        }
+      };
+      if (__builtin_amdgcn_ballot_w64(raise)) {
+        const float shift = raise ? mloc : 0.f;                       // the reference moves up by the block max
+        const float m_new = raise ? (m_run == -INFINITY ? 0.f : m_run) + mloc : m_run;
+        const float alpha = raise ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.f;  // 0 from a reference of -inf
+        l_run *= alpha;
+#pragma unroll
+        for (int t = 0; t < D / 32; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
+        m_run = m_new;
+        const float c = m_run == -INFINITY ? 0.f : -m_run;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) cinit[r] = c;
+        // this block's exponents relative to the new reference
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) st[t][r] -= shift;
+      }
+      probs();
+      // Oᵀ[d, q] += Σ_key Vᵀ[d, key] · P[q, key]; k-step s covers keys [16s, 16s+16) in the accumulator's key order:
+      // element e of lane l ↔ key 16s + 8·(e/4) + 4·(l/32) + e%4. The Vᵀ fragment (row d = l % 32) is read from the
+      // [key][d] tile with two ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i % 4 of the
+      // 8-byte chunks addressed by lanes i/4 + 4m (m = 0..3), so lane i addresses key row k0 + i/4 and column
+      // c0 + 4·(i % 4), and receives keys k0 .. k0+3 of column c0 + i — with k0 = 16s + 4·(l/32) and k0 + 8, exactly
+      // the accumulator's key order.
+      // Fragments of k-step s + 1 are read while the MFMAs of k-step s run (two register sets).
+      const uint32_t vaddr = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const char*)sV;
+      u32x2a vf[2][2 * (D / 32)];
+      auto vread = [&](auto sc, u32x2a (&f)[2 * (D / 32)]) {
+        constexpr int S = decltype(sc)::value;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) {
+          f[2 * dt] = lds_read_tr16_asm<16 * S * C::RB>(vaddr + (v_lo ^ (64 * dt)));
+          f[2 * dt + 1] = lds_read_tr16_asm<16 * S * C::RB>(vaddr + (v_hi ^ (64 * dt)));
+        }
+      };
+      vread(std::integral_constant<int, 0>{}, vf[0]);
+      static_for4([&](auto sc) {
+        constexpr int S = decltype(sc)::value;
+        tr16_wait(vf[S & 1]);
+        if constexpr (S + 1 < BKV / 16) vread(std::integral_constant<int, S + 1>{}, vf[(S + 1) & 1]);
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) {
+          const u32x2a lo = vf[S & 1][2 * dt], hi = vf[S & 1][2 * dt + 1];
+          o[dt] = mma_bf16(u32x4a{lo.x, lo.y, hi.x, hi.y}, pf[S], o[dt]);
+        }
+      });
+      dma_wait_sync();
     }
-    // the other half-wave's maximum, by a lane swap across the halves (no LDS round trip): one of the swap's two
-    // results holds it, the other this lane's own value
-    {
-      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mloc), __float_as_uint(mloc), false, false);
-      mloc = fmaxf(mloc, fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])));
-    }
-    // Lazy rescaling: the exponent reference m_run only moves when this block's maximum exceeds it by more than 8 in
-    // log2 units (probabilities then stay ≤ 2^8; o and l share the reference, so o / l is unchanged), and the
-    // rescale of o is skipped when no lane moved its reference.
-    // (bitwise operators: a short-circuit would become a divergent branch)
-    const bool raise = ((mloc - m_run) * sl2 > 8.0f) | ((m_run == -INFINITY) & (mloc != -INFINITY));
-    const float m_new = raise ? mloc : m_run;
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;  // a fully masked row keeps p = 0
-    if (__builtin_amdgcn_ballot_w64(raise)) {
-      const float alpha = __builtin_amdgcn_exp2f((m_run - m_use) * sl2);  // 1 where the reference did not move
-      l_run *= alpha;
+
+    // normalise and write out through LDS (lane-per-query layout → row-major rows)
+    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+    const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+    float* so = (float*)smem;
+    const int ql = wave * 32 + (lane & 31);
 #pragma unroll
-      for (int t = 0; t < D / 32; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
-    }
-    m_run = m_new;
-    // P = 2^((s - m)·scale·log2 e) with one FMA and v_exp_f32 per score, packed to bf16 (round to nearest even) as
-    // the B operand of Oᵀ = Vᵀ·Pᵀ
-    const float mb = -m_use * sl2;
-    u32x4a pf[4];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      float p[16];
+    for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        p[r] = __builtin_amdgcn_exp2f(fmaf(st[t][r], sl2, mb));
-        l_run += p[r];
+        int d = dt * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+        *(float*)((char*)so + ql * C::OP + d * 4) = o[dt][r] * inv;
       }
-      pf[2 * t] = u32x4a{pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3]), pack_bf16(p[4], p[5]), pack_bf16(p[6], p[7])};
-      pf[2 * t + 1] = u32x4a{pack_bf16(p[8], p[9]), pack_bf16(p[10], p[11]), pack_bf16(p[12], p[13]), pack_bf16(p[14], p[15])};
-    }
-    // Oᵀ[d, q] += Σ_key Vᵀ[d, key] · P[q, key]; k-step s covers keys [16s, 16s+16) in the accumulator's key order:
-    // element e of lane l ↔ key 16s + 8·(e/4) + 4·(l/32) + e%4. The Vᵀ fragment (row d = l % 32) is read from the
-    // [key][d] tile with two ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i % 4 of the
-    // 8-byte chunks addressed by lanes i/4 + 4m (m = 0..3), so lane i addresses key row k0 + i/4 and column
-    // c0 + 4·(i % 4), and receives keys k0 .. k0+3 of column c0 + i — with k0 = 16s + 4·(l/32) and k0 + 8, exactly
-    // the accumulator's key order.
-    // Fragments of k-step s + 1 are read while the MFMAs of k-step s run (two register sets).
-    const uint32_t vaddr = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const char*)sV;
-    u32x2a vf[2][2 * (D / 32)];
-    auto vread = [&](auto sc, u32x2a (&f)[2 * (D / 32)]) {
-      constexpr int S = decltype(sc)::value;
-#pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt) {
-        f[2 * dt] = lds_read_tr16_asm<16 * S * C::RB>(vaddr + (v_lo ^ (64 * dt)));
-        f[2 * dt + 1] = lds_read_tr16_asm<16 * S * C::RB>(vaddr + (v_hi ^ (64 * dt)));
+    __syncthreads();
+    char* Og = (char*)A.o;
+    const int osz = A.out_dtype == DT_F32 ? 4 : 2;
+    for (int idx = tid; idx < BQ * D / 4; idx += 256) {
+      int qr = idx / (D / 4), c4 = idx % (D / 4);
+      float4 v = *(const float4*)((char*)so + qr * C::OP + c4 * 16);
+      int64_t off = (int64_t)b * A.os[0] + (int64_t)h * A.os[1] + (int64_t)(q0 + qr) * A.os[2] + c4 * 4;
+      if (osz == 4) {
+        *(float4*)(Og + off * 4) = v;
+      } else {
+        uint2 pk = uint2{pack_bf16(v.x, v.y), pack_bf16(v.z, v.w)};
+        *(uint2*)(Og + off * 2) = pk;
       }
-    };
-    vread(std::integral_constant<int, 0>{}, vf[0]);
-    static_for4([&](auto sc) {
-      constexpr int S = decltype(sc)::value;
-      tr16_wait(vf[S & 1]);
-      if constexpr (S + 1 < BKV / 16) vread(std::integral_constant<int, S + 1>{}, vf[(S + 1) & 1]);
-#pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt) {
-        const u32x2a lo = vf[S & 1][2 * dt], hi = vf[S & 1][2 * dt + 1];
-        o[dt] = mma_bf16(u32x4a{lo.x, lo.y, hi.x, hi.y}, pf[S], o[dt]);
-      }
-    });
-    dma_wait_sync();
-  }
-
-  // normalise and write out through LDS (lane-per-query layout → row-major rows)
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
-  const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-  float* so = (float*)smem;
-  const int ql = wave * 32 + (lane & 31);
-#pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      int d = dt * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-      *(float*)((char*)so + ql * C::OP + d * 4) = o[dt][r] * inv;
     }
-  __syncthreads();
-  char* Og = (char*)A.o;
-  const int osz = A.out_dtype == DT_F32 ? 4 : 2;
-  for (int idx = tid; idx < BQ * D / 4; idx += 256) {
-    int qr = idx / (D / 4), c4 = idx % (D / 4);
-    float4 v = *(const float4*)((char*)so + qr * C::OP + c4 * 16);
-    int64_t off = (int64_t)b * A.os[0] + (int64_t)h * A.os[1] + (int64_t)(q0 + qr) * A.os[2] + c4 * 4;
-    if (osz == 4) {
-      *(float4*)(Og + off * 4) = v;
-    } else {
-      uint2 pk = uint2{pack_bf16(v.x, v.y), pack_bf16(v.z, v.w)};
-      *(uint2*)(Og + off * 2) = pk;
-    }
+    __syncthreads();  // the next block's key / value loads reuse the staging area
   }
 }
 
@@ -337,7 +379,9 @@ const char* attention_unsupported(const AttnArgs& a) {
 
 void launch_attention(const AttnArgs& a, hipStream_t stream, hipEvent_t done) {
   if (const char* why = attention_unsupported(a)) fail(PJRT_Error_Code_UNIMPLEMENTED, why);
-  int64_t blocks = (int64_t)a.B * a.H * (a.Sq / BQ);
+  // workgroups: per (batch, head), one per query block, or one per pair of blocks under a causal mask
+  const int64_t nq = a.Sq / BQ;
+  const int64_t blocks = (int64_t)a.B * a.H * (a.causal && nq > 1 ? (nq + 1) / 2 : nq);
   if (blocks == 0) return record_done(done, stream);
   hipError_t e;
   if (a.D == 128) {

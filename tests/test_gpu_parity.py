@@ -159,7 +159,16 @@ def test_c3_int8_full(gpu_client):
     _run_and_check(gpu_client, configs.c3_int8_gemm())
 
 
-@pytest.mark.parametrize("kw", [dict(b=1, h=2, s=256, d=128), dict(b=2, h=1, s=128, d=64), dict(b=1, h=1, s=512, d=128)])
+@pytest.mark.parametrize("kw", [dict(b=1, h=2, s=256, d=128), dict(b=2, h=1, s=128, d=64), dict(b=1, h=1, s=512, d=128),
+                                # unmasked, key blocks of 64 in odd and even counts (the last step computes no next
+                                # block's scores; the first is the last when there is one)
+                                dict(b=1, h=2, s=128, d=128, mask=None, sk=192),
+                                dict(b=1, h=1, s=256, d=64, mask=None, sk=320),
+                                dict(b=1, h=2, s=128, d=128, mask=None, sk=64),
+                                dict(b=2, h=1, s=256, d=128, mask=None),
+                                # causal with an odd number of 256-query tiles (the middle one alone) and a last tile
+                                # of 128 queries
+                                dict(b=1, h=3, s=640, d=128), dict(b=1, h=2, s=384, d=64)])
 def test_c4_attention_small(gpu_client, kw):
     w = configs.c4_causal_attention(**kw)
     outs, exe = _run_and_check(gpu_client, w)
