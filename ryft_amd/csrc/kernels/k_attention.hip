@@ -228,7 +228,11 @@ __global__ void __launch_bounds__(256, 2) attention_fwd_kernel(const AttnArgs A)
       // wave's first query need the causal mask (a wave-uniform branch between two copies)
       const int kbase = j * BKV;
       const bool need_mask = A.causal && (kbase + BKV - 1 > q0 + wave * 32 + A.causal_offset);
-      float mloc = -INFINITY;
+      // The maximum as a signed integer over the exponents' bit patterns: among positive floats the order is the
+      // integers' and every negative float (-inf included) is a negative integer, so it tells whether any exponent
+      // exceeds 8 — with integer instructions, which run beside the other wave's MFMAs where float ones do not.
+      // The float maximum itself is only needed when the reference moves (the rare branch below).
+      int imax = (int)0x80000000u;
       if (need_mask) {
 #pragma unroll
         for (int t = 0; t < 2; ++t)
@@ -237,25 +241,26 @@ __global__ void __launch_bounds__(256, 2) attention_fwd_kernel(const AttnArgs A)
             const int key = kbase + t * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
             const float v = key > myq + A.causal_offset ? -INFINITY : st[t][r];
             st[t][r] = v;
-            mloc = fmaxf(mloc, v);
+            imax = max(imax, (int)__float_as_uint(v));
           }
       } else {
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, st[t][r]);
+          for (int r = 0; r < 16; ++r) imax = max(imax, (int)__float_as_uint(st[t][r]));
       }
       // the other half-wave's maximum, by a lane swap across the halves (no LDS round trip): one of the swap's two
       // results holds it, the other this lane's own value
-      {
-        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mloc), __float_as_uint(mloc), false, false);
-        mloc = fmaxf(mloc, fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])));
-      }
+      auto halves = [](int v) {
+        const auto sw = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+        return max(v, max((int)sw[0], (int)sw[1]));
+      };
+      imax = halves(imax);
       // Lazy rescaling: the exponent reference m_run only moves when this block's maximum exceeds it by more than 8
       // (probabilities then stay ≤ 2^8; o and l share the reference, so o / l is unchanged), and the rescale of o
-      // runs only when some lane moved its reference; otherwise P = 2^exponent with no further arithmetic.
-      // (bitwise operators: a short-circuit would become a divergent branch)
-      const bool raise = (mloc > 8.0f) | ((m_run == -INFINITY) & (mloc != -INFINITY));
+      // runs only when some lane moved its reference (or has none yet); otherwise P = 2^exponent with no further
+      // arithmetic.
+      const bool maybe = (imax > (int)0x41000000) | (m_run == -INFINITY);  // 0x41000000 = 8.0f
       u32x4a pf[4];
       // P packed to bf16 (round to nearest even) as the B operand of Oᵀ = Vᵀ·Pᵀ; l sums the packed probabilities
       // (one v_dot2 against (1, 1) per pair), so that o / l weighs V by exactly the probabilities P·V uses
@@ -276,7 +281,18 @@ __global__ void __launch_bounds__(256, 2) attention_fwd_kernel(const AttnArgs A)
           pf[2 * t + 1] = u32x4a{w[4], w[5], w[6], w[7]};
         }
       };
-      if (__builtin_amdgcn_ballot_w64(raise)) {
+      if (__builtin_amdgcn_ballot_w64(maybe)) {
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, st[t][r]);
+        {
+          const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mloc), __float_as_uint(mloc), false, false);
+          mloc = fmaxf(mloc, fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])));
+        }
+        // (bitwise operators: a short-circuit would become a divergent branch)
+        const bool raise = (mloc > 8.0f) | ((m_run == -INFINITY) & (mloc != -INFINITY));
         const float shift = raise ? mloc : 0.f;                       // the reference moves up by the block max
         const float m_new = raise ? (m_run == -INFINITY ? 0.f : m_run) + mloc : m_run;
         const float alpha = raise ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.f;  // 0 from a reference of -inf
