@@ -48,6 +48,16 @@ __device__ __forceinline__ void vstore(char* p, const T& v) {
   else *(T*)p = v;
 }
 
+// N consecutive 32-bit words as 16-byte stores, then an 8- and a 4-byte store for the rest.
+template <bool NT, int N>
+__device__ __forceinline__ void store_words_nt(char* p, const uint32_t* w) {
+#pragma unroll
+  for (int i = 0; i + 4 <= N; i += 4) vstore<NT>(p + 4 * i, u32x4v{w[i], w[i + 1], w[i + 2], w[i + 3]});
+  constexpr int R = N & ~3;
+  if constexpr ((N & 3) >= 2) vstore<NT>(p + 4 * R, u32x2v{w[R], w[R + 1]});
+  if constexpr (N & 1) vstore<NT>(p + 4 * (N - 1), w[N - 1]);
+}
+
 template <int V, bool NT = false>
 __device__ __forceinline__ void store_vec(void* out, int64_t lin, int dtype, const uint32_t* v, bool is_float) {
   static_assert(V == 4 || V == 8, "vector stores are written for 4 or 8 elements");
@@ -200,6 +210,131 @@ __global__ void __launch_bounds__(VNT) ew_stream_kernel(const EwProgram P) {
   }
 }
 
+// Direct form of the commonest streaming maps: one float operation (negate, abs, add, subtract, multiply, divide,
+// maximum, minimum, convert) over one or two contiguous leaves of one type (f32 or bf16), or a leaf and a constant,
+// written as f32 or bf16 — with no interpreter: the operation is picked by a uniform switch outside the element
+// loop, each thread takes one 16-byte vector per leaf, and the grid covers the iteration space (a probe of this
+// shape streams a 256 MiB copy at ~6.6 TB/s). Same arithmetic and rounding as the interpreter's instructions.
+struct MapArgs {
+  const void* a;
+  const void* b;      // second leaf, or null (constant operand or unary)
+  void* out;
+  uint32_t imm;       // constant operand (f32 bits)
+  int32_t op;         // EwOp
+  int32_t b_kind;     // 0 none, 1 leaf, 2 constant
+  int32_t b_first;    // the leaf / constant is the first operand (a - b with the constant on the left)
+  int64_t chunks;     // 16-byte input vectors
+};
+
+template <int OP>
+__device__ __forceinline__ float map_op(float x, float y) {
+  if constexpr (OP == EW_NEG) return -x;
+  else if constexpr (OP == EW_ABS) return fabsf(x);
+  else if constexpr (OP == EW_CVT_F2F) return x;
+  else if constexpr (OP == EW_ADD) return x + y;
+  else if constexpr (OP == EW_SUB) return x - y;
+  else if constexpr (OP == EW_MUL) return x * y;
+  else if constexpr (OP == EW_DIV) return x / y;
+  else if constexpr (OP == EW_MAX) return (x != x || y != y) ? __uint_as_float(0x7fc00000u) : fmaxf(x, y);
+  else return (x != x || y != y) ? __uint_as_float(0x7fc00000u) : fminf(x, y);  // EW_MIN
+}
+
+// ES: leaf element size (4: f32, 2: bf16); OUT_BF16: results rounded to and stored as bf16
+template <int OP, int ES, bool OUT_BF16, bool NT>
+__device__ __forceinline__ void map_loop(const MapArgs& A) {
+  constexpr int V = 16 / ES;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < A.chunks; c += stride) {
+    const u32x4v wa = NT ? __builtin_nontemporal_load((const u32x4v*)A.a + c) : ((const u32x4v*)A.a)[c];
+    u32x4v wb = u32x4v{A.imm, A.imm, A.imm, A.imm};
+    if (A.b_kind == 1) wb = NT ? __builtin_nontemporal_load((const u32x4v*)A.b + c) : ((const u32x4v*)A.b)[c];
+    float r[V];
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      const uint32_t ua = ES == 4 ? wa[e] : ((e & 1) ? (wa[e >> 1] & 0xffff0000u) : (wa[e >> 1] << 16));
+      const uint32_t ub = A.b_kind != 1 ? A.imm : ES == 4 ? wb[e] : ((e & 1) ? (wb[e >> 1] & 0xffff0000u) : (wb[e >> 1] << 16));
+      const float x = __uint_as_float(ua), y = __uint_as_float(ub);
+      r[e] = A.b_first ? map_op<OP>(y, x) : map_op<OP>(x, y);
+    }
+    if constexpr (OUT_BF16) {
+      uint32_t w[V / 2];
+#pragma unroll
+      for (int q = 0; q < V / 2; ++q) w[q] = f32x2_to_bf16x2_bits(r[2 * q], r[2 * q + 1]);
+      store_words_nt<NT, V / 2>((char*)A.out + c * (V * 2), w);
+    } else {
+      uint32_t w[V];
+#pragma unroll
+      for (int e = 0; e < V; ++e) w[e] = __float_as_uint(r[e]);
+      store_words_nt<NT, V>((char*)A.out + c * (V * 4), w);
+    }
+  }
+}
+
+template <int ES, bool OUT_BF16, bool NT>
+__global__ void __launch_bounds__(256) ew_map_kernel(const MapArgs A) {
+  switch (A.op) {
+    case EW_NEG: map_loop<EW_NEG, ES, OUT_BF16, NT>(A); break;
+    case EW_ABS: map_loop<EW_ABS, ES, OUT_BF16, NT>(A); break;
+    case EW_CVT_F2F: map_loop<EW_CVT_F2F, ES, OUT_BF16, NT>(A); break;
+    case EW_ADD: map_loop<EW_ADD, ES, OUT_BF16, NT>(A); break;
+    case EW_SUB: map_loop<EW_SUB, ES, OUT_BF16, NT>(A); break;
+    case EW_MUL: map_loop<EW_MUL, ES, OUT_BF16, NT>(A); break;
+    case EW_DIV: map_loop<EW_DIV, ES, OUT_BF16, NT>(A); break;
+    case EW_MAX: map_loop<EW_MAX, ES, OUT_BF16, NT>(A); break;
+    case EW_MIN: map_loop<EW_MIN, ES, OUT_BF16, NT>(A); break;
+    default: break;
+  }
+}
+
+// Recognises a program of that form: loads and constants, then one such operation whose result is the one output.
+static bool map_args(const EwProgram& v, MapArgs* m) {
+  if (v.n_out != 1 || v.needs_coords || v.out_strided || v.n_leaves < 1 || v.n_leaves > 2 || v.n_instr < 2) return false;
+  const int ldt = v.leaves[0].dtype;
+  if (ldt != DT_F32 && ldt != DT_BF16) return false;
+  const int es = ldt == DT_F32 ? 4 : 2;
+  for (int i = 0; i < v.n_leaves; ++i) {
+    const EwLeaf& L = v.leaves[i];
+    if (L.dtype != ldt || L.kind == EW_LEAF_SCALAR || L.vmode != EW_VEC_CONTIG) return false;
+    if (((uintptr_t)L.ptr + (uintptr_t)(L.offset * es)) % 16) return false;
+  }
+  // sources of the registers before the operation: leaf index (>= 0), constant (-2), undefined (-1)
+  int src[EW_MAX_REGS];
+  uint32_t imm[EW_MAX_REGS];
+  for (int r = 0; r < EW_MAX_REGS; ++r) src[r] = -1, imm[r] = 0;
+  for (int i = 0; i + 1 < v.n_instr; ++i) {
+    const EwInstr& I = v.instr[i];
+    if (I.dst >= EW_MAX_REGS) return false;
+    if (I.op == EW_LOAD && (I.round == 0 || I.round == ldt)) src[I.dst] = I.a;
+    else if (I.op == EW_CONST) src[I.dst] = -2, imm[I.dst] = I.imm.u;
+    else return false;
+  }
+  const EwInstr& I = v.instr[v.n_instr - 1];
+  const bool unary = I.op == EW_NEG || I.op == EW_ABS || I.op == EW_CVT_F2F;
+  const bool binary = I.op == EW_ADD || I.op == EW_SUB || I.op == EW_MUL || I.op == EW_DIV || I.op == EW_MAX ||
+                      I.op == EW_MIN;
+  if (!(unary || binary) || I.dst != v.out_reg[0] || I.a >= EW_MAX_REGS || (binary && I.b >= EW_MAX_REGS)) return false;
+  const int round = I.round == 0 ? DT_F32 : I.round;
+  if ((round != DT_F32 && round != DT_BF16) || v.out_dtype[0] != round || !(v.out_float_mask & 1)) return false;
+  if ((uintptr_t)v.out_ptr[0] % 16) return false;
+  if (v.total % (16 / es)) return false;
+  // the first operand comes from a leaf; the second (binary) from a leaf or a constant, either side
+  int sa = src[I.a], sb = binary ? src[I.b] : -3;
+  bool b_first = false;
+  if (binary && sa == -2 && sb >= 0) std::swap(sa, sb), b_first = true;
+  if (sa < 0 || (binary && sb == -1)) return false;
+  m->a = (const char*)v.leaves[sa].ptr + v.leaves[sa].offset * es;
+  m->out = v.out_ptr[0];
+  m->b = nullptr;
+  m->imm = 0;
+  m->b_kind = 0;
+  if (binary && sb >= 0) m->b = (const char*)v.leaves[sb].ptr + v.leaves[sb].offset * es, m->b_kind = 1;
+  if (binary && sb == -2) m->imm = imm[b_first ? I.a : I.b], m->b_kind = 2;
+  m->b_first = b_first;
+  m->op = I.op;
+  m->chunks = v.total / (16 / es);
+  return true;
+}
+
 // Registers a program touches (one past the highest register it reads or writes).
 constexpr int EW_SMALL_REGS = 4;
 static int program_regs(const EwProgram& p) {
@@ -272,7 +407,19 @@ void launch_elementwise(const EwProgram& p, hipStream_t stream, hipEvent_t done)
     for (int i = 0; streaming && i < v.n_leaves; ++i)
       streaming = v.leaves[i].vmode == EW_VEC_CONTIG && elem_size(v.leaves[i].dtype) == les;
     for (int i = 0; streaming && i < v.n_instr; ++i) streaming = !ew_is_heavy(v.instr[i].op);
-    if (streaming) {
+    MapArgs m;
+    if (map_args(v, &m)) {
+      int64_t bytes = v.total * (int64_t)(elem_size(v.leaves[0].dtype) * (m.b_kind == 1 ? 2 : 1) + elem_size(v.out_dtype[0]));
+      const bool nt = bytes >= ((int64_t)256 << 20);
+      const bool f32in = v.leaves[0].dtype == DT_F32, bf16out = v.out_dtype[0] == DT_BF16;
+      dim3 mgrid((unsigned)std::min<int64_t>((m.chunks + 255) / 256, (int64_t)1 << 20)), mblock(256);
+#define RYFT_MAP(ES, OB)                                                                            \
+  (nt ? launch_k(done, ew_map_kernel<ES, OB, true>, mgrid, mblock, 0, stream, m)                     \
+      : launch_k(done, ew_map_kernel<ES, OB, false>, mgrid, mblock, 0, stream, m))
+      if (f32in) { if (bf16out) RYFT_MAP(4, true); else RYFT_MAP(4, false); }
+      else { if (bf16out) RYFT_MAP(2, true); else RYFT_MAP(2, false); }
+#undef RYFT_MAP
+    } else if (streaming) {
       // a chunk per thread (the grid covers the iteration space up to 2^20 workgroups); non-temporal accesses when
       // the step streams more than the 256 MB last-level cache could keep for its consumer anyway
       const int64_t sblocks = grid_for(v.total / VEC, VNT);

@@ -366,3 +366,60 @@ def test_streaming_maps_by_element_size(gpu_client, dt, bt):
     outs, exe = run_pjrt(gpu_client, prog, ins)
     for o, w, name in zip(outs, oracle_outputs(prog, ins), ("convert-negate", "add")):
         check(o, w, 0.0, f"{dt} {name}")
+
+
+_MAP_SPECIALS = np.array([np.nan, -np.nan, np.inf, -np.inf, 0.0, -0.0, 1e-40, -3e-39, 3.0e38, -1.5, 2.5, 1.0],
+                         np.float32)
+
+
+def _map_input(seed, shape, dt):
+    x = (hd.normal(seed, shape) * 10).astype(np.float32).reshape(-1)
+    x[seed % 7::97][:len(_MAP_SPECIALS)] = _MAP_SPECIALS[:len(x[seed % 7::97])]
+    x = x.reshape(shape)
+    if dt == "bf16":
+        return configs.HostInput(hd.f32_to_bf16_bits(x), pjrt.BufferType.BF16, shape)
+    return configs.HostInput(x, pjrt.BufferType.F32, shape)
+
+
+def _same_bits(got_raw, want, name):
+    """Exactly the oracle's values: equal numbers with equal signs (zeros included), NaN where it has NaN."""
+    vals, dt = want
+    got = sh.from_raw(got_raw, dt)
+    nan = np.isnan(vals)
+    assert np.array_equal(np.isnan(got), nan), f"{name}: NaN positions differ"
+    ok = (got[~nan] == vals[~nan]) & (np.signbit(got[~nan]) == np.signbit(vals[~nan]))
+    assert np.all(ok), f"{name}: {np.count_nonzero(~ok)} elements differ"
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("form", ["leaves", "const_right", "const_left", "same_leaf"])
+@pytest.mark.parametrize("op", ["add", "subtract", "multiply", "divide", "maximum", "minimum"])
+def test_direct_binary_maps(gpu_client, dt, form, op):
+    """One binary operation over contiguous f32 / bf16 leaves (or a leaf and a splat constant on either side) runs the
+    direct map kernel: bit-exact against the oracle, NaN / infinity / signed-zero / subnormal inputs included."""
+    shape = (8, 1024)
+    T = _t(shape, dt)
+    const = f"    %c = stablehlo.constant dense<-2.500000e+00> : {T}\n"
+    lhs, rhs, args = {"leaves": ("%arg0", "%arg1", [T, T]), "const_right": ("%arg0", "%c", [T]),
+                      "const_left": ("%c", "%arg0", [T]), "same_leaf": ("%arg0", "%arg0", [T])}[form]
+    body = (const if "const" in form else "") + f"    %0 = stablehlo.{op} {lhs}, {rhs} : {T}\n    return %0 : {T}"
+    prog = _mod(args, [T], body)
+    ins = [_map_input(61 + i, shape, dt) for i in range(len(args))]
+    outs, _ = run_pjrt(gpu_client, prog, ins)
+    _same_bits(outs[0], oracle_outputs(prog, ins)[0], f"{dt} {form} {op}")
+
+
+@pytest.mark.parametrize("case", ["negate_f32", "abs_bf16", "negate_bf16", "convert_f32_bf16", "convert_bf16_f32"])
+def test_direct_unary_maps(gpu_client, case):
+    shape = (4, 2048)
+    F, B = _t(shape), _t(shape, "bf16")
+    if case.startswith("convert"):
+        src, dst = (F, B) if case == "convert_f32_bf16" else (B, F)
+        body = f"    %0 = stablehlo.convert %arg0 : ({src}) -> {dst}\n    return %0 : {dst}"
+        prog, ins = _mod([src], [dst], body), [_map_input(71, shape, "f32" if src == F else "bf16")]
+    else:
+        op, dt = case.split("_")
+        T = _t(shape, dt)
+        prog, ins = _mod([T], [T], f"    %0 = stablehlo.{op} %arg0 : {T}\n    return %0 : {T}"), [_map_input(72, shape, dt)]
+    outs, _ = run_pjrt(gpu_client, prog, ins)
+    _same_bits(outs[0], oracle_outputs(prog, ins)[0], case)
