@@ -763,24 +763,10 @@ __global__ void __launch_bounds__(VNT) rownorm_wave_kernel(const RowArgs A) {
   const RowNormArgs& N = A.norm;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t chunks = A.inner / 8;
-  if (N.w) {
-    const int64_t nbytes = A.inner * (N.w_dtype == DT_F32 ? 4 : 2);
-    for (int64_t b = threadIdx.x * 16; b < nbytes; b += VNT * 16)
-      *(u32x4v*)(wrow + b) = *(const u32x4v*)((const char*)N.w + b);
-  }
-  __syncthreads();
   constexpr int W = XB * 2;  // raw words per chunk
-  auto decode_x = [&](const uint32_t* w, float* v) {
-    if constexpr (XB == 4) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = __uint_as_float(w[e]);
-    } else {
-      decode8_f32(N.x_dtype, w, v);
-    }
-  };
-  for (int64_t o = (int64_t)blockIdx.x * (VNT / 64) + wave; o < A.rows; o += (int64_t)gridDim.x * (VNT / 64)) {
+  uint32_t xr[NCW][W];
+  auto fetch = [&](int64_t o) {
     const char* xrow = (const char*)N.x + o * A.inner * XB;
-    uint32_t xr[NCW][W];
 #pragma unroll
     for (int q = 0; q < NCW; ++q) {
       const int c = lane + 64 * q;
@@ -792,6 +778,26 @@ __global__ void __launch_bounds__(VNT) rownorm_wave_kernel(const RowArgs A) {
         }
       }
     }
+  };
+  // the first row's words are requested before the weight row is staged (and the barrier that follows it)
+  const int64_t first = (int64_t)blockIdx.x * (VNT / 64) + wave;
+  if (first < A.rows) fetch(first);
+  if (N.w) {
+    const int64_t nbytes = A.inner * (N.w_dtype == DT_F32 ? 4 : 2);
+    for (int64_t b = threadIdx.x * 16; b < nbytes; b += VNT * 16)
+      *(u32x4v*)(wrow + b) = *(const u32x4v*)((const char*)N.w + b);
+  }
+  __syncthreads();
+  auto decode_x = [&](const uint32_t* w, float* v) {
+    if constexpr (XB == 4) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = __uint_as_float(w[e]);
+    } else {
+      decode8_f32(N.x_dtype, w, v);
+    }
+  };
+  for (int64_t o = first; o < A.rows; o += (int64_t)gridDim.x * (VNT / 64)) {
+    if (o != first) fetch(o);
     float acc = 0.0f;
 #pragma unroll
     for (int q = 0; q < NCW; ++q)
