@@ -775,7 +775,7 @@ class Buffer(_Owned):
         size = self.api.call("PJRT_Buffer_ToHostBuffer", src=self.handle, dst=None).dst_size
         out = (C.c_uint8 * max(size, 1))()
         a = self.api.call("PJRT_Buffer_ToHostBuffer", src=self.handle, dst=C.cast(out, _vp), dst_size=size)
-        return Event(self.api, a.event, lambda: bytes(out)[:size])
+        return Event(self.api, a.event, lambda: C.string_at(out, size))
 
     def copy_raw_to_host(self, size: int, offset: int = 0) -> Event:
         """Buffer::copy_raw_to_host_buffer (buffers.rs:1318-1340): `size` bytes of the on-device bytes from `offset`;
@@ -792,14 +792,23 @@ class Buffer(_Owned):
     def to_numpy(self):
         """Copy to host and view as numpy (bf16 / f8 come back as raw uint16 / uint8 bits)."""
         import numpy as np
-        data = self.copy_to_host().await_()
         t = self.element_type()
         np_t = {BufferType.PRED: np.bool_, BufferType.S8: np.int8, BufferType.S16: np.int16, BufferType.S32: np.int32,
                 BufferType.S64: np.int64, BufferType.U8: np.uint8, BufferType.U16: np.uint16,
                 BufferType.U32: np.uint32, BufferType.U64: np.uint64, BufferType.F16: np.float16,
                 BufferType.F32: np.float32, BufferType.F64: np.float64, BufferType.BF16: np.uint16,
                 BufferType.F8E4M3FN: np.uint8, BufferType.F8E5M2: np.uint8}[t]
-        return np.frombuffer(data, dtype=np_t).reshape(self.dimensions())
+        # the device bytes land directly in the array (ToHostBuffer: size query, then the copy)
+        dims = self.dimensions()
+        size = self.api.call("PJRT_Buffer_ToHostBuffer", src=self.handle, dst=None).dst_size
+        out = np.empty(dims, dtype=np_t)
+        if out.nbytes != size:
+            raise PjrtError(ErrorCode.INTERNAL, f"buffer holds {size} bytes, its shape {out.nbytes}")
+        if size:
+            a = self.api.call("PJRT_Buffer_ToHostBuffer", src=self.handle, dst=C.c_void_p(out.ctypes.data),
+                              dst_size=size)
+            Event(self.api, a.event).await_()
+        return out
 
     def __del__(self):
         try:
@@ -1303,21 +1312,32 @@ class Client(_Owned):
             device = self.addressable_devices()[0]
         if memory is None:
             memory = device.default_memory()
-        raw = data.tobytes() if hasattr(data, "tobytes") else bytes(data)
         expected = int(BufferType(element_type).size)
         for d in dims:
             expected *= int(d)
-        if byte_strides is None and len(raw) != expected:
-            raise PjrtError(ErrorCode.INVALID_ARGUMENT, f"expected {expected} bytes of host data, got {len(raw)}")
-        src = C.create_string_buffer(raw, max(len(raw), 1))
+        # a C-contiguous array is handed over in place (the plugin copies the bytes before the call returns);
+        # anything else is copied into a contiguous block first
+        if hasattr(data, "ctypes") and hasattr(data, "flags") and data.flags["C_CONTIGUOUS"]:
+            keep, nbytes, ptr = data, int(data.nbytes), data.ctypes.data
+        else:
+            raw = data.tobytes() if hasattr(data, "tobytes") else bytes(data)
+            keep = C.create_string_buffer(raw, max(len(raw), 1))
+            nbytes, ptr = len(raw), C.addressof(keep)
+        if byte_strides is None and nbytes != expected:
+            raise PjrtError(ErrorCode.INVALID_ARGUMENT, f"expected {expected} bytes of host data, got {nbytes}")
+        if not nbytes:  # (no bytes are read, but the pointer must not be null)
+            keep = C.create_string_buffer(1)
+            ptr = C.addressof(keep)
+        src = C.c_void_p(ptr)
         dims_arr = (C.c_int64 * max(len(dims), 1))(*dims)
         kw = {}
         if byte_strides is not None:
             kw["byte_strides"] = (C.c_int64 * len(byte_strides))(*byte_strides)
             kw["num_byte_strides"] = len(byte_strides)
-        a = self.api.call("PJRT_Client_BufferFromHostBuffer", client=self.handle, data=C.cast(src, _vp),
+        a = self.api.call("PJRT_Client_BufferFromHostBuffer", client=self.handle, data=src,
                           type=int(element_type), dims=dims_arr, num_dims=len(dims), host_buffer_semantics=0,
                           device=None, memory=memory.handle, device_layout=None, **kw)
+        del keep
         if a.done_with_host_buffer:
             Event(self.api, a.done_with_host_buffer)  # dropped, as ryft-pjrt does
         return Buffer(self, a.buffer)
