@@ -85,46 +85,90 @@ __global__ void __launch_bounds__(256) gemm_generic_kernel(const GemmArgs G) {
 // ------------------------------------------------------------------------------------------------ dispatch
 // ------------------------------------------------------------------------------------------------ split-K
 // Sums the K ranges' partial accumulators in range order and applies the epilogue, with the same per-element
-// arithmetic (and operation order) as the MFMA kernels' epilogue passes. Each thread owns 4 consecutive columns.
-template <bool INT, bool DUAL>
+// arithmetic (and operation order) as the MFMA kernels' epilogue passes. Each thread owns 8 consecutive elements of
+// the result (N is a multiple of 16 on every split-K plan): S (the number of ranges, a template argument so that
+// every range's two 16-byte loads are in flight together) × 2 loads per accumulator set, then one vector store per
+// output.
+template <int DT>
+__device__ __forceinline__ void store_oct(void* out, int64_t e0, const uint32_t* v, bool is_float) {
+  constexpr int OS = out_size<DT>();
+  uint32_t w[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) w[e] = out_bits<DT>(v[e], is_float);
+  char* p = (char*)out + e0 * OS;
+  if constexpr (OS == 4) {
+    *(u32x4*)p = u32x4{w[0], w[1], w[2], w[3]};
+    *(u32x4*)(p + 16) = u32x4{w[4], w[5], w[6], w[7]};
+  } else if constexpr (OS == 2) {
+    *(u32x4*)p = u32x4{w[0] | w[1] << 16, w[2] | w[3] << 16, w[4] | w[5] << 16, w[6] | w[7] << 16};
+  } else {
+    *(uint2*)p = uint2{w[0] | w[1] << 8 | w[2] << 16 | w[3] << 24, w[4] | w[5] << 8 | w[6] << 16 | w[7] << 24};
+  }
+}
+
+__device__ __forceinline__ void store_oct_any(void* out, int64_t e0, int dt, const uint32_t* v, bool is_float) {
+  switch (dt) {
+    case DT_F32: return store_oct<DT_F32>(out, e0, v, is_float);
+    case DT_S32: return store_oct<DT_S32>(out, e0, v, is_float);
+    case DT_BF16: return store_oct<DT_BF16>(out, e0, v, is_float);
+    case DT_F16: return store_oct<DT_F16>(out, e0, v, is_float);
+    case DT_F8E4M3FN: return store_oct<DT_F8E4M3FN>(out, e0, v, is_float);
+    default:
+#pragma unroll
+      for (int e = 0; e < 8; ++e) store_bits(out, e0 + e, dt, v[e], is_float);
+  }
+}
+
+template <bool INT, bool DUAL, int S>
 __global__ void __launch_bounds__(256) splitk_reduce_kernel(const GemmArgs G) {
-  const int64_t quads = (int64_t)G.batch * G.M * G.N / 4;
+  const int64_t octs = (int64_t)G.batch * G.M * G.N / 8;
   const int64_t slice = (int64_t)G.batch * G.M * G.N;  // elements of one accumulator set
-  const int nb = DUAL ? 2 : 1;
-  for (int64_t qd = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; qd < quads; qd += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t e0 = qd * 4;
+  constexpr int NB = DUAL ? 2 : 1;
+  auto add = [](uint32_t a, uint32_t x) {
+    return INT ? (uint32_t)((int32_t)a + (int32_t)x) : __float_as_uint(__uint_as_float(a) + __uint_as_float(x));
+  };
+  for (int64_t oc = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; oc < octs; oc += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t e0 = oc * 8;
     const int n = (int)(e0 % G.N);
     const int64_t bm = e0 / G.N;
     const int m = (int)(bm % G.M), b = (int)(bm / G.M);
-    uint32_t v[4], v2[4];
-    {
-      const u32x4 w = *(const u32x4*)((const uint32_t*)G.ws + e0);
-      v[0] = w.x, v[1] = w.y, v[2] = w.z, v[3] = w.w;
-      if (DUAL) {
-        const u32x4 w2 = *(const u32x4*)((const uint32_t*)G.ws + slice + e0);
-        v2[0] = w2.x, v2[1] = w2.y, v2[2] = w2.z, v2[3] = w2.w;
-      }
-    }
-    for (int s = 1; s < G.splits; ++s) {
-      const u32x4 w = *(const u32x4*)((const uint32_t*)G.ws + (int64_t)s * nb * slice + e0);
-      const uint32_t x[4] = {w.x, w.y, w.z, w.w};
+    u32x4 w[S][NB][2];
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        v[e] = INT ? (uint32_t)((int32_t)v[e] + (int32_t)x[e]) : __float_as_uint(__uint_as_float(v[e]) + __uint_as_float(x[e]));
-      if (DUAL) {
-        const u32x4 w2 = *(const u32x4*)((const uint32_t*)G.ws + ((int64_t)s * nb + 1) * slice + e0);
-        const uint32_t x2[4] = {w2.x, w2.y, w2.z, w2.w};
+    for (int s = 0; s < S; ++s)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v2[e] = __float_as_uint(__uint_as_float(v2[e]) + __uint_as_float(x2[e]));
+      for (int k = 0; k < NB; ++k) {
+        const u32x4* p = (const u32x4*)((const uint32_t*)G.ws + ((int64_t)s * NB + k) * slice + e0);
+        w[s][k][0] = p[0];
+        w[s][k][1] = p[1];
       }
+    uint32_t v[8], v2[8];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      v[4 * h] = w[0][0][h].x, v[4 * h + 1] = w[0][0][h].y, v[4 * h + 2] = w[0][0][h].z, v[4 * h + 3] = w[0][0][h].w;
+      if constexpr (DUAL)
+        v2[4 * h] = w[0][1][h].x, v2[4 * h + 1] = w[0][1][h].y, v2[4 * h + 2] = w[0][1][h].z,
+        v2[4 * h + 3] = w[0][1][h].w;
     }
-    uint32_t raw[4] = {v[0], v[1], v[2], v[3]};
+#pragma unroll
+    for (int s = 1; s < S; ++s)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        v[4 * h] = add(v[4 * h], w[s][0][h].x), v[4 * h + 1] = add(v[4 * h + 1], w[s][0][h].y);
+        v[4 * h + 2] = add(v[4 * h + 2], w[s][0][h].z), v[4 * h + 3] = add(v[4 * h + 3], w[s][0][h].w);
+        if constexpr (DUAL) {
+          v2[4 * h] = add(v2[4 * h], w[s][1][h].x), v2[4 * h + 1] = add(v2[4 * h + 1], w[s][1][h].y);
+          v2[4 * h + 2] = add(v2[4 * h + 2], w[s][1][h].z), v2[4 * h + 3] = add(v2[4 * h + 3], w[s][1][h].w);
+        }
+      }
+    uint32_t raw[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) raw[e] = v[e];
     bool is_float = !INT;
     if (G.epilogue == EPI_SCALE) {
       float rs = G.alpha;
       if (G.row) rs *= G.row[(int64_t)b * G.row_sb + (int64_t)m * G.row_sm];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
+      for (int e = 0; e < 8; ++e) {
         const float cs = G.col ? G.col[(int64_t)b * G.col_sb + (int64_t)(n + e) * G.col_sn] : 1.0f;
         float x = INT ? (float)(int32_t)v[e] : __uint_as_float(v[e]);
         x = x * rs * cs;
@@ -134,7 +178,7 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const GemmArgs G) {
       is_float = true;
     } else if (DUAL && G.epilogue == EPI_SWIGLU) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
+      for (int e = 0; e < 8; ++e) {
         const float c1 = G.col ? G.col[(int64_t)b * G.col_sb + (int64_t)(n + e) * G.col_sn] : 1.0f;
         const float c2 = G.col2 ? G.col2[(int64_t)b * G.col2_sb + (int64_t)(n + e) * G.col2_sn] : 1.0f;
         const float a = __uint_as_float(v[e]) * c1;
@@ -146,12 +190,21 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const GemmArgs G) {
       }
       is_float = true;
     }
-    const int64_t o = e0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) store_bits(G.out_ptr[0], o + e, G.out_dtype[0], v[e], is_float);
-    if (G.epilogue == EPI_SCALE && G.raw_out)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) store_bits(G.out_ptr[1], o + e, G.out_dtype[1], raw[e], !INT);
+    store_oct_any(G.out_ptr[0], e0, G.out_dtype[0], v, is_float);
+    if (G.epilogue == EPI_SCALE && G.raw_out) store_oct_any(G.out_ptr[1], e0, G.out_dtype[1], raw, !INT);
+  }
+}
+
+template <bool INT, bool DUAL>
+static void launch_splitk_reduce(const GemmArgs& g, hipStream_t stream, hipEvent_t done) {
+  const int64_t octs = (int64_t)g.batch * g.M * g.N / 8;
+  const dim3 grid((unsigned)std::min<int64_t>((octs + 255) / 256, 256 * 16)), block(256);
+  switch (g.splits) {
+    case 2: return launch_k(done, splitk_reduce_kernel<INT, DUAL, 2>, grid, block, 0, stream, g);
+    case 4: return launch_k(done, splitk_reduce_kernel<INT, DUAL, 4>, grid, block, 0, stream, g);
+    case 8: return launch_k(done, splitk_reduce_kernel<INT, DUAL, 8>, grid, block, 0, stream, g);
+    case 16: return launch_k(done, splitk_reduce_kernel<INT, DUAL, 16>, grid, block, 0, stream, g);
+    default: fail(PJRT_Error_Code_INTERNAL, "split-K over " + std::to_string(g.splits) + " ranges");
   }
 }
 
@@ -278,11 +331,10 @@ void launch_gemm(const GemmArgs& g, hipStream_t stream, hipEvent_t done) {
                                                 stream, start, main_done, 0)
                            : hipLaunchKernel(c.fn, dim3((unsigned)blocks), dim3(c.threads), args, (size_t)c.lds, stream);
     if (e == hipSuccess && splits > 1) {
-      const int64_t quads = (int64_t)g.batch * g.M * g.N / 4;
-      const unsigned rb = (unsigned)std::min<int64_t>((quads + 255) / 256, 256 * 16);
-      if (g.acc_is_int) launch_k(done, splitk_reduce_kernel<true, false>, dim3(rb), dim3(256), 0, stream, g);
-      else if (g.dual) launch_k(done, splitk_reduce_kernel<false, true>, dim3(rb), dim3(256), 0, stream, g);
-      else launch_k(done, splitk_reduce_kernel<false, false>, dim3(rb), dim3(256), 0, stream, g);
+      if (g.N % 16) fail(PJRT_Error_Code_INTERNAL, "split-K reduction needs N to be a multiple of 16");
+      if (g.acc_is_int) launch_splitk_reduce<true, false>(g, stream, done);
+      else if (g.dual) launch_splitk_reduce<false, true>(g, stream, done);
+      else launch_splitk_reduce<false, false>(g, stream, done);
       e = hipGetLastError();
     }
   } else {
