@@ -732,7 +732,9 @@ __device__ __forceinline__ float rownorm_scale(const RowArgs& A, float acc) {
 }
 
 // y = round(x·s·w) for 8 elements, stored as the output type; uniform branches once per vector of 8, straight-line
-// element work inside each.
+// element work inside each. NAN_FREE: the caller has shown that no y is a NaN, so an f8E4M3FN output needs no NaN
+// sign repair after the hardware conversion.
+template <bool NAN_FREE = false>
 __device__ __forceinline__ void rownorm_emit(const RowNormArgs& N, int64_t lin, const float* v, const float* wv, float s,
                                              int out_dtype) {
 #pragma clang fp contract(off)
@@ -744,6 +746,15 @@ __device__ __forceinline__ void rownorm_emit(const RowNormArgs& N, int64_t lin, 
     for (int e = 0; e < 8; ++e) y[e] = y[e] * wv[e];
   }
   round8(y, N.mid_round);
+  if (NAN_FREE && out_dtype == DT_F8E4M3FN) {
+    // v_cvt_pk_fp8_f32 gives the f8E4M3FN bits of every non-NaN input
+    uint32_t w0 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
+    w0 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], (int)w0, true);
+    uint32_t w1 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y[4], y[5], 0, false);
+    w1 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y[6], y[7], (int)w1, true);
+    vstore<false>((char*)N.out + lin, u32x2v{w0, w1});
+    return;
+  }
   uint32_t b[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) b[e] = __float_as_uint(y[e]);
@@ -830,6 +841,114 @@ __global__ void __launch_bounds__(VNT) rownorm_wave_kernel(const RowArgs A) {
       case DT_F8E4M3FN: emit_all(std::integral_constant<int, DT_F8E4M3FN>{}); break;
       default: emit_all(std::integral_constant<int, DT_F8E5M2>{}); break;
     }
+  }
+}
+
+// RMSNorm of many bf16 rows (bf16 weights, or none: W) of at most 64·8·NCW elements, a wavefront per row like
+// rownorm_wave_kernel, for grids that give each wavefront several rows: its lanes' weight chunks are loaded once and
+// kept in registers (raw words; no LDS staging and no barrier), and a wavefront moves on to its next row without
+// waiting for the others. The square of a bf16 value is exact in f32, so Σx² folds with FMAs (one rounding each, the
+// same as the separate multiply and add) in the same order, and the output bits equal rownorm_wave_kernel's. The
+// output type is chosen once, outside the row loop.
+template <int NCW, bool W, int ODT>
+__device__ __forceinline__ void rownorm_rows(const RowArgs& A) {
+#pragma clang fp contract(off)
+  const RowNormArgs& N = A.norm;
+  const int lane = threadIdx.x & 63;
+  const int64_t chunks = A.inner / 8;
+  const int64_t stride = (int64_t)gridDim.x * (VNT / 64);
+  int64_t o = (int64_t)blockIdx.x * (VNT / 64) + (threadIdx.x >> 6);
+  if (o >= A.rows) return;
+  uint32_t x[NCW][4], w[W ? NCW : 1][4];  // raw bf16 inputs and weights
+  auto fetch = [&](int64_t r) __attribute__((always_inline)) {
+    const char* xrow = (const char*)N.x + r * A.inner * 2;
+#pragma unroll
+    for (int q = 0; q < NCW; ++q) {
+      const int c = lane + 64 * q;
+      if (c < chunks) {
+        const u32x4v a = *(const u32x4v*)(xrow + (int64_t)c * 16);
+        x[q][0] = a.x, x[q][1] = a.y, x[q][2] = a.z, x[q][3] = a.w;
+      }
+    }
+  };
+  fetch(o);
+  if constexpr (W) {
+#pragma unroll
+    for (int q = 0; q < NCW; ++q) {
+      const int c = lane + 64 * q;
+      if (c < chunks) {
+        const u32x4v a = *(const u32x4v*)((const char*)N.w + (int64_t)c * 16);
+        w[q][0] = a.x, w[q][1] = a.y, w[q][2] = a.z, w[q][3] = a.w;
+      }
+    }
+  }
+  // f8E4M3FN output: whether every weight is finite (bf16 exponent field not all ones), once per wavefront
+  bool w_finite = true;
+  if constexpr (W && ODT == DT_F8E4M3FN) {
+    bool ok = true;
+#pragma unroll
+    for (int q = 0; q < NCW; ++q)
+      if (lane + 64 * q < chunks)
+#pragma unroll
+        for (int h = 0; h < 4; ++h)
+          ok = ok && (w[q][h] & 0x7f80u) != 0x7f80u && (w[q][h] & 0x7f800000u) != 0x7f800000u;
+    w_finite = __all(ok);
+  }
+  for (;;) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NCW; ++q)
+      if (lane + 64 * q < chunks) {
+        float v[8];
+        decode8_f32(DT_BF16, x[q], v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(v[e], v[e], acc);
+      }
+    for (int off = 32; off > 0; off >>= 1) acc = acc + __shfl_xor(acc, off, 64);
+    acc = __shfl(acc, 0, 64);
+    const float sc = rownorm_scale(A, acc);
+    auto emit_row = [&](auto nan_free) __attribute__((always_inline)) {
+#pragma unroll
+      for (int q = 0; q < NCW; ++q) {
+        const int c = lane + 64 * q;
+        if (c < chunks) {
+          // decoded here from raw words the compiler cannot see through, rather than kept decoded from the Σx²
+          // pass (x) or from before the row loop (w): that would hold 16·NCW more registers per lane
+          uint32_t xw[4] = {x[q][0], x[q][1], x[q][2], x[q][3]};
+          __asm__ __volatile__("" : "+v"(xw[0]), "+v"(xw[1]), "+v"(xw[2]), "+v"(xw[3]));
+          float v[8], wv[8];
+          decode8_f32(DT_BF16, xw, v);
+          if constexpr (W) {
+            uint32_t ww[4] = {w[q][0], w[q][1], w[q][2], w[q][3]};
+            __asm__ __volatile__("" : "+v"(ww[0]), "+v"(ww[1]), "+v"(ww[2]), "+v"(ww[3]));
+            decode8_f32(DT_BF16, ww, wv);
+          }
+          rownorm_emit<decltype(nan_free)::value>(N, o * A.inner + (int64_t)c * 8, v, wv, sc, ODT);
+        }
+      }
+    };
+    // No y = round(x·s·w) is a NaN when Σx² and s are finite (so is every x, and |x·s| ≤ √Σx²·s), √Σx²·s stays
+    // far below the f32 overflow threshold (x·s finite) and every weight is finite: (x·s)·w is then finite or
+    // infinite, and so is its rounding. Such rows skip the NaN sign repair of the f8E4M3FN conversion.
+    if (ODT == DT_F8E4M3FN && w_finite && __builtin_isfinite(acc) && __builtin_isfinite(sc) &&
+        sqrtf(acc) * sc < 1e37f)
+      emit_row(std::true_type{});
+    else
+      emit_row(std::false_type{});
+    o += stride;
+    if (o >= A.rows) break;
+    fetch(o);
+  }
+}
+
+template <int NCW, bool W>
+__global__ void __launch_bounds__(VNT) rownorm_rows_kernel(const RowArgs A) {
+  switch (A.norm.out_dtype) {
+    case DT_F32: return rownorm_rows<NCW, W, DT_F32>(A);
+    case DT_BF16: return rownorm_rows<NCW, W, DT_BF16>(A);
+    case DT_F16: return rownorm_rows<NCW, W, DT_F16>(A);
+    case DT_F8E4M3FN: return rownorm_rows<NCW, W, DT_F8E4M3FN>(A);
+    default: return rownorm_rows<NCW, W, DT_F8E5M2>(A);
   }
 }
 
@@ -939,13 +1058,30 @@ void launch_row(const RowArgs& a, hipStream_t stream, hipEvent_t done) {
   if (a.fast == ROW_FAST_NORM && rownorm_launchable(a)) {
     const int64_t chunks = a.inner / 8;
     const dim3 block(VNT);
-    if (row_per_wave(a.rows, a.inner)) {
+    const int ncw = (int)((chunks + 63) / 64);
+    if (row_per_wave(a.rows, a.inner) && a.norm.x_dtype == DT_BF16 && (!a.norm.w || a.norm.w_dtype == DT_BF16) &&
+        ncw <= 8) {
+      // a wavefront per row, the weights in registers; as many workgroups as the compute units hold at once (each
+      // wavefront then takes every stride-th row), or fewer when there are fewer rows
+      auto go = [&](auto kernel) {
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, VNT, 0) != hipSuccess || per_cu < 1)
+          per_cu = 1;
+        int64_t blocks = (a.rows + 3) / 4;
+        if (blocks > 256 * (int64_t)per_cu) blocks = 256 * (int64_t)per_cu;
+        launch_k(done, kernel, dim3((unsigned)blocks), block, 0, stream, a);
+      };
+      const bool w = a.norm.w != nullptr;
+      if (ncw <= 1) w ? go(rownorm_rows_kernel<1, true>) : go(rownorm_rows_kernel<1, false>);
+      else if (ncw <= 2) w ? go(rownorm_rows_kernel<2, true>) : go(rownorm_rows_kernel<2, false>);
+      else if (ncw <= 4) w ? go(rownorm_rows_kernel<4, true>) : go(rownorm_rows_kernel<4, false>);
+      else w ? go(rownorm_rows_kernel<8, true>) : go(rownorm_rows_kernel<8, false>);
+    } else if (row_per_wave(a.rows, a.inner)) {
       // a wavefront per row, four rows per workgroup, the weight row in dynamic LDS
       int64_t blocks = (a.rows + 3) / 4;
       if (blocks > 256 * 64) blocks = 256 * 64;
       const dim3 grid((unsigned)blocks);
       const uint32_t lds = a.norm.w ? (uint32_t)(a.inner * (a.norm.w_dtype == DT_F32 ? 4 : 2)) : 0u;
-      const int ncw = (int)((chunks + 63) / 64);
       auto go = [&](auto kernel) { launch_k(done, kernel, grid, block, lds, stream, a); };
       if (a.norm.x_dtype == DT_F32) {
         if (ncw <= 1) go(rownorm_wave_kernel<1, 4>);

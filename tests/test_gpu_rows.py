@@ -10,6 +10,7 @@ import pytest
 
 from ryft_amd import configs, hostdata as hd, pjrt
 from tests import row_programs
+from oracle import stablehlo as sh
 from tests.helpers import check, oracle_outputs, run_pjrt
 
 pytestmark = pytest.mark.gpu
@@ -51,13 +52,17 @@ def test_rmsnorm(gpu_client, shape, dt):
                                             ((8, 256), "bf16", None), ((2, 3, 4096), "bf16", "f8E4M3FN"),
                                             ((4, 8192), "f32", None), ((3, 16400), "bf16", None),
                                             ((2048, 4096), "bf16", "f8E4M3FN"), ((2048, 4096), "f32", None),
-                                            ((2048, 8192), "f32", None), ((2049, 1016), "f32", None)])
+                                            ((2048, 8192), "f32", None), ((2049, 1016), "f32", None),
+                                            ((6000, 2048), "bf16", None), ((16384, 4096), "bf16", "f8E4M3FN"),
+                                            ((8192, 520), "bf16", "f8E4M3FN")])
 def test_rmsnorm_fast_path_matches_interpreter(gpu_client, interp_client, shape, dt, quant):
     # the row-norm kernels and the interpreted row kernel fold in the same order: identical bits, and both match the
     # oracle. C5's normalise-and-quantise step at its full size is the first case. With few rows a workgroup takes a
     # row: rows of ≤ 2048, ≤ 4096, ≤ 8192 and longer elements cover the one-, two-, four-chunk register-resident and
     # the re-reading variants. Short rows, and rows of ≤ 8192 elements when there are ≥ 2048 of them, take a
-    # wavefront each (8 and 16 chunks per lane, 16- and 32-bit inputs, a ragged last chunk column).
+    # wavefront each (8 and 16 chunks per lane, 16- and 32-bit inputs, a ragged last chunk column); with 16-bit
+    # inputs and more rows than the chip holds wavefronts, a wavefront takes several rows (the last three cases: a
+    # ragged number of rows per wavefront, the calibration workload's shape, a ragged last chunk column).
     d = shape[-1]
     mk = _f32 if dt == "f32" else _bf16
     ins = [mk(51, shape), mk(52, (d,), 1.0, 0.02)]
@@ -70,6 +75,42 @@ def test_rmsnorm_fast_path_matches_interpreter(gpu_client, interp_client, shape,
     want = oracle_outputs(prog, ins)[0]
     # f8 outputs: one quantisation step (2^-3 relative) where the f32 sums round differently, so a looser bound
     check(fast[0], want, 1e-5 if dt == "f32" else (3e-2 if quant else 1e-2), f"rmsnorm{shape}")
+
+
+@pytest.mark.parametrize("weights", ["finite", "special"])
+def test_rmsnorm_f8_rows_with_special_values(gpu_client, interp_client, weights):
+    # many bf16 rows (a wavefront takes several): rows holding +NaN, -NaN, ±inf, an all-zero row (s = rsqrt(eps)),
+    # a row whose x·s overflows f32, and ordinary rows; the f8E4M3FN conversion must keep each NaN's sign wherever a
+    # NaN arises. With "special" weights (a +NaN, a -NaN and an inf column) every row takes the NaN sign repair.
+    m, d = 4096, 4096
+    rng = np.random.default_rng(61)
+    x = hd.f32_to_bf16_bits(rng.standard_normal((m, d)).astype(np.float32))
+    w = hd.f32_to_bf16_bits(rng.normal(1.0, 0.02, d).astype(np.float32))
+    x[7, 5], x[9, 100], x[11, 3], x[13, 4000] = 0x7FC0, 0xFFC0, 0x7F80, 0xFF80
+    x[15] = 0
+    x[17, :] = 0
+    x[17, 0] = 0x7F7F  # the largest finite bf16: its square overflows f32, so s = 0
+    x[19, :] = 0x0001  # the smallest bf16 subnormal in every column: Σx² is tiny, s = rsqrt(eps)
+    if weights == "special":
+        w[1], w[2], w[3] = 0x7FC0, 0xFFC0, 0x7F80
+    ins = [configs.HostInput(x, pjrt.BufferType.BF16, (m, d)), configs.HostInput(w, pjrt.BufferType.BF16, (d,))]
+    prog = row_programs.rmsnorm((m, d), "bf16", quant="f8E4M3FN")
+    fast, exe = run_pjrt(gpu_client, prog, ins)
+    assert exe.describe_plan().split()[1] == "row_norm"
+    slow, _ = run_pjrt(interp_client, prog, ins)
+    assert np.array_equal(fast[0], slow[0]), f"{np.count_nonzero(fast[0] != slow[0])} differing elements"
+    # NaN bytes (0x7f / 0xff) where the oracle has NaNs; the sign each NaN keeps is the interpreter's (above)
+    vals, dt = oracle_outputs(prog, ins)[0]
+    assert np.array_equal((fast[0] & 0x7F) == 0x7F, np.isnan(vals))
+    if weights == "finite":
+        # elementwise: at most one f8E4M3FN step apart (where the f32 sums round differently from the oracle's),
+        # and rarely so
+        rows = [r for r in range(m) if r not in (7, 9, 11, 13)]
+        got, want = sh.from_raw(fast[0][rows], dt), vals[rows]
+        with np.errstate(divide="ignore"):
+            step = np.maximum(2.0 ** (np.floor(np.log2(np.abs(want))) - 3), 2.0 ** -9)
+        assert np.all(np.abs(got - want) <= step)
+        assert np.count_nonzero(got != want) < 1e-3 * got.size
 
 
 @pytest.mark.parametrize("shape", [(4, 8, 200), (6, 2048), (5, 37)])
