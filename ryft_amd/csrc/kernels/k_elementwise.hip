@@ -1027,6 +1027,19 @@ static bool row_per_wave(int64_t rows, int64_t inner) {
   return inner / VEC < VNT || (inner / VEC <= ROW_WAVE_CHUNKS && rows >= ROW_WAVE_MIN_ROWS);
 }
 
+// Workgroups of rownorm_rows_kernel<NCW, W> one compute unit holds at once (asked of the runtime once per
+// instantiation; gfx950 only, so one answer serves every device).
+template <int NCW, bool W>
+static int rownorm_rows_per_cu() {
+  static const int n = [] {
+    int v = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, rownorm_rows_kernel<NCW, W>, VNT, 0) != hipSuccess || v < 1)
+      v = 1;
+    return v;
+  }();
+  return n;
+}
+
 static bool rownorm_launchable(const RowArgs& a) {
   const RowNormArgs& n = a.norm;
   auto float_ok = [](int dt) { return dt == DT_F32 || dt == DT_BF16 || dt == DT_F16; };
@@ -1063,19 +1076,22 @@ void launch_row(const RowArgs& a, hipStream_t stream, hipEvent_t done) {
         ncw <= 8) {
       // a wavefront per row, the weights in registers; as many workgroups as the compute units hold at once (each
       // wavefront then takes every stride-th row), or fewer when there are fewer rows
-      auto go = [&](auto kernel) {
-        int per_cu = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, VNT, 0) != hipSuccess || per_cu < 1)
-          per_cu = 1;
+      auto go = [&](auto ncw_c, auto w_c) {
+        constexpr int K = decltype(ncw_c)::value;
+        constexpr bool W = decltype(w_c)::value;
+        const int64_t per_cu = rownorm_rows_per_cu<K, W>();
         int64_t blocks = (a.rows + 3) / 4;
-        if (blocks > 256 * (int64_t)per_cu) blocks = 256 * (int64_t)per_cu;
-        launch_k(done, kernel, dim3((unsigned)blocks), block, 0, stream, a);
+        if (blocks > 256 * per_cu) blocks = 256 * per_cu;
+        launch_k(done, rownorm_rows_kernel<K, W>, dim3((unsigned)blocks), block, 0, stream, a);
       };
-      const bool w = a.norm.w != nullptr;
-      if (ncw <= 1) w ? go(rownorm_rows_kernel<1, true>) : go(rownorm_rows_kernel<1, false>);
-      else if (ncw <= 2) w ? go(rownorm_rows_kernel<2, true>) : go(rownorm_rows_kernel<2, false>);
-      else if (ncw <= 4) w ? go(rownorm_rows_kernel<4, true>) : go(rownorm_rows_kernel<4, false>);
-      else w ? go(rownorm_rows_kernel<8, true>) : go(rownorm_rows_kernel<8, false>);
+      auto go_w = [&](auto ncw_c) {
+        if (a.norm.w) go(ncw_c, std::true_type{});
+        else go(ncw_c, std::false_type{});
+      };
+      if (ncw <= 1) go_w(std::integral_constant<int, 1>{});
+      else if (ncw <= 2) go_w(std::integral_constant<int, 2>{});
+      else if (ncw <= 4) go_w(std::integral_constant<int, 4>{});
+      else go_w(std::integral_constant<int, 8>{});
     } else if (row_per_wave(a.rows, a.inner)) {
       // a wavefront per row, four rows per workgroup, the weight row in dynamic LDS
       int64_t blocks = (a.rows + 3) / 4;

@@ -320,8 +320,8 @@ void launch_gemm(const GemmArgs& g, hipStream_t stream, hipEvent_t done) {
       if (e != hipSuccess) fail(PJRT_Error_Code_INTERNAL, std::string("LDS attribute failed: ") + hipGetErrorString(e));
     }
     const int splits = g.splits > 1 ? g.splits : 1;
-    if (splits > 1 && (!g.ws || g.K % (splits * 16) || c.edge))
-      fail(PJRT_Error_Code_INTERNAL, "split-K without a workspace or on partial tiles");
+    if (splits > 1 && (!g.ws || g.K % (splits * 16) || g.N % 16 || c.edge))
+      fail(PJRT_Error_Code_INTERNAL, "split-K without a workspace, on partial tiles or with N not a multiple of 16");
     int64_t blocks = (int64_t)((g.M + c.bm - 1) / c.bm) * ((g.N + c.bn - 1) / c.bn) * g.batch * splits;
     if (blocks > INT32_MAX) fail(PJRT_Error_Code_UNIMPLEMENTED, "too many GEMM tiles");
     void* args[] = {(void*)&g};
@@ -331,7 +331,6 @@ void launch_gemm(const GemmArgs& g, hipStream_t stream, hipEvent_t done) {
                                                 stream, start, main_done, 0)
                            : hipLaunchKernel(c.fn, dim3((unsigned)blocks), dim3(c.threads), args, (size_t)c.lds, stream);
     if (e == hipSuccess && splits > 1) {
-      if (g.N % 16) fail(PJRT_Error_Code_INTERNAL, "split-K reduction needs N to be a multiple of 16");
       if (g.acc_is_int) launch_splitk_reduce<true, false>(g, stream, done);
       else if (g.dual) launch_splitk_reduce<false, true>(g, stream, done);
       else launch_splitk_reduce<false, false>(g, stream, done);
