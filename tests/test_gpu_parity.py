@@ -140,6 +140,15 @@ def test_c1_f32_full(gpu_client):
     _run_and_check(gpu_client, configs.c1_f32_dot())
 
 
+@pytest.mark.parametrize("kw", [dict(m=128, k=1024, n=128), dict(m=256, k=1024, n=128), dict(m=128, k=2048, n=192)])
+def test_f32_split_k_ranges(gpu_client, kw):
+    # split-K f32 GEMMs over 16 K ranges of 64 (the first two) and 128 (the last) elements, ragged N / M ratios
+    w = configs.c1_f32_dot(**kw)
+    exe = gpu_client.compile(pjrt.Program.mlir(w.program))
+    assert "_splitk" in exe.describe_plan()
+    _run_and_check(gpu_client, w)
+
+
 @pytest.mark.parametrize("kw", [dict(batch=2, m=128, k=128, n=128), dict(batch=1, m=64, k=96, n=80),
                                 dict(batch=3, m=256, k=512, n=256)])
 def test_c2_bf16_small(gpu_client, kw):
