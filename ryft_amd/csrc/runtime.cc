@@ -376,7 +376,12 @@ static void host_copy(void* dst, const void* src, size_t bytes) {
     const size_t off = i * piece;
     if (off >= bytes) break;
     const size_t n = std::min(piece, bytes - off);
-    pool.emplace_back([=] { memcpy((char*)dst + off, (const char*)src + off, n); });
+    try {
+      pool.emplace_back([=] { memcpy((char*)dst + off, (const char*)src + off, n); });
+    } catch (...) {  // no thread to be had: the calling thread copies the rest
+      memcpy((char*)dst + off, (const char*)src + off, bytes - off);
+      break;
+    }
   }
   memcpy(dst, src, std::min(piece, bytes));
   for (auto& th : pool) th.join();
