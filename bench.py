@@ -243,7 +243,7 @@ def main():
     names = ALL if args.config == "all" else [args.config]
     head = HEADLINE if args.config == "all" else args.config
     plugin = pjrt.load_plugin()
-    client = plugin.client()
+    client = plugin.client({"visible_devices": [0]})
     dev = client.addressable_devices()[0]
     cpu_s = 0.0 if args.no_cpu_baseline else args.cpu_seconds
     per = {}

@@ -141,6 +141,13 @@ extern "C" int RyftMi355x_ExecuteNoAlloc(PJRT_LoadedExecutable* executable, cons
         break;
     }
   }
+  // the caller's current device is put back on every return path
+  int prev = -1;
+  if (hipGetDevice(&prev) != hipSuccess) return report(PJRT_Error_Code_INTERNAL, "cannot read the current device");
+  struct RestoreDevice {
+    int dev;
+    ~RestoreDevice() { (void)hipSetDevice(dev); }
+  } restore{prev};
   try {
     std::lock_guard<std::recursive_mutex> lk(d->launch_mu);
     if (hipSetDevice(d->hip_ordinal) != hipSuccess)

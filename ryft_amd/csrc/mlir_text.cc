@@ -34,7 +34,7 @@ const std::unordered_map<std::string, Op>& mlir_simple_ops() {
       {"divide", Op::Divide},       {"maximum", Op::Maximum}, {"minimum", Op::Minimum},
       {"power", Op::Power},         {"remainder", Op::Remainder}, {"and", Op::And},
       {"or", Op::Or},               {"xor", Op::Xor},         {"select", Op::Select},
-      {"clamp", Op::Clamp},         {"reshape", Op::Reshape}, {"bitcast_convert", Op::Convert},
+      {"clamp", Op::Clamp},         {"reshape", Op::Reshape},
   };
   return m;
 }

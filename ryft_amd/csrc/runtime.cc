@@ -370,7 +370,8 @@ static void host_copy(void* dst, const void* src, size_t bytes) {
     memcpy(dst, src, bytes);
     return;
   }
-  const size_t piece = (bytes / nt + 4095) & ~(size_t)4095;
+  // pieces of ceil(bytes / nt) rounded up to a page: nt of them always cover the whole buffer
+  const size_t piece = ((bytes + nt - 1) / nt + 4095) & ~(size_t)4095;
   std::vector<std::thread> pool;
   for (size_t i = 1; i < nt; ++i) {
     const size_t off = i * piece;

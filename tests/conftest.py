@@ -27,5 +27,5 @@ def compile_client(plugin):
 
 @pytest.fixture(scope="session")
 def gpu_client(plugin):
-    c = plugin.client()
+    c = plugin.client({"visible_devices": [0]})
     yield c

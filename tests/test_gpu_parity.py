@@ -58,6 +58,25 @@ def test_buffer_round_trip(gpu_client, bt, np_t):
     assert b.copy_to_host().await_() == raw.tobytes()
 
 
+@pytest.mark.parametrize("n,bt,np_t", [((16 << 20) + 1, pjrt.BufferType.U8, np.uint8),
+                                       ((24 << 20) + 2, pjrt.BufferType.U8, np.uint8),
+                                       (10485761, pjrt.BufferType.F32, np.float32)])
+def test_buffer_round_trip_split_copies(gpu_client, n, bt, np_t):
+    # sizes whose host staging copy is split over 2, 3 and 5 threads with a remainder the page-rounded pieces must
+    # still cover; a stained staging block first, so stale bytes from an earlier transfer cannot pass for the data
+    print(f"[round trip] {n} x {np.dtype(np_t).name}", flush=True)
+    rng = np.random.default_rng(n)
+    stain = np.frombuffer(np.full(n * np.dtype(np_t).itemsize, 0x5A, np.uint8).tobytes(), dtype=np_t)
+    gpu_client.buffer(stain, bt, (n,)).to_numpy()
+    raw = rng.integers(0, 256, size=n * np.dtype(np_t).itemsize, dtype=np.uint8)
+    raw[-64:] = np.arange(1, 65, dtype=np.uint8)          # the tail carries no 0x5A byte
+    x = raw.view(np_t)
+    b = gpu_client.buffer(x, bt, (n,))
+    back = b.to_numpy()
+    assert np.array_equal(back.view(np.uint8), raw)
+    assert b.copy_to_host().await_() == raw.tobytes()
+
+
 def test_buffer_strided_upload(gpu_client):
     x = np.arange(12, dtype=np.float32).reshape(3, 4)
     xt = np.asfortranarray(x)
@@ -184,6 +203,27 @@ def test_c4_attention_small(gpu_client, kw):
     assert "attention_fwd" in exe.describe_plan()
 
 
+@pytest.mark.parametrize("kw", [
+    # batch·heads a multiple of 8: the workgroups of a head are grouped on one XCD (workgroup x → head slot x mod 8)
+    dict(b=1, h=8, s=256, d=128),                 # causal, one query-block pair per head
+    dict(b=4, h=2, s=384, d=128),                 # causal, 3 query blocks: a pair and a block alone
+    dict(b=2, h=8, s=640, d=64),                  # causal, 5 query blocks, 16 heads over two slot rounds
+    dict(b=1, h=8, s=256, d=128, mask=None),      # unmasked: one workgroup per query block
+    dict(b=1, h=16, s=128, d=128, mask=None, sk=192)])
+def test_c4_attention_heads_grouped_per_xcd(gpu_client, kw):
+    w = configs.c4_causal_attention(**kw)
+    outs, exe = run_pjrt(gpu_client, w.program, w.inputs)
+    assert "attention_fwd" in exe.describe_plan()
+    assert (kw["b"] * kw["h"]) % 8 == 0
+    (want, dt), = oracle_outputs(w.program, w.inputs)
+    got = sh.from_raw(outs[0], dt)
+    for bi in range(kw["b"]):
+        for hi in range(kw["h"]):
+            err = sh.rel_error(got[bi, hi], want[bi, hi])
+            assert err <= w.tolerance, f"head ({bi},{hi}): relative error {err:.3e}"
+    print(f"[parity] {w.name} {kw}: every head within {w.tolerance}", flush=True)
+
+
 def test_c4_attention_full_sampled(gpu_client):
     w = configs.c4_causal_attention()
     outs, exe = run_pjrt(gpu_client, w.program, w.inputs)
@@ -193,7 +233,11 @@ def test_c4_attention_full_sampled(gpu_client):
     v = sh.from_raw(w.inputs[2].data, "bf16")
     assert np.array_equal(got[:, :, 0, :], nm.round_to(v[:, :, 0, :], "bf16"))  # row 0 attends to key 0 only
     small = configs.c4_causal_attention(b=1, h=1, s=2048, d=128)
-    for (bi, hi) in [(0, 0), (3, 31), (2, 17)]:
+    # one head per residue of b·H + h modulo 8 (the head slot its workgroups take on the XCDs), plus the first and
+    # last heads
+    heads = [(0, 0), (0, 9), (0, 18), (0, 27), (1, 4), (1, 13), (2, 22), (3, 31), (3, 23)]
+    assert sorted({(b * 32 + h) % 8 for b, h in heads}) == list(range(8))
+    for (bi, hi) in heads:
         sub = [configs.HostInput(x.data[bi:bi + 1, hi:hi + 1].copy(), x.type, (1, 1, 2048, 128)) for x in w.inputs]
         (want, dt), = oracle_outputs(small.program, sub)
         err = sh.rel_error(got[bi:bi + 1, hi:hi + 1], want)

@@ -27,7 +27,7 @@ def _bf16(seed, shape, mean=0.0, std=1.0):
 @pytest.fixture(scope="module")
 def interp_client(plugin):
     """A client whose plans keep every row-fused step on the interpreted row kernel (no specialised kernels)."""
-    return plugin.client({"fast_paths": False})
+    return plugin.client({"fast_paths": False, "visible_devices": [0]})
 
 
 def _run(client, prog, ins, tol, name):

@@ -68,8 +68,14 @@ def test_no_alloc_rejects_what_it_cannot_run(plugin, gpu_client):
     w = configs.c4_causal_attention(b=1, h=4, s=2048, d=128, mask="GT")
     exe = gpu_client.compile(pjrt.Program.mlir(w.program))
     assert "attention_fwd" not in exe.describe_plan()
-    sizes = [int(np.prod(x.dims)) * 2 for x in w.inputs]
-    rc, msg = _call(plugin, exe, [0x1000] * 3, sizes, [0x1000], [sizes[0]])
+    # real, correctly sized buffers: should the plan ever fit the scratch, the call runs on valid memory and the
+    # wrong return code is what fails
+    ins = [gpu_client.uninitialized_buffer(x.type, x.dims) for x in w.inputs]
+    out = gpu_client.uninitialized_buffer(w.inputs[0].type, w.inputs[0].dims)
+    sizes = [b.on_device_size_in_bytes() for b in ins]
+    rc, msg = _call(plugin, exe, [b.unsafe_pointer() for b in ins], sizes, [out.unsafe_pointer()],
+                    [out.on_device_size_in_bytes()])
+    assert _hip().hipDeviceSynchronize() == 0
     assert rc == pjrt.ErrorCode.RESOURCE_EXHAUSTED and "scratch" in msg, (rc, msg)
     # a size that is not the program's, and a misaligned pointer: rejected before anything is launched
     w = configs.c2_bf16_batched_dot(batch=1, m=256, k=256, n=256)
