@@ -3,13 +3,15 @@
 // GEMM kernels for gfx950 (see also k_gemm_dispatch.hip).
 //
 // MFMA path: one workgroup computes a BM×BN tile of C[b] = A[b]·B[b]ᵀ (B addressed as [n, k]); WM×WN wavefronts
-// each own a (BM/WM)×(BN/WN) sub-tile made of 32×32 MFMA tiles. Operand tiles are staged through LDS in a
-// K-packed layout (each row holds BK consecutive k of one m or n) in two LDS stages, fed by buffer loads one k-tile
-// ahead (tile t+2 is requested while tile t multiplies); LDS fragments are double-buffered in registers across
-// k-steps and across the one barrier per k-tile. Operands whose contiguous dimension is m / n (row-major [K, N]
-// weights, for example) are transposed in registers with v_perm_b32 on their way into LDS, so no separate transpose
-// pass over HBM is needed. Workgroups are mapped onto the 8 XCDs so that the tiles one XCD computes
-// share A row-panels and B column-panels in that XCD's L2.
+// each own a (BM/WM)×(BN/WN) sub-tile made of 32×32 MFMA tiles. Full tiles of a K-contiguous A go from global memory
+// straight into LDS (buffer_load ... lds) in unpadded, XOR-swizzled K-packed rows (each row holds BK consecutive k of
+// one m), together with B — K-packed the same way, or, when its contiguous dimension is n (row-major [K, N] weights),
+// as unchanged [k][n] rows read back with transposing LDS reads — in two or three LDS stages, so no register staging
+// and no LDS store instructions are needed. Edge tiles and m-contiguous A operands take a register-staged path
+// instead: buffer loads one k-tile ahead into registers, padded LDS rows, m / n-contiguous operands transposed in
+// registers with v_perm_b32 on their way into LDS. Either way LDS fragments are double-buffered in registers across
+// k-steps and across the one barrier per k-tile, and no separate transpose pass over HBM is needed. Workgroups are
+// mapped onto the 8 XCDs so that the tiles one XCD computes share A row-panels and B column-panels in that XCD's L2.
 //
 // Instruction per compute type (all dense, f32 or i32 accumulation):
 //   bf16  v_mfma_f32_32x32x16_bf16      f16  v_mfma_f32_32x32x16_f16
@@ -331,7 +333,67 @@ __device__ __forceinline__ uint2 lds_read_tr8(const char* p) {
   return __builtin_bit_cast(uint2, v);
 }
 
-template <int KIND, int BM, int BN, int BK, int WM, int WN, bool A_R, bool B_R, bool DUAL>
+// ------------------------------------------------------------------------------------------------ LDS-DMA tiles
+// XOR swizzles of the DMA tile layouts: the 16-byte chunk c of tile row r sits at chunk position c ^ swz(r).
+// K-packed rows of 128 bytes (A, K-contiguous B): a fragment read takes one chunk of each of 16 consecutive rows per
+// 16 lanes (ds_read_b128); rows alternate between the two 128-byte halves of the 64 banks, so the 8 rows of a half
+// need 8 distinct positions. Period 16 rows.
+__device__ __forceinline__ int swz_k128(int r) { return (r >> 1) & 7; }
+// [k][n] rows read with transposing reads (32 lanes per pass): 16-bit rows (≥ 256 bytes): 4 consecutive rows × 4
+// consecutive chunks, so the 4 rows' chunk quads go to distinct quads (period 4); 8-bit rows of ≥ 256 bytes: 8 rows
+// × 2 chunks (period 8); 8-bit rows of 128 bytes: the even and the odd rows of 8 fall in different bank halves, 4 rows
+// × 2 chunks each (period 8).
+template <int ES, int RB>
+__device__ __forceinline__ int swz_tr(int r) {
+  if constexpr (ES == 2) return 4 * (r & 3);
+  else if constexpr (RB >= 256) return 2 * (r & 7);
+  else return 2 * ((r >> 1) & 3);
+}
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+// One wave-wide load of 16 bytes per lane from a buffer straight into LDS: lane l's bytes (buffer offset voff + soff)
+// land at lds + 16·l (lds and soff wave-uniform).
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, char* lds, int voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds, 16, voff, soff, 0, 0);
+}
+// LDS fragment reads as inline assembly: the compiler cannot tell the stage they read from the stages the DMA loads
+// are filling and would otherwise wait for every outstanding load before each read. Their completion is waited for
+// explicitly (lgkm_wait), with the fragments passed through the wait so that their uses follow it.
+template <int OFF>
+__device__ __forceinline__ u32x4 lds_rd128(uint32_t a) {
+  u32x4 r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(a), "i"(OFF));
+  return r;
+}
+template <int OFF>
+__device__ __forceinline__ u32x2v lds_rd_tr16(uint32_t a) {
+  u32x2v r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(a), "i"(OFF));
+  return r;
+}
+template <int OFF>
+__device__ __forceinline__ u32x2v lds_rd_tr8(uint32_t a) {
+  u32x2v r;
+  asm volatile("ds_read_b64_tr_b8 %0, %1 offset:%2" : "=v"(r) : "v"(a), "i"(OFF));
+  return r;
+}
+// Waits until at most N of this wave's LDS reads are outstanding.
+template <int N>
+__device__ __forceinline__ void lgkm_wait() {
+  asm volatile("s_waitcnt lgkmcnt(%[n])" ::[n] "n"(N));
+}
+// Orders the uses of a register after the preceding wait (volatile asm statements keep their order).
+template <class T>
+__device__ __forceinline__ void after_wait(T& r) {
+  asm volatile("" : "+v"(r));
+}
+// Waits for this wave's DMA loads down to N outstanding and for its LDS reads, then joins the workgroup barrier.
+template <int N>
+__device__ __forceinline__ void dma_barrier() {
+  asm volatile("s_waitcnt vmcnt(%[n]) lgkmcnt(0)\n\ts_barrier" ::[n] "n"(N) : "memory");
+}
+
+template <int KIND, int BM, int BN, int BK, int WM, int WN, bool A_R, bool B_R, bool DUAL, bool EDGE = false>
 struct MfmaCfg {
   using M = Mma<KIND>;
   static constexpr int ESIZE = M::ESIZE, KPACK = M::KPACK, MK = 2 * KPACK;
@@ -350,13 +412,26 @@ struct MfmaCfg {
   static constexpr int BLES = BTR ? BES : ESIZE;
   static constexpr int LDB = BN * BLES + (BLES == 2 ? 64 : 32);
   static constexpr int BREG = BTR ? BK * LDB : BN * LDK;  // bytes of one B operand tile
-  static constexpr int STAGE = BM * LDK + NB * BREG;
+  // DMA: full tiles of a K-contiguous A and a B that reaches LDS unchanged (n-contiguous 16- / 8-bit, or K-contiguous
+  // without widening) go from global memory straight into LDS (buffer_load ... lds, 16 bytes per lane): unpadded rows
+  // whose 16-byte chunks are XOR-swizzled per row (so that the fragment reads stay conflict-free), no register
+  // staging and no LDS stores; NST stages (three when they fit) keep the loads two k-tiles ahead.
+  static constexpr int RBA = BK * ESIZE;                       // bytes per A row (and per K-contiguous B row)
+  static constexpr int RBB = BTR ? BN * BLES : BK * ESIZE;     // bytes per B row ([k][n] rows when BTR)
+  static constexpr bool DMA = !EDGE && !A_R && ESIZE <= 2 && (BTR || BES == ESIZE) && RBA == 128 &&
+                              (BM * RBA) % (1024 * WM * WN) == 0 && (BTR ? BK : BN) * RBB % (1024 * WM * WN) == 0 &&
+                              (!BTR || RBB == 128 || RBB == 256 || RBB == 512);
+  static constexpr int BREG_D = BTR ? BK * RBB : BN * RBA;
+  static constexpr int STAGE_D = BM * RBA + NB * BREG_D;
+  // three stages when they fit the 160 KB of LDS and two stages would already leave room for one workgroup only
+  static constexpr int NST = DMA && 3 * STAGE_D <= 163840 && 2 * STAGE_D > 163840 / 2 ? 3 : 2;
+  static constexpr int STAGE = DMA ? STAGE_D : BM * LDK + NB * BREG;
   static_assert(BK % MK == 0, "BK must be a multiple of the MFMA K");
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32");
   // epilogue rounds: the largest number of 32-row tile-rows (dividing TM) whose f32 patches fit in the LDS the two
   // stages occupy (at least one round's worth)
   static constexpr int epi_bytes(int rows) { return WM * WN * NB * rows * 32 * (WTN + 4) * 4; }
-  static constexpr int LDS_BYTES = 2 * STAGE > epi_bytes(1) ? 2 * STAGE : epi_bytes(1);
+  static constexpr int LDS_BYTES = NST * STAGE > epi_bytes(1) ? NST * STAGE : epi_bytes(1);
   static constexpr int EPI_ROWS = (TM % 4 == 0 && epi_bytes(4) <= LDS_BYTES)   ? 4
                                   : (TM % 2 == 0 && epi_bytes(2) <= LDS_BYTES) ? 2
                                                                                : 1;
@@ -548,7 +623,7 @@ __device__ __forceinline__ void epi_round(const GemmArgs& G, int b, int m0, int 
 // 16-byte vector (the last k-tile loads zeros past K); no split-K.
 template <int KIND, int BM, int BN, int BK, int WM, int WN, bool A_R, bool B_R, bool DUAL, bool EDGE>
 __global__ void __launch_bounds__(64 * WM * WN) gemm_mfma_kernel(const GemmArgs G) {
-  using C = MfmaCfg<KIND, BM, BN, BK, WM, WN, A_R, B_R, DUAL>;
+  using C = MfmaCfg<KIND, BM, BN, BK, WM, WN, A_R, B_R, DUAL, EDGE>;
   using M = typename C::M;
   using Acc = typename M::Acc;
   using F = Frag<C::KPACK * C::ESIZE>;
@@ -584,14 +659,6 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_mfma_kernel(const GemmArgs 
   const char* Bb = (const char*)G.B.ptr + ((int64_t)b * G.B.sb + (int64_t)n0 * G.B.sr) * BES;
   const char* B2b = DUAL ? (const char*)G.B2.ptr + ((int64_t)b * G.B2.sb + (int64_t)n0 * G.B2.sr) * BES : nullptr;
 
-  // One register stage of global prefetch: tile kt + 2 is requested at the start of k-tile kt (right after tile
-  // kt + 1 went from registers to LDS), so each load has a whole k-tile of MFMA work to arrive in. Two LDS stages.
-  using BLoader = std::conditional_t<
-      C::BTR, TileCopyLoader<C::BLES, BN, BK, C::THREADS>,
-      std::conditional_t<BES != ES, TileWidenLoader<BN, BK, C::THREADS>, TileLoader<ES, BN, BK, C::THREADS, B_R>>>;
-  TileLoader<ES, BM, BK, C::THREADS, A_R> la;
-  BLoader lb;
-  BLoader lb2;
 
   Acc acc[C::TM][C::TN];
   Acc acc2[DUAL ? C::TM : 1][DUAL ? C::TN : 1];
@@ -606,170 +673,397 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_mfma_kernel(const GemmArgs 
   // k-tiles of this workgroup's K range
   const int KT = EDGE ? (G.K + BK - 1) / BK : (G.splits > 1 ? G.K / BK / G.splits : G.K / BK);
   const int kt0 = split * KT;
-  // edge kernels: the last byte of each operand (its loads are bounded to it), as an address
-  auto op_end = [&](const GemmOperand& o, int rows, int es) -> const char* {
-    return (const char*)o.ptr +
-           ((int64_t)(G.batch - 1) * o.sb + (int64_t)(rows - 1) * o.sr + (int64_t)(G.K - 1) * o.sk + 1) * es;
-  };
-  const char* const a_end = EDGE ? op_end(G.A, G.M, ES) : nullptr;
-  const char* const b_end = EDGE ? op_end(G.B, G.N, BES) : nullptr;
-  const char* const b2_end = EDGE && DUAL ? op_end(G.B2, G.N, BES) : nullptr;
-  auto bounds = [&](const char* p, const char* end, int kvalid) {
-    LoadBounds r;
-    r.nrec = (int)min((int64_t)(end - p), (int64_t)0x7fffffff);
-    r.kvalid = kvalid;
-    return r;
-  };
-  auto gload = [&](int kt) {
-    const int64_t ko = (int64_t)(kt0 + kt) * BK;
-    const char* pa = Ab + ko * G.A.sk * ES;
-    const char* pb = Bb + ko * G.B.sk * BES;
-    if constexpr (EDGE) {
-      const int kvalid = G.K - (int)ko;
-      la.template load<true>(pa, G.A.sr, G.A.sk, tid, bounds(pa, a_end, kvalid));
-      lb.template load<true>(pb, G.B.sr, G.B.sk, tid, bounds(pb, b_end, kvalid));
+  if constexpr (C::DMA) {
+    // ---- operand tiles straight from global memory into LDS (buffer_load ... lds), NST stages
+    constexpr int NW = WM * WN, NST = C::NST, RBA = C::RBA, RBB = C::RBB;
+    constexpr int UA = RBA / 16, R1A = 1024 / RBA, PA = BM * RBA / 1024 / NW;  // chunks / row, rows / piece, pieces
+    constexpr int BROWS = C::BTR ? BK : BN;
+    constexpr int UB = RBB / 16, R1B = 1024 / RBB, PB = BROWS * RBB / 1024 / NW;
+    constexpr int OPS = PA + C::NB * PB;  // DMA loads per wave per k-tile
+    constexpr int BREG = C::BREG_D;
+    static_assert((NW * R1A) % 16 == 0 && (NW * R1B) % (C::BTR ? 8 : 16) == 0, "piece rows must keep the swizzle");
+    static_assert(OPS <= 63, "vmcnt range");
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    // per-lane source offsets of piece 0 (pieces i of a wave are i·NW·R1 rows further: a scalar offset)
+    const int64_t a_rs = G.A.sr * ES;
+    const int ra = wave_u * R1A + lane / UA;
+    const int a_voff = (int)(ra * a_rs) + 16 * ((lane % UA) ^ swz_k128(ra));
+    const int a_pstep = (int)(NW * R1A * a_rs);
+    auto bsw = [&](int r) { if constexpr (C::BTR) return swz_tr<C::BLES, RBB>(r); else return swz_k128(r); };
+    const int rb = wave_u * R1B + lane / UB;
+    const int64_t b_rs = C::BTR ? G.B.sk * BES : G.B.sr * ES;
+    const int b_voff = (int)(rb * b_rs) + 16 * ((lane % UB) ^ bsw(rb));
+    const int b_pstep = (int)(NW * R1B * b_rs);
+    int b2_voff = 0, b2_pstep = 0;
+    if constexpr (DUAL) {
+      const int64_t b2_rs = C::BTR ? G.B2.sk * BES : G.B2.sr * ES;
+      b2_voff = (int)(rb * b2_rs) + 16 * ((lane % UB) ^ bsw(rb));
+      b2_pstep = (int)(NW * R1B * b2_rs);
+    }
+    auto dma = [&](int t, int st) {
+      const int64_t ko = (int64_t)(kt0 + t) * BK;
+      char* sb = smem + st * C::STAGE;
+      const __amdgpu_buffer_rsrc_t rsa =
+          __builtin_amdgcn_make_buffer_rsrc((void*)(Ab + ko * G.A.sk * ES), (short)0, -1, 0x00020000);
+      const __amdgpu_buffer_rsrc_t rsb =
+          __builtin_amdgcn_make_buffer_rsrc((void*)(Bb + ko * G.B.sk * BES), (short)0, -1, 0x00020000);
+#pragma unroll
+      for (int i = 0; i < PA; ++i) lds_dma16(rsa, sb + (wave_u + i * NW) * 1024, a_voff, i * a_pstep);
+#pragma unroll
+      for (int i = 0; i < PB; ++i) lds_dma16(rsb, sb + BM * RBA + (wave_u + i * NW) * 1024, b_voff, i * b_pstep);
       if constexpr (DUAL) {
-        const char* pb2 = B2b + ko * G.B2.sk * BES;
-        lb2.template load<true>(pb2, G.B2.sr, G.B2.sk, tid, bounds(pb2, b2_end, kvalid));
-      }
-    } else {
-      la.load(pa, G.A.sr, G.A.sk, tid);
-      lb.load(pb, G.B.sr, G.B.sk, tid);
-      if constexpr (DUAL) lb2.load(B2b + ko * G.B2.sk * BES, G.B2.sr, G.B2.sk, tid);
-    }
-  };
-  auto lstore = [&](int buf) {
-    char* s = smem + buf * C::STAGE;
-    la.template store<C::LDK>(s, tid);
-    constexpr int BP = C::BTR ? C::LDB : C::LDK;
-    lb.template store<BP>(s + BM * C::LDK, tid);
-    if constexpr (DUAL) lb2.template store<BP>(s + BM * C::LDK + C::BREG, tid);
-  };
-
-  // Fragments of MFMA k-step s live in register slot s & 1: step s + 1 is read from LDS while step s multiplies.
-  constexpr int S = BK / C::MK;
-  static_assert(S % 2 == 0, "k-steps per tile must be even (fragment slots alternate)");
-  // f8 B in LDS for the bf16 MFMA: B fragments are kept as the raw bytes of their transposing read and widened
-  // right before the MFMAs that use them, so their LDS reads stay in flight across the previous step's MFMAs
-  constexpr bool BWIDEN = C::BTR && C::BLES == 1 && ES == 2;
-  using BF = std::conditional_t<BWIDEN, u32x2w, typename F::T>;
-  typename F::T fa[2][C::TM];
-  BF fb[2][C::TN], fb2[2][DUAL ? C::TN : 1];
-  const int lrow = lane & 31;
-  const int lk = (lane >> 5) * C::KPACK * ES;  // byte offset of this lane's k-pack within an MFMA k-step
-  const int a_off = (wm * C::WTM + lrow) * C::LDK + lk;
-  // K-packed B: row n, k-pack of this lane. Transposed-read B: lane s of each 16-lane group addresses k-row
-  // 8·(lane/32) + s/4 and column 16·((lane/16) % 2) + 4·(s % 4), so the pair of reads (k-rows +0 and +4) delivers
-  // B[8·(lane/32) .. +7][lane % 32] — the MFMA operand fragment.
-  // (8-bit: lane s addresses k-row KPACK·(lane/32) + s/2 and column 16·((lane/16) % 2) + 8·(s % 2); each read
-  // delivers 8 consecutive k, KPACK / 8 reads make the fragment.)
-  const int b_off = !C::BTR ? BM * C::LDK + (wn * C::WTN + lrow) * C::LDK + lk
-                    : C::BLES == 2 ? BM * C::LDK + (8 * (lane >> 5) + ((lane & 15) >> 2)) * C::LDB +
-                                         (wn * C::WTN + 16 * ((lane >> 4) & 1) + 4 * (lane & 3)) * 2
-                                   : BM * C::LDK + (C::KPACK * (lane >> 5) + ((lane & 15) >> 1)) * C::LDB +
-                                         (wn * C::WTN + 16 * ((lane >> 4) & 1) + 8 * (lane & 1));
-  auto bfrag = [&](const char* p) -> BF {
-    if constexpr (!C::BTR) {
-      return F::load(p);
-    } else if constexpr (C::BLES == 2) {
-      const uint2 lo = lds_read_tr16(p), hi = lds_read_tr16(p + 4 * C::LDB);
-      return u32x4{lo.x, lo.y, hi.x, hi.y};
-    } else if constexpr (BWIDEN) {  // one transposing read gives the 8 k of the fragment
-      const uint2 a = lds_read_tr8(p);
-      return u32x2w{a.x, a.y};
-    } else if constexpr (C::KPACK == 16) {
-      const uint2 a = lds_read_tr8(p), b = lds_read_tr8(p + 8 * C::LDB);
-      return u32x4{a.x, a.y, b.x, b.y};
-    } else {
-      const uint2 a = lds_read_tr8(p), b = lds_read_tr8(p + 8 * C::LDB), c = lds_read_tr8(p + 16 * C::LDB),
-                  d = lds_read_tr8(p + 24 * C::LDB);
-      return u32x8{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
-    }
-  };
-  auto lfrag = [&](int buf, auto s, auto slot) {
-    constexpr int SL = decltype(slot)::value;
-    constexpr int ko = decltype(s)::value * C::MK * ES;
-    // B fragment j / k-step offset: K-packed rows are n (32 per tile) with k along the row; transposed rows are k
-    constexpr int bko = C::BTR ? decltype(s)::value * C::MK * C::LDB : ko;
-    constexpr int bjo = C::BTR ? 32 * C::BLES : 32 * C::LDK;
-    const char* st = smem + buf * C::STAGE;
+        const __amdgpu_buffer_rsrc_t rsb2 =
+            __builtin_amdgcn_make_buffer_rsrc((void*)(B2b + ko * G.B2.sk * BES), (short)0, -1, 0x00020000);
 #pragma unroll
-    for (int i = 0; i < C::TM; ++i) fa[SL][i] = F::load(st + a_off + i * 32 * C::LDK + ko);
-#pragma unroll
-    for (int j = 0; j < C::TN; ++j) {
-      fb[SL][j] = bfrag(st + b_off + j * bjo + bko);
-      if constexpr (DUAL) fb2[SL][j] = bfrag(st + b_off + C::BREG + j * bjo + bko);
-    }
-  };
-
-  // prologue: tile 0 in LDS stage 0, tile 1 in flight in registers
-  gload(0);
-  lstore(0);
-  gload(min(1, KT - 1));
-  __syncthreads();
-  lfrag(0, int_c<0>{}, int_c<0>{});
-
-  // k-tile kt reads LDS stage kt & 1. Per k-step s: the fragments of step s + 1 are requested first and a
-  // scheduling barrier keeps them ahead of the MFMAs of step s (the compiler would otherwise sink each read to just
-  // before its first use and expose the LDS latency). After the MFMAs of step 0, tile kt + 1 goes from registers to
-  // the other stage and tile kt + 2 is requested (past the last tile the last one is re-read: unconditional loads
-  // keep the wait counters exact). The single barrier sits before the MFMAs of the last k-step: by then every wave
-  // holds its last fragments of this stage and has stored tile kt + 1, so the first fragments of tile kt + 1 are read
-  // while the last k-step multiplies; the barrier also orders the reads of this stage before its next overwrite.
-  //
-  // MFMA operands are swapped (B fragment first): each accumulator holds the transposed 32×32 tile, so a lane's
-  // registers are 4 runs of 4 consecutive output columns of one row, which the epilogue writes as 16-byte words.
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
-    static_for<0, S>([&](auto s) {
-      constexpr int SS = decltype(s)::value;
-      if constexpr (SS + 1 < S) {
-        lfrag(cur, int_c<SS + 1>{}, int_c<(SS + 1) & 1>{});
-      } else {
-        __syncthreads();
-        lfrag(cur ^ 1, int_c<0>{}, int_c<0>{});
+        for (int i = 0; i < PB; ++i)
+          lds_dma16(rsb2, sb + BM * RBA + BREG + (wave_u + i * NW) * 1024, b2_voff, i * b2_pstep);
       }
-      __builtin_amdgcn_sched_barrier(0);
-      typename F::T wb[C::TN], wb2[DUAL ? C::TN : 1];
+    };
+
+    // ---- fragment read addresses (bytes from the stage base)
+    constexpr int S = BK / C::MK;
+    constexpr int CPL = C::KPACK * ES / 16;  // 16-byte chunks per lane per K-packed fragment (2 for fp8)
+    const int half = lane >> 5, l32 = lane & 31;
+    int a_rd[S][CPL];
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+      for (int q = 0; q < CPL; ++q)
+        a_rd[s][q] = (wm * C::WTM + l32) * RBA + 16 * ((s * 2 * CPL + half * CPL + q) ^ swz_k128(l32));
+    constexpr int NBR = C::BTR ? C::TN : S * CPL;
+    int b_rd[NBR];
+    if constexpr (C::BTR) {
 #pragma unroll
       for (int j = 0; j < C::TN; ++j) {
-        if constexpr (BWIDEN) {
-          wb[j] = f8x8_to_bf16(fb[SS & 1][j]);
-          if constexpr (DUAL) wb2[j] = f8x8_to_bf16(fb2[SS & 1][j]);
+        if constexpr (C::BLES == 2) {
+          const int kr = 8 * half + ((lane & 15) >> 2);
+          const int ch = (wn * C::WTN + 32 * j) / 8 + 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+          b_rd[j] = BM * RBA + kr * RBB + 16 * (ch ^ swz_tr<2, RBB>(kr)) + 8 * (lane & 1);
         } else {
-          wb[j] = fb[SS & 1][j];
-          if constexpr (DUAL) wb2[j] = fb2[SS & 1][j];
+          const int kr = C::KPACK * half + ((lane & 15) >> 1);
+          const int ch = (wn * C::WTN + 32 * j) / 16 + ((lane >> 4) & 1);
+          b_rd[j] = BM * RBA + kr * RBB + 16 * (ch ^ swz_tr<1, RBB>(kr)) + 8 * (lane & 1);
         }
       }
+    } else {
 #pragma unroll
-      for (int i = 0; i < C::TM; ++i)
+      for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int q = 0; q < CPL; ++q)
+          b_rd[s * CPL + q] = BM * RBA + (wn * C::WTN + l32) * RBA + 16 * ((s * 2 * CPL + half * CPL + q) ^ swz_k128(l32));
+    }
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)smem;
+
+    constexpr bool BWIDEN = C::BTR && C::BLES == 1 && ES == 2;
+    using FT = typename F::T;
+    using BF = std::conditional_t<BWIDEN, u32x2w, FT>;
+    FT fa[2][C::TM];
+    BF fb[2][C::TN], fb2[2][DUAL ? C::TN : 1];
+    auto lfrag = [&](int st, auto sc, auto slot) {
+      constexpr int SS = decltype(sc)::value, SL = decltype(slot)::value;
+      const uint32_t sb = lds0 + st * C::STAGE;
+      static_for<0, C::TM>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        if constexpr (CPL == 1) {
+          fa[SL][i] = lds_rd128<i * 32 * RBA>(sb + a_rd[SS][0]);
+        } else {
+          const u32x4 lo = lds_rd128<i * 32 * RBA>(sb + a_rd[SS][0]), hi = lds_rd128<i * 32 * RBA>(sb + a_rd[SS][1]);
+          fa[SL][i] = FT{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        }
+      });
+      static_for<0, C::TN>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        static_for<0, C::NB>([&](auto bc) {
+          constexpr int bi = decltype(bc)::value;
+          BF v;
+          if constexpr (C::BTR) {
+            constexpr int O = SS * C::MK * RBB + bi * BREG;
+            const uint32_t ad = sb + b_rd[j];
+            if constexpr (C::BLES == 2) {
+              const u32x2v lo = lds_rd_tr16<O>(ad), hi = lds_rd_tr16<O + 4 * RBB>(ad);
+              v = BF{lo.x, lo.y, hi.x, hi.y};
+            } else if constexpr (BWIDEN) {
+              const u32x2v a = lds_rd_tr8<O>(ad);
+              v = BF{a.x, a.y};
+            } else if constexpr (C::KPACK == 16) {
+              const u32x2v a = lds_rd_tr8<O>(ad), b = lds_rd_tr8<O + 8 * RBB>(ad);
+              v = BF{a.x, a.y, b.x, b.y};
+            } else {
+              const u32x2v a = lds_rd_tr8<O>(ad), b = lds_rd_tr8<O + 8 * RBB>(ad), c = lds_rd_tr8<O + 16 * RBB>(ad),
+                           d = lds_rd_tr8<O + 24 * RBB>(ad);
+              v = BF{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
+            }
+          } else {
+            constexpr int O = j * 32 * RBA + bi * BREG;
+            if constexpr (CPL == 1) {
+              v = lds_rd128<O>(sb + b_rd[SS * CPL]);
+            } else {
+              const u32x4 lo = lds_rd128<O>(sb + b_rd[SS * CPL]), hi = lds_rd128<O>(sb + b_rd[SS * CPL + 1]);
+              v = BF{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+            }
+          }
+          if constexpr (bi == 0) fb[SL][j] = v;
+          else fb2[SL][j] = v;
+        });
+      });
+    };
+    // LDS read instructions per k-step (the wait count that leaves the next step's reads in flight)
+    constexpr int BREADS = !C::BTR ? CPL : (C::BLES == 2 ? 2 : (BWIDEN ? 1 : C::KPACK / 8));
+    constexpr int NREAD = C::TM * CPL + C::TN * C::NB * BREADS;
+    // (lgkmcnt counts to 15: with more reads per step the wait also covers some of the next step's reads)
+    constexpr int NWAIT = NREAD < 15 ? NREAD : 15;
+    // the reads into fragment slot SL are complete once at most N LDS reads are outstanding (N < 0: already waited
+    // for); the slot's fragments pass through the wait
+    auto wait_slot = [&](auto slot, auto n) {
+      constexpr int SL = decltype(slot)::value, N = decltype(n)::value;
+      if constexpr (N >= 0) lgkm_wait<N>();
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i) after_wait(fa[SL][i]);
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j) {
+        after_wait(fb[SL][j]);
+        if constexpr (DUAL) after_wait(fb2[SL][j]);
+      }
+    };
+
+    // prologue: tiles 0 (and 1 with three stages) in flight, tile 0 waited for
+    dma(0, 0);
+    if constexpr (NST == 3) {
+      if (KT > 1) {
+        dma(1, 1);
+        dma_barrier<OPS>();
+      } else {
+        dma_barrier<0>();
+      }
+    } else {
+      dma_barrier<0>();
+    }
+    lfrag(0, int_c<0>{}, int_c<0>{});
+    int cur = 0;
+    for (int kt = 0; kt < KT; ++kt) {
+      const int nxt = cur + 1 == NST ? 0 : cur + 1;
+      static_for<0, S>([&](auto s) {
+        constexpr int SS = decltype(s)::value;
+        if constexpr (SS + 1 < S) {
+          lfrag(cur, int_c<SS + 1>{}, int_c<(SS + 1) & 1>{});
+          wait_slot(int_c<SS & 1>{}, int_c<NWAIT>{});
+        } else {
+          // tile kt + 1 complete in every wave's LDS, and every wave done reading stage cur
+          if (NST == 3 && kt + 2 < KT) dma_barrier<NST == 3 ? OPS : 0>();
+          else dma_barrier<0>();
+          wait_slot(int_c<SS & 1>{}, int_c<-1>{});
+          lfrag(nxt, int_c<0>{}, int_c<0>{});
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        typename F::T wb[C::TN], wb2[DUAL ? C::TN : 1];
 #pragma unroll
         for (int j = 0; j < C::TN; ++j) {
-          acc[i][j] = M::mma(wb[j], fa[SS & 1][i], acc[i][j]);
-          if constexpr (DUAL) acc2[i][j] = M::mma(wb2[j], fa[SS & 1][i], acc2[i][j]);
+          if constexpr (BWIDEN) {
+            wb[j] = f8x8_to_bf16(fb[SS & 1][j]);
+            if constexpr (DUAL) wb2[j] = f8x8_to_bf16(fb2[SS & 1][j]);
+          } else {
+            wb[j] = fb[SS & 1][j];
+            if constexpr (DUAL) wb2[j] = fb2[SS & 1][j];
+          }
         }
-      // The LDS store of tile kt + 1 (step 0) and the loads of tile kt + 2 (step 1) are spread between this step's
-      // MFMAs, one memory instruction per MFMA: issued as a burst they would queue in the memory pipeline and stall
-      // the in-order issue of the MFMAs behind them.
-      constexpr int NM = C::TM * C::TN * C::NB;
-      if constexpr (SS == 0) {
-        lstore(cur ^ 1);
-        static_for<0, NM>([&](auto) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU (transposes, addresses)
-          __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS write
-        });
+#pragma unroll
+        for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+          for (int j = 0; j < C::TN; ++j) {
+            acc[i][j] = M::mma(wb[j], fa[SS & 1][i], acc[i][j]);
+            if constexpr (DUAL) acc2[i][j] = M::mma(wb2[j], fa[SS & 1][i], acc2[i][j]);
+          }
+        if constexpr (SS == 0) {
+          // tile kt + NST - 1 into the stage tile kt - 1 used (every wave finished reading it before the last barrier)
+          const int t = kt + NST - 1;
+          if (t < KT) {
+            dma(t, t % NST);
+            constexpr int NM = C::TM * C::TN * C::NB;
+            static_for<0, (OPS < NM ? OPS : NM)>([&](auto) {
+              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+              __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read (DMA)
+            });
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      cur = nxt;
+    }
+  } else {
+    // One register stage of global prefetch: tile kt + 2 is requested at the start of k-tile kt (right after tile
+    // kt + 1 went from registers to LDS), so each load has a whole k-tile of MFMA work to arrive in. Two LDS stages.
+    using BLoader = std::conditional_t<
+        C::BTR, TileCopyLoader<C::BLES, BN, BK, C::THREADS>,
+        std::conditional_t<BES != ES, TileWidenLoader<BN, BK, C::THREADS>, TileLoader<ES, BN, BK, C::THREADS, B_R>>>;
+    TileLoader<ES, BM, BK, C::THREADS, A_R> la;
+    BLoader lb;
+    BLoader lb2;
+    // edge kernels: the last byte of each operand (its loads are bounded to it), as an address
+    auto op_end = [&](const GemmOperand& o, int rows, int es) -> const char* {
+      return (const char*)o.ptr +
+             ((int64_t)(G.batch - 1) * o.sb + (int64_t)(rows - 1) * o.sr + (int64_t)(G.K - 1) * o.sk + 1) * es;
+    };
+    const char* const a_end = EDGE ? op_end(G.A, G.M, ES) : nullptr;
+    const char* const b_end = EDGE ? op_end(G.B, G.N, BES) : nullptr;
+    const char* const b2_end = EDGE && DUAL ? op_end(G.B2, G.N, BES) : nullptr;
+    auto bounds = [&](const char* p, const char* end, int kvalid) {
+      LoadBounds r;
+      r.nrec = (int)min((int64_t)(end - p), (int64_t)0x7fffffff);
+      r.kvalid = kvalid;
+      return r;
+    };
+    auto gload = [&](int kt) {
+      const int64_t ko = (int64_t)(kt0 + kt) * BK;
+      const char* pa = Ab + ko * G.A.sk * ES;
+      const char* pb = Bb + ko * G.B.sk * BES;
+      if constexpr (EDGE) {
+        const int kvalid = G.K - (int)ko;
+        la.template load<true>(pa, G.A.sr, G.A.sk, tid, bounds(pa, a_end, kvalid));
+        lb.template load<true>(pb, G.B.sr, G.B.sk, tid, bounds(pb, b_end, kvalid));
+        if constexpr (DUAL) {
+          const char* pb2 = B2b + ko * G.B2.sk * BES;
+          lb2.template load<true>(pb2, G.B2.sr, G.B2.sk, tid, bounds(pb2, b2_end, kvalid));
+        }
+      } else {
+        la.load(pa, G.A.sr, G.A.sk, tid);
+        lb.load(pb, G.B.sr, G.B.sk, tid);
+        if constexpr (DUAL) lb2.load(B2b + ko * G.B2.sk * BES, G.B2.sr, G.B2.sk, tid);
       }
-      if constexpr (SS == (S > 2 ? 1 : 0)) {
-        gload(min(kt + 2, KT - 1));
-        static_for<0, NM>([&](auto) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global load
-        });
+    };
+    auto lstore = [&](int buf) {
+      char* s = smem + buf * C::STAGE;
+      la.template store<C::LDK>(s, tid);
+      constexpr int BP = C::BTR ? C::LDB : C::LDK;
+      lb.template store<BP>(s + BM * C::LDK, tid);
+      if constexpr (DUAL) lb2.template store<BP>(s + BM * C::LDK + C::BREG, tid);
+    };
+
+    // Fragments of MFMA k-step s live in register slot s & 1: step s + 1 is read from LDS while step s multiplies.
+    constexpr int S = BK / C::MK;
+    static_assert(S % 2 == 0, "k-steps per tile must be even (fragment slots alternate)");
+    // f8 B in LDS for the bf16 MFMA: B fragments are kept as the raw bytes of their transposing read and widened
+    // right before the MFMAs that use them, so their LDS reads stay in flight across the previous step's MFMAs
+    constexpr bool BWIDEN = C::BTR && C::BLES == 1 && ES == 2;
+    using BF = std::conditional_t<BWIDEN, u32x2w, typename F::T>;
+    typename F::T fa[2][C::TM];
+    BF fb[2][C::TN], fb2[2][DUAL ? C::TN : 1];
+    const int lrow = lane & 31;
+    const int lk = (lane >> 5) * C::KPACK * ES;  // byte offset of this lane's k-pack within an MFMA k-step
+    const int a_off = (wm * C::WTM + lrow) * C::LDK + lk;
+    // K-packed B: row n, k-pack of this lane. Transposed-read B: lane s of each 16-lane group addresses k-row
+    // 8·(lane/32) + s/4 and column 16·((lane/16) % 2) + 4·(s % 4), so the pair of reads (k-rows +0 and +4) delivers
+    // B[8·(lane/32) .. +7][lane % 32] — the MFMA operand fragment.
+    // (8-bit: lane s addresses k-row KPACK·(lane/32) + s/2 and column 16·((lane/16) % 2) + 8·(s % 2); each read
+    // delivers 8 consecutive k, KPACK / 8 reads make the fragment.)
+    const int b_off = !C::BTR ? BM * C::LDK + (wn * C::WTN + lrow) * C::LDK + lk
+                      : C::BLES == 2 ? BM * C::LDK + (8 * (lane >> 5) + ((lane & 15) >> 2)) * C::LDB +
+                                           (wn * C::WTN + 16 * ((lane >> 4) & 1) + 4 * (lane & 3)) * 2
+                                     : BM * C::LDK + (C::KPACK * (lane >> 5) + ((lane & 15) >> 1)) * C::LDB +
+                                           (wn * C::WTN + 16 * ((lane >> 4) & 1) + 8 * (lane & 1));
+    auto bfrag = [&](const char* p) -> BF {
+      if constexpr (!C::BTR) {
+        return F::load(p);
+      } else if constexpr (C::BLES == 2) {
+        const uint2 lo = lds_read_tr16(p), hi = lds_read_tr16(p + 4 * C::LDB);
+        return u32x4{lo.x, lo.y, hi.x, hi.y};
+      } else if constexpr (BWIDEN) {  // one transposing read gives the 8 k of the fragment
+        const uint2 a = lds_read_tr8(p);
+        return u32x2w{a.x, a.y};
+      } else if constexpr (C::KPACK == 16) {
+        const uint2 a = lds_read_tr8(p), b = lds_read_tr8(p + 8 * C::LDB);
+        return u32x4{a.x, a.y, b.x, b.y};
+      } else {
+        const uint2 a = lds_read_tr8(p), b = lds_read_tr8(p + 8 * C::LDB), c = lds_read_tr8(p + 16 * C::LDB),
+                    d = lds_read_tr8(p + 24 * C::LDB);
+        return u32x8{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
       }
-      __builtin_amdgcn_sched_barrier(0);
-    });
-  }
+    };
+    auto lfrag = [&](int buf, auto s, auto slot) {
+      constexpr int SL = decltype(slot)::value;
+      constexpr int ko = decltype(s)::value * C::MK * ES;
+      // B fragment j / k-step offset: K-packed rows are n (32 per tile) with k along the row; transposed rows are k
+      constexpr int bko = C::BTR ? decltype(s)::value * C::MK * C::LDB : ko;
+      constexpr int bjo = C::BTR ? 32 * C::BLES : 32 * C::LDK;
+      const char* st = smem + buf * C::STAGE;
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i) fa[SL][i] = F::load(st + a_off + i * 32 * C::LDK + ko);
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j) {
+        fb[SL][j] = bfrag(st + b_off + j * bjo + bko);
+        if constexpr (DUAL) fb2[SL][j] = bfrag(st + b_off + C::BREG + j * bjo + bko);
+      }
+    };
+
+    // prologue: tile 0 in LDS stage 0, tile 1 in flight in registers
+    gload(0);
+    lstore(0);
+    gload(min(1, KT - 1));
+    __syncthreads();
+    lfrag(0, int_c<0>{}, int_c<0>{});
+
+    // k-tile kt reads LDS stage kt & 1. Per k-step s: the fragments of step s + 1 are requested first and a
+    // scheduling barrier keeps them ahead of the MFMAs of step s (the compiler would otherwise sink each read to just
+    // before its first use and expose the LDS latency). After the MFMAs of step 0, tile kt + 1 goes from registers to
+    // the other stage and tile kt + 2 is requested (past the last tile the last one is re-read: unconditional loads
+    // keep the wait counters exact). The single barrier sits before the MFMAs of the last k-step: by then every wave
+    // holds its last fragments of this stage and has stored tile kt + 1, so the first fragments of tile kt + 1 are read
+    // while the last k-step multiplies; the barrier also orders the reads of this stage before its next overwrite.
+    //
+    // MFMA operands are swapped (B fragment first): each accumulator holds the transposed 32×32 tile, so a lane's
+    // registers are 4 runs of 4 consecutive output columns of one row, which the epilogue writes as 16-byte words.
+    for (int kt = 0; kt < KT; ++kt) {
+      const int cur = kt & 1;
+      static_for<0, S>([&](auto s) {
+        constexpr int SS = decltype(s)::value;
+        if constexpr (SS + 1 < S) {
+          lfrag(cur, int_c<SS + 1>{}, int_c<(SS + 1) & 1>{});
+        } else {
+          __syncthreads();
+          lfrag(cur ^ 1, int_c<0>{}, int_c<0>{});
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        typename F::T wb[C::TN], wb2[DUAL ? C::TN : 1];
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j) {
+          if constexpr (BWIDEN) {
+            wb[j] = f8x8_to_bf16(fb[SS & 1][j]);
+            if constexpr (DUAL) wb2[j] = f8x8_to_bf16(fb2[SS & 1][j]);
+          } else {
+            wb[j] = fb[SS & 1][j];
+            if constexpr (DUAL) wb2[j] = fb2[SS & 1][j];
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+          for (int j = 0; j < C::TN; ++j) {
+            acc[i][j] = M::mma(wb[j], fa[SS & 1][i], acc[i][j]);
+            if constexpr (DUAL) acc2[i][j] = M::mma(wb2[j], fa[SS & 1][i], acc2[i][j]);
+          }
+        // The LDS store of tile kt + 1 (step 0) and the loads of tile kt + 2 (step 1) are spread between this step's
+        // MFMAs, one memory instruction per MFMA: issued as a burst they would queue in the memory pipeline and stall
+        // the in-order issue of the MFMAs behind them.
+        constexpr int NM = C::TM * C::TN * C::NB;
+        if constexpr (SS == 0) {
+          lstore(cur ^ 1);
+          static_for<0, NM>([&](auto) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU (transposes, addresses)
+            __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS write
+          });
+        }
+        if constexpr (SS == (S > 2 ? 1 : 0)) {
+          gload(min(kt + 2, KT - 1));
+          static_for<0, NM>([&](auto) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global load
+          });
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      });
+    }
+
+  }  // main loop
 
   // Epilogue. With the swapped operands, register r of lane l holds C[l%32][8·(r/4) + 4·(l/32) + r%4] of its
   // 32×32 tile: registers 4g..4g+3 are 4 consecutive columns of one row. Each wave stages its accumulators in its own
@@ -833,7 +1127,7 @@ struct Choice {
 
 template <int KIND, int BM, int BN, int BK, int WM, int WN, bool A_R, bool B_R, bool DUAL, bool EDGE = false>
 Choice make_choice(const char* name) {
-  using C = MfmaCfg<KIND, BM, BN, BK, WM, WN, A_R, B_R, DUAL>;
+  using C = MfmaCfg<KIND, BM, BN, BK, WM, WN, A_R, B_R, DUAL, EDGE>;
   Choice c;
   c.fn = (const void*)&gemm_mfma_kernel<KIND, BM, BN, BK, WM, WN, A_R, B_R, DUAL, EDGE>;
   c.edge = EDGE;
