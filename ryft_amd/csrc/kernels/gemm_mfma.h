@@ -476,6 +476,19 @@ __device__ __forceinline__ uint32_t out_bits(uint32_t x, bool is_float) {
   }
 }
 
+// The first `nvalid` (at most 16 / OS) elements of a 16-byte output chunk packed in w, stored an element at a time.
+template <int OS>
+__device__ __forceinline__ void store_chunk_elements(char* p, const uint32_t (&w)[4], int nvalid) {
+#pragma unroll
+  for (int e = 0; e < 16 / OS; ++e) {
+    if (e >= nvalid) break;
+    const uint32_t word = w[e * OS / 4];
+    if constexpr (OS == 4) *(uint32_t*)(p + 4 * e) = word;
+    else if constexpr (OS == 2) *(uint16_t*)(p + 2 * e) = (uint16_t)(word >> (16 * (e & 1)));
+    else *(uint8_t*)(p + e) = (uint8_t)(word >> (8 * (e & 3)));
+  }
+}
+
 // One epilogue pass over a wave's staged accumulators: ROWS rows of WTN words at `reg` (and `reg2`, the second
 // accumulator of a dual GEMM), row pitch PITCH words. Each lane owns one 16-byte output chunk column (16 / size(DT)
 // values) and walks the rows in steps of 64 / chunks-per-row, so consecutive lanes write consecutive bytes of a row.
@@ -492,9 +505,12 @@ __device__ __forceinline__ void epi_pass(const GemmArgs& G, void* out, int b, in
   constexpr int RSTEP = 64 / CPR, ITER = ROWS * CPR / 64;
   const int row0 = lane / CPR, col = (lane % CPR) * VPC;
   const int n = n0 + col;
-  // partial edge tiles: chunks past N (N is a multiple of 16, so a chunk is all in or all out) and rows past M are
-  // neither read from the per-row / per-column operands nor stored
-  const bool col_ok = !EDGE || n < G.N;
+  // partial edge tiles: columns past N and rows past M are neither read from the per-row / per-column operands nor
+  // stored; a chunk that runs past N, or any chunk of rows that are not 16-byte aligned (N·size not a multiple of
+  // 16), is stored an element at a time
+  const int nvalid = EDGE ? G.N - n : VPC;
+  const bool col_ok = nvalid > 0;
+  const bool vec_ok = !EDGE || (nvalid >= VPC && ((int64_t)G.N * OS) % 16 == 0);
   char* optr = (char*)out + (((int64_t)b * G.M + m0 + row0) * (int64_t)G.N + n) * OS;
   const int64_t ostep = (int64_t)RSTEP * G.N * OS;
   // per-column operands are the same for every row this lane visits
@@ -502,12 +518,12 @@ __device__ __forceinline__ void epi_pass(const GemmArgs& G, void* out, int b, in
   if constexpr (KIND == EPI_SCALE || KIND == EPI_SWIGLU) {
     const float* cp = G.col && col_ok ? G.col + (int64_t)b * G.col_sb + (int64_t)n * G.col_sn : nullptr;
 #pragma unroll
-    for (int e = 0; e < VPC; ++e) cs[e] = cp ? cp[(int64_t)e * G.col_sn] : 1.0f;
+    for (int e = 0; e < VPC; ++e) cs[e] = cp && e < nvalid ? cp[(int64_t)e * G.col_sn] : 1.0f;
   }
   if constexpr (KIND == EPI_SWIGLU) {
     const float* cp = G.col2 && col_ok ? G.col2 + (int64_t)b * G.col2_sb + (int64_t)n * G.col2_sn : nullptr;
 #pragma unroll
-    for (int e = 0; e < VPC; ++e) cs2[e] = cp ? cp[(int64_t)e * G.col2_sn] : 1.0f;
+    for (int e = 0; e < VPC; ++e) cs2[e] = cp && e < nvalid ? cp[(int64_t)e * G.col2_sn] : 1.0f;
   }
 #pragma unroll 4
   for (int it = 0; it < ITER; ++it) {
@@ -565,7 +581,8 @@ __device__ __forceinline__ void epi_pass(const GemmArgs& G, void* out, int b, in
                (out_bits<DT>(v[4 * q + 2], is_float) << 16) | (out_bits<DT>(v[4 * q + 3], is_float) << 24);
       }
     }
-    *(u32x4*)(optr + it * ostep) = u32x4{w[0], w[1], w[2], w[3]};
+    if (vec_ok) *(u32x4*)(optr + it * ostep) = u32x4{w[0], w[1], w[2], w[3]};
+    else store_chunk_elements<OS>(optr + it * ostep, w, nvalid);
   }
 }
 
@@ -898,10 +915,16 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_mfma_kernel(const GemmArgs 
     TileLoader<ES, BM, BK, C::THREADS, A_R> la;
     BLoader lb;
     BLoader lb2;
-    // edge kernels: the last byte of each operand (its loads are bounded to it), as an address
+    // edge kernels: one past the last byte of each operand their loads may read, as an address (the loads are
+    // bounded to it). An operand contiguous along its rows / columns (sr == 1) is read in 16-byte vectors along them,
+    // so the bound is the end of the vector holding the last element: a vector straddling the last element's byte
+    // would otherwise read as zero whole. (That vector stays inside the row pitch, which the layout check keeps a
+    // multiple of the vector.)
     auto op_end = [&](const GemmOperand& o, int rows, int es) -> const char* {
+      const int ve = 16 / es;
+      const int64_t r = o.sr == 1 ? ((int64_t)rows + ve - 1) / ve * ve : rows;
       return (const char*)o.ptr +
-             ((int64_t)(G.batch - 1) * o.sb + (int64_t)(rows - 1) * o.sr + (int64_t)(G.K - 1) * o.sk + 1) * es;
+             ((int64_t)(G.batch - 1) * o.sb + (r - 1) * o.sr + (int64_t)(G.K - 1) * o.sk + 1) * es;
     };
     const char* const a_end = EDGE ? op_end(G.A, G.M, ES) : nullptr;
     const char* const b_end = EDGE ? op_end(G.B, G.N, BES) : nullptr;

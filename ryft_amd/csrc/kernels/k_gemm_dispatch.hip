@@ -223,11 +223,34 @@ static int mma_kind(const GemmArgs& g) {
   }
 }
 
+// Operands (bit 0: A, 1: B, 2: B2) whose layout the MFMA kernels cannot read: neither K-contiguous nor contiguous
+// along their free dimension in 16-byte vectors (`kbytes`-byte pieces along k for a K-contiguous f8 B widened to
+// bf16), misaligned, or with rows too far apart for the 32-bit buffer offsets of a tile.
+static unsigned layout_gaps(const GemmArgs& g, int kind, int* ar, int* br) {
+  const int es = kind == MMA_BF16 || kind == MMA_F16 || kind == MMA_BF16_F8 ? 2 : (kind == MMA_F32 ? 4 : 1);
+  const int bes = kind == MMA_BF16_F8 ? 1 : es;  // B's element size in HBM
+  auto layout = [&](const GemmOperand& o, int oes, int kbytes, int* r) -> bool {
+    const int ve = 16 / oes, vk = kbytes / oes;
+    if (((uintptr_t)o.ptr & 15) != 0) return false;
+    // tiles (≤ 256 rows / k-rows) are read through 32-bit buffer offsets from the tile origin
+    if ((o.sr > o.sk ? o.sr : o.sk) * (int64_t)oes * 256 >= ((int64_t)1 << 31)) return false;
+    if (o.sk == 1 && (o.sr % vk) == 0 && (o.sb % vk) == 0) { *r = 0; return true; }
+    if (o.sr == 1 && (o.sk % ve) == 0 && (o.sb % ve) == 0) { *r = 1; return true; }
+    return false;
+  };
+  const int bkb = kind == MMA_BF16_F8 ? 8 : 16;
+  unsigned gaps = 0;
+  int br2 = -1;
+  if (!layout(g.A, es, 16, ar)) gaps |= 1;
+  if (!layout(g.B, bes, bkb, br)) gaps |= 2;
+  if (g.dual && (!layout(g.B2, bes, bkb, &br2) || (!(gaps & 2) && br2 != *br))) gaps |= 4;
+  return gaps;
+}
+
 // Returns true and fills `c` when an MFMA instantiation covers these arguments.
 static bool pick_mfma(const GemmArgs& g, Choice* c) {
   // MFMA epilogues implement store / scale / SwiGLU; generic programs run on the generic kernel
   if (g.epilogue == EPI_PROGRAM || (g.dual && g.epilogue != EPI_SWIGLU)) return false;
-  if (g.N % 16) return false;  // 16-element row segments in the epilogue
   int kind = mma_kind(g);
   if (kind < 0) return false;
   // output types the MFMA epilogue writes (outputs are whole device allocations, so 16-byte aligned)
@@ -239,21 +262,8 @@ static bool pick_mfma(const GemmArgs& g, Choice* c) {
   if (g.epilogue == EPI_STORE && g.mid_round) return false;
   const int es = kind == MMA_BF16 || kind == MMA_F16 || kind == MMA_BF16_F8 ? 2 : (kind == MMA_F32 ? 4 : 1);
   const int bes = kind == MMA_BF16_F8 ? 1 : es;  // B's element size in HBM
-  // operand layouts: K-contiguous (sk == 1) or row-contiguous (sr == 1), read in 16-byte vectors of `oes`-byte
-  // elements (`kbytes`-byte pieces along k for a K-contiguous f8 B widened to bf16)
-  auto layout = [&](const GemmOperand& o, int oes, int kbytes, int* r) -> bool {
-    const int ve = 16 / oes, vk = kbytes / oes;
-    if (((uintptr_t)o.ptr & 15) != 0) return false;
-    // tiles (≤ 256 rows / k-rows) are read through 32-bit buffer offsets from the tile origin
-    if ((o.sr > o.sk ? o.sr : o.sk) * (int64_t)oes * 256 >= ((int64_t)1 << 31)) return false;
-    if (o.sk == 1 && (o.sr % vk) == 0 && (o.sb % vk) == 0) { *r = 0; return true; }
-    if (o.sr == 1 && (o.sk % ve) == 0 && (o.sb % ve) == 0) { *r = 1; return true; }
-    return false;
-  };
-  const int bkb = kind == MMA_BF16_F8 ? 8 : 16;
-  int ar, br, br2 = -1;
-  if (!layout(g.A, es, 16, &ar) || !layout(g.B, bes, bkb, &br)) return false;
-  if (g.dual && (!layout(g.B2, bes, bkb, &br2) || br2 != br)) return false;
+  int ar = 0, br = 0;
+  if (layout_gaps(g, kind, &ar, &br)) return false;
   bool ok = false;
   switch (kind) {
     case MMA_BF16: ok = pick_bf16(g, ar, br, c); break;
@@ -272,6 +282,24 @@ static bool pick_mfma(const GemmArgs& g, Choice* c) {
     if (g.K % kgran) ok = false;
   }
   return ok;
+}
+
+int gemm_mfma_layout_gaps(const GemmArgs& a) {
+  GemmArgs g = a;
+  g.splits = 1;
+  if (g.epilogue == EPI_PROGRAM) g.epilogue = EPI_STORE;
+  const int kind = mma_kind(g);
+  if (kind < 0 || (g.dual && g.epilogue != EPI_SWIGLU)) return -1;
+  int ar = 0, br = 0;
+  unsigned gaps = layout_gaps(g, kind, &ar, &br);
+  // K-contiguous operands of the edge kernels are read a vector (8-byte piece for a widened f8 B) at a time up to K
+  const int es = kind == MMA_BF16 || kind == MMA_F16 || kind == MMA_BF16_F8 ? 2 : (kind == MMA_F32 ? 4 : 1);
+  const int bes = kind == MMA_BF16_F8 ? 1 : es;
+  if (!(gaps & 1) && ar == 0 && g.K % (16 / es)) gaps |= 1;
+  if (!(gaps & 2) && br == 0 && g.K % (kind == MMA_BF16_F8 ? 8 : 16 / bes)) gaps |= g.dual ? 6 : 2;
+  if (gaps) return (int)gaps;
+  Choice c;
+  return pick_mfma(g, &c) ? 0 : -1;
 }
 
 const char* gemm_kernel_name(const GemmArgs& a) {

@@ -19,6 +19,9 @@ void launch_row(const RowArgs& a, hipStream_t stream, hipEvent_t done = nullptr)
 void launch_gemm(const GemmArgs& a, hipStream_t stream, hipEvent_t done = nullptr);
 void launch_attention(const AttnArgs& a, hipStream_t stream, hipEvent_t done = nullptr);
 
+// Operands of these GEMM arguments (bit 0: A, 1: B, 2: B2) whose layout keeps them from the MFMA kernels (0: the
+// MFMA kernels run them as they are; -1: their element types or epilogue have no MFMA kernel whatever the layout).
+int gemm_mfma_layout_gaps(const GemmArgs& a);
 // Name of the GEMM kernel launch_gemm() picks for these arguments (used for profiling labels).
 const char* gemm_kernel_name(const GemmArgs& a);
 // Number of K ranges launch_gemm splits these arguments into when given a workspace of

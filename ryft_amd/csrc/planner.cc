@@ -169,6 +169,7 @@ class Planner {
   void push_strided_step(ExprBuilder& b, const char* name, int out, int64_t out_offset,
                          const std::vector<int64_t>& out_strides, double in_bytes, double out_bytes);
   int canonical_copy(int node, const std::vector<int64_t>& order);
+  void padded_operand_copy(int dot, int which, GemmOperand* op, int* slot);
   void push_program_patches(Step& st, size_t base, const EwProgram& p, const std::vector<Leaf>& leaves,
                             const std::vector<int>& out_slots);
   bool splat_value(int node, double* v);
@@ -1050,6 +1051,61 @@ int Planner::canonical_copy(int node, const std::vector<int64_t>& order) {
   return slot;
 }
 
+// Operand `which` of a dot copied into a [batch][k][free] layout whose free dimension (M for the lhs, N for the rhs)
+// runs contiguously in rows padded to a multiple of 16 elements: 16-byte aligned rows that the MFMA edge kernels read
+// for any M, N and K (the padding columns only feed output rows / columns that are never stored).
+void Planner::padded_operand_copy(int dot, int which, GemmOperand* op, int* slot) {
+  const Node& d = g_.nodes[dot];
+  int node = d.operands[which];
+  // exact widening converts are left to the GEMM's loads, so the copy keeps the narrow type (an f8 weight stays f8
+  // and is widened in registers)
+  while (!materialized(node) && g_.nodes[node].op == Op::Convert &&
+         exact_widening(g_.nodes[g_.nodes[node].operands[0]].type.dtype, g_.nodes[node].type.dtype))
+    node = g_.nodes[node].operands[0];
+  const Node& on = g_.nodes[node];
+  const auto& batch = which == 0 ? d.dot.lhs_batch : d.dot.rhs_batch;
+  const auto& contract = which == 0 ? d.dot.lhs_contract : d.dot.rhs_contract;
+  std::vector<int64_t> free_dims;
+  for (int i = 0; i < on.type.rank(); ++i)
+    if (std::find(batch.begin(), batch.end(), i) == batch.end() &&
+        std::find(contract.begin(), contract.end(), i) == contract.end())
+      free_dims.push_back(i);
+  int64_t nb = 1, K = 1, F = 1;
+  for (auto i : batch) nb *= on.type.shape[i];
+  for (auto i : contract) K *= on.type.shape[i];
+  for (auto i : free_dims) F *= on.type.shape[i];
+  const int64_t Fp = (F + 15) / 16 * 16;
+  // iteration space: batch dims, contracting dims, free dims (operand dim order[i] ↔ space dim i)
+  std::vector<int64_t> order = batch;
+  order.insert(order.end(), contract.begin(), contract.end());
+  order.insert(order.end(), free_dims.begin(), free_dims.end());
+  std::vector<int64_t> space, out_strides(order.size());
+  for (auto o : order) space.push_back(on.type.shape[o]);
+  // output strides: free dims row-major within a padded row of Fp elements, contracting dims in units of Fp, batch
+  // dims in units of K·Fp
+  const size_t nbd = batch.size(), ncd = contract.size();
+  int64_t st = 1;
+  for (int i = (int)order.size() - 1; i >= 0; --i) {
+    if ((size_t)i + 1 == nbd + ncd) st = Fp;  // innermost contracting dim
+    if ((size_t)i + 1 == nbd) st = Fp * K;    // innermost batch dim
+    out_strides[i] = st;
+    st *= space[i];
+  }
+  std::vector<int> src(on.type.rank());
+  for (size_t i = 0; i < order.size(); ++i) src[order[i]] = (int)i;
+  const int out = new_slot(Slot::TEMP, TensorType{on.type.dtype, {nb, K, Fp}});
+  ExprBuilder b(*this, space);
+  b.add_output(b.emit(node, src), on.type.dtype);
+  push_strided_step(b, "dot_operand_copy", out, 0, out_strides, leaf_bytes(plan_, b.leaves()),
+                    (double)on.type.bytes());
+  op->ptr = nullptr;
+  op->sb = K * Fp;
+  op->sr = 1;
+  op->sk = Fp;
+  op->dtype = (int32_t)on.type.dtype;
+  *slot = out;
+}
+
 // Describe operand `which` (0 = lhs → A, 1 = rhs → B) of a dot as a strided [batch, row, k] view, peeling transposes
 // and exact widening converts into the GEMM's loads. Falls back to a canonical contiguous copy.
 bool Planner::dot_operand(int dot, int which, GemmOperand* op, int* slot, int force_copy) {
@@ -1176,6 +1232,21 @@ void Planner::emit_dot(const std::vector<int>& dots_in, int target, int root) {
   G.n_out = 1;
   G.alpha = 1.0f;
   G.out_dtype[0] = (int32_t)d.type.dtype;
+  {
+    // operands whose layout keeps an MFMA-capable dot from the MFMA kernels (rows that are not 16-byte aligned, a
+    // contiguous dimension the loads cannot use) are copied into a padded layout those kernels read
+    GemmArgs probe = G;
+    probe.epilogue = G.dual ? EPI_SWIGLU : EPI_STORE;
+    probe.out_dtype[0] = (int32_t)(G.dual ? DType::F32 : d.type.dtype);
+    const int gaps = gemm_mfma_layout_gaps(probe);
+    if (gaps > 0) {
+      if (gaps & 1) padded_operand_copy(dots[0], 0, &G.A, &sa);
+      if (gaps & 6) {
+        padded_operand_copy(dots[0], 1, &G.B, &sbs);
+        if (G.dual) padded_operand_copy(dots[1], 1, &G.B2, &sb2);
+      }
+    }
+  }
   st.patches.push_back({offsetof(GemmArgs, A) + offsetof(GemmOperand, ptr), sa});
   st.patches.push_back({offsetof(GemmArgs, B) + offsetof(GemmOperand, ptr), sbs});
   if (sb2 >= 0) st.patches.push_back({offsetof(GemmArgs, B2) + offsetof(GemmOperand, ptr), sb2});

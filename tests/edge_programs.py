@@ -71,4 +71,22 @@ CASES = [
      "gemm_bf16f8_mfma_edge_128x128", 1e-2),
     (dot("f16_ragged", (136, 200), (200, 80), "f16", "f32", [1], [0], seed=11),
      "gemm_f16_mfma_edge_128x128", 1e-2),
+    # N not a multiple of 16: partial output chunks stored an element at a time; rhs rows that are not 16-byte
+    # aligned (n-contiguous N·size % 16 != 0) copied into padded rows first
+    (dot("bf16_n1000", (1000, 1000), (1000, 1000), "bf16", "f32", [1], [0], out_convert="bf16", seed=12),
+     "gemm_bf16_mfma_edge_128x128", 1e-2),
+    (dot("bf16_n100_unaligned_rhs", (512, 4096), (4096, 100), "bf16", "f32", [1], [0], seed=13),
+     "gemm_bf16_mfma_edge_128x128", 1e-2),
+    (dot("f32_n250_unaligned_rhs", (256, 512), (512, 250), "f32", "f32", [1], [0], seed=14),
+     "gemm_f32_mfma_edge_64x64", 1e-4),
+    (dot("i8_n4008_unaligned_rhs", (4096, 4096), (4096, 4008), "i8", "i32", [1], [0], seed=15),
+     "gemm_i8_mfma_edge_128x128", 0.0),
+    (dot("bf16_odd_n37_k99", (64, 99), (99, 37), "bf16", "f32", [1], [0], out_convert="bf16", seed=16),
+     "gemm_bf16_mfma_edge_128x128", 1e-2),
+    (dot("fp8_n40", (96, 256), (256, 40), "f8E4M3FN", "f32", [1], [0], seed=17),
+     "gemm_fp8_mfma_edge_128x128", 1e-2),
+    (dot("bf16_f8_n72", (100, 264), (264, 72), "bf16", "f32", [1], [0], rhs_dt="f8E4M3FN", seed=18),
+     "gemm_bf16f8_mfma_edge_128x128", 1e-2),
+    (dot("f16_k_contiguous_n24", (80, 64), (24, 64), "f16", "f32", [1], [1], seed=19),
+     "gemm_f16_mfma_edge_128x128", 1e-2),
 ]

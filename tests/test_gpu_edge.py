@@ -30,6 +30,20 @@ def test_c3_scale_epilogue_on_partial_tiles(gpu_client):
         check(o, r, w.tolerance, f"c3 edge [{i}]")
 
 
+@pytest.mark.parametrize("kw", [dict(m=64, d=128, f=100), dict(m=100, d=200, f=136)])
+def test_c5_ragged_unaligned_weights(gpu_client, kw):
+    # f8 weight rows of 100 / 136 / 200 bytes (not 16-byte aligned): padded copies feed the dual SwiGLU GEMM and the
+    # down projection on the MFMA edge kernels, whose epilogues store the partial output chunks element by element
+    from ryft_amd import configs
+    w = configs.c5_swiglu_fp8(**kw)
+    print(f"[edge] c5 {kw}", flush=True)
+    outs, exe = run_pjrt(gpu_client, w.program, w.inputs)
+    plan = exe.describe_plan()
+    assert "gemm_bf16f8_mfma_dual_edge_128x128" in plan and "gemm_generic" not in plan, plan
+    err = check(outs[0], oracle_outputs(w.program, w.inputs)[0], w.tolerance, f"c5 {kw}")
+    print(f"[edge] c5 {kw} error {err:.3e}", flush=True)
+
+
 def test_c5_on_partial_tiles(gpu_client):
     # C5's graph at sizes that are not tile multiples: dual SwiGLU GEMM and down projection on the edge kernels
     from ryft_amd import configs

@@ -541,11 +541,22 @@ def test_attention_declined_when_the_kernel_cannot_run_it(compile_client, name, 
 
 
 def test_edge_tile_plans(compile_client):
-    # shapes that are not tile multiples, and m-contiguous lhs operands, plan to the edge MFMA kernels
+    # shapes that are not tile multiples, and m-contiguous lhs operands, plan to the edge MFMA kernels; operands whose
+    # rows are not 16-byte aligned are copied into padded rows first
     from tests.edge_programs import CASES
     for (name, prog, _), kernel, _ in CASES:
         _, kernels = _plan(compile_client, prog)
-        assert kernels == [kernel], (name, kernels)
+        assert kernels[-1] == kernel and all(k == "dot_operand_copy" for k in kernels[:-1]), (name, kernels)
+        unaligned = "unaligned" in name or "odd" in name or name in ("fp8_n40", "bf16_f8_n72")
+        assert ("dot_operand_copy" in kernels) == unaligned, (name, kernels)
+
+
+@pytest.mark.parametrize("kw", [dict(m=64, d=128, f=100), dict(m=100, d=200, f=136)])
+def test_ragged_swiglu_plans_stay_on_mfma(compile_client, kw):
+    # weights whose rows are not 16-byte aligned are copied (still f8) into padded rows: the dual SwiGLU GEMM and the
+    # down projection run on the bf16 x f8 MFMA edge kernels
+    _, kernels = _plan(compile_client, configs.c5_swiglu_fp8(**kw).program)
+    assert "gemm_generic" not in kernels and "gemm_bf16f8_mfma_dual_edge_128x128" in kernels, kernels
 
 
 @pytest.mark.parametrize("name,build,reductions", [
