@@ -81,6 +81,13 @@ class Rd {  // a cursor over one encoded span
     return v >> 1;
   }
   Span blob() { return bytes((size_t)varint()); }
+  // a varint giving the number of items that follow in this span, each taking at least one byte: larger counts
+  // are malformed (and would otherwise size containers from untrusted bytes)
+  uint64_t count() {
+    const uint64_t n = varint();
+    if (n > left()) bad("item count exceeds the data that follows");
+    return n;
+  }
   // {id, length, [alignment, padding], data}; alignment is relative to the start of the file
   int section(Span* data, const uint8_t* file) {
     const uint8_t id = byte();
@@ -140,6 +147,10 @@ struct BOp {
   std::vector<int> result_types;
   std::vector<int64_t> operands, results;  // value ids
   std::map<std::string, int> attrs;        // inherent + discardable attributes (attribute indices)
+  // the attributes as another property order reads them, when both orders decode (the graph builder falls back to
+  // it when the first reading does not type-check)
+  std::map<std::string, int> alt_attrs;
+  bool has_alt = false;
   std::vector<BRegion> regions;
 };
 
@@ -202,7 +213,7 @@ class BytecodeParser {
   // ---------------------------------------------------------------------------------------------- tables
   void read_strings(Span d) {
     Rd r(d);
-    const uint64_t n = r.varint();
+    const uint64_t n = r.count();
     std::vector<uint64_t> sizes(n);
     for (uint64_t k = 0; k < n; ++k) sizes[n - 1 - k] = r.varint();  // sizes are stored last string first
     size_t end = d.n;
@@ -262,7 +273,8 @@ class BytecodeParser {
 
   void read_attr_type_offsets(Span data, Span offsets) {
     Rd r(offsets);
-    const uint64_t n_attrs = r.varint(), n_types = r.varint();
+    const uint64_t n_attrs = r.count(), n_types = r.count();
+    if (n_attrs + n_types > r.left()) bad("attribute/type counts exceed their offset table");
     attr_entries_.resize(n_attrs);
     type_entries_.resize(n_types);
     size_t off = 0;
@@ -291,7 +303,7 @@ class BytecodeParser {
   void read_properties(Span d) {
     if (d.n == 0) return;
     Rd r(d);
-    const uint64_t n = r.varint();
+    const uint64_t n = r.count();
     for (uint64_t k = 0; k < n; ++k) props_.push_back(r.blob());
   }
 
@@ -370,6 +382,7 @@ class BytecodeParser {
           if (dim < 0) unimplemented("dynamic shapes are not supported");
           t.shape.push_back(dim);
         }
+        check_tensor_shape(t.shape);
         const BType& el = type(r.varint());
         if (el.kind != BType::SCALAR) unimplemented("tensor element type " + el.text + " is not supported");
         t.kind = BType::TENSOR;
@@ -434,7 +447,7 @@ class BytecodeParser {
   }
 
   std::vector<int64_t> svarints(Rd& r) {
-    std::vector<int64_t> v(r.varint());
+    std::vector<int64_t> v(r.count());
     for (auto& x : v) x = r.svarint();
     return v;
   }
@@ -641,9 +654,19 @@ class BytecodeParser {
     const Span inner = props_[index];
     auto it = schemas().find(op.name);
     if (it == schemas().end()) return;  // ops without attributes the plugin reads
-    if (decode_props(inner, it->second, &op.attrs)) return;
-    if (decode_props(inner, declared(op.name, it->second), &op.attrs)) return;
-    bad("cannot decode the properties of " + op.name);
+    // Both property orders are tried: a blob of one order can also decode in the other (an attribute index read as
+    // another field's). The sorted reading is taken when it decodes; a different declared-order reading is kept
+    // beside it for the graph builder.
+    const std::vector<Field> decl = declared(op.name, it->second);
+    std::map<std::string, int> sorted_attrs = op.attrs, decl_attrs = op.attrs;
+    const bool ok_sorted = decode_props(inner, it->second, &sorted_attrs);
+    const bool ok_decl = decode_props(inner, decl, &decl_attrs);
+    if (!ok_sorted && !ok_decl) bad("cannot decode the properties of " + op.name);
+    op.attrs = ok_sorted ? sorted_attrs : decl_attrs;
+    if (ok_sorted && ok_decl && sorted_attrs != decl_attrs) {
+      op.alt_attrs = std::move(decl_attrs);
+      op.has_alt = true;
+    }
   }
 
   void merge_dict(BOp& op, uint64_t index) {
@@ -685,6 +708,7 @@ class BytecodeParser {
   void read_block(Rd& r, BBlock& b) {
     bool has_args;
     const uint64_t n_ops = r.varint_flag(&has_args);
+    if (n_ops > r.left()) bad("op count exceeds the data that follows");
     if (has_args) {
       const uint64_t n = r.varint();
       for (uint64_t k = 0; k < n; ++k) {
@@ -705,9 +729,9 @@ class BytecodeParser {
   }
 
   void read_region(Rd& r, BRegion& reg) {
-    const uint64_t n_blocks = r.varint();
+    const uint64_t n_blocks = r.count();
     if (n_blocks == 0) return;
-    const uint64_t n_values = r.varint();
+    const uint64_t n_values = r.count();
     Scope& s = scopes_.back();
     const size_t base = s.values.size();
     s.next.push_back(base);
@@ -733,21 +757,24 @@ class BytecodeParser {
       else merge_dict(op, r.varint());
     }
     if (mask & 0x02) {
-      const uint64_t n = r.varint();
+      const uint64_t n = r.count();
       for (uint64_t k = 0; k < n; ++k) op.result_types.push_back((int)r.varint());
     }
     if (mask & 0x04) {
-      const uint64_t n = r.varint();
+      const uint64_t n = r.count();
       for (uint64_t k = 0; k < n; ++k) op.operands.push_back(use(r.varint()));
     }
     if (mask & 0x08) {
-      const uint64_t n = r.varint();
+      const uint64_t n = r.count();
       for (uint64_t k = 0; k < n; ++k) r.varint();
     }
     if (version_ >= 3 && (mask & 0x20)) skip_use_list_orders(r, op.result_types.size());
     uint64_t n_regions = 0;
     bool isolated = false;
-    if (mask & 0x10) n_regions = r.varint_flag(&isolated);
+    if (mask & 0x10) {
+      n_regions = r.varint_flag(&isolated);
+      if (n_regions > r.left() + 1) bad("region count exceeds the data that follows");
+    }
     for (size_t k = 0; k < op.result_types.size(); ++k) op.results.push_back(define());
     if (!n_regions) return;
     op.regions.resize(n_regions);
@@ -759,9 +786,11 @@ class BytecodeParser {
       sub = Rd(d);
       rr = &sub;
     }
+    if (++depth_ > kMaxNesting) bad("regions nested too deeply");
     if (isolated) scopes_.emplace_back();
     for (auto& reg : op.regions) read_region(*rr, reg);
     if (isolated) scopes_.pop_back();
+    --depth_;
   }
 
   const BOp* find_function(const BBlock& b, const std::string& entry) {
@@ -890,106 +919,120 @@ class BytecodeParser {
       if (op.name.rfind("stablehlo.", 0) != 0) unimplemented(op.name + " is not supported by the MI355X plugin");
       const std::string nm = op.name.substr(10);
       if (op.result_types.size() != 1) unimplemented(op.name + " with " + std::to_string(op.result_types.size()) + " results is not supported");
-      Node n;
-      n.debug = "%" + std::to_string(g.nodes.size());
-      n.type = tensor_type(op.result_types[0]);
-      for (int64_t v : op.operands) n.operands.push_back(value(v));
-      if (nm == "bitcast_convert") unimplemented("bitcast_convert is not supported");
-      auto it = simple.find(nm);
-      if (it != simple.end()) {
-        n.op = it->second;
-      } else if (nm == "constant") {
-        n.op = Op::Constant;
-        dense_literal(need(op, "value"), n.type, n);
-      } else if (nm == "iota") {
-        n.op = Op::Iota;
-        const BAttr& a = need(op, "iota_dimension");
-        n.iota_dim = a.kind == BAttr::INT ? a.i : mlir_int_list_text(a.str).at(0);
-      } else if (nm == "broadcast_in_dim") {
-        n.op = Op::BroadcastInDim;
-        n.dims = int_list(op, "broadcast_dimensions");
-      } else if (nm == "transpose") {
-        n.op = Op::Transpose;
-        n.dims = int_list(op, "permutation");
-      } else if (nm == "slice") {
-        n.op = Op::Slice;
-        n.lo = int_list(op, "start_indices");
-        n.hi = int_list(op, "limit_indices");
-        n.step = int_list(op, "strides");
-      } else if (nm == "concatenate") {
-        n.op = Op::Concatenate;
-        const BAttr& a = need(op, "dimension");
-        n.axis = a.kind == BAttr::INT ? a.i : mlir_int_list_text(a.str).at(0);
-      } else if (nm == "pad") {
-        n.op = Op::Pad;
-        n.lo = int_list(op, "edge_padding_low");
-        n.hi = int_list(op, "edge_padding_high");
-        n.step = int_list(op, "interior_padding");
-      } else if (nm == "compare") {
-        n.op = Op::Compare;
-        const BAttr& d = need(op, "comparison_direction");
-        if (d.kind == BAttr::CMP_DIR) {
-          if (d.i < 0 || d.i > 5) bad("comparison direction out of range");
-          n.cmp = (CmpDir)d.i;
-        } else {
-          n.cmp = mlir_cmp_dir_text(d.str);
-        }
-        if (const BAttr* t = get(op, "compare_type")) {
-          if (t->kind == BAttr::CMP_TYPE) {
-            if (t->i < 0 || t->i > 4) bad("comparison type out of range");
-            n.cmp_type = (CmpType)t->i;
+      auto make_node = [&](const BOp& op) {
+        Node n;
+        n.debug = "%" + std::to_string(g.nodes.size());
+        n.type = tensor_type(op.result_types[0]);
+        for (int64_t v : op.operands) n.operands.push_back(value(v));
+        if (nm == "bitcast_convert") unimplemented("bitcast_convert is not supported");
+        auto it = simple.find(nm);
+        if (it != simple.end()) {
+          n.op = it->second;
+        } else if (nm == "constant") {
+          n.op = Op::Constant;
+          dense_literal(need(op, "value"), n.type, n);
+        } else if (nm == "iota") {
+          n.op = Op::Iota;
+          const BAttr& a = need(op, "iota_dimension");
+          n.iota_dim = a.kind == BAttr::INT ? a.i : first_int(mlir_int_list_text(a.str), "iota_dimension");
+        } else if (nm == "broadcast_in_dim") {
+          n.op = Op::BroadcastInDim;
+          n.dims = int_list(op, "broadcast_dimensions");
+        } else if (nm == "transpose") {
+          n.op = Op::Transpose;
+          n.dims = int_list(op, "permutation");
+        } else if (nm == "slice") {
+          n.op = Op::Slice;
+          n.lo = int_list(op, "start_indices");
+          n.hi = int_list(op, "limit_indices");
+          n.step = int_list(op, "strides");
+        } else if (nm == "concatenate") {
+          n.op = Op::Concatenate;
+          const BAttr& a = need(op, "dimension");
+          n.axis = a.kind == BAttr::INT ? a.i : first_int(mlir_int_list_text(a.str), "dimension");
+        } else if (nm == "pad") {
+          n.op = Op::Pad;
+          n.lo = int_list(op, "edge_padding_low");
+          n.hi = int_list(op, "edge_padding_high");
+          n.step = int_list(op, "interior_padding");
+        } else if (nm == "compare") {
+          n.op = Op::Compare;
+          const BAttr& d = need(op, "comparison_direction");
+          if (d.kind == BAttr::CMP_DIR) {
+            if (d.i < 0 || d.i > 5) bad("comparison direction out of range");
+            n.cmp = (CmpDir)d.i;
           } else {
-            n.cmp_type = mlir_cmp_type_text(t->str);
+            n.cmp = mlir_cmp_dir_text(d.str);
           }
-        }
-      } else if (nm == "reduce") {
-        n.op = Op::Reduce;
-        if (n.operands.size() != 2) unimplemented("variadic reduce is not supported");
-        n.dims = int_list(op, "dimensions");
-        if (op.regions.size() != 1 || op.regions[0].blocks.size() != 1 || op.regions[0].blocks[0].ops.empty())
-          invalid("reduce: expected a one-block body");
-        const BBlock& rb = op.regions[0].blocks[0];
-        std::string b = rb.ops[0].name;
-        if (b.rfind("stablehlo.", 0) == 0) b = b.substr(10);
-        if (rb.ops[0].operands.size() != 2 || rb.args.size() != 2 ||
-            !std::is_permutation(rb.ops[0].operands.begin(), rb.ops[0].operands.end(), rb.args.begin()))
-          unimplemented("reduce body must apply one binary op to its two arguments");
-        if (b == "add") n.reduce_body = ReduceBody::Add;
-        else if (b == "maximum") n.reduce_body = ReduceBody::Max;
-        else if (b == "minimum") n.reduce_body = ReduceBody::Min;
-        else if (b == "multiply") n.reduce_body = ReduceBody::Mul;
-        else if (b == "and") n.reduce_body = ReduceBody::And;
-        else if (b == "or") n.reduce_body = ReduceBody::Or;
-        else unimplemented("reduce body '" + b + "' is not supported");
-      } else if (nm == "dot_general") {
-        n.op = Op::DotGeneral;
-        const BAttr& d = need(op, "dot_dimension_numbers");
-        if (d.kind == BAttr::DOT_DIMS) {
-          n.dot = d.dot;
+          if (const BAttr* t = get(op, "compare_type")) {
+            if (t->kind == BAttr::CMP_TYPE) {
+              if (t->i < 0 || t->i > 4) bad("comparison type out of range");
+              n.cmp_type = (CmpType)t->i;
+            } else {
+              n.cmp_type = mlir_cmp_type_text(t->str);
+            }
+          }
+        } else if (nm == "reduce") {
+          n.op = Op::Reduce;
+          if (n.operands.size() != 2) unimplemented("variadic reduce is not supported");
+          n.dims = int_list(op, "dimensions");
+          if (op.regions.size() != 1 || op.regions[0].blocks.size() != 1 || op.regions[0].blocks[0].ops.empty())
+            invalid("reduce: expected a one-block body");
+          const BBlock& rb = op.regions[0].blocks[0];
+          std::string b = rb.ops[0].name;
+          if (b.rfind("stablehlo.", 0) == 0) b = b.substr(10);
+          if (rb.ops[0].operands.size() != 2 || rb.args.size() != 2 ||
+              !std::is_permutation(rb.ops[0].operands.begin(), rb.ops[0].operands.end(), rb.args.begin()))
+            unimplemented("reduce body must apply one binary op to its two arguments");
+          if (b == "add") n.reduce_body = ReduceBody::Add;
+          else if (b == "maximum") n.reduce_body = ReduceBody::Max;
+          else if (b == "minimum") n.reduce_body = ReduceBody::Min;
+          else if (b == "multiply") n.reduce_body = ReduceBody::Mul;
+          else if (b == "and") n.reduce_body = ReduceBody::And;
+          else if (b == "or") n.reduce_body = ReduceBody::Or;
+          else unimplemented("reduce body '" + b + "' is not supported");
+        } else if (nm == "dot_general") {
+          n.op = Op::DotGeneral;
+          const BAttr& d = need(op, "dot_dimension_numbers");
+          if (d.kind == BAttr::DOT_DIMS) {
+            n.dot = d.dot;
+          } else {
+            auto field = [&](const char* f) {
+              size_t p = d.str.find(f);
+              if (p == std::string::npos) return std::vector<int64_t>();
+              size_t lb = d.str.find('[', p), rb2 = d.str.find(']', p);
+              if (lb == std::string::npos || rb2 == std::string::npos || rb2 < lb)
+                invalid(std::string("dot_dimension_numbers: malformed ") + f);
+              return mlir_int_list_text(d.str.substr(lb, rb2 - lb + 1));
+            };
+            n.dot.lhs_batch = field("lhs_batching_dimensions");
+            n.dot.rhs_batch = field("rhs_batching_dimensions");
+            n.dot.lhs_contract = field("lhs_contracting_dimensions");
+            n.dot.rhs_contract = field("rhs_contracting_dimensions");
+          }
+          if (const BAttr* al = get(op, "algorithm")) {
+            if (al->kind == BAttr::DOT_ALGORITHM) {
+              const BType& lt = type(al->lhs_precision);
+              const BType& rt = type(al->rhs_precision);
+              n.dot_lhs_precision = lt.kind == BType::SCALAR ? lt.dtype : DType::F32;  // tf32 → f32
+              n.dot_rhs_precision = rt.kind == BType::SCALAR ? rt.dtype : DType::F32;
+            }
+          }
         } else {
-          auto field = [&](const char* f) {
-            size_t p = d.str.find(f);
-            if (p == std::string::npos) return std::vector<int64_t>();
-            size_t lb = d.str.find('[', p), rb2 = d.str.find(']', p);
-            return mlir_int_list_text(d.str.substr(lb, rb2 - lb + 1));
-          };
-          n.dot.lhs_batch = field("lhs_batching_dimensions");
-          n.dot.rhs_batch = field("rhs_batching_dimensions");
-          n.dot.lhs_contract = field("lhs_contracting_dimensions");
-          n.dot.rhs_contract = field("rhs_contracting_dimensions");
+          unimplemented("stablehlo." + nm + " is not supported by the MI355X plugin");
         }
-        if (const BAttr* al = get(op, "algorithm")) {
-          if (al->kind == BAttr::DOT_ALGORITHM) {
-            const BType& lt = type(al->lhs_precision);
-            const BType& rt = type(al->rhs_precision);
-            n.dot_lhs_precision = lt.kind == BType::SCALAR ? lt.dtype : DType::F32;  // tf32 → f32
-            n.dot_rhs_precision = rt.kind == BType::SCALAR ? rt.dtype : DType::F32;
-          }
-        }
-      } else {
-        unimplemented("stablehlo." + nm + " is not supported by the MI355X plugin");
+        validate_node(g, n);
+        return n;
+      };
+      Node n;
+      try {
+        n = make_node(op);
+      } catch (const Status&) {
+        if (!op.has_alt) throw;
+        BOp alt = op;  // the other property order's reading
+        alt.attrs = op.alt_attrs;
+        n = make_node(alt);
       }
-      validate_node(g, n);
       node_of[op.results[0]] = add(std::move(n));
     }
     if (g.results.empty()) invalid("function @" + entry + " returns nothing");
@@ -1007,6 +1050,8 @@ class BytecodeParser {
   std::vector<std::shared_ptr<BType>> types_;
   std::vector<Span> props_;
   std::vector<Scope> scopes_;
+  static constexpr int kMaxNesting = 64;  // op regions inside op regions (a module's function bodies nest 2 deep)
+  int depth_ = 0;
   int64_t next_value_ = 0;
 };
 

@@ -17,6 +17,11 @@ void mlir_dense_text(const std::string& text, const TensorType& tt, Node& n);  /
 CmpDir mlir_cmp_dir_text(const std::string& raw);                   // text containing EQ / NE / GE / GT / LE / LT
 CmpType mlir_cmp_type_text(const std::string& raw);                 // text containing FLOAT / SIGNED / ...
 void validate_node(const Graph& g, Node& n);                        // operand counts, shapes, dimension ranges
+void check_tensor_shape(const std::vector<int64_t>& shape);         // dims and element count within plan limits
+inline int64_t first_int(const std::vector<int64_t>& v, const char* what) {  // a one-integer attribute's value
+  if (v.empty()) invalid(std::string("attribute `") + what + "` holds no integer");
+  return v[0];
+}
 // StableHLO op names (no dialect prefix) that map to one Op and carry no attributes ("add" → Op::Add, ...).
 const std::unordered_map<std::string, Op>& mlir_simple_ops();
 

@@ -8,6 +8,7 @@
 //   iota              .../miscellaneous.rs:1181       convert   .../casting.rs:456
 //   compare           .../comparison.rs:500, control_flow.rs:534
 //   slice / concatenate / pad  .../manipulation.rs:2438, 2388, 2257
+#include <algorithm>
 #include <cctype>
 #include <cmath>
 #include <cstdlib>
@@ -176,6 +177,7 @@ class Cursor {
   char peek_raw() const { return p_ < s_.size() ? s_[p_] : '\0'; }
 
   void skip_ws() {
+    if (p_ > s_.size()) p_ = s_.size();  // a scan that stepped over the end (an escape as the last character)
     for (;;) {
       while (p_ < s_.size() && isspace((unsigned char)s_[p_])) ++p_;
       if (p_ + 1 < s_.size() && s_[p_] == '/' && s_[p_ + 1] == '/') {
@@ -224,7 +226,7 @@ class Cursor {
     skip_ws();
     if (peek_raw() != '"') error("expected string");
     size_t b = ++p_;
-    while (p_ < s_.size() && s_[p_] != '"') p_ += (s_[p_] == '\\') ? 2 : 1;
+    skip_string_body();
     std::string r = s_.substr(b, p_ - b);
     ++p_;
     return r;
@@ -237,13 +239,21 @@ class Cursor {
     if (b == p_) error("expected integer");
     return std::strtoll(s_.c_str() + b, nullptr, 10);
   }
+  // Past a string's body (the opening quote consumed) to its closing quote; an unterminated string is an error.
+  void skip_string_body() {
+    while (p_ < s_.size() && s_[p_] != '"') p_ += (s_[p_] == '\\') ? 2 : 1;
+    if (p_ >= s_.size()) {
+      p_ = s_.size();
+      error("unterminated string");
+    }
+  }
   // Raw text up to the bracket matching the one just consumed (nesting aware, strings skipped).
   std::string skip_balanced(char open, char close) {
     size_t b = p_;
     int depth = 1;
     while (p_ < s_.size() && depth > 0) {
       char c = s_[p_];
-      if (c == '"') { ++p_; while (p_ < s_.size() && s_[p_] != '"') p_ += (s_[p_] == '\\') ? 2 : 1; }
+      if (c == '"') { ++p_; skip_string_body(); }
       else if (c == open) ++depth;
       else if (c == close) --depth;
       ++p_;
@@ -257,7 +267,7 @@ class Cursor {
     int depth = 1;
     while (p_ < s_.size() && depth > 0) {
       char c = s_[p_];
-      if (c == '"') { ++p_; while (p_ < s_.size() && s_[p_] != '"') p_ += (s_[p_] == '\\') ? 2 : 1; }
+      if (c == '"') { ++p_; skip_string_body(); }
       else if (c == '-' && p_ + 1 < s_.size() && s_[p_ + 1] == '>') { p_ += 2; continue; }
       else if (c == '<') ++depth;
       else if (c == '>') --depth;
@@ -267,10 +277,11 @@ class Cursor {
     return s_.substr(b, p_ - b - 1);
   }
   [[noreturn]] void error(const std::string& what) const {
+    const size_t at = std::min(p_, s_.size());
     size_t line = 1, col = 1;
-    for (size_t i = 0; i < p_ && i < s_.size(); ++i) { if (s_[i] == '\n') { ++line; col = 1; } else ++col; }
-    size_t e = s_.find('\n', p_);
-    std::string ctx = s_.substr(p_, std::min<size_t>(60, (e == std::string::npos ? s_.size() : e) - p_));
+    for (size_t i = 0; i < at; ++i) { if (s_[i] == '\n') { ++line; col = 1; } else ++col; }
+    size_t e = s_.find('\n', at);
+    std::string ctx = s_.substr(at, std::min<size_t>(60, (e == std::string::npos ? s_.size() : e) - at));
     invalid("MLIR parse error at " + std::to_string(line) + ":" + std::to_string(col) + ": " + what + " near '" + ctx + "'");
   }
   const std::string& text() const { return s_; }
@@ -314,6 +325,7 @@ TensorType parse_tensor_body(const std::string& body) {
     break;
   }
   tt.dtype = parse_element_type(b.substr(i));
+  check_tensor_shape(tt.shape);
   return tt;
 }
 
@@ -901,7 +913,7 @@ class Parser {
       parse_dense(payload, n.type, n);
     } else if (nm == "iota") {
       n.op = Op::Iota;
-      n.iota_dim = parse_int_list_text(get("iota_dimension")).at(0);
+      n.iota_dim = first_int(parse_int_list_text(get("iota_dimension")), "iota_dimension");
     } else if (nm == "broadcast_in_dim") {
       n.op = Op::BroadcastInDim;
       std::string d = get("dims");
@@ -921,7 +933,7 @@ class Parser {
       n.op = Op::Concatenate;
       std::string d = get("dim");
       if (d.empty()) d = get("dimension");
-      n.axis = parse_int_list_text(d).at(0);
+      n.axis = first_int(parse_int_list_text(d), "dimension");
     } else if (nm == "pad") {
       n.op = Op::Pad;
       std::string l = get("low"), h = get("high"), in = get("interior");
@@ -953,6 +965,8 @@ class Parser {
           size_t p = dd.find(f);
           if (p == std::string::npos) return std::vector<int64_t>();
           size_t lb = dd.find('[', p), rb = dd.find(']', p);
+          if (lb == std::string::npos || rb == std::string::npos || rb < lb)
+            invalid(std::string("dot_dimension_numbers: malformed ") + f);
           return parse_int_list_text(dd.substr(lb, rb - lb + 1));
         };
         n.dot.lhs_batch = field("lhs_batching_dimensions");
@@ -1020,8 +1034,33 @@ void mlir_dense_text(const std::string& text, const TensorType& tt, Node& n) {
 CmpDir mlir_cmp_dir_text(const std::string& raw) { return Parser::parse_dir(raw); }
 CmpType mlir_cmp_type_text(const std::string& raw) { return Parser::parse_cmp_type(raw); }
 
+// Tensor shapes whose element count (and byte size, at up to 8 bytes an element) fits a signed 64-bit integer with
+// room to spare: 2^48 elements at most, so that no size computed from a shape can overflow.
+void check_tensor_shape(const std::vector<int64_t>& shape) {
+  constexpr int64_t kMax = (int64_t)1 << 48;
+  int64_t n = 1;
+  for (int64_t d : shape) {
+    if (d < 0 || d > kMax) invalid("tensor dimension " + std::to_string(d) + " is out of range");
+    if (d && n > kMax / d) invalid("tensor " + shape_str(shape) + " has too many elements");
+    n *= d;
+  }
+}
+
 void validate_node(const Graph& g, Node& n) {
-  auto opt = [&](int i) -> const TensorType& { return g.nodes[n.operands.at(i)].type; };
+  auto opt = [&](int i) -> const TensorType& {
+    if (i < 0 || (size_t)i >= n.operands.size() || n.operands[i] < 0 || (size_t)n.operands[i] >= g.nodes.size())
+      invalid(std::string(op_name(n.op)) + ": missing operand " + std::to_string(i));
+    return g.nodes[n.operands[i]].type;
+  };
+  // dimension lists of one operand: each index in [0, rank), none repeated across the lists
+  auto dims_in_range = [&](std::initializer_list<const std::vector<int64_t>*> lists, int rank, const char* what) {
+    std::vector<char> used(rank > 0 ? rank : 0, 0);
+    for (const auto* l : lists)
+      for (int64_t d : *l) {
+        if (d < 0 || d >= rank || used[d]) invalid(std::string(what) + ": dimension out of range or repeated");
+        used[d] = 1;
+      }
+  };
   auto need = [&](size_t k) {
     if (n.operands.size() != k) invalid(std::string(op_name(n.op)) + " expects " + std::to_string(k) + " operands");
   };
@@ -1037,7 +1076,9 @@ void validate_node(const Graph& g, Node& n) {
       break;
     case Op::Transpose:
       need(1);
-      if ((int)n.dims.size() != opt(0).rank()) invalid("transpose: permutation size must equal rank");
+      if ((int)n.dims.size() != opt(0).rank() || n.type.rank() != opt(0).rank())
+        invalid("transpose: permutation size must equal rank");
+      dims_in_range({&n.dims}, opt(0).rank(), "transpose");
       for (size_t i = 0; i < n.dims.size(); ++i)
         if (n.type.shape[i] != opt(0).shape[n.dims[i]]) invalid("transpose: result shape mismatch");
       break;
@@ -1048,8 +1089,8 @@ void validate_node(const Graph& g, Node& n) {
     case Op::Slice: {
       need(1);
       const int r = opt(0).rank();
-      if ((int)n.lo.size() != r || (int)n.hi.size() != r || (int)n.step.size() != r)
-        invalid("slice: start / limit / stride lists must have one entry per dimension");
+      if ((int)n.lo.size() != r || (int)n.hi.size() != r || (int)n.step.size() != r || n.type.rank() != r)
+        invalid("slice: start / limit / stride lists and the result must have one entry per dimension");
       for (int d = 0; d < r; ++d) {
         if (n.step[d] < 1) invalid("slice: strides must be positive");
         if (n.lo[d] < 0 || n.lo[d] > n.hi[d] || n.hi[d] > opt(0).shape[d]) invalid("slice: indices out of range");
@@ -1076,8 +1117,8 @@ void validate_node(const Graph& g, Node& n) {
     case Op::Pad: {
       need(2);
       const int r = opt(0).rank();
-      if ((int)n.lo.size() != r || (int)n.hi.size() != r || (int)n.step.size() != r)
-        invalid("pad: padding lists must have one entry per dimension");
+      if ((int)n.lo.size() != r || (int)n.hi.size() != r || (int)n.step.size() != r || n.type.rank() != r)
+        invalid("pad: padding lists and the result must have one entry per dimension");
       if (opt(1).rank() != 0 || opt(1).dtype != opt(0).dtype || n.type.dtype != opt(0).dtype)
         invalid("pad: padding value must be a scalar of the operand's type");
       for (int d = 0; d < r; ++d) {
@@ -1094,15 +1135,32 @@ void validate_node(const Graph& g, Node& n) {
       auto& R = opt(1);
       if (n.dot.lhs_batch.size() != n.dot.rhs_batch.size() || n.dot.lhs_contract.size() != n.dot.rhs_contract.size())
         invalid("dot_general: mismatched dimension lists");
+      dims_in_range({&n.dot.lhs_batch, &n.dot.lhs_contract}, L.rank(), "dot_general");
+      dims_in_range({&n.dot.rhs_batch, &n.dot.rhs_contract}, R.rank(), "dot_general");
       for (size_t i = 0; i < n.dot.lhs_batch.size(); ++i)
-        if (L.shape.at(n.dot.lhs_batch[i]) != R.shape.at(n.dot.rhs_batch[i])) invalid("dot_general: batch size mismatch");
+        if (L.shape[n.dot.lhs_batch[i]] != R.shape[n.dot.rhs_batch[i]]) invalid("dot_general: batch size mismatch");
       for (size_t i = 0; i < n.dot.lhs_contract.size(); ++i)
-        if (L.shape.at(n.dot.lhs_contract[i]) != R.shape.at(n.dot.rhs_contract[i]))
+        if (L.shape[n.dot.lhs_contract[i]] != R.shape[n.dot.rhs_contract[i]])
           invalid("dot_general: contracting size mismatch");
+      {
+        // result: batch dims, then the lhs free dims, then the rhs free dims, each in operand order
+        std::vector<int64_t> want;
+        for (int64_t d : n.dot.lhs_batch) want.push_back(L.shape[d]);
+        auto free_of = [&](const TensorType& t, const std::vector<int64_t>& b, const std::vector<int64_t>& c) {
+          for (int d = 0; d < t.rank(); ++d)
+            if (std::find(b.begin(), b.end(), d) == b.end() && std::find(c.begin(), c.end(), d) == c.end())
+              want.push_back(t.shape[d]);
+        };
+        free_of(L, n.dot.lhs_batch, n.dot.lhs_contract);
+        free_of(R, n.dot.rhs_batch, n.dot.rhs_contract);
+        if (want != n.type.shape) invalid("dot_general: result shape mismatch");
+      }
       break;
     }
     case Op::Reduce: {
+      need(2);
       auto& in = opt(0);
+      dims_in_range({&n.dims}, in.rank(), "reduce");
       std::vector<int64_t> out;
       for (int d = 0; d < in.rank(); ++d) {
         bool red = false;
@@ -1116,12 +1174,27 @@ void validate_node(const Graph& g, Node& n) {
     case Op::Select:
       need(3);
       if (opt(0).dtype != DType::PRED) invalid("select: predicate must be i1");
+      if ((opt(0).rank() != 0 && opt(0).shape != n.type.shape) || opt(1).shape != n.type.shape ||
+          opt(2).shape != n.type.shape)
+        invalid("select: operand shapes must match the result (the predicate may be a scalar)");
       break;
     case Op::Iota:
       if (n.iota_dim < 0 || n.iota_dim >= n.type.rank()) invalid("iota: dimension out of range");
       break;
     default:
       if (op_is_elementwise(n.op)) {
+        switch (n.op) {
+          case Op::Add: case Op::Subtract: case Op::Multiply: case Op::Divide: case Op::Maximum: case Op::Minimum:
+          case Op::Power: case Op::Remainder: case Op::And: case Op::Or: case Op::Xor: case Op::Compare:
+            need(2);
+            break;
+          case Op::Clamp:
+            need(3);
+            break;
+          default:
+            need(1);
+            break;
+        }
         for (size_t i = 0; i < n.operands.size(); ++i) {
           auto& t = opt(i);
           bool scalar_ok = (n.op == Op::Select && i == 0) || n.op == Op::Clamp;

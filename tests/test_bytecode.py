@@ -49,6 +49,9 @@ PROGRAMS = {
     "layernorm": lambda: row_programs.layernorm((8, 33)),
     "int_row_max": lambda: row_programs.int_row_max_gap((8, 64)),
     "slice_concatenate_pad": lambda: SLICE_CONCAT_PAD,
+    # two dot_generals whose dimension numbers differ and whose contracted sizes differ (128 queries, 192 keys): a
+    # property blob read in the wrong field order would hand one dot the other's numbers
+    "attention_cross_lengths": lambda: configs.c4_causal_attention(b=1, h=1, s=128, d=64, mask=None, sk=192).program,
 }
 
 
