@@ -26,6 +26,8 @@ import os
 import sys
 import time
 
+import numpy as np
+
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
@@ -62,23 +64,53 @@ def _blas_threads():
     return int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
 
 
-def _cpu_baseline(name, seconds):
-    """The oracle (a numpy port of the StableHLO semantics, dots as f32 GEMMs the way XLA's CPU backend upcasts
-    bf16) timed on a bounded sample of the same workload on this host's cores."""
+def _cpu_baseline(name, seconds, w=None, gpu_outputs=None):
+    """CPU baseline of graph `name`: the C++ / OpenMP executor of the graph (oracle/cpu_exec.cc, built -O3
+    -march=native for this host, OpenMP over its cores) on the full workload `w` — the same input bytes the GPU
+    ran — for at least 5 evaluations and `seconds`; its outputs are compared with the GPU's (`gpu_outputs`, raw
+    arrays). Graphs it does not implement (the fp8-activation C5 extra) time the numpy oracle on a bounded sample."""
+    from oracle import cpu_exec
     from oracle import stablehlo as sh
     from ryft_amd import configs
     from tests.helpers import MLIR_DT
 
-    samples = {
-        "c1": (configs.c1_f32_dot, {}, "full C1"),
-        "c2": (configs.c2_bf16_batched_dot, {"batch": 2}, "2 of the 16 batches of C2"),
-        "c3": (configs.c3_int8_gemm, {"m": 512}, "512 of the 4096 rows of C3"),
-        "c4": (configs.c4_causal_attention, {"b": 1, "h": 2}, "2 of the 128 heads of C4"),
-        "c5": (configs.c5_swiglu_fp8, {"m": 64}, "64 of the 512 tokens of C5"),
-        "c5x": (configs.c5x_swiglu_fp8_activations, {"m": 64}, "64 of the 512 tokens of C5 (fp8 activations)"),
-        "copy": (configs.hbm_copy_f32, {}, "the full copy calibration vector"),
-        "rmsnorm": (configs.rmsnorm_fp8_rows, {"m": 1024}, "1024 of the 16384 rows"),
-    }
+    if name in ("c1", "c2", "c3", "c4", "c5", "copy", "rmsnorm"):
+        w = w or configs.CONFIGS[name]()
+        fn, outs = cpu_exec.prepare(name, w)
+        _, arch = cpu_exec.library()
+        threads = cpu_exec.threads()
+        fn()  # first touch of the output pages and the packed panels
+        t0 = time.perf_counter()
+        reps = 0
+        while True:
+            fn()
+            reps += 1
+            el = time.perf_counter() - t0
+            if (reps >= 5 and el >= seconds) or reps >= 500:
+                break
+        agree = None
+        if gpu_outputs:
+            errs = []
+            for got, ref in zip(outs, gpu_outputs):
+                if got.dtype.kind in "iu" and ref.dtype.kind in "iu" and got.dtype == ref.dtype and \
+                        got.dtype.itemsize == 4:
+                    errs.append(float(np.count_nonzero(got != ref)))  # integer accumulators: mismatch count
+                else:
+                    dt = {2: "bf16", 1: "f8E4M3FN"}.get(got.dtype.itemsize, "f32") if got.dtype.kind in "iu" else "f32"
+                    errs.append(sh.rel_error(sh.from_raw(got, dt), sh.from_raw(ref, dt)))
+            agree = errs
+        what = (f"the full {w.name} workload (same input bytes as the GPU run), {reps} evaluation(s) in {el:.2f} s; "
+                f"C++ executor oracle/cpu_exec.cc (-O3 -march={arch}, OpenMP, {threads} threads; register-tiled "
+                f"GEMMs over packed panels, bf16 / f8 widened to f32 while packing, int8 exactly in int32); host "
+                f"{_cpu_model()}, {os.cpu_count()} logical CPUs visible")
+        res = {"unit": "GB/s" if not w.flops else "TFLOP/s", "cores": threads, "kind": "port", "sample": what,
+               "evaluations": reps, "seconds": round(el, 3)}
+        res["value"] = round(w.bytes * reps / el / 1e9, 4) if not w.flops else round(w.flops * reps / el / 1e12, 6)
+        if agree is not None:
+            res["rel_error_vs_gpu"] = agree
+        return res
+
+    samples = {"c5x": (configs.c5x_swiglu_fp8_activations, {"m": 64}, "64 of the 512 tokens of C5 (fp8 activations)")}
     fn, kw, desc = samples[name]
     w = fn(**kw)
     vals = [sh.from_raw(x.data, MLIR_DT[x.type]) for x in w.inputs]
@@ -93,9 +125,6 @@ def _cpu_baseline(name, seconds):
     threads = _blas_threads()
     what = (f"{desc}, {reps} evaluation(s) in {el:.1f} s (numpy oracle: f32 dots on {threads} BLAS threads, "
             f"other ops single-threaded; host {_cpu_model()}, {os.cpu_count()} logical CPUs visible)")
-    if not w.flops:
-        return {"value": round(w.bytes * reps / el / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
-                "sample": what}
     return {"value": round(w.flops * reps / el / 1e12, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "sample": what}
 
@@ -157,8 +186,7 @@ def measure(name, steps, warmup, cpu_seconds, client, dev):
         hb = [client.buffer(x.data, x.type, x.dims, device=dev) for x in w.inputs]
         res = exe.execute([hb])[0]
         res.done.await_()
-        for o in res.outputs:
-            o.to_numpy()
+        gpu_outputs = [o.to_numpy() for o in res.outputs]
     ms_pcie = (time.perf_counter() - t2) / pcie_steps * 1e3
 
     # kernel timing pass (HIP events on the plugin stream, carried by the launches themselves)
@@ -211,7 +239,7 @@ def measure(name, steps, warmup, cpu_seconds, client, dev):
         "kernels": {k: {"median_us": round(v["median_us"], 2), "avg_us": round(v["avg_us"], 2),
                         "count_per_step": v["count"] / steps} for k, v in kernels.items()},
         "roofline": roofline,
-        "cpu_baseline": None if cpu_seconds <= 0 else _cpu_baseline(name, cpu_seconds),
+        "cpu_baseline": None if cpu_seconds <= 0 else _cpu_baseline(name, cpu_seconds, w, gpu_outputs),
     }
     if w.info.get("baseline_config") is False or name in ("copy", "rmsnorm"):
         result["note"] = "calibration / extra workload, not a BASELINE config"
@@ -227,7 +255,8 @@ def main():
     ap.add_argument("--config", default="all", choices=CHOICES,
                     help="all (default): every BASELINE graph plus the HBM calibrations, C5 as the headline; "
                          "or one workload, which then is the headline")
-    ap.add_argument("--cpu-seconds", type=float, default=4.0, help="CPU baseline sample length per graph")
+    ap.add_argument("--cpu-seconds", type=float, default=2.0,
+                    help="CPU baseline: time each graph's CPU executor for at least 5 evaluations and this long")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
