@@ -185,6 +185,10 @@ struct GemmArgs {
   int32_t splits;
   int32_t pad_splits;
   void* ws;
+  // split-K with per-output-tile arrival counters (zero between launches; the finishing range sets its tile's back
+  // to zero): the K range that completes a tile last sums the ranges' partial sums and applies the epilogue inside
+  // the GEMM kernel, with no reduction launch. Null: a reduction kernel follows the GEMM.
+  int32_t* tile_counters;
   // EPI_PROGRAM: iteration space = the dot result's dims; epi_groups = #dims in (batch, lhs-free, rhs-free)
   int32_t epi_groups[3];
   EwProgram epi;

@@ -476,6 +476,19 @@ __device__ __forceinline__ uint32_t out_bits(uint32_t x, bool is_float) {
   }
 }
 
+// Device-scope (sc1) vector store and load for the partial sums of split-K ranges: the stores write through to the
+// point of device coherence and the loads do not return stale L2 copies, whichever XCD each workgroup runs on, so no
+// cache write-back or invalidation is needed between the ranges and the one that finishes the tile. The loads are
+// not seen by the compiler's wait-count tracking: wait_loads() completes them.
+__device__ __forceinline__ void store_coherent16(void* p, const u32x4& v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ u32x4 load_coherent16(const void* p) {
+  u32x4 r;
+  asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(r) : "v"(p) : "memory");
+  return r;
+}
+
 // The first `nvalid` (at most 16 / OS) elements of a 16-byte output chunk packed in w, stored an element at a time.
 template <int OS>
 __device__ __forceinline__ void store_chunk_elements(char* p, const uint32_t (&w)[4], int nvalid) {
@@ -495,7 +508,7 @@ __device__ __forceinline__ void store_chunk_elements(char* p, const uint32_t (&w
 // KIND is EPI_STORE / EPI_SCALE / EPI_SWIGLU; the output type, the epilogue kind and the trip count are
 // compile-time, so each pass is a short unrolled loop whose LDS reads can be issued ahead of the conversions. MIDR:
 // the value is rounded to G.mid_round (bf16 or f16) before the output conversion.
-template <int KIND, int DT, bool INT, bool MIDR, int WTN, int PITCH, int ROWS, bool EDGE = false>
+template <int KIND, int DT, bool INT, bool MIDR, int WTN, int PITCH, int ROWS, bool EDGE = false, bool COH = false>
 __device__ __forceinline__ void epi_pass(const GemmArgs& G, void* out, int b, int m0, int n0, const uint32_t* reg,
                                          const uint32_t* reg2, int lane) {
   constexpr int OS = out_size<DT>();
@@ -581,8 +594,135 @@ __device__ __forceinline__ void epi_pass(const GemmArgs& G, void* out, int b, in
                (out_bits<DT>(v[4 * q + 2], is_float) << 16) | (out_bits<DT>(v[4 * q + 3], is_float) << 24);
       }
     }
-    if (vec_ok) *(u32x4*)(optr + it * ostep) = u32x4{w[0], w[1], w[2], w[3]};
+    if constexpr (COH) store_coherent16(optr + it * ostep, u32x4{w[0], w[1], w[2], w[3]});
+    else if (vec_ok) *(u32x4*)(optr + it * ostep) = u32x4{w[0], w[1], w[2], w[3]};
     else store_chunk_elements<OS>(optr + it * ostep, w, nvalid);
+  }
+}
+
+// ------------------------------------------------------------------------------------------------ split-K finish
+// Eight consecutive summed accumulators of the result (element e0 = (b, m, n .. n+7)) through the epilogue and stored:
+// the arithmetic and operation order of the MFMA kernels' epilogue passes. Shared by the reduction kernel and the
+// in-kernel finish below, so both give the same bits.
+template <int DT>
+__device__ __forceinline__ void store_oct(void* out, int64_t e0, const uint32_t* v, bool is_float) {
+  constexpr int OS = out_size<DT>();
+  uint32_t w[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) w[e] = out_bits<DT>(v[e], is_float);
+  char* p = (char*)out + e0 * OS;
+  if constexpr (OS == 4) {
+    *(u32x4*)p = u32x4{w[0], w[1], w[2], w[3]};
+    *(u32x4*)(p + 16) = u32x4{w[4], w[5], w[6], w[7]};
+  } else if constexpr (OS == 2) {
+    *(u32x4*)p = u32x4{w[0] | w[1] << 16, w[2] | w[3] << 16, w[4] | w[5] << 16, w[6] | w[7] << 16};
+  } else {
+    *(uint2*)p = uint2{w[0] | w[1] << 8 | w[2] << 16 | w[3] << 24, w[4] | w[5] << 8 | w[6] << 16 | w[7] << 24};
+  }
+}
+
+__device__ __forceinline__ void store_oct_any(void* out, int64_t e0, int dt, const uint32_t* v, bool is_float) {
+  switch (dt) {
+    case DT_F32: return store_oct<DT_F32>(out, e0, v, is_float);
+    case DT_S32: return store_oct<DT_S32>(out, e0, v, is_float);
+    case DT_BF16: return store_oct<DT_BF16>(out, e0, v, is_float);
+    case DT_F16: return store_oct<DT_F16>(out, e0, v, is_float);
+    case DT_F8E4M3FN: return store_oct<DT_F8E4M3FN>(out, e0, v, is_float);
+    default:
+#pragma unroll
+      for (int e = 0; e < 8; ++e) store_bits(out, e0 + e, dt, v[e], is_float);
+  }
+}
+
+
+template <bool INT, bool DUAL>
+__device__ __forceinline__ void splitk_epilogue_oct(const GemmArgs& G, int64_t e0, int b, int m, int n, uint32_t (&v)[8],
+                                                    const uint32_t (&v2)[8]) {
+  uint32_t raw[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) raw[e] = v[e];
+  bool is_float = !INT;
+  if (G.epilogue == EPI_SCALE) {
+    float rs = G.alpha;
+    if (G.row) rs *= G.row[(int64_t)b * G.row_sb + (int64_t)m * G.row_sm];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float cs = G.col ? G.col[(int64_t)b * G.col_sb + (int64_t)(n + e) * G.col_sn] : 1.0f;
+      float x = INT ? (float)(int32_t)v[e] : __uint_as_float(v[e]);
+      x = x * rs * cs;
+      if (G.mid_round) x = G.mid_round == DT_BF16 ? bf16_bits_to_f32(f32_to_bf16_bits(x)) : (float)(_Float16)x;
+      v[e] = __float_as_uint(x);
+    }
+    is_float = true;
+  } else if (DUAL && G.epilogue == EPI_SWIGLU) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float c1 = G.col ? G.col[(int64_t)b * G.col_sb + (int64_t)(n + e) * G.col_sn] : 1.0f;
+      const float c2 = G.col2 ? G.col2[(int64_t)b * G.col2_sb + (int64_t)(n + e) * G.col2_sn] : 1.0f;
+      const float a = __uint_as_float(v[e]) * c1;
+      const float u = __uint_as_float(v2[e]) * c2;
+      const float lg = 1.0f / (1.0f + expf(-a));
+      float x = (a * lg) * u;
+      if (G.mid_round) x = G.mid_round == DT_BF16 ? bf16_bits_to_f32(f32_to_bf16_bits(x)) : (float)(_Float16)x;
+      v[e] = __float_as_uint(x);
+    }
+    is_float = true;
+  }
+  store_oct_any(G.out_ptr[0], e0, G.out_dtype[0], v, is_float);
+  if (G.epilogue == EPI_SCALE && G.raw_out) store_oct_any(G.out_ptr[1], e0, G.out_dtype[1], raw, !INT);
+}
+
+// The K range that finishes a BM×BN tile last: sums the S ranges' partial sums in range order (the reduction
+// kernel's order) and applies the epilogue, eight consecutive elements per thread and step, with the loads of
+// 16 / S steps in flight together.
+template <bool INT, int S, int BM, int BN, int THREADS>
+__device__ __forceinline__ void splitk_finish_tile(const GemmArgs& G, int b, int m0, int n0, int tid) {
+  constexpr int OCTS = BM * BN / 8, PER = OCTS / THREADS, B0 = S >= 16 ? 1 : 16 / S, BATCH = PER < B0 ? PER : B0;
+  static_assert(OCTS % THREADS == 0 && PER % BATCH == 0, "finish layout");
+  const int64_t slice = (int64_t)G.batch * G.M * G.N;
+  const uint32_t* ws = (const uint32_t*)G.ws;
+  auto add = [](uint32_t a, uint32_t x) {
+    return INT ? (uint32_t)((int32_t)a + (int32_t)x) : __float_as_uint(__uint_as_float(a) + __uint_as_float(x));
+  };
+  for (int o0 = 0; o0 < PER; o0 += BATCH) {
+    u32x4 w[BATCH][S][2];
+    int64_t e0[BATCH];
+#pragma unroll
+    for (int q = 0; q < BATCH; ++q) {
+      const int oc = tid + (o0 + q) * THREADS;
+      const int r = oc / (BN / 8), c = (oc % (BN / 8)) * 8;
+      e0[q] = ((int64_t)b * G.M + m0 + r) * G.N + n0 + c;
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        w[q][s][0] = load_coherent16(ws + s * slice + e0[q]);
+        w[q][s][1] = load_coherent16(ws + s * slice + e0[q] + 4);
+      }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int q = 0; q < BATCH; ++q)
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        asm volatile("" : "+v"(w[q][s][0]));
+        asm volatile("" : "+v"(w[q][s][1]));
+      }
+#pragma unroll
+    for (int q = 0; q < BATCH; ++q) {
+      uint32_t v[8];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        v[4 * h] = w[q][0][h].x, v[4 * h + 1] = w[q][0][h].y, v[4 * h + 2] = w[q][0][h].z, v[4 * h + 3] = w[q][0][h].w;
+      }
+#pragma unroll
+      for (int s = 1; s < S; ++s)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          v[4 * h] = add(v[4 * h], w[q][s][h].x), v[4 * h + 1] = add(v[4 * h + 1], w[q][s][h].y);
+          v[4 * h + 2] = add(v[4 * h + 2], w[q][s][h].z), v[4 * h + 3] = add(v[4 * h + 3], w[q][s][h].w);
+        }
+      const int oc = tid + (o0 + q) * THREADS;
+      splitk_epilogue_oct<INT, false>(G, e0[q], b, m0 + oc / (BN / 8), n0 + (oc % (BN / 8)) * 8, v, v);
+    }
   }
 }
 
@@ -1126,15 +1266,47 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_mfma_kernel(const GemmArgs 
       constexpr int PDT = M::INT ? DT_S32 : DT_F32;
       const int64_t slice = (int64_t)G.batch * G.M * G.N * 4;
       char* ws = (char*)G.ws + (int64_t)split * C::NB * slice;
-      epi_pass<EPI_STORE, PDT, M::INT, false, C::WTN, PITCH, EPI_ROWS * 32>(G, ws, b, em0, en0, patch, nullptr, lane);
-      if constexpr (DUAL)
-        epi_pass<EPI_STORE, PDT, M::INT, false, C::WTN, PITCH, EPI_ROWS * 32>(G, ws + slice, b, em0, en0, patch + REGION,
-                                                                             nullptr, lane);
+      if (G.tile_counters) {  // read back by the range that finishes the tile: device-scope stores
+        epi_pass<EPI_STORE, PDT, M::INT, false, C::WTN, PITCH, EPI_ROWS * 32, false, true>(G, ws, b, em0, en0, patch,
+                                                                                          nullptr, lane);
+      } else {
+        epi_pass<EPI_STORE, PDT, M::INT, false, C::WTN, PITCH, EPI_ROWS * 32>(G, ws, b, em0, en0, patch, nullptr, lane);
+        if constexpr (DUAL)
+          epi_pass<EPI_STORE, PDT, M::INT, false, C::WTN, PITCH, EPI_ROWS * 32>(G, ws + slice, b, em0, en0,
+                                                                               patch + REGION, nullptr, lane);
+      }
     } else {
       epi_round<M::INT, DUAL, C::WTN, PITCH, EPI_ROWS * 32, EDGE>(G, b, em0, en0, patch, patch + REGION, lane);
     }
     if constexpr (round + 1 < C::TM / EPI_ROWS) __asm__ __volatile__("" ::: "memory");  // reads before next writes
   });
+
+  // Split-K with arrival counters: once every thread's partial stores are complete at device scope, the workgroup
+  // counts its arrival at the tile; the last of the S ranges to arrive sums them all and applies the epilogue. No
+  // workgroup waits for another, and no cache is flushed or invalidated (the partials are written and read at
+  // device scope); the counter is back at zero when the launch ends.
+  if constexpr (!EDGE && !DUAL) {
+    if (G.splits > 1 && G.tile_counters) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      int* last = (int*)smem;
+      if (tid == 0) {
+        int32_t* cnt = G.tile_counters + ((int64_t)b * tiles_m + tm) * tiles_n + tn;
+        const int arrived = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
+        if (arrived == G.splits) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *last = arrived == G.splits;
+      }
+      __syncthreads();
+      if (*(volatile int*)last) {
+        switch (G.splits) {
+          case 2: splitk_finish_tile<M::INT, 2, BM, BN, C::THREADS>(G, b, m0, n0, tid); break;
+          case 4: splitk_finish_tile<M::INT, 4, BM, BN, C::THREADS>(G, b, m0, n0, tid); break;
+          case 8: splitk_finish_tile<M::INT, 8, BM, BN, C::THREADS>(G, b, m0, n0, tid); break;
+          case 16: splitk_finish_tile<M::INT, 16, BM, BN, C::THREADS>(G, b, m0, n0, tid); break;
+        }
+      }
+    }
+  }
 }
 
 

@@ -84,41 +84,11 @@ __global__ void __launch_bounds__(256) gemm_generic_kernel(const GemmArgs G) {
 
 // ------------------------------------------------------------------------------------------------ dispatch
 // ------------------------------------------------------------------------------------------------ split-K
-// Sums the K ranges' partial accumulators in range order and applies the epilogue, with the same per-element
-// arithmetic (and operation order) as the MFMA kernels' epilogue passes. Each thread owns 8 consecutive elements of
-// the result (N is a multiple of 16 on every split-K plan): S (the number of ranges, a template argument so that
+// Sums the K ranges' partial accumulators in range order and applies the epilogue (splitk_epilogue_oct, shared with
+// the in-kernel finish of the MFMA kernels, so the two give the same bits). Each thread owns 8 consecutive elements
+// of the result (N is a multiple of 16 on every split-K plan): S (the number of ranges, a template argument so that
 // every range's two 16-byte loads are in flight together) × 2 loads per accumulator set, then one vector store per
 // output.
-template <int DT>
-__device__ __forceinline__ void store_oct(void* out, int64_t e0, const uint32_t* v, bool is_float) {
-  constexpr int OS = out_size<DT>();
-  uint32_t w[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) w[e] = out_bits<DT>(v[e], is_float);
-  char* p = (char*)out + e0 * OS;
-  if constexpr (OS == 4) {
-    *(u32x4*)p = u32x4{w[0], w[1], w[2], w[3]};
-    *(u32x4*)(p + 16) = u32x4{w[4], w[5], w[6], w[7]};
-  } else if constexpr (OS == 2) {
-    *(u32x4*)p = u32x4{w[0] | w[1] << 16, w[2] | w[3] << 16, w[4] | w[5] << 16, w[6] | w[7] << 16};
-  } else {
-    *(uint2*)p = uint2{w[0] | w[1] << 8 | w[2] << 16 | w[3] << 24, w[4] | w[5] << 8 | w[6] << 16 | w[7] << 24};
-  }
-}
-
-__device__ __forceinline__ void store_oct_any(void* out, int64_t e0, int dt, const uint32_t* v, bool is_float) {
-  switch (dt) {
-    case DT_F32: return store_oct<DT_F32>(out, e0, v, is_float);
-    case DT_S32: return store_oct<DT_S32>(out, e0, v, is_float);
-    case DT_BF16: return store_oct<DT_BF16>(out, e0, v, is_float);
-    case DT_F16: return store_oct<DT_F16>(out, e0, v, is_float);
-    case DT_F8E4M3FN: return store_oct<DT_F8E4M3FN>(out, e0, v, is_float);
-    default:
-#pragma unroll
-      for (int e = 0; e < 8; ++e) store_bits(out, e0 + e, dt, v[e], is_float);
-  }
-}
-
 template <bool INT, bool DUAL, int S>
 __global__ void __launch_bounds__(256) splitk_reduce_kernel(const GemmArgs G) {
   const int64_t octs = (int64_t)G.batch * G.M * G.N / 8;
@@ -160,38 +130,7 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const GemmArgs G) {
           v2[4 * h + 2] = add(v2[4 * h + 2], w[s][1][h].z), v2[4 * h + 3] = add(v2[4 * h + 3], w[s][1][h].w);
         }
       }
-    uint32_t raw[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) raw[e] = v[e];
-    bool is_float = !INT;
-    if (G.epilogue == EPI_SCALE) {
-      float rs = G.alpha;
-      if (G.row) rs *= G.row[(int64_t)b * G.row_sb + (int64_t)m * G.row_sm];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float cs = G.col ? G.col[(int64_t)b * G.col_sb + (int64_t)(n + e) * G.col_sn] : 1.0f;
-        float x = INT ? (float)(int32_t)v[e] : __uint_as_float(v[e]);
-        x = x * rs * cs;
-        if (G.mid_round) x = G.mid_round == DT_BF16 ? bf16_bits_to_f32(f32_to_bf16_bits(x)) : (float)(_Float16)x;
-        v[e] = __float_as_uint(x);
-      }
-      is_float = true;
-    } else if (DUAL && G.epilogue == EPI_SWIGLU) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float c1 = G.col ? G.col[(int64_t)b * G.col_sb + (int64_t)(n + e) * G.col_sn] : 1.0f;
-        const float c2 = G.col2 ? G.col2[(int64_t)b * G.col2_sb + (int64_t)(n + e) * G.col2_sn] : 1.0f;
-        const float a = __uint_as_float(v[e]) * c1;
-        const float u = __uint_as_float(v2[e]) * c2;
-        const float lg = 1.0f / (1.0f + expf(-a));
-        float x = (a * lg) * u;
-        if (G.mid_round) x = G.mid_round == DT_BF16 ? bf16_bits_to_f32(f32_to_bf16_bits(x)) : (float)(_Float16)x;
-        v[e] = __float_as_uint(x);
-      }
-      is_float = true;
-    }
-    store_oct_any(G.out_ptr[0], e0, G.out_dtype[0], v, is_float);
-    if (G.epilogue == EPI_SCALE && G.raw_out) store_oct_any(G.out_ptr[1], e0, G.out_dtype[1], raw, !INT);
+    splitk_epilogue_oct<INT, DUAL>(G, e0, b, m, n, v, v2);
   }
 }
 
@@ -350,15 +289,19 @@ void launch_gemm(const GemmArgs& g, hipStream_t stream, hipEvent_t done) {
     const int splits = g.splits > 1 ? g.splits : 1;
     if (splits > 1 && (!g.ws || g.K % (splits * 16) || g.N % 16 || c.edge))
       fail(PJRT_Error_Code_INTERNAL, "split-K without a workspace, on partial tiles or with N not a multiple of 16");
+    if (splits > 1 && g.tile_counters && (g.dual || (splits & (splits - 1)) || splits > 16))
+      fail(PJRT_Error_Code_INTERNAL, "in-kernel split-K finish for a dual GEMM or " + std::to_string(splits) + " ranges");
     int64_t blocks = (int64_t)((g.M + c.bm - 1) / c.bm) * ((g.N + c.bn - 1) / c.bn) * g.batch * splits;
     if (blocks > INT32_MAX) fail(PJRT_Error_Code_UNIMPLEMENTED, "too many GEMM tiles");
     void* args[] = {(void*)&g};
-    hipEvent_t main_done = splits > 1 ? nullptr : done;  // split-K: the reduction launch carries it
+    // split-K finished by a reduction launch: that launch carries the completion event
+    const bool reduce = splits > 1 && !g.tile_counters;
+    hipEvent_t main_done = reduce ? nullptr : done;
     hipEvent_t start = take_start();
     e = main_done || start ? hipExtLaunchKernel(c.fn, dim3((unsigned)blocks), dim3(c.threads), args, (size_t)c.lds,
                                                 stream, start, main_done, 0)
                            : hipLaunchKernel(c.fn, dim3((unsigned)blocks), dim3(c.threads), args, (size_t)c.lds, stream);
-    if (e == hipSuccess && splits > 1) {
+    if (e == hipSuccess && reduce) {
       if (g.acc_is_int) launch_splitk_reduce<true, false>(g, stream, done);
       else if (g.dual) launch_splitk_reduce<false, true>(g, stream, done);
       else launch_splitk_reduce<false, false>(g, stream, done);
