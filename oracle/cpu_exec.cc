@@ -160,6 +160,13 @@ inline uint8_t f32_to_e4m3(float x) {
   const int code = dl < dh ? lo : dh < dl ? hi : ((lo & 1) ? hi : lo);
   return sign | (uint8_t)code;
 }
+// the same encode of every bf16 value, by its bits (a bf16-rounded value is converted with one table load)
+uint8_t bf16_e4m3_table[65536];
+struct Bf16E4m3Init {
+  Bf16E4m3Init() {
+    for (int v = 0; v < 65536; ++v) bf16_e4m3_table[v] = f32_to_e4m3(bf16_to_f32((uint16_t)v));
+  }
+} bf16_e4m3_init;
 
 // rsqrt(Σx²·inv_d + eps) of one bf16 row with the graph's f32 roundings: the squares (exact in f32 for bf16 values)
 // summed in double and rounded once, then the f32 multiply, add and rsqrt.
@@ -376,7 +383,7 @@ void cpu_rmsnorm_f8(const uint16_t* x, const uint16_t* w, uint8_t* out, int M, i
     const uint16_t* xr = x + (int64_t)m * D;
     const float r = row_rsqrt(xr, D, inv_d, eps);
     for (int d = 0; d < D; ++d)
-      out[(int64_t)m * D + d] = f32_to_e4m3(bf16_to_f32(f32_to_bf16((bf16_to_f32(xr[d]) * r) * bf16_to_f32(w[d]))));
+      out[(int64_t)m * D + d] = bf16_e4m3_table[f32_to_bf16((bf16_to_f32(xr[d]) * r) * bf16_to_f32(w[d]))];
   }
 }
 

@@ -205,7 +205,10 @@ def quantize_columns_e4m3(w: np.ndarray):
 def c5_swiglu_fp8(m=512, d=4096, f=14336, seed=0xC5, activations="bf16", weights="convert") -> Workload:
     """Llama-style SwiGLU MLP with f8E4M3FN weights (per-output-column f32 scales): BASELINE.json's C5.
 
-    RMSNorm(x)·w (eps 1e-6) in f32 → bf16; silu(x·W_gate)·(x·W_up) with f32 accumulation; · W_down → bf16.
+    RMSNorm(x)·w (eps 1e-6) in f32 → bf16; silu(x·W_gate)·(x·W_up) with f32 accumulation, rounded to bf16 (`%24`);
+    · W_down → bf16. The bf16 rounding of the SwiGLU product before W_down is the Llama-style reading (BASELINE.json
+    names no dtype for that intermediate); it makes the down projection a bf16 × f8E4M3FN contraction like the other
+    two.
 
     activations="bf16" (the default, C5 as BASELINE.json states it): bf16 activations times f8E4M3FN weights. With
     weights="convert" each weight is widened by an explicit `convert` f8E4M3FN → bf16 feeding a bf16 dot_general;

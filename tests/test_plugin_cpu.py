@@ -430,14 +430,16 @@ def test_malformed_serialized_executable_is_invalid_argument(compile_client, mut
 
 
 def test_memory_statistics_and_memory_kinds(compile_client):
-    # C1 plans an 8-range split-K: the f32 partial sums are the executable's only temporary (8 × 256 × 256 × 4 B)
+    # C1 plans an 8-range split-K: the f32 partial sums are the executable's only temporary (8 × 256 × 256 × 4 B);
+    # its one constant is the zero-initialised arrival counter per 64×64 output tile of the in-kernel finish (16 × 4 B)
     e = compile_client.compile(pjrt.Program.mlir(configs.c1_f32_dot().program)).executable()
     st = e.memory_statistics()
     assert st["argument_size_in_bytes"] == 2 * 256 * 512 * 4
     assert st["output_size_in_bytes"] == 256 * 256 * 4
     assert st["temp_size_in_bytes"] == 8 * 256 * 256 * 4
     assert st["generated_code_size_in_bytes"] == 0 and st["alias_size_in_bytes"] == 0
-    assert st["peak_memory_in_bytes"] == st["argument_size_in_bytes"] + st["output_size_in_bytes"] + st["temp_size_in_bytes"]
+    assert st["peak_memory_in_bytes"] == (st["argument_size_in_bytes"] + st["output_size_in_bytes"] +
+                                          st["temp_size_in_bytes"] + 16 * 4)
     assert e.input_memory_kinds() == ["device", "device"]
     assert e.output_memory_kinds() == ["device"]
 
