@@ -472,6 +472,24 @@ typedef struct PJRT_Client_CreateUninitializedBuffer_Args {
 } PJRT_Client_CreateUninitializedBuffer_Args;
 typedef PJRT_Error* PJRT_Client_CreateUninitializedBuffer(PJRT_Client_CreateUninitializedBuffer_Args* args);
 
+/* A buffer that holds an error instead of data (crates/ryft-pjrt/src/buffers.rs:2338-2430, 3415-3430). */
+typedef struct PJRT_Client_CreateErrorBuffer_Args {
+  PJRT_ARGS_HEAD;
+  PJRT_Client* client;
+  PJRT_Error_Code error_code;
+  const char* error_message;
+  size_t error_message_size;
+  const int64_t* shape_dims;
+  size_t shape_num_dims;
+  PJRT_Buffer_Type shape_element_type;
+  PJRT_Buffer_MemoryLayout* shape_layout;
+  PJRT_Memory* memory;
+  PJRT_Buffer* buffer; /* out */
+  const PJRT_NamedValue* payload;
+  size_t payload_size;
+} PJRT_Client_CreateErrorBuffer_Args;
+typedef PJRT_Error* PJRT_Client_CreateErrorBuffer(PJRT_Client_CreateErrorBuffer_Args* args);
+
 typedef struct PJRT_Buffer_Destroy_Args {
   PJRT_ARGS_HEAD;
   PJRT_Buffer* buffer;
@@ -737,6 +755,21 @@ typedef struct PJRT_Device_MemoryStats_Args {
   bool peak_pool_bytes_is_set;
 } PJRT_Device_MemoryStats_Args;
 typedef PJRT_Error* PJRT_Device_MemoryStats(PJRT_Device_MemoryStats_Args* args);
+
+/* Poisons the earliest unfinished execution with this launch id on the device (crates/ryft-pjrt/src/devices.rs:257-300,
+   987-998): its results turn into error buffers carrying the given error. */
+typedef struct PJRT_Device_PoisonExecution_Args {
+  PJRT_ARGS_HEAD;
+  PJRT_Device* device;
+  int32_t launch_id;
+  PJRT_Error_Code error_code;
+  const char* error_message;
+  size_t error_message_size;
+  bool poisoned; /* out */
+  const PJRT_NamedValue* payload;
+  size_t payload_size;
+} PJRT_Device_PoisonExecution_Args;
+typedef PJRT_Error* PJRT_Device_PoisonExecution(PJRT_Device_PoisonExecution_Args* args);
 
 /* ---------------------------------------------------------------- memories (memories.rs:195-330) */
 typedef struct PJRT_Memory_Id_Args {
@@ -1368,10 +1401,10 @@ typedef struct PJRT_Api {
   PJRT_NOSLOT(PJRT_Client_CreateAliasBuffer);
   PJRT_NOSLOT(PJRT_Client_FulfillAliasBuffer);
   PJRT_SLOT(PJRT_LoadedExecutable_GetDeviceAssignment);
-  PJRT_NOSLOT(PJRT_Client_CreateErrorBuffer);
+  PJRT_SLOT(PJRT_Client_CreateErrorBuffer);
   PJRT_NOSLOT(PJRT_AsyncHostToDeviceTransferManager_TransferLiteral);
   PJRT_NOSLOT(PJRT_Buffer_CopyRawToHostFuture);
-  PJRT_NOSLOT(PJRT_Device_PoisonExecution);
+  PJRT_SLOT(PJRT_Device_PoisonExecution);
   PJRT_NOSLOT(PJRT_Device_CreateAsyncTrackingEvent);
   PJRT_NOSLOT(PJRT_AsyncTrackingEvent_Destroy);
   PJRT_SLOT(PJRT_Executable_GetCompileOptions);
@@ -1415,6 +1448,12 @@ PJRT_ASSERT(offsetof(PJRT_Buffer_MemoryLayout, type) == 72, "PJRT_Buffer_MemoryL
 PJRT_ASSERT(sizeof(PJRT_Buffer_GetMemoryLayout_Args) == 104, "PJRT_Buffer_GetMemoryLayout_Args");
 PJRT_ASSERT(sizeof(PJRT_Client_BufferFromHostBuffer_Args) == 120, "PJRT_Client_BufferFromHostBuffer_Args");
 PJRT_ASSERT(offsetof(PJRT_Client_BufferFromHostBuffer_Args, type) == 32, "BufferFromHostBuffer.type");
+PJRT_ASSERT(sizeof(PJRT_Client_CreateErrorBuffer_Args) == 112, "PJRT_Client_CreateErrorBuffer_Args");
+PJRT_ASSERT(offsetof(PJRT_Client_CreateErrorBuffer_Args, shape_element_type) == 64, "CreateErrorBuffer.type");
+PJRT_ASSERT(offsetof(PJRT_Client_CreateErrorBuffer_Args, buffer) == 88, "CreateErrorBuffer.buffer");
+PJRT_ASSERT(sizeof(PJRT_Device_PoisonExecution_Args) == 72, "PJRT_Device_PoisonExecution_Args");
+PJRT_ASSERT(offsetof(PJRT_Device_PoisonExecution_Args, error_code) == 28, "PoisonExecution.error_code");
+PJRT_ASSERT(offsetof(PJRT_Device_PoisonExecution_Args, poisoned) == 48, "PoisonExecution.poisoned");
 PJRT_ASSERT(offsetof(PJRT_Client_BufferFromHostBuffer_Args, host_buffer_semantics) == 72, "semantics");
 PJRT_ASSERT(offsetof(PJRT_Client_BufferFromHostBuffer_Args, buffer) == 112, "BufferFromHostBuffer.buffer");
 PJRT_ASSERT(sizeof(PJRT_Buffer_ToHostBuffer_Args) == 56, "PJRT_Buffer_ToHostBuffer_Args");

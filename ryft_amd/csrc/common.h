@@ -54,9 +54,12 @@ bool dtype_from_pjrt(PJRT_Buffer_Type t, DType* out);
 
 // Errors inside the plugin are C++ exceptions carrying a PJRT error code; the C API boundary converts them to
 // PJRT_Error objects (crates/ryft-pjrt/src/errors.rs:76-180 reads them back).
+// An error may carry (name, value) payload strings, as PJRT_Error_ForEachPayload reports them.
+using Payload = std::vector<std::pair<std::string, std::string>>;
 struct Status : std::runtime_error {
   PJRT_Error_Code code;
-  Status(PJRT_Error_Code c, const std::string& m) : std::runtime_error(m), code(c) {}
+  Payload payload;
+  Status(PJRT_Error_Code c, const std::string& m, Payload p = {}) : std::runtime_error(m), code(c), payload(std::move(p)) {}
 };
 [[noreturn]] inline void fail(PJRT_Error_Code code, const std::string& msg) { throw Status(code, msg); }
 [[noreturn]] inline void invalid(const std::string& msg) { fail(PJRT_Error_Code_INVALID_ARGUMENT, msg); }

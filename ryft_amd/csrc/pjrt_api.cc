@@ -13,6 +13,7 @@
 #include <mutex>
 #include <string>
 
+#include "mlir_common.h"
 #include "ryft_mi355x.h"
 #include "runtime.h"
 
@@ -21,10 +22,11 @@ namespace ryft {
 struct ErrorObj {
   PJRT_Error_Code code;
   std::string message;
+  Payload payload;
 };
 
-PJRT_Error* make_pjrt_error(PJRT_Error_Code code, const std::string& msg) {
-  return reinterpret_cast<PJRT_Error*>(new ErrorObj{code, msg});
+PJRT_Error* make_pjrt_error(PJRT_Error_Code code, const std::string& msg, const Payload& payload) {
+  return reinterpret_cast<PJRT_Error*>(new ErrorObj{code, msg, payload});
 }
 
 }  // namespace ryft
@@ -41,7 +43,7 @@ H* to(T* p) { return reinterpret_cast<H*>(p); }
 #define API_TRY try {
 #define API_CATCH                                                                 \
   }                                                                               \
-  catch (const Status& s) { return make_pjrt_error(s.code, s.what()); }           \
+  catch (const Status& s) { return make_pjrt_error(s.code, s.what(), s.payload); }\
   catch (const std::bad_alloc&) {                                                 \
     return make_pjrt_error(PJRT_Error_Code_RESOURCE_EXHAUSTED, "host allocation failed"); \
   }                                                                               \
@@ -77,7 +79,12 @@ PJRT_Error* Error_GetCode(PJRT_Error_GetCode_Args* args) {
 }
 PJRT_Error* Error_ForEachPayload(PJRT_Error_ForEachPayload_Args* args) {
   NEED_ARGS(PJRT_Error_ForEachPayload_Args, user_arg);
-  return nullptr;  // errors carry no payload
+  const ErrorObj* e = reinterpret_cast<const ErrorObj*>(args->error);
+  if (!e || e->payload.empty()) return nullptr;
+  NEED(args->visitor, "visitor");
+  for (const auto& kv : e->payload)
+    args->visitor(kv.first.data(), kv.first.size(), kv.second.data(), kv.second.size(), args->user_arg);
+  return nullptr;
 }
 
 // ------------------------------------------------------------------------------------------------ plugin
@@ -155,7 +162,7 @@ PJRT_Error* Event_Error(PJRT_Event_Error_Args* args) {
   auto& st = from<Event>(args->event)->state;
   std::lock_guard<std::mutex> lk(st->mu);
   if (!st->ready) return make_pjrt_error(PJRT_Error_Code_FAILED_PRECONDITION, "event is not ready");
-  return st->code == PJRT_Error_Code_OK ? nullptr : make_pjrt_error(st->code, st->message);
+  return st->code == PJRT_Error_Code_OK ? nullptr : make_pjrt_error(st->code, st->message, st->payload);
 }
 PJRT_Error* Event_Await(PJRT_Event_Await_Args* args) {
   NEED_ARGS(PJRT_Event_Await_Args, event);
@@ -164,7 +171,7 @@ PJRT_Error* Event_Await(PJRT_Event_Await_Args* args) {
   auto& st = from<Event>(args->event)->state;
   st->wait();
   std::lock_guard<std::mutex> lk(st->mu);
-  if (st->code != PJRT_Error_Code_OK) return make_pjrt_error(st->code, st->message);
+  if (st->code != PJRT_Error_Code_OK) return make_pjrt_error(st->code, st->message, st->payload);
   API_CATCH
 }
 PJRT_Error* Event_OnReady(PJRT_Event_OnReady_Args* args) {
@@ -393,6 +400,71 @@ PJRT_Error* Client_CreateUninitializedBuffer(PJRT_Client_CreateUninitializedBuff
   API_CATCH
 }
 
+// (name, value) payload strings from PJRT_NamedValues; non-string values are printed in decimal
+Payload payload_from(const PJRT_NamedValue* v, size_t n) {
+  Payload out;
+  if (n && !v) invalid("payload is null");
+  for (size_t i = 0; i < n; ++i) {
+    if (v[i].name_size && !v[i].name) invalid("payload name is null");
+    std::string name(v[i].name ? v[i].name : "", v[i].name_size), value;
+    switch (v[i].type) {
+      case PJRT_NamedValue_kString:
+        if (v[i].value_size && !v[i].string_value) invalid("payload value is null");
+        value.assign(v[i].string_value ? v[i].string_value : "", v[i].value_size);
+        break;
+      case PJRT_NamedValue_kInt64: value = std::to_string(v[i].int64_value); break;
+      case PJRT_NamedValue_kFloat: value = std::to_string(v[i].float_value); break;
+      case PJRT_NamedValue_kBool: value = v[i].bool_value ? "true" : "false"; break;
+      case PJRT_NamedValue_kInt64List:
+        for (size_t k = 0; k < v[i].value_size; ++k)
+          value += (k ? "," : "") + std::to_string(v[i].int64_array_value[k]);
+        break;
+      default: invalid("payload value of unknown type " + std::to_string((int)v[i].type));
+    }
+    out.emplace_back(std::move(name), std::move(value));
+  }
+  return out;
+}
+
+// The error a caller hands in (message bytes, code, payload), checked to be an error.
+Status caller_error(PJRT_Error_Code code, const char* msg, size_t msg_size, const PJRT_NamedValue* payload,
+                    size_t payload_size) {
+  if (code == PJRT_Error_Code_OK) invalid("error code is OK");
+  if (msg_size && !msg) invalid("error message is null");
+  return Status(code, std::string(msg ? msg : "", msg_size), payload_from(payload, payload_size));
+}
+
+PJRT_Error* Client_CreateErrorBuffer(PJRT_Client_CreateErrorBuffer_Args* args) {
+  NEED_ARGS(PJRT_Client_CreateErrorBuffer_Args, buffer);
+  NEED(args->client, "client");
+  NEED(args->memory, "memory");
+  API_TRY
+  Client* c = from<Client>(args->client);
+  // the payload fields follow `buffer`: a caller's older, shorter struct has none
+  const bool has_payload = args->struct_size >= offsetof(PJRT_Client_CreateErrorBuffer_Args, payload_size) +
+                                                     sizeof(args->payload_size);
+  Status err = caller_error(args->error_code, args->error_message, args->error_message_size,
+                            has_payload ? args->payload : nullptr, has_payload ? args->payload_size : 0);
+  DType t;
+  if (!dtype_from_pjrt(args->shape_element_type, &t))
+    return make_pjrt_error(PJRT_Error_Code_UNIMPLEMENTED, "unsupported element type");
+  if (args->shape_num_dims && !args->shape_dims) invalid("shape_dims is null");
+  if (args->shape_layout && !(args->shape_layout->type == PJRT_Buffer_MemoryLayout_Type_Tiled &&
+                              args->shape_layout->tiled.num_tiles == 0))
+    return make_pjrt_error(PJRT_Error_Code_UNIMPLEMENTED, "custom device layouts are not supported");
+  std::vector<int64_t> dims(args->shape_dims, args->shape_dims + args->shape_num_dims);
+  check_tensor_shape(dims);
+  auto b = std::make_unique<Buffer>();
+  b->client = c;
+  b->device = device_for(c, nullptr, args->memory);
+  b->dtype = t;
+  b->dims = std::move(dims);
+  for (int i = (int)b->dims.size() - 1; i >= 0; --i) b->minor_to_major.push_back(i);
+  b->ready = error_event(err);  // no device memory: every consumer fails with the error
+  args->buffer = to<PJRT_Buffer>(b.release());
+  API_CATCH
+}
+
 // ------------------------------------------------------------------------------------------------ devices
 PJRT_Error* DeviceDescription_Id(PJRT_DeviceDescription_Id_Args* args) {
   NEED_ARGS(PJRT_DeviceDescription_Id_Args, id);
@@ -467,6 +539,15 @@ PJRT_Error* Device_DefaultMemory(PJRT_Device_DefaultMemory_Args* args) {
   NEED(args->device, "device");
   args->memory = to<PJRT_Memory>(from<Device>(args->device)->default_memory);
   return nullptr;
+}
+PJRT_Error* Device_PoisonExecution(PJRT_Device_PoisonExecution_Args* args) {
+  NEED_ARGS(PJRT_Device_PoisonExecution_Args, payload_size);
+  NEED(args->device, "device");
+  API_TRY
+  Status err = caller_error(args->error_code, args->error_message, args->error_message_size, args->payload,
+                            args->payload_size);
+  args->poisoned = poison_execution(from<Device>(args->device), args->launch_id, err);
+  API_CATCH
 }
 PJRT_Error* Device_MemoryStats(PJRT_Device_MemoryStats_Args* args) {
   NEED_ARGS(PJRT_Device_MemoryStats_Args, peak_pool_bytes_is_set);
@@ -851,7 +932,7 @@ PJRT_Error* LoadedExecutable_Execute(PJRT_LoadedExecutable_Execute_Args* args) {
     if (!argv && args->num_args) return make_pjrt_error(PJRT_Error_Code_INVALID_ARGUMENT, "argument list is null");
     const PJRT_ExecuteOptions* o = args->options;
     EventPtr done = execute(le, dev, argv, args->num_args, &outs, o ? o->non_donatable_input_indices : nullptr,
-                            o ? o->num_non_donatable_input_indices : 0);
+                            o ? o->num_non_donatable_input_indices : 0, o ? o->launch_id : 0);
     for (size_t o = 0; o < outs.size(); ++o) args->output_lists[d][o] = to<PJRT_Buffer>(outs[o]);
     if (args->device_complete_events) args->device_complete_events[d] = wrap_event(done);
   }
@@ -1195,6 +1276,7 @@ PJRT_Api make_api() {
   SET(Client_DefaultDeviceAssignment);
   SET(Client_BufferFromHostBuffer);
   SET(Client_CreateUninitializedBuffer);
+  SET(Client_CreateErrorBuffer);
   SET(DeviceDescription_Id);
   SET(DeviceDescription_ProcessIndex);
   SET(DeviceDescription_Attributes);
@@ -1207,6 +1289,7 @@ PJRT_Api make_api() {
   SET(Device_AddressableMemories);
   SET(Device_DefaultMemory);
   SET(Device_MemoryStats);
+  SET(Device_PoisonExecution);
   SET(Memory_Id);
   SET(Memory_Kind);
   SET(Memory_Kind_Id);

@@ -26,8 +26,6 @@ hipEvent_t& pending_start() {
 }
 
 
-PJRT_Error* make_pjrt_error(PJRT_Error_Code code, const std::string& msg);  // pjrt_api.cc
-
 // ------------------------------------------------------------------------------------------------ events
 EventState::~EventState() {
   if (hip_event) (void)hipEventDestroy(hip_event);
@@ -38,6 +36,7 @@ void EventState::set_ready(PJRT_Error_Code c, const std::string& msg) {
   {
     std::lock_guard<std::mutex> lk(mu);
     if (ready) return;
+    if (poisoned) c = code;  // the poison's error wins over the device work's own outcome
     if (c == PJRT_Error_Code_OK && on_complete) {
       try {
         on_complete();
@@ -53,7 +52,32 @@ void EventState::set_ready(PJRT_Error_Code c, const std::string& msg) {
     cbs.swap(callbacks);
   }
   cv.notify_all();
-  for (auto& cb : cbs) cb.first(code == PJRT_Error_Code_OK ? nullptr : make_pjrt_error(code, message), cb.second);
+  for (auto& cb : cbs)
+    cb.first(code == PJRT_Error_Code_OK ? nullptr : make_pjrt_error(code, message, payload), cb.second);
+}
+
+bool EventState::error_now(Status* out) {
+  std::lock_guard<std::mutex> lk(mu);
+  if (!(ready || poisoned) || code == PJRT_Error_Code_OK) return false;
+  *out = Status(code, message, payload);
+  return true;
+}
+
+bool EventState::poison(const Status& err) {
+  std::lock_guard<std::mutex> lk(mu);
+  if (ready || poisoned) return false;
+  poisoned = true;
+  code = err.code;
+  message = err.what();
+  payload = err.payload;
+  return true;
+}
+
+EventPtr error_event(const Status& err) {
+  auto e = std::make_shared<EventState>();
+  e->payload = err.payload;
+  e->set_ready(err.code, err.what());
+  return e;
 }
 
 void EventState::wait() {
@@ -445,10 +469,15 @@ Buffer* buffer_from_host(Client* c, Device* d, const void* data, DType t, const 
   return b.release();
 }
 
+// The error `b` carries (an error buffer, or the result of a poisoned execution), if any.
+static bool buffer_error(const Buffer* b, Status* err) { return b->ready && b->ready->error_now(err); }
+
 EventPtr buffer_to_host(Buffer* b, void* dst, size_t dst_size) {
   if (b->deleted) fail(PJRT_Error_Code_FAILED_PRECONDITION, "ToHostBuffer on a deleted buffer");
   size_t bytes = b->bytes();
   if (dst_size < bytes) invalid("ToHostBuffer: destination holds " + std::to_string(dst_size) + " bytes, need " + std::to_string(bytes));
+  Status err(PJRT_Error_Code_OK, "");
+  if (buffer_error(b, &err)) return error_event(err);
   Client* c = b->client;
   Device* d = b->device;
   if (bytes == 0) return ready_event();
@@ -475,6 +504,8 @@ EventPtr buffer_raw_to_host(Buffer* b, void* dst, int64_t offset, int64_t size) 
     invalid("CopyRawToHost: bytes [" + std::to_string(offset) + ", " + std::to_string(offset) + " + " +
             std::to_string(size) + ") are outside the buffer's " + std::to_string(bytes) + " bytes");
   if (size > 0 && !dst) invalid("CopyRawToHost: dst is null");
+  Status err(PJRT_Error_Code_OK, "");
+  if (buffer_error(b, &err)) return error_event(err);
   Client* c = b->client;
   Device* d = b->device;
   if (size == 0) return ready_event();
@@ -505,6 +536,11 @@ Buffer* copy_buffer(Buffer* src, Device* d) {
   b->dtype = src->dtype;
   b->dims = src->dims;
   b->minor_to_major = src->minor_to_major;
+  Status err(PJRT_Error_Code_OK, "");
+  if (buffer_error(src, &err)) {  // the copy of an error buffer is an error buffer
+    b->ready = error_event(err);
+    return b.release();
+  }
   b->mem = c->allocate(d, src->bytes());
   std::lock_guard<std::recursive_mutex> lk(d->launch_mu);
   HIP_CHECK(hipSetDevice(d->hip_ordinal));
@@ -718,7 +754,7 @@ bool enqueue_steps(Client* c, const Plan& plan, void* const* ptr, hipStream_t st
 }
 
 EventPtr execute(LoadedExecutable* le, Device* d, Buffer* const* args, size_t num_args, std::vector<Buffer*>* outputs,
-                 const int64_t* non_donatable, size_t num_non_donatable) {
+                 const int64_t* non_donatable, size_t num_non_donatable, int launch_id) {
   const int64_t host_begin = wall_clock_ns();
   Executable& exe = *le->exe;
   const Plan& plan = exe.plan;
@@ -734,6 +770,11 @@ EventPtr execute(LoadedExecutable* le, Device* d, Buffer* const* args, size_t nu
     if (b->dtype != t.dtype || b->dims != t.shape)
       invalid("argument " + std::to_string(i) + " has type " + TensorType{b->dtype, b->dims}.str() + " but the program expects " + t.str());
     if (b->device != d) invalid("argument " + std::to_string(i) + " lives on another device");
+  }
+  // an error buffer among the arguments fails the execution with its error
+  for (size_t i = 0; i < num_args; ++i) {
+    Status err(PJRT_Error_Code_OK, "");
+    if (buffer_error(args[i], &err)) throw err;
   }
   // donation (XLA's aliasing semantics): an argument aliased to a result is donated unless the caller marked it
   // non-donatable, in which case the result simply gets a buffer of its own
@@ -800,6 +841,23 @@ EventPtr execute(LoadedExecutable* le, Device* d, Buffer* const* args, size_t nu
     // completion worker.
     done->lazy_owner = c;
   }
+  {
+    // in-flight record for poison_execution: entries whose event is gone or ready are dropped from the front; the
+    // oldest beyond kMaxInflight are dropped too (on one in-order stream they have long finished)
+    constexpr size_t kMaxInflight = 1024;
+    std::lock_guard<std::mutex> lk(d->inflight_mu);
+    while (!d->inflight.empty()) {
+      EventPtr e = d->inflight.front().second.lock();
+      bool gone = !e;
+      if (e) {
+        std::lock_guard<std::mutex> el(e->mu);
+        gone = e->ready;
+      }
+      if (!gone && d->inflight.size() < kMaxInflight) break;
+      d->inflight.pop_front();
+    }
+    d->inflight.emplace_back(launch_id, done);
+  }
   outputs->clear();
   for (size_t i = 0; i < plan.output_slots.size(); ++i) {
     int s = plan.output_slots[i];
@@ -822,6 +880,23 @@ EventPtr execute(LoadedExecutable* le, Device* d, Buffer* const* args, size_t nu
     }
   if (profiler_sessions_active()) profiler_record_host("execute " + exe.name, host_begin, wall_clock_ns());
   return done;
+}
+
+bool poison_execution(Device* d, int launch_id, const Status& err) {
+  std::vector<EventPtr> cand;
+  {
+    std::lock_guard<std::mutex> lk(d->inflight_mu);
+    for (auto& e : d->inflight)
+      if (e.first == launch_id)
+        if (EventPtr p = e.second.lock()) cand.push_back(std::move(p));
+  }
+  // oldest first; poll() resolves executions whose device work has ended (without the device lock held: it may run
+  // OnReady callbacks)
+  for (EventPtr& e : cand) {
+    if (e->poll()) continue;
+    if (e->poison(err)) return true;
+  }
+  return false;
 }
 
 std::string kernel_timing_json(Client* c) {

@@ -29,6 +29,9 @@ namespace ryft {
 
 struct Client;
 
+// A PJRT_Error object (pjrt_api.cc); the caller owns it.
+PJRT_Error* make_pjrt_error(PJRT_Error_Code code, const std::string& msg, const Payload& payload = {});
+
 // ------------------------------------------------------------------------------------------------ events
 struct EventState {
   std::mutex mu;
@@ -36,6 +39,10 @@ struct EventState {
   bool ready = false;
   PJRT_Error_Code code = PJRT_Error_Code_OK;
   std::string message;
+  Payload payload;
+  // Set by PJRT_Device_PoisonExecution before the event is ready: it then turns ready with this error (code,
+  // message and payload above) whatever the device work's own outcome.
+  bool poisoned = false;
   std::vector<std::pair<PJRT_Event_OnReadyCallback, void*>> callbacks;
   hipEvent_t hip_event = nullptr;  // completion marker on the device stream (null for host events)
   std::function<void()> on_complete;  // host work run before the event turns ready (e.g. staging → user copy)
@@ -50,8 +57,15 @@ struct EventState {
   // Blocks until the event is ready; synchronizes its HIP event on the calling thread when it has one.
   void wait();
   bool poll();
+  // The error this event already carries — set, or poisoned and pending — if any (buffers defined by it are then
+  // error buffers: their consumers fail with it instead of reading their memory).
+  bool error_now(Status* out);
+  // Poisons a pending event with `err`; false if the event is already ready.
+  bool poison(const Status& err);
 };
 using EventPtr = std::shared_ptr<EventState>;
+// An event that is ready with `err` from the start.
+EventPtr error_event(const Status& err);
 
 struct Event {  // PJRT_Event
   EventPtr state;
@@ -119,6 +133,10 @@ struct Device {  // PJRT_Device and PJRT_DeviceDescription
   hipStream_t stream = nullptr;
   std::unique_ptr<DeviceAllocator> allocator;
   std::recursive_mutex launch_mu;  // serializes enqueue on the device stream
+  // Executions enqueued on this device and not yet seen finished, oldest first, by launch id
+  // (PJRT_ExecuteOptions.launch_id), for PJRT_Device_PoisonExecution.
+  std::mutex inflight_mu;
+  std::deque<std::pair<int, std::weak_ptr<EventState>>> inflight;
 };
 
 struct Memory {  // PJRT_Memory
@@ -276,9 +294,15 @@ std::shared_ptr<Executable> compile_program(Client* c, const std::string& code, 
                                             const std::string& options);
 // Enqueues one execution; fills outputs and returns the completion event. Arguments that the program aliases to a
 // result are donated unless their index is in `non_donatable`: the result takes over (or replaces) the argument's
-// device memory and the argument buffer is marked deleted.
+// device memory and the argument buffer is marked deleted. An argument that is an error buffer (made by
+// PJRT_Client_CreateErrorBuffer, or a result of a poisoned execution) fails the call with its error, before anything
+// is enqueued. The execution is recorded under `launch_id` for poison_execution.
 EventPtr execute(LoadedExecutable* le, Device* d, Buffer* const* args, size_t num_args, std::vector<Buffer*>* outputs,
-                 const int64_t* non_donatable = nullptr, size_t num_non_donatable = 0);
+                 const int64_t* non_donatable = nullptr, size_t num_non_donatable = 0, int launch_id = 0);
+// PJRT_Device_PoisonExecution: the earliest execution on `d` under `launch_id` that has not finished turns ready
+// with `err` when its device work ends (its results become error buffers at once); false when every such execution
+// has finished already. The device work itself runs to its end.
+bool poison_execution(Device* d, int launch_id, const Status& err);
 // Enqueues every step of `plan` on `st`, slot s living at ptr[s] (the caller has made the plan's device current).
 // `done` (optional) is recorded by the last kernel launch when it can; returns whether it was. With `prof`, each
 // step's first and last launch record timing events appended to c->timings; while a profiler session is started,

@@ -254,6 +254,14 @@ for _n, _f in {
                                               ("shape_num_dims", _sz), ("shape_element_type", C.c_uint),
                                               ("shape_layout", _vp), ("device", _vp), ("memory", _vp),
                                               ("buffer", _vp)],
+    "PJRT_Client_CreateErrorBuffer": [("client", _vp), ("error_code", C.c_uint), ("error_message", _vp),
+                                      ("error_message_size", _sz), ("shape_dims", C.POINTER(C.c_int64)),
+                                      ("shape_num_dims", _sz), ("shape_element_type", C.c_uint),
+                                      ("shape_layout", _vp), ("memory", _vp), ("buffer", _vp),
+                                      ("payload", C.POINTER(NamedValue)), ("payload_size", _sz)],
+    "PJRT_Device_PoisonExecution": [("device", _vp), ("launch_id", C.c_int32), ("error_code", C.c_uint),
+                                    ("error_message", _vp), ("error_message_size", _sz), ("poisoned", C.c_bool),
+                                    ("payload", C.POINTER(NamedValue)), ("payload_size", _sz)],
     "PJRT_Buffer_UnsafePointer": [("buffer", _vp), ("buffer_pointer", C.c_size_t)],
     "PJRT_Buffer_Destroy": [("buffer", _vp)],
     "PJRT_Buffer_ElementType": [("buffer", _vp), ("type", C.c_uint)],
@@ -535,6 +543,36 @@ class Api:
         return _named_values(a.attributes, a.num_attributes)
 
 
+def _named_value_array(items):
+    """A PJRT_NamedValue array of (name, value) pairs (bool, int, float, int list, else string), and the Python
+    objects that must outlive it (values.rs:146, NamedValue::to_c_api)."""
+    items = list(items)
+    keep = []
+    vals = (NamedValue * max(len(items), 1))()
+    for i, (k, v) in enumerate(items):
+        nv = vals[i]
+        nv.struct_size = C.sizeof(NamedValue)
+        kb = k.encode()
+        keep.append(kb)
+        nv.name = C.cast(C.c_char_p(kb), _vp)
+        nv.name_size = len(kb)
+        if isinstance(v, bool):
+            nv.type, nv.bool_value, nv.value_size = 4, v, 1
+        elif isinstance(v, int):
+            nv.type, nv.int64_value, nv.value_size = 1, v, 1
+        elif isinstance(v, float):
+            nv.type, nv.float_value, nv.value_size = 3, v, 1
+        elif isinstance(v, (list, tuple)):
+            arr = (C.c_int64 * len(v))(*v)
+            keep.append(arr)
+            nv.type, nv.int64_array_value, nv.value_size = 2, arr, len(v)
+        else:
+            sb = str(v).encode()
+            keep.append(sb)
+            nv.type, nv.string_value, nv.value_size = 0, C.cast(C.c_char_p(sb), _vp), len(sb)
+    return vals, keep
+
+
 def _named_values(ptr, n) -> Dict[str, object]:
     out: Dict[str, object] = {}
     for i in range(n):
@@ -683,6 +721,17 @@ class Device:
     def addressable_memories(self) -> List[Memory]:
         a = self.client.api.call("PJRT_Device_AddressableMemories", device=self.handle)
         return [Memory(self.client, a.memories[i]) for i in range(a.num_memories)]
+
+    def poison_execution(self, launch_id: int, error: PjrtError, payload: Optional[Dict[str, str]] = None) -> bool:
+        """Device::poison_execution(_with_payload) (devices.rs:257-300): the earliest unfinished execution on this
+        device under `launch_id` completes with `error` (its results become error buffers); False when it had
+        already finished."""
+        msg = error.message.encode()
+        vals, keep = _named_value_array((payload or {}).items())
+        a = self.client.api.call("PJRT_Device_PoisonExecution", device=self.handle, launch_id=int(launch_id),
+                                 error_code=int(error.code), error_message=C.cast(C.c_char_p(msg), _vp),
+                                 error_message_size=len(msg), payload=vals, payload_size=len(payload or {}))
+        return bool(a.poisoned)
 
 
 # ----------------------------------------------------------------------------------------------- events
@@ -1189,29 +1238,7 @@ class Client(_Owned):
     @staticmethod
     def _create(plugin: Plugin, options: Dict[str, object]) -> "Client":
         api = plugin.api()
-        keep = []
-        vals = (NamedValue * max(len(options), 1))()
-        for i, (k, v) in enumerate(options.items()):
-            nv = vals[i]
-            nv.struct_size = C.sizeof(NamedValue)
-            kb = k.encode()
-            keep.append(kb)
-            nv.name = C.cast(C.c_char_p(kb), _vp)
-            nv.name_size = len(kb)
-            if isinstance(v, bool):
-                nv.type, nv.bool_value, nv.value_size = 4, v, 1
-            elif isinstance(v, int):
-                nv.type, nv.int64_value, nv.value_size = 1, v, 1
-            elif isinstance(v, float):
-                nv.type, nv.float_value, nv.value_size = 3, v, 1
-            elif isinstance(v, (list, tuple)):
-                arr = (C.c_int64 * len(v))(*v)
-                keep.append(arr)
-                nv.type, nv.int64_array_value, nv.value_size = 2, arr, len(v)
-            else:
-                sb = str(v).encode()
-                keep.append(sb)
-                nv.type, nv.string_value, nv.value_size = 0, C.cast(C.c_char_p(sb), _vp), len(sb)
+        vals, keep = _named_value_array(options.items())
         a = api.call("PJRT_Client_Create", create_options=vals, num_options=len(options))
         return Client(plugin, a.client)
 
@@ -1352,6 +1379,21 @@ class Client(_Owned):
         a = self.api.call("PJRT_Client_CreateUninitializedBuffer", client=self.handle, shape_dims=dims_arr,
                           shape_num_dims=len(dims), shape_element_type=int(element_type), shape_layout=None,
                           device=None, memory=memory.handle)
+        return Buffer(self, a.buffer)
+
+    def error_buffer(self, error: PjrtError, element_type: BufferType, dims: Sequence[int],
+                     memory: Optional[Memory] = None, payload: Optional[Dict[str, str]] = None) -> Buffer:
+        """Client::error_buffer(_with_payload) (buffers.rs:2321-2392): a buffer of the given type and dimensions that
+        holds `error` instead of data; its ready event, copies to host and executions that take it fail with it."""
+        if memory is None:
+            memory = self.addressable_devices()[0].default_memory()
+        dims_arr = (C.c_int64 * max(len(dims), 1))(*dims)
+        msg = error.message.encode()
+        vals, keep = _named_value_array((payload or {}).items())
+        a = self.api.call("PJRT_Client_CreateErrorBuffer", client=self.handle, error_code=int(error.code),
+                          error_message=C.cast(C.c_char_p(msg), _vp), error_message_size=len(msg),
+                          shape_dims=dims_arr, shape_num_dims=len(dims), shape_element_type=int(element_type),
+                          shape_layout=None, memory=memory.handle, payload=vals, payload_size=len(payload or {}))
         return Buffer(self, a.buffer)
 
     # --- plugin extension: kernel timing on the device stream

@@ -54,6 +54,24 @@ def test_api_table(plugin):
     assert e.value.code == pjrt.ErrorCode.UNIMPLEMENTED
 
 
+def test_failure_propagation_slots(plugin, compile_client):
+    # error buffers and poisoned executions (buffers.rs:2321-2430, devices.rs:257-300): both slots are filled, the
+    # args structs the Python mirror declares have the sizes the header asserts, and a compile-only client (no
+    # memory to place the buffer in) rejects an error buffer without a memory
+    api = plugin.api()
+    assert api.fn("PJRT_Client_CreateErrorBuffer") is not None
+    assert api.fn("PJRT_Device_PoisonExecution") is not None
+    assert ctypes.sizeof(pjrt.A["PJRT_Client_CreateErrorBuffer"]) == 112
+    assert ctypes.sizeof(pjrt.A["PJRT_Device_PoisonExecution"]) == 72
+    dims = (ctypes.c_int64 * 1)(4)
+    msg = b"boom"
+    with pytest.raises(pjrt.PjrtError) as e:
+        api.call("PJRT_Client_CreateErrorBuffer", client=compile_client.handle, error_code=int(pjrt.ErrorCode.ABORTED),
+                 error_message=ctypes.cast(ctypes.c_char_p(msg), ctypes.c_void_p), error_message_size=len(msg),
+                 shape_dims=dims, shape_num_dims=1, shape_element_type=int(pjrt.BufferType.U8), memory=None)
+    assert e.value.code == pjrt.ErrorCode.INVALID_ARGUMENT and "memory" in e.value.message
+
+
 def test_plugin_attributes(plugin):
     attrs = plugin.attributes()
     assert attrs["stablehlo_current_version"] == [1, 16, 0]
