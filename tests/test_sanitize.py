@@ -3,7 +3,9 @@ bytecode front-ends, the planner and the CompileOptionsProto decoder (the bytes 
 PJRT_Client_Compile, crates/ryft-pjrt/src/programs.rs:1245-1263) built with -fsanitize=address,undefined
 (tests/sanitize/Makefile) and fed the test corpus — every config, edge, row, donation and manipulation program as
 text and as bytecode in each writer variant, and CompileOptions encodings — plus truncated and bit-flipped copies of
-every file (tests/sanitize/frontend_check.cc). Rejections are expected; a sanitizer report fails the test."""
+every file (tests/sanitize/frontend_check.cc). Rejections are expected; a sanitizer report fails the test. The whole
+host side of the plugin (runtime, C API, profiler included) is also built with -fsanitize=thread and driven from several
+threads at once (tests/sanitize/tsan_check.cc)."""
 import os
 import subprocess
 
@@ -75,3 +77,23 @@ def test_host_path_under_sanitizers(tmp_path):
     print(run.stdout[-2000:], run.stderr[-2000:])
     assert run.returncode == 0, run.stdout[-3000:] + run.stderr[-6000:]
     assert "frontend_check:" in run.stdout and "AddressSanitizer" not in run.stderr and "runtime error" not in run.stderr
+
+
+def test_c_api_from_several_threads_under_tsan(tmp_path):
+    """tests/sanitize/tsan_check.cc under ThreadSanitizer: compiles on four threads of one compile-only client beside
+    profiler sessions, and user events whose OnReady callbacks are registered from three threads while another
+    thread sets them and two more await them (each callback exactly once, with its event's outcome)."""
+    build = subprocess.run(["make", "-C", HERE, "-j8", "_build/tsan_check"], capture_output=True, text=True,
+                           timeout=1200)
+    assert build.returncode == 0, build.stdout[-3000:] + build.stderr[-3000:]
+    files = []
+    for name, text in _programs().items():
+        p = tmp_path / f"{name}.mlir"
+        p.write_text(text)
+        files.append(str(p))
+    env = dict(os.environ, TSAN_OPTIONS="halt_on_error=1:second_deadlock_stack=1")
+    run = subprocess.run([os.path.join(HERE, "_build", "tsan_check")] + files, capture_output=True, text=True,
+                         timeout=900, env=env)
+    print(run.stdout[-2000:], run.stderr[-2000:])
+    assert run.returncode == 0, run.stdout[-3000:] + run.stderr[-6000:]
+    assert "tsan_check:" in run.stdout and "ThreadSanitizer" not in run.stderr
