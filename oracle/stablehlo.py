@@ -256,6 +256,35 @@ def _eval_op(op: str, rest: str, env, dot_precision: str) -> Tuple[np.ndarray, s
             f = [int(v) for v in part.split(":")]
             sl.append(slice(f[0], f[1], f[2] if len(f) > 2 else 1))
         return np.asarray(x)[tuple(sl)].copy(), dt
+    if op in ("dynamic_slice", "dynamic_update_slice"):
+        # manipulation.rs:943-1130: the window starts at clamp(0, start_indices, shape(operand) - window) per
+        # dimension (window = slice_sizes, or the update's shape); dynamic_slice returns it, dynamic_update_slice
+        # returns the operand with the window replaced by the update
+        head = rest.split(":")[0]
+        names = re.findall(r"%[\w.$-]+", head)
+        x, dt = env[names[0]]
+        x = np.asarray(x)
+        upd = op == "dynamic_update_slice"
+        if upd:
+            u = np.asarray(env[names[1]][0])
+            win = list(u.shape)
+        else:
+            win = _ints(re.search(r"sizes\s*=\s*\[(.*?)\]", head).group(1))
+        starts = []
+        for nm_ in names[2 if upd else 1:]:
+            v, idt = env[nm_]
+            v = int(np.asarray(v).reshape(()))
+            if idt.startswith("ui"):  # unsigned: the stored value modulo 2^bits
+                v %= 1 << INT_BITS[idt]
+            starts.append(v)
+        assert len(starts) == x.ndim and len(win) == x.ndim
+        sl = tuple(slice(a, a + k) for a, k in ((min(max(v, 0), x.shape[d] - win[d]), win[d])
+                                                for d, v in enumerate(starts)))
+        if not upd:
+            return x[sl].copy(), dt
+        out = x.copy()
+        out[sl] = u
+        return out, dt
     if op == "concatenate":
         # manipulation.rs:778-822: the inputs one after another along `dim`, in operand order
         head = rest.split(":")[0]

@@ -41,7 +41,7 @@ enum class Op : uint8_t {
   // elementwise, ternary
   Select, Clamp,
   // data movement
-  BroadcastInDim, Transpose, Reshape, Iota, Slice, Concatenate, Pad,
+  BroadcastInDim, Transpose, Reshape, Iota, Slice, Concatenate, Pad, DynamicSlice, DynamicUpdateSlice,
   // contractions and reductions
   DotGeneral, Reduce,
 };
@@ -61,7 +61,7 @@ struct Node {
   TensorType type;
   std::vector<int> operands;
   // attributes (meaning depends on op)
-  std::vector<int64_t> dims;  // broadcast_dimensions / permutation / reduce dimensions
+  std::vector<int64_t> dims;  // broadcast_dimensions / permutation / reduce dimensions / dynamic_slice slice_sizes
   // slice: start / limit / stride per dim; pad: edge_padding_low / edge_padding_high / interior_padding
   std::vector<int64_t> lo, hi, step;
   int64_t axis = 0;  // concatenate dimension

@@ -212,4 +212,25 @@ struct AttnArgs {
   int64_t qs[4], ks[4], vs[4], os[4];
 };
 
+// ------------------------------------------------------------------------------------------------ dynamic windows
+// dynamic_slice / dynamic_update_slice (crates/ryft-mlir/src/dialects/stable_hlo/operations/manipulation.rs:943-1130):
+// a window of win[] elements of a row-major tensor of shape[], at start indices read from device memory (one 0-d
+// integer tensor per dimension, all of type idx_dtype) and clamped to [0, shape - win] per dimension.
+//   WIN_READ:  dst (row-major over win) = the window of src (shape)
+//   WIN_WRITE: the window of dst (shape) = src (row-major over win); dst's other elements are left as they are
+#define WIN_MAX_RANK 6
+enum WinMode : int32_t { WIN_READ = 0, WIN_WRITE = 1 };
+struct WindowArgs {
+  const void* src;
+  void* dst;
+  const void* idx[WIN_MAX_RANK];
+  int32_t idx_dtype;   // DType of the start indices
+  int32_t rank;
+  int32_t elem_bytes;  // 1, 2, 4 or 8
+  int32_t mode;        // WinMode
+  int64_t shape[WIN_MAX_RANK];
+  int64_t win[WIN_MAX_RANK];
+  int64_t total;       // elements of the window
+};
+
 }  // namespace ryft

@@ -597,6 +597,7 @@ class BytecodeParser {
         {"stablehlo.slice", {{"limit_indices", true, {BAttr::DENSE_ARRAY}}, {"start_indices", true, {BAttr::DENSE_ARRAY}},
                              {"strides", true, {BAttr::DENSE_ARRAY}}}},
         {"stablehlo.concatenate", {{"dimension", true, {BAttr::INT}}}},
+        {"stablehlo.dynamic_slice", {{"slice_sizes", true, {BAttr::DENSE_ARRAY}}}},
         {"stablehlo.pad", {{"edge_padding_high", true, {BAttr::DENSE_ARRAY}}, {"edge_padding_low", true, {BAttr::DENSE_ARRAY}},
                            {"interior_padding", true, {BAttr::DENSE_ARRAY}}}},
         {"stablehlo.compare",
@@ -946,6 +947,11 @@ class BytecodeParser {
           n.lo = int_list(op, "start_indices");
           n.hi = int_list(op, "limit_indices");
           n.step = int_list(op, "strides");
+        } else if (nm == "dynamic_slice") {
+          n.op = Op::DynamicSlice;
+          n.dims = int_list(op, "slice_sizes");
+        } else if (nm == "dynamic_update_slice") {
+          n.op = Op::DynamicUpdateSlice;
         } else if (nm == "concatenate") {
           n.op = Op::Concatenate;
           const BAttr& a = need(op, "dimension");

@@ -87,6 +87,8 @@ const char* op_name(Op op) {
     case Op::Slice: return "slice";
     case Op::Concatenate: return "concatenate";
     case Op::Pad: return "pad";
+    case Op::DynamicSlice: return "dynamic_slice";
+    case Op::DynamicUpdateSlice: return "dynamic_update_slice";
     case Op::Iota: return "iota";
     case Op::DotGeneral: return "dot_general";
     case Op::Reduce: return "reduce";
@@ -929,6 +931,12 @@ class Parser {
       n.lo = parse_int_list_text(get("start_indices"));
       n.hi = parse_int_list_text(get("limit_indices"));
       n.step = parse_int_list_text(get("strides"));
+    } else if (nm == "dynamic_slice") {
+      n.op = Op::DynamicSlice;
+      std::string sz = get("sizes");
+      n.dims = parse_int_list_text(sz.empty() ? get("slice_sizes") : sz);
+    } else if (nm == "dynamic_update_slice") {
+      n.op = Op::DynamicUpdateSlice;
     } else if (nm == "concatenate") {
       n.op = Op::Concatenate;
       std::string d = get("dim");
@@ -1181,6 +1189,35 @@ void validate_node(const Graph& g, Node& n) {
     case Op::Iota:
       if (n.iota_dim < 0 || n.iota_dim >= n.type.rank()) invalid("iota: dimension out of range");
       break;
+    case Op::DynamicSlice:
+    case Op::DynamicUpdateSlice: {
+      // manipulation.rs:943-1130: one 0-d start index per operand dimension, all of one integer type; the window
+      // (slice_sizes, or the update's shape) fits the operand; the result has the window's (dynamic_slice) or the
+      // operand's (dynamic_update_slice) type
+      const bool upd = n.op == Op::DynamicUpdateSlice;
+      const size_t first = upd ? 2 : 1;
+      if (n.operands.size() < first) invalid(std::string(op_name(n.op)) + ": missing operands");
+      const TensorType& x = opt(0);
+      const int r = x.rank();
+      need(first + (size_t)r);
+      const std::vector<int64_t>& win = upd ? opt(1).shape : n.dims;
+      if ((int)win.size() != r) invalid(std::string(op_name(n.op)) + ": the window must have one size per dimension");
+      for (int d = 0; d < r; ++d)
+        if (win[d] < 0 || win[d] > x.shape[d]) invalid(std::string(op_name(n.op)) + ": window larger than the operand");
+      const DType it = opt((int)first).dtype;
+      for (size_t i = first; i < n.operands.size(); ++i) {
+        const TensorType& t = opt((int)i);
+        const bool int_type = t.dtype == DType::S8 || t.dtype == DType::S16 || t.dtype == DType::S32 ||
+                              t.dtype == DType::S64 || t.dtype == DType::U8 || t.dtype == DType::U16 ||
+                              t.dtype == DType::U32 || t.dtype == DType::U64;
+        if (t.rank() != 0 || !int_type || t.dtype != it)
+          invalid(std::string(op_name(n.op)) + ": start indices must be 0-d tensors of one integer type");
+      }
+      if (upd && opt(1).dtype != x.dtype) invalid("dynamic_update_slice: update element type mismatch");
+      if (n.type.dtype != x.dtype || n.type.shape != (upd ? x.shape : win))
+        invalid(std::string(op_name(n.op)) + ": result type mismatch");
+      break;
+    }
     default:
       if (op_is_elementwise(n.op)) {
         switch (n.op) {

@@ -166,6 +166,10 @@ class Planner {
   bool dot_operand(int dot, int which, GemmOperand* op, int* slot, int force_copy);
   void emit_concatenate(int node, int target);
   void emit_pad(int node, int target);
+  void emit_dynamic_slice(int node, int target);
+  void emit_dynamic_update_slice(int node, int target);
+  void push_window_step(const char* name, int mode, int src, int dst, const std::vector<int>& idx,
+                        const TensorType& big, const std::vector<int64_t>& win, DType idx_dtype);
   void push_strided_step(ExprBuilder& b, const char* name, int out, int64_t out_offset,
                          const std::vector<int64_t>& out_strides, double in_bytes, double out_bytes);
   int canonical_copy(int node, const std::vector<int64_t>& order);
@@ -531,6 +535,12 @@ int Planner::materialize(int node, int target) {
     case Op::Pad:
       emit_pad(node, target);
       break;
+    case Op::DynamicSlice:
+      emit_dynamic_slice(node, target);
+      break;
+    case Op::DynamicUpdateSlice:
+      emit_dynamic_update_slice(node, target);
+      break;
     case Op::Reshape: {
       int s = materialize(n.operands[0]);
       if (target >= 0) {
@@ -677,6 +687,71 @@ void Planner::emit_concatenate(int node, int target) {
     }
     at += len;
   }
+  mat_[node] = out;
+}
+
+// One window step (kernels/k_window.hip): mode WIN_READ copies the window of `src` (a tensor of type `big`) into
+// `dst`, WIN_WRITE copies `src` into the window of `dst`; the window origin is read from the start-index slots `idx`.
+void Planner::push_window_step(const char* name, int mode, int src, int dst, const std::vector<int>& idx,
+                               const TensorType& big, const std::vector<int64_t>& win, DType idx_dtype) {
+  const int r = big.rank();
+  if (r > WIN_MAX_RANK) unimplemented(std::string(name) + " of rank " + std::to_string(r));
+  const size_t es = dtype_size(big.dtype);
+  if (es != 1 && es != 2 && es != 4 && es != 8)
+    unimplemented(std::string(name) + " of " + dtype_name(big.dtype) + " elements");
+  Step st{};
+  st.kind = Step::WINDOW;
+  st.name = name;
+  WindowArgs& w = st.win;
+  w.idx_dtype = (int32_t)idx_dtype;
+  w.rank = r;
+  w.elem_bytes = (int32_t)es;
+  w.mode = mode;
+  w.total = 1;
+  for (int d = 0; d < r; ++d) {
+    w.shape[d] = big.shape[d];
+    w.win[d] = win[d];
+    w.total *= win[d];
+  }
+  st.patches = {{offsetof(WindowArgs, src), src}, {offsetof(WindowArgs, dst), dst}};
+  for (int d = 0; d < r; ++d) st.patches.push_back({offsetof(WindowArgs, idx) + d * sizeof(void*), idx[d]});
+  st.bytes = 2.0 * (double)w.total * (double)es;
+  plan_.steps.push_back(std::move(st));
+}
+
+// dynamic_slice (manipulation.rs:943-1034): result = operand[clamp(0, start, shape - sizes) + index], the start
+// indices read on the device. The operand is materialized contiguously (views are copied first).
+void Planner::emit_dynamic_slice(int node, int target) {
+  const Node& n = g_.nodes[node];
+  const Node& xn = g_.nodes[n.operands[0]];
+  std::vector<int> idx;
+  for (size_t k = 1; k < n.operands.size(); ++k) idx.push_back(materialize(n.operands[k]));
+  const int src = materialize(n.operands[0]);
+  const int out = temp_or(target, n.type);
+  const DType it = xn.type.rank() ? g_.nodes[n.operands[1]].type.dtype : DType::S32;
+  push_window_step("dynamic_slice", WIN_READ, src, out, idx, xn.type, n.dims, it);
+  mat_[node] = out;
+}
+
+// dynamic_update_slice (manipulation.rs:1036-1130): the operand's values with the window at clamp(0, start, shape -
+// update shape) replaced by the update. The start indices and the update are computed first, then the operand is
+// copied (or computed) into the result and the update written over its window. When the operand is a donated
+// parameter whose buffer the result takes over, the copy is a no-op and only the window is written
+// (Planner::in_place).
+void Planner::emit_dynamic_update_slice(int node, int target) {
+  const Node& n = g_.nodes[node];
+  const Node& un = g_.nodes[n.operands[1]];
+  std::vector<int> idx;
+  for (size_t k = 2; k < n.operands.size(); ++k) idx.push_back(materialize(n.operands[k]));
+  const int upd = materialize(n.operands[1]);
+  const int out = temp_or(target, n.type);
+  // the operand's value is computed straight into the result only when nothing else reads it (the window write
+  // would change it under its other readers); otherwise it gets a slot of its own and is copied
+  const int xo = n.operands[0];
+  if (users_[xo].size() > 1 || results_.count(xo)) emit_copy(materialize(xo), 0, out, n.type.bytes());
+  else materialize(xo, out);
+  const DType it = n.type.rank() ? g_.nodes[n.operands[2]].type.dtype : DType::S32;
+  push_window_step("dynamic_update_slice", WIN_WRITE, upd, out, idx, n.type, un.type.shape, it);
   mat_[node] = out;
 }
 
@@ -1779,13 +1854,36 @@ void Planner::plan_aliasing() {
 bool Planner::in_place(int ps, int os) const {
   const auto& steps = plan_.steps;
   int writer = -1;
+  std::vector<int> windows;  // window writes over the first writer's result (dynamic_update_slice)
   for (size_t i = 0; i < steps.size(); ++i)
     for (auto& pt : steps[i].patches)
       if (pt.second == os) {
-        if (writer >= 0 && writer != (int)i) return false;
+        if (writer >= 0 && writer != (int)i) {
+          const Step& w = steps[i];
+          // a later window write into the result that reads neither the parameter nor the result elsewhere
+          const bool window = w.kind == Step::WINDOW && w.win.mode == WIN_WRITE && w.patches[1].second == os &&
+                              std::none_of(w.patches.begin(), w.patches.end(), [&](const std::pair<size_t, int>& q) {
+                                return q.second == ps || (q.second == os && q.first != offsetof(WindowArgs, dst));
+                              });
+          if (!window) return false;
+          if (windows.empty() || windows.back() != (int)i) windows.push_back((int)i);
+          continue;
+        }
         writer = (int)i;
       }
   if (writer < 0) return false;
+  if (!windows.empty()) {
+    // the result is the parameter's bytes with windows written over them: in place when the first writer is a
+    // whole-buffer copy of the parameter and nothing after it reads the parameter
+    const Step& c = steps[writer];
+    if (c.kind != Step::COPY || c.patches.size() != 2 || c.patches[0].second != ps || c.patches[1].second != os ||
+        c.copy.src_offset != 0 || c.copy.bytes != (int64_t)plan_.slots[os].type.bytes())
+      return false;
+    for (size_t i = writer + 1; i < steps.size(); ++i)
+      for (auto& pt : steps[i].patches)
+        if (pt.second == ps) return false;
+    return true;
+  }
   for (size_t i = writer + 1; i < steps.size(); ++i)
     for (auto& pt : steps[i].patches)
       if (pt.second == ps) return false;
@@ -1839,6 +1937,8 @@ std::string Plan::describe() const {
          << " instrs=" << s.row.prog.n_instr << " leaves=" << s.row.prog.n_leaves;
     } else if (s.kind == Step::ATTENTION) {
       os << " B=" << s.attn.B << " H=" << s.attn.H << " S=" << s.attn.Sq << " D=" << s.attn.D << " causal=" << s.attn.causal;
+    } else if (s.kind == Step::WINDOW) {
+      os << " window=" << s.win.total << " of rank " << s.win.rank;
     }
     os << " flops=" << s.flops << " bytes=" << s.bytes << "\n";
   }

@@ -17,13 +17,14 @@ struct Slot {
 };
 
 struct Step {
-  enum Kind { ELEMENTWISE, REDUCE, GEMM, ATTENTION, COPY, ROW } kind;
+  enum Kind { ELEMENTWISE, REDUCE, GEMM, ATTENTION, COPY, ROW, WINDOW } kind;
   std::string name;  // kernel family, for profiling ("gemm_bf16_mfma", "attention_fwd", ...)
   EwProgram ew;
   ReduceArgs red;
   GemmArgs gemm;
   AttnArgs attn;
   RowArgs row;
+  WindowArgs win;
   struct { int64_t bytes; int64_t src_offset; } copy;  // src_offset: bytes into the source slot
   // Pointer fields inside the args block that refer to slots: (byte offset of the pointer field, slot). The
   // field's initial value is a byte offset into the slot's buffer.
@@ -37,6 +38,7 @@ struct Step {
       case GEMM: return &gemm;
       case ATTENTION: return &attn;
       case ROW: return &row;
+      case WINDOW: return &win;
       default: return nullptr;
     }
   }

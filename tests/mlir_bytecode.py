@@ -195,6 +195,9 @@ def _parse_op(res: str, name: str, rest: str) -> Op:
         key = "broadcast_dimensions" if short == "broadcast_in_dim" else "permutation"
         kv = [x for x in items if x.startswith("dims")][0]
         attrs[key] = ("i64s", _ints(kv.split("=", 1)[1]))
+    if short == "dynamic_slice":
+        kv = [x for x in items if x.startswith("sizes")][0]
+        attrs["slice_sizes"] = ("i64s", _ints(kv.split("=", 1)[1]))
     if short == "concatenate":
         kv = [x for x in items if x.startswith("dim")][0]
         attrs["dimension"] = ("i64", int(kv.split("=", 1)[1]))
@@ -238,7 +241,7 @@ DECLARED = {
 }
 REQUIRED = {"function_type", "sym_name", "comparison_direction", "dot_dimension_numbers", "value", "iota_dimension",
             "broadcast_dimensions", "permutation", "dimensions", "start_indices", "limit_indices", "strides",
-            "dimension", "edge_padding_low", "edge_padding_high", "interior_padding"}
+            "dimension", "edge_padding_low", "edge_padding_high", "interior_padding", "slice_sizes"}
 
 
 class Writer:

@@ -13,6 +13,7 @@ import pytest
 
 from ryft_amd import configs, pjrt
 from tests import donation_programs, edge_programs, mlir_bytecode as mb, row_programs
+from tests import test_dynamic_window as dw
 from tests.test_bytecode import SLICE_CONCAT_PAD, VARIANTS
 
 HERE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "sanitize")
@@ -34,6 +35,8 @@ def _programs():
         "layernorm": row_programs.layernorm((8, 33)),
         "int_row_max": row_programs.int_row_max_gap((8, 64)),
         "slice_concatenate_pad": SLICE_CONCAT_PAD,
+        "dynamic_slice": dw.ds_program((5, 7, 9), (2, 3, 4), dt="bf16", it="i32"),
+        "dynamic_update_slice": dw.dus_program((2, 8, 256, 64), (2, 8, 1, 64), dt="bf16", it="i32", donate=True),
     }
     for (name, prog, _), _, _ in edge_programs.CASES:
         progs["edge_" + name] = prog
