@@ -184,6 +184,13 @@ def evaluate(text: str, inputs: Sequence[np.ndarray], dot_precision: str = "f64"
             return [env[n] for n in names]
         m = re.match(r"(%[\w.$-]+)\s*=\s*(?:stablehlo|mhlo)\.(\w+)\s*(.*)$", st)
         if not m:
+            # the generic form `%r = "stablehlo.op"(%a, %b) <{attrs}> : (types) -> type`, handed on as
+            # `%a, %b <{attrs}> : (types) -> type`
+            m = re.match(r'(%[\w.$-]+)\s*=\s*"(?:stablehlo|mhlo)\.(\w+)"\((.*?)\)\s*(.*)$', st)
+            if m:
+                env[m.group(1)] = _eval_op(m.group(2), m.group(3) + " " + m.group(4), env, dot_precision)
+                continue
+        if not m:
             raise ValueError(f"cannot parse statement: {st}")
         res, op, rest = m.group(1), m.group(2), m.group(3)
         env[res] = _eval_op(op, rest, env, dot_precision)
@@ -196,6 +203,51 @@ _RET = re.compile(r"(?:func\.)?return\s+(.*?)(?:\s*:\s*.*)?$")
 def _operands(rest: str, n: int, env) -> List[Tuple[np.ndarray, str]]:
     names = re.findall(r"%[\w.$-]+", rest.split(":")[0])[:n]
     return [env[x] for x in names]
+
+
+def _gather(rest: str, env, out_shape) -> Tuple[np.ndarray, str]:
+    """gather (manipulation.rs:1235-1307), element by element as the StableHLO specification defines it: for result
+    index i, batch_dims = the result dims not in offset_dims; the start-indices coordinate is i's batch coordinates
+    with the index vector dim inserted; full_start_index[start_index_map[k]] = clamp(index_vector[k], 0,
+    dim - slice_sizes); full_batching_index[operand_batching_dims[j]] = the batch coordinate of
+    start_indices_batching_dims[j]; full_offset_index = i's offset coordinates placed on the operand dims that are
+    neither collapsed nor batching, in order; operand index = the sum of the three."""
+    head = rest.split("<{")[0]
+    names = re.findall(r"%[\w.$-]+", head)
+    (x, dt), (ix, idt) = env[names[0]], env[names[1]]
+    x, ix = np.asarray(x), np.asarray(ix)
+    attrs = rest[rest.index("<{"):rest.rindex("}>")]
+    dn = re.search(r"#stablehlo\.gather<(.*?)>", attrs, re.S).group(1)
+
+    def field(name):
+        m = re.search(name + r"\s*=\s*\[(.*?)\]", dn)
+        return _ints(m.group(1)) if m else []
+
+    offset_dims, collapsed = field("offset_dims"), field("collapsed_slice_dims")
+    op_batch, idx_batch = field("operand_batching_dims"), field("start_indices_batching_dims")
+    start_map = field("start_index_map")
+    ivd = int(re.search(r"index_vector_dim\s*=\s*(\d+)", dn).group(1))
+    sizes = _ints(re.search(r"slice_sizes\s*=\s*array<i64:(.*?)>", attrs).group(1))
+    if idt.startswith("ui"):
+        ix = ix.astype(object) % (1 << INT_BITS[idt])
+    out = np.empty(out_shape, dtype=x.dtype)
+    batch_dims = [d for d in range(len(out_shape)) if d not in offset_dims]
+    offset_operand = [d for d in range(x.ndim) if d not in collapsed and d not in op_batch]
+    for i in np.ndindex(*out_shape):
+        bi = [i[d] for d in batch_dims]
+        if ivd < ix.ndim:
+            vec = [ix[tuple(bi[:ivd] + [k] + bi[ivd:])] for k in range(ix.shape[ivd])]
+        else:
+            vec = [ix[tuple(bi)]]
+        idx = [0] * x.ndim
+        for k, d in enumerate(start_map):
+            idx[d] += min(max(int(vec[k]), 0), x.shape[d] - sizes[d])
+        for d_op, d_start in zip(op_batch, idx_batch):
+            idx[d_op] += bi[d_start - (0 if d_start < ivd else 1)]
+        for k, d in enumerate(offset_dims):
+            idx[offset_operand[k]] += i[d]
+        out[i] = x[tuple(idx)]
+    return out, dt
 
 
 def _eval_op(op: str, rest: str, env, dot_precision: str) -> Tuple[np.ndarray, str]:
@@ -285,6 +337,8 @@ def _eval_op(op: str, rest: str, env, dot_precision: str) -> Tuple[np.ndarray, s
         out = x.copy()
         out[sl] = u
         return out, dt
+    if op == "gather":
+        return _gather(rest, env, out_shape)
     if op == "concatenate":
         # manipulation.rs:778-822: the inputs one after another along `dim`, in operand order
         head = rest.split(":")[0]

@@ -41,7 +41,7 @@ enum class Op : uint8_t {
   // elementwise, ternary
   Select, Clamp,
   // data movement
-  BroadcastInDim, Transpose, Reshape, Iota, Slice, Concatenate, Pad, DynamicSlice, DynamicUpdateSlice,
+  BroadcastInDim, Transpose, Reshape, Iota, Slice, Concatenate, Pad, DynamicSlice, DynamicUpdateSlice, Gather,
   // contractions and reductions
   DotGeneral, Reduce,
 };
@@ -56,12 +56,19 @@ struct DotDims {
   std::vector<int64_t> lhs_batch, rhs_batch, lhs_contract, rhs_contract;
 };
 
+// gather's dimension numbers (crates/ryft-mlir/src/dialects/stable_hlo/operations/manipulation.rs:1128-1225)
+struct GatherDims {
+  std::vector<int64_t> offset_dims, collapsed_slice_dims, operand_batching_dims, start_indices_batching_dims,
+      start_index_map;
+  int64_t index_vector_dim = 0;
+};
+
 struct Node {
   Op op;
   TensorType type;
   std::vector<int> operands;
   // attributes (meaning depends on op)
-  std::vector<int64_t> dims;  // broadcast_dimensions / permutation / reduce dimensions / dynamic_slice slice_sizes
+  std::vector<int64_t> dims;  // broadcast_dimensions / permutation / reduce dimensions / slice_sizes (dynamic_slice, gather)
   // slice: start / limit / stride per dim; pad: edge_padding_low / edge_padding_high / interior_padding
   std::vector<int64_t> lo, hi, step;
   int64_t axis = 0;  // concatenate dimension
@@ -69,6 +76,7 @@ struct Node {
   CmpDir cmp = CmpDir::EQ;
   CmpType cmp_type = CmpType::NOTYPE;
   DotDims dot;
+  GatherDims gather;
   DType dot_lhs_precision = DType::INVALID;  // algorithm lhs/rhs_precision_type, if given
   DType dot_rhs_precision = DType::INVALID;
   ReduceBody reduce_body = ReduceBody::Add;

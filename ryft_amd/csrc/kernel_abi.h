@@ -233,4 +233,23 @@ struct WindowArgs {
   int64_t total;       // elements of the window
 };
 
+// gather (manipulation.rs:1235-1307): out[i] = operand[start(i) + batch(i) + offset(i)] per result element i, with
+//   offset(i): result dim r with out_to_op[r] >= 0 contributes its coordinate to operand dim out_to_op[r];
+//   batch(i): result dim r with out_to_idx[r] >= 0 is the coordinate of start-indices dim out_to_idx[r]; operand dim
+//             d with op_batch[d] >= 0 adds the coordinate of start-indices dim op_batch[d];
+//   start(i): component k of the index vector (start-indices dim ivd at k, or the scalar when ivd == idx_rank)
+//             is added to operand dim map[k] after clamping to [0, op_shape - slice].
+struct GatherArgs {
+  const void* operand;
+  const void* indices;
+  void* out;
+  int32_t idx_dtype;   // DType of the start indices
+  int32_t elem_bytes;  // 1, 2, 4 or 8
+  int32_t out_rank, op_rank, idx_rank, ivd, n_map;
+  int32_t pad_;
+  int64_t out_shape[WIN_MAX_RANK], op_shape[WIN_MAX_RANK], idx_shape[WIN_MAX_RANK], slice[WIN_MAX_RANK];
+  int32_t out_to_op[WIN_MAX_RANK], out_to_idx[WIN_MAX_RANK], op_batch[WIN_MAX_RANK], map[WIN_MAX_RANK];
+  int64_t total;       // result elements
+};
+
 }  // namespace ryft

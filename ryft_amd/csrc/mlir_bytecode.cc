@@ -118,7 +118,7 @@ struct BType {
 struct BAttr {
   enum Kind {
     STRING, INT, FLOAT, ARRAY, DICT, DENSE_ARRAY, DENSE_ELEMENTS, TYPE, UNIT, SYMREF, LOCATION,
-    CMP_DIR, CMP_TYPE, DOT_DIMS, PRECISION, DOT_ALGORITHM, TEXT, OTHER
+    CMP_DIR, CMP_TYPE, DOT_DIMS, GATHER_DIMS, PRECISION, DOT_ALGORITHM, TEXT, OTHER
   } kind = OTHER;
   std::string str;                                // STRING, SYMREF, TEXT
   int64_t i = 0;                                  // INT, CMP_DIR, CMP_TYPE, PRECISION
@@ -129,6 +129,7 @@ struct BAttr {
   std::vector<int64_t> ints;                      // DENSE_ARRAY (integer element types)
   std::vector<uint8_t> raw;                       // DENSE_ELEMENTS: MLIR's raw element storage
   DotDims dot;                                    // DOT_DIMS
+  GatherDims gather;                              // GATHER_DIMS
   int lhs_precision = -1, rhs_precision = -1;     // DOT_ALGORITHM: type indices
 };
 
@@ -557,6 +558,15 @@ class BytecodeParser {
           a.dot.lhs_contract = svarints(r);
           a.dot.rhs_contract = svarints(r);
           break;
+        case 7:                                                                 // GatherDimensionNumbersAttr
+          a.kind = BAttr::GATHER_DIMS;
+          a.gather.offset_dims = svarints(r);
+          a.gather.collapsed_slice_dims = svarints(r);
+          a.gather.operand_batching_dims = svarints(r);
+          a.gather.start_indices_batching_dims = svarints(r);
+          a.gather.start_index_map = svarints(r);
+          a.gather.index_vector_dim = r.svarint();
+          break;
         case 8: a.kind = BAttr::PRECISION; a.i = (int64_t)r.varint(); break;  // PrecisionAttr
         case 15:                                                                // DotAlgorithmAttr
           a.kind = BAttr::DOT_ALGORITHM;
@@ -598,6 +608,10 @@ class BytecodeParser {
                              {"strides", true, {BAttr::DENSE_ARRAY}}}},
         {"stablehlo.concatenate", {{"dimension", true, {BAttr::INT}}}},
         {"stablehlo.dynamic_slice", {{"slice_sizes", true, {BAttr::DENSE_ARRAY}}}},
+        {"stablehlo.gather",
+         {{"dimension_numbers", true, {BAttr::GATHER_DIMS}},
+          {"indices_are_sorted", false, {BAttr::INT}},
+          {"slice_sizes", true, {BAttr::DENSE_ARRAY}}}},
         {"stablehlo.pad", {{"edge_padding_high", true, {BAttr::DENSE_ARRAY}}, {"edge_padding_low", true, {BAttr::DENSE_ARRAY}},
                            {"interior_padding", true, {BAttr::DENSE_ARRAY}}}},
         {"stablehlo.compare",
@@ -621,6 +635,7 @@ class BytecodeParser {
     if (op == "func.func") return pick({"sym_name", "function_type", "sym_visibility", "arg_attrs", "res_attrs"});
     if (op == "stablehlo.compare") return pick({"comparison_direction", "compare_type"});
     if (op == "stablehlo.dot_general") return pick({"dot_dimension_numbers", "precision_config", "algorithm"});
+    if (op == "stablehlo.gather") return pick({"dimension_numbers", "slice_sizes", "indices_are_sorted"});
     // (slice and pad: three fields of one kind, so another order could not be told apart; sorted only)
     return sorted;
   }
@@ -952,6 +967,11 @@ class BytecodeParser {
           n.dims = int_list(op, "slice_sizes");
         } else if (nm == "dynamic_update_slice") {
           n.op = Op::DynamicUpdateSlice;
+        } else if (nm == "gather") {
+          n.op = Op::Gather;
+          const BAttr& d = need(op, "dimension_numbers");
+          n.gather = d.kind == BAttr::GATHER_DIMS ? d.gather : mlir_gather_dims_text(d.str);
+          n.dims = int_list(op, "slice_sizes");
         } else if (nm == "concatenate") {
           n.op = Op::Concatenate;
           const BAttr& a = need(op, "dimension");

@@ -16,6 +16,7 @@ std::vector<int64_t> mlir_int_list_text(const std::string& raw);    // "[0, 1]",
 void mlir_dense_text(const std::string& text, const TensorType& tt, Node& n);  // "dense<...>" → n.literal / n.splat
 CmpDir mlir_cmp_dir_text(const std::string& raw);                   // text containing EQ / NE / GE / GT / LE / LT
 CmpType mlir_cmp_type_text(const std::string& raw);                 // text containing FLOAT / SIGNED / ...
+GatherDims mlir_gather_dims_text(const std::string& raw);           // "#stablehlo.gather<offset_dims = [..], ...>"
 void validate_node(const Graph& g, Node& n);                        // operand counts, shapes, dimension ranges
 void check_tensor_shape(const std::vector<int64_t>& shape);         // dims and element count within plan limits
 inline int64_t first_int(const std::vector<int64_t>& v, const char* what) {  // a one-integer attribute's value

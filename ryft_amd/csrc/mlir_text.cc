@@ -89,6 +89,7 @@ const char* op_name(Op op) {
     case Op::Pad: return "pad";
     case Op::DynamicSlice: return "dynamic_slice";
     case Op::DynamicUpdateSlice: return "dynamic_update_slice";
+    case Op::Gather: return "gather";
     case Op::Iota: return "iota";
     case Op::DotGeneral: return "dot_general";
     case Op::Reduce: return "reduce";
@@ -937,6 +938,10 @@ class Parser {
       n.dims = parse_int_list_text(sz.empty() ? get("slice_sizes") : sz);
     } else if (nm == "dynamic_update_slice") {
       n.op = Op::DynamicUpdateSlice;
+    } else if (nm == "gather") {
+      n.op = Op::Gather;
+      n.gather = mlir_gather_dims_text(get("dimension_numbers"));
+      n.dims = parse_int_list_text(get("slice_sizes"));
     } else if (nm == "concatenate") {
       n.op = Op::Concatenate;
       std::string d = get("dim");
@@ -1032,6 +1037,53 @@ TensorType mlir_type_text(const std::string& text) {
   return parse_type(c);
 }
 std::vector<int64_t> mlir_int_list_text(const std::string& raw) { return parse_int_list_text(raw); }
+
+// "#stablehlo.gather<offset_dims = [2, 3], collapsed_slice_dims = [0], start_index_map = [1, 0],
+// index_vector_dim = 2>" (manipulation.rs:2622-2636): each field `name = [list]` or `name = int`; absent lists are
+// empty, index_vector_dim is required.
+GatherDims mlir_gather_dims_text(const std::string& raw) {
+  const size_t open = raw.find('<'), close = raw.rfind('>');
+  if (raw.find("gather") == std::string::npos || open == std::string::npos || close == std::string::npos ||
+      close < open)
+    invalid("gather dimension numbers: expected #stablehlo.gather<...>, got '" + raw.substr(0, 80) + "'");
+  const std::string body = raw.substr(open + 1, close - open - 1);
+  GatherDims g;
+  bool have_ivd = false;
+  size_t i = 0;
+  while (i < body.size()) {
+    while (i < body.size() && (isspace((unsigned char)body[i]) || body[i] == ',')) ++i;
+    if (i >= body.size()) break;
+    size_t e = i;
+    while (e < body.size() && (isalnum((unsigned char)body[e]) || body[e] == '_')) ++e;
+    const std::string name = body.substr(i, e - i);
+    while (e < body.size() && isspace((unsigned char)body[e])) ++e;
+    if (name.empty() || e >= body.size() || body[e] != '=') invalid("gather dimension numbers: malformed field");
+    ++e;
+    while (e < body.size() && isspace((unsigned char)body[e])) ++e;
+    if (name == "index_vector_dim") {
+      char* end = nullptr;
+      const long long v = std::strtoll(body.c_str() + e, &end, 10);
+      if (end == body.c_str() + e) invalid("gather dimension numbers: index_vector_dim is not an integer");
+      g.index_vector_dim = v;
+      have_ivd = true;
+      i = end - body.c_str();
+      continue;
+    }
+    if (e >= body.size() || body[e] != '[') invalid("gather dimension numbers: field `" + name + "` is not a list");
+    const size_t rb = body.find(']', e);
+    if (rb == std::string::npos) invalid("gather dimension numbers: unterminated list");
+    std::vector<int64_t> v = parse_int_list_text(body.substr(e, rb - e + 1));
+    if (name == "offset_dims") g.offset_dims = v;
+    else if (name == "collapsed_slice_dims") g.collapsed_slice_dims = v;
+    else if (name == "operand_batching_dims") g.operand_batching_dims = v;
+    else if (name == "start_indices_batching_dims") g.start_indices_batching_dims = v;
+    else if (name == "start_index_map") g.start_index_map = v;
+    else invalid("gather dimension numbers: unknown field `" + name + "`");
+    i = rb + 1;
+  }
+  if (!have_ivd) invalid("gather dimension numbers: index_vector_dim is missing");
+  return g;
+}
 void mlir_dense_text(const std::string& text, const TensorType& tt, Node& n) {
   size_t d = text.find("dense<");
   if (d == std::string::npos) unimplemented("constant value '" + text + "' is not a dense literal");
@@ -1216,6 +1268,70 @@ void validate_node(const Graph& g, Node& n) {
       if (upd && opt(1).dtype != x.dtype) invalid("dynamic_update_slice: update element type mismatch");
       if (n.type.dtype != x.dtype || n.type.shape != (upd ? x.shape : win))
         invalid(std::string(op_name(n.op)) + ": result type mismatch");
+      break;
+    }
+    case Op::Gather: {
+      // the StableHLO gather constraints (manipulation.rs:1235-1307): index vector dimension within the start
+      // indices' rank (equal to it: an implicit trailing 1), start_index_map as long as the index vectors, the
+      // dimension lists in range and without repeats, collapsed / batching slices of size ≤ 1, and the result made
+      // of the batch dimensions (the start indices' other dimensions, in order) and the offset dimensions (the
+      // operand's non-collapsed, non-batching slice sizes, in order)
+      need(2);
+      const TensorType& x = opt(0);
+      const TensorType& ix = opt(1);
+      const GatherDims& gd = n.gather;
+      const int r = x.rank(), ri = ix.rank(), ro = n.type.rank();
+      if (!(ix.dtype == DType::S8 || ix.dtype == DType::S16 || ix.dtype == DType::S32 || ix.dtype == DType::S64 ||
+            ix.dtype == DType::U8 || ix.dtype == DType::U16 || ix.dtype == DType::U32 || ix.dtype == DType::U64))
+        invalid("gather: start indices must be integers");
+      if (gd.index_vector_dim < 0 || gd.index_vector_dim > ri) invalid("gather: index_vector_dim out of range");
+      const int64_t nvec = gd.index_vector_dim < ri ? ix.shape[gd.index_vector_dim] : 1;
+      if ((int64_t)gd.start_index_map.size() != nvec) invalid("gather: start_index_map must match the index vectors");
+      if ((int)n.dims.size() != r) invalid("gather: slice_sizes must have one entry per operand dimension");
+      dims_in_range({&gd.collapsed_slice_dims, &gd.operand_batching_dims}, r, "gather");
+      dims_in_range({&gd.start_index_map}, r, "gather");
+      dims_in_range({&gd.offset_dims}, ro, "gather");
+      if (gd.start_indices_batching_dims.size() != gd.operand_batching_dims.size())
+        invalid("gather: batching dimension lists differ in length");
+      {
+        std::vector<int64_t> sb = gd.start_indices_batching_dims;
+        dims_in_range({&sb}, ri, "gather");
+        for (int64_t d : sb)
+          if (d == gd.index_vector_dim) invalid("gather: a batching dimension is the index vector dimension");
+      }
+      for (int64_t d : gd.start_index_map)
+        if (std::find(gd.operand_batching_dims.begin(), gd.operand_batching_dims.end(), d) !=
+            gd.operand_batching_dims.end())
+          invalid("gather: start_index_map names a batching dimension");
+      for (int d = 0; d < r; ++d)
+        if (n.dims[d] < 0 || n.dims[d] > x.shape[d]) invalid("gather: slice size out of range");
+      for (int64_t d : gd.collapsed_slice_dims)
+        if (n.dims[d] > 1) invalid("gather: collapsed slices must have size 0 or 1");
+      for (size_t i = 0; i < gd.operand_batching_dims.size(); ++i) {
+        const int64_t d = gd.operand_batching_dims[i];
+        if (n.dims[d] > 1) invalid("gather: batching slices must have size 0 or 1");
+        if (x.shape[d] != ix.shape[gd.start_indices_batching_dims[i]]) invalid("gather: batching dimension sizes differ");
+      }
+      for (size_t i = 1; i < gd.offset_dims.size(); ++i)
+        if (gd.offset_dims[i] <= gd.offset_dims[i - 1]) invalid("gather: offset_dims must be sorted");
+      std::vector<int64_t> offs, batch;
+      for (int d = 0; d < r; ++d)
+        if (std::find(gd.collapsed_slice_dims.begin(), gd.collapsed_slice_dims.end(), d) ==
+                gd.collapsed_slice_dims.end() &&
+            std::find(gd.operand_batching_dims.begin(), gd.operand_batching_dims.end(), d) ==
+                gd.operand_batching_dims.end())
+          offs.push_back(n.dims[d]);
+      for (int d = 0; d < ri; ++d)
+        if (d != gd.index_vector_dim) batch.push_back(ix.shape[d]);
+      if (offs.size() != gd.offset_dims.size() || (int)(offs.size() + batch.size()) != ro)
+        invalid("gather: result rank mismatch");
+      std::vector<int64_t> want(ro);
+      size_t ko = 0, kb = 0;
+      for (int d = 0; d < ro; ++d) {
+        const bool is_off = ko < gd.offset_dims.size() && gd.offset_dims[ko] == d;
+        want[d] = is_off ? offs[ko++] : batch[kb++];
+      }
+      if (want != n.type.shape || n.type.dtype != x.dtype) invalid("gather: result type mismatch");
       break;
     }
     default:

@@ -168,6 +168,7 @@ class Planner {
   void emit_pad(int node, int target);
   void emit_dynamic_slice(int node, int target);
   void emit_dynamic_update_slice(int node, int target);
+  void emit_gather(int node, int target);
   void push_window_step(const char* name, int mode, int src, int dst, const std::vector<int>& idx,
                         const TensorType& big, const std::vector<int64_t>& win, DType idx_dtype);
   void push_strided_step(ExprBuilder& b, const char* name, int out, int64_t out_offset,
@@ -541,6 +542,9 @@ int Planner::materialize(int node, int target) {
     case Op::DynamicUpdateSlice:
       emit_dynamic_update_slice(node, target);
       break;
+    case Op::Gather:
+      emit_gather(node, target);
+      break;
     case Op::Reshape: {
       int s = materialize(n.operands[0]);
       if (target >= 0) {
@@ -752,6 +756,64 @@ void Planner::emit_dynamic_update_slice(int node, int target) {
   else materialize(xo, out);
   const DType it = n.type.rank() ? g_.nodes[n.operands[2]].type.dtype : DType::S32;
   push_window_step("dynamic_update_slice", WIN_WRITE, upd, out, idx, n.type, un.type.shape, it);
+  mat_[node] = out;
+}
+
+// gather (manipulation.rs:1235-1307): one step over the result (kernels/k_window.hip), the operand and the start
+// indices materialized contiguously. The dimension numbers become per-dimension maps: each result dim is an offset
+// dim (it walks one operand dim: the operand's non-collapsed, non-batching dims in order) or a batch dim (one of the
+// start indices' dims other than the index vector dim, in order); each operand batching dim takes the coordinate of
+// its start-indices batching dim; index-vector component k moves operand dim start_index_map[k].
+void Planner::emit_gather(int node, int target) {
+  const Node& n = g_.nodes[node];
+  const TensorType& xt = g_.nodes[n.operands[0]].type;
+  const TensorType& it = g_.nodes[n.operands[1]].type;
+  const GatherDims& gd = n.gather;
+  const int r = xt.rank(), ri = it.rank(), ro = n.type.rank();
+  if (r > WIN_MAX_RANK || ri > WIN_MAX_RANK || ro > WIN_MAX_RANK)
+    unimplemented("gather of rank above " + std::to_string(WIN_MAX_RANK));
+  const size_t es = dtype_size(n.type.dtype);
+  if (es != 1 && es != 2 && es != 4 && es != 8) unimplemented(std::string("gather of ") + dtype_name(n.type.dtype));
+  const int x = materialize(n.operands[0]);
+  const int ix = materialize(n.operands[1]);
+  const int out = temp_or(target, n.type);
+  Step st{};
+  st.kind = Step::GATHER;
+  st.name = "gather";
+  GatherArgs& a = st.gat;
+  a.idx_dtype = (int32_t)it.dtype;
+  a.elem_bytes = (int32_t)es;
+  a.out_rank = ro;
+  a.op_rank = r;
+  a.idx_rank = ri;
+  a.ivd = (int32_t)gd.index_vector_dim;
+  a.n_map = (int32_t)gd.start_index_map.size();
+  a.total = 1;
+  for (int d = 0; d < WIN_MAX_RANK; ++d) a.out_to_op[d] = a.out_to_idx[d] = a.op_batch[d] = a.map[d] = -1;
+  for (int d = 0; d < r; ++d) {
+    a.op_shape[d] = xt.shape[d];
+    a.slice[d] = n.dims[d];
+  }
+  for (int d = 0; d < ri; ++d) a.idx_shape[d] = it.shape[d];
+  auto has = [](const std::vector<int64_t>& v, int64_t d) { return std::find(v.begin(), v.end(), d) != v.end(); };
+  std::vector<int> offset_operand_dims, batch_index_dims;
+  for (int d = 0; d < r; ++d)
+    if (!has(gd.collapsed_slice_dims, d) && !has(gd.operand_batching_dims, d)) offset_operand_dims.push_back(d);
+  for (int d = 0; d < ri; ++d)
+    if (d != gd.index_vector_dim) batch_index_dims.push_back(d);
+  size_t ko = 0, kb = 0;
+  for (int d = 0; d < ro; ++d) {
+    a.out_shape[d] = n.type.shape[d];
+    a.total *= n.type.shape[d];
+    if (has(gd.offset_dims, d)) a.out_to_op[d] = offset_operand_dims.at(ko++);
+    else a.out_to_idx[d] = batch_index_dims.at(kb++);
+  }
+  for (size_t i = 0; i < gd.operand_batching_dims.size(); ++i)
+    a.op_batch[gd.operand_batching_dims[i]] = (int32_t)gd.start_indices_batching_dims[i];
+  for (size_t k = 0; k < gd.start_index_map.size(); ++k) a.map[k] = (int32_t)gd.start_index_map[k];
+  st.patches = {{offsetof(GatherArgs, operand), x}, {offsetof(GatherArgs, indices), ix}, {offsetof(GatherArgs, out), out}};
+  st.bytes = 2.0 * (double)n.type.bytes() + (double)it.bytes();
+  plan_.steps.push_back(std::move(st));
   mat_[node] = out;
 }
 
@@ -1939,6 +2001,8 @@ std::string Plan::describe() const {
       os << " B=" << s.attn.B << " H=" << s.attn.H << " S=" << s.attn.Sq << " D=" << s.attn.D << " causal=" << s.attn.causal;
     } else if (s.kind == Step::WINDOW) {
       os << " window=" << s.win.total << " of rank " << s.win.rank;
+    } else if (s.kind == Step::GATHER) {
+      os << " elems=" << s.gat.total << " index_vector=" << s.gat.n_map;
     }
     os << " flops=" << s.flops << " bytes=" << s.bytes << "\n";
   }

@@ -692,7 +692,7 @@ bool enqueue_steps(Client* c, const Plan& plan, void* const* ptr, hipStream_t st
   const bool record = profilable && profiler_sessions_active();  // started profiler sessions take the events too
   const bool timed = prof || record;
   constexpr size_t kBlock = std::max({sizeof(EwProgram), sizeof(ReduceArgs), sizeof(GemmArgs), sizeof(RowArgs),
-                                      sizeof(AttnArgs), sizeof(WindowArgs)});
+                                      sizeof(AttnArgs), sizeof(WindowArgs), sizeof(GatherArgs)});
   alignas(64) static thread_local unsigned char block[kBlock + 64];
   bool recorded = false;
   for (size_t si = 0; si < plan.steps.size(); ++si) {
@@ -722,6 +722,7 @@ bool enqueue_steps(Client* c, const Plan& plan, void* const* ptr, hipStream_t st
                   : step.kind == Step::GEMM      ? sizeof(GemmArgs)
                   : step.kind == Step::ROW       ? sizeof(RowArgs)
                   : step.kind == Step::WINDOW    ? sizeof(WindowArgs)
+                  : step.kind == Step::GATHER    ? sizeof(GatherArgs)
                                                  : sizeof(AttnArgs);
       memcpy(block, const_cast<Step&>(step).args_block(), sz);
       for (auto& p : step.patches) {
@@ -736,6 +737,7 @@ bool enqueue_steps(Client* c, const Plan& plan, void* const* ptr, hipStream_t st
         case Step::GEMM: launch_gemm(*(GemmArgs*)block, st, last); break;
         case Step::ATTENTION: launch_attention(*(AttnArgs*)block, st, last); break;
         case Step::WINDOW: launch_window(*(WindowArgs*)block, st, last); break;
+        case Step::GATHER: launch_gather(*(GatherArgs*)block, st, last); break;
         default: recorded = false; break;
       }
       if (hipEvent_t unused = pending_start()) {  // no launch took it

@@ -132,6 +132,9 @@ def parse_module(text: str):
         name, rest = rhs.split(None, 1) if " " in rhs else (rhs, "")
         if name.startswith("stablehlo.reduce("):
             name, rest = "stablehlo.reduce", rhs[len("stablehlo.reduce"):]
+        if rhs.startswith('"stablehlo.gather"('):
+            ops.append(_parse_gather(lhs, rhs))
+            continue
         ops.append(_parse_op(lhs, name, rest))
     return arg_names, arg_types, res_types, ops, returned
 
@@ -151,6 +154,27 @@ def arg_attr_dicts(text: str) -> List[Dict[str, Tuple[str, str]]]:
                 d[k.strip().strip('"')] = (val.strip(), ty.strip())
         out.append(d)
     return out
+
+
+def _parse_gather(res: str, rhs: str) -> Op:
+    # `"stablehlo.gather"(%a, %b) <{dimension_numbers = #stablehlo.gather<...>, indices_are_sorted = ...,
+    # slice_sizes = array<i64: ...>}> : (A, B) -> R`
+    m = re.fullmatch(r'"stablehlo\.gather"\((%\w+), (%\w+)\) <\{(.*)\}> : (.*)', rhs.strip())
+    assert m, rhs
+    attrs_txt = m.group(3)
+    dn = re.search(r"#stablehlo\.gather<(.*?)>", attrs_txt).group(1)
+
+    def field(name):
+        f = re.search(name + r"\s*=\s*\[(.*?)\]", dn)
+        return _ints(f.group(1)) if f else []
+
+    g = {k: field(k) for k in ("offset_dims", "collapsed_slice_dims", "operand_batching_dims",
+                               "start_indices_batching_dims", "start_index_map")}
+    g["index_vector_dim"] = int(re.search(r"index_vector_dim\s*=\s*(\d+)", dn).group(1))
+    sizes = _ints(re.search(r"slice_sizes\s*=\s*array<i64:(.*?)>", attrs_txt).group(1))
+    ins, outs = _types_after_colon(m.group(4))
+    attrs = {"dimension_numbers": ("gather_dims", g), "slice_sizes": ("i64s", sizes)}
+    return Op("stablehlo.gather", [m.group(1), m.group(2)], [res], outs, attrs)
 
 
 def _parse_op(res: str, name: str, rest: str) -> Op:
@@ -228,6 +252,7 @@ SORTED = {
     "stablehlo.dot_general": ["algorithm", "dot_dimension_numbers", "precision_config"],
     "stablehlo.slice": ["limit_indices", "start_indices", "strides"],
     "stablehlo.pad": ["edge_padding_high", "edge_padding_low", "interior_padding"],
+    "stablehlo.gather": ["dimension_numbers", "indices_are_sorted", "slice_sizes"],
 }
 # ... and in declaration order
 DECLARED = {
@@ -238,10 +263,12 @@ DECLARED = {
     # order apart)
     "stablehlo.slice": ["limit_indices", "start_indices", "strides"],
     "stablehlo.pad": ["edge_padding_high", "edge_padding_low", "interior_padding"],
+    "stablehlo.gather": ["dimension_numbers", "slice_sizes", "indices_are_sorted"],
 }
 REQUIRED = {"function_type", "sym_name", "comparison_direction", "dot_dimension_numbers", "value", "iota_dimension",
             "broadcast_dimensions", "permutation", "dimensions", "start_indices", "limit_indices", "strides",
-            "dimension", "edge_padding_low", "edge_padding_high", "interior_padding", "slice_sizes"}
+            "dimension", "edge_padding_low", "edge_padding_high", "interior_padding", "slice_sizes",
+            "dimension_numbers"}
 
 
 class Writer:
@@ -342,6 +369,19 @@ class Writer:
             data = varint(5)
             for k in ("lhs_batch", "rhs_batch", "lhs_contract", "rhs_contract"):
                 data += varint(len(d[k])) + b"".join(svarint(v) for v in d[k])
+            return self._entry("attr", "stablehlo", True, data)
+        if kind == "gather_dims":
+            g = spec[1]
+            lists = ("offset_dims", "collapsed_slice_dims", "operand_batching_dims", "start_indices_batching_dims",
+                     "start_index_map")
+            if self.text_attrs:
+                fields = [f"{k} = {g[k]}" for k in lists if g[k]] + [f"index_vector_dim = {g['index_vector_dim']}"]
+                return self._entry("attr", "stablehlo", False, ("#stablehlo.gather<" + ", ".join(fields) + ">").encode()
+                                   + b"\0")
+            data = varint(7)
+            for k in lists:
+                data += varint(len(g[k])) + b"".join(svarint(v) for v in g[k])
+            data += svarint(g["index_vector_dim"])
             return self._entry("attr", "stablehlo", True, data)
         raise ValueError(kind)
 

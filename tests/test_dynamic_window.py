@@ -1,8 +1,9 @@
-"""dynamic_slice / dynamic_update_slice on the CPU: the oracle pinned to the reference's worked examples
-(crates/ryft-mlir/src/dialects/stable_hlo/operations/manipulation.rs:955-976, 1045-1071) and to the clamping
-formula by brute force, and the plugin's front-ends and planner — the printed forms of the reference's builder
-tests (manipulation.rs:2447-2580) compile, text and bytecode plan alike, malformed windows are rejected, and a
-donated operand is updated in place."""
+"""dynamic_slice / dynamic_update_slice and gather on the CPU: the oracle pinned to the reference's worked examples
+(crates/ryft-mlir/src/dialects/stable_hlo/operations/manipulation.rs:955-976, 1045-1071, 1240-1300), to the
+clamping formula by brute force and to numpy's indexing for gather's special cases (row lookup, take_along_axis), and
+the plugin's front-ends and planner — the printed forms of the reference's builder tests (manipulation.rs:2447-2580,
+2690-2710) compile, text and bytecode plan alike, malformed windows and gathers are rejected, and a donated operand
+is updated in place."""
 import itertools
 
 import numpy as np
@@ -173,3 +174,101 @@ def test_operand_read_elsewhere_keeps_its_own_buffer(compile_client):
     _, plan = _plan(compile_client, prog)
     lines = [ln.split()[1] for ln in plan.strip().splitlines()]
     assert lines == ["elementwise", "copy", "dynamic_update_slice"], lines
+
+
+# ------------------------------------------------------------------------------------------------ gather
+def gather_program(x_t, i_t, out_t, offset_dims, collapsed, start_map, ivd, sizes, op_batch=(), idx_batch=()):
+    fields = [f"offset_dims = {list(offset_dims)}", f"collapsed_slice_dims = {list(collapsed)}"]
+    if op_batch:
+        fields += [f"operand_batching_dims = {list(op_batch)}", f"start_indices_batching_dims = {list(idx_batch)}"]
+    fields += [f"start_index_map = {list(start_map)}", f"index_vector_dim = {ivd}"]
+    sz = ", ".join(map(str, sizes))
+    return _mod([x_t, i_t], out_t, f'    %0 = "stablehlo.gather"(%arg0, %arg1) <{{dimension_numbers = '
+                                   f'#stablehlo.gather<{", ".join(fields)}>, indices_are_sorted = false, '
+                                   f'slice_sizes = array<i64: {sz}>}}> : ({x_t}, {i_t}) -> {out_t}\n'
+                                   f'    return %0 : {out_t}')
+
+
+# manipulation.rs:1240-1300: batching dims, a collapsed dim, an index vector of two, and one out-of-range start
+# ([0, 9] clamps to [0, 2]) — the documented result
+GATHER_EXAMPLE = dict(
+    x=np.arange(1, 49).reshape(2, 3, 4, 2),
+    idx=np.array([[[[0, 0], [1, 0], [2, 1]], [[0, 1], [1, 1], [0, 9]]],
+                  [[[0, 0], [2, 1], [2, 2]], [[1, 2], [0, 1], [1, 0]]]]),
+    want=[[[[[1, 2], [3, 4]], [[3, 4], [5, 6]], [[13, 14], [15, 16]]],
+           [[[33, 34], [35, 36]], [[35, 36], [37, 38]], [[41, 42], [43, 44]]]],
+          [[[[1, 2], [3, 4]], [[13, 14], [15, 16]], [[21, 22], [23, 24]]],
+           [[[43, 44], [45, 46]], [[33, 34], [35, 36]], [[27, 28], [29, 30]]]]])
+
+
+def gather_example_program():
+    return gather_program("tensor<2x3x4x2xi32>", "tensor<2x2x3x2xi64>", "tensor<2x2x3x2x2xi32>", [3, 4], [1], [2, 1],
+                          3, [1, 1, 2, 2], op_batch=[0], idx_batch=[1])
+
+
+def test_gather_reference_example():
+    (out, _), = sh.evaluate(gather_example_program(), [GATHER_EXAMPLE["x"], GATHER_EXAMPLE["idx"]])
+    assert out.tolist() == GATHER_EXAMPLE["want"]
+
+
+def test_gather_embedding_lookup_and_take_along_axis():
+    # two textbook special cases, against numpy: rows of a table by index (clamped at the end), and a gather of one
+    # element per row along the last axis (index vector dim = rank of the indices: an implicit trailing 1)
+    table = np.arange(50).reshape(10, 5)
+    ids = np.array([3, 0, 9, 12, -2])
+    prog = gather_program("tensor<10x5xi32>", "tensor<5xi32>", "tensor<5x5xi32>", [1], [0], [0], 1, [1, 5])
+    (out, _), = sh.evaluate(prog, [table, ids])
+    assert np.array_equal(out, table[np.clip(ids, 0, 9)])
+    x = np.arange(24).reshape(4, 6)
+    cols = np.array([[5], [0], [2], [3]])
+    prog = gather_program("tensor<4x6xi32>", "tensor<4x1xi32>", "tensor<4xi32>", [], [1], [1], 1, [1, 1],
+                          op_batch=[0], idx_batch=[0])
+    (out, _), = sh.evaluate(prog, [x, cols])
+    assert np.array_equal(out, np.take_along_axis(x, cols, axis=1)[:, 0])
+
+
+GATHER_PRINTED = """module {
+  func.func @main(%arg0: tensor<3x4x2xi64>, %arg1: tensor<2x3x2xi64>) -> tensor<2x3x2x2xi64> {
+    %0 = "stablehlo.gather"(%arg0, %arg1) <{dimension_numbers = #stablehlo.gather<offset_dims = [2, 3], collapsed_slice_dims = [0], start_index_map = [1, 0], index_vector_dim = 2>, indices_are_sorted = false, slice_sizes = array<i64: 1, 2, 2>}> : (tensor<3x4x2xi64>, tensor<2x3x2xi64>) -> tensor<2x3x2x2xi64>
+    return %0 : tensor<2x3x2x2xi64>
+  }
+}"""
+
+
+def test_gather_plans(compile_client):
+    # the printed form of the reference's builder test (manipulation.rs:2690-2710), the documented example, a row
+    # lookup and a take_along_axis (collapsed and batching dims kept apart, as StableHLO requires)
+    rows = gather_program("tensor<10x5xi32>", "tensor<5xi32>", "tensor<5x5xi32>", [1], [0], [0], 1, [1, 5])
+    along = gather_program("tensor<4x6xi32>", "tensor<4x1xi32>", "tensor<4xi32>", [], [1], [1], 1, [1, 1],
+                           op_batch=[0], idx_batch=[0])
+    for prog in (GATHER_PRINTED, gather_example_program(), rows, along):
+        _, plan = _plan(compile_client, prog)
+        assert plan.split("\n")[0].split()[1] == "gather", plan
+
+
+@pytest.mark.parametrize("bad", [
+    dict(ivd=3),                                  # index vector dim past the indices' rank
+    dict(start_map=[0]),                          # one start index map entry for index vectors of two
+    dict(sizes=[1, 4, 2]),                        # a slice larger than the operand
+    dict(collapsed=[1]),                          # a collapsed dim whose slice is 2
+    dict(offset_dims=[3, 2]),                     # offset dims not sorted
+    dict(op_batch=[0], idx_batch=[0]),           # dim 0 both collapsed and a batching dim
+    dict(out_t="tensor<2x3x2x3xi64>"),            # result not the gathered shape
+])
+def test_malformed_gathers_are_invalid(compile_client, bad):
+    kw = dict(x_t="tensor<3x4x2xi64>", i_t="tensor<2x3x2xi64>", out_t="tensor<2x3x2x2xi64>", offset_dims=[2, 3],
+              collapsed=[0], start_map=[1, 0], ivd=2, sizes=[1, 2, 2])
+    kw.update(bad)
+    with pytest.raises(pjrt.PjrtError) as e:
+        compile_client.compile(pjrt.Program.mlir(gather_program(**kw)))
+    assert e.value.code == pjrt.ErrorCode.INVALID_ARGUMENT, e.value.message
+
+
+def test_gather_bytecode_plans_like_text(compile_client):
+    # every writer variant (dialect-encoded or assembly-text dimension numbers, sorted or declared property order)
+    from tests.test_bytecode import VARIANTS
+    for prog in (GATHER_PRINTED, gather_example_program()):
+        _, text = _plan(compile_client, prog)
+        for vname, opts in VARIANTS.items():
+            _, code = _plan(compile_client, mb.to_bytecode(prog, **opts))
+            assert code == text, vname

@@ -1,8 +1,8 @@
-"""dynamic_slice / dynamic_update_slice on the GPU (crates/ryft-mlir/src/dialects/stable_hlo/operations/
-manipulation.rs:943-1130), bit-exact against the oracle: the reference's worked examples, every element size with
+"""dynamic_slice / dynamic_update_slice and gather on the GPU (crates/ryft-mlir/src/dialects/stable_hlo/operations/
+manipulation.rs:943-1307), bit-exact against the oracle: the reference's worked examples, every element size with
 start indices of several integer types inside, below and past the bounds (clamped), windows moved as 16-byte vectors
-and element by element, a fused consumer and a read-modify-write of one window, and a KV-cache style update of a
-donated buffer written in place."""
+and element by element, a fused consumer and a read-modify-write of one window, a KV-cache style update of a
+donated buffer written in place, and gathers with batching dimensions, embedding rows and unaligned windows."""
 import numpy as np
 import pytest
 
@@ -121,3 +121,57 @@ def test_kv_cache_update_in_place(gpu_client):
     out.done.await_()
     assert buf.unsafe_pointer() == p0
     assert np.array_equal(buf.to_numpy(), want)
+
+
+# ------------------------------------------------------------------------------------------------ gather
+from tests.test_dynamic_window import GATHER_EXAMPLE, gather_example_program, gather_program  # noqa: E402
+
+
+def test_gather_reference_example(gpu_client):
+    ins = [configs.HostInput(GATHER_EXAMPLE["x"].astype(np.int32), pjrt.BufferType.S32, (2, 3, 4, 2)),
+           configs.HostInput(GATHER_EXAMPLE["idx"].astype(np.int64), pjrt.BufferType.S64, (2, 2, 3, 2))]
+    outs, exe = run_pjrt(gpu_client, gather_example_program(), ins)
+    assert "gather" in exe.describe_plan()
+    assert outs[0].tolist() == GATHER_EXAMPLE["want"]
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f32", "i8", "f64"])
+def test_gather_embedding_rows(gpu_client, dt):
+    # rows of a [1000, 256] table by 4096 ids, some out of range (clamped to the first / last row): 16-byte vectors
+    # along the rows; checked against numpy's indexing (the oracle's agreement with it is pinned on the CPU)
+    table = _tensor(20, (1000, 256), dt)
+    rng = np.random.default_rng(21)
+    ids = rng.integers(-20, 1020, size=4096).astype(np.int32)
+    t = "tensor<1000x256x" + dt + ">"
+    prog = gather_program(t, "tensor<4096xi32>", "tensor<4096x256x" + dt + ">", [1], [0], [0], 1, [1, 256])
+    outs, _ = run_pjrt(gpu_client, prog, [table, configs.HostInput(ids, pjrt.BufferType.S32, (4096,))])
+    want = table.data[np.clip(ids, 0, 999)]
+    assert np.array_equal(outs[0].view(np.uint8), np.ascontiguousarray(want).view(np.uint8))
+
+
+@pytest.mark.parametrize("case", ["take_along_axis", "unaligned_windows", "reference_printed"])
+def test_gather_against_the_oracle(gpu_client, case):
+    if case == "take_along_axis":
+        # batching dims: one element per row at a per-row column
+        x = _tensor(22, (64, 100), "f32")
+        cols = configs.HostInput(np.random.default_rng(23).integers(-5, 110, size=(64, 1)).astype(np.int64),
+                                 pjrt.BufferType.S64, (64, 1))
+        prog = gather_program("tensor<64x100xf32>", "tensor<64x1xi64>", "tensor<64xf32>", [], [1], [1], 1,
+                              [1, 1], op_batch=[0], idx_batch=[0])
+        ins = [x, cols]
+    elif case == "unaligned_windows":
+        # 3x8 windows of a [50, 12] f32 table at (row, column) start pairs: rows of whole vectors, origins mostly not
+        # on a vector boundary (the kernel's element path inside its vector form)
+        x = _tensor(24, (50, 12), "f32")
+        starts = np.random.default_rng(25).integers(-3, 60, size=(5, 7, 2)).astype(np.int32)
+        prog = gather_program("tensor<50x12xf32>", "tensor<5x7x2xi32>", "tensor<5x7x3x8xf32>", [2, 3], [], [0, 1],
+                              2, [3, 8])
+        ins = [x, configs.HostInput(starts, pjrt.BufferType.S32, (5, 7, 2))]
+    else:
+        # the printed form of the reference's builder test with data of its shapes
+        from tests.test_dynamic_window import GATHER_PRINTED
+        prog = GATHER_PRINTED
+        ins = [_tensor(26, (3, 4, 2), "i64"),
+               configs.HostInput(np.random.default_rng(27).integers(-1, 5, size=(2, 3, 2)).astype(np.int64),
+                                 pjrt.BufferType.S64, (2, 3, 2))]
+    _check_exact(gpu_client, prog, ins, f"gather {case}")

@@ -37,6 +37,8 @@ def _programs():
         "slice_concatenate_pad": SLICE_CONCAT_PAD,
         "dynamic_slice": dw.ds_program((5, 7, 9), (2, 3, 4), dt="bf16", it="i32"),
         "dynamic_update_slice": dw.dus_program((2, 8, 256, 64), (2, 8, 1, 64), dt="bf16", it="i32", donate=True),
+        "gather": dw.gather_example_program(),
+        "gather_printed": dw.GATHER_PRINTED,
     }
     for (name, prog, _), _, _ in edge_programs.CASES:
         progs["edge_" + name] = prog
