@@ -228,6 +228,8 @@ void launch_gather(const GatherArgs& a, hipStream_t stream, hipEvent_t done) {
       fail(PJRT_Error_Code_INTERNAL, "gather start_index_map");
   if ((a.ivd < a.idx_rank ? a.idx_shape[a.ivd] : 1) != a.n_map) fail(PJRT_Error_Code_INTERNAL, "gather index vectors");
   if (total == 0) return record_done(done, stream);
+  for (int d = 0; d < a.op_rank; ++d)  // a non-empty result of an empty operand has no element to read
+    if (a.op_shape[d] == 0) fail(PJRT_Error_Code_INVALID_ARGUMENT, "gather from an empty operand into a non-empty result");
   const int es = a.elem_bytes;
   const int last = a.out_rank - 1;
   const bool vec = es < 16 && last >= 0 && a.out_to_op[last] == a.op_rank - 1 && (a.out_shape[last] * es) % 16 == 0 &&

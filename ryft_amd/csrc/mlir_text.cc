@@ -1332,6 +1332,7 @@ void validate_node(const Graph& g, Node& n) {
         want[d] = is_off ? offs[ko++] : batch[kb++];
       }
       if (want != n.type.shape || n.type.dtype != x.dtype) invalid("gather: result type mismatch");
+      if (x.elements() == 0 && n.type.elements() > 0) invalid("gather: a non-empty result from an empty operand");
       break;
     }
     default:
