@@ -17,7 +17,8 @@ Parity unpinned (no reference test, fixture or documented example fixes them; th
 which the plugin implements too): integer division by zero (quotient -1, all bits set for unsigned; remainder = the
 dividend); float → integer conversion of NaN (0) and of values outside the target range (saturated to its bounds),
 which the StableHLO specification leaves implementation-defined; the exact bits of transcendental functions (exp,
-log, tanh, logistic, power), which parity tests cover with tolerances. The XLA CPU plugin itself
+log, tanh, logistic, power, sine, cosine, tan, atan2, cbrt), which parity tests cover with tolerances (their
+values are pinned to the math module and to identities in tests/test_bit_trig_round_ops.py). The XLA CPU plugin itself
 is unavailable offline (no Bazel, no network), so semantics rest on the ryft-mlir op documentation cited per
 function, the reference's known-answer tests (README.md:122-137, programs.rs:2781-2829), closed forms, brute force
 on small cases, and torch's CPU dtype conversions for the narrow float types.

@@ -401,6 +401,10 @@ def _eval_op(op: str, rest: str, env, dot_precision: str) -> Tuple[np.ndarray, s
                  "maximum": lambda: np.maximum(a, b), "minimum": lambda: np.minimum(a, b),
                  "and": lambda: a & b, "or": lambda: a | b, "xor": lambda: a ^ b}[op]()
         return wrap_int(r, dt), dt
+    if op in _BITS:
+        return _bit_op(op, rest, env)
+    if op in _FLOAT_ONLY:
+        return _float_op(op, rest, env)
     if op in _UN:
         # exponential.rs (exponential :245, rsqrt :151, logistic :434), arithmetic.rs:134 (negate)
         (x, dt), = _operands(rest, 1, env)
@@ -424,6 +428,68 @@ def _eval_op(op: str, rest: str, env, dot_precision: str) -> Tuple[np.ndarray, s
     if op == "reduce":
         return _reduce(rest, env, out_shape, out_dt)
     raise NotImplementedError(f"stablehlo.{op}")
+
+
+_BITS = {"shift_left", "shift_right_arithmetic", "shift_right_logical", "popcnt", "count_leading_zeros"}
+_FLOAT_ONLY = {"sine", "cosine", "tan", "cbrt", "round_nearest_even", "round_nearest_afz", "is_finite", "atan2"}
+
+
+def _bit_op(op, rest, env):
+    """bit_manipulation.rs:5-280 on the two's complement bits of each element at its own width w: shift_left and
+    shift_right_logical give 0 and shift_right_arithmetic the sign fill when the shift amount, read as a w-bit
+    unsigned integer, is at least w; popcnt counts the set bits and count_leading_zeros the zero bits above the
+    highest set one (w for 0)."""
+    n = 2 if op.startswith("shift") else 1
+    vals = _operands(rest, n, env)
+    dt = vals[0][1]
+    w = INT_BITS[dt]
+    full = (1 << w) - 1 if w < 64 else 0xFFFFFFFFFFFFFFFF
+    mask = np.uint64(full)
+    u = np.asarray(vals[0][0], dtype=np.int64).view(np.uint64) & mask
+    if op == "popcnt":
+        return wrap_int(np.bitwise_count(u).astype(np.int64), dt), dt
+    if op == "count_leading_zeros":
+        length = np.zeros(u.shape, dtype=np.int64)
+        v = u.copy()
+        for k in (32, 16, 8, 4, 2, 1):
+            big = v >= np.uint64(1 << k)
+            v = np.where(big, v >> np.uint64(k), v)
+            length += np.where(big, k, 0)
+        length += (v > 0).astype(np.int64)
+        return wrap_int(w - length, dt), dt
+    amount = np.asarray(vals[1][0], dtype=np.int64).view(np.uint64) & mask
+    inside = amount < np.uint64(w)
+    s = np.where(inside, amount, np.uint64(0)).astype(np.uint64)
+    if op == "shift_left":
+        r = ((u << s) & mask).view(np.int64)
+        r = np.where(inside, r, 0)
+    elif op == "shift_right_logical":
+        r = np.where(inside, (u >> s).view(np.int64), 0)
+    else:
+        signed = u.view(np.int64) if w == 64 else np.where(u >= np.uint64(1 << (w - 1)), u.astype(np.int64) - (1 << w),
+                                                                   u.astype(np.int64))
+        r = np.where(inside, signed >> s.astype(np.int64), np.where(signed < 0, -1, 0))
+    return wrap_int(np.asarray(r, dtype=np.int64), dt), dt
+
+
+def _float_op(op, rest, env):
+    """trigonometric.rs:7-155, 203-262 (sine, cosine, tan, atan2), exponential.rs:166-210 (cbrt),
+    rounding.rs:91-180 (round_nearest_afz: ties away from zero; round_nearest_even: ties to even),
+    arithmetic.rs:470-515 (is_finite: i1, false for infinities and NaN)."""
+    vals = _operands(rest, 2 if op == "atan2" else 1, env)
+    dt = vals[0][1]
+    x = np.asarray(vals[0][0], dtype=np.float64)
+    if op == "is_finite":
+        return np.isfinite(x).astype(np.int64), "i1"
+    with np.errstate(all="ignore"):
+        if op == "atan2":
+            r = np.arctan2(x, np.asarray(vals[1][0], dtype=np.float64))
+        elif op == "round_nearest_afz":
+            t = np.trunc(x)
+            r = np.where(np.abs(x - t) >= 0.5, t + np.sign(x), t)
+        else:
+            r = {"sine": np.sin, "cosine": np.cos, "tan": np.tan, "cbrt": np.cbrt, "round_nearest_even": np.rint}[op](x)
+    return normalize(r, dt), dt
 
 
 def _dot_general(rest, env, out_shape, out_dt, dot_precision):

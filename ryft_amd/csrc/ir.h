@@ -36,8 +36,10 @@ enum class Op : uint8_t {
   Constant,
   // elementwise, unary
   Negate, Abs, Exp, Log, Rsqrt, Sqrt, Tanh, Logistic, Not, Convert, Floor, Ceil, Sign, Expm1, Log1p,
+  Sine, Cosine, Tan, Cbrt, RoundNearestEven, RoundNearestAfz, IsFinite, Popcnt, CountLeadingZeros,
   // elementwise, binary
   Add, Subtract, Multiply, Divide, Maximum, Minimum, Power, Remainder, And, Or, Xor, Compare,
+  Atan2, ShiftLeft, ShiftRightArithmetic, ShiftRightLogical,
   // elementwise, ternary
   Select, Clamp,
   // data movement

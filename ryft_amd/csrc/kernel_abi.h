@@ -39,16 +39,22 @@ enum EwOp : uint8_t {
   EW_ACC,       // r = GEMM accumulator a (0: first dot, 1: second dot); epilogues only
   // unary, float class
   EW_NEG, EW_ABS, EW_EXP, EW_LOG, EW_RSQRT, EW_SQRT, EW_TANH, EW_LOGISTIC, EW_FLOOR, EW_CEIL, EW_SIGN,
-  EW_EXPM1, EW_LOG1P,
-  // unary, int class
-  EW_INEG, EW_IABS, EW_NOT, EW_ISIGN,
+  EW_EXPM1, EW_LOG1P, EW_SIN, EW_COS, EW_TAN, EW_CBRT,
+  EW_RINT,      // round half to even
+  EW_ROUND,     // round half away from zero
+  EW_ISFINITE,  // float → pred
+  // unary, int class (EW_POPCNT / EW_CLZ: imm.i = the element width in bits)
+  EW_INEG, EW_IABS, EW_NOT, EW_ISIGN, EW_POPCNT, EW_CLZ,
   // conversions
   EW_CVT_F2F, EW_CVT_F2I, EW_CVT_I2F, EW_CVT_I2I, EW_CVT_F2P, EW_CVT_I2P,
   // binary, float class
-  EW_ADD, EW_SUB, EW_MUL, EW_DIV, EW_MAX, EW_MIN, EW_POW, EW_REM,
+  EW_ADD, EW_SUB, EW_MUL, EW_DIV, EW_MAX, EW_MIN, EW_POW, EW_REM, EW_ATAN2,
   // binary, int class
   EW_IADD, EW_ISUB, EW_IMUL, EW_IDIV, EW_IMAX, EW_IMIN, EW_IREM, EW_AND, EW_OR, EW_XOR,
   EW_UDIV, EW_UREM, EW_UMAX, EW_UMIN,
+  // shifts: imm.i = the element width in bits; the shift amount is read as unsigned, and one of at least the width
+  // gives 0 (left, logical) or the sign fill (arithmetic)
+  EW_SHL, EW_SRA, EW_SRL,
   // comparisons: imm.i = direction (0 EQ,1 NE,2 GE,3 GT,4 LE,5 LT)
   EW_FCMP, EW_ICMP, EW_UCMP,
   // ternary

@@ -172,6 +172,13 @@ __device__ __forceinline__ bool cmp_i(T x, T y, int dir) {
   }
 }
 
+// The low `w` bits (w in 1..32).
+__device__ __forceinline__ uint32_t width_mask(int w) { return w >= 32 ? 0xffffffffu : (1u << w) - 1u; }
+// The low `w` bits read as a w-bit two's complement integer.
+__device__ __forceinline__ int32_t sign_extend(uint32_t v, int w) {
+  return w >= 32 ? (int32_t)v : (int32_t)(v << (32 - w)) >> (32 - w);
+}
+
 __device__ __forceinline__ float f_logistic(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
 // Saturating float → int conversion (NaN → 0), truncating toward zero.
@@ -371,6 +378,11 @@ __device__ __noinline__ uint32_t ew_heavy(int op, uint32_t a, uint32_t b, int ro
     case EW_TANH: return __float_as_uint(tanhf(fa));
     case EW_EXPM1: return __float_as_uint(expm1f(fa));
     case EW_LOG1P: return __float_as_uint(log1pf(fa));
+    case EW_SIN: return __float_as_uint(sinf(fa));
+    case EW_COS: return __float_as_uint(cosf(fa));
+    case EW_TAN: return __float_as_uint(tanf(fa));
+    case EW_CBRT: return __float_as_uint(cbrtf(fa));
+    case EW_ATAN2: return __float_as_uint(atan2f(fa, fb));
     case EW_CVT_F2I: return (uint32_t)f2i_sat(fa, round);
     case EW_POW: return __float_as_uint(powf(fa, fb));
     case EW_REM: return __float_as_uint(fmodf(fa, fb));
@@ -422,7 +434,8 @@ __device__ __forceinline__ T uniform_read(const T* p) {
 __host__ __device__ inline bool ew_is_heavy(int op) {
   switch (op) {
     case EW_LOG: case EW_TANH: case EW_EXPM1: case EW_LOG1P: case EW_CVT_F2I: case EW_POW: case EW_REM:
-    case EW_IDIV: case EW_IREM: case EW_UDIV: case EW_UREM:
+    case EW_IDIV: case EW_IREM: case EW_UDIV: case EW_UREM: case EW_SIN: case EW_COS: case EW_TAN: case EW_CBRT:
+    case EW_ATAN2:
       return true;
     default:
       return false;
@@ -484,10 +497,21 @@ __device__ __forceinline__ void ew_run_v(const EwProgram& P, int64_t lin, const 
       EW_F(EW_SIGN, EW_FA != EW_FA ? EW_FA : (EW_FA > 0.f ? 1.f : (EW_FA < 0.f ? -1.f : EW_FA)))
       EW_HEAVY(EW_EXPM1)
       EW_HEAVY(EW_LOG1P)
+      EW_HEAVY(EW_SIN)
+      EW_HEAVY(EW_COS)
+      EW_HEAVY(EW_TAN)
+      EW_HEAVY(EW_CBRT)
+      EW_F(EW_RINT, rintf(EW_FA))
+      EW_F(EW_ROUND, roundf(EW_FA))
+      EW_U(EW_ISFINITE, (EW_UA & 0x7f800000u) != 0x7f800000u)
       EW_U(EW_INEG, -EW_IA)
       EW_U(EW_IABS, EW_IA < 0 ? -EW_IA : EW_IA)
       EW_U(EW_NOT, (I.round == DT_PRED) ? (uint32_t)(EW_IA == 0) : ~EW_UA)
       EW_U(EW_ISIGN, EW_IA > 0 ? 1 : (EW_IA < 0 ? -1 : 0))
+      // bit counts over the element's own width (a narrow signed register holds its value sign-extended)
+      EW_U(EW_POPCNT, __builtin_popcount(EW_UA & width_mask(I.imm.i)))
+      EW_U(EW_CLZ, (EW_UA & width_mask(I.imm.i)) ? __builtin_clz(EW_UA & width_mask(I.imm.i)) - (32 - I.imm.i)
+                                                  : I.imm.i)
       EW_F(EW_CVT_F2F, EW_FA)
       EW_HEAVY(EW_CVT_F2I)
       EW_F(EW_CVT_I2F, I.imm.i ? (float)EW_UA : (float)EW_IA)  // imm: source unsigned
@@ -502,6 +526,7 @@ __device__ __forceinline__ void ew_run_v(const EwProgram& P, int64_t lin, const 
       EW_F(EW_MIN, (EW_FA != EW_FA || EW_FB != EW_FB) ? __uint_as_float(0x7fc00000u) : fminf(EW_FA, EW_FB))
       EW_HEAVY(EW_POW)
       EW_HEAVY(EW_REM)
+      EW_HEAVY(EW_ATAN2)
       EW_U(EW_IADD, EW_IA + EW_IB)
       EW_U(EW_ISUB, EW_IA - EW_IB)
       EW_U(EW_IMUL, EW_IA * EW_IB)
@@ -516,6 +541,9 @@ __device__ __forceinline__ void ew_run_v(const EwProgram& P, int64_t lin, const 
       EW_U(EW_AND, EW_UA & EW_UB)
       EW_U(EW_OR, EW_UA | EW_UB)
       EW_U(EW_XOR, EW_UA ^ EW_UB)
+      EW_U(EW_SHL, EW_UB < (uint32_t)I.imm.i ? EW_UA << EW_UB : 0u)
+      EW_U(EW_SRL, EW_UB < (uint32_t)I.imm.i ? (EW_UA & width_mask(I.imm.i)) >> EW_UB : 0u)
+      EW_U(EW_SRA, sign_extend(EW_UA, I.imm.i) >> (EW_UB < (uint32_t)I.imm.i ? EW_UB : 31u))
       EW_U(EW_FCMP, cmp_f(EW_FA, EW_FB, I.imm.i))
       EW_U(EW_ICMP, cmp_i<int32_t>(EW_IA, EW_IB, I.imm.i))
       EW_U(EW_UCMP, cmp_i<uint32_t>(EW_UA, EW_UB, I.imm.i))

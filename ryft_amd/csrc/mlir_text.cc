@@ -36,6 +36,12 @@ const std::unordered_map<std::string, Op>& mlir_simple_ops() {
       {"power", Op::Power},         {"remainder", Op::Remainder}, {"and", Op::And},
       {"or", Op::Or},               {"xor", Op::Xor},         {"select", Op::Select},
       {"clamp", Op::Clamp},         {"reshape", Op::Reshape},
+      {"sine", Op::Sine},           {"cosine", Op::Cosine},   {"tan", Op::Tan},
+      {"cbrt", Op::Cbrt},           {"round_nearest_even", Op::RoundNearestEven},
+      {"round_nearest_afz", Op::RoundNearestAfz}, {"is_finite", Op::IsFinite},
+      {"popcnt", Op::Popcnt},       {"count_leading_zeros", Op::CountLeadingZeros},
+      {"atan2", Op::Atan2},         {"shift_left", Op::ShiftLeft},
+      {"shift_right_arithmetic", Op::ShiftRightArithmetic}, {"shift_right_logical", Op::ShiftRightLogical},
   };
   return m;
 }
@@ -67,6 +73,19 @@ const char* op_name(Op op) {
     case Op::Sign: return "sign";
     case Op::Expm1: return "exponential_minus_one";
     case Op::Log1p: return "log_plus_one";
+    case Op::Sine: return "sine";
+    case Op::Cosine: return "cosine";
+    case Op::Tan: return "tan";
+    case Op::Cbrt: return "cbrt";
+    case Op::RoundNearestEven: return "round_nearest_even";
+    case Op::RoundNearestAfz: return "round_nearest_afz";
+    case Op::IsFinite: return "is_finite";
+    case Op::Popcnt: return "popcnt";
+    case Op::CountLeadingZeros: return "count_leading_zeros";
+    case Op::Atan2: return "atan2";
+    case Op::ShiftLeft: return "shift_left";
+    case Op::ShiftRightArithmetic: return "shift_right_arithmetic";
+    case Op::ShiftRightLogical: return "shift_right_logical";
     case Op::Add: return "add";
     case Op::Subtract: return "subtract";
     case Op::Multiply: return "multiply";
@@ -103,7 +122,10 @@ bool op_is_elementwise(Op op) {
     case Op::Logistic: case Op::Not: case Op::Convert: case Op::Floor: case Op::Ceil: case Op::Sign: case Op::Expm1:
     case Op::Log1p: case Op::Add: case Op::Subtract: case Op::Multiply: case Op::Divide: case Op::Maximum:
     case Op::Minimum: case Op::Power: case Op::Remainder: case Op::And: case Op::Or: case Op::Xor: case Op::Compare:
-    case Op::Select: case Op::Clamp:
+    case Op::Select: case Op::Clamp: case Op::Sine: case Op::Cosine: case Op::Tan: case Op::Cbrt:
+    case Op::RoundNearestEven: case Op::RoundNearestAfz: case Op::IsFinite: case Op::Popcnt:
+    case Op::CountLeadingZeros: case Op::Atan2: case Op::ShiftLeft: case Op::ShiftRightArithmetic:
+    case Op::ShiftRightLogical:
       return true;
     default:
       return false;
@@ -1340,6 +1362,7 @@ void validate_node(const Graph& g, Node& n) {
         switch (n.op) {
           case Op::Add: case Op::Subtract: case Op::Multiply: case Op::Divide: case Op::Maximum: case Op::Minimum:
           case Op::Power: case Op::Remainder: case Op::And: case Op::Or: case Op::Xor: case Op::Compare:
+          case Op::Atan2: case Op::ShiftLeft: case Op::ShiftRightArithmetic: case Op::ShiftRightLogical:
             need(2);
             break;
           case Op::Clamp:
@@ -1355,6 +1378,35 @@ void validate_node(const Graph& g, Node& n) {
           if (t.shape != n.type.shape && !(scalar_ok && t.rank() == 0))
             invalid(std::string(op_name(n.op)) + ": operand shape " + shape_str(t.shape) + " does not match result " +
                     shape_str(n.type.shape));
+        }
+        // element types of the float-only and integer-only ops (trigonometric.rs:7-262, exponential.rs:166-210,
+        // rounding.rs:91-180, arithmetic.rs:470-515, bit_manipulation.rs:5-280)
+        auto all_types = [&](bool (*ok)(DType), const char* what, bool same_result) {
+          for (size_t i = 0; i < n.operands.size(); ++i) {
+            const DType t = opt((int)i).dtype;
+            if (!ok(t)) invalid(std::string(op_name(n.op)) + " requires " + what + " operands");
+            if (t != opt(0).dtype) invalid(std::string(op_name(n.op)) + ": operand element types differ");
+          }
+          if (same_result && n.type.dtype != opt(0).dtype)
+            invalid(std::string(op_name(n.op)) + ": result element type must match the operands'");
+        };
+        auto is_float = [](DType t) { return dtype_is_float(t); };
+        auto is_integer = [](DType t) { return dtype_is_int(t) && t != DType::PRED; };
+        switch (n.op) {
+          case Op::Sine: case Op::Cosine: case Op::Tan: case Op::Cbrt: case Op::RoundNearestEven:
+          case Op::RoundNearestAfz: case Op::Atan2:
+            all_types(is_float, "floating-point", true);
+            break;
+          case Op::IsFinite:
+            all_types(is_float, "floating-point", false);
+            if (n.type.dtype != DType::PRED) invalid("is_finite: the result element type must be i1");
+            break;
+          case Op::Popcnt: case Op::CountLeadingZeros: case Op::ShiftLeft: case Op::ShiftRightArithmetic:
+          case Op::ShiftRightLogical:
+            all_types(is_integer, "integer", true);
+            break;
+          default:
+            break;
         }
       }
       break;

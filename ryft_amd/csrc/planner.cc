@@ -348,6 +348,32 @@ ExprBuilder::Val ExprBuilder::emit(int node, const std::vector<int>& src) {
         out = un(m.at(n.op), m.at(n.op));
         break;
       }
+      case Op::Sine: case Op::Cosine: case Op::Tan: case Op::Cbrt: case Op::RoundNearestEven:
+      case Op::RoundNearestAfz: {
+        static const std::map<Op, EwOp> m = {{Op::Sine, EW_SIN}, {Op::Cosine, EW_COS}, {Op::Tan, EW_TAN},
+                                             {Op::Cbrt, EW_CBRT}, {Op::RoundNearestEven, EW_RINT},
+                                             {Op::RoundNearestAfz, EW_ROUND}};
+        out = un(m.at(n.op), m.at(n.op));
+        break;
+      }
+      case Op::Atan2: out = bin(EW_ATAN2, EW_ATAN2, EW_ATAN2); break;
+      case Op::IsFinite:
+        ins.op = EW_ISFINITE;
+        ins.round = 0;
+        out = {push(ins, false, {ops[0].instr}), false};
+        break;
+      case Op::Popcnt: case Op::CountLeadingZeros: case Op::ShiftLeft: case Op::ShiftRightArithmetic:
+      case Op::ShiftRightLogical: {
+        // the bit operations see the element's own width; 64-bit elements live in 32-bit registers here
+        if (dtype_size(ot) > 4) unimplemented(std::string(op_name(n.op)) + " on 64-bit integers is not supported");
+        ins.imm.i = (int32_t)(8 * dtype_size(ot));
+        if (n.op == Op::Popcnt) out = un(EW_POPCNT, EW_POPCNT);
+        else if (n.op == Op::CountLeadingZeros) out = un(EW_CLZ, EW_CLZ);
+        else if (n.op == Op::ShiftLeft) out = bin(EW_SHL, EW_SHL, EW_SHL);
+        else if (n.op == Op::ShiftRightArithmetic) out = bin(EW_SRA, EW_SRA, EW_SRA);
+        else out = bin(EW_SRL, EW_SRL, EW_SRL);
+        break;
+      }
       case Op::Compare:
         ins.op = float_class(ot) ? EW_FCMP
                                  : ((dtype_is_unsigned(ot) || n.cmp_type == CmpType::UNSIGNED) ? EW_UCMP : EW_ICMP);

@@ -9,7 +9,8 @@ from ryft_amd import pjrt
 MLIR_DT = {pjrt.BufferType.F32: "f32", pjrt.BufferType.BF16: "bf16", pjrt.BufferType.S8: "i8",
            pjrt.BufferType.S32: "i32", pjrt.BufferType.F8E4M3FN: "f8E4M3FN", pjrt.BufferType.F16: "f16",
            pjrt.BufferType.PRED: "i1", pjrt.BufferType.S64: "i64", pjrt.BufferType.U8: "ui8",
-           pjrt.BufferType.S16: "i16", pjrt.BufferType.F64: "f64", pjrt.BufferType.U32: "ui32"}
+           pjrt.BufferType.S16: "i16", pjrt.BufferType.F64: "f64", pjrt.BufferType.U32: "ui32",
+           pjrt.BufferType.U16: "ui16"}
 
 
 def run_pjrt(client, program: str, host_inputs, executable=None):

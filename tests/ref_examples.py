@@ -26,6 +26,7 @@ class Example:
     out_type: str
     want: list                             # documented result values
     attrs: str = ""                        # text after the operands (compare direction etc.)
+    atol: float = 0.0                      # documented values that are rounded decimals (sin(pi) printed as 0.0)
 
     def program(self) -> str:
         dims = "".join(f"{d}x" for d in self.shape)
@@ -91,6 +92,50 @@ EXAMPLES = [
             [[1.0, 5.0, 3.0], [2.0, 4.0, 6.0]], "f32", [1.0, 4.0, 3.0]),
     Example("compare_ge_f32", "comparison.rs:86-93", "compare", ["f32", "f32"], (2,), [[1.0, 3.0], [1.1, 2.9]], "i1",
             [0, 1], attrs="GE"),
+    Example("sqrt_f32", "exponential.rs:86-88", "sqrt", ["f32"], (2, 2), [[[0.0, 1.0], [4.0, 9.0]]], "f32",
+            [[0.0, 1.0], [2.0, 3.0]]),
+    # the documented 0.33333343 is 0.333333343 (the f32 nearest 1/3) with a digit dropped: checked to 1e-7
+    Example("rsqrt_f32", "exponential.rs:132-134", "rsqrt", ["f32"], (2, 2), [[[1.0, 4.0], [9.0, 25.0]]], "f32",
+            [[1.0, 0.5], [0.33333343, 0.2]], atol=1e-7),
+    # documented for f64 with f64 results: the f32 nearest each of them
+    Example("exponential_f32", "exponential.rs:225-227", "exponential", ["f32"], (2, 2), [[[0.0, 1.0], [2.0, 3.0]]],
+            "f32", [[1.0, 2.7182818284590451], [7.3890560989306504, 20.085536923187668]]),
+    Example("log_f32", "exponential.rs:320-322", "log", ["f32"], (2, 2), [[[1.0, 2.0], [3.0, 4.0]]], "f32",
+            [[0.0, 0.69314718055994529], [1.0986122886681098, 1.3862943611198906]]),
+    Example("logistic_f32", "exponential.rs:415-417", "logistic", ["f32"], (2, 2), [[[0.0, 1.0], [2.0, 3.0]]], "f32",
+            [[0.5, 0.73105858], [0.88079708, 0.95257413]]),
+    Example("tanh_f32", "trigonometric.rs:169-171", "tanh", ["f32"], (3,), [[-1.0, 0.0, 1.0]], "f32",
+            [-0.76159416, 0.0, 0.76159416]),
+    # sin / cos at the f32 values nearest 0, pi/2, pi and 3pi/2: the documented 0.0 / 1.0 / -1.0 are rounded
+    # decimals (sin of the f32 pi is -8.74e-08), so these two are checked to 1e-7
+    Example("sine_f32", "trigonometric.rs:14-24", "sine", ["f32"], (2, 2),
+            [[[0.0, 1.57079632], [3.14159265, 4.71238898]]], "f32", [[0.0, 1.0], [0.0, -1.0]], atol=1e-7),
+    Example("cosine_f32", "trigonometric.rs:63-73", "cosine", ["f32"], (2, 2),
+            [[[0.0, 1.57079632], [3.14159265, 4.71238898]]], "f32", [[1.0, 0.0], [-1.0, 0.0]], atol=1e-7),
+    # documented as tensor<4xf64> with three values; 1.57079637 is the f32 nearest pi/2
+    Example("atan2_f32", "trigonometric.rs:210-224", "atan2", ["f32", "f32"], (3,),
+            [[0.0, 1.0, -1.0], [0.0, 0.0, 0.0]], "f32", [0.0, 1.57079637, -1.57079637]),
+    Example("cbrt_f32", "exponential.rs:173-181", "cbrt", ["f32"], (4,), [[0.0, 1.0, 8.0, 27.0]], "f32",
+            [0.0, 1.0, 2.0, 3.0]),
+    Example("round_nearest_afz_f32", "rounding.rs:100-108", "round_nearest_afz", ["f32"], (5,),
+            [[-2.5, 0.4, 0.5, 0.6, 2.5]], "f32", [-3.0, 0.0, 1.0, 1.0, 3.0]),
+    # documented as tensor<6xf32> with five values
+    Example("round_nearest_even_f32", "rounding.rs:145-153", "round_nearest_even", ["f32"], (5,),
+            [[-2.5, 0.4, 0.5, 0.6, 2.5]], "f32", [-2.0, 0.0, 0.0, 1.0, 2.0]),
+    Example("is_finite_f32", "arithmetic.rs:482-490", "is_finite", ["f32"], (5,), [[0.0, 1.0, INF, -INF, NAN]], "i1",
+            [1, 1, 0, 0, 0]),
+    Example("shift_left_i32", "bit_manipulation.rs:10-19", "shift_left", ["i32", "i32"], (3,),
+            [[-1, 0, 1], [1, 2, 3]], "i32", [-2, 0, 8]),
+    Example("shift_right_arithmetic_i32", "bit_manipulation.rs:74-84", "shift_right_arithmetic", ["i32", "i32"],
+            (3,), [[-1, 0, 8], [1, 2, 3]], "i32", [-1, 0, 1]),
+    # documented as tensor<3xi32> with the i64 result 9223372036854775807 for -1 >> 1; the i32 result is 2^31 - 1
+    Example("shift_right_logical_i32", "bit_manipulation.rs:139-149", "shift_right_logical", ["i32", "i32"], (3,),
+            [[-1, 0, 8], [1, 2, 3]], "i32", [2147483647, 0, 1]),
+    # documented for i64 ([[64, 63], [56, 0]]): the same values at 32 bits
+    Example("count_leading_zeros_i32", "bit_manipulation.rs:202-209", "count_leading_zeros", ["i32"], (2, 2),
+            [[[0, 1], [128, -1]]], "i32", [[32, 31], [24, 0]]),
+    Example("popcnt_i32", "bit_manipulation.rs:243-250", "popcnt", ["i32"], (4,), [[0, 1, 2, 127]], "i32",
+            [0, 1, 1, 7]),
 ]
 
 
@@ -98,7 +143,8 @@ def f32(v):
     return np.asarray(v, dtype=np.float64).astype(np.float32)
 
 
-TRANSCENDENTAL = {"power", "exponential_minus_one", "log_plus_one"}
+TRANSCENDENTAL = {"power", "exponential_minus_one", "log_plus_one", "sine", "cosine", "tan", "atan2", "cbrt",
+                  "exponential", "log", "logistic", "tanh"}
 
 
 def check_values(got, ex: Example, ulps: int = 0):
@@ -112,6 +158,9 @@ def check_values(got, ex: Example, ulps: int = 0):
         w = f32(want)
         nan = np.isnan(w)
         assert np.array_equal(np.isnan(g), nan), (ex.name, g, w)
+        if ex.atol:
+            assert np.all(np.abs(g[~nan].astype(np.float64) - w[~nan]) <= ex.atol), (ex.name, g, w)
+            return
         assert np.array_equal(np.signbit(g[~nan]), np.signbit(w[~nan])), (ex.name, "signs", g, w)
         gi, wi = g[~nan].view(np.int32).astype(np.int64), w[~nan].view(np.int32).astype(np.int64)
         assert np.all(np.abs(gi - wi) <= ulps), (ex.name, g, w)

@@ -105,13 +105,13 @@ def test_unsupported_op_in_bytecode_is_unimplemented(compile_client):
     T = "tensor<8xf32>"
     text = f"""module {{
   func.func @main(%arg0: {T}) -> {T} {{
-    %0 = stablehlo.sine %arg0 : {T}
+    %0 = stablehlo.real %arg0 : {T}
     return %0 : {T}
   }}
 }}
 """
     err = _error(compile_client, mb.to_bytecode(text))
-    assert err.code == pjrt.ErrorCode.UNIMPLEMENTED and "stablehlo.sine" in err.message
+    assert err.code == pjrt.ErrorCode.UNIMPLEMENTED and "stablehlo.real" in err.message
 
 
 def test_missing_entry_function_is_invalid_argument(compile_client):

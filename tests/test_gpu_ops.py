@@ -289,7 +289,7 @@ _NP = {"f32": np.float32, "i32": np.int32, "i8": np.int8, "i1": np.bool_}
 @pytest.mark.parametrize("ex", EXAMPLES, ids=[e.name for e in EXAMPLES])
 def test_reference_worked_examples(gpu_client, ex):
     """The reference's documented example of each op (tests/ref_examples.py) on the GPU: bit-exact, except 2 ulps of
-    slack for power / expm1 / log1p (device libm)."""
+    slack for the ops computed by device libm (tests/ref_examples.py's TRANSCENDENTAL)."""
     ins = [configs.HostInput(np.asarray(v, dtype=np.float64).astype(_NP[t]), _BT[t], ex.shape)
            for v, t in zip(ex.inputs, ex.in_types)]
     outs, _ = run_pjrt(gpu_client, ex.program(), ins)
@@ -423,3 +423,146 @@ def test_direct_unary_maps(gpu_client, case):
         prog, ins = _mod([T], [T], f"    %0 = stablehlo.{op} %arg0 : {T}\n    return %0 : {T}"), [_map_input(72, shape, dt)]
     outs, _ = run_pjrt(gpu_client, prog, ins)
     _same_bits(outs[0], oracle_outputs(prog, ins)[0], case)
+
+
+# ------------------------------------------------------------------ trigonometric, rounding and bit operations
+def _within_ulps(got_raw, want, ulps, name):
+    """Equal NaN positions and infinities; finite values within `ulps` units in the last place of the oracle's value
+    at the result type (device libm against float64 rounded once)."""
+    vals, dt = want
+    got = sh.from_raw(got_raw, dt)
+    nan = np.isnan(vals)
+    assert np.array_equal(np.isnan(got), nan), f"{name}: NaN positions differ"
+    g, w = got[~nan], vals[~nan]
+    inf = np.isinf(w)
+    assert np.array_equal(g[inf], w[inf]), f"{name}: infinities differ"
+    unit = np.spacing(np.abs(w[~inf]).astype(np.float32)).astype(np.float64) * (65536.0 if dt == "bf16" else 1.0)
+    err = np.abs(g[~inf] - w[~inf]) / unit
+    assert np.all(err <= ulps), f"{name}: {np.count_nonzero(err > ulps)} values beyond {ulps} ulps (max {err.max()})"
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("shape", [(8, 33), (4, 2048)])
+def test_trigonometric_cbrt_rounding_is_finite(gpu_client, dt, shape):
+    """sine, cosine, tan, cbrt and atan2 within 4 ulps (f32) or 1 ulp (bf16, one rounding of the f32 result) of the
+    oracle; round_nearest_even, round_nearest_afz and is_finite bit-exact; NaN, infinities, signed zeros,
+    subnormals and 3e38 among the operands."""
+    T, P = _t(shape, dt), _t(shape, "i1")
+    ops = ["sine", "cosine", "tan", "cbrt", "round_nearest_even", "round_nearest_afz"]
+    body = "".join(f"    %{i} = stablehlo.{op} %arg0 : {T}\n" for i, op in enumerate(ops))
+    body += f"    %6 = stablehlo.atan2 %arg0, %arg1 : {T}\n"
+    body += f"    %7 = stablehlo.is_finite %arg0 : ({T}) -> {P}\n"
+    body += "    return " + ", ".join(f"%{i}" for i in range(8)) + " : " + ", ".join([T] * 7 + [P])
+    prog = _mod([T, T], [T] * 7 + [P], body)
+    ins = [_map_input(81, shape, dt), _map_input(82, shape, dt)]
+    print(f"[ops] trig/round {dt} {shape}", flush=True)
+    outs, _ = run_pjrt(gpu_client, prog, ins)
+    want = oracle_outputs(prog, ins)
+    for i, name in enumerate(ops + ["atan2"]):
+        if name.startswith("round"):
+            _same_bits(outs[i], want[i], f"{dt} {name}")
+        else:
+            _within_ulps(outs[i], want[i], 4 if dt == "f32" else 1, f"{dt} {name}")
+    check(outs[7], want[7], 0, "is_finite")
+
+
+_INT_TYPES = {"i8": (np.int8, pjrt.BufferType.S8), "ui8": (np.uint8, pjrt.BufferType.U8),
+              "i16": (np.int16, pjrt.BufferType.S16), "ui16": (np.uint16, pjrt.BufferType.U16),
+              "i32": (np.int32, pjrt.BufferType.S32), "ui32": (np.uint32, pjrt.BufferType.U32)}
+
+
+@pytest.mark.parametrize("dt", list(_INT_TYPES))
+@pytest.mark.parametrize("shape", [(8, 33), (4, 1024)])
+def test_bit_operations(gpu_client, dt, shape):
+    """shift_left / shift_right_arithmetic / shift_right_logical by amounts inside and outside the width (negative
+    ones too), popcnt and count_leading_zeros, bit-exact against the oracle at every integer width."""
+    npt, bt = _INT_TYPES[dt]
+    info, w = np.iinfo(npt), np.iinfo(npt).bits
+    rng = np.random.default_rng(w + 3 * (dt[0] == "u"))
+    a = rng.integers(info.min, info.max, size=shape, endpoint=True).astype(npt)
+    a.reshape(-1)[:4] = [info.min, info.max, 0, 1]
+    k = rng.integers(max(info.min, -3), w + 3, size=shape).astype(npt)
+    T = _t(shape, dt)
+    ops = ["shift_left", "shift_right_arithmetic", "shift_right_logical"]
+    body = "".join(f"    %{i} = stablehlo.{op} %arg0, %arg1 : {T}\n" for i, op in enumerate(ops))
+    body += f"    %3 = stablehlo.popcnt %arg0 : {T}\n    %4 = stablehlo.count_leading_zeros %arg0 : {T}\n"
+    body += "    return %0, %1, %2, %3, %4 : " + ", ".join([T] * 5)
+    prog = _mod([T, T], [T] * 5, body)
+    ins = [configs.HostInput(a, bt, shape), configs.HostInput(k, bt, shape)]
+    print(f"[ops] bits {dt} {shape}", flush=True)
+    outs, _ = run_pjrt(gpu_client, prog, ins)
+    for o, want, name in zip(outs, oracle_outputs(prog, ins), ops + ["popcnt", "count_leading_zeros"]):
+        check(o, want, 0, f"{dt} {name}")
+
+
+@pytest.mark.parametrize("dt", ["i8", "ui8"])
+def test_shifts_over_every_8bit_pair(gpu_client, dt):
+    npt, bt = _INT_TYPES[dt]
+    vals = np.arange(np.iinfo(npt).min, np.iinfo(npt).max + 1)
+    a, k = (x.astype(npt) for x in np.meshgrid(vals, vals, indexing="ij"))
+    T = _t((256, 256), dt)
+    ops = ["shift_left", "shift_right_arithmetic", "shift_right_logical"]
+    body = "".join(f"    %{i} = stablehlo.{op} %arg0, %arg1 : {T}\n" for i, op in enumerate(ops))
+    body += "    return %0, %1, %2 : " + ", ".join([T] * 3)
+    prog = _mod([T, T], [T] * 3, body)
+    ins = [configs.HostInput(a, bt, (256, 256)), configs.HostInput(k, bt, (256, 256))]
+    outs, _ = run_pjrt(gpu_client, prog, ins)
+    for o, want, name in zip(outs, oracle_outputs(prog, ins), ops):
+        check(o, want, 0, f"{dt} {name}")
+
+
+def test_counter_hash_rounds_ui32(gpu_client):
+    """A counter-based hash in the style of threefry's rounds (add, rotate by shift_left | shift_right_logical, xor)
+    over an iota counter and a key, bit-exact against the same rounds in numpy's uint32 arithmetic."""
+    n = 1 << 14
+    U = f"tensor<{n}xui32>"
+    S = "tensor<ui32>"
+    lines = [f"    %x0 = stablehlo.iota dim = 0 : {U}",
+             f"    %k = stablehlo.broadcast_in_dim %arg0, dims = [] : ({S}) -> {U}",
+             f"    %y0 = stablehlo.xor %x0, %k : {U}"]
+    x, y = "%x0", "%y0"
+    rots = [13, 15, 26, 6]
+    for i, r in enumerate(rots):
+        lines += [f"    %r{i} = stablehlo.constant dense<{r}> : {U}",
+                  f"    %q{i} = stablehlo.constant dense<{32 - r}> : {U}",
+                  f"    %s{i} = stablehlo.add {x}, {y} : {U}",
+                  f"    %l{i} = stablehlo.shift_left {y}, %r{i} : {U}",
+                  f"    %h{i} = stablehlo.shift_right_logical {y}, %q{i} : {U}",
+                  f"    %o{i} = stablehlo.or %l{i}, %h{i} : {U}",
+                  f"    %t{i} = stablehlo.xor %o{i}, %s{i} : {U}"]
+        x, y = f"%s{i}", f"%t{i}"
+    lines.append(f"    return {x}, {y} : {U}, {U}")
+    prog = _mod([S], [U, U], "\n".join(lines))
+    key = np.uint32(0x1BD11BDA)
+    outs, _ = run_pjrt(gpu_client, prog, [configs.HostInput(np.array(key), pjrt.BufferType.U32, ())])
+    xs = np.arange(n, dtype=np.uint32)
+    ys = xs ^ key
+    for r in rots:
+        xs = xs + ys
+        ys = ((ys << np.uint32(r)) | (ys >> np.uint32(32 - r))) ^ xs
+    assert np.array_equal(outs[0].view(np.uint32), xs) and np.array_equal(outs[1].view(np.uint32), ys)
+
+
+def test_rotary_angles_from_positions_bf16(gpu_client):
+    """Rotary position angles computed in the program: positions (iota) times per-column frequencies, cosine and
+    sine fused with the bf16 products x·cos + y·sin; against the oracle to bf16 rounding."""
+    S, D = 512, 128
+    X, F, A = f"tensor<{S}x{D}xbf16>", f"tensor<{D}xf32>", f"tensor<{S}x{D}xf32>"
+    body = f"""    %p = stablehlo.iota dim = 0 : {A}
+    %f = stablehlo.broadcast_in_dim %arg2, dims = [1] : ({F}) -> {A}
+    %a = stablehlo.multiply %p, %f : {A}
+    %c = stablehlo.cosine %a : {A}
+    %s = stablehlo.sine %a : {A}
+    %x = stablehlo.convert %arg0 : ({X}) -> {A}
+    %y = stablehlo.convert %arg1 : ({X}) -> {A}
+    %xc = stablehlo.multiply %x, %c : {A}
+    %ys = stablehlo.multiply %y, %s : {A}
+    %r = stablehlo.add %xc, %ys : {A}
+    %o = stablehlo.convert %r : ({A}) -> {X}
+    return %o : {X}"""
+    prog = _mod([X, X, F], [X], body)
+    freqs = (10000.0 ** (-np.arange(D) / D)).astype(np.float32)
+    ins = [configs.HostInput(hd.f32_to_bf16_bits(hd.normal(91 + i, (S, D))), pjrt.BufferType.BF16, (S, D))
+           for i in range(2)] + [configs.HostInput(freqs, pjrt.BufferType.F32, (D,))]
+    outs, _ = run_pjrt(gpu_client, prog, ins)
+    check(outs[0], oracle_outputs(prog, ins)[0], 4e-3, "rotary bf16")
