@@ -145,14 +145,22 @@ class Module:
             if not ln or ln.startswith("//") or ln == "}":
                 continue
             if "reducer(" in ln or (ln.startswith("%") and "stablehlo.reduce(" in ln and "applies" not in ln):
-                # region form: collect up to the closing brace of the reducer block
+                # pretty region form: collect up to the closing brace of the reducer block (line breaks kept)
                 block = [ln]
                 while "}" not in lines[i - 1] or len(block) == 1:
                     block.append(lines[i].strip())
                     i += 1
                     if block[-1].startswith("}"):
                         break
-                out.append(" ".join(block))
+                out.append("\n".join(block))
+                continue
+            if ln.startswith("%") and '"stablehlo.reduce"(' in ln and "({" in ln:
+                # generic region form: up to the line that closes the region, `}) ... : (...) -> (...)`
+                block = [ln]
+                while not block[-1].startswith("})"):
+                    block.append(lines[i].strip())
+                    i += 1
+                out.append("\n".join(block))
                 continue
             out.append(ln)
         return out
@@ -182,18 +190,22 @@ def evaluate(text: str, inputs: Sequence[np.ndarray], dot_precision: str = "f64"
         if r:
             names = re.findall(r"%[\w.$#-]+", r.group(1))
             return [env[n] for n in names]
-        m = re.match(r"(%[\w.$-]+)\s*=\s*(?:stablehlo|mhlo)\.(\w+)\s*(.*)$", st)
-        if not m:
+        m = re.match(r"(%[\w.$-]+)(?::\d+)?\s*=\s*(?:stablehlo|mhlo)\.(\w+)\s*(.*)$", st, re.S)
+        if m:
+            res, op, rest = m.group(1), m.group(2), m.group(3)
+        else:
             # the generic form `%r = "stablehlo.op"(%a, %b) <{attrs}> : (types) -> type`, handed on as
             # `%a, %b <{attrs}> : (types) -> type`
-            m = re.match(r'(%[\w.$-]+)\s*=\s*"(?:stablehlo|mhlo)\.(\w+)"\((.*?)\)\s*(.*)$', st)
-            if m:
-                env[m.group(1)] = _eval_op(m.group(2), m.group(3) + " " + m.group(4), env, dot_precision)
-                continue
-        if not m:
-            raise ValueError(f"cannot parse statement: {st}")
-        res, op, rest = m.group(1), m.group(2), m.group(3)
-        env[res] = _eval_op(op, rest, env, dot_precision)
+            m = re.match(r'(%[\w.$-]+)(?::\d+)?\s*=\s*"(?:stablehlo|mhlo)\.(\w+)"\((.*?)\)\s*(.*)$', st, re.S)
+            if not m:
+                raise ValueError(f"cannot parse statement: {st}")
+            res, op, rest = m.group(1), m.group(2), m.group(3) + " " + m.group(4)
+        val = _eval_op(op, rest, env, dot_precision)
+        if isinstance(val, list):  # a multi-result op (`%r:2 = ...`): %r#0, %r#1, ...
+            for k, v in enumerate(val):
+                env[f"{res}#{k}"] = v
+        else:
+            env[res] = val
     raise ValueError("function has no return")
 
 
@@ -367,10 +379,15 @@ def _eval_op(op: str, rest: str, env, dot_precision: str) -> Tuple[np.ndarray, s
     if op == "compare":
         # comparison.rs:44-135
         m = re.match(r"(\w+)\s*,\s*(%[\w.$-]+)\s*,\s*(%[\w.$-]+)", rest)
-        a, _ = env[m.group(2)]
-        b, _ = env[m.group(3)]
+        if m:
+            direction, an, bn = m.group(1), m.group(2), m.group(3)
+        else:  # generic: `%a, %b <{comparison_direction = #stablehlo<comparison_direction GT>, ...}> : ...`
+            an, bn = re.findall(r"%[\w.$-]+", rest.split("<{")[0])[:2]
+            direction = re.search(r"\b(EQ|NE|GE|GT|LE|LT)\b", rest).group(1)
+        a, _ = env[an]
+        b, _ = env[bn]
         fn = {"EQ": np.equal, "NE": np.not_equal, "GE": np.greater_equal, "GT": np.greater, "LE": np.less_equal,
-              "LT": np.less}[m.group(1)]
+              "LT": np.less}[direction]
         return fn(a, b).astype(np.int64), "i1"
     if op == "select":
         # control_flow.rs:216-300: pred ? on_true : on_false (a scalar predicate selects whole tensors)
@@ -527,18 +544,89 @@ def _dot_general(rest, env, out_shape, out_dt, dot_precision):
 
 
 def _reduce(rest, env, out_shape, out_dt):
-    """functional.rs:109-135: reduce `dimensions` of the input with the body, starting from the init value; the
-    combination order is implementation-defined (sums here are exact-as-float64 then rounded once)."""
-    m = re.match(r"\((%[\w.$-]+)\s+init:\s*(%[\w.$-]+)\)\s*(?:applies\s+stablehlo\.(\w+))?\s*across\s+dimensions\s*=\s*\[(.*?)\]", rest)
-    x, dt = env[m.group(1)]
-    init, _ = env[m.group(2)]
-    body = m.group(3)
-    if body is None:
-        bm = re.search(r"stablehlo\.(add|maximum|minimum|multiply|and|or)\s", rest[m.end():])
-        body = bm.group(1)
-    dims = tuple(_ints(m.group(4)))
-    init = np.asarray(init).reshape(())
-    x = np.asarray(x)
+    """functional.rs:109-230: reduce `dimensions` of N inputs together, starting from their N init values, with the
+    body; the combination order is implementation-defined. One input with a single-op body (`applies`, or a region
+    applying one op to its two arguments): numpy's reduction of the whole axis set (sums exact as float64, rounded
+    once). Otherwise (several inputs, e.g. argmax's (value, index) pairs, or a longer body): the body's statements
+    are evaluated element by element in index order over the reduced dims, acc = body(acc, x), acc starting at the
+    init values. Returns one (values, dtype) per result (a list when N > 1)."""
+    head = rest.split("\n")[0]
+    pairs = re.findall(r"\((%[\w.$-]+)\s+init:\s*(%[\w.$-]+)\)", head)
+    applies = re.search(r"applies\s+stablehlo\.(\w+)", head)
+    if pairs:  # pretty form
+        inputs, inits = [p[0] for p in pairs], [p[1] for p in pairs]
+        dims = tuple(_ints(re.search(r"across\s+dimensions\s*=\s*\[(.*?)\]", head).group(1)))
+        types = _types(head[head.index(":"):])
+        region = None if applies else rest[rest.index("reducer"):]
+    else:  # generic form: `%a, %b, %c, %d <{dimensions = ...}> ({ ^bb0(...): ... }) : (...) -> (...)`
+        names = re.findall(r"%[\w.$-]+", rest[:rest.index("(")] if "(" in rest else rest)
+        inputs, inits = names[:len(names) // 2], names[len(names) // 2:]
+        dm = re.search(r"dimensions\s*=\s*(array<[^>]*>|dense<[^>]*>|\[[^\]]*\])", rest)
+        dims = tuple(_ints(dm.group(1).split(":", 1)[1] if dm.group(1).startswith("array") else dm.group(1)))
+        types = _types(rest[rest.rindex("})"):])
+        region = rest[rest.index("^bb"):rest.rindex("})")]
+    n = len(inputs)
+    res_types = types[-n:]
+    body = _region(region, n) if region is not None else None
+    single = applies.group(1) if applies else (body[2] if body is not None and n == 1 else None)
+    if n == 1 and single in ("add", "multiply", "maximum", "minimum", "and", "or"):
+        x, dt = env[inputs[0]]
+        return _reduce_single(single, np.asarray(x), dt, np.asarray(env[inits[0]][0]).reshape(()), dims,
+                              res_types[0][1])
+    args, stmts, _, rets = body
+    xs, accs = [], []
+    for i in range(n):
+        x, dt = env[inputs[i]]
+        x = np.asarray(x)
+        kept = [d for d in range(x.ndim) if d not in dims]
+        x = np.transpose(x, kept + sorted(dims))
+        shape = x.shape[:len(kept)]
+        xs.append((x.reshape(shape + (-1,)), dt))
+        accs.append((np.broadcast_to(np.asarray(env[inits[i]][0]).reshape(()), shape).copy(), dt))
+    for r in range(xs[0][0].shape[-1]):
+        benv = dict(zip(args, accs + [(x[..., r], dt) for x, dt in xs]))
+        for st in stmts:
+            m = re.match(r"(%[\w.$-]+)\s*=\s*(?:stablehlo|mhlo)\.(\w+)\s*(.*)$", st, re.S)
+            if m:
+                benv[m.group(1)] = _eval_op(m.group(2), m.group(3), benv, "f64")
+                continue
+            m = re.match(r'(%[\w.$-]+)\s*=\s*"(?:stablehlo|mhlo)\.(\w+)"\((.*?)\)\s*(.*)$', st, re.S)
+            benv[m.group(1)] = _eval_op(m.group(2), m.group(3) + " " + m.group(4), benv, "f64")
+        accs = [(np.asarray(benv[v][0]), res_types[i][1]) for i, v in enumerate(rets)]
+    out = [(normalize(np.asarray(a), dt), dt) for a, dt in accs]
+    return out if n > 1 else out[0]
+
+
+def _region(text, n):
+    """A reduce body: (block arguments in order, body statements, the single op of a one-op body or None, returned
+    names). Pretty `reducer(%a0: T, %b0: T) (%a1: U, %b1: U) { ... }` lists one (first, second) pair per input: the
+    block arguments are the pairs' first members, then their second members. Generic `^bb0(%x: T, ...): ...`."""
+    first_line, _, body = text.partition("\n")
+    if text.startswith("reducer"):
+        pairs = re.findall(r"\((%[\w.$-]+)\s*:\s*tensor<[^>]*>\s*,\s*(%[\w.$-]+)\s*:\s*tensor<[^>]*>\)", first_line)
+        args = [p[0] for p in pairs] + [p[1] for p in pairs]
+    else:
+        args = re.findall(r"(%[\w.$-]+)\s*:", first_line[:first_line.index(")")])
+    assert len(args) == 2 * n, (args, n)
+    stmts, rets = [], None
+    for ln in body.split("\n"):
+        ln = ln.strip()
+        if not ln or ln.startswith("}") or ln.startswith("{"):
+            continue
+        rm = re.match(r'"?stablehlo\.return"?\s*\(?(.*?)\)?\s*:', ln)
+        if rm:
+            rets = re.findall(r"%[\w.$-]+", rm.group(1))
+            break
+        stmts.append(ln)
+    single = None
+    if len(stmts) == 1:
+        m = re.match(r'%[\w.$-]+\s*=\s*"?stablehlo\.(\w+)"?\s*\(?\s*(%[\w.$-]+)\s*,\s*(%[\w.$-]+)', stmts[0])
+        if m and sorted(m.group(2, 3)) == sorted(args):
+            single = m.group(1)
+    return args, stmts, single, rets
+
+
+def _reduce_single(body, x, dt, init, dims, out_dt):
     if dt in FLOAT:
         x = x.astype(np.float64)
         with np.errstate(all="ignore"):

@@ -52,7 +52,8 @@ bool op_is_elementwise(Op op);  // one output element depends on the same-index 
 
 enum class CmpDir : uint8_t { EQ, NE, GE, GT, LE, LT };
 enum class CmpType : uint8_t { NOTYPE, FLOAT, TOTALORDER, SIGNED, UNSIGNED };
-enum class ReduceBody : uint8_t { Add, Max, Min, Mul, And, Or };
+// A reduce body that is one binary op of its two block arguments, or General: any other body (kept as a graph).
+enum class ReduceBody : uint8_t { Add, Max, Min, Mul, And, Or, General };
 
 struct DotDims {
   std::vector<int64_t> lhs_batch, rhs_batch, lhs_contract, rhs_contract;
@@ -64,6 +65,8 @@ struct GatherDims {
       start_index_map;
   int64_t index_vector_dim = 0;
 };
+
+struct Graph;
 
 struct Node {
   Op op;
@@ -82,6 +85,12 @@ struct Node {
   DType dot_lhs_precision = DType::INVALID;  // algorithm lhs/rhs_precision_type, if given
   DType dot_rhs_precision = DType::INVALID;
   ReduceBody reduce_body = ReduceBody::Add;
+  // reduce with N inputs (operands: the N inputs, then their N init values): a node per result, `result_index`
+  // naming it; the nodes of one op share operands, dimensions and body. `body` (ReduceBody::General) is the body
+  // region as a graph of rank-0 values: its parameters are the block arguments (the N accumulated values, then the
+  // N values folded in), its results the N new accumulated values.
+  int result_index = 0;
+  std::shared_ptr<const Graph> body;
   int param_index = -1;
   // constant payload: raw little-endian bytes in `type.dtype`; splat constants hold one element
   std::vector<uint8_t> literal;

@@ -107,6 +107,29 @@ struct ReduceArgs {
   const void* init_ptr;  // non-null: the init value is a device scalar (a program argument)
 };
 
+// A reduce whose body is not one of the ReduceKinds, over N ≤ RED_MAX_N inputs at once (argmax / argmin pair a value
+// with its index): the prologue yields the N input values at (o, r) in its output registers, and the body program
+// combines them into the running values — it reads the N accumulated values as EW_ACC 0..N-1 and the N values
+// folded in as EW_ACC N..2N-1, and leaves the N new accumulated values in its output registers (no leaves, no
+// stores). Every output's elements are folded in some tree order, then the init values are folded with the result
+// (init first): the order StableHLO leaves to the implementation.
+#define RED_MAX_N 2
+struct ReduceBodyArgs {
+  EwProgram prologue;
+  EwProgram body;
+  int64_t outer;                    // number of output elements
+  int64_t inner;                    // reduced elements per output
+  int32_t n;                        // inputs / results
+  int32_t pad_;
+  uint32_t init[RED_MAX_N];         // init values as register bits, when init_ptr is null
+  const void* init_ptr[RED_MAX_N];  // non-null: the init value is a device scalar of init_dtype
+  int32_t init_dtype[RED_MAX_N];
+  int32_t out_dtype[RED_MAX_N];
+  int32_t out_float[RED_MAX_N];     // the result register holds float bits
+  int32_t pad2_[2];
+  void* out[RED_MAX_N];             // contiguous over `outer`
+};
+
 // ------------------------------------------------------------------------------------------------ row fusion
 // Reductions over the innermost dimension whose results are broadcast back along that dimension into an elementwise
 // consumer over the same [rows, inner] space (RMSNorm, LayerNorm, an unfused softmax), run as one kernel: each row

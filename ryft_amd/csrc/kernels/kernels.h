@@ -15,6 +15,7 @@ hipEvent_t& pending_start();
 // `done` (optional): an event the launcher records on `stream` after its last kernel, as part of that launch.
 void launch_elementwise(const EwProgram& p, hipStream_t stream, hipEvent_t done = nullptr);
 void launch_reduce(const ReduceArgs& a, hipStream_t stream, hipEvent_t done = nullptr);
+void launch_reduce_body(const ReduceBodyArgs& a, hipStream_t stream, hipEvent_t done = nullptr);
 void launch_row(const RowArgs& a, hipStream_t stream, hipEvent_t done = nullptr);
 void launch_gemm(const GemmArgs& a, hipStream_t stream, hipEvent_t done = nullptr);
 void launch_attention(const AttnArgs& a, hipStream_t stream, hipEvent_t done = nullptr);

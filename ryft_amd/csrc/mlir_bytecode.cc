@@ -921,6 +921,39 @@ class BytecodeParser {
         }
       }
     }
+    build_ops(body, g, node_of);
+    if (g.results.empty()) invalid("function @" + entry + " returns nothing");
+    return g;
+  }
+
+  // A reduce body region → a graph of rank-0 values (block arguments as its parameters, in order); values of the
+  // enclosing function are not visible inside.
+  std::shared_ptr<Graph> build_region(const BRegion& r) {
+    if (r.blocks.size() != 1) invalid("reduce: expected a one-block body");
+    const BBlock& b = r.blocks[0];
+    auto g = std::make_shared<Graph>();
+    std::map<int64_t, int> node_of;
+    for (size_t k = 0; k < b.args.size(); ++k) {
+      Node n;
+      n.op = Op::Parameter;
+      n.type = tensor_type(b.arg_types[k]);
+      n.param_index = (int)k;
+      g->nodes.push_back(std::move(n));
+      g->params.push_back((int)g->nodes.size() - 1);
+      node_of[b.args[k]] = (int)g->nodes.size() - 1;
+    }
+    if (b.args.empty()) invalid("reduce body without block arguments");
+    build_ops(b, *g, node_of);
+    if (g->results.empty()) invalid("reduce body returns nothing");
+    return g;
+  }
+
+  // The ops of one block into `g`, up to its return (whose operands become g's results).
+  void build_ops(const BBlock& body, Graph& g, std::map<int64_t, int>& node_of) {
+    auto add = [&](Node n) {
+      g.nodes.push_back(std::move(n));
+      return (int)g.nodes.size() - 1;
+    };
     auto value = [&](int64_t v) {
       auto it = node_of.find(v);
       if (it == node_of.end()) unimplemented("an operand is not produced by a supported op");
@@ -934,6 +967,20 @@ class BytecodeParser {
       }
       if (op.name.rfind("stablehlo.", 0) != 0) unimplemented(op.name + " is not supported by the MI355X plugin");
       const std::string nm = op.name.substr(10);
+      if (nm == "reduce") {
+        // reduce (functional.rs:109-230): a node per result, sharing operands, dimensions and body
+        Node n;
+        n.debug = "%" + std::to_string(g.nodes.size());
+        for (int64_t v : op.operands) n.operands.push_back(value(v));
+        n.dims = int_list(op, "dimensions");
+        if (op.regions.size() != 1) invalid("reduce: expected one body region");
+        std::vector<TensorType> results;
+        for (int t : op.result_types) results.push_back(tensor_type(t));
+        std::vector<Node> nodes = mlir_reduce_nodes(g, n, results, std::string(), build_region(op.regions[0]));
+        if (op.results.size() != nodes.size()) invalid("reduce: result count mismatch");
+        for (size_t i = 0; i < nodes.size(); ++i) node_of[op.results[i]] = add(std::move(nodes[i]));
+        continue;
+      }
       if (op.result_types.size() != 1) unimplemented(op.name + " with " + std::to_string(op.result_types.size()) + " results is not supported");
       auto make_node = [&](const BOp& op) {
         Node n;
@@ -998,25 +1045,6 @@ class BytecodeParser {
               n.cmp_type = mlir_cmp_type_text(t->str);
             }
           }
-        } else if (nm == "reduce") {
-          n.op = Op::Reduce;
-          if (n.operands.size() != 2) unimplemented("variadic reduce is not supported");
-          n.dims = int_list(op, "dimensions");
-          if (op.regions.size() != 1 || op.regions[0].blocks.size() != 1 || op.regions[0].blocks[0].ops.empty())
-            invalid("reduce: expected a one-block body");
-          const BBlock& rb = op.regions[0].blocks[0];
-          std::string b = rb.ops[0].name;
-          if (b.rfind("stablehlo.", 0) == 0) b = b.substr(10);
-          if (rb.ops[0].operands.size() != 2 || rb.args.size() != 2 ||
-              !std::is_permutation(rb.ops[0].operands.begin(), rb.ops[0].operands.end(), rb.args.begin()))
-            unimplemented("reduce body must apply one binary op to its two arguments");
-          if (b == "add") n.reduce_body = ReduceBody::Add;
-          else if (b == "maximum") n.reduce_body = ReduceBody::Max;
-          else if (b == "minimum") n.reduce_body = ReduceBody::Min;
-          else if (b == "multiply") n.reduce_body = ReduceBody::Mul;
-          else if (b == "and") n.reduce_body = ReduceBody::And;
-          else if (b == "or") n.reduce_body = ReduceBody::Or;
-          else unimplemented("reduce body '" + b + "' is not supported");
         } else if (nm == "dot_general") {
           n.op = Op::DotGeneral;
           const BAttr& d = need(op, "dot_dimension_numbers");
@@ -1061,8 +1089,6 @@ class BytecodeParser {
       }
       node_of[op.results[0]] = add(std::move(n));
     }
-    if (g.results.empty()) invalid("function @" + entry + " returns nothing");
-    return g;
   }
 
   const uint8_t* file_;

@@ -25,5 +25,10 @@ inline int64_t first_int(const std::vector<int64_t>& v, const char* what) {  // 
 }
 // StableHLO op names (no dialect prefix) that map to one Op and carry no attributes ("add" → Op::Add, ...).
 const std::unordered_map<std::string, Op>& mlir_simple_ops();
+// The nodes of one reduce op, one per result (`proto` holds the operands and dimensions). The body is `applies`
+// (the pretty form's single body op, e.g. "stablehlo.add") or `body`, the region as a graph; a region that applies
+// one recognised binary op to its two block arguments becomes that op, any other a ReduceBody::General node.
+std::vector<Node> mlir_reduce_nodes(const Graph& g, const Node& proto, const std::vector<TensorType>& results,
+                                    const std::string& applies, std::shared_ptr<const Graph> body);
 
 }  // namespace ryft

@@ -505,8 +505,9 @@ struct OpSyntax {  // everything an op line carries, in generic form
   std::vector<std::string> operands;
   std::map<std::string, std::string> attrs;  // raw attribute text
   FnType type;
-  // reduce body, when given as a region
+  // reduce body: the pretty form's `applies` op, or the region as a graph
   std::string body_op;
+  std::shared_ptr<Graph> body;
 };
 
 class Parser {
@@ -673,59 +674,64 @@ class Parser {
     return s.substr(b, p - b);
   }
 
-  // Reducer region: returns the binary op the body applies to its two block arguments.
-  std::string parse_reducer_region() {
-    // generic: ({ ^bb0(%a: tensor<f32>, %b: tensor<f32>): %r = op %a, %b ...; return %r })
-    // pretty:  reducer(%a: tensor<f32>, %b: tensor<f32>) { ... }
-    std::string body_op;
-    size_t depth0 = 0;
-    (void)depth0;
-    std::map<std::string, int> saved = names_;
-    // block args
-    if (c_.try_consume("^bb0") || c_.try_consume("^bb")) {
-      if (c_.peek() != '(') c_.ident();
-    }
-    c_.expect("(");
-    std::vector<std::string> args;
-    do {
-      args.push_back(c_.sigil_name('%'));
-      c_.expect(":");
-      parse_type(c_);
-    } while (c_.try_consume(","));
-    c_.expect(")");
-    c_.try_consume(":");
-    c_.try_consume("{");
-    // body: expect exactly one binary op then a return
-    std::string op_name_s;
-    std::string result_name;
-    for (;;) {
-      if (c_.try_consume("stablehlo.return") || c_.try_consume("\"stablehlo.return\"") || c_.try_consume("return")) {
-        bool g = c_.try_consume("(");
-        std::string rv = c_.sigil_name('%');
-        if (g) c_.expect(")");
-        if (c_.try_consume(":")) parse_fn_or_types(c_);
-        if (rv != result_name) unimplemented("reduce body must return its single binary op result");
-        break;
+  // A reduce body region as a graph of its own. Generic form (after the region's `{`): `^bb0(%a: T, %b: T): ops;
+  // return; }`. Pretty form: `(%a0: T, %b0: T) (%a1: U, %b1: U) { ops; return }` — one parenthesised pair per input,
+  // the pairs' first members being the first N block arguments and their second members the last N. Values of the
+  // enclosing function are not visible inside.
+  std::shared_ptr<Graph> parse_region(bool pretty) {
+    std::vector<std::pair<std::string, TensorType>> args;
+    if (pretty) {
+      std::vector<std::pair<std::string, TensorType>> second;
+      while (c_.try_consume("(")) {
+        for (int k = 0; k < 2; ++k) {
+          if (k) c_.expect(",");
+          std::string nm = c_.sigil_name('%');
+          c_.expect(":");
+          (k ? second : args).push_back({nm, parse_type(c_)});
+        }
+        c_.expect(")");
       }
-      if (!op_name_s.empty()) unimplemented("reduce bodies with more than one op are not supported");
-      result_name = c_.sigil_name('%');
-      c_.expect("=");
-      c_.skip_ws();
-      bool quoted = c_.peek_raw() == '"';
-      op_name_s = quoted ? c_.quoted() : c_.ident();
-      if (quoted) c_.expect("(");
-      std::string a = c_.sigil_name('%');
-      c_.expect(",");
-      std::string b = c_.sigil_name('%');
-      if (quoted) c_.expect(")");
-      if (!((a == args[0] && b == args[1]) || (a == args[1] && b == args[0])))
-        unimplemented("reduce body must combine its two block arguments");
-      c_.expect(":");
-      parse_fn_or_types(c_);
+      args.insert(args.end(), second.begin(), second.end());
+      c_.expect("{");
+    } else {
+      if (c_.try_consume("^bb0") || c_.try_consume("^bb")) {
+        if (c_.peek() != '(') c_.ident();
+      }
+      c_.expect("(");
+      if (!c_.try_consume(")")) {
+        do {
+          std::string nm = c_.sigil_name('%');
+          c_.expect(":");
+          args.push_back({nm, parse_type(c_)});
+        } while (c_.try_consume(","));
+        c_.expect(")");
+      }
+      c_.try_consume(":");
     }
-    c_.try_consume("}");
-    names_ = saved;
-    return op_name_s;
+    if (args.empty()) invalid("reduce body without block arguments");
+    Graph outer = std::move(graph_);
+    std::map<std::string, int> outer_names = std::move(names_);
+    std::vector<TensorType> outer_types = std::move(result_types_);
+    graph_ = Graph();
+    names_.clear();
+    result_types_.clear();
+    for (auto& [nm, t] : args) {
+      Node n;
+      n.op = Op::Parameter;
+      n.type = t;
+      n.param_index = (int)graph_.params.size();
+      n.debug = nm;
+      const int id = add(std::move(n));
+      graph_.params.push_back(id);
+      names_[nm] = id;
+    }
+    parse_block_body(/*top=*/true);  // through the region's closing brace, collecting the returned values
+    auto body = std::make_shared<Graph>(std::move(graph_));
+    graph_ = std::move(outer);
+    names_ = std::move(outer_names);
+    result_types_ = std::move(outer_types);
+    if (body->results.empty()) invalid("reduce body returns nothing");
+    return body;
   }
 
   void parse_op_line() {
@@ -735,11 +741,11 @@ class Parser {
     if (c_.peek_raw() == '%') {
       do {
         std::string nm = c_.sigil_name('%');
-        if (c_.try_consume(":")) {
-          int64_t k = c_.integer();
-          if (k != 1) unimplemented("multi-result ops are not supported (" + nm + ")");
-        }
-        os.results.push_back(nm);
+        int64_t k = 1;
+        if (c_.try_consume(":")) k = c_.integer();
+        if (k < 1 || k > 64) invalid("bad result count for " + nm);
+        if (k == 1) os.results.push_back(nm);
+        for (int64_t i = 0; k > 1 && i < k; ++i) os.results.push_back(nm + "#" + std::to_string(i));
       } while (c_.try_consume(","));
       c_.expect("=");
     }
@@ -765,7 +771,7 @@ class Parser {
     if (c_.try_consume("<{")) parse_attr_dict(os.attrs), c_.expect(">");
     if (c_.try_consume("(")) {  // regions
       c_.expect("{");
-      os.body_op = parse_reducer_region();
+      os.body = parse_region(/*pretty=*/false);
       c_.expect(")");
     }
     if (c_.try_consume("{")) parse_attr_dict(os.attrs);
@@ -801,13 +807,17 @@ class Parser {
       return;
     }
     if (n == "reduce") {
-      // stablehlo.reduce(%x init: %i) [applies <op>] across dimensions = [..] : fn  [reducer(...) {...}]
-      c_.expect("(");
-      os.operands.push_back(c_.sigil_name('%'));
-      c_.expect("init:");
-      os.operands.push_back(c_.sigil_name('%'));
-      c_.expect(")");
-      if (c_.try_consume(",")) unimplemented("variadic reduce is not supported");
+      // stablehlo.reduce(%x init: %i)[, (%y init: %j) ...] [applies <op>] across dimensions = [..] : fn
+      //   [reducer(%a: T, %b: T) ... {...}]
+      std::vector<std::string> inits;
+      do {
+        c_.expect("(");
+        os.operands.push_back(c_.sigil_name('%'));
+        c_.expect("init:");
+        inits.push_back(c_.sigil_name('%'));
+        c_.expect(")");
+      } while (c_.try_consume(","));
+      os.operands.insert(os.operands.end(), inits.begin(), inits.end());
       if (c_.try_consume("applies")) os.body_op = c_.ident();
       c_.expect("across");
       c_.expect("dimensions");
@@ -819,7 +829,7 @@ class Parser {
       os.type = parse_fn_or_types(c_);
       if (os.body_op.empty()) {
         c_.expect("reducer");
-        os.body_op = parse_reducer_region();
+        os.body = parse_region(/*pretty=*/true);
       }
       return;
     }
@@ -981,17 +991,14 @@ class Parser {
       n.cmp_type = parse_cmp_type(get("compare_type"));
     } else if (nm == "reduce") {
       n.op = Op::Reduce;
-      if (n.operands.size() != 2) unimplemented("variadic reduce is not supported");
       n.dims = parse_int_list_text(get("dimensions"));
-      std::string b = os.body_op;
-      if (b.rfind("stablehlo.", 0) == 0) b = b.substr(10);
-      if (b == "add") n.reduce_body = ReduceBody::Add;
-      else if (b == "maximum") n.reduce_body = ReduceBody::Max;
-      else if (b == "minimum") n.reduce_body = ReduceBody::Min;
-      else if (b == "multiply") n.reduce_body = ReduceBody::Mul;
-      else if (b == "and") n.reduce_body = ReduceBody::And;
-      else if (b == "or") n.reduce_body = ReduceBody::Or;
-      else unimplemented("reduce body '" + b + "' is not supported");
+      std::vector<TensorType> results = os.type.results;
+      if (results.empty()) results.push_back(result_type(os));
+      std::vector<Node> nodes = mlir_reduce_nodes(graph_, n, results, os.body_op, os.body);
+      if (os.results.size() != nodes.size())
+        invalid("reduce: " + std::to_string(nodes.size()) + " results, " + std::to_string(os.results.size()) + " names");
+      for (size_t i = 0; i < nodes.size(); ++i) names_[os.results[i]] = add(std::move(nodes[i]));
+      return;
     } else if (nm == "dot_general") {
       n.op = Op::DotGeneral;
       std::string dd = get("dot_dimension_numbers");
@@ -1035,6 +1042,7 @@ class Parser {
       unimplemented("stablehlo." + nm + " is not supported by the MI355X plugin");
     }
     validate(n);
+    if (os.results.size() > 1) unimplemented("stablehlo." + nm + " with " + std::to_string(os.results.size()) + " results is not supported");
     int id = add(std::move(n));
     for (auto& r : os.results) names_[r] = id;
   }
@@ -1240,8 +1248,17 @@ void validate_node(const Graph& g, Node& n) {
       break;
     }
     case Op::Reduce: {
-      need(2);
-      auto& in = opt(0);
+      // inputs, then one init value per input (functional.rs:109-230); this node is result `result_index`
+      if (n.operands.size() < 2 || n.operands.size() % 2) invalid("reduce expects its inputs and one init value each");
+      const int ni = (int)n.operands.size() / 2;
+      if (n.result_index < 0 || n.result_index >= ni) invalid("reduce: result index out of range");
+      auto& in = opt(n.result_index);
+      for (int i = 0; i < ni; ++i) {
+        if (opt(i).shape != in.shape) invalid("reduce: inputs of different shapes");
+        if (opt(ni + i).rank() != 0) invalid("reduce: init value must be a scalar");
+        if (opt(ni + i).dtype != opt(i).dtype) invalid("reduce: an init value's element type differs from its input's");
+      }
+      if (n.type.dtype != in.dtype) invalid("reduce: result element type differs from its input's");
       dims_in_range({&n.dims}, in.rank(), "reduce");
       std::vector<int64_t> out;
       for (int d = 0; d < in.rank(); ++d) {
@@ -1250,7 +1267,6 @@ void validate_node(const Graph& g, Node& n) {
         if (!red) out.push_back(in.shape[d]);
       }
       if (out != n.type.shape) invalid("reduce: result shape mismatch");
-      if (opt(1).rank() != 0) invalid("reduce: init value must be a scalar");
       break;
     }
     case Op::Select:
@@ -1411,6 +1427,68 @@ void validate_node(const Graph& g, Node& n) {
       }
       break;
   }
+}
+
+std::vector<Node> mlir_reduce_nodes(const Graph& g, const Node& proto, const std::vector<TensorType>& results,
+                                    const std::string& applies, std::shared_ptr<const Graph> body) {
+  const size_t ni = proto.operands.size() / 2;
+  if (proto.operands.size() < 2 || proto.operands.size() % 2)
+    invalid("reduce expects its inputs and one init value each");
+  if (results.size() != ni) invalid("reduce: " + std::to_string(ni) + " results expected");
+  auto kind_of = [](std::string b) {
+    if (b.rfind("stablehlo.", 0) == 0) b = b.substr(10);
+    static const std::map<std::string, ReduceBody> k = {{"add", ReduceBody::Add},      {"maximum", ReduceBody::Max},
+                                                        {"minimum", ReduceBody::Min},  {"multiply", ReduceBody::Mul},
+                                                        {"and", ReduceBody::And},      {"or", ReduceBody::Or}};
+    auto it = k.find(b);
+    return it == k.end() ? ReduceBody::General : it->second;
+  };
+  ReduceBody kind = ReduceBody::General;
+  if (!applies.empty()) {
+    if (ni != 1) invalid("reduce: `applies` takes one input");
+    kind = kind_of(applies);
+    if (kind == ReduceBody::General) unimplemented("reduce body '" + applies + "' is not supported");
+    body = nullptr;
+  } else {
+    if (!body) invalid("reduce without a body");
+    const Graph& b = *body;
+    if (b.params.size() != 2 * ni || b.results.size() != ni)
+      invalid("reduce: the body takes " + std::to_string(2 * ni) + " arguments and returns " + std::to_string(ni));
+    for (size_t k = 0; k < 2 * ni; ++k) {
+      const TensorType& t = b.nodes[b.params[k]].type;
+      if (t.rank() != 0) invalid("reduce: body arguments must be scalars");
+      if (t.dtype != g.nodes[proto.operands[k % ni]].type.dtype)
+        unimplemented("reduce: body arguments of another element type than the inputs' are not supported");
+    }
+    for (size_t k = 0; k < ni; ++k) {
+      const TensorType& t = b.nodes[b.results[k]].type;
+      if (t.rank() != 0 || t.dtype != results[k].dtype) invalid("reduce: body results must be scalars of the result types");
+    }
+    for (const Node& bn : b.nodes)
+      if (bn.op != Op::Parameter && bn.op != Op::Constant && !op_is_elementwise(bn.op))
+        unimplemented(std::string("reduce bodies with stablehlo.") + op_name(bn.op) + " are not supported");
+    // one recognised binary op of the two block arguments (in either order): the fast reductions
+    if (ni == 1 && b.nodes.size() == 3) {
+      const Node& op = b.nodes[b.results[0]];
+      const int p0 = b.params[0], p1 = b.params[1];
+      if (op.operands.size() == 2 && ((op.operands[0] == p0 && op.operands[1] == p1) ||
+                                      (op.operands[0] == p1 && op.operands[1] == p0)))
+        kind = kind_of(op_name(op.op));
+    }
+    if (kind != ReduceBody::General) body = nullptr;
+  }
+  std::vector<Node> out;
+  for (size_t i = 0; i < ni; ++i) {
+    Node m = proto;
+    m.op = Op::Reduce;
+    m.type = results[i];
+    m.result_index = (int)i;
+    m.reduce_body = kind;
+    m.body = body;
+    validate_node(g, m);
+    out.push_back(std::move(m));
+  }
+  return out;
 }
 
 Graph parse_mlir_text(const std::string& text, const std::string& entry) {

@@ -12,6 +12,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstddef>
+#include <cstring>
 #include <functional>
 #include <map>
 #include <set>
@@ -92,6 +93,9 @@ class ExprBuilder {
   bool dry = false;              // dry run: record leaves, materialize nothing
   std::vector<std::pair<int, std::vector<int>>> dry_leaves;
   std::set<int> inner_nodes;     // elementwise nodes computed inside the program
+  // Body mode: nodes come from `body` (a reduce body's graph of rank-0 values) instead of the planner's graph; its
+  // parameters are read as the EW_ACC registers acc_nodes names. Only constants and elementwise ops may appear.
+  const Graph* body = nullptr;
 
   Val emit(int node, const std::vector<int>& src);
   // A load of a materialized view read along the iteration space (view dim d ↔ space dim d), `extra` elements on.
@@ -157,6 +161,7 @@ class Planner {
   int materialize(int node, int target = -1);
   void emit_elementwise_root(int node, int target);
   void emit_reduce(int node, int target);
+  void emit_reduce_body(int node, int target);
   bool try_row_fusion(int node, int target);
   void classify_row(Step& st);
   bool row_reducible(int reduce, const TensorType& space);
@@ -254,7 +259,7 @@ ExprBuilder::Val ExprBuilder::emit(int node, const std::vector<int>& src) {
   auto key = std::make_pair(node, src);
   auto it = memo_.find(key);
   if (it != memo_.end()) return it->second;
-  const Graph& g = P_.graph();
+  const Graph& g = body ? *body : P_.graph();
   const Node& n = g.nodes[node];
   DType dt = n.type.dtype;
   bool fl = float_class(dt);
@@ -277,6 +282,8 @@ ExprBuilder::Val ExprBuilder::emit(int node, const std::vector<int>& src) {
     if (fl) ins.imm.f = (float)literal_as_double(n);
     else ins.imm.i = (int32_t)literal_as_int(n);
     out = {push(ins, fl, {}), fl};
+  } else if (body && !op_is_elementwise(n.op)) {
+    unimplemented(std::string("reduce bodies with stablehlo.") + op_name(n.op) + " are not supported");
   } else if (P_.materialized(node)) {
     out = leaf_load(node, src, dt);
   } else if (n.op == Op::Iota) {
@@ -898,8 +905,107 @@ void Planner::emit_pad(int node, int target) {
   mat_[node] = out;
 }
 
+// A reduce with a general body or several inputs: one REDUCE_BODY step computes every result of the op (the nodes
+// that share its operands and body), the node asked for into `target`.
+void Planner::emit_reduce_body(int node, int target) {
+  const Node& n = g_.nodes[node];
+  const int ni = (int)n.operands.size() / 2;
+  if (ni > RED_MAX_N) unimplemented("reduce over more than " + std::to_string(RED_MAX_N) + " inputs is not supported");
+  if (!n.body) fail(PJRT_Error_Code_INTERNAL, "variadic reduce without a body graph");
+  std::vector<int> res(ni, -1);  // the op's result nodes
+  for (size_t k = 0; k < g_.nodes.size(); ++k) {
+    const Node& m = g_.nodes[k];
+    if (m.op == Op::Reduce && m.operands == n.operands && m.body == n.body && m.dims == n.dims) res[m.result_index] = (int)k;
+  }
+  const Node& xn = g_.nodes[n.operands[0]];
+  std::vector<int64_t> red = n.dims;
+  std::sort(red.begin(), red.end());
+  std::vector<int64_t> space;
+  std::vector<int> src(xn.type.rank());
+  int pos = 0;
+  int64_t outer = 1, inner = 1;
+  for (int d = 0; d < xn.type.rank(); ++d)
+    if (!std::binary_search(red.begin(), red.end(), (int64_t)d)) {
+      src[d] = pos++;
+      space.push_back(xn.type.shape[d]);
+      outer *= xn.type.shape[d];
+    }
+  for (auto d : red) {
+    src[d] = pos++;
+    space.push_back(xn.type.shape[d]);
+    inner *= xn.type.shape[d];
+  }
+  // the body: block arguments k → EW_ACC k
+  ExprBuilder bb(*this, {});
+  bb.body = n.body.get();
+  for (size_t k = 0; k < n.body->params.size(); ++k) bb.acc_nodes[n.body->params[k]] = (int)k;
+  for (int i = 0; i < ni; ++i) bb.add_output(bb.emit(n.body->results[i], {}), n.body->nodes[n.body->results[i]].type.dtype);
+  const EwProgram body = bb.finish();
+  if (body.n_leaves) fail(PJRT_Error_Code_INTERNAL, "reduce body program reads memory");
+  for (int attempt = 0; attempt < 2; ++attempt) {
+    try {
+      ExprBuilder b(*this, space);
+      for (int i = 0; i < ni; ++i) b.add_output(b.emit(n.operands[i], src), g_.nodes[n.operands[i]].type.dtype);
+      Step st{};
+      st.kind = Step::REDUCE_BODY;
+      st.name = "reduce";
+      ReduceBodyArgs& a = st.rbody;
+      a.prologue = b.finish();
+      a.body = body;
+      a.outer = outer;
+      a.inner = inner;
+      a.n = ni;
+      push_program_patches(st, offsetof(ReduceBodyArgs, prologue), a.prologue, b.leaves(), {});
+      double bytes = leaf_bytes(plan_, b.leaves());
+      for (int i = 0; i < ni; ++i) {
+        const Node& init = g_.nodes[n.operands[ni + i]];
+        const bool fl = float_class(init.type.dtype);
+        double v;
+        if (splat_value(n.operands[ni + i], &v)) {
+          if (fl) {
+            const float f = (float)v;
+            std::memcpy(&a.init[i], &f, 4);
+          } else {
+            a.init[i] = (uint32_t)(int32_t)(int64_t)v;
+          }
+        } else {
+          a.init_dtype[i] = (int32_t)init.type.dtype;
+          st.patches.push_back({offsetof(ReduceBodyArgs, init_ptr) + i * sizeof(void*), materialize(n.operands[ni + i])});
+        }
+        const TensorType& rt = n.body->nodes[n.body->results[i]].type;
+        a.out_dtype[i] = (int32_t)rt.dtype;
+        a.out_float[i] = float_class(rt.dtype);
+        TensorType ot = xn.type;
+        ot.dtype = rt.dtype;
+        ot.shape.clear();
+        for (int d = 0; d < xn.type.rank(); ++d)
+          if (!std::binary_search(red.begin(), red.end(), (int64_t)d)) ot.shape.push_back(xn.type.shape[d]);
+        const int r = res[i];
+        int slot = -1;
+        if (r == node) {
+          slot = temp_or(target, ot);
+        } else if (r >= 0) {  // another result of the op: straight into its output buffer when the function returns it
+          for (size_t k = 0; k < g_.results.size() && slot < 0; ++k)
+            if (g_.results[k] == r) slot = plan_.output_slots[k];
+        }
+        if (slot < 0) slot = new_slot(Slot::TEMP, ot);
+        if (r >= 0) mat_[r] = slot;
+        st.patches.push_back({offsetof(ReduceBodyArgs, out) + i * sizeof(void*), slot});
+        bytes += (double)ot.bytes();
+      }
+      st.bytes = bytes;
+      plan_.steps.push_back(std::move(st));
+      return;
+    } catch (const Status& s) {
+      if (s.code != PJRT_Error_Code_RESOURCE_EXHAUSTED || attempt == 1) throw;
+      for (int i = 0; i < ni; ++i) materialize(n.operands[i]);
+    }
+  }
+}
+
 void Planner::emit_reduce(int node, int target) {
   const Node& n = g_.nodes[node];
+  if (n.reduce_body == ReduceBody::General || n.operands.size() != 2) return emit_reduce_body(node, target);
   int x = n.operands[0];
   const Node& xn = g_.nodes[x];
   double initv = 0.0;
@@ -939,6 +1045,7 @@ void Planner::emit_reduce(int node, int target) {
         case ReduceBody::Mul: st.red.kind = RED_MUL; break;
         case ReduceBody::And: st.red.kind = RED_AND; break;
         case ReduceBody::Or: st.red.kind = RED_OR; break;
+        case ReduceBody::General: fail(PJRT_Error_Code_INTERNAL, "general reduce body on the fast path");
       }
       if (st.red.is_float) st.red.init.f = (float)initv;
       else st.red.init.i = (int32_t)(int64_t)initv;
@@ -962,7 +1069,8 @@ void Planner::emit_reduce(int node, int target) {
 // shaped like the consumer, starts from a constant init, and yields a 32-bit register type.
 bool Planner::row_reducible(int reduce, const TensorType& space) {
   const Node& r = g_.nodes[reduce];
-  if (r.op != Op::Reduce || materialized(reduce) || r.operands.size() != 2) return false;
+  if (r.op != Op::Reduce || materialized(reduce) || r.operands.size() != 2 || r.reduce_body == ReduceBody::General)
+    return false;
   const Node& x = g_.nodes[r.operands[0]];
   const int rank = space.rank();
   if (x.type.shape != space.shape || r.dims.size() != 1 || r.dims[0] != rank - 1) return false;
@@ -1032,6 +1140,7 @@ bool Planner::try_row_fusion(int node, int target) {
         case ReduceBody::Mul: ra.kind[k] = RED_MUL; break;
         case ReduceBody::And: ra.kind[k] = RED_AND; break;
         case ReduceBody::Or: ra.kind[k] = RED_OR; break;
+        case ReduceBody::General: fail(PJRT_Error_Code_INTERNAL, "general reduce body in a row-fused step");
       }
       ra.red_dtype[k] = (int32_t)r.type.dtype;
       b.row_nodes[order[k]] = (int)k;
@@ -2020,6 +2129,10 @@ std::string Plan::describe() const {
       os << " instrs=" << s.ew.n_instr << " leaves=" << s.ew.n_leaves << " elems=" << s.ew.total;
     } else if (s.kind == Step::REDUCE) {
       os << " outer=" << s.red.outer << " inner=" << s.red.inner;
+    } else if (s.kind == Step::REDUCE_BODY) {
+      os << " outer=" << s.rbody.outer << " inner=" << s.rbody.inner << " inputs=" << s.rbody.n
+         << " body_instrs=" << s.rbody.body.n_instr << " out=";
+      for (int i = 0; i < s.rbody.n; ++i) os << (i ? "," : "") << dtype_name((DType)s.rbody.out_dtype[i]);
     } else if (s.kind == Step::ROW) {
       os << " rows=" << s.row.rows << " inner=" << s.row.inner << " reductions=" << s.row.n_red
          << " instrs=" << s.row.prog.n_instr << " leaves=" << s.row.prog.n_leaves;

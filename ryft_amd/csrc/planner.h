@@ -17,7 +17,7 @@ struct Slot {
 };
 
 struct Step {
-  enum Kind { ELEMENTWISE, REDUCE, GEMM, ATTENTION, COPY, ROW, WINDOW, GATHER } kind;
+  enum Kind { ELEMENTWISE, REDUCE, GEMM, ATTENTION, COPY, ROW, WINDOW, GATHER, REDUCE_BODY } kind;
   std::string name;  // kernel family, for profiling ("gemm_bf16_mfma", "attention_fwd", ...)
   EwProgram ew;
   ReduceArgs red;
@@ -26,6 +26,7 @@ struct Step {
   RowArgs row;
   WindowArgs win;
   GatherArgs gat;
+  ReduceBodyArgs rbody;
   struct { int64_t bytes; int64_t src_offset; } copy;  // src_offset: bytes into the source slot
   // Pointer fields inside the args block that refer to slots: (byte offset of the pointer field, slot). The
   // field's initial value is a byte offset into the slot's buffer.
@@ -41,6 +42,7 @@ struct Step {
       case ROW: return &row;
       case WINDOW: return &win;
       case GATHER: return &gat;
+      case REDUCE_BODY: return &rbody;
       default: return nullptr;
     }
   }

@@ -105,6 +105,7 @@ class Op:
         self.result_types = result_types  # type strings
         self.attrs = attrs or {}          # name → ("kind", value)
         self.body = body                  # reduce: (op name, arg type)
+        self.region = None                # reduce with a general body: (arg names, arg types, ops, returned names)
 
 
 def parse_module(text: str):
@@ -117,14 +118,23 @@ def parse_module(text: str):
     res = m.group(2).strip()
     res_types = _split_top(res[1:-1]) if res.startswith("(") else [res]
     body = text[m.end():]
+    ops, returned = _parse_lines([ln.strip() for ln in body.split("\n")], "return")
+    return arg_names, arg_types, res_types, ops, returned
+
+
+def _parse_lines(lines: List[str], ret: str):
+    """Ops of a block up to its `ret` line; returns (ops, returned names). A `%r:k = ...` op names its results
+    %r#0 .. %r#(k-1); a reduce followed by a `reducer(...) {` line takes the region up to its closing brace."""
     ops: List[Op] = []
     returned: List[str] = []
-    for line in body.split("\n"):
-        line = line.strip()
+    i = 0
+    while i < len(lines):
+        line = lines[i]
+        i += 1
         if not line or line == "}":
             continue
-        if line.startswith("return"):
-            vals = line[6:].split(":")[0]
+        if line.startswith(ret):
+            vals = line[len(ret):].split(":")[0]
             returned = [v.strip() for v in vals.split(",")]
             break
         lhs, rhs = line.split("=", 1)
@@ -135,8 +145,41 @@ def parse_module(text: str):
         if rhs.startswith('"stablehlo.gather"('):
             ops.append(_parse_gather(lhs, rhs))
             continue
+        if name == "stablehlo.reduce" and "applies" not in rest:
+            region_lines = []
+            while not lines[i].startswith("}"):
+                region_lines.append(lines[i])
+                i += 1
+            i += 1
+            ops.append(_parse_general_reduce(lhs, rest, region_lines))
+            continue
         ops.append(_parse_op(lhs, name, rest))
-    return arg_names, arg_types, res_types, ops, returned
+    return ops, returned
+
+
+def _result_names(lhs: str) -> List[str]:
+    if ":" in lhs:
+        nm, k = lhs.split(":")
+        return [f"{nm.strip()}#{j}" for j in range(int(k))]
+    return [lhs]
+
+
+def _parse_general_reduce(lhs: str, rest: str, region_lines: List[str]) -> Op:
+    # `(%x init: %i), (%y init: %j) across dimensions = [..] : (types) -> (types)`, then
+    # `reducer(%a0: T, %b0: T) (%a1: U, %b1: U) {`, the body's ops and `stablehlo.return ...`
+    head, ty = rest.split(" : ", 1)
+    pairs = re.findall(r"\((%\w+) init: (%\w+)\)", head)
+    dims = _ints(re.search(r"dimensions = \[(.*?)\]", head).group(1))
+    ins, outs = _types_after_colon(ty)
+    op = Op("stablehlo.reduce", [p[0] for p in pairs] + [p[1] for p in pairs], _result_names(lhs), outs,
+            {"dimensions": ("i64s", dims)})
+    decl = region_lines[0]
+    arg_pairs = re.findall(r"\((%\w+): (tensor<[^>]*>), (%\w+): (tensor<[^>]*>)\)", decl)
+    names = [a[0] for a in arg_pairs] + [a[2] for a in arg_pairs]
+    types = [a[1] for a in arg_pairs] + [a[3] for a in arg_pairs]
+    body_ops, returned = _parse_lines(region_lines[1:], "stablehlo.return")
+    op.region = (names, types, body_ops, returned)
+    return op
 
 
 def arg_attr_dicts(text: str) -> List[Dict[str, Tuple[str, str]]]:
@@ -477,6 +520,21 @@ class Writer:
                 ret = self._op("stablehlo.return", {}, [], [base + 2])
                 regions = varint(1) + varint(3) + self._block([st, st], [comb, ret])
                 n_regions = 1
+            elif op.region:
+                # a general body: its block arguments, its ops (values numbered after the arguments) and a return
+                base = 0 if self.isolated_reduce else n_func_values
+                names, types, rops, rets = op.region
+                rvals = {nm: base + k for k, nm in enumerate(names)}
+                n_vals = len(names) + sum(len(o.results) for o in rops)
+                enc = []
+                for o in rops:
+                    enc.append(self._op(o.name, {k: self.attr(v) for k, v in o.attrs.items()},
+                                        [self.tensor(t) for t in o.result_types], [rvals[x] for x in o.operands]))
+                    for r in o.results:
+                        rvals[r] = base + len(rvals)
+                enc.append(self._op("stablehlo.return", {}, [], [rvals[r] for r in rets]))
+                regions = varint(1) + varint(n_vals) + self._block([self.tensor(t) for t in types], enc)
+                n_regions = 1
             body_ops.append(self._op(op.name, attrs, rtypes, operands, regions, self.isolated_reduce, n_regions))
             for r in op.results:
                 values[r] = len(values)
@@ -552,7 +610,9 @@ def to_bytecode(text: str, **options) -> bytes:
     # op names are numbered by the dialect-grouped order of the dialect section: register them in that order first
     _, _, _, ops, _ = parse_module(text)
     names = {"builtin.module", "func.func", "func.return"} | {o.name for o in ops}
-    names |= {o.body[0] for o in ops if o.body} | ({"stablehlo.return"} if any(o.body for o in ops) else set())
+    names |= {o.body[0] for o in ops if o.body} | ({"stablehlo.return"} if any(o.body or o.region for o in ops)
+                                                   else set())
+    names |= {r.name for o in ops if o.region for r in o.region[2]}
     for n in sorted(names, key=lambda x: (w.dialects.index(x.split(".")[0]), x)):
         w.opname(n)
     return w.module(text)

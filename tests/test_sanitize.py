@@ -1,9 +1,9 @@
 """The plugin's host path under AddressSanitizer and UndefinedBehaviorSanitizer, on the CPU: the MLIR text and
 bytecode front-ends, the planner and the CompileOptionsProto decoder (the bytes ryft-pjrt hands to
 PJRT_Client_Compile, crates/ryft-pjrt/src/programs.rs:1245-1263) built with -fsanitize=address,undefined
-(tests/sanitize/Makefile) and fed the test corpus — every config, edge, row, donation and manipulation program as
-text and as bytecode in each writer variant, and CompileOptions encodings — plus truncated and bit-flipped copies of
-every file (tests/sanitize/frontend_check.cc). Rejections are expected; a sanitizer report fails the test. The whole
+(tests/sanitize/Makefile) and fed the test corpus — every config, edge, row, donation, manipulation, reduce-body and
+elementwise-op program as text and as bytecode in each writer variant, and CompileOptions encodings — plus truncated
+and bit-flipped copies of every file (tests/sanitize/frontend_check.cc). Rejections are expected; a sanitizer report fails the test. The whole
 host side of the plugin (runtime, C API, profiler included) is also built with -fsanitize=thread and driven from several
 threads at once (tests/sanitize/tsan_check.cc)."""
 import os
@@ -13,7 +13,7 @@ import pytest
 
 from ryft_amd import configs, pjrt
 from tests import donation_programs, edge_programs, mlir_bytecode as mb, row_programs
-from tests import test_dynamic_window as dw
+from tests import test_bit_trig_round_ops as bt, test_dynamic_window as dw, test_reduce_bodies as rb
 from tests.test_bytecode import SLICE_CONCAT_PAD, VARIANTS
 
 HERE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "sanitize")
@@ -39,6 +39,13 @@ def _programs():
         "dynamic_update_slice": dw.dus_program((2, 8, 256, 64), (2, 8, 1, 64), dt="bf16", it="i32", donate=True),
         "gather": dw.gather_example_program(),
         "gather_printed": dw.GATHER_PRINTED,
+        "argmax": rb.argmax_program((8, 100), 1),
+        "argmin_generic": rb.argmax_program((6, 7, 9), 0, kind="argmin", form="generic"),
+        "sum_max": rb.sum_max_program((6, 50, 40), [0, 2]),
+        "xor_reduce": rb.one_input_program((4, 33), 1, "xor", "i32"),
+        "shift_left": bt._prog("shift_left", ["i8", "i8"], "i8", (4, 33)),
+        "is_finite": bt._prog("is_finite", ["bf16"], "i1", (4, 33)),
+        "atan2": bt._prog("atan2", ["f32", "f32"], "f32", (4, 33), generic=True),
     }
     for (name, prog, _), _, _ in edge_programs.CASES:
         progs["edge_" + name] = prog
