@@ -13,10 +13,13 @@ holds C1–C5 plus the two HBM calibrations (copy, rmsnorm), each with its own v
 baseline. HBM traffic and MFMA utilisation come from rocprofv3 counter runs committed under profiles/
 (counters_<workload>.json): MFMA busy = (SQ_VALU_MFMA_BUSY_CYCLES / 1024 SIMDs) / (SQ_BUSY_CU_CYCLES / 256 CUs).
 
+`--config argmax` runs an extra workload that is not a BASELINE graph: greedy decoding's argmax over f32 logits
+[64, 128256] (a value-and-position reduce), priced in bytes like the calibrations.
+
 The cyclic garbage collector is paused during the timed region (as `timeit` does); the plugin's own work is
 unchanged.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config all|c1|c2|c3|c4|c5|c5x|copy|rmsnorm]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config all|c1|c2|c3|c4|c5|c5x|copy|rmsnorm|argmax]
                        [--cpu-seconds S] [--no-cpu-baseline]
 """
 import argparse
@@ -34,7 +37,7 @@ sys.path.insert(0, ROOT)
 METRIC = "TFLOP/s and % of MFMA/HBM roofline per StableHLO graph on 1 MI355X vs XLA CPU"
 HEADLINE = "c5"
 ALL = ["c5", "c1", "c2", "c3", "c4", "copy", "rmsnorm"]
-CHOICES = ["all", "c1", "c2", "c3", "c4", "c5", "c5x", "copy", "rmsnorm"]
+CHOICES = ["all", "c1", "c2", "c3", "c4", "c5", "c5x", "copy", "rmsnorm", "argmax"]
 
 
 def _workload(name):
@@ -109,6 +112,25 @@ def _cpu_baseline(name, seconds, w=None, gpu_outputs=None):
         if agree is not None:
             res["rel_error_vs_gpu"] = agree
         return res
+
+    if name == "argmax":
+        # numpy's argmax of the same logits (first occurrence, as the comparator body picks): the oracle folds the
+        # body element by element, too slow to be a fair CPU figure
+        w = w or configs.CONFIGS[name]()
+        x = w.inputs[0].data
+        t0 = time.perf_counter()
+        reps = 0
+        while True:
+            np.argmax(x, axis=1)
+            np.max(x, axis=1)
+            reps += 1
+            el = time.perf_counter() - t0
+            if (reps >= 5 and el >= seconds) or reps >= 10000:
+                break
+        what = (f"the full {w.name} workload, {reps} evaluation(s) in {el:.2f} s (numpy argmax + max over the rows, "
+                f"one thread; host {_cpu_model()}, {os.cpu_count()} logical CPUs visible)")
+        return {"value": round(w.bytes * reps / el / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": what, "evaluations": reps, "seconds": round(el, 3)}
 
     samples = {"c5x": (configs.c5x_swiglu_fp8_activations, {"m": 64}, "64 of the 512 tokens of C5 (fp8 activations)")}
     fn, kw, desc = samples[name]

@@ -371,6 +371,40 @@ def rmsnorm_fp8_rows(m=16384, d=4096, seed=0xCD) -> Workload:
                     tolerance=3e-2)
 
 
+def argmax_logits(m=64, v=128256, seed=0xCE) -> Workload:
+    """Extra workload, not a BASELINE config: greedy decoding's argmax over f32 logits [m, v] (a batch of 64 rows of a
+    128256-entry vocabulary), written as JAX lowers argmax — the logits and an iota of positions reduced together by a
+    comparator body (the larger value wins, a NaN wins, equal values go to the lower position). Reads m·v·4 bytes,
+    writes the m maxima and the m positions (StableHLO reduce, functional.rs:109-230)."""
+    X, I, S, SI = _t((m, v), "f32"), _t((m, v), "i32"), "tensor<f32>", "tensor<i32>"
+    RX, RI = _t((m,), "f32"), _t((m,), "i32")
+    prog = f"""module {{
+  func.func @main(%arg0: {X}) -> ({RX}, {RI}) {{
+    %0 = stablehlo.iota dim = 1 : {I}
+    %cst = stablehlo.constant dense<0xFF800000> : {S}
+    %c = stablehlo.constant dense<0> : {SI}
+    %1:2 = stablehlo.reduce(%arg0 init: %cst), (%0 init: %c) across dimensions = [1] : ({X}, {I}, {S}, {SI}) -> ({RX}, {RI})
+     reducer(%a: {S}, %b: {S}) (%ai: {SI}, %bi: {SI})  {{
+      %2 = stablehlo.compare  GT, %a, %b,  FLOAT : ({S}, {S}) -> tensor<i1>
+      %3 = stablehlo.compare  NE, %a, %a,  FLOAT : ({S}, {S}) -> tensor<i1>
+      %4 = stablehlo.or %2, %3 : tensor<i1>
+      %5 = stablehlo.compare  EQ, %a, %b,  FLOAT : ({S}, {S}) -> tensor<i1>
+      %6 = stablehlo.compare  LT, %ai, %bi,  SIGNED : ({SI}, {SI}) -> tensor<i1>
+      %7 = stablehlo.and %5, %6 : tensor<i1>
+      %8 = stablehlo.or %4, %7 : tensor<i1>
+      %9 = stablehlo.select %4, %a, %b : tensor<i1>, {S}
+      %10 = stablehlo.select %8, %ai, %bi : tensor<i1>, {SI}
+      stablehlo.return %9, %10 : {S}, {SI}
+    }}
+    return %1#0, %1#1 : {RX}, {RI}
+  }}
+}}
+"""
+    x = hd.normal(seed * 16, (m, v), 0.0, 4.0)
+    return Workload("argmax_logits", prog, [HostInput(x, BufferType.F32, (m, v))], flops=0.0,
+                    bytes=4.0 * m * v + 8.0 * m, compute_dtype="f32", tolerance=0.0, info={"baseline_config": False})
+
+
 CONFIGS: Dict[str, Callable[..., Workload]] = {
     "c1": c1_f32_dot,
     "c2": c2_bf16_batched_dot,
@@ -380,4 +414,5 @@ CONFIGS: Dict[str, Callable[..., Workload]] = {
     "c5x": c5x_swiglu_fp8_activations,
     "copy": hbm_copy_f32,
     "rmsnorm": rmsnorm_fp8_rows,
+    "argmax": argmax_logits,
 }

@@ -113,14 +113,27 @@ struct ReduceArgs {
 // folded in as EW_ACC N..2N-1, and leaves the N new accumulated values in its output registers (no leaves, no
 // stores). Every output's elements are folded in some tree order, then the init values are folded with the result
 // (init first): the order StableHLO leaves to the implementation.
+// argmax / argmin (arg_kind ARG_MAX / ARG_MIN, two inputs: a value and an iota of positions along the one reduced
+// dim): the body is not interpreted; the prologue yields only the value (n_out = 1), the position is the element's
+// index r, and a (value, position) pair replaces another when its value is larger (smaller) — a NaN value beating
+// every number — or equal with a lower position. `val` names which result is the value (the other is the position).
+// Long rows run in `segs` segments of `seg_len` elements: the first launch (PARTIAL) writes each segment's folded
+// values and a have-flag to `ws` ([outer][segs][n + 1] words), a second folds them in segment order with the inits.
 #define RED_MAX_N 2
+enum ArgKind : int32_t { ARG_NONE = 0, ARG_MAX = 1, ARG_MIN = 2 };
+enum ValueClass : int32_t { VC_FLOAT = 0, VC_SIGNED = 1, VC_UNSIGNED = 2 };
 struct ReduceBodyArgs {
   EwProgram prologue;
   EwProgram body;
   int64_t outer;                    // number of output elements
   int64_t inner;                    // reduced elements per output
+  int64_t segs;                     // segments per output (1: one pass)
+  int64_t seg_len;                  // reduced elements per segment
+  void* ws;                         // segs > 1: partial results
   int32_t n;                        // inputs / results
-  int32_t pad_;
+  int32_t arg_kind;                 // ArgKind
+  int32_t val;                      // arg_kind != ARG_NONE: the result (and input) index of the value
+  int32_t value_class;              // arg_kind != ARG_NONE: ValueClass of the value
   uint32_t init[RED_MAX_N];         // init values as register bits, when init_ptr is null
   const void* init_ptr[RED_MAX_N];  // non-null: the init value is a device scalar of init_dtype
   int32_t init_dtype[RED_MAX_N];

@@ -12,6 +12,7 @@
 
 #include "../common.h"
 #include "ew_device.h"
+#include "ew_vec.h"
 #include "kernels.h"
 #include "launch.h"
 
@@ -36,9 +37,6 @@ __global__ void __launch_bounds__(256) ew_kernel(const EwProgram P) {
   }
 }
 
-constexpr int VEC = 8;    // elements per thread in the vectorised kernels
-constexpr int VNT = 256;  // threads per workgroup there
-using VRegs = SwitchRegFile<VEC>;
 
 // Stores V consecutive register values (float bits if `is_float`, else int32) as `dtype` at out[lin..lin+V).
 // 16- / 8-byte vector store, non-temporal (streamed past the caches, for data no kernel re-reads soon) when NT.
@@ -125,20 +123,6 @@ __device__ __forceinline__ void store_vec(void* out, int64_t lin, int dtype, con
 #pragma unroll
       for (int e = 0; e < V; ++e) store_bits(out, lin + e, dtype, v[e], is_float);
       break;
-  }
-}
-
-// Coordinates of a linear index; 32-bit arithmetic when the iteration space allows it.
-__device__ __forceinline__ void decompose_fast(int64_t lin, const EwProgram& P, int32_t* coord) {
-  if (P.total <= 0x7fffffff) {
-    uint32_t l = (uint32_t)lin;
-    for (int d = P.rank - 1; d >= 0; --d) {
-      const uint32_t sd = (uint32_t)P.shape[d];
-      coord[d] = (int32_t)(l % sd);
-      l /= sd;
-    }
-  } else {
-    decompose(lin, P, coord);
   }
 }
 
@@ -359,41 +343,6 @@ static int grid_for(int64_t total, int threads) {
   return (int)blocks;
 }
 
-// Element size in bytes of the types leaves and outputs use.
-static int elem_size(int dt) {
-  switch (dt) {
-    case DT_F64: case DT_S64: case DT_U64: return 8;
-    case DT_F32: case DT_S32: case DT_U32: return 4;
-    case DT_BF16: case DT_F16: case DT_S16: case DT_U16: return 2;
-    default: return 1;
-  }
-}
-
-// Chooses how each leaf is read when VEC consecutive innermost elements are evaluated together; false when the
-// program cannot run VEC-wide (innermost extent not a multiple of VEC, misaligned outputs, huge strides).
-static bool prepare_vec(EwProgram& p, bool check_outputs) {
-  if (p.rank < 1 || p.shape[p.rank - 1] % VEC != 0) return false;
-  for (int i = 0; i < p.n_leaves; ++i) {
-    EwLeaf& L = p.leaves[i];
-    const int es = elem_size(L.dtype);
-    const int64_t s = L.kind == EW_LEAF_SCALAR ? 0 : (L.kind == EW_LEAF_IDENTITY ? 1 : L.strides[p.rank - 1]);
-    L.vstride = 0;
-    if (s == 0) { L.vmode = EW_VEC_BCAST; continue; }
-    bool contig = s == 1 && es <= 4 && ((uintptr_t)L.ptr % (uintptr_t)(VEC * es)) == 0 && L.offset % VEC == 0;
-    if (contig && L.kind == EW_LEAF_GENERAL)
-      for (int d = 0; d < p.rank - 1; ++d)
-        if (L.strides[d] % VEC) contig = false;
-    if (contig) { L.vmode = EW_VEC_CONTIG; continue; }
-    if (s > INT32_MAX || s < INT32_MIN) return false;
-    L.vmode = EW_VEC_GATHER;
-    L.vstride = (int32_t)s;
-  }
-  if (check_outputs)
-    for (int o = 0; o < p.n_out; ++o)
-      if (((uintptr_t)p.out_ptr[o] % (uintptr_t)(VEC * elem_size(p.out_dtype[o]))) != 0) return false;
-  return true;
-}
-
 void launch_elementwise(const EwProgram& p, hipStream_t stream, hipEvent_t done) {
   if (p.total == 0) return record_done(done, stream);
   if (p.out_strided && (p.n_out != 1 || !p.needs_coords))
@@ -585,126 +534,6 @@ void launch_reduce(const ReduceArgs& a, hipStream_t stream, hipEvent_t done) {
     dim3 grid((unsigned)blocks), block(256);
     if (a.prologue.needs_coords) launch_k(done, reduce_kernel<true>, grid, block, 0, stream, a);
     else launch_k(done, reduce_kernel<false>, grid, block, 0, stream, a);
-  }
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) fail(PJRT_Error_Code_INTERNAL, std::string("reduce launch failed: ") + hipGetErrorString(e));
-}
-
-// ------------------------------------------------------------------------------------------------ general bodies
-// x ← body(x, y) over the N values of a reduce (the body program reads x as EW_ACC 0..N-1, y as EW_ACC N..2N-1).
-__device__ __forceinline__ void body_fold(const EwProgram& B, int n, uint32_t* x, const uint32_t* y) {
-  uint32_t in[2 * RED_MAX_N];
-#pragma unroll
-  for (int i = 0; i < RED_MAX_N; ++i) {
-    in[i] = x[i];
-    in[RED_MAX_N + i] = y[i];
-  }
-  if (n < RED_MAX_N) in[n] = y[0];  // (n = 1: the folded value is EW_ACC 1)
-  RegFile1 R;
-  ew_run(B, 0, nullptr, in, R);
-#pragma unroll
-  for (int i = 0; i < RED_MAX_N; ++i)
-    if (i < n) x[i] = R.get(B.out_reg[i]);
-}
-
-// G threads per output (256: a workgroup, 64: a wavefront). Each thread folds every G-th element of its output,
-// starting from its first one (no identity is known for a general body); the threads' values are then folded
-// across lanes with shuffles and, for G = 256, across wavefronts through LDS, and the init values last.
-template <int G, bool COORDS>
-__global__ void __launch_bounds__(256) reduce_body_kernel(const ReduceBodyArgs A) {
-  __shared__ uint32_t part[4][RED_MAX_N + 1];
-  const EwProgram& P = A.prologue;
-  const EwProgram& B = A.body;
-  const int n = A.n;
-  constexpr int RB = 256 / G;  // outputs per workgroup
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int g = threadIdx.x / G, t = threadIdx.x % G;
-  for (int64_t o = (int64_t)blockIdx.x * RB + g; o < A.outer; o += (int64_t)gridDim.x * RB) {
-    uint32_t acc[RED_MAX_N] = {};
-    bool have = false;
-    for (int64_t r = t; r < A.inner; r += G) {
-      const int64_t lin = o * A.inner + r;
-      int32_t coord[EW_MAX_RANK];
-      if (COORDS) decompose(lin, P, coord);
-      RegFile1 R;
-      ew_run(P, lin, coord, nullptr, R);
-      uint32_t v[RED_MAX_N];
-#pragma unroll
-      for (int i = 0; i < RED_MAX_N; ++i) v[i] = i < n ? R.get(P.out_reg[i]) : 0u;
-      if (have) {
-        body_fold(B, n, acc, v);
-      } else {
-#pragma unroll
-        for (int i = 0; i < RED_MAX_N; ++i) acc[i] = v[i];
-        have = true;
-      }
-    }
-    // across the wavefront (G ≥ 64: every lane of it belongs to this output)
-    for (int off = 32; off > 0; off >>= 1) {
-      uint32_t y[RED_MAX_N];
-#pragma unroll
-      for (int i = 0; i < RED_MAX_N; ++i) y[i] = (uint32_t)__shfl_xor((int)acc[i], off, 64);
-      const bool yh = __shfl_xor((int)have, off, 64) != 0;
-      if (have && yh) {
-        body_fold(B, n, acc, y);
-      } else if (yh) {
-#pragma unroll
-        for (int i = 0; i < RED_MAX_N; ++i) acc[i] = y[i];
-        have = true;
-      }
-    }
-    bool write = lane == 0;
-    if constexpr (G == 256) {
-      if (lane == 0) {
-#pragma unroll
-        for (int i = 0; i < RED_MAX_N; ++i) part[wave][i] = acc[i];
-        part[wave][RED_MAX_N] = have;
-      }
-      __syncthreads();
-      write = threadIdx.x == 0;
-      if (write) {
-        for (int w = 1; w < 4; ++w) {
-          if (!part[w][RED_MAX_N]) continue;
-          if (have) {
-            body_fold(B, n, acc, part[w]);
-          } else {
-#pragma unroll
-            for (int i = 0; i < RED_MAX_N; ++i) acc[i] = part[w][i];
-            have = true;
-          }
-        }
-      }
-    }
-    if (write) {
-      uint32_t res[RED_MAX_N];
-#pragma unroll
-      for (int i = 0; i < RED_MAX_N; ++i)
-        res[i] = i >= n ? 0u : (A.init_ptr[i] ? load_bits(A.init_ptr[i], 0, A.init_dtype[i]) : A.init[i]);
-      if (have) body_fold(B, n, res, acc);
-#pragma unroll
-      for (int i = 0; i < RED_MAX_N; ++i)
-        if (i < n) store_bits(A.out[i], o, A.out_dtype[i], res[i], A.out_float[i] != 0);
-    }
-    if constexpr (G == 256) __syncthreads();  // part[] is reused by the next output
-  }
-}
-
-void launch_reduce_body(const ReduceBodyArgs& a, hipStream_t stream, hipEvent_t done) {
-  if (a.n < 1 || a.n > RED_MAX_N || a.prologue.n_out != a.n || a.body.n_out != a.n || a.body.n_leaves != 0)
-    fail(PJRT_Error_Code_INTERNAL, "reduce body step with inconsistent programs");
-  if (a.outer == 0) return record_done(done, stream);
-  const bool coords = a.prologue.needs_coords != 0;
-  dim3 block(256);
-  if (a.inner >= 1024) {  // long rows: a workgroup per output
-    dim3 grid((unsigned)(a.outer < 256 * 16 ? a.outer : 256 * 16));
-    if (coords) launch_k(done, reduce_body_kernel<256, true>, grid, block, 0, stream, a);
-    else launch_k(done, reduce_body_kernel<256, false>, grid, block, 0, stream, a);
-  } else {  // a wavefront per output
-    int64_t blocks = (a.outer + 3) / 4;
-    if (blocks > 256 * 16) blocks = 256 * 16;
-    dim3 grid((unsigned)blocks);
-    if (coords) launch_k(done, reduce_body_kernel<64, true>, grid, block, 0, stream, a);
-    else launch_k(done, reduce_body_kernel<64, false>, grid, block, 0, stream, a);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) fail(PJRT_Error_Code_INTERNAL, std::string("reduce launch failed: ") + hipGetErrorString(e));

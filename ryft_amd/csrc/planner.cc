@@ -905,6 +905,89 @@ void Planner::emit_pad(int node, int target) {
   mat_[node] = out;
 }
 
+// A reduce body's graph evaluated on host scalars: float values as doubles, integers (small ones) and predicates (0 /
+// 1) as doubles too. Only comparisons, selects and the logic ops are evaluated; false for a body with anything else.
+static bool eval_body_host(const Graph& b, const std::vector<double>& args, std::vector<double>* out) {
+  std::vector<double> v(b.nodes.size(), 0.0);
+  if (args.size() != b.params.size()) return false;
+  for (size_t k = 0; k < b.params.size(); ++k) v[b.params[k]] = args[k];
+  for (size_t i = 0; i < b.nodes.size(); ++i) {
+    const Node& n = b.nodes[i];
+    if (n.op == Op::Parameter) continue;
+    auto a = [&](size_t j) { return v[n.operands[j]]; };
+    const bool pred = n.type.dtype == DType::PRED;
+    switch (n.op) {
+      case Op::Compare: {
+        const double x = a(0), y = a(1);
+        bool r = false;
+        switch (n.cmp) {
+          case CmpDir::EQ: r = x == y; break;
+          case CmpDir::NE: r = x != y; break;
+          case CmpDir::GE: r = x >= y; break;
+          case CmpDir::GT: r = x > y; break;
+          case CmpDir::LE: r = x <= y; break;
+          case CmpDir::LT: r = x < y; break;
+        }
+        v[i] = r;
+        break;
+      }
+      case Op::Select: v[i] = a(0) != 0 ? a(1) : a(2); break;
+      case Op::And: case Op::Or: case Op::Xor: {
+        if (!pred) return false;
+        const bool x = a(0) != 0, y = a(1) != 0;
+        v[i] = n.op == Op::And ? (x && y) : n.op == Op::Or ? (x || y) : (x != y);
+        break;
+      }
+      case Op::Not:
+        if (!pred) return false;
+        v[i] = a(0) == 0;
+        break;
+      default:
+        return false;
+    }
+  }
+  out->clear();
+  for (int r : b.results) out->push_back(v[r]);
+  return true;
+}
+
+// Is the body argmax (ARG_MAX) or argmin (ARG_MIN) over (value, position) pairs, input `val` the value? A pair
+// replaces the accumulated one when its value is larger (smaller), a NaN beating every number, or equal with a
+// lower position. Checked on every ordering of accumulated and folded values (NaN, infinities, numbers, ties) and of
+// positions where the accumulated one is not the later (the order of a fold in index order, the one the kernel's
+// result equals): exhaustive for a body of comparisons, selects and logic ops, whose result depends only on how its
+// arguments compare.
+static int arg_kind_of(const Graph& b, int val, bool is_float, bool is_unsigned) {
+  const double inf = INFINITY, nan = NAN;
+  std::vector<double> vals = is_float ? std::vector<double>{nan, -inf, -2.5, 0.0, 1.0, 3.0, inf}
+                                      : (is_unsigned ? std::vector<double>{0, 1, 2, 9, 200}
+                                                     : std::vector<double>{-7, -1, 0, 2, 9});
+  const std::vector<double> pos = {0, 1, 4};
+  for (int kind : {ARG_MAX, ARG_MIN}) {
+    bool ok = true;
+    for (double a : vals)
+      for (double ai : pos)
+        for (double c : vals)
+          for (double ci : pos) {
+            if (!ok || ai > ci) continue;
+            // block arguments: the accumulated pair (value at index val), then the folded pair
+            std::vector<double> args(4), out;
+            args[val] = a, args[1 - val] = ai, args[2 + val] = c, args[3 - val] = ci;
+            if (!eval_body_host(b, args, &out) || out.size() != 2) return ARG_NONE;
+            const bool an = a != a, cn = c != c;
+            bool take;  // does (c, ci) replace (a, ai)?
+            if (an || cn) take = cn && (!an || ci < ai);
+            else if (a == c) take = ci < ai;
+            else take = kind == ARG_MAX ? c > a : c < a;
+            const double wv = take ? c : a, wi = take ? ci : ai;
+            const double gv = out[val], gi = out[1 - val];
+            if (gi != wi || !((gv != gv && wv != wv) || gv == wv)) ok = false;
+          }
+    if (ok) return kind;
+  }
+  return ARG_NONE;
+}
+
 // A reduce with a general body or several inputs: one REDUCE_BODY step computes every result of the op (the nodes
 // that share its operands and body), the node asked for into `target`.
 void Planner::emit_reduce_body(int node, int target) {
@@ -935,27 +1018,70 @@ void Planner::emit_reduce_body(int node, int target) {
     space.push_back(xn.type.shape[d]);
     inner *= xn.type.shape[d];
   }
-  // the body: block arguments k → EW_ACC k
-  ExprBuilder bb(*this, {});
-  bb.body = n.body.get();
-  for (size_t k = 0; k < n.body->params.size(); ++k) bb.acc_nodes[n.body->params[k]] = (int)k;
-  for (int i = 0; i < ni; ++i) bb.add_output(bb.emit(n.body->results[i], {}), n.body->nodes[n.body->results[i]].type.dtype);
-  const EwProgram body = bb.finish();
-  if (body.n_leaves) fail(PJRT_Error_Code_INTERNAL, "reduce body program reads memory");
+  // argmax / argmin: a value and an iota of positions along the one reduced dim, splat inits (position 0), and a
+  // body that behaves as the rule of arg_kind_of
+  int arg = ARG_NONE, val = 0;
+  if (ni == 2 && n.dims.size() == 1 && inner <= INT32_MAX) {
+    for (int v = 0; v < 2 && arg == ARG_NONE; ++v) {
+      const Node& x = g_.nodes[n.operands[v]];
+      const Node& ix = g_.nodes[n.operands[1 - v]];
+      const DType xt = x.type.dtype, it = ix.type.dtype;
+      double iv, xv;
+      const bool value_ok = float_class(xt) ? dtype_size(xt) <= 4 : (dtype_is_int(xt) && xt != DType::PRED &&
+                                                                      dtype_size(xt) <= 4);
+      if (!value_ok || ix.op != Op::Iota || ix.iota_dim != n.dims[0] || !dtype_is_int(it) || it == DType::PRED ||
+          !splat_value(n.operands[2 + v], &xv) || !splat_value(n.operands[3 - v], &iv) || iv != 0)
+        continue;
+      arg = arg_kind_of(*n.body, v, float_class(xt), dtype_is_unsigned(xt));
+      val = v;
+    }
+  }
+  EwProgram body{};
+  if (arg == ARG_NONE) {
+    // the body: block arguments k → EW_ACC k
+    ExprBuilder bb(*this, {});
+    bb.body = n.body.get();
+    for (size_t k = 0; k < n.body->params.size(); ++k) bb.acc_nodes[n.body->params[k]] = (int)k;
+    for (int i = 0; i < ni; ++i)
+      bb.add_output(bb.emit(n.body->results[i], {}), n.body->nodes[n.body->results[i]].type.dtype);
+    body = bb.finish();
+    if (body.n_leaves) fail(PJRT_Error_Code_INTERNAL, "reduce body program reads memory");
+  }
+  // long rows of few outputs run in segments (about 1024 items over the chip, ≥ 8192 elements each: 32 per thread of
+  // a workgroup), folded by a second launch in segment order
+  int64_t segs = 1;
+  if (inner >= 16384 && outer < 1024) segs = std::min<int64_t>((1024 + outer - 1) / outer, inner / 8192);
+  // (segments of whole 64-element chunks, so that the kernel can read them 8 elements at a time)
+  const int64_t seg_len = segs > 1 ? ((inner + segs - 1) / segs + 63) / 64 * 64 : std::max<int64_t>(1, inner);
   for (int attempt = 0; attempt < 2; ++attempt) {
     try {
       ExprBuilder b(*this, space);
-      for (int i = 0; i < ni; ++i) b.add_output(b.emit(n.operands[i], src), g_.nodes[n.operands[i]].type.dtype);
+      for (int i = 0; i < ni; ++i)
+        if (arg == ARG_NONE || i == val) b.add_output(b.emit(n.operands[i], src), g_.nodes[n.operands[i]].type.dtype);
       Step st{};
       st.kind = Step::REDUCE_BODY;
-      st.name = "reduce";
+      st.name = arg == ARG_MAX ? "argmax" : arg == ARG_MIN ? "argmin" : "reduce";
       ReduceBodyArgs& a = st.rbody;
       a.prologue = b.finish();
       a.body = body;
       a.outer = outer;
       a.inner = inner;
       a.n = ni;
+      a.segs = segs;
+      a.seg_len = seg_len;
+      a.arg_kind = arg;
+      a.val = val;
+      if (arg != ARG_NONE) {
+        const DType xt = g_.nodes[n.operands[val]].type.dtype;
+        a.value_class = float_class(xt) ? VC_FLOAT : dtype_is_unsigned(xt) ? VC_UNSIGNED : VC_SIGNED;
+      }
       push_program_patches(st, offsetof(ReduceBodyArgs, prologue), a.prologue, b.leaves(), {});
+      if (segs > 1) {
+        TensorType wt;
+        wt.dtype = DType::U32;
+        wt.shape = {outer * segs * (RED_MAX_N + 1)};
+        st.patches.push_back({offsetof(ReduceBodyArgs, ws), new_slot(Slot::TEMP, wt)});
+      }
       double bytes = leaf_bytes(plan_, b.leaves());
       for (int i = 0; i < ni; ++i) {
         const Node& init = g_.nodes[n.operands[ni + i]];
@@ -2131,7 +2257,7 @@ std::string Plan::describe() const {
       os << " outer=" << s.red.outer << " inner=" << s.red.inner;
     } else if (s.kind == Step::REDUCE_BODY) {
       os << " outer=" << s.rbody.outer << " inner=" << s.rbody.inner << " inputs=" << s.rbody.n
-         << " body_instrs=" << s.rbody.body.n_instr << " out=";
+         << " body_instrs=" << s.rbody.body.n_instr << " segments=" << s.rbody.segs << " out=";
       for (int i = 0; i < s.rbody.n; ++i) os << (i ? "," : "") << dtype_name((DType)s.rbody.out_dtype[i]);
     } else if (s.kind == Step::ROW) {
       os << " rows=" << s.row.rows << " inner=" << s.row.inner << " reductions=" << s.row.n_red

@@ -21,6 +21,6 @@ def test_more_than_one_gpu_exits_with_a_message():
 def test_help_lists_the_configs():
     r = _bench("--help")
     assert r.returncode == 0
-    for c in ("c1", "c2", "c3", "c4", "c5", "copy", "rmsnorm"):
+    for c in ("c1", "c2", "c3", "c4", "c5", "copy", "rmsnorm", "argmax"):
         assert c in r.stdout
     assert "--steps" in r.stdout and "--warmup" in r.stdout

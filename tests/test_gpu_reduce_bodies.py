@@ -53,11 +53,32 @@ def _exact(client, prog, ins, name):
 
 @pytest.mark.parametrize("kind", ["argmax", "argmin"])
 @pytest.mark.parametrize("dt", ["f32", "bf16", "i32"])
-@pytest.mark.parametrize("shape,dim", [((8, 1000), 1), ((8, 32000), 1), ((4100, 40), 1), ((300, 7, 3), 0),
-                                       ((5, 129, 6), 1)])
+@pytest.mark.parametrize("shape,dim", [((8, 1000), 1), ((8, 32000), 1), ((2, 100000), 1), ((4100, 40), 1),
+                                       ((300, 7, 3), 0), ((5, 129, 6), 1)])
 def test_argmax_argmin(gpu_client, kind, dt, shape, dim):
+    """The argmax / argmin rule (one wavefront or workgroup per row, or segments folded by a second launch for long
+    rows of few outputs), against the oracle's fold of the body in index order."""
     prog = argmax_program(shape, dim, dt=dt, kind=kind)
     _exact(gpu_client, prog, [_values(11, shape, dim, dt, nan=dt != "i32")], f"{kind} {dt} {shape} dim {dim}")
+
+
+def test_argmax_i64_positions_and_several_nans(gpu_client):
+    # i64 positions; rows with several NaNs (the first one wins, as in a fold in index order)
+    shape = (40, 6000)
+    x = _values(17, shape, 1, "f32")
+    x.data[3, [10, 20, 4000]] = np.nan
+    x.data[7, [5999, 1]] = np.nan
+    for kind in ("argmax", "argmin"):
+        _exact(gpu_client, argmax_program(shape, 1, it="i64", kind=kind), [x], f"{kind} i64 positions")
+
+
+def test_body_program_in_segments(gpu_client):
+    # a body the rule does not cover (xor) over long rows of few outputs: segments folded by a second launch
+    shape = (3, 50000)
+    x = np.random.default_rng(18).integers(-2 ** 31, 2 ** 31, size=shape).astype(np.int32)
+    prog = one_input_program(shape, 1, "xor", "i32")
+    assert "segments=" in gpu_client.compile(pjrt.Program.mlir(prog)).describe_plan()
+    _exact(gpu_client, prog, [configs.HostInput(x, pjrt.BufferType.S32, shape)], "xor in segments")
 
 
 def test_argmax_generic_form_and_bytecode(gpu_client):

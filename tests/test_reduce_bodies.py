@@ -194,9 +194,33 @@ def test_forms_plan_alike(compile_client, kind):
                                                                                    form="generic"))]
     plans += [_plan(compile_client, mb.to_bytecode(printed, **o)) for o in ({}, {"isolated_reduce": True})]
     assert all(p == plans[0] for p in plans), plans
-    # one step computes both results, each written straight into its output buffer
-    assert plans[0].count("reduce") == 1 and "inputs=2" in plans[0] and "copy" not in plans[0]
-    assert "out=f32,i32" in plans[0], plans[0]
+    # one step computes both results, each written straight into its output buffer; the body is recognised as the
+    # argmax / argmin rule (no body program)
+    assert plans[0].startswith(f"0: {kind} ") and "inputs=2" in plans[0] and "copy" not in plans[0], plans[0]
+    assert "out=f32,i32" in plans[0] and "body_instrs=0" in plans[0], plans[0]
+
+
+def test_argmax_recognition(compile_client):
+    # integer and bf16 values, the reduced dim outermost, an i64 position
+    for prog in (argmax_program((6, 40), 1, dt="i32"), argmax_program((40, 6), 0, dt="bf16", it="i64"),
+                 argmax_program((3, 4, 50), 2, kind="argmin", form="generic")):
+        plan = _plan(compile_client, prog)
+        assert plan.split()[1] in ("argmax", "argmin") and "body_instrs=0" in plan, plan
+    # long rows of few outputs: segments folded by a second launch
+    plan = _plan(compile_client, argmax_program((8, 32000), 1))
+    assert "segments=3" in plan, plan
+    # bodies that are not the rule run the body program: the later position winning ties, or a value compared
+    # with a constant
+    later = argmax_program((6, 40), 1).replace("LT, %ai, %bi", "GT, %ai, %bi")
+    capped = argmax_program((6, 40), 1).replace(
+        "%3 = stablehlo.compare  NE, %a, %a,  FLOAT", "%k = stablehlo.constant dense<1.000000e+00> : tensor<f32>\n"
+        "      %3 = stablehlo.compare  NE, %a, %k,  FLOAT")
+    for prog in (later, capped):
+        plan = _plan(compile_client, prog)
+        assert plan.startswith("0: reduce ") and "body_instrs=0" not in plan, plan
+    # the index input must be an iota along the reduced dim
+    other_dim = argmax_program((6, 40), 1).replace("stablehlo.iota dim = 1", "stablehlo.iota dim = 0")
+    assert _plan(compile_client, other_dim).startswith("0: reduce ")
 
 
 def test_one_input_general_bodies_plan(compile_client):
@@ -255,3 +279,17 @@ def test_inputs_of_different_shapes_and_three_inputs(compile_client):
     with pytest.raises(pjrt.PjrtError) as e:
         compile_client.compile(pjrt.Program.mlir(three))
     assert e.value.code == pjrt.ErrorCode.UNIMPLEMENTED and "inputs" in e.value.message
+
+
+def test_argmax_workload(compile_client):
+    """bench.py's argmax workload (ryft_amd/configs.py) is the argmax rule: its plan, and its oracle against numpy's
+    argmax on a small instance."""
+    from ryft_amd import configs
+    w = configs.CONFIGS["argmax"](m=4, v=4096)
+    plan = _plan(compile_client, w.program)
+    assert plan.startswith("0: argmax ") and "out=f32,i32" in plan, plan
+    x = sh.from_raw(w.inputs[0].data, "f32")
+    (v, _), (i, _) = sh.evaluate(w.program, [x])
+    assert np.array_equal(i, np.argmax(x, axis=1)) and np.array_equal(v, np.max(x, axis=1))
+    full = configs.CONFIGS["argmax"]()
+    assert _plan(compile_client, full.program).startswith("0: argmax ") and full.bytes == 4.0 * 64 * 128256 + 8 * 64
