@@ -154,8 +154,8 @@ class Module:
                         break
                 out.append("\n".join(block))
                 continue
-            if ln.startswith("%") and '"stablehlo.reduce"(' in ln and "({" in ln:
-                # generic region form: up to the line that closes the region, `}) ... : (...) -> (...)`
+            if ln.startswith("%") and ln.endswith("({"):
+                # generic region form (reduce, map): up to the line that closes the region, `}) ... : (...) -> (...)`
                 block = [ln]
                 while not block[-1].startswith("})"):
                     block.append(lines[i].strip())
@@ -213,7 +213,7 @@ _RET = re.compile(r"(?:func\.)?return\s+(.*?)(?:\s*:\s*.*)?$")
 
 
 def _operands(rest: str, n: int, env) -> List[Tuple[np.ndarray, str]]:
-    names = re.findall(r"%[\w.$-]+", rest.split(":")[0])[:n]
+    names = re.findall(r"%[\w.$#-]+", rest.split(":")[0])[:n]
     return [env[x] for x in names]
 
 
@@ -351,6 +351,51 @@ def _eval_op(op: str, rest: str, env, dot_precision: str) -> Tuple[np.ndarray, s
         return out, dt
     if op == "gather":
         return _gather(rest, env, out_shape)
+    if op == "reverse":
+        # miscellaneous.rs:309-370: result[i] = operand[i with each listed dim d read from the end]
+        (x, dt), = _operands(rest, 1, env)
+        dm = re.search(r"(?:dims|dimensions)\s*=\s*(array<[^>]*>|\[[^\]]*\])", rest)
+        dims = _ints(dm.group(1).split(":", 1)[1] if dm.group(1).startswith("array") else dm.group(1))
+        return np.flip(np.asarray(x), axis=tuple(dims)).copy(), dt
+    if op == "optimization_barrier":
+        # miscellaneous.rs:405-450: the identity on each operand
+        names = re.findall(r"%[\w.$#-]+", rest.split(":")[0])
+        vals = [env[n] for n in names]
+        return vals if len(vals) > 1 else vals[0]
+    if op == "bitcast_convert":
+        # casting.rs:8-73 (same element width): the element's bits reread as the result type
+        (x, dt), = _operands(rest, 1, env)
+        raw = np.ascontiguousarray(to_raw(np.asarray(x), dt))
+        want = {"f32": np.float32, "i32": np.int32, "ui32": np.uint32, "bf16": np.uint16, "f16": np.uint16,
+                "i16": np.int16, "ui16": np.uint16, "f8E4M3FN": np.uint8, "f8E5M2": np.uint8, "i8": np.int8,
+                "ui8": np.uint8}[out_dt]
+        if raw.dtype.itemsize != np.dtype(want).itemsize:
+            raise NotImplementedError("bitcast_convert between widths")
+        return from_raw(raw.view(want), out_dt), out_dt
+    if op == "map":
+        # functional.rs:13-104: the body applied to the inputs' elements (here to whole arrays at once)
+        names = re.findall(r"%[\w.$-]+", rest[:rest.index("(")] if "(" in rest else rest)
+        region = rest[rest.index("^bb"):rest.rindex("})")]
+        first, _, body = region.partition("\n")
+        args = re.findall(r"(%[\w.$-]+)\s*:", first[:first.index(")")])
+        benv = dict(zip(args, [env[n] for n in names]))
+        rets = None
+        for ln in body.split("\n"):
+            ln = ln.strip()
+            if not ln:
+                continue
+            rm = re.match(r'"?stablehlo\.return"?\s*\(?(.*?)\)?\s*:', ln)
+            if rm:
+                rets = re.findall(r"%[\w.$-]+", rm.group(1))
+                break
+            m = re.match(r"(%[\w.$-]+)\s*=\s*(?:stablehlo|mhlo)\.(\w+)\s*(.*)$", ln)
+            if m:
+                benv[m.group(1)] = _eval_op(m.group(2), m.group(3), benv, dot_precision)
+            else:
+                m = re.match(r'(%[\w.$-]+)\s*=\s*"(?:stablehlo|mhlo)\.(\w+)"\((.*?)\)\s*(.*)$', ln)
+                benv[m.group(1)] = _eval_op(m.group(2), m.group(3) + " " + m.group(4), benv, dot_precision)
+        v, dt = benv[rets[0]]
+        return normalize(np.broadcast_to(np.asarray(v), out_shape), out_dt), out_dt
     if op == "concatenate":
         # manipulation.rs:778-822: the inputs one after another along `dim`, in operand order
         head = rest.split(":")[0]

@@ -40,10 +40,13 @@ enum class Op : uint8_t {
   // elementwise, binary
   Add, Subtract, Multiply, Divide, Maximum, Minimum, Power, Remainder, And, Or, Xor, Compare,
   Atan2, ShiftLeft, ShiftRightArithmetic, ShiftRightLogical,
+  // elementwise, unary, the element's bits reread as another type of the same width
+  BitcastConvert,
   // elementwise, ternary
   Select, Clamp,
   // data movement
   BroadcastInDim, Transpose, Reshape, Iota, Slice, Concatenate, Pad, DynamicSlice, DynamicUpdateSlice, Gather,
+  Reverse,
   // contractions and reductions
   DotGeneral, Reduce,
 };
@@ -73,7 +76,7 @@ struct Node {
   TensorType type;
   std::vector<int> operands;
   // attributes (meaning depends on op)
-  std::vector<int64_t> dims;  // broadcast_dimensions / permutation / reduce dimensions / slice_sizes (dynamic_slice, gather)
+  std::vector<int64_t> dims;  // broadcast_dimensions / permutation / reduce and reverse dimensions / slice_sizes
   // slice: start / limit / stride per dim; pad: edge_padding_low / edge_padding_high / interior_padding
   std::vector<int64_t> lo, hi, step;
   int64_t axis = 0;  // concatenate dimension

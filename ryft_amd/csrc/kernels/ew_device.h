@@ -179,6 +179,31 @@ __device__ __forceinline__ int32_t sign_extend(uint32_t v, int w) {
   return w >= 32 ? (int32_t)v : (int32_t)(v << (32 - w)) >> (32 - w);
 }
 
+// bitcast_convert of one element between types of one width: the register form of `from` → the element's raw bits
+// → the register form of `to` (floats as f32 values, bf16 as its bits in the high half, integers sign- or
+// zero-extended).
+__device__ __noinline__ uint32_t bitcast_reg(uint32_t r, int from, int to) {
+  uint32_t bits;
+  switch (from) {
+    case DT_BF16: bits = r >> 16; break;
+    case DT_F16: bits = __builtin_bit_cast(uint16_t, (_Float16)__uint_as_float(r)); break;
+    case DT_F8E4M3FN: bits = f32_to_e4m3fn_bits(__uint_as_float(r)); break;
+    case DT_F8E5M2: bits = f32_to_e5m2_bits(__uint_as_float(r)); break;
+    case DT_S8: case DT_U8: bits = r & 0xffu; break;
+    case DT_S16: case DT_U16: bits = r & 0xffffu; break;
+    default: bits = r; break;  // 32-bit types
+  }
+  switch (to) {
+    case DT_BF16: return bits << 16;
+    case DT_F16: return __float_as_uint((float)__builtin_bit_cast(_Float16, (uint16_t)bits));
+    case DT_F8E4M3FN: return __float_as_uint(e4m3fn_bits_to_f32(bits));
+    case DT_F8E5M2: return __float_as_uint(e5m2_bits_to_f32(bits));
+    case DT_S8: return (uint32_t)(int32_t)(int8_t)bits;
+    case DT_S16: return (uint32_t)(int32_t)(int16_t)bits;
+    default: return bits;  // 32-bit types, u8, u16
+  }
+}
+
 __device__ __forceinline__ float f_logistic(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
 // Saturating float → int conversion (NaN → 0), truncating toward zero.
@@ -435,7 +460,7 @@ __host__ __device__ inline bool ew_is_heavy(int op) {
   switch (op) {
     case EW_LOG: case EW_TANH: case EW_EXPM1: case EW_LOG1P: case EW_CVT_F2I: case EW_POW: case EW_REM:
     case EW_IDIV: case EW_IREM: case EW_UDIV: case EW_UREM: case EW_SIN: case EW_COS: case EW_TAN: case EW_CBRT:
-    case EW_ATAN2:
+    case EW_ATAN2: case EW_BITCAST:
       return true;
     default:
       return false;
@@ -504,6 +529,11 @@ __device__ __forceinline__ void ew_run_v(const EwProgram& P, int64_t lin, const 
       EW_F(EW_RINT, rintf(EW_FA))
       EW_F(EW_ROUND, roundf(EW_FA))
       EW_U(EW_ISFINITE, (EW_UA & 0x7f800000u) != 0x7f800000u)
+      case EW_BITCAST:  // out of line, like the heavy ops
+        if constexpr (!PRE) {
+          _Pragma("unroll 1") for (int e = 0; e < V; ++e) r[e] = bitcast_reg(ra[e], I.imm.i >> 8, I.imm.i & 0xff);
+        }
+        break;
       EW_U(EW_INEG, -EW_IA)
       EW_U(EW_IABS, EW_IA < 0 ? -EW_IA : EW_IA)
       EW_U(EW_NOT, (I.round == DT_PRED) ? (uint32_t)(EW_IA == 0) : ~EW_UA)

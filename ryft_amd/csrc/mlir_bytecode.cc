@@ -608,6 +608,8 @@ class BytecodeParser {
                              {"strides", true, {BAttr::DENSE_ARRAY}}}},
         {"stablehlo.concatenate", {{"dimension", true, {BAttr::INT}}}},
         {"stablehlo.dynamic_slice", {{"slice_sizes", true, {BAttr::DENSE_ARRAY}}}},
+        {"stablehlo.reverse", {{"dimensions", true, {BAttr::DENSE_ARRAY}}}},
+        {"stablehlo.map", {{"dimensions", true, {BAttr::DENSE_ARRAY}}}},
         {"stablehlo.gather",
          {{"dimension_numbers", true, {BAttr::GATHER_DIMS}},
           {"indices_are_sorted", false, {BAttr::INT}},
@@ -967,6 +969,21 @@ class BytecodeParser {
       }
       if (op.name.rfind("stablehlo.", 0) != 0) unimplemented(op.name + " is not supported by the MI355X plugin");
       const std::string nm = op.name.substr(10);
+      if (nm == "optimization_barrier") {  // (miscellaneous.rs:405-450) the identity on each operand
+        if (op.results.size() != op.operands.size()) invalid("optimization_barrier: one result per operand");
+        for (size_t i = 0; i < op.results.size(); ++i) node_of[op.results[i]] = value(op.operands[i]);
+        continue;
+      }
+      if (nm == "map") {  // (functional.rs:13-104) the body inlined over the inputs' shape
+        if (op.regions.size() != 1 || op.results.size() != 1 || op.result_types.size() != 1)
+          invalid("map: expected one body region and one result");
+        std::vector<int> inputs;
+        for (int64_t v : op.operands) inputs.push_back(value(v));
+        const std::shared_ptr<Graph> body = build_region(op.regions[0]);
+        node_of[op.results[0]] =
+            mlir_inline_map(g, inputs, tensor_type(op.result_types[0]), int_list(op, "dimensions"), *body);
+        continue;
+      }
       if (nm == "reduce") {
         // reduce (functional.rs:109-230): a node per result, sharing operands, dimensions and body
         Node n;
@@ -987,7 +1004,6 @@ class BytecodeParser {
         n.debug = "%" + std::to_string(g.nodes.size());
         n.type = tensor_type(op.result_types[0]);
         for (int64_t v : op.operands) n.operands.push_back(value(v));
-        if (nm == "bitcast_convert") unimplemented("bitcast_convert is not supported");
         auto it = simple.find(nm);
         if (it != simple.end()) {
           n.op = it->second;
@@ -1012,6 +1028,9 @@ class BytecodeParser {
         } else if (nm == "dynamic_slice") {
           n.op = Op::DynamicSlice;
           n.dims = int_list(op, "slice_sizes");
+        } else if (nm == "reverse") {
+          n.op = Op::Reverse;
+          n.dims = int_list(op, "dimensions");
         } else if (nm == "dynamic_update_slice") {
           n.op = Op::DynamicUpdateSlice;
         } else if (nm == "gather") {

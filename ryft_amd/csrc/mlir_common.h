@@ -28,6 +28,9 @@ const std::unordered_map<std::string, Op>& mlir_simple_ops();
 // The nodes of one reduce op, one per result (`proto` holds the operands and dimensions). The body is `applies`
 // (the pretty form's single body op, e.g. "stablehlo.add") or `body`, the region as a graph; a region that applies
 // one recognised binary op to its two block arguments becomes that op, any other a ReduceBody::General node.
+// map: the body's ops copied into `g` over the result's shape; returns the node of the body's result.
+int mlir_inline_map(Graph& g, const std::vector<int>& inputs, const TensorType& result, const std::vector<int64_t>& dims,
+                    const Graph& body);
 std::vector<Node> mlir_reduce_nodes(const Graph& g, const Node& proto, const std::vector<TensorType>& results,
                                     const std::string& applies, std::shared_ptr<const Graph> body);
 

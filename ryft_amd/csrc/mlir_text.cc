@@ -42,6 +42,7 @@ const std::unordered_map<std::string, Op>& mlir_simple_ops() {
       {"popcnt", Op::Popcnt},       {"count_leading_zeros", Op::CountLeadingZeros},
       {"atan2", Op::Atan2},         {"shift_left", Op::ShiftLeft},
       {"shift_right_arithmetic", Op::ShiftRightArithmetic}, {"shift_right_logical", Op::ShiftRightLogical},
+      {"bitcast_convert", Op::BitcastConvert},
   };
   return m;
 }
@@ -110,6 +111,8 @@ const char* op_name(Op op) {
     case Op::DynamicUpdateSlice: return "dynamic_update_slice";
     case Op::Gather: return "gather";
     case Op::Iota: return "iota";
+    case Op::Reverse: return "reverse";
+    case Op::BitcastConvert: return "bitcast_convert";
     case Op::DotGeneral: return "dot_general";
     case Op::Reduce: return "reduce";
   }
@@ -125,7 +128,7 @@ bool op_is_elementwise(Op op) {
     case Op::Select: case Op::Clamp: case Op::Sine: case Op::Cosine: case Op::Tan: case Op::Cbrt:
     case Op::RoundNearestEven: case Op::RoundNearestAfz: case Op::IsFinite: case Op::Popcnt:
     case Op::CountLeadingZeros: case Op::Atan2: case Op::ShiftLeft: case Op::ShiftRightArithmetic:
-    case Op::ShiftRightLogical:
+    case Op::ShiftRightLogical: case Op::BitcastConvert:
       return true;
     default:
       return false;
@@ -933,7 +936,6 @@ class Parser {
       auto it = os.attrs.find(k);
       return it == os.attrs.end() ? std::string() : it->second;
     };
-    if (nm == "bitcast_convert") unimplemented("bitcast_convert is not supported");
     auto it = simple.find(nm);
     if (it != simple.end()) {
       n.op = it->second;
@@ -989,6 +991,21 @@ class Parser {
       n.op = Op::Compare;
       n.cmp = parse_dir(get("comparison_direction"));
       n.cmp_type = parse_cmp_type(get("compare_type"));
+    } else if (nm == "reverse") {
+      n.op = Op::Reverse;
+      std::string d = get("dims");
+      n.dims = parse_int_list_text(d.empty() ? get("dimensions") : d);
+    } else if (nm == "optimization_barrier") {
+      // (miscellaneous.rs:405-450) the identity on each operand
+      if (os.results.size() != n.operands.size()) invalid("optimization_barrier: one result per operand");
+      for (size_t i = 0; i < n.operands.size(); ++i) names_[os.results[i]] = n.operands[i];
+      return;
+    } else if (nm == "map") {
+      if (!os.body) invalid("map without a body");
+      if (os.results.size() != 1) invalid("map has one result");
+      names_[os.results[0]] = mlir_inline_map(graph_, n.operands, result_type(os), parse_int_list_text(get("dimensions")),
+                                              *os.body);
+      return;
     } else if (nm == "reduce") {
       n.op = Op::Reduce;
       n.dims = parse_int_list_text(get("dimensions"));
@@ -1175,6 +1192,12 @@ void validate_node(const Graph& g, Node& n) {
     case Op::Reshape:
       need(1);
       if (opt(0).elements() != n.type.elements()) invalid("reshape: element count mismatch");
+      break;
+    case Op::Reverse:
+      // miscellaneous.rs:309-370: dimensions distinct and in range, the result the operand's type
+      need(1);
+      dims_in_range({&n.dims}, opt(0).rank(), "reverse");
+      if (!(n.type == opt(0))) invalid("reverse: result type differs from the operand's");
       break;
     case Op::Slice: {
       need(1);
@@ -1421,6 +1444,14 @@ void validate_node(const Graph& g, Node& n) {
           case Op::ShiftRightLogical:
             all_types(is_integer, "integer", true);
             break;
+          case Op::BitcastConvert: {
+            // (casting.rs:8-73) same shape here: a change of element width would add or drop a dimension
+            const DType a = opt(0).dtype, r = n.type.dtype;
+            if (a == DType::PRED || r == DType::PRED || dtype_size(a) != dtype_size(r))
+              unimplemented("bitcast_convert between element types of different widths (or i1) is not supported");
+            if (dtype_size(a) > 4) unimplemented("bitcast_convert of 64-bit elements is not supported");
+            break;
+          }
           default:
             break;
         }
@@ -1489,6 +1520,46 @@ std::vector<Node> mlir_reduce_nodes(const Graph& g, const Node& proto, const std
     out.push_back(std::move(m));
   }
   return out;
+}
+
+// map (functional.rs:13-104): the body applied to the inputs' elements. Its ops are copied into `g` over the inputs'
+// shape (block argument k → input k, rank-0 constants → splat constants of that shape), so that the result is an
+// ordinary elementwise expression; returns the node of the body's result.
+int mlir_inline_map(Graph& g, const std::vector<int>& inputs, const TensorType& result, const std::vector<int64_t>& dims,
+                    const Graph& body) {
+  const int r = result.rank();
+  if ((int)dims.size() != r) invalid("map: dimensions must name every dimension");
+  for (int d = 0; d < r; ++d)
+    if (dims[d] != d) invalid("map: dimensions must be 0, 1, ..., rank - 1");
+  if (inputs.empty() || body.params.size() != inputs.size() || body.results.size() != 1)
+    invalid("map: the body takes one argument per input and returns one value");
+  for (size_t k = 0; k < inputs.size(); ++k) {
+    const TensorType& it = g.nodes[inputs[k]].type;
+    const TensorType& pt = body.nodes[body.params[k]].type;
+    if (it.shape != result.shape) invalid("map: inputs and result must have one shape");
+    if (pt.rank() != 0 || pt.dtype != it.dtype) invalid("map: body arguments must be scalars of the inputs' types");
+  }
+  const TensorType& rt = body.nodes[body.results[0]].type;
+  if (rt.rank() != 0 || rt.dtype != result.dtype) invalid("map: the body result must be a scalar of the result type");
+  std::vector<int> id(body.nodes.size(), -1);
+  for (size_t k = 0; k < body.params.size(); ++k) id[body.params[k]] = inputs[k];
+  for (size_t i = 0; i < body.nodes.size(); ++i) {
+    const Node& bn = body.nodes[i];
+    if (bn.op == Op::Parameter) continue;
+    if (bn.op != Op::Constant && !op_is_elementwise(bn.op))
+      unimplemented(std::string("map bodies with stablehlo.") + op_name(bn.op) + " are not supported");
+    Node m = bn;
+    m.type.shape = result.shape;
+    for (int& o : m.operands) {
+      if (o < 0 || id[o] < 0) invalid("map: body value used before its definition");
+      o = id[o];
+    }
+    if (bn.op == Op::Constant && !bn.splat) invalid("map: a body constant must be a scalar");
+    validate_node(g, m);
+    g.nodes.push_back(std::move(m));
+    id[i] = (int)g.nodes.size() - 1;
+  }
+  return id[body.results[0]];
 }
 
 Graph parse_mlir_text(const std::string& text, const std::string& entry) {

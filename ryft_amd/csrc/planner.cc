@@ -119,6 +119,7 @@ class ExprBuilder {
   int push(EwInstr ins, bool is_float, std::vector<int> srcs);
   int leaf_index(const Leaf& l);
   Val leaf_load(int node, const std::vector<int>& src, DType dtype);
+  Val leaf_of_view(const View& v, const std::vector<int>& src, DType dtype);
   Val convert(Val v, DType from, DType to);
 
   Planner& P_;
@@ -217,7 +218,12 @@ ExprBuilder::Val ExprBuilder::leaf_load(int node, const std::vector<int>& src, D
     ins.op = EW_CONST;
     return {push(ins, float_class(dtype), {}), float_class(dtype)};
   }
-  View v = P_.view_of(node);
+  return leaf_of_view(P_.view_of(node), src, dtype);
+}
+
+// A load of view `v` (view dim d ↔ space dim src[d], -1: broadcast along it).
+ExprBuilder::Val ExprBuilder::leaf_of_view(const View& v, const std::vector<int>& src, DType dtype) {
+  EwInstr ins{};
   Leaf l;
   l.slot = v.slot;
   l.dtype = v.dtype;
@@ -307,6 +313,18 @@ ExprBuilder::Val ExprBuilder::emit(int node, const std::vector<int>& src) {
   } else if (n.op == Op::Slice) {
     // a slice is a view of its operand: offset by the start indices, strides scaled by the slice strides
     out = leaf_load(node, src, dt);
+  } else if (n.op == Op::Reverse) {
+    // a reverse reads its operand's view backwards along the reversed dims: from the last element, negated strides
+    if (dry) {
+      out = leaf_load(node, src, dt);
+    } else {
+      View v = P_.view_of(n.operands[0]);
+      for (int64_t d : n.dims) {
+        v.offset += (n.type.shape[d] - 1) * v.strides[d];
+        v.strides[d] = -v.strides[d];
+      }
+      out = leaf_of_view(v, src, dt);
+    }
   } else if (op_is_elementwise(n.op)) {
     inner_nodes.insert(node);
     std::vector<Val> ops;
@@ -364,6 +382,13 @@ ExprBuilder::Val ExprBuilder::emit(int node, const std::vector<int>& src) {
         break;
       }
       case Op::Atan2: out = bin(EW_ATAN2, EW_ATAN2, EW_ATAN2); break;
+      case Op::BitcastConvert:
+        // the element's bits reread as `dt`: imm = (from type << 8) | to type
+        ins.op = EW_BITCAST;
+        ins.imm.i = ((int32_t)ot << 8) | (int32_t)dt;
+        ins.round = 0;
+        out = {push(ins, fl, {ops[0].instr}), fl};
+        break;
       case Op::IsFinite:
         ins.op = EW_ISFINITE;
         ins.round = 0;
@@ -595,6 +620,33 @@ int Planner::materialize(int node, int target) {
   return mat_.at(node);
 }
 
+// A program that only moves 64-bit elements (one load of one leaf, stored as the same type) rewritten to move them as
+// pairs of 32-bit words: one more innermost dimension of extent 2, strides and offsets in words. The VM's registers
+// are 32 bits wide, so a 64-bit value read through them would lose bits; a reverse, slice, transpose or broadcast of
+// f64 / i64 / ui64 values stays exact this way.
+static void move_64bit_as_words(EwProgram& p) {
+  if (p.n_instr != 1 || p.instr[0].op != EW_LOAD || p.n_leaves != 1 || p.n_out != 1 || p.rank >= EW_MAX_RANK) return;
+  EwLeaf& L = p.leaves[0];
+  if (L.dtype != p.out_dtype[0] || dtype_size((DType)L.dtype) != 8 || L.kind == EW_LEAF_SCALAR) return;
+  const int r = p.rank;
+  p.shape[r] = 2;
+  p.rank = r + 1;
+  p.total *= 2;
+  L.offset *= 2;
+  if (L.kind == EW_LEAF_GENERAL) {
+    for (int d = 0; d < r; ++d) L.strides[d] *= 2;
+    L.strides[r] = 1;
+  }
+  L.dtype = p.out_dtype[0] = (int32_t)DType::U32;
+  p.instr[0].round = 0;
+  p.out_float_mask = 0;
+  if (p.out_strided) {
+    for (int d = 0; d < r; ++d) p.out_strides[d] *= 2;
+    p.out_strides[r] = 1;
+    p.out_offset *= 2;
+  }
+}
+
 void Planner::emit_elementwise_root(int node, int target) {
   const Node& n = g_.nodes[node];
   std::vector<int> ident(n.type.rank());
@@ -664,6 +716,7 @@ void Planner::emit_elementwise_root(int node, int target) {
       } else {
         st.kind = Step::ELEMENTWISE;
         st.name = "elementwise";
+        move_64bit_as_words(p);
         st.ew = p;
         push_program_patches(st, 0, p, b.leaves(), {out});
         st.bytes = leaf_bytes(plan_, b.leaves()) + (double)n.type.bytes();
@@ -687,6 +740,7 @@ void Planner::push_strided_step(ExprBuilder& b, const char* name, int out, int64
   p.needs_coords = 1;
   p.out_offset = out_offset;
   for (int d = 0; d < p.rank; ++d) p.out_strides[d] = out_strides[d];
+  move_64bit_as_words(p);
   Step st{};
   st.kind = Step::ELEMENTWISE;
   st.name = name;

@@ -222,6 +222,9 @@ def _parse_gather(res: str, rhs: str) -> Op:
 
 def _parse_op(res: str, name: str, rest: str) -> Op:
     short = name.split(".", 1)[1]
+    if short == "optimization_barrier":  # `%r:k = stablehlo.optimization_barrier %a, %b : A, B`
+        body, ty = rest.split(" : ", 1)
+        return Op(name, [x.strip() for x in body.split(",")], _result_names(res), [t.strip() for t in _split_top(ty)])
     if short == "constant":
         val, ty = rest.rsplit(":", 1)
         return Op(name, [], [res], [ty.strip()], {"value": ("dense", val.strip(), ty.strip())})
@@ -262,6 +265,9 @@ def _parse_op(res: str, name: str, rest: str) -> Op:
         key = "broadcast_dimensions" if short == "broadcast_in_dim" else "permutation"
         kv = [x for x in items if x.startswith("dims")][0]
         attrs[key] = ("i64s", _ints(kv.split("=", 1)[1]))
+    if short == "reverse":
+        kv = [x for x in items if x.startswith("dims")][0]
+        attrs["dimensions"] = ("i64s", _ints(kv.split("=", 1)[1]))
     if short == "dynamic_slice":
         kv = [x for x in items if x.startswith("sizes")][0]
         attrs["slice_sizes"] = ("i64s", _ints(kv.split("=", 1)[1]))

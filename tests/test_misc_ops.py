@@ -1,0 +1,177 @@
+"""reverse, optimization_barrier, map and same-width bitcast_convert (crates/ryft-mlir/src/dialects/stable_hlo/
+operations/miscellaneous.rs:309-450, functional.rs:13-104, casting.rs:8-73), on the CPU:
+
+  * oracle      the reference's worked examples (reverse [[1, 2], [3, 4], [5, 6]] along dim 1, map's multiply of
+                [[0, 1], [2, 3]] and [[4, 5], [6, 7]], optimization_barrier's identity), numpy's flip for more
+                reversals, and bitcast_convert against numpy's views of the same bytes;
+  * front-ends  printed, generic and bytecode forms plan alike (map as its generic form: it has no printed one);
+                reverse is a backwards read (one elementwise step, no copy), optimization_barrier and map leave no
+                step of their own;
+  * checks      repeated or out-of-range reverse dims, map dimensions other than 0..rank-1, a map body of the wrong
+                arity and a bitcast_convert that changes the element width are refused.
+GPU parity: tests/test_gpu_misc_ops.py."""
+import numpy as np
+import pytest
+
+from oracle import stablehlo as sh
+from ryft_amd import pjrt
+from tests import mlir_bytecode as mb
+
+
+def _t(shape, dt):
+    return "tensor<" + "".join(f"{d}x" for d in shape) + dt + ">"
+
+
+def reverse_program(shape, dims, dt="i32", consumer=False):
+    T = _t(shape, dt)
+    ds = ", ".join(map(str, dims))
+    extra = f"\n    %1 = stablehlo.add %0, %arg0 : {T}" if consumer else ""
+    ret = "%1" if consumer else "%0"
+    return f"""module {{
+  func.func @main(%arg0: {T}) -> {T} {{
+    %0 = stablehlo.reverse %arg0, dims = [{ds}] : {T}{extra}
+    return {ret} : {T}
+  }}
+}}
+"""
+
+
+def map_program(shape, dt="i32"):
+    """The reference's example body (multiply), plus a compare / select and a constant to inline."""
+    T, S = _t(shape, dt), f"tensor<{dt}>"
+    P = _t(shape, "i1")
+    return f"""module {{
+  func.func @main(%arg0: {T}, %arg1: {T}) -> ({T}, {T}) {{
+    %0 = "stablehlo.map"(%arg0, %arg1) <{{dimensions = array<i64: {", ".join(str(d) for d in range(len(shape)))}>}}> ({{
+    ^bb0(%arg2: {S}, %arg3: {S}):
+      %1 = stablehlo.multiply %arg2, %arg3 : {S}
+      stablehlo.return %1 : {S}
+    }}) : ({T}, {T}) -> {T}
+    %2 = "stablehlo.map"(%arg0, %arg1) <{{dimensions = array<i64: {", ".join(str(d) for d in range(len(shape)))}>}}> ({{
+    ^bb0(%a: {S}, %b: {S}):
+      %c = stablehlo.constant dense<3> : {S}
+      %d = stablehlo.add %a, %c : {S}
+      %e = stablehlo.compare  GT, %d, %b : ({S}, {S}) -> tensor<i1>
+      %f = stablehlo.select %e, %d, %b : tensor<i1>, {S}
+      stablehlo.return %f : {S}
+    }}) : ({T}, {T}) -> {T}
+    return %0, %2 : {T}, {T}
+  }}
+}}
+"""
+
+
+def barrier_program(shape):
+    T = _t(shape, "f32")
+    return f"""module {{
+  func.func @main(%arg0: {T}, %arg1: {T}) -> ({T}, {T}) {{
+    %0:2 = stablehlo.optimization_barrier %arg0, %arg1 : {T}, {T}
+    %1 = stablehlo.multiply %0#0, %0#1 : {T}
+    return %1, %0#1 : {T}, {T}
+  }}
+}}
+"""
+
+
+def bitcast_program(shape, src, dst, generic=False):
+    A, B = _t(shape, src), _t(shape, dst)
+    op = (f'%0 = "stablehlo.bitcast_convert"(%arg0) : ({A}) -> {B}' if generic
+          else f"%0 = stablehlo.bitcast_convert %arg0 : ({A}) -> {B}")
+    return f"""module {{
+  func.func @main(%arg0: {A}) -> {B} {{
+    {op}
+    return %0 : {B}
+  }}
+}}
+"""
+
+
+def _plan(client, program):
+    return client.compile(pjrt.Program.mlir(program)).describe_plan()
+
+
+# ------------------------------------------------------------------------------------------------ oracle
+def test_reference_examples():
+    # miscellaneous.rs:320-327
+    (r, _), = sh.evaluate(reverse_program((3, 2), [1]), [np.array([[1, 2], [3, 4], [5, 6]])])
+    assert r.tolist() == [[2, 1], [4, 3], [6, 5]]
+    # functional.rs:29-37 (documented for i64: the same values in i32)
+    (m, _), (s, _) = sh.evaluate(map_program((2, 2)), [np.array([[0, 1], [2, 3]]), np.array([[4, 5], [6, 7]])])
+    assert m.tolist() == [[0, 5], [12, 21]]
+    assert s.tolist() == [[4, 5], [6, 7]]  # max(a + 3, b)
+    # miscellaneous.rs:418-424: the identity
+    a, b = np.array([1.0]), np.array([2.0])
+    (p, _), (q, _) = sh.evaluate(barrier_program((1,)), [a, b])
+    assert p.tolist() == [2.0] and q.tolist() == [2.0]
+
+
+@pytest.mark.parametrize("shape,dims", [((4, 5, 6), [0, 2]), ((7,), [0]), ((3, 4), []), ((2, 3, 4, 5), [1, 2, 3])])
+def test_reverse_is_numpys_flip(shape, dims):
+    x = np.arange(np.prod(shape)).reshape(shape)
+    (r, _), = sh.evaluate(reverse_program(shape, dims), [x])
+    assert np.array_equal(r, np.flip(x, axis=tuple(dims)))
+
+
+@pytest.mark.parametrize("src,dst,npsrc,npdst", [("f32", "i32", np.float32, np.int32), ("i32", "f32", np.int32, np.float32),
+                                                 ("ui32", "i32", np.uint32, np.int32), ("i16", "ui16", np.int16, np.uint16),
+                                                 ("i8", "ui8", np.int8, np.uint8)])
+def test_bitcast_is_numpys_view(src, dst, npsrc, npdst):
+    rng = np.random.default_rng(3)
+    if npsrc == np.float32:
+        x = rng.standard_normal(64).astype(np.float32)
+    else:
+        info = np.iinfo(npsrc)
+        x = rng.integers(info.min, info.max, size=64, endpoint=True).astype(npsrc)
+        if npdst == np.float32:  # bit patterns of finite floats (NaN payloads are not carried by the oracle's values)
+            x = np.where(np.isfinite(x.view(np.float32)), x, 0).astype(npsrc)
+    (r, dt), = sh.evaluate(bitcast_program((64,), src, dst), [x.astype(np.float64 if npsrc == np.float32 else np.int64)])
+    want = x.view(npdst)
+    assert dt == dst and np.array_equal(np.asarray(r), want.astype(np.float64 if npdst == np.float32 else np.int64))
+
+
+def test_bitcast_of_narrow_floats_round_trips():
+    # bf16 / f16 / f8 bits through an integer of the same width and back
+    x = np.array([1.0, -2.5, 0.15625, 3.0e4, -0.0])
+    for ft, it in (("bf16", "i16"), ("f16", "ui16"), ("f8E4M3FN", "ui8")):
+        xs = sh.normalize(x, ft)
+        (bits, _), = sh.evaluate(bitcast_program((5,), ft, it), [xs])
+        (back, _), = sh.evaluate(bitcast_program((5,), it, ft), [bits])
+        assert np.array_equal(np.asarray(back), xs, equal_nan=True) and np.array_equal(np.signbit(back), np.signbit(xs))
+        raw = sh.to_raw(xs, ft)
+        assert np.array_equal(np.asarray(bits).astype(np.int64) & (0xFFFF if it.endswith("16") else 0xFF),
+                              raw.astype(np.int64))
+
+
+# ------------------------------------------------------------------------------------------------ front-ends
+def test_forms_plan_alike(compile_client):
+    for prog in (reverse_program((8, 64), [1], consumer=True), barrier_program((8, 64)),
+                 bitcast_program((8, 64), "f32", "i32")):
+        generic = prog.replace("stablehlo.reverse %arg0, dims = [1] : tensor<8x64xi32>",
+                               '"stablehlo.reverse"(%arg0) <{dimensions = array<i64: 1>}> : (tensor<8x64xi32>) -> '
+                               'tensor<8x64xi32>')
+        plans = [_plan(compile_client, p) for p in (prog, generic, mb.to_bytecode(prog))]
+        assert plans[0] == plans[1] == plans[2], plans
+    # a reverse feeding an add is one elementwise step reading backwards; the barrier adds no step of its own (its
+    # second result is the parameter itself, returned by a copy)
+    plan = _plan(compile_client, reverse_program((8, 64), [1], consumer=True)).strip().split("\n")
+    assert len(plan) == 1 and plan[0].startswith("0: elementwise") and "leaves=2" in plan[0], plan
+    plan = _plan(compile_client, barrier_program((8, 64))).strip().split("\n")
+    assert len(plan) == 2 and "elementwise" in plan[0] and "copy" in plan[1], plan
+    # each map's body inlined into one elementwise step over the inputs
+    plan = _plan(compile_client, map_program((8, 64))).strip().split("\n")
+    assert len(plan) == 2 and all("elementwise" in ln and "leaves=2" in ln for ln in plan), plan
+
+
+@pytest.mark.parametrize("prog,code", [
+    (reverse_program((4, 5), [1, 1]), "INVALID_ARGUMENT"),
+    (reverse_program((4, 5), [2]), "INVALID_ARGUMENT"),
+    (map_program((2, 2)).replace("array<i64: 0, 1>", "array<i64: 1, 0>", 1), "INVALID_ARGUMENT"),
+    (map_program((2, 2)).replace("^bb0(%arg2: tensor<i32>, %arg3: tensor<i32>):",
+                                 "^bb0(%arg2: tensor<i32>, %arg3: tensor<i32>, %arg9: tensor<i32>):"), "INVALID_ARGUMENT"),
+    (bitcast_program((4,), "f32", "i16"), "UNIMPLEMENTED"),
+    (bitcast_program((4,), "f64", "i64"), "UNIMPLEMENTED"),
+])
+def test_malformed(compile_client, prog, code):
+    with pytest.raises(pjrt.PjrtError) as e:
+        compile_client.compile(pjrt.Program.mlir(prog))
+    assert e.value.code == getattr(pjrt.ErrorCode, code), e.value.message
