@@ -798,11 +798,14 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_mfma_kernel(const GemmArgs 
   const int tiles_n = EDGE ? (G.N + BN - 1) / BN : G.N / BN, tiles_m = EDGE ? (G.M + BM - 1) / BM : G.M / BM;
   const int per_batch = tiles_n * tiles_m;
   const int total = per_batch * G.batch;
-  // split-K: the K range is the slow index of the grid, so the tile order below (and its XCD mapping) is the same
-  // within every range
-  const int split = G.splits > 1 ? (int)(blockIdx.x / total) : 0;
-  int bid = G.splits > 1 ? (int)(blockIdx.x % total) : (int)blockIdx.x;
-  if ((total & 7) == 0) bid = (bid & 7) * (total >> 3) + (bid >> 3);
+  // split-K: the K range is the slow index of the work order, so each XCD's run covers one K range (or a few) and
+  // the tiles of that range fetch only its slices of A and B (with the range inside the XCD's run every XCD would
+  // fetch the whole of A)
+  const int nsplit = G.splits > 1 ? G.splits : 1;
+  int work = (int)blockIdx.x;
+  if (((total * nsplit) & 7) == 0) work = (work & 7) * ((total * nsplit) >> 3) + (work >> 3);
+  const int split = nsplit > 1 ? work / total : 0;
+  const int bid = nsplit > 1 ? work % total : work;
   const int b = bid / per_batch, t = bid % per_batch;
   const int GM = tiles_m < 8 ? tiles_m : 8;
   const int first_m = (t / (GM * tiles_n)) * GM;
