@@ -262,6 +262,88 @@ def _gather(rest: str, env, out_shape) -> Tuple[np.ndarray, str]:
     return out, dt
 
 
+def _region_fn(rest: str, dot_precision: str):
+    """The one-block region of a generic op (`({ ^bb0(%a: T, %b: T): ... stablehlo.return %r : T })`) as a function
+    of its block arguments ((values, dtype) pairs; values may be whole arrays), evaluated with this module's ops."""
+    region = rest[rest.index("^bb"):rest.rindex("})")]
+    first, _, body = region.partition("\n")
+    args = re.findall(r"(%[\w.$-]+)\s*:", first[:first.index(")")])
+
+    def fn(*vals):
+        benv = dict(zip(args, vals))
+        for ln in body.split("\n"):
+            ln = ln.strip()
+            if not ln:
+                continue
+            rm = re.match(r'"?stablehlo\.return"?\s*\(?(.*?)\)?\s*:', ln)
+            if rm:
+                return benv[re.findall(r"%[\w.$-]+", rm.group(1))[0]]
+            m = re.match(r"(%[\w.$-]+)\s*=\s*(?:stablehlo|mhlo)\.(\w+)\s*(.*)$", ln)
+            if m:
+                benv[m.group(1)] = _eval_op(m.group(2), m.group(3), benv, dot_precision)
+            else:
+                m = re.match(r'(%[\w.$-]+)\s*=\s*"(?:stablehlo|mhlo)\.(\w+)"\((.*?)\)\s*(.*)$', ln)
+                benv[m.group(1)] = _eval_op(m.group(2), m.group(3) + " " + m.group(4), benv, dot_precision)
+        raise ValueError("region without a return")
+    return fn
+
+
+def _scatter(rest: str, env, dot_precision: str) -> Tuple[np.ndarray, str]:
+    """scatter (manipulation.rs:1614-1690), one input, as the StableHLO specification defines it: for each scatter
+    position (the updates' dims other than update_window_dims, in row-major order — the order XLA's CPU backend
+    applies them in, which is what fixes the result when windows overlap), start = the index vector placed on
+    scatter_dims_to_operand_dims plus the position's batching coordinates on input_batching_dims; the update window
+    (the update_window_dims, walking the operand's non-inserted, non-batching dims in order) is combined into the
+    result with the update computation (current value first). A window that does not lie inside the operand in every
+    dimension is skipped whole (XLA's choice; the specification leaves out-of-bounds updates implementation-defined)."""
+    head = rest.split("<{")[0]
+    names = re.findall(r"%[\w.$#-]+", head)
+    (x, dt), (ix, idt), (u, _) = env[names[0]], env[names[1]], env[names[2]]
+    x, ix, u = np.asarray(x), np.asarray(ix), np.asarray(u)
+    attrs = rest[rest.index("<{"):rest.index("}>")]
+    dn = re.search(r"#stablehlo\.scatter<(.*?)>", attrs, re.S).group(1)
+
+    def field(name):
+        m = re.search(name + r"\s*=\s*\[(.*?)\]", dn)
+        return _ints(m.group(1)) if m else []
+
+    uwd, inserted = field("update_window_dims"), field("inserted_window_dims")
+    in_batch, idx_batch = field("input_batching_dims"), field("scatter_indices_batching_dims")
+    to_operand = field("scatter_dims_to_operand_dims")
+    ivd = int(re.search(r"index_vector_dim\s*=\s*(\d+)", dn).group(1))
+    fn = _region_fn(rest, dot_precision)
+    if idt.startswith("ui"):
+        ix = ix.astype(object) % (1 << INT_BITS[idt])
+    out = x.copy()
+    scatter_dims = [d for d in range(u.ndim) if d not in uwd]
+    window_operand = [d for d in range(x.ndim) if d not in inserted and d not in in_batch]
+    win = [1] * x.ndim
+    for k, d in enumerate(uwd):
+        win[window_operand[k]] = u.shape[d]
+    for si in np.ndindex(*[u.shape[d] for d in scatter_dims]):
+        si = list(si)
+        if ivd < ix.ndim:
+            vec = [ix[tuple(si[:ivd] + [k] + si[ivd:])] for k in range(ix.shape[ivd])]
+        else:
+            vec = [ix[tuple(si)]]
+        start = [0] * x.ndim
+        for k, d in enumerate(to_operand):
+            start[d] += int(vec[k])
+        for d_op, d_idx in zip(in_batch, idx_batch):
+            start[d_op] += si[d_idx - (0 if d_idx < ivd else 1)]
+        if any(start[d] < 0 or start[d] + win[d] > x.shape[d] for d in range(x.ndim)):
+            continue
+        usl = [slice(None)] * u.ndim
+        for k, d in enumerate(scatter_dims):
+            usl[d] = si[k]
+        uw = u[tuple(usl)]  # the window, in update_window_dims order = the window operand dims' order
+        osl = tuple(slice(start[d], start[d] + win[d]) for d in range(x.ndim))
+        cur = out[osl].reshape(uw.shape)
+        new, _ = fn((cur, dt), (uw, dt))
+        out[osl] = np.broadcast_to(normalize(np.asarray(new), dt), uw.shape).reshape(out[osl].shape)
+    return out, dt
+
+
 def _eval_op(op: str, rest: str, env, dot_precision: str) -> Tuple[np.ndarray, str]:
     ty = rest[rest.rfind(":"):] if ":" in rest else ""
     if op == "constant":
@@ -375,27 +457,10 @@ def _eval_op(op: str, rest: str, env, dot_precision: str) -> Tuple[np.ndarray, s
     if op == "map":
         # functional.rs:13-104: the body applied to the inputs' elements (here to whole arrays at once)
         names = re.findall(r"%[\w.$-]+", rest[:rest.index("(")] if "(" in rest else rest)
-        region = rest[rest.index("^bb"):rest.rindex("})")]
-        first, _, body = region.partition("\n")
-        args = re.findall(r"(%[\w.$-]+)\s*:", first[:first.index(")")])
-        benv = dict(zip(args, [env[n] for n in names]))
-        rets = None
-        for ln in body.split("\n"):
-            ln = ln.strip()
-            if not ln:
-                continue
-            rm = re.match(r'"?stablehlo\.return"?\s*\(?(.*?)\)?\s*:', ln)
-            if rm:
-                rets = re.findall(r"%[\w.$-]+", rm.group(1))
-                break
-            m = re.match(r"(%[\w.$-]+)\s*=\s*(?:stablehlo|mhlo)\.(\w+)\s*(.*)$", ln)
-            if m:
-                benv[m.group(1)] = _eval_op(m.group(2), m.group(3), benv, dot_precision)
-            else:
-                m = re.match(r'(%[\w.$-]+)\s*=\s*"(?:stablehlo|mhlo)\.(\w+)"\((.*?)\)\s*(.*)$', ln)
-                benv[m.group(1)] = _eval_op(m.group(2), m.group(3) + " " + m.group(4), benv, dot_precision)
-        v, dt = benv[rets[0]]
+        v, dt = _region_fn(rest, dot_precision)(*[env[n] for n in names])
         return normalize(np.broadcast_to(np.asarray(v), out_shape), out_dt), out_dt
+    if op == "scatter":
+        return _scatter(rest, env, dot_precision)
     if op == "concatenate":
         # manipulation.rs:778-822: the inputs one after another along `dim`, in operand order
         head = rest.split(":")[0]

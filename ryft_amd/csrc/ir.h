@@ -46,7 +46,7 @@ enum class Op : uint8_t {
   Select, Clamp,
   // data movement
   BroadcastInDim, Transpose, Reshape, Iota, Slice, Concatenate, Pad, DynamicSlice, DynamicUpdateSlice, Gather,
-  Reverse,
+  Reverse, Scatter,
   // contractions and reductions
   DotGeneral, Reduce,
 };
@@ -57,6 +57,10 @@ enum class CmpDir : uint8_t { EQ, NE, GE, GT, LE, LT };
 enum class CmpType : uint8_t { NOTYPE, FLOAT, TOTALORDER, SIGNED, UNSIGNED };
 // A reduce body that is one binary op of its two block arguments, or General: any other body (kept as a graph).
 enum class ReduceBody : uint8_t { Add, Max, Min, Mul, And, Or, General };
+
+// How scatter combines an update with the value it lands on: the update replaces it (a body returning its second
+// argument), or one of the binary ops applied to (current, update).
+enum class ScatterCombine : uint8_t { Set, Add, Mul, Min, Max, And, Or };
 
 struct DotDims {
   std::vector<int64_t> lhs_batch, rhs_batch, lhs_contract, rhs_contract;
@@ -84,7 +88,11 @@ struct Node {
   CmpDir cmp = CmpDir::EQ;
   CmpType cmp_type = CmpType::NOTYPE;
   DotDims dot;
-  GatherDims gather;
+  GatherDims gather;  // gather's dimension numbers; scatter's in the same roles (update_window_dims → offset_dims,
+                      // inserted_window_dims → collapsed_slice_dims, input / scatter_indices batching dims → operand /
+                      // start_indices batching dims, scatter_dims_to_operand_dims → start_index_map)
+  ScatterCombine scatter_combine = ScatterCombine::Set;
+  bool unique_indices = false;  // scatter: the caller promises that no two update windows overlap
   DType dot_lhs_precision = DType::INVALID;  // algorithm lhs/rhs_precision_type, if given
   DType dot_rhs_precision = DType::INVALID;
   ReduceBody reduce_body = ReduceBody::Add;

@@ -296,4 +296,29 @@ struct GatherArgs {
   int64_t total;       // result elements
 };
 
+// ------------------------------------------------------------------------------------------------ scatter
+enum ScatterKind : int32_t { SC_SET = 0, SC_ADD = 1, SC_MUL = 2, SC_MIN = 3, SC_MAX = 4, SC_AND = 5, SC_OR = 6 };
+
+// scatter: `out` holds the input's values when the step starts; each update window whose start lies inside the
+// operand (every mapped dimension: 0 ≤ start and start + window ≤ extent) is combined into it, the others skipped.
+// Update dims are window dims (upd_to_op: the operand dim each walks) or scatter dims (upd_to_idx: the indices dim
+// each walks); op_batch / map as in GatherArgs. serial = 1: one workgroup applies the windows one after another in
+// row-major order of the scatter dims (the sequential semantics, for windows that may overlap); 0: every update
+// element at once (windows promised disjoint).
+struct ScatterArgs {
+  void* out;
+  const void* indices;
+  const void* updates;
+  int32_t dtype;       // DType of the result and the updates
+  int32_t idx_dtype;   // DType of the scatter indices
+  int32_t elem_bytes;  // 1, 2, 4 or 8
+  int32_t kind;        // ScatterKind
+  int32_t upd_rank, op_rank, idx_rank, ivd, n_map, serial;
+  int64_t upd_shape[WIN_MAX_RANK], op_shape[WIN_MAX_RANK], idx_shape[WIN_MAX_RANK], win[WIN_MAX_RANK];
+  int32_t upd_to_op[WIN_MAX_RANK], upd_to_idx[WIN_MAX_RANK], op_batch[WIN_MAX_RANK], map[WIN_MAX_RANK];
+  int64_t total;       // update elements
+  int64_t n_windows;   // scatter positions: the product of the scatter dims' extents
+  int64_t win_elems;   // elements per update window
+};
+
 }  // namespace ryft

@@ -167,6 +167,168 @@ void launch_es(const WindowArgs& a, bool vec, hipStream_t stream, hipEvent_t don
   else launch_k(done, window_kernel<ES, false>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
 }
 
+
+// ------------------------------------------------------------------------------------------------ scatter
+// scatter (manipulation.rs:1614-1690): update element u lands on result index full_start + full_batching +
+// full_window, where full_start places the index vector of u's scatter coordinates on the operand dims named by
+// scatter_dims_to_operand_dims, full_batching the scatter coordinate of each input batching dim's indices batching dim,
+// and full_window u's window coordinates on the operand dims that are neither inserted nor batching. A window whose
+// start lies outside the operand (some mapped dim with start < 0 or start + window > extent) is skipped whole, as
+// XLA does. Combining runs on 32-bit register values (floats as f32, rounded back to the element type; integers
+// wrapped), the same arithmetic as the elementwise kernels; 64-bit elements are only replaced.
+
+// The value `cur` combined with `upd` (register forms of element type dt).
+__device__ __forceinline__ uint32_t scatter_combine(uint32_t cur, uint32_t upd, int kind, int dt) {
+  if (kind == SC_SET) return upd;
+  if (dt_is_float(dt)) {
+    const float a = __uint_as_float(cur), b = __uint_as_float(upd);
+    float r;
+    switch (kind) {
+      case SC_ADD: r = a + b; break;
+      case SC_MUL: r = a * b; break;
+      case SC_MIN: r = (a != a || b != b) ? __uint_as_float(0x7fc00000u) : fminf(a, b); break;
+      default: r = (a != a || b != b) ? __uint_as_float(0x7fc00000u) : fmaxf(a, b); break;
+    }
+    return __float_as_uint(r);
+  }
+  const bool uns = dt == DT_U8 || dt == DT_U16 || dt == DT_U32 || dt == DT_PRED;
+  const int32_t a = (int32_t)cur, b = (int32_t)upd;
+  int32_t r;
+  switch (kind) {
+    case SC_ADD: r = dt == DT_PRED ? (a | b) : (int32_t)((uint32_t)a + (uint32_t)b); break;
+    case SC_MUL: r = dt == DT_PRED ? (a & b) : (int32_t)((uint32_t)a * (uint32_t)b); break;
+    case SC_MIN: r = uns ? (int32_t)min((uint32_t)a, (uint32_t)b) : min(a, b); break;
+    case SC_MAX: r = uns ? (int32_t)max((uint32_t)a, (uint32_t)b) : max(a, b); break;
+    case SC_AND: r = a & b; break;
+    default: r = a | b; break;
+  }
+  return (uint32_t)r;
+}
+
+// One update element combined into the result element at `o` (u: its offset in the updates).
+template <int ES>
+__device__ __forceinline__ void scatter_apply(const ScatterArgs& A, int64_t o, int64_t u) {
+  if constexpr (ES == 8) {  // replaced only (the planner admits no other combination of 64-bit elements)
+    ((uint64_t*)A.out)[o] = ((const uint64_t*)A.updates)[u];
+  } else {
+    if (A.kind == SC_SET) {
+      if constexpr (ES == 1) ((uint8_t*)A.out)[o] = ((const uint8_t*)A.updates)[u];
+      else if constexpr (ES == 2) ((uint16_t*)A.out)[o] = ((const uint16_t*)A.updates)[u];
+      else ((uint32_t*)A.out)[o] = ((const uint32_t*)A.updates)[u];
+      return;
+    }
+    const uint32_t r = scatter_combine(load_bits(A.out, o, A.dtype), load_bits(A.updates, u, A.dtype), A.kind, A.dtype);
+    store_bits(A.out, o, A.dtype, r, dt_is_float(A.dtype));
+  }
+}
+
+// Row-major strides of the operand and the updates, and the operand offset of the window of scatter position
+// `icoord` (its coordinates along the indices' dims; the index vector dim's is 0). False when the window starts outside
+// the operand.
+__device__ __forceinline__ bool scatter_window(const ScatterArgs& A, const int64_t (&icoord)[WIN_MAX_RANK],
+                                               const int64_t (&ostride)[WIN_MAX_RANK], int64_t* op_off) {
+  int64_t istride[WIN_MAX_RANK];
+  int64_t s = 1;
+  for (int d = A.idx_rank - 1; d >= 0; --d) {
+    istride[d] = s;
+    s *= A.idx_shape[d];
+  }
+  int64_t ioff = 0;
+  for (int d = 0; d < A.idx_rank; ++d) ioff += icoord[d] * istride[d];
+  const int64_t ivstep = A.ivd < A.idx_rank ? istride[A.ivd] : 0;
+  int64_t off = 0;
+  bool ok = true;
+  for (int k = 0; k < A.n_map; ++k) {
+    const char* p = (const char*)A.indices + (ioff + k * ivstep) * (int64_t)elem_size_of(A.idx_dtype);
+    const int64_t v = start_index(p, A.idx_dtype);
+    const int d = A.map[k];
+    ok = ok && v >= 0 && v <= A.op_shape[d] - A.win[d];
+    off += v * ostride[d];
+  }
+  for (int d = 0; d < A.op_rank; ++d)
+    if (A.op_batch[d] >= 0) off += icoord[A.op_batch[d]] * ostride[d];
+  *op_off = off;
+  return ok;
+}
+
+__device__ __forceinline__ void scatter_strides(const ScatterArgs& A, int64_t (&ostride)[WIN_MAX_RANK],
+                                                int64_t (&ustride)[WIN_MAX_RANK]) {
+  int64_t s = 1;
+  for (int d = A.op_rank - 1; d >= 0; --d) {
+    ostride[d] = s;
+    s *= A.op_shape[d];
+  }
+  s = 1;
+  for (int d = A.upd_rank - 1; d >= 0; --d) {
+    ustride[d] = s;
+    s *= A.upd_shape[d];
+  }
+}
+
+// serial: one workgroup, the windows in row-major order of the update's scatter dims, a barrier after each (the
+// elements of one window land on distinct result elements, so its threads never collide).
+template <int ES>
+__global__ void __launch_bounds__(1024) scatter_serial_kernel(const ScatterArgs A) {
+  int64_t ostride[WIN_MAX_RANK], ustride[WIN_MAX_RANK];
+  scatter_strides(A, ostride, ustride);
+  for (int64_t w = 0; w < A.n_windows; ++w) {
+    int64_t icoord[WIN_MAX_RANK] = {0, 0, 0, 0, 0, 0};
+    int64_t ubase = 0, rem = w;
+    for (int r = A.upd_rank - 1; r >= 0; --r)
+      if (A.upd_to_idx[r] >= 0) {
+        const int64_t c = rem % A.upd_shape[r];
+        rem /= A.upd_shape[r];
+        icoord[A.upd_to_idx[r]] = c;
+        ubase += c * ustride[r];
+      }
+    int64_t obase;
+    if (scatter_window(A, icoord, ostride, &obase)) {
+      for (int64_t e = threadIdx.x; e < A.win_elems; e += blockDim.x) {
+        int64_t o = obase, u = ubase, q = e;
+        for (int r = A.upd_rank - 1; r >= 0; --r)
+          if (A.upd_to_op[r] >= 0) {
+            const int64_t c = q % A.upd_shape[r];
+            q /= A.upd_shape[r];
+            o += c * ostride[A.upd_to_op[r]];
+            u += c * ustride[r];
+          }
+        scatter_apply<ES>(A, o, u);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// parallel: every update element at once (the windows are disjoint).
+template <int ES>
+__global__ void __launch_bounds__(256) scatter_parallel_kernel(const ScatterArgs A) {
+  int64_t ostride[WIN_MAX_RANK], ustride[WIN_MAX_RANK];
+  scatter_strides(A, ostride, ustride);
+  for (int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; u < A.total; u += (int64_t)gridDim.x * blockDim.x) {
+    int64_t icoord[WIN_MAX_RANK] = {0, 0, 0, 0, 0, 0};
+    int64_t wo = 0, rem = u;
+    for (int r = A.upd_rank - 1; r >= 0; --r) {
+      const int64_t c = rem % A.upd_shape[r];
+      rem /= A.upd_shape[r];
+      if (A.upd_to_idx[r] >= 0) icoord[A.upd_to_idx[r]] = c;
+      else wo += c * ostride[A.upd_to_op[r]];
+    }
+    int64_t obase;
+    if (scatter_window(A, icoord, ostride, &obase)) scatter_apply<ES>(A, obase + wo, u);
+  }
+}
+
+template <int ES>
+void launch_scatter_es(const ScatterArgs& a, hipStream_t stream, hipEvent_t done) {
+  if (a.serial) {
+    const int threads = a.win_elems >= 1024 ? 1024 : (a.win_elems >= 256 ? 256 : 64);
+    launch_k(done, scatter_serial_kernel<ES>, dim3(1), dim3(threads), 0, stream, a);
+  } else {
+    const int64_t blocks = std::min<int64_t>((a.total + 255) / 256, 256 * 16);
+    launch_k(done, scatter_parallel_kernel<ES>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+  }
+}
+
 }  // namespace
 
 void launch_window(const WindowArgs& a, hipStream_t stream, hipEvent_t done) {
@@ -241,6 +403,53 @@ void launch_gather(const GatherArgs& a, hipStream_t stream, hipEvent_t done) {
     case 4: return launch_gather_es<4>(a, vec, stream, done);
     case 8: return launch_gather_es<8>(a, vec, stream, done);
     default: fail(PJRT_Error_Code_INTERNAL, "gather element size " + std::to_string(es));
+  }
+}
+
+void launch_scatter(const ScatterArgs& a, hipStream_t stream, hipEvent_t done) {
+  // the shapes the kernels' index arithmetic relies on, checked before the launch: each update dim walks either an
+  // operand dim (inside that dim's window) or an indices dim (of the same extent), each operand batching dim has a
+  // same-sized indices batching dim, and the index vectors have one component per mapped operand dim
+  auto rank_ok = [](int r) { return r >= 0 && r <= WIN_MAX_RANK; };
+  if (!rank_ok(a.upd_rank) || !rank_ok(a.op_rank) || !rank_ok(a.idx_rank) || a.n_map < 0 || a.n_map > a.op_rank ||
+      a.ivd < 0 || a.ivd > a.idx_rank)
+    fail(PJRT_Error_Code_INTERNAL, "scatter ranks out of range");
+  if (a.idx_dtype < DT_S8 || a.idx_dtype > DT_U64) fail(PJRT_Error_Code_INTERNAL, "scatter indices must be integers");
+  if (a.kind < SC_SET || a.kind > SC_OR || (a.elem_bytes == 8 && a.kind != SC_SET))
+    fail(PJRT_Error_Code_INTERNAL, "scatter combination");
+  int64_t total = 1, windows = 1, welems = 1;
+  int walks[WIN_MAX_RANK] = {0, 0, 0, 0, 0, 0};
+  for (int r = 0; r < a.upd_rank; ++r) {
+    total *= a.upd_shape[r];
+    const int d = a.upd_to_op[r], i = a.upd_to_idx[r];
+    if ((d >= 0) == (i >= 0)) fail(PJRT_Error_Code_INTERNAL, "scatter update dimension must be a window or a scatter dim");
+    if (d >= a.op_rank || (d >= 0 && (++walks[d] > 1 || a.upd_shape[r] != a.win[d])))
+      fail(PJRT_Error_Code_INTERNAL, "scatter window dim");
+    if (i >= a.idx_rank || i == a.ivd || (i >= 0 && a.upd_shape[r] != a.idx_shape[i]))
+      fail(PJRT_Error_Code_INTERNAL, "scatter scatter dim");
+    if (d >= 0) welems *= a.upd_shape[r];
+    else windows *= a.upd_shape[r];
+  }
+  if (total != a.total || windows != a.n_windows || welems != a.win_elems)
+    fail(PJRT_Error_Code_INTERNAL, "scatter element counts");
+  for (int d = 0; d < a.op_rank; ++d) {
+    if (a.win[d] < 0 || a.win[d] > a.op_shape[d] || (!walks[d] && a.win[d] != 1))
+      fail(PJRT_Error_Code_INTERNAL, "scatter window size");
+    const int b = a.op_batch[d];
+    if (b >= a.idx_rank || b == a.ivd || (b >= 0 && (a.idx_shape[b] != a.op_shape[d] || walks[d])))
+      fail(PJRT_Error_Code_INTERNAL, "scatter batching dim");
+  }
+  for (int k = 0; k < a.n_map; ++k)
+    if (a.map[k] < 0 || a.map[k] >= a.op_rank || a.op_batch[a.map[k]] >= 0)
+      fail(PJRT_Error_Code_INTERNAL, "scatter_dims_to_operand_dims");
+  if ((a.ivd < a.idx_rank ? a.idx_shape[a.ivd] : 1) != a.n_map) fail(PJRT_Error_Code_INTERNAL, "scatter index vectors");
+  if (total == 0) return record_done(done, stream);
+  switch (a.elem_bytes) {
+    case 1: return launch_scatter_es<1>(a, stream, done);
+    case 2: return launch_scatter_es<2>(a, stream, done);
+    case 4: return launch_scatter_es<4>(a, stream, done);
+    case 8: return launch_scatter_es<8>(a, stream, done);
+    default: fail(PJRT_Error_Code_INTERNAL, "scatter element size " + std::to_string(a.elem_bytes));
   }
 }
 

@@ -21,6 +21,7 @@ void launch_gemm(const GemmArgs& a, hipStream_t stream, hipEvent_t done = nullpt
 void launch_attention(const AttnArgs& a, hipStream_t stream, hipEvent_t done = nullptr);
 void launch_window(const WindowArgs& a, hipStream_t stream, hipEvent_t done = nullptr);
 void launch_gather(const GatherArgs& a, hipStream_t stream, hipEvent_t done = nullptr);
+void launch_scatter(const ScatterArgs& a, hipStream_t stream, hipEvent_t done = nullptr);
 
 // Operands of these GEMM arguments (bit 0: A, 1: B, 2: B2) whose layout keeps them from the MFMA kernels (0: the
 // MFMA kernels run them as they are; -1: their element types or epilogue have no MFMA kernel whatever the layout).

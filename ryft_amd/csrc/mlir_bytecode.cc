@@ -118,7 +118,7 @@ struct BType {
 struct BAttr {
   enum Kind {
     STRING, INT, FLOAT, ARRAY, DICT, DENSE_ARRAY, DENSE_ELEMENTS, TYPE, UNIT, SYMREF, LOCATION,
-    CMP_DIR, CMP_TYPE, DOT_DIMS, GATHER_DIMS, PRECISION, DOT_ALGORITHM, TEXT, OTHER
+    CMP_DIR, CMP_TYPE, DOT_DIMS, GATHER_DIMS, SCATTER_DIMS, PRECISION, DOT_ALGORITHM, TEXT, OTHER
   } kind = OTHER;
   std::string str;                                // STRING, SYMREF, TEXT
   int64_t i = 0;                                  // INT, CMP_DIR, CMP_TYPE, PRECISION
@@ -129,7 +129,7 @@ struct BAttr {
   std::vector<int64_t> ints;                      // DENSE_ARRAY (integer element types)
   std::vector<uint8_t> raw;                       // DENSE_ELEMENTS: MLIR's raw element storage
   DotDims dot;                                    // DOT_DIMS
-  GatherDims gather;                              // GATHER_DIMS
+  GatherDims gather;                              // GATHER_DIMS, SCATTER_DIMS (in gather's roles)
   int lhs_precision = -1, rhs_precision = -1;     // DOT_ALGORITHM: type indices
 };
 
@@ -568,6 +568,15 @@ class BytecodeParser {
           a.gather.index_vector_dim = r.svarint();
           break;
         case 8: a.kind = BAttr::PRECISION; a.i = (int64_t)r.varint(); break;  // PrecisionAttr
+        case 11:                                                                // ScatterDimensionNumbersAttr
+          a.kind = BAttr::SCATTER_DIMS;
+          a.gather.offset_dims = svarints(r);                  // update_window_dims
+          a.gather.collapsed_slice_dims = svarints(r);         // inserted_window_dims
+          a.gather.operand_batching_dims = svarints(r);        // input_batching_dims
+          a.gather.start_indices_batching_dims = svarints(r);  // scatter_indices_batching_dims
+          a.gather.start_index_map = svarints(r);              // scatter_dims_to_operand_dims
+          a.gather.index_vector_dim = r.svarint();
+          break;
         case 15:                                                                // DotAlgorithmAttr
           a.kind = BAttr::DOT_ALGORITHM;
           a.lhs_precision = (int)r.varint();
@@ -614,6 +623,10 @@ class BytecodeParser {
          {{"dimension_numbers", true, {BAttr::GATHER_DIMS}},
           {"indices_are_sorted", false, {BAttr::INT}},
           {"slice_sizes", true, {BAttr::DENSE_ARRAY}}}},
+        {"stablehlo.scatter",
+         {{"indices_are_sorted", false, {BAttr::INT}},
+          {"scatter_dimension_numbers", true, {BAttr::SCATTER_DIMS}},
+          {"unique_indices", false, {BAttr::INT}}}},
         {"stablehlo.pad", {{"edge_padding_high", true, {BAttr::DENSE_ARRAY}}, {"edge_padding_low", true, {BAttr::DENSE_ARRAY}},
                            {"interior_padding", true, {BAttr::DENSE_ARRAY}}}},
         {"stablehlo.compare",
@@ -638,6 +651,7 @@ class BytecodeParser {
     if (op == "stablehlo.compare") return pick({"comparison_direction", "compare_type"});
     if (op == "stablehlo.dot_general") return pick({"dot_dimension_numbers", "precision_config", "algorithm"});
     if (op == "stablehlo.gather") return pick({"dimension_numbers", "slice_sizes", "indices_are_sorted"});
+    if (op == "stablehlo.scatter") return pick({"scatter_dimension_numbers", "indices_are_sorted", "unique_indices"});
     // (slice and pad: three fields of one kind, so another order could not be told apart; sorted only)
     return sorted;
   }
@@ -1033,6 +1047,16 @@ class BytecodeParser {
           n.dims = int_list(op, "dimensions");
         } else if (nm == "dynamic_update_slice") {
           n.op = Op::DynamicUpdateSlice;
+        } else if (nm == "scatter") {
+          // scatter (manipulation.rs:1614-1690): one input, its update computation as a region
+          n.op = Op::Scatter;
+          if (n.operands.size() != 3) unimplemented("scatter of several inputs is not supported");
+          if (op.regions.size() != 1) invalid("scatter: expected one update computation region");
+          const BAttr& d = need(op, "scatter_dimension_numbers");
+          n.gather = d.kind == BAttr::SCATTER_DIMS ? d.gather : mlir_scatter_dims_text(d.str);
+          if (const BAttr* u = get(op, "unique_indices")) n.unique_indices = u->kind == BAttr::INT ? u->i != 0 : u->str == "true";
+          const std::shared_ptr<Graph> body = build_region(op.regions[0]);
+          mlir_scatter_body(n, body.get(), g.nodes[n.operands[0]].type.dtype);
         } else if (nm == "gather") {
           n.op = Op::Gather;
           const BAttr& d = need(op, "dimension_numbers");

@@ -17,6 +17,9 @@ void mlir_dense_text(const std::string& text, const TensorType& tt, Node& n);  /
 CmpDir mlir_cmp_dir_text(const std::string& raw);                   // text containing EQ / NE / GE / GT / LE / LT
 CmpType mlir_cmp_type_text(const std::string& raw);                 // text containing FLOAT / SIGNED / ...
 GatherDims mlir_gather_dims_text(const std::string& raw);           // "#stablehlo.gather<offset_dims = [..], ...>"
+GatherDims mlir_scatter_dims_text(const std::string& raw);          // "#stablehlo.scatter<update_window_dims = [..], ...>"
+// scatter: the combination its update computation `body` performs on elements of type `dt` (into n.scatter_combine)
+void mlir_scatter_body(Node& n, const Graph* body, DType dt);
 void validate_node(const Graph& g, Node& n);                        // operand counts, shapes, dimension ranges
 void check_tensor_shape(const std::vector<int64_t>& shape);         // dims and element count within plan limits
 inline int64_t first_int(const std::vector<int64_t>& v, const char* what) {  // a one-integer attribute's value

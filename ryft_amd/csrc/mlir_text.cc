@@ -112,6 +112,7 @@ const char* op_name(Op op) {
     case Op::Gather: return "gather";
     case Op::Iota: return "iota";
     case Op::Reverse: return "reverse";
+    case Op::Scatter: return "scatter";
     case Op::BitcastConvert: return "bitcast_convert";
     case Op::DotGeneral: return "dot_general";
     case Op::Reduce: return "reduce";
@@ -976,6 +977,13 @@ class Parser {
       n.op = Op::Gather;
       n.gather = mlir_gather_dims_text(get("dimension_numbers"));
       n.dims = parse_int_list_text(get("slice_sizes"));
+    } else if (nm == "scatter") {
+      n.op = Op::Scatter;
+      if (n.operands.size() != 3 || os.results.size() != 1)
+        unimplemented("scatter of several inputs is not supported");
+      n.gather = mlir_scatter_dims_text(get("scatter_dimension_numbers"));
+      n.unique_indices = get("unique_indices") == "true";
+      mlir_scatter_body(n, os.body.get(), graph_.nodes[n.operands[0]].type.dtype);
     } else if (nm == "concatenate") {
       n.op = Op::Concatenate;
       std::string d = get("dim");
@@ -1086,15 +1094,18 @@ TensorType mlir_type_text(const std::string& text) {
 std::vector<int64_t> mlir_int_list_text(const std::string& raw) { return parse_int_list_text(raw); }
 
 // "#stablehlo.gather<offset_dims = [2, 3], collapsed_slice_dims = [0], start_index_map = [1, 0],
-// index_vector_dim = 2>" (manipulation.rs:2622-2636): each field `name = [list]` or `name = int`; absent lists are
-// empty, index_vector_dim is required.
-GatherDims mlir_gather_dims_text(const std::string& raw) {
+// index_vector_dim = 2>" (manipulation.rs:2622-2636) and "#stablehlo.scatter<update_window_dims = [..], ...>": each
+// field `name = [list]` or `name = int`; absent lists are empty, index_vector_dim is required. `names` are the five
+// list fields in GatherDims order (offset, collapsed, operand batching, indices batching, index map).
+static GatherDims parse_dim_numbers(const std::string& raw, const char* tag, const char* const (&names)[5]) {
+  const std::string what = std::string(tag) + " dimension numbers";
   const size_t open = raw.find('<'), close = raw.rfind('>');
-  if (raw.find("gather") == std::string::npos || open == std::string::npos || close == std::string::npos ||
-      close < open)
-    invalid("gather dimension numbers: expected #stablehlo.gather<...>, got '" + raw.substr(0, 80) + "'");
+  if (raw.find(tag) == std::string::npos || open == std::string::npos || close == std::string::npos || close < open)
+    invalid(what + ": expected #stablehlo." + tag + "<...>, got '" + raw.substr(0, 80) + "'");
   const std::string body = raw.substr(open + 1, close - open - 1);
   GatherDims g;
+  std::vector<int64_t>* lists[5] = {&g.offset_dims, &g.collapsed_slice_dims, &g.operand_batching_dims,
+                                    &g.start_indices_batching_dims, &g.start_index_map};
   bool have_ivd = false;
   size_t i = 0;
   while (i < body.size()) {
@@ -1104,33 +1115,84 @@ GatherDims mlir_gather_dims_text(const std::string& raw) {
     while (e < body.size() && (isalnum((unsigned char)body[e]) || body[e] == '_')) ++e;
     const std::string name = body.substr(i, e - i);
     while (e < body.size() && isspace((unsigned char)body[e])) ++e;
-    if (name.empty() || e >= body.size() || body[e] != '=') invalid("gather dimension numbers: malformed field");
+    if (name.empty() || e >= body.size() || body[e] != '=') invalid(what + ": malformed field");
     ++e;
     while (e < body.size() && isspace((unsigned char)body[e])) ++e;
     if (name == "index_vector_dim") {
       char* end = nullptr;
       const long long v = std::strtoll(body.c_str() + e, &end, 10);
-      if (end == body.c_str() + e) invalid("gather dimension numbers: index_vector_dim is not an integer");
+      if (end == body.c_str() + e) invalid(what + ": index_vector_dim is not an integer");
       g.index_vector_dim = v;
       have_ivd = true;
       i = end - body.c_str();
       continue;
     }
-    if (e >= body.size() || body[e] != '[') invalid("gather dimension numbers: field `" + name + "` is not a list");
+    if (e >= body.size() || body[e] != '[') invalid(what + ": field `" + name + "` is not a list");
     const size_t rb = body.find(']', e);
-    if (rb == std::string::npos) invalid("gather dimension numbers: unterminated list");
+    if (rb == std::string::npos) invalid(what + ": unterminated list");
     std::vector<int64_t> v = parse_int_list_text(body.substr(e, rb - e + 1));
-    if (name == "offset_dims") g.offset_dims = v;
-    else if (name == "collapsed_slice_dims") g.collapsed_slice_dims = v;
-    else if (name == "operand_batching_dims") g.operand_batching_dims = v;
-    else if (name == "start_indices_batching_dims") g.start_indices_batching_dims = v;
-    else if (name == "start_index_map") g.start_index_map = v;
-    else invalid("gather dimension numbers: unknown field `" + name + "`");
+    int k = 0;
+    while (k < 5 && name != names[k]) ++k;
+    if (k == 5) invalid(what + ": unknown field `" + name + "`");
+    *lists[k] = v;
     i = rb + 1;
   }
-  if (!have_ivd) invalid("gather dimension numbers: index_vector_dim is missing");
+  if (!have_ivd) invalid(what + ": index_vector_dim is missing");
   return g;
 }
+
+GatherDims mlir_gather_dims_text(const std::string& raw) {
+  static const char* const names[5] = {"offset_dims", "collapsed_slice_dims", "operand_batching_dims",
+                                        "start_indices_batching_dims", "start_index_map"};
+  return parse_dim_numbers(raw, "gather", names);
+}
+
+// "#stablehlo.scatter<update_window_dims = [..], inserted_window_dims = [..], input_batching_dims = [..],
+// scatter_indices_batching_dims = [..], scatter_dims_to_operand_dims = [..], index_vector_dim = N>"
+// (manipulation.rs:1526-1600), held in GatherDims's fields of the same roles.
+GatherDims mlir_scatter_dims_text(const std::string& raw) {
+  static const char* const names[5] = {"update_window_dims", "inserted_window_dims", "input_batching_dims",
+                                        "scatter_indices_batching_dims", "scatter_dims_to_operand_dims"};
+  return parse_dim_numbers(raw, "scatter", names);
+}
+
+// scatter's update computation (manipulation.rs:1614-1690): a body returning its second argument replaces the
+// value, one recognised binary op of its two arguments combines them (current value first; the ops here are
+// commutative, so either order); other bodies are not supported.
+void mlir_scatter_body(Node& n, const Graph* body, DType dt) {
+  if (!body) invalid("scatter without an update computation");
+  const Graph& b = *body;
+  if (b.params.size() != 2 || b.results.size() != 1)
+    unimplemented("scatter with several inputs (or a body of another arity) is not supported");
+  for (int p : b.params)
+    if (b.nodes[p].type.rank() != 0 || b.nodes[p].type.dtype != dt)
+      invalid("scatter: the update computation takes two scalars of the input's element type");
+  const int res = b.results[0];
+  if (b.nodes[res].type.rank() != 0 || b.nodes[res].type.dtype != dt)
+    invalid("scatter: the update computation returns a scalar of the input's element type");
+  const int p0 = b.params[0], p1 = b.params[1];
+  if (res == p1) {
+    n.scatter_combine = ScatterCombine::Set;
+    return;
+  }
+  const Node& op = b.nodes[res];
+  if (b.nodes.size() == 3 && op.operands.size() == 2 &&
+      ((op.operands[0] == p0 && op.operands[1] == p1) || (op.operands[0] == p1 && op.operands[1] == p0))) {
+    const bool fl = dtype_is_float(dt);
+    switch (op.op) {
+      case Op::Add: n.scatter_combine = ScatterCombine::Add; return;
+      case Op::Multiply: n.scatter_combine = ScatterCombine::Mul; return;
+      case Op::Minimum: n.scatter_combine = ScatterCombine::Min; return;
+      case Op::Maximum: n.scatter_combine = ScatterCombine::Max; return;
+      case Op::And: if (!fl) { n.scatter_combine = ScatterCombine::And; return; } break;
+      case Op::Or: if (!fl) { n.scatter_combine = ScatterCombine::Or; return; } break;
+      default: break;
+    }
+  }
+  unimplemented("scatter update computations other than replace / add / multiply / minimum / maximum / and / or "
+                "are not supported");
+}
+
 void mlir_dense_text(const std::string& text, const TensorType& tt, Node& n) {
   size_t d = text.find("dense<");
   if (d == std::string::npos) unimplemented("constant value '" + text + "' is not a dense literal");
@@ -1329,6 +1391,64 @@ void validate_node(const Graph& g, Node& n) {
       if (upd && opt(1).dtype != x.dtype) invalid("dynamic_update_slice: update element type mismatch");
       if (n.type.dtype != x.dtype || n.type.shape != (upd ? x.shape : win))
         invalid(std::string(op_name(n.op)) + ": result type mismatch");
+      break;
+    }
+    case Op::Scatter: {
+      // the StableHLO scatter constraints (manipulation.rs:1614-1690), one input: integer indices, index vector
+      // dimension within their rank (equal to it: an implicit trailing 1), scatter_dims_to_operand_dims as long as the
+      // index vectors, the dimension lists in range and without repeats, update_window_dims and inserted_window_dims
+      // sorted, the operand's dims split into window, inserted and batching ones, the updates made of the scatter
+      // dimensions (the indices' other dims, in order) and the window dimensions (at most the operand's extents)
+      need(3);
+      const TensorType& x = opt(0);
+      const TensorType& ix = opt(1);
+      const TensorType& u = opt(2);
+      const GatherDims& sd = n.gather;
+      const int r = x.rank(), ri = ix.rank(), ru = u.rank();
+      if (!dtype_is_int(ix.dtype) || ix.dtype == DType::PRED) invalid("scatter: indices must be integers");
+      if (sd.index_vector_dim < 0 || sd.index_vector_dim > ri) invalid("scatter: index_vector_dim out of range");
+      const int64_t nvec = sd.index_vector_dim < ri ? ix.shape[sd.index_vector_dim] : 1;
+      if ((int64_t)sd.start_index_map.size() != nvec)
+        invalid("scatter: scatter_dims_to_operand_dims must match the index vectors");
+      dims_in_range({&sd.collapsed_slice_dims, &sd.operand_batching_dims}, r, "scatter");
+      dims_in_range({&sd.start_index_map}, r, "scatter");
+      dims_in_range({&sd.offset_dims}, ru, "scatter");
+      if (sd.start_indices_batching_dims.size() != sd.operand_batching_dims.size())
+        invalid("scatter: batching dimension lists differ in length");
+      {
+        std::vector<int64_t> sb = sd.start_indices_batching_dims;
+        dims_in_range({&sb}, ri, "scatter");
+        for (int64_t d : sb)
+          if (d == sd.index_vector_dim) invalid("scatter: a batching dimension is the index vector dimension");
+      }
+      auto has = [](const std::vector<int64_t>& v, int64_t d) { return std::find(v.begin(), v.end(), d) != v.end(); };
+      for (int64_t d : sd.start_index_map)
+        if (has(sd.operand_batching_dims, d)) invalid("scatter: scatter_dims_to_operand_dims names a batching dimension");
+      for (const std::vector<int64_t>* l : {&sd.offset_dims, &sd.collapsed_slice_dims})
+        for (size_t i = 1; i < l->size(); ++i)
+          if ((*l)[i] <= (*l)[i - 1]) invalid("scatter: update_window_dims / inserted_window_dims must be sorted");
+      if ((int)(sd.offset_dims.size() + sd.collapsed_slice_dims.size() + sd.operand_batching_dims.size()) != r)
+        invalid("scatter: the operand's rank must equal the window, inserted and batching dimension counts");
+      std::vector<int64_t> win_dims;
+      for (int d = 0; d < r; ++d)
+        if (!has(sd.collapsed_slice_dims, d) && !has(sd.operand_batching_dims, d)) win_dims.push_back(d);
+      std::vector<int64_t> scat;
+      for (int d = 0; d < ri; ++d)
+        if (d != sd.index_vector_dim) scat.push_back(ix.shape[d]);
+      if ((int)(sd.offset_dims.size() + scat.size()) != ru) invalid("scatter: updates rank mismatch");
+      size_t kw = 0, ks = 0;
+      for (int d = 0; d < ru; ++d) {
+        if (kw < sd.offset_dims.size() && sd.offset_dims[kw] == d) {
+          if (u.shape[d] > x.shape[win_dims[kw]]) invalid("scatter: an update window is larger than the operand");
+          ++kw;
+        } else if (u.shape[d] != scat[ks++]) {
+          invalid("scatter: update scatter dimensions must match the indices' dimensions");
+        }
+      }
+      for (size_t i = 0; i < sd.operand_batching_dims.size(); ++i)
+        if (x.shape[sd.operand_batching_dims[i]] != ix.shape[sd.start_indices_batching_dims[i]])
+          invalid("scatter: batching dimension sizes differ");
+      if (u.dtype != x.dtype || !(n.type == x)) invalid("scatter: result and updates must have the input's type");
       break;
     }
     case Op::Gather: {

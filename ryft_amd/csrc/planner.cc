@@ -167,6 +167,7 @@ class Planner {
   void classify_row(Step& st);
   bool row_reducible(int reduce, const TensorType& space);
   void emit_dot(const std::vector<int>& dots, int target, int root);
+  void emit_scatter(int node, int target);
   bool try_attention(int d2, int target, DType out_dtype, int root);
   void emit_copy(int src_slot, int64_t src_off, int dst_slot, size_t bytes);
   bool dot_operand(int dot, int which, GemmOperand* op, int* slot, int force_copy);
@@ -603,6 +604,9 @@ int Planner::materialize(int node, int target) {
     case Op::Gather:
       emit_gather(node, target);
       break;
+    case Op::Scatter:
+      emit_scatter(node, target);
+      break;
     case Op::Reshape: {
       int s = materialize(n.operands[0]);
       if (target >= 0) {
@@ -902,6 +906,91 @@ void Planner::emit_gather(int node, int target) {
   st.bytes = 2.0 * (double)n.type.bytes() + (double)it.bytes();
   plan_.steps.push_back(std::move(st));
   mat_[node] = out;
+}
+
+// scatter (manipulation.rs:1614-1690): the input is materialized and copied into the result (never computed straight
+// into it, and a donated input is not updated in place), then one step combines the update windows into it
+// (kernels/k_window.hip). The dimension numbers become per-dimension maps like gather's: each update dim is a window
+// dim (walking one operand
+// dim: the operand's non-inserted, non-batching dims in order) or a scatter dim (one of the indices' dims other than
+// the index vector dim, in order). Windows that may overlap are applied one after another in row-major order of the
+// scatter dims (the sequential order XLA's CPU backend applies them in), so the result does not depend on timing;
+// with unique_indices every update element is applied at once.
+void Planner::emit_scatter(int node, int target) {
+  const Node& n = g_.nodes[node];
+  const TensorType& xt = g_.nodes[n.operands[0]].type;
+  const TensorType& it = g_.nodes[n.operands[1]].type;
+  const TensorType& ut = g_.nodes[n.operands[2]].type;
+  const GatherDims& sd = n.gather;
+  const int r = xt.rank(), ri = it.rank(), ru = ut.rank();
+  if (r > WIN_MAX_RANK || ri > WIN_MAX_RANK || ru > WIN_MAX_RANK)
+    unimplemented("scatter of rank above " + std::to_string(WIN_MAX_RANK));
+  const size_t es = dtype_size(n.type.dtype);
+  if (es != 1 && es != 2 && es != 4 && es != 8) unimplemented(std::string("scatter of ") + dtype_name(n.type.dtype));
+  if (es == 8 && n.scatter_combine != ScatterCombine::Set)
+    unimplemented("scatter combining 64-bit elements other than by replacing them");
+  const int ix = materialize(n.operands[1]);
+  const int upd = materialize(n.operands[2]);
+  const int out = temp_or(target, n.type);
+  emit_copy(materialize(n.operands[0]), 0, out, n.type.bytes());
+  mat_[node] = out;
+  if (ut.elements() == 0 || xt.elements() == 0) return;  // nothing to combine (every window of an empty operand is outside it)
+  Step st{};
+  st.kind = Step::SCATTER;
+  st.name = "scatter";
+  ScatterArgs& a = st.sca;
+  a.dtype = (int32_t)n.type.dtype;
+  a.idx_dtype = (int32_t)it.dtype;
+  a.elem_bytes = (int32_t)es;
+  switch (n.scatter_combine) {
+    case ScatterCombine::Set: a.kind = SC_SET; break;
+    case ScatterCombine::Add: a.kind = SC_ADD; break;
+    case ScatterCombine::Mul: a.kind = SC_MUL; break;
+    case ScatterCombine::Min: a.kind = SC_MIN; break;
+    case ScatterCombine::Max: a.kind = SC_MAX; break;
+    case ScatterCombine::And: a.kind = SC_AND; break;
+    case ScatterCombine::Or: a.kind = SC_OR; break;
+  }
+  a.upd_rank = ru;
+  a.op_rank = r;
+  a.idx_rank = ri;
+  a.ivd = (int32_t)sd.index_vector_dim;
+  a.n_map = (int32_t)sd.start_index_map.size();
+  a.serial = n.unique_indices ? 0 : 1;
+  for (int d = 0; d < WIN_MAX_RANK; ++d) a.upd_to_op[d] = a.upd_to_idx[d] = a.op_batch[d] = a.map[d] = -1;
+  auto has = [](const std::vector<int64_t>& v, int64_t d) { return std::find(v.begin(), v.end(), d) != v.end(); };
+  std::vector<int> window_operand_dims, scatter_index_dims;
+  for (int d = 0; d < r; ++d) {
+    a.op_shape[d] = xt.shape[d];
+    a.win[d] = 1;
+    if (!has(sd.collapsed_slice_dims, d) && !has(sd.operand_batching_dims, d)) window_operand_dims.push_back(d);
+  }
+  for (int d = 0; d < ri; ++d) {
+    a.idx_shape[d] = it.shape[d];
+    if (d != sd.index_vector_dim) scatter_index_dims.push_back(d);
+  }
+  size_t kw = 0, ks = 0;
+  a.total = a.n_windows = a.win_elems = 1;
+  for (int d = 0; d < ru; ++d) {
+    a.upd_shape[d] = ut.shape[d];
+    a.total *= ut.shape[d];
+    if (has(sd.offset_dims, d)) {
+      const int od = window_operand_dims.at(kw++);
+      a.upd_to_op[d] = od;
+      a.win[od] = ut.shape[d];
+      a.win_elems *= ut.shape[d];
+    } else {
+      a.upd_to_idx[d] = scatter_index_dims.at(ks++);
+      a.n_windows *= ut.shape[d];
+    }
+  }
+  for (size_t i = 0; i < sd.operand_batching_dims.size(); ++i)
+    a.op_batch[sd.operand_batching_dims[i]] = (int32_t)sd.start_indices_batching_dims[i];
+  for (size_t k = 0; k < sd.start_index_map.size(); ++k) a.map[k] = (int32_t)sd.start_index_map[k];
+  st.patches = {{offsetof(ScatterArgs, out), out}, {offsetof(ScatterArgs, indices), ix},
+                {offsetof(ScatterArgs, updates), upd}};
+  st.bytes = 3.0 * (double)ut.bytes() + (double)it.bytes();
+  plan_.steps.push_back(std::move(st));
 }
 
 // pad (manipulation.rs:530-642): result[lo + i·(interior + 1)] = operand[i] where that index is inside the result,
@@ -2322,6 +2411,9 @@ std::string Plan::describe() const {
       os << " window=" << s.win.total << " of rank " << s.win.rank;
     } else if (s.kind == Step::GATHER) {
       os << " elems=" << s.gat.total << " index_vector=" << s.gat.n_map;
+    } else if (s.kind == Step::SCATTER) {
+      os << " windows=" << s.sca.n_windows << " window_elems=" << s.sca.win_elems << " kind=" << s.sca.kind
+         << (s.sca.serial ? " serial" : " parallel");
     }
     os << " flops=" << s.flops << " bytes=" << s.bytes << "\n";
   }

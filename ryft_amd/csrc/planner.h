@@ -17,7 +17,7 @@ struct Slot {
 };
 
 struct Step {
-  enum Kind { ELEMENTWISE, REDUCE, GEMM, ATTENTION, COPY, ROW, WINDOW, GATHER, REDUCE_BODY } kind;
+  enum Kind { ELEMENTWISE, REDUCE, GEMM, ATTENTION, COPY, ROW, WINDOW, GATHER, REDUCE_BODY, SCATTER } kind;
   std::string name;  // kernel family, for profiling ("gemm_bf16_mfma", "attention_fwd", ...)
   EwProgram ew;
   ReduceArgs red;
@@ -26,6 +26,7 @@ struct Step {
   RowArgs row;
   WindowArgs win;
   GatherArgs gat;
+  ScatterArgs sca;
   ReduceBodyArgs rbody;
   struct { int64_t bytes; int64_t src_offset; } copy;  // src_offset: bytes into the source slot
   // Pointer fields inside the args block that refer to slots: (byte offset of the pointer field, slot). The
@@ -42,6 +43,7 @@ struct Step {
       case ROW: return &row;
       case WINDOW: return &win;
       case GATHER: return &gat;
+      case SCATTER: return &sca;
       case REDUCE_BODY: return &rbody;
       default: return nullptr;
     }

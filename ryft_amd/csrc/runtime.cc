@@ -693,7 +693,7 @@ bool enqueue_steps(Client* c, const Plan& plan, void* const* ptr, hipStream_t st
   const bool timed = prof || record;
   constexpr size_t kBlock = std::max({sizeof(EwProgram), sizeof(ReduceArgs), sizeof(GemmArgs), sizeof(RowArgs),
                                       sizeof(AttnArgs), sizeof(WindowArgs), sizeof(GatherArgs),
-                                      sizeof(ReduceBodyArgs)});
+                                      sizeof(ReduceBodyArgs), sizeof(ScatterArgs)});
   alignas(64) static thread_local unsigned char block[kBlock + 64];
   bool recorded = false;
   for (size_t si = 0; si < plan.steps.size(); ++si) {
@@ -724,6 +724,7 @@ bool enqueue_steps(Client* c, const Plan& plan, void* const* ptr, hipStream_t st
                   : step.kind == Step::ROW       ? sizeof(RowArgs)
                   : step.kind == Step::WINDOW    ? sizeof(WindowArgs)
                   : step.kind == Step::GATHER    ? sizeof(GatherArgs)
+                  : step.kind == Step::SCATTER   ? sizeof(ScatterArgs)
                   : step.kind == Step::REDUCE_BODY ? sizeof(ReduceBodyArgs)
                                                  : sizeof(AttnArgs);
       memcpy(block, const_cast<Step&>(step).args_block(), sz);
@@ -740,6 +741,7 @@ bool enqueue_steps(Client* c, const Plan& plan, void* const* ptr, hipStream_t st
         case Step::ATTENTION: launch_attention(*(AttnArgs*)block, st, last); break;
         case Step::WINDOW: launch_window(*(WindowArgs*)block, st, last); break;
         case Step::GATHER: launch_gather(*(GatherArgs*)block, st, last); break;
+        case Step::SCATTER: launch_scatter(*(ScatterArgs*)block, st, last); break;
         case Step::REDUCE_BODY: launch_reduce_body(*(ReduceBodyArgs*)block, st, last); break;
         default: recorded = false; break;
       }

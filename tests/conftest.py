@@ -13,6 +13,13 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
 
 
+def pytest_unconfigure(config):
+    # a process still alive 60 s after the test session ended (stuck while exiting) prints every thread's Python stack
+    # to stderr, so that the place it waits in is on record
+    import faulthandler
+    faulthandler.dump_traceback_later(60, exit=False, file=sys.__stderr__)
+
+
 @pytest.fixture(scope="session")
 def plugin():
     from ryft_amd import pjrt

@@ -145,6 +145,14 @@ def _parse_lines(lines: List[str], ret: str):
         if rhs.startswith('"stablehlo.gather"('):
             ops.append(_parse_gather(lhs, rhs))
             continue
+        if rhs.startswith('"stablehlo.scatter"('):
+            region_lines = []
+            while not lines[i].startswith("})"):
+                region_lines.append(lines[i])
+                i += 1
+            ops.append(_parse_scatter(lhs, rhs, region_lines, lines[i]))
+            i += 1
+            continue
         if name == "stablehlo.reduce" and "applies" not in rest:
             region_lines = []
             while not lines[i].startswith("}"):
@@ -218,6 +226,35 @@ def _parse_gather(res: str, rhs: str) -> Op:
     ins, outs = _types_after_colon(m.group(4))
     attrs = {"dimension_numbers": ("gather_dims", g), "slice_sizes": ("i64s", sizes)}
     return Op("stablehlo.gather", [m.group(1), m.group(2)], [res], outs, attrs)
+
+
+def _parse_scatter(res: str, rhs: str, region_lines: List[str], close: str) -> Op:
+    # `"stablehlo.scatter"(%a, %i, %u) <{indices_are_sorted = .., scatter_dimension_numbers = #stablehlo.scatter<..>,
+    # unique_indices = ..}> ({`, the region `^bb0(%x: T, %y: T):`, its ops and return, then `}) : (A, I, U) -> A`
+    m = re.fullmatch(r'"stablehlo\.scatter"\((%\w+), (%\w+), (%\w+)\) <\{(.*)\}> \(\{', rhs.strip())
+    assert m, rhs
+    attrs_txt = m.group(4)
+    dn = re.search(r"#stablehlo\.scatter<(.*?)>", attrs_txt).group(1)
+
+    def field(name):
+        f = re.search(name + r"\s*=\s*\[(.*?)\]", dn)
+        return _ints(f.group(1)) if f else []
+
+    g = {k: field(k) for k in ("update_window_dims", "inserted_window_dims", "input_batching_dims",
+                               "scatter_indices_batching_dims", "scatter_dims_to_operand_dims")}
+    g["index_vector_dim"] = int(re.search(r"index_vector_dim\s*=\s*(\d+)", dn).group(1))
+    attrs = {"scatter_dimension_numbers": ("scatter_dims", g)}
+    for b in ("indices_are_sorted", "unique_indices"):
+        bm = re.search(b + r"\s*=\s*(true|false)", attrs_txt)
+        if bm:
+            attrs[b] = ("bool", bm.group(1) == "true")
+    ins, outs = _types_after_colon(close[len("})"):].strip().lstrip(":").strip())
+    op = Op("stablehlo.scatter", [m.group(1), m.group(2), m.group(3)], [res], outs, attrs)
+    decl = region_lines[0]
+    args = re.findall(r"(%\w+): (tensor<[^>]*>)", decl)
+    body_ops, returned = _parse_lines(region_lines[1:], "stablehlo.return")
+    op.region = ([a[0] for a in args], [a[1] for a in args], body_ops, returned)
+    return op
 
 
 def _parse_op(res: str, name: str, rest: str) -> Op:
@@ -302,6 +339,7 @@ SORTED = {
     "stablehlo.slice": ["limit_indices", "start_indices", "strides"],
     "stablehlo.pad": ["edge_padding_high", "edge_padding_low", "interior_padding"],
     "stablehlo.gather": ["dimension_numbers", "indices_are_sorted", "slice_sizes"],
+    "stablehlo.scatter": ["indices_are_sorted", "scatter_dimension_numbers", "unique_indices"],
 }
 # ... and in declaration order
 DECLARED = {
@@ -313,11 +351,12 @@ DECLARED = {
     "stablehlo.slice": ["limit_indices", "start_indices", "strides"],
     "stablehlo.pad": ["edge_padding_high", "edge_padding_low", "interior_padding"],
     "stablehlo.gather": ["dimension_numbers", "slice_sizes", "indices_are_sorted"],
+    "stablehlo.scatter": ["scatter_dimension_numbers", "indices_are_sorted", "unique_indices"],
 }
 REQUIRED = {"function_type", "sym_name", "comparison_direction", "dot_dimension_numbers", "value", "iota_dimension",
             "broadcast_dimensions", "permutation", "dimensions", "start_indices", "limit_indices", "strides",
             "dimension", "edge_padding_low", "edge_padding_high", "interior_padding", "slice_sizes",
-            "dimension_numbers"}
+            "dimension_numbers", "scatter_dimension_numbers"}
 
 
 class Writer:
@@ -418,6 +457,21 @@ class Writer:
             data = varint(5)
             for k in ("lhs_batch", "rhs_batch", "lhs_contract", "rhs_contract"):
                 data += varint(len(d[k])) + b"".join(svarint(v) for v in d[k])
+            return self._entry("attr", "stablehlo", True, data)
+        if kind == "bool":  # BoolAttr: an IntegerAttr of type i1 (builtin code 8)
+            return self.battr(varint(8) + varint(self.elem("i1")) + bytes([1 if spec[1] else 0]))
+        if kind == "scatter_dims":
+            g = spec[1]
+            lists = ("update_window_dims", "inserted_window_dims", "input_batching_dims",
+                     "scatter_indices_batching_dims", "scatter_dims_to_operand_dims")
+            if self.text_attrs:
+                fields = [f"{k} = {g[k]}" for k in lists if g[k]] + [f"index_vector_dim = {g['index_vector_dim']}"]
+                return self._entry("attr", "stablehlo", False, ("#stablehlo.scatter<" + ", ".join(fields) + ">").encode()
+                                   + b"\0")
+            data = varint(11)
+            for k in lists:
+                data += varint(len(g[k])) + b"".join(svarint(v) for v in g[k])
+            data += svarint(g["index_vector_dim"])
             return self._entry("attr", "stablehlo", True, data)
         if kind == "gather_dims":
             g = spec[1]
