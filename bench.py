@@ -243,6 +243,8 @@ def measure(name, steps, warmup, cpu_seconds, client, dev):
         roofline["mfma_busy"] = ctr["mfma_busy"]
     if "shader_mhz" in ctr:
         roofline["shader_mhz"] = ctr["shader_mhz"]
+    if ctr:  # traffic / MFMA busy / clock are read from committed counter runs, not measured by this run
+        roofline["counters_source"] = f"profiles/counters_{w.name}.json (rocprofv3 --pmc runs of bench.py, committed)"
 
     if w.flops:
         value, vunit = w.flops / (ms_per_step * 1e-3) / 1e12, "TFLOP/s"
