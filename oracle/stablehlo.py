@@ -444,6 +444,35 @@ def _eval_op(op: str, rest: str, env, dot_precision: str) -> Tuple[np.ndarray, s
         names = re.findall(r"%[\w.$#-]+", rest.split(":")[0])
         vals = [env[n] for n in names]
         return vals if len(vals) > 1 else vals[0]
+    if op == "reduce_precision":
+        # casting.rs:259-300, on the element's own bits as XLA's emitter does: the mantissa rounded to m bits (ties to
+        # even, a carry moving into the exponent), then exponents the e-bit format cannot hold overflow to ±inf or
+        # underflow to ±0 (its subnormals included); NaN unchanged
+        (x, dt), = _operands(rest, 1, env)
+        fm = re.search(r"format\s*=\s*e(\d+)m(\d+)", rest)
+        if fm:
+            e, m = int(fm.group(1)), int(fm.group(2))
+        else:
+            e = int(re.search(r"exponent_bits\s*=\s*(\d+)", rest).group(1))
+            m = int(re.search(r"mantissa_bits\s*=\s*(\d+)", rest).group(1))
+        sm, se, width = {"f32": (23, 8, 32), "bf16": (7, 8, 16), "f16": (10, 5, 16)}[dt]
+        xv = np.asarray(x)
+        raw0 = np.asarray(to_raw(xv, dt))
+        bits = (raw0.view(np.uint32) if dt == "f32" else raw0).astype(np.int64)  # the element's bits
+        if m < sm:
+            shift = sm - m
+            last = 1 << shift
+            bits = (bits + ((bits & last) >> shift) + ((last >> 1) - 1)) & ~(last - 1)
+        if e < se:
+            exp_mask, sign = ((1 << se) - 1) << sm, 1 << (sm + se)
+            bias, rbias = (1 << (se - 1)) - 1, (1 << (e - 1)) - 1
+            xe = bits & exp_mask
+            bits = np.where(xe > ((bias + rbias) << sm), (bits & sign) | exp_mask,
+                            np.where(xe <= ((bias - rbias) << sm), bits & sign, bits))
+        bits &= (1 << width) - 1
+        raw = bits.astype(np.uint32).view(np.float32) if width == 32 else bits.astype(np.uint16)
+        out = np.asarray(from_raw(raw, dt), dtype=np.float64).reshape(xv.shape)
+        return np.where(np.isnan(xv), xv, out), dt
     if op == "bitcast_convert":
         # casting.rs:8-73 (same element width): the element's bits reread as the result type
         (x, dt), = _operands(rest, 1, env)

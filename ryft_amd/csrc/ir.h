@@ -42,6 +42,8 @@ enum class Op : uint8_t {
   Atan2, ShiftLeft, ShiftRightArithmetic, ShiftRightLogical,
   // elementwise, unary, the element's bits reread as another type of the same width
   BitcastConvert,
+  // elementwise, unary: rounded to `dims` = {exponent bits, mantissa bits} and back (casting.rs:259-300)
+  ReducePrecision,
   // elementwise, ternary
   Select, Clamp,
   // data movement

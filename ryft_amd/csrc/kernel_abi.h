@@ -46,6 +46,7 @@ enum EwOp : uint8_t {
   // unary, int class (EW_POPCNT / EW_CLZ: imm.i = the element width in bits)
   EW_INEG, EW_IABS, EW_NOT, EW_ISIGN, EW_POPCNT, EW_CLZ,
   EW_BITCAST,   // imm.i = (source type << 8) | result type (same width): the element's bits reread
+  EW_REDPREC,   // imm.i = (element type << 16) | (exponent bits << 8) | mantissa bits: reduce_precision
 
   // conversions
   EW_CVT_F2F, EW_CVT_F2I, EW_CVT_I2F, EW_CVT_I2I, EW_CVT_F2P, EW_CVT_I2P,

@@ -204,6 +204,32 @@ __device__ __noinline__ uint32_t bitcast_reg(uint32_t r, int from, int to) {
   }
 }
 
+// reduce_precision (casting.rs:259-300) of one element of type dt (f32, bf16 or f16; register form: an f32 value), on
+// the element's own bits as XLA's emitter does: the mantissa rounded to m bits (ties to even; a carry moves into the
+// exponent), then values whose exponent the e-bit format cannot hold overflow to ±inf or underflow to ±0 (the
+// reduced format's subnormals included); a NaN comes back unchanged.
+__device__ __noinline__ uint32_t reduce_precision_reg(uint32_t r, int dt, int e, int m) {
+  const float v = __uint_as_float(r);
+  if (v != v) return r;
+  const int sm = dt == DT_BF16 ? 7 : (dt == DT_F16 ? 10 : 23), se = dt == DT_F16 ? 5 : 8;
+  uint32_t x = dt == DT_BF16 ? r >> 16 : (dt == DT_F16 ? (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v) : r);
+  if (m < sm) {
+    const int shift = sm - m;
+    const uint32_t last = 1u << shift;
+    x = (x + ((x & last) >> shift) + ((last >> 1) - 1)) & ~(last - 1);
+  }
+  if (e < se) {
+    const uint32_t exp_mask = ((1u << se) - 1) << sm, sign = 1u << (sm + se);
+    const int bias = (1 << (se - 1)) - 1, rbias = (1 << (e - 1)) - 1;
+    const uint32_t xe = x & exp_mask;
+    if (xe > ((uint32_t)(bias + rbias) << sm)) x = (x & sign) | exp_mask;
+    else if (xe <= ((uint32_t)(bias - rbias) << sm)) x = x & sign;
+  }
+  if (dt == DT_BF16) return x << 16;
+  if (dt == DT_F16) return __float_as_uint((float)__builtin_bit_cast(_Float16, (uint16_t)x));
+  return x;
+}
+
 __device__ __forceinline__ float f_logistic(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
 // Saturating float → int conversion (NaN → 0), truncating toward zero.
@@ -460,7 +486,7 @@ __host__ __device__ inline bool ew_is_heavy(int op) {
   switch (op) {
     case EW_LOG: case EW_TANH: case EW_EXPM1: case EW_LOG1P: case EW_CVT_F2I: case EW_POW: case EW_REM:
     case EW_IDIV: case EW_IREM: case EW_UDIV: case EW_UREM: case EW_SIN: case EW_COS: case EW_TAN: case EW_CBRT:
-    case EW_ATAN2: case EW_BITCAST:
+    case EW_ATAN2: case EW_BITCAST: case EW_REDPREC:
       return true;
     default:
       return false;
@@ -532,6 +558,12 @@ __device__ __forceinline__ void ew_run_v(const EwProgram& P, int64_t lin, const 
       case EW_BITCAST:  // out of line, like the heavy ops
         if constexpr (!PRE) {
           _Pragma("unroll 1") for (int e = 0; e < V; ++e) r[e] = bitcast_reg(ra[e], I.imm.i >> 8, I.imm.i & 0xff);
+        }
+        break;
+      case EW_REDPREC:
+        if constexpr (!PRE) {
+          _Pragma("unroll 1") for (int e = 0; e < V; ++e)
+            r[e] = reduce_precision_reg(ra[e], I.imm.i >> 16, (I.imm.i >> 8) & 0xff, I.imm.i & 0xff);
         }
         break;
       EW_U(EW_INEG, -EW_IA)

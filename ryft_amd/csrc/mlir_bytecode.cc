@@ -618,6 +618,7 @@ class BytecodeParser {
         {"stablehlo.concatenate", {{"dimension", true, {BAttr::INT}}}},
         {"stablehlo.dynamic_slice", {{"slice_sizes", true, {BAttr::DENSE_ARRAY}}}},
         {"stablehlo.reverse", {{"dimensions", true, {BAttr::DENSE_ARRAY}}}},
+        {"stablehlo.reduce_precision", {{"exponent_bits", true, {BAttr::INT}}, {"mantissa_bits", true, {BAttr::INT}}}},
         {"stablehlo.map", {{"dimensions", true, {BAttr::DENSE_ARRAY}}}},
         {"stablehlo.gather",
          {{"dimension_numbers", true, {BAttr::GATHER_DIMS}},
@@ -1042,6 +1043,13 @@ class BytecodeParser {
         } else if (nm == "dynamic_slice") {
           n.op = Op::DynamicSlice;
           n.dims = int_list(op, "slice_sizes");
+        } else if (nm == "reduce_precision") {
+          n.op = Op::ReducePrecision;
+          auto bits = [&](const char* k) {
+            const BAttr& a = need(op, k);
+            return a.kind == BAttr::INT ? a.i : first_int(mlir_int_list_text(a.str), k);
+          };
+          n.dims = {bits("exponent_bits"), bits("mantissa_bits")};
         } else if (nm == "reverse") {
           n.op = Op::Reverse;
           n.dims = int_list(op, "dimensions");

@@ -11,6 +11,7 @@
 #include <algorithm>
 #include <cctype>
 #include <cmath>
+#include <cstdio>
 #include <cstdlib>
 #include <functional>
 #include <sstream>
@@ -114,6 +115,7 @@ const char* op_name(Op op) {
     case Op::Reverse: return "reverse";
     case Op::Scatter: return "scatter";
     case Op::BitcastConvert: return "bitcast_convert";
+    case Op::ReducePrecision: return "reduce_precision";
     case Op::DotGeneral: return "dot_general";
     case Op::Reduce: return "reduce";
   }
@@ -129,7 +131,7 @@ bool op_is_elementwise(Op op) {
     case Op::Select: case Op::Clamp: case Op::Sine: case Op::Cosine: case Op::Tan: case Op::Cbrt:
     case Op::RoundNearestEven: case Op::RoundNearestAfz: case Op::IsFinite: case Op::Popcnt:
     case Op::CountLeadingZeros: case Op::Atan2: case Op::ShiftLeft: case Op::ShiftRightArithmetic:
-    case Op::ShiftRightLogical: case Op::BitcastConvert:
+    case Op::ShiftRightLogical: case Op::BitcastConvert: case Op::ReducePrecision:
       return true;
     default:
       return false;
@@ -999,6 +1001,18 @@ class Parser {
       n.op = Op::Compare;
       n.cmp = parse_dir(get("comparison_direction"));
       n.cmp_type = parse_cmp_type(get("compare_type"));
+    } else if (nm == "reduce_precision") {
+      // pretty `format = e5m10`, generic `exponent_bits = 5 : i32, mantissa_bits = 10 : i32`
+      n.op = Op::ReducePrecision;
+      const std::string f = get("format");
+      if (!f.empty()) {
+        int e = -1, m = -1;
+        if (std::sscanf(f.c_str(), "e%dm%d", &e, &m) != 2) invalid("reduce_precision: malformed format '" + f + "'");
+        n.dims = {e, m};
+      } else {
+        n.dims = {first_int(parse_int_list_text(get("exponent_bits")), "exponent_bits"),
+                  first_int(parse_int_list_text(get("mantissa_bits")), "mantissa_bits")};
+      }
     } else if (nm == "reverse") {
       n.op = Op::Reverse;
       std::string d = get("dims");
@@ -1564,6 +1578,15 @@ void validate_node(const Graph& g, Node& n) {
           case Op::ShiftRightLogical:
             all_types(is_integer, "integer", true);
             break;
+          case Op::ReducePrecision: {
+            // (casting.rs:259-300) exponent_bits ≥ 1, mantissa_bits ≥ 0, the result the operand's type
+            if (n.dims.size() != 2 || n.dims[0] < 1 || n.dims[1] < 0) invalid("reduce_precision: bad exponent / mantissa bits");
+            if (!(n.type == opt(0))) invalid("reduce_precision: result type differs from the operand's");
+            const DType t = n.type.dtype;
+            if (t != DType::F32 && t != DType::BF16 && t != DType::F16)
+              unimplemented(std::string("reduce_precision of ") + dtype_name(t) + " is not supported");
+            break;
+          }
           case Op::BitcastConvert: {
             // (casting.rs:8-73) same shape here: a change of element width would add or drop a dimension
             const DType a = opt(0).dtype, r = n.type.dtype;

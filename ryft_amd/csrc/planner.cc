@@ -390,6 +390,14 @@ ExprBuilder::Val ExprBuilder::emit(int node, const std::vector<int>& src) {
         ins.round = 0;
         out = {push(ins, fl, {ops[0].instr}), fl};
         break;
+      case Op::ReducePrecision: {
+        // bits past the element type's own are a no-op (the kernel skips those steps); the type's own counts then
+        const int e = (int)std::min<int64_t>(n.dims[0], 8), m = (int)std::min<int64_t>(n.dims[1], 23);
+        ins.op = EW_REDPREC;
+        ins.imm.i = ((int32_t)dt << 16) | (e << 8) | m;
+        out = {push(ins, true, {ops[0].instr}), true};
+        break;
+      }
       case Op::IsFinite:
         ins.op = EW_ISFINITE;
         ins.round = 0;

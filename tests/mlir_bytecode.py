@@ -302,6 +302,11 @@ def _parse_op(res: str, name: str, rest: str) -> Op:
         key = "broadcast_dimensions" if short == "broadcast_in_dim" else "permutation"
         kv = [x for x in items if x.startswith("dims")][0]
         attrs[key] = ("i64s", _ints(kv.split("=", 1)[1]))
+    if short == "reduce_precision":  # `%x, format = e5m10`
+        kv = [x for x in items if x.startswith("format")][0]
+        fm = re.match(r"format\s*=\s*e(\d+)m(\d+)", kv)
+        attrs["exponent_bits"] = ("i32", int(fm.group(1)))
+        attrs["mantissa_bits"] = ("i32", int(fm.group(2)))
     if short == "reverse":
         kv = [x for x in items if x.startswith("dims")][0]
         attrs["dimensions"] = ("i64s", _ints(kv.split("=", 1)[1]))
@@ -356,7 +361,7 @@ DECLARED = {
 REQUIRED = {"function_type", "sym_name", "comparison_direction", "dot_dimension_numbers", "value", "iota_dimension",
             "broadcast_dimensions", "permutation", "dimensions", "start_indices", "limit_indices", "strides",
             "dimension", "edge_padding_low", "edge_padding_high", "interior_padding", "slice_sizes",
-            "dimension_numbers", "scatter_dimension_numbers"}
+            "dimension_numbers", "scatter_dimension_numbers", "exponent_bits", "mantissa_bits"}
 
 
 class Writer:
@@ -431,6 +436,8 @@ class Writer:
         if kind == "i64s":
             raw = b"".join(struct.pack("<q", v) for v in spec[1])
             return self.battr(varint(17) + varint(self.elem("i64")) + varint(len(spec[1])) + varint(len(raw)) + raw)
+        if kind == "i32":
+            return self.battr(varint(8) + varint(self.elem("i32")) + svarint(spec[1]))
         if kind == "i64":
             return self.battr(varint(8) + varint(self.elem("i64")) + svarint(spec[1]))
         if kind == "dense":

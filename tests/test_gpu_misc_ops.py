@@ -8,7 +8,10 @@ stable_hlo/operations/miscellaneous.rs:309-450, functional.rs:13-104, casting.rs
   * optimization_barrier  the identity on each operand;
   * bitcast_convert    against numpy's view of the same bytes (the definition of the op) for 32-, 16- and 8-bit pairs,
                        float ones included (finite values, infinities, signed zeros and subnormals; NaN patterns of
-                       the 32-bit float type kept bit for bit)."""
+                       the 32-bit float type kept bit for bit);
+  * reduce_precision   against the oracle (itself pinned to bf16 / f16 rounding and a closed form for f16
+                       subnormals) on every non-NaN 16-bit pattern of bf16 and f16 and on f32 values across the whole
+                       exponent range, for several formats."""
 import numpy as np
 import pytest
 
@@ -165,3 +168,18 @@ def test_bitcast_round_trip_fused(gpu_client):
     x = np.abs(_random(9, (1024,), "f32")) + np.float32(1e-3)
     outs, _ = run_pjrt(gpu_client, prog, [_input(x, "f32")])
     assert np.array_equal(outs[0].view(np.float32), np.nextafter(x, np.float32(np.inf)))
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("e,m", [(5, 10), (8, 7), (4, 3), (2, 0), (8, 23), (6, 12)])
+def test_reduce_precision(gpu_client, dt, e, m):
+    from tests.test_misc_ops import reduce_precision_program
+    rng = np.random.default_rng(30 + e * 31 + m)
+    if dt == "f32":
+        x = (rng.standard_normal(4096) * np.exp2(rng.integers(-140, 128, 4096))).astype(np.float32)
+        x[:6] = [np.inf, -np.inf, 0.0, -0.0, 1.0 + 2.0 ** -8, 3.0 * 2.0 ** -149]
+    else:  # every 16-bit pattern but the NaNs
+        x = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+        exp_mask, man_mask = (0x7F80, 0x7F) if dt == "bf16" else (0x7C00, 0x3FF)
+        x = x[~(((x & exp_mask) == exp_mask) & ((x & man_mask) != 0))]
+    _exact(gpu_client, reduce_precision_program(x.shape, e, m, dt), [_input(x, dt)], f"reduce_precision {dt} e{e}m{m}")

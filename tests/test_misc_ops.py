@@ -175,3 +175,76 @@ def test_malformed(compile_client, prog, code):
     with pytest.raises(pjrt.PjrtError) as e:
         compile_client.compile(pjrt.Program.mlir(prog))
     assert e.value.code == getattr(pjrt.ErrorCode, code), e.value.message
+
+
+# ------------------------------------------------------------------------------------------------ reduce_precision
+def reduce_precision_program(shape, e, m, dt="f32", generic=False):
+    T = _t(shape, dt)
+    op = (f'%0 = "stablehlo.reduce_precision"(%arg0) <{{exponent_bits = {e} : i32, mantissa_bits = {m} : i32}}> : '
+          f'({T}) -> {T}' if generic else f"%0 = stablehlo.reduce_precision %arg0, format = e{e}m{m} : {T}")
+    return f"""module {{
+  func.func @main(%arg0: {T}) -> {T} {{
+    {op}
+    return %0 : {T}
+  }}
+}}
+"""
+
+
+def _rp(x, e, m, dt="f32"):
+    (r, _), = sh.evaluate(reduce_precision_program(np.shape(x), e, m, dt), [x])
+    return np.asarray(r)
+
+
+def test_reduce_precision_reference_example_and_identity():
+    # casting.rs:293-300: [1, 2, 3] at e5m10 stay as they are; a format as wide as the type is the identity
+    assert _rp(np.array([1.0, 2.0, 3.0]), 5, 10).tolist() == [1.0, 2.0, 3.0]
+    x = np.random.default_rng(4).standard_normal(256).astype(np.float32).astype(np.float64)
+    assert np.array_equal(_rp(x, 8, 23), x)
+
+
+def test_reduce_precision_e8m7_is_bf16_rounding():
+    # the bf16 format: round to nearest even at 7 mantissa bits, f32's exponent range (bf16 conversion is pinned
+    # exhaustively against torch in test_oracle)
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal(4096) * np.exp2(rng.integers(-60, 60, 4096))).astype(np.float32).astype(np.float64)
+    x[:4] = [1.0 + 2.0 ** -8, 1.0 + 3 * 2.0 ** -8, -(1.0 + 2.0 ** -8), 3.4e38]  # ties to even, overflow by rounding
+    assert np.array_equal(_rp(x, 8, 7), sh.normalize(x, "bf16"))
+
+
+def test_reduce_precision_e5m10_is_float16_in_its_normal_range():
+    rng = np.random.default_rng(6)
+    x = (rng.standard_normal(4096) * np.exp2(rng.integers(-13, 15, 4096))).astype(np.float32).astype(np.float64)
+    r = _rp(x, 5, 10)
+    ok = np.abs(x.astype(np.float16).astype(np.float64)) >= 2.0 ** -14  # numpy's f16 (RNE), outside its subnormals
+    assert np.array_equal(r[ok], x[ok].astype(np.float16).astype(np.float64))
+    # past the largest f16 (65504, rounding up from 65520) ±inf; below the smallest normal (2^-14) ±0, subnormals
+    # of the reduced format included
+    big = _rp(np.array([65519.0, 65520.0, -1e6, 2.0 ** -14, 2.0 ** -15, -3e-6]), 5, 10)
+    assert big.tolist()[:3] == [65504.0, np.inf, -np.inf] and big[3] == 2.0 ** -14
+    assert big[4] == 0.0 and big[5] == 0.0 and np.signbit(big[5])
+
+
+def test_reduce_precision_of_f16_subnormals_rounds_their_own_field():
+    # an f16 subnormal keeps exponent field 0: m mantissa bits leave it a multiple of 2^(-24 + 10 - m), rounded to
+    # nearest with ties to the even multiple (closed form against the bit algorithm)
+    v = np.arange(1, 1024) * 2.0 ** -24  # every positive f16 subnormal
+    for m in (0, 3, 7):
+        q = 2.0 ** (-24 + 10 - m)
+        want = np.round(v / q) * q  # numpy rounds half to even
+        got = _rp(v, 5, m, "f16")
+        assert np.array_equal(got, want), m
+
+
+def test_reduce_precision_nan_and_forms(compile_client):
+    r = _rp(np.array([np.nan, np.inf, -np.inf]), 3, 2)
+    assert np.isnan(r[0]) and r[1] == np.inf and r[2] == -np.inf
+    progs = [reduce_precision_program((8, 64), 4, 3), reduce_precision_program((8, 64), 4, 3, generic=True)]
+    plans = [_plan(compile_client, p) for p in progs + [mb.to_bytecode(progs[0])]]
+    assert plans[0] == plans[1] == plans[2] and plans[0].count("elementwise") == 1, plans
+    with pytest.raises(pjrt.PjrtError) as e:
+        compile_client.compile(pjrt.Program.mlir(reduce_precision_program((4,), 0, 3)))
+    assert e.value.code == pjrt.ErrorCode.INVALID_ARGUMENT
+    with pytest.raises(pjrt.PjrtError) as e:
+        compile_client.compile(pjrt.Program.mlir(reduce_precision_program((4,), 5, 10, dt="f64")))
+    assert e.value.code == pjrt.ErrorCode.UNIMPLEMENTED
