@@ -444,6 +444,9 @@ def _eval_op(op: str, rest: str, env, dot_precision: str) -> Tuple[np.ndarray, s
         names = re.findall(r"%[\w.$#-]+", rest.split(":")[0])
         vals = [env[n] for n in names]
         return vals if len(vals) > 1 else vals[0]
+    if op in ("replica_id", "partition_id"):
+        # communication.rs:110-190: the id of the one replica / partition, 0
+        return np.zeros((), np.int64), "ui32"
     if op == "reduce_precision":
         # casting.rs:259-300, on the element's own bits as XLA's emitter does: the mantissa rounded to m bits (ties to
         # even, a carry moving into the exponent), then exponents the e-bit format cannot hold overflow to ±inf or

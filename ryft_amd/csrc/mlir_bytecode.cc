@@ -1043,6 +1043,13 @@ class BytecodeParser {
         } else if (nm == "dynamic_slice") {
           n.op = Op::DynamicSlice;
           n.dims = int_list(op, "slice_sizes");
+        } else if (nm == "replica_id" || nm == "partition_id") {
+          // (communication.rs:110-190) one replica and one partition: the id is 0, a ui32 scalar
+          if (!n.operands.empty() || n.type.rank() != 0 || n.type.dtype != DType::U32)
+            invalid(nm + ": expected no operands and a tensor<ui32> result");
+          n.op = Op::Constant;
+          n.literal.assign(4, 0);
+          n.splat = true;
         } else if (nm == "reduce_precision") {
           n.op = Op::ReducePrecision;
           auto bits = [&](const char* k) {

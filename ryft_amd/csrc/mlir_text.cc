@@ -1001,6 +1001,13 @@ class Parser {
       n.op = Op::Compare;
       n.cmp = parse_dir(get("comparison_direction"));
       n.cmp_type = parse_cmp_type(get("compare_type"));
+    } else if (nm == "replica_id" || nm == "partition_id") {
+      // (communication.rs:110-190) one replica and one partition: the id is 0, a ui32 scalar
+      if (!n.operands.empty() || n.type.rank() != 0 || n.type.dtype != DType::U32)
+        invalid(nm + ": expected no operands and a tensor<ui32> result");
+      n.op = Op::Constant;
+      n.literal.assign(4, 0);
+      n.splat = true;
     } else if (nm == "reduce_precision") {
       // pretty `format = e5m10`, generic `exponent_bits = 5 : i32, mantissa_bits = 10 : i32`
       n.op = Op::ReducePrecision;

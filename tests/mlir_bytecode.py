@@ -293,6 +293,8 @@ def _parse_op(res: str, name: str, rest: str) -> Op:
         ins, outs = _types_after_colon(m.group(3))
         return Op(name, [m.group(1)], [res], outs, {"start_indices": ("i64s", starts), "limit_indices": ("i64s", limits),
                                                     "strides": ("i64s", strides)})
+    if short in ("replica_id", "partition_id"):  # `%r = stablehlo.replica_id : tensor<ui32>`
+        return Op(name, [], [res], [rest.strip().lstrip(":").strip()])
     body, ty = rest.split(" : ", 1)
     ins, outs = _types_after_colon(ty)
     items = _split_top(body)

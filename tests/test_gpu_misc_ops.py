@@ -183,3 +183,20 @@ def test_reduce_precision(gpu_client, dt, e, m):
         exp_mask, man_mask = (0x7F80, 0x7F) if dt == "bf16" else (0x7C00, 0x3FF)
         x = x[~(((x & exp_mask) == exp_mask) & ((x & man_mask) != 0))]
     _exact(gpu_client, reduce_precision_program(x.shape, e, m, dt), [_input(x, dt)], f"reduce_precision {dt} e{e}m{m}")
+
+
+def test_replica_and_partition_ids(gpu_client):
+    # communication.rs:110-190: one replica, one partition; both ids 0
+    prog = """module {
+  func.func @main(%arg0: tensor<4xui32>) -> (tensor<4xui32>, tensor<ui32>) {
+    %0 = stablehlo.replica_id : tensor<ui32>
+    %1 = "stablehlo.partition_id"() : () -> tensor<ui32>
+    %2 = stablehlo.add %0, %1 : tensor<ui32>
+    %3 = stablehlo.broadcast_in_dim %2, dims = [] : (tensor<ui32>) -> tensor<4xui32>
+    %4 = stablehlo.add %arg0, %3 : tensor<4xui32>
+    return %4, %0 : tensor<4xui32>, tensor<ui32>
+  }
+}
+"""
+    outs, _ = run_pjrt(gpu_client, prog, [_input(np.arange(4, dtype=np.uint32) + 7, "ui32")])
+    assert outs[0].tolist() == [7, 8, 9, 10] and int(outs[1]) == 0

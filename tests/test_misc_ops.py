@@ -248,3 +248,22 @@ def test_reduce_precision_nan_and_forms(compile_client):
     with pytest.raises(pjrt.PjrtError) as e:
         compile_client.compile(pjrt.Program.mlir(reduce_precision_program((4,), 5, 10, dt="f64")))
     assert e.value.code == pjrt.ErrorCode.UNIMPLEMENTED
+
+
+def test_replica_and_partition_ids(compile_client):
+    # communication.rs:110-190: with one replica and one partition both ids are 0
+    prog = """module {
+  func.func @main(%arg0: tensor<4xui32>) -> (tensor<4xui32>, tensor<ui32>) {
+    %0 = stablehlo.replica_id : tensor<ui32>
+    %1 = "stablehlo.partition_id"() : () -> tensor<ui32>
+    %2 = stablehlo.add %0, %1 : tensor<ui32>
+    %3 = stablehlo.broadcast_in_dim %2, dims = [] : (tensor<ui32>) -> tensor<4xui32>
+    %4 = stablehlo.add %arg0, %3 : tensor<4xui32>
+    return %4, %0 : tensor<4xui32>, tensor<ui32>
+  }
+}
+"""
+    (a, _), (b, _) = sh.evaluate(prog, [np.arange(4)])
+    assert a.tolist() == [0, 1, 2, 3] and int(b) == 0
+    pretty = prog.replace('"stablehlo.partition_id"() : () -> tensor<ui32>', "stablehlo.partition_id : tensor<ui32>")
+    assert _plan(compile_client, prog) == _plan(compile_client, pretty) == _plan(compile_client, mb.to_bytecode(pretty))
