@@ -185,7 +185,15 @@ def evaluate(text: str, inputs: Sequence[np.ndarray], dot_precision: str = "f64"
         if tuple(x.shape) != tuple(shape):
             raise ValueError(f"{name}: expected shape {shape}, got {x.shape}")
         env[name] = (x, dt)
-    for st in mod.stmts:
+    out = _run(mod.stmts, env, dot_precision)
+    if out is None:
+        raise ValueError("function has no return")
+    return out
+
+
+def _run(stmts, env, dot_precision: str):
+    """Evaluates statements into `env` up to a return; returns the returned values (None without a return)."""
+    for st in stmts:
         r = _RET.match(st)
         if r:
             names = re.findall(r"%[\w.$#-]+", r.group(1))
@@ -206,10 +214,10 @@ def evaluate(text: str, inputs: Sequence[np.ndarray], dot_precision: str = "f64"
                 env[f"{res}#{k}"] = v
         else:
             env[res] = val
-    raise ValueError("function has no return")
+    return None
 
 
-_RET = re.compile(r"(?:func\.)?return\s+(.*?)(?:\s*:\s*.*)?$")
+_RET = re.compile(r'(?:func\.|stablehlo\.|"stablehlo\.)?return"?\s*\(?\s*(.*?)\)?(?:\s*:\s*.*)?$')
 
 
 def _operands(rest: str, n: int, env) -> List[Tuple[np.ndarray, str]]:
@@ -444,6 +452,19 @@ def _eval_op(op: str, rest: str, env, dot_precision: str) -> Tuple[np.ndarray, s
         names = re.findall(r"%[\w.$#-]+", rest.split(":")[0])
         vals = [env[n] for n in names]
         return vals if len(vals) > 1 else vals[0]
+    if op in ("if", "case"):
+        # control_flow.rs: the branch the predicate picks (case: the one at the index, the last one for an index
+        # outside the branches), its ops evaluated in the enclosing scope
+        (sel, _), = _operands(rest, 1, env)
+        body = rest[rest.index("({") + 2:rest.rindex("})")]
+        branches = re.split(r"\n\s*\},\s*\{\s*(?=\n)", body)
+        if op == "if":
+            k = 0 if bool(np.asarray(sel)) else 1
+        else:
+            k = int(np.asarray(sel))
+            k = k if 0 <= k < len(branches) else len(branches) - 1
+        vals = _run(Module._statements(branches[k] + "\n"), dict(env), dot_precision)
+        return vals if len(vals) != 1 else vals[0]
     if op in ("replica_id", "partition_id"):
         # communication.rs:110-190: the id of the one replica / partition, 0
         return np.zeros((), np.int64), "ui32"

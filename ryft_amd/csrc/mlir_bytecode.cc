@@ -989,6 +989,26 @@ class BytecodeParser {
         for (size_t i = 0; i < op.results.size(); ++i) node_of[op.results[i]] = value(op.operands[i]);
         continue;
       }
+      if (nm == "if" || nm == "case") {
+        // (control_flow.rs) every branch's ops into `g` (they may use any value of the enclosing scope), each result
+        // a select among the branches' returned values
+        std::vector<std::vector<int>> branches;
+        for (const BRegion& r : op.regions) {
+          if (r.blocks.size() != 1 || !r.blocks[0].args.empty()) invalid(nm + ": a branch is one block without arguments");
+          const size_t before = g.results.size();
+          build_ops(r.blocks[0], g, node_of);
+          branches.emplace_back(g.results.begin() + before, g.results.end());
+          g.results.resize(before);
+        }
+        std::vector<int> operands;
+        for (int64_t v : op.operands) operands.push_back(value(v));
+        std::vector<TensorType> results;
+        for (int t : op.result_types) results.push_back(tensor_type(t));
+        if (op.results.size() != results.size()) invalid(nm + ": result count mismatch");
+        const std::vector<int> picks = mlir_select_branches(g, nm, operands, results, branches);
+        for (size_t r = 0; r < picks.size(); ++r) node_of[op.results[r]] = picks[r];
+        continue;
+      }
       if (nm == "map") {  // (functional.rs:13-104) the body inlined over the inputs' shape
         if (op.regions.size() != 1 || op.results.size() != 1 || op.result_types.size() != 1)
           invalid("map: expected one body region and one result");

@@ -31,6 +31,10 @@ const std::unordered_map<std::string, Op>& mlir_simple_ops();
 // The nodes of one reduce op, one per result (`proto` holds the operands and dimensions). The body is `applies`
 // (the pretty form's single body op, e.g. "stablehlo.add") or `body`, the region as a graph; a region that applies
 // one recognised binary op to its two block arguments becomes that op, any other a ReduceBody::General node.
+// if / case: each result as a select among the branches' values (every branch computed); returns their nodes.
+std::vector<int> mlir_select_branches(Graph& g, const std::string& nm, const std::vector<int>& operands,
+                                      const std::vector<TensorType>& results,
+                                      const std::vector<std::vector<int>>& branches);
 // map: the body's ops copied into `g` over the result's shape; returns the node of the body's result.
 int mlir_inline_map(Graph& g, const std::vector<int>& inputs, const TensorType& result, const std::vector<int64_t>& dims,
                     const Graph& body);

@@ -514,6 +514,8 @@ struct OpSyntax {  // everything an op line carries, in generic form
   // reduce body: the pretty form's `applies` op, or the region as a graph
   std::string body_op;
   std::shared_ptr<Graph> body;
+  // if / case: each branch's returned values (its ops parsed straight into the enclosing graph)
+  std::vector<std::vector<int>> branches;
 };
 
 class Parser {
@@ -740,6 +742,19 @@ class Parser {
     return body;
   }
 
+  // A branch of if / case (no block arguments; it may use any value of the enclosing scope): its ops go into the
+  // enclosing graph through its closing brace; returns the nodes of the values it returns.
+  std::vector<int> parse_inline_block() {
+    const size_t before = graph_.results.size();
+    std::vector<TensorType> outer_types = std::move(result_types_);
+    result_types_.clear();
+    parse_block_body(/*top=*/true);
+    result_types_ = std::move(outer_types);
+    std::vector<int> ret(graph_.results.begin() + before, graph_.results.end());
+    graph_.results.resize(before);
+    return ret;
+  }
+
   void parse_op_line() {
     OpSyntax os;
     // results
@@ -776,8 +791,15 @@ class Parser {
     }
     if (c_.try_consume("<{")) parse_attr_dict(os.attrs), c_.expect(">");
     if (c_.try_consume("(")) {  // regions
-      c_.expect("{");
-      os.body = parse_region(/*pretty=*/false);
+      if (os.name == "if" || os.name == "case") {
+        do {
+          c_.expect("{");
+          os.branches.push_back(parse_inline_block());
+        } while (c_.try_consume(","));
+      } else {
+        c_.expect("{");
+        os.body = parse_region(/*pretty=*/false);
+      }
       c_.expect(")");
     }
     if (c_.try_consume("{")) parse_attr_dict(os.attrs);
@@ -1001,6 +1023,12 @@ class Parser {
       n.op = Op::Compare;
       n.cmp = parse_dir(get("comparison_direction"));
       n.cmp_type = parse_cmp_type(get("compare_type"));
+    } else if (nm == "if" || nm == "case") {
+      const std::vector<TensorType>& results = os.type.results;
+      if (os.results.size() != results.size()) invalid(nm + ": result names and types differ in number");
+      const std::vector<int> picks = mlir_select_branches(graph_, nm, n.operands, results, os.branches);
+      for (size_t r = 0; r < picks.size(); ++r) names_[os.results[r]] = picks[r];
+      return;
     } else if (nm == "replica_id" || nm == "partition_id") {
       // (communication.rs:110-190) one replica and one partition: the id is 0, a ui32 scalar
       if (!n.operands.empty() || n.type.rank() != 0 || n.type.dtype != DType::U32)
@@ -1668,6 +1696,65 @@ std::vector<Node> mlir_reduce_nodes(const Graph& g, const Node& proto, const std
     m.body = body;
     validate_node(g, m);
     out.push_back(std::move(m));
+  }
+  return out;
+}
+
+// if / case (control_flow.rs): every branch is computed (its ops are already in `g`: StableHLO ops have no side
+// effects, so computing a branch that is not taken changes nothing but the time spent) and each result selects the
+// taken branch's value: if → select(pred, then, else); case → the branch at the index, the last one for an index
+// outside [0, branches) as StableHLO specifies, by a chain of compare / select. Returns the node of each result.
+std::vector<int> mlir_select_branches(Graph& g, const std::string& nm, const std::vector<int>& operands,
+                                      const std::vector<TensorType>& results,
+                                      const std::vector<std::vector<int>>& branches) {
+  if (operands.size() != 1) invalid(nm + ": expected one operand (the predicate or the branch index)");
+  const TensorType& sel = g.nodes[operands[0]].type;
+  if (sel.rank() != 0) invalid(nm + ": the predicate / index must be a scalar");
+  if (nm == "if" && (sel.dtype != DType::PRED || branches.size() != 2)) invalid("if: an i1 predicate and two branches");
+  if (nm == "case" && (sel.dtype != DType::S32 || branches.empty())) invalid("case: an i32 index and at least one branch");
+  for (const auto& b : branches) {
+    if (b.size() != results.size()) invalid(nm + ": every branch returns one value per result");
+    for (size_t r = 0; r < b.size(); ++r)
+      if (!(g.nodes[b[r]].type == results[r])) invalid(nm + ": a branch returns another type than the result's");
+  }
+  auto push = [&](Node n) {
+    validate_node(g, n);
+    g.nodes.push_back(std::move(n));
+    return (int)g.nodes.size() - 1;
+  };
+  // per branch but the last: its predicate (case: index == k)
+  std::vector<int> pred(branches.size() - 1);
+  for (size_t k = 0; k + 1 < branches.size(); ++k) {
+    if (nm == "if") {
+      pred[k] = operands[0];
+      continue;
+    }
+    Node c;
+    c.op = Op::Constant;
+    c.type = sel;
+    const int32_t kv = (int32_t)k;
+    c.literal.assign((const uint8_t*)&kv, (const uint8_t*)&kv + 4);
+    c.splat = true;
+    const int ck = push(std::move(c));
+    Node e;
+    e.op = Op::Compare;
+    e.type = TensorType{DType::PRED, {}};
+    e.cmp = CmpDir::EQ;
+    e.cmp_type = CmpType::SIGNED;
+    e.operands = {operands[0], ck};
+    pred[k] = push(std::move(e));
+  }
+  std::vector<int> out(results.size());
+  for (size_t r = 0; r < results.size(); ++r) {
+    int v = branches.back()[r];
+    for (size_t k = branches.size() - 1; k-- > 0;) {
+      Node s;
+      s.op = Op::Select;
+      s.type = results[r];
+      s.operands = {pred[k], branches[k][r], v};
+      v = push(std::move(s));
+    }
+    out[r] = v;
   }
   return out;
 }

@@ -106,6 +106,7 @@ class Op:
         self.attrs = attrs or {}          # name → ("kind", value)
         self.body = body                  # reduce: (op name, arg type)
         self.region = None                # reduce with a general body: (arg names, arg types, ops, returned names)
+        self.branches = None              # if / case: per branch (ops, returned names), no block arguments
 
 
 def parse_module(text: str):
@@ -144,6 +145,25 @@ def _parse_lines(lines: List[str], ret: str):
             name, rest = "stablehlo.reduce", rhs[len("stablehlo.reduce"):]
         if rhs.startswith('"stablehlo.gather"('):
             ops.append(_parse_gather(lhs, rhs))
+            continue
+        if rhs.startswith('"stablehlo.if"(') or rhs.startswith('"stablehlo.case"('):
+            # `%r = "stablehlo.if"(%p) ({`, branch ops and return, `}, {`, ..., then `}) : (I) -> R`: one block
+            # without arguments per branch, using values of the enclosing scope
+            branches, cur = [], []
+            while not lines[i].startswith("})"):
+                if lines[i] == "}, {":
+                    branches.append(cur)
+                    cur = []
+                else:
+                    cur.append(lines[i])
+                i += 1
+            branches.append(cur)
+            m = re.fullmatch(r'"(stablehlo\.\w+)"\((%\w+)\) \(\{', rhs.strip())
+            _, outs = _types_after_colon(lines[i][len("})"):].strip().lstrip(":").strip())
+            op = Op(m.group(1), [m.group(2)], _result_names(lhs), outs)
+            op.branches = [_parse_lines(b, "stablehlo.return") for b in branches]
+            ops.append(op)
+            i += 1
             continue
         if rhs.startswith('"stablehlo.scatter"('):
             region_lines = []
@@ -604,6 +624,25 @@ class Writer:
                 enc.append(self._op("stablehlo.return", {}, [], [rvals[r] for r in rets]))
                 regions = varint(1) + varint(n_vals) + self._block([self.tensor(t) for t in types], enc)
                 n_regions = 1
+            elif op.branches:
+                # one region per branch: a block without arguments whose values are numbered after the function
+                # body's (every sibling region from the same base); operands from the enclosing scope keep their ids
+                regions, n_regions = b"", len(op.branches)
+                for rops, rets in op.branches:
+                    rvals: Dict[str, int] = {}
+                    enc = []
+                    for o in rops:
+                        enc.append(self._op(o.name, {k: self.attr(v) for k, v in o.attrs.items()},
+                                            [self.tensor(t) for t in o.result_types],
+                                            [rvals[x] if x in rvals else values[x] for x in o.operands]))
+                        for r in o.results:
+                            rvals[r] = n_func_values + len(rvals)
+                    enc.append(self._op("stablehlo.return", {}, [], [rvals[r] if r in rvals else values[r] for r in rets]))
+                    regions += varint(1) + varint(len(rvals)) + self._block([], enc)
+                body_ops.append(self._op(op.name, attrs, rtypes, operands, regions, False, n_regions))
+                for r in op.results:
+                    values[r] = len(values)
+                continue
             body_ops.append(self._op(op.name, attrs, rtypes, operands, regions, self.isolated_reduce, n_regions))
             for r in op.results:
                 values[r] = len(values)
@@ -682,6 +721,8 @@ def to_bytecode(text: str, **options) -> bytes:
     names |= {o.body[0] for o in ops if o.body} | ({"stablehlo.return"} if any(o.body or o.region for o in ops)
                                                    else set())
     names |= {r.name for o in ops if o.region for r in o.region[2]}
+    names |= {r.name for o in ops if o.branches for b in o.branches for r in b[0]}
+    names |= {"stablehlo.return"} if any(o.branches for o in ops) else set()
     for n in sorted(names, key=lambda x: (w.dialects.index(x.split(".")[0]), x)):
         w.opname(n)
     return w.module(text)

@@ -11,7 +11,9 @@ stable_hlo/operations/miscellaneous.rs:309-450, functional.rs:13-104, casting.rs
                        the 32-bit float type kept bit for bit);
   * reduce_precision   against the oracle (itself pinned to bf16 / f16 rounding and a closed form for f16
                        subnormals) on every non-NaN 16-bit pattern of bf16 and f16 and on f32 values across the whole
-                       exponent range, for several formats."""
+                       exponent range, for several formats;
+  * if / case          every branch computed and the taken one selected, against the oracle (which runs only the taken
+                       branch) for in-range and out-of-range indices, with the reference's worked example."""
 import numpy as np
 import pytest
 
@@ -31,7 +33,9 @@ BT = {"f32": (pjrt.BufferType.F32, np.float32), "bf16": (pjrt.BufferType.BF16, n
 
 
 def _input(raw: np.ndarray, dt: str) -> configs.HostInput:
-    return configs.HostInput(np.ascontiguousarray(raw), BT[dt][0], tuple(raw.shape))
+    raw = np.asarray(raw)
+    raw = np.ascontiguousarray(raw) if raw.ndim else raw  # (ascontiguousarray makes a 0-d array 1-d)
+    return configs.HostInput(raw, BT[dt][0], tuple(raw.shape))
 
 
 def _random(seed, shape, dt):
@@ -200,3 +204,23 @@ def test_replica_and_partition_ids(gpu_client):
 """
     outs, _ = run_pjrt(gpu_client, prog, [_input(np.arange(4, dtype=np.uint32) + 7, "ui32")])
     assert outs[0].tolist() == [7, 8, 9, 10] and int(outs[1]) == 0
+
+
+@pytest.mark.parametrize("idx", [0, 1, 2, 5, -3])
+def test_case(gpu_client, idx):
+    from tests.test_misc_ops import CASE_EXAMPLE, case_program
+    shape = (16, 256)
+    ins = [_input(np.array(idx, np.int32), "i32"), _input(_random(40, shape, "f32"), "f32"),
+           _input(_random(41, shape, "f32"), "f32")]
+    _exact(gpu_client, case_program(3, shape), ins, f"case index {idx}")
+    outs, _ = run_pjrt(gpu_client, CASE_EXAMPLE, [_input(np.array(idx, np.int32), "i32")])
+    assert outs[0].tolist() == ([0, 0] if idx == 0 else [1, 1])  # control_flow.rs:19-33
+
+
+@pytest.mark.parametrize("pred", [True, False])
+def test_if(gpu_client, pred):
+    from tests.test_misc_ops import if_program
+    shape = (16, 256)
+    ins = [_input(np.array(pred), "i1"), _input(_random(42, shape, "f32"), "f32"),
+           _input(_random(43, shape, "f32"), "f32")]
+    _exact(gpu_client, if_program(shape), ins, f"if {pred}")

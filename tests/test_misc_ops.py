@@ -267,3 +267,91 @@ def test_replica_and_partition_ids(compile_client):
     assert a.tolist() == [0, 1, 2, 3] and int(b) == 0
     pretty = prog.replace('"stablehlo.partition_id"() : () -> tensor<ui32>', "stablehlo.partition_id : tensor<ui32>")
     assert _plan(compile_client, prog) == _plan(compile_client, pretty) == _plan(compile_client, mb.to_bytecode(pretty))
+
+
+# ------------------------------------------------------------------------------------------------ if / case
+CASE_EXAMPLE = """module {
+  func.func @main(%arg0: tensor<i32>) -> tensor<2xi64> {
+    %result = "stablehlo.case"(%arg0) ({
+      %c = stablehlo.constant dense<0> : tensor<2xi64>
+      stablehlo.return %c : tensor<2xi64>
+    }, {
+      %c = stablehlo.constant dense<1> : tensor<2xi64>
+      stablehlo.return %c : tensor<2xi64>
+    }) : (tensor<i32>) -> tensor<2xi64>
+    return %result : tensor<2xi64>
+  }
+}
+"""
+IF_EXAMPLE = CASE_EXAMPLE.replace('"stablehlo.case"', '"stablehlo.if"').replace("tensor<i32>", "tensor<i1>")
+
+
+def if_program(shape):
+    """Two results; the branches use the function's arguments (values of the enclosing scope) and return one of them."""
+    T = _t(shape, "f32")
+    return f"""module {{
+  func.func @main(%arg0: tensor<i1>, %arg1: {T}, %arg2: {T}) -> ({T}, {T}) {{
+    %s = stablehlo.subtract %arg1, %arg2 : {T}
+    %0:2 = "stablehlo.if"(%arg0) ({{
+      %1 = stablehlo.add %s, %arg2 : {T}
+      stablehlo.return %1, %arg1 : {T}, {T}
+    }}, {{
+      %1 = stablehlo.multiply %arg1, %arg2 : {T}
+      stablehlo.return %1, %s : {T}, {T}
+    }}) : (tensor<i1>) -> ({T}, {T})
+    %2 = stablehlo.add %0#0, %0#1 : {T}
+    return %2, %0#1 : {T}, {T}
+  }}
+}}
+"""
+
+
+def case_program(n_branches, shape):
+    """Branch k returns arg1 · (k + 1) + arg2 (as a product with a constant and a sum)."""
+    T = _t(shape, "f32")
+    branches = []
+    for k in range(n_branches):
+        branches.append(f"""      %c = stablehlo.constant dense<{k + 1}.0> : {T}
+      %m = stablehlo.multiply %arg1, %c : {T}
+      %a = stablehlo.add %m, %arg2 : {T}
+      stablehlo.return %a : {T}""")
+    body = "\n    }, {\n".join(branches)
+    return f"""module {{
+  func.func @main(%arg0: tensor<i32>, %arg1: {T}, %arg2: {T}) -> {T} {{
+    %0 = "stablehlo.case"(%arg0) ({{
+{body}
+    }}) : (tensor<i32>) -> {T}
+    return %0 : {T}
+  }}
+}}
+"""
+
+
+def test_if_and_case_reference_examples():
+    # control_flow.rs:19-33 (case, index 1 → [1, 1]) and :77-91 (if, true → [0, 0]); out-of-range indices take the
+    # last branch (control_flow.rs:13-15)
+    for idx, want in ((1, [1, 1]), (0, [0, 0]), (7, [1, 1]), (-1, [1, 1])):
+        (r, _), = sh.evaluate(CASE_EXAMPLE, [np.array(idx)])
+        assert r.tolist() == want, idx
+    for p, want in ((True, [0, 0]), (False, [1, 1])):
+        (r, _), = sh.evaluate(IF_EXAMPLE, [np.array(p)])
+        assert r.tolist() == want
+
+
+def test_if_with_captures_and_two_results():
+    rng = np.random.default_rng(11)
+    a, b = rng.standard_normal((2, 4, 8))
+    for p in (True, False):
+        (r0, _), (r1, _) = sh.evaluate(if_program((4, 8)), [np.array(p), a, b])
+        s = sh.normalize(a - b, "f32")
+        first, second = (sh.normalize(s + b, "f32"), a) if p else (sh.normalize(a * b, "f32"), s)
+        assert np.array_equal(r0, sh.normalize(first + second, "f32")) and np.array_equal(r1, second)
+
+
+def test_if_and_case_forms_plan_alike(compile_client):
+    for prog in (CASE_EXAMPLE, IF_EXAMPLE, if_program((8, 64)), case_program(3, (8, 64))):
+        plans = [_plan(compile_client, p) for p in (prog, mb.to_bytecode(prog))]
+        assert plans[0] == plans[1], plans
+    # every branch computed, the results selected: one fused elementwise step per result
+    plan = _plan(compile_client, case_program(3, (8, 64))).strip().split("\n")
+    assert len(plan) == 1 and "elementwise" in plan[0], plan
