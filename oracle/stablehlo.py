@@ -465,6 +465,11 @@ def _eval_op(op: str, rest: str, env, dot_precision: str) -> Tuple[np.ndarray, s
             k = k if 0 <= k < len(branches) else len(branches) - 1
         vals = _run(Module._statements(branches[k] + "\n"), dict(env), dot_precision)
         return vals if len(vals) != 1 else vals[0]
+    if op == "get_dimension_size":
+        # manipulation.rs:12-40: the extent of dimension `dim`, an i32 scalar
+        (x, _), = _operands(rest, 1, env)
+        d = int(re.search(r"dim(?:ension)?\s*=\s*(\d+)", rest).group(1))
+        return np.array(np.shape(x)[d]), "i32"
     if op in ("replica_id", "partition_id"):
         # communication.rs:110-190: the id of the one replica / partition, 0
         return np.zeros((), np.int64), "ui32"

@@ -800,12 +800,20 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_mfma_kernel(const GemmArgs 
   const int total = per_batch * G.batch;
   // split-K: the K range is the slow index of the work order, so each XCD's run covers one K range (or a few) and
   // the tiles of that range fetch only its slices of A and B (with the range inside the XCD's run every XCD would
-  // fetch the whole of A)
+  // fetch the whole of A). A split finished in-kernel (small partial sums) keeps every K range of a tile on the
+  // tile's XCD instead, so that the finishing range reads partial sums written on its own XCD.
   const int nsplit = G.splits > 1 ? G.splits : 1;
-  int work = (int)blockIdx.x;
-  if (((total * nsplit) & 7) == 0) work = (work & 7) * ((total * nsplit) >> 3) + (work >> 3);
-  const int split = nsplit > 1 ? work / total : 0;
-  const int bid = nsplit > 1 ? work % total : work;
+  int split, bid;
+  if (nsplit > 1 && G.tile_counters) {
+    split = (int)blockIdx.x / total;
+    bid = (int)blockIdx.x % total;
+    if ((total & 7) == 0) bid = (bid & 7) * (total >> 3) + (bid >> 3);
+  } else {
+    int work = (int)blockIdx.x;
+    if (((total * nsplit) & 7) == 0) work = (work & 7) * ((total * nsplit) >> 3) + (work >> 3);
+    split = nsplit > 1 ? work / total : 0;
+    bid = nsplit > 1 ? work % total : work;
+  }
   const int b = bid / per_batch, t = bid % per_batch;
   const int GM = tiles_m < 8 ? tiles_m : 8;
   const int first_m = (t / (GM * tiles_n)) * GM;

@@ -618,6 +618,7 @@ class BytecodeParser {
         {"stablehlo.concatenate", {{"dimension", true, {BAttr::INT}}}},
         {"stablehlo.dynamic_slice", {{"slice_sizes", true, {BAttr::DENSE_ARRAY}}}},
         {"stablehlo.reverse", {{"dimensions", true, {BAttr::DENSE_ARRAY}}}},
+        {"stablehlo.get_dimension_size", {{"dimension", true, {BAttr::INT}}}},
         {"stablehlo.reduce_precision", {{"exponent_bits", true, {BAttr::INT}}, {"mantissa_bits", true, {BAttr::INT}}}},
         {"stablehlo.map", {{"dimensions", true, {BAttr::DENSE_ARRAY}}}},
         {"stablehlo.gather",
@@ -1063,6 +1064,20 @@ class BytecodeParser {
         } else if (nm == "dynamic_slice") {
           n.op = Op::DynamicSlice;
           n.dims = int_list(op, "slice_sizes");
+        } else if (nm == "get_dimension_size") {
+          // (manipulation.rs:12-40) shapes are static here: the extent of dimension `dimension`, an i32 scalar
+          if (n.operands.size() != 1 || n.type.rank() != 0 || n.type.dtype != DType::S32)
+            invalid("get_dimension_size: one operand and a tensor<i32> result");
+          const TensorType& x = g.nodes[n.operands[0]].type;
+          const BAttr& a = need(op, "dimension");
+          const int64_t d = a.kind == BAttr::INT ? a.i : first_int(mlir_int_list_text(a.str), "dimension");
+          if (d < 0 || d >= x.rank()) invalid("get_dimension_size: dimension out of range");
+          if (x.shape[d] > INT32_MAX) invalid("get_dimension_size: the extent does not fit an i32");
+          const int32_t v = (int32_t)x.shape[d];
+          n.op = Op::Constant;
+          n.operands.clear();
+          n.literal.assign((const uint8_t*)&v, (const uint8_t*)&v + 4);
+          n.splat = true;
         } else if (nm == "replica_id" || nm == "partition_id") {
           // (communication.rs:110-190) one replica and one partition: the id is 0, a ui32 scalar
           if (!n.operands.empty() || n.type.rank() != 0 || n.type.dtype != DType::U32)

@@ -1029,6 +1029,20 @@ class Parser {
       const std::vector<int> picks = mlir_select_branches(graph_, nm, n.operands, results, os.branches);
       for (size_t r = 0; r < picks.size(); ++r) names_[os.results[r]] = picks[r];
       return;
+    } else if (nm == "get_dimension_size") {
+      // (manipulation.rs:12-40) shapes are static here: the extent of dimension `dimension`, an i32 scalar
+      if (n.operands.size() != 1 || n.type.rank() != 0 || n.type.dtype != DType::S32)
+        invalid("get_dimension_size: one operand and a tensor<i32> result");
+      const TensorType& x = graph_.nodes[n.operands[0]].type;
+      const std::string ds = get("dim").empty() ? get("dimension") : get("dim");
+      const int64_t d = first_int(parse_int_list_text(ds), "dimension");
+      if (d < 0 || d >= x.rank()) invalid("get_dimension_size: dimension out of range");
+      if (x.shape[d] > INT32_MAX) invalid("get_dimension_size: the extent does not fit an i32");
+      const int32_t v = (int32_t)x.shape[d];
+      n.op = Op::Constant;
+      n.operands.clear();
+      n.literal.assign((const uint8_t*)&v, (const uint8_t*)&v + 4);
+      n.splat = true;
     } else if (nm == "replica_id" || nm == "partition_id") {
       // (communication.rs:110-190) one replica and one partition: the id is 0, a ui32 scalar
       if (!n.operands.empty() || n.type.rank() != 0 || n.type.dtype != DType::U32)

@@ -313,6 +313,10 @@ def _parse_op(res: str, name: str, rest: str) -> Op:
         ins, outs = _types_after_colon(m.group(3))
         return Op(name, [m.group(1)], [res], outs, {"start_indices": ("i64s", starts), "limit_indices": ("i64s", limits),
                                                     "strides": ("i64s", strides)})
+    if short == "get_dimension_size":  # `%r = stablehlo.get_dimension_size %x, dim = 1 : (T) -> tensor<i32>`
+        m = re.fullmatch(r"(%\w+), dim = (\d+) : (.*)", rest.strip())
+        _, outs = _types_after_colon(m.group(3))
+        return Op(name, [m.group(1)], [res], outs, {"dimension": ("i64", int(m.group(2)))})
     if short in ("replica_id", "partition_id"):  # `%r = stablehlo.replica_id : tensor<ui32>`
         return Op(name, [], [res], [rest.strip().lstrip(":").strip()])
     body, ty = rest.split(" : ", 1)
@@ -383,7 +387,7 @@ DECLARED = {
 REQUIRED = {"function_type", "sym_name", "comparison_direction", "dot_dimension_numbers", "value", "iota_dimension",
             "broadcast_dimensions", "permutation", "dimensions", "start_indices", "limit_indices", "strides",
             "dimension", "edge_padding_low", "edge_padding_high", "interior_padding", "slice_sizes",
-            "dimension_numbers", "scatter_dimension_numbers", "exponent_bits", "mantissa_bits"}
+            "dimension_numbers", "scatter_dimension_numbers", "exponent_bits", "mantissa_bits", "dimension"}
 
 
 class Writer:

@@ -224,3 +224,10 @@ def test_if(gpu_client, pred):
     ins = [_input(np.array(pred), "i1"), _input(_random(42, shape, "f32"), "f32"),
            _input(_random(43, shape, "f32"), "f32")]
     _exact(gpu_client, if_program(shape), ins, f"if {pred}")
+
+
+def test_get_dimension_size(gpu_client):
+    from tests.test_misc_ops import GET_DIM_EXAMPLE
+    outs, _ = run_pjrt(gpu_client, GET_DIM_EXAMPLE, [configs.HostInput(np.array([[1, 2, 3], [4, 5, 6]], np.int64),
+                                                                       pjrt.BufferType.S64, (2, 3))])
+    assert int(outs[0]) == 3 and int(outs[1]) == 2  # manipulation.rs:22-26

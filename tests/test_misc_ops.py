@@ -355,3 +355,26 @@ def test_if_and_case_forms_plan_alike(compile_client):
     # every branch computed, the results selected: one fused elementwise step per result
     plan = _plan(compile_client, case_program(3, (8, 64))).strip().split("\n")
     assert len(plan) == 1 and "elementwise" in plan[0], plan
+
+
+GET_DIM_EXAMPLE = """module {
+  func.func @main(%arg0: tensor<2x3xi64>) -> (tensor<i32>, tensor<i32>) {
+    %0 = stablehlo.get_dimension_size %arg0, dim = 1 : (tensor<2x3xi64>) -> tensor<i32>
+    %1 = "stablehlo.get_dimension_size"(%arg0) <{dimension = 0 : i64}> : (tensor<2x3xi64>) -> tensor<i32>
+    return %0, %1 : tensor<i32>, tensor<i32>
+  }
+}
+"""
+
+
+def test_get_dimension_size(compile_client):
+    # manipulation.rs:22-26: [[1, 2, 3], [4, 5, 6]], dim = 1 → 3
+    (a, dt), (b, _) = sh.evaluate(GET_DIM_EXAMPLE, [np.array([[1, 2, 3], [4, 5, 6]])])
+    assert dt == "i32" and int(a) == 3 and int(b) == 2
+    pretty = GET_DIM_EXAMPLE.replace('"stablehlo.get_dimension_size"(%arg0) <{dimension = 0 : i64}> :',
+                                     "stablehlo.get_dimension_size %arg0, dim = 0 :")
+    assert _plan(compile_client, GET_DIM_EXAMPLE) == _plan(compile_client, pretty) == \
+        _plan(compile_client, mb.to_bytecode(pretty))
+    with pytest.raises(pjrt.PjrtError) as e:
+        compile_client.compile(pjrt.Program.mlir(GET_DIM_EXAMPLE.replace("dim = 1", "dim = 2")))
+    assert e.value.code == pjrt.ErrorCode.INVALID_ARGUMENT
